@@ -1,0 +1,193 @@
+/*
+ * sparkq.h -- C-ABI of the MI355X (gfx950) quantized-linear hot path.
+ *
+ * One shared library, libsparkq.so, exports these entry points. Every entry
+ * point:
+ *   - takes caller-owned device pointers and a hipStream_t (passed as void*,
+ *     NULL means the default stream), enqueues its kernels on that stream and
+ *     returns without synchronising;
+ *   - never allocates device memory: scratch space, where an operation needs
+ *     it, is a caller-provided workspace sized by the matching
+ *     *_workspace_bytes() query;
+ *   - returns SPARKQ_OK (0) or a negative status, with a thread-local message
+ *     available from sparkq_last_error().
+ * Tensors are row-major and densely packed unless a stride argument says
+ * otherwise. Element types are given by the sparkq_dtype codes below.
+ *
+ * Reference interfaces (paths relative to the Spark-MLX-LLM repository; X/ is
+ * extensions/spark-mlx-ext/) are cited at each entry point.
+ */
+#ifndef SPARKQ_H_
+#define SPARKQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. */
+enum sparkq_dtype {
+  SPARKQ_F32 = 0,
+  SPARKQ_F16 = 1,
+  SPARKQ_BF16 = 2,
+};
+
+/* KV-cache storage formats for the INT8-KV decode attention. */
+enum sparkq_kv_format {
+  /* Symmetric signed int8 codes [B,Hkv,Ncap,D] plus one fp16 scale per
+   * (batch, KV head, token) [B,Hkv,Ncap]; value = code * scale. */
+  SPARKQ_KV_S8_F16SCALE = 0,
+  /* MLX affine 8-bit tuple (packed, scales, biases): packed uint32
+   * [B,Hkv,Ncap,D/4] with byte j of word w holding dim 4w+j, scales and
+   * biases [B,Hkv,Ncap,D/G] in the query dtype; value = u8 * scale + bias. */
+  SPARKQ_KV_AFFINE_U8 = 1,
+};
+
+/* Status codes. */
+#define SPARKQ_OK 0
+#define SPARKQ_ERR_INVALID (-1)     /* bad shape, dtype, pointer or size */
+#define SPARKQ_ERR_UNSUPPORTED (-2) /* valid request this build does not run */
+#define SPARKQ_ERR_DEVICE (-3)      /* HIP runtime or launch failure */
+#define SPARKQ_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+
+/* Thread-local description of the last failing call on this thread. */
+const char* sparkq_last_error(void);
+
+/* ABI version, bumped on any signature change. */
+int sparkq_abi_version(void);
+
+/* 1 when the current HIP device is a gfx950 (MI355X) that runs every kernel
+ * of this library, 0 otherwise. Replaces the capability probe
+ * is_w8a8_available (X/src/spark_w8a8.cpp:204-216), which answers the same
+ * question for Apple M5+ GPUs. */
+int sparkq_is_available(void);
+
+/* ------------------------------------------------------------------------
+ * W4A16 affine quantized linear (MLX layout)
+ * y[m,n] = sum_k x[m,k] * (q[n,k] * s[n,k/G] + b[n,k/G])
+ *   x       [M,K]   x_dtype (BF16 or F16)
+ *   w       [N,K/8] uint32, nibble k%8 of word k/8 at bits 4*(k%8)
+ *   scales  [N,K/G] x_dtype
+ *   biases  [N,K/G] x_dtype
+ *   y       [M,N]   y_dtype (x_dtype, or F32 for the unrounded epilogue)
+ * group_size in {32, 64, 128}; bits must be 4; K % 64 == 0; K % G == 0.
+ * Dispatches internally: M <= 32 runs the weight-streaming skinny kernel
+ * (MFMA 32x32x16, split-K with a reduction pass when the shape needs it),
+ * larger M runs the LDS-tiled MFMA GEMM behind a group-sum prologue.
+ *
+ * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True,
+ * group_size, bits, mode="affine") as called by AffineParameters.native
+ * (spark_mlx_llm/ops/linear.py:181-191), the split-K GEMV w4a16_qmv
+ * (X/spark_mlx_ext/w4a16_qmv.py:37-98) and the M=2..8 verify kernels
+ * w4a16_multirow (X/spark_mlx_ext/w4a16_multirow.py:238-437).
+ * ---------------------------------------------------------------------- */
+size_t sparkq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K,
+                                    int group_size);
+int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, void* y, int64_t M, int64_t N,
+                        int64_t K, int group_size, int bits, int x_dtype,
+                        int y_dtype, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Exact dequantization to fp32: out[n,k] = q[n,k] * s[n,k/G] + b[n,k/G].
+ * The product of a 4-bit code and a 16-bit float is exact in fp32, so the
+ * result has one rounding and is bit-identical however it is computed.
+ * Debug entry; the reference's equivalent is the per-element decode of the
+ * affine kernels (X/spark_mlx_ext/_w4a16_multirow_sources.py:31-39). */
+int sparkq_w4a16_dequantize(const uint32_t* w, const void* scales,
+                            const void* biases, float* out, int64_t N,
+                            int64_t K, int group_size, int scale_dtype,
+                            void* stream);
+
+/* Affine 4-bit quantizer on the device (the mx.quantize(bits=4) producer of
+ * the layout above, spark_mlx_llm/dspark/draft_quantization.py:119):
+ * per group of G values, scale = to_dtype((max-min)/15), bias = to_dtype(min),
+ * code = clamp(rint((w - bias) / scale), 0, 15) with the rounded scale and
+ * bias (a zero scale gives code 0). w is [N,K] in dtype (BF16 or F16). */
+int sparkq_w4_quantize(const void* w, uint32_t* wq, void* scales, void* biases,
+                       int64_t N, int64_t K, int group_size, int dtype,
+                       void* stream);
+
+/* ------------------------------------------------------------------------
+ * W8A8: per-token int8 activations, per-channel int8 weights, int32 MACs
+ * ---------------------------------------------------------------------- */
+
+/* Per-token symmetric quantizer, bit-exact with
+ * X/src/kernels/w8a8_quantize.metal:11-27: amax = max|x[m,:]|,
+ * scale = amax > 0 ? amax / 127 : 1 (IEEE fp32 division),
+ * q = (int8) clamp(rint(x / scale), -127, 127). x is [M,K] in x_dtype. */
+int sparkq_a8_quantize_per_token(const void* x, int8_t* q, float* scales,
+                                 int64_t M, int64_t K, int x_dtype,
+                                 void* stream);
+
+/* Raw int32 C[M,N] = A[M,K] . B[N,K]^T, exact. Replaces int8_matmul_int32
+ * (X/src/spark_w8a8.cpp:218-228, X/src/bindings.cpp:33-35).
+ * K % 32 == 0 and K <= 131040 so that no int32 sum can overflow. The
+ * workspace holds int32 split-K partials when the shape uses them. */
+size_t sparkq_int8_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int sparkq_int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c,
+                           int64_t M, int64_t N, int64_t K, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Workspace for sparkq_w8a8_linear: the int8 activations, their fp32 scales
+ * and any split-K int32 partials. */
+size_t sparkq_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* y[m,n] = to_dtype(fmaf(float(acc[m,n]) * sa[m], sw[n], bias[n])) with acc
+ * the exact int32 dot of the per-token int8 activations and the int8 weights.
+ * x [M,K] and y [M,N] in x_dtype; w [N,K] int8; w_scales [N] fp32; bias [N]
+ * in bias_dtype or NULL (zero). Replaces w8a8_linear
+ * (X/src/spark_w8a8.cpp:230-257; epilogue X/src/kernels/w8a8_tensor.metal:63).
+ * y_dtype may be F32 to read the unrounded epilogue. */
+int sparkq_w8a8_linear(const void* x, const int8_t* w, const float* w_scales,
+                       const void* bias, int bias_dtype, void* y, int64_t M,
+                       int64_t N, int64_t K, int x_dtype, int y_dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * INT8-KV GQA decode attention (one query token per sequence)
+ *   q    [B,Hq,D] (the L=1 axis of [B,Hq,1,D] dropped), q_dtype
+ *   out  [B,Hq,D], out_dtype (q_dtype, or F32 for the unrounded epilogue)
+ *   K/V codes, scales and biases per kv_format (see enum above), each a view
+ *   whose innermost axis is contiguous: element strides (batch, head, token)
+ *   are given in strides[] in this order:
+ *     strides[0..2]  key codes    (bytes)
+ *     strides[3..5]  key scales   (elements; biases share them)
+ *     strides[6..8]  value codes  (bytes)
+ *     strides[9..11] value scales (elements; biases share them)
+ *   All N tokens are visible (bottom-right causal decode with L=1).
+ * out = softmax(scale * q . K^T) . V in fp32 with an online softmax, split
+ * over the context and merged by log-sum-exp.
+ * Replaces int8_quantized_sdpa (X/spark_mlx_ext/int8_quantized_sdpa.py:
+ * 156-287) and its kernels spark_affine_u8_sdpa_{decode,merge,short}
+ * (X/spark_mlx_ext/_int8_sdpa_sources.py:8-376). D in {64,128,256};
+ * Hq/Hkv in {1,2,4,8}; for the affine format group_size in {32,64,128}.
+ * ---------------------------------------------------------------------- */
+size_t sparkq_int8kv_sdpa_workspace_bytes(int64_t B, int64_t Hq, int64_t N,
+                                          int64_t D);
+int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes,
+                              const void* k_scales, const void* k_biases,
+                              const void* v_codes, const void* v_scales,
+                              const void* v_biases, void* out, int64_t B,
+                              int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                              int group_size, int kv_format, int q_dtype,
+                              int out_dtype, float scale,
+                              const int64_t* strides, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Symmetric int8 KV quantizer for the S8_F16SCALE format (the quantize-on-
+ * append producer, mlx-lm QuantizedKVCache as configured by
+ * spark_mlx_llm/generation.py:316-329,339-384): per row of D values,
+ * scale = fp16(amax / 127) (1 when that is zero), code =
+ * clamp(rint(x / float(scale)), -127, 127). x [R,D] in x_dtype; codes [R,D]
+ * int8; scales [R] fp16. */
+int sparkq_kv_quantize_s8(const void* x, int8_t* codes, void* scales,
+                          int64_t R, int64_t D, int x_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARKQ_H_ */

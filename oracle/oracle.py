@@ -1,0 +1,346 @@
+"""ctypes binding of the C oracle (oracle/sparkq_oracle.c) plus numpy helpers.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). Every function restates a
+reference algorithm; the C source cites the reference file:line for each.
+16-bit floats travel as their uint16 bit patterns.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+__all__ = [
+    "F32", "F16", "BF16",
+    "bf16_bits", "bits_to_f32", "f16_bits", "round16",
+    "randn", "randn16",
+    "pack4", "unpack4", "w4_quantize", "w4_quantize_converter",
+    "w4_dequantize", "w4a16_matmul",
+    "a8_quantize", "w8_quantize_channel", "w8_unpack_affine",
+    "int8_matmul", "w8a8_epilogue",
+    "kv_quantize_s8", "kv_quantize_affine_u8", "kv_dequantize_s8",
+    "kv_dequantize_affine_u8", "sdpa_decode",
+    "cpu_w4a16_gemv", "scalar_f32_to_bf16", "scalar_f32_to_f16",
+    "scalar_f16_to_f32",
+]
+
+F32, F16, BF16 = 0, 1, 2
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_CPU = None
+
+
+def _build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "libsparkq_oracle.so")
+        if not os.path.exists(path):
+            _build()
+        _LIB = ctypes.CDLL(path)
+        _declare(_LIB)
+    return _LIB
+
+
+def _cpu():
+    global _CPU
+    if _CPU is None:
+        path = os.path.join(_HERE, "libsparkq_cpubase.so")
+        if not os.path.exists(path):
+            _build()
+        _CPU = ctypes.CDLL(path)
+        _CPU.sq_cpu_w4a16_gemv.restype = ctypes.c_int
+        _CPU.sq_cpu_w4a16_gemv.argtypes = [ctypes.c_void_p] * 4 + [
+            ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+            ctypes.c_void_p, ctypes.c_int]
+    return _CPU
+
+
+def _declare(lib):
+    P, I64, I, F, D, U64 = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                            ctypes.c_float, ctypes.c_double, ctypes.c_uint64)
+    sig = {
+        "sq_f32_to_bf16": (ctypes.c_uint16, [F]),
+        "sq_f32_to_f16": (ctypes.c_uint16, [F]),
+        "sq_f16_to_f32": (F, [ctypes.c_uint16]),
+        "sq_randn": (None, [U64, U64, F, P, I64]),
+        "sq_randn16": (None, [U64, U64, F, I, P, I64]),
+        "sq_pack4": (None, [P, P, I64, I64]),
+        "sq_unpack4": (None, [P, P, I64, I64]),
+        "sq_w4_quantize": (None, [P, I64, I64, I, I, P, P, P]),
+        "sq_w4_quantize_converter": (None, [P, I64, I64, I, P, P, P]),
+        "sq_w4_dequantize": (None, [P, P, P, I64, I64, I, I, P]),
+        "sq_w4a16_matmul": (None, [P, I, P, P, P, I64, I64, I64, I, P]),
+        "sq_a8_quantize": (None, [P, I64, I64, P, P]),
+        "sq_w8_quantize_channel": (None, [P, I64, I64, P, P]),
+        "sq_w8_unpack_affine": (None, [P, I64, I64, P]),
+        "sq_int8_matmul": (I, [P, P, I64, I64, I64, P]),
+        "sq_w8a8_epilogue": (None, [P, P, P, P, I64, I64, P]),
+        "sq_kv_quantize_s8": (None, [P, I64, I64, P, P]),
+        "sq_kv_quantize_affine_u8": (None, [P, I64, I64, I, I, P, P, P]),
+        "sq_kv_dequantize_s8": (None, [P, P, I64, I64, P]),
+        "sq_kv_dequantize_affine_u8": (None, [P, P, P, I64, I64, I, I, P]),
+        "sq_sdpa_decode": (None, [P, P, P, I64, I64, I64, I64, I64, D, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------------------
+# vectorised 16-bit conversions (same rules as the C scalars; pinned in tests)
+# ---------------------------------------------------------------------------
+
+def bf16_bits(x) -> np.ndarray:
+    """fp32 -> bf16 bits, round-to-nearest-even (conversion.py:154-159)."""
+    w = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (w & 0x7FFFFFFF) > 0x7F800000
+    r = ((w.astype(np.uint64) + 0x7FFF + ((w >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((w >> 16) | 0x40).astype(np.uint16), r)
+
+
+def f16_bits(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def bits_to_f32(h, dtype) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    if dtype == F16:
+        return h.view(np.float16).astype(np.float32)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def round16(x, dtype) -> np.ndarray:
+    return f16_bits(x) if dtype == F16 else bf16_bits(x)
+
+
+def scalar_f32_to_bf16(f: float) -> int:
+    return int(_lib().sq_f32_to_bf16(f))
+
+
+def scalar_f32_to_f16(f: float) -> int:
+    return int(_lib().sq_f32_to_f16(f))
+
+
+def scalar_f16_to_f32(h: int) -> float:
+    return float(_lib().sq_f16_to_f32(h))
+
+
+# ---------------------------------------------------------------------------
+# generator
+# ---------------------------------------------------------------------------
+
+def randn(seed: int, stream: int, n: int, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    _lib().sq_randn(seed, stream, std, _p(out), n)
+    return out
+
+
+def randn16(seed: int, stream: int, n: int, std: float = 1.0,
+            dtype: int = BF16) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    _lib().sq_randn16(seed, stream, std, dtype, _p(out), n)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# W4 affine
+# ---------------------------------------------------------------------------
+
+def pack4(codes) -> np.ndarray:
+    codes = _c(codes, np.uint8)
+    n, k = codes.shape
+    out = np.empty((n, k // 8), np.uint32)
+    _lib().sq_pack4(_p(codes), _p(out), n, k)
+    return out
+
+
+def unpack4(words, k: int) -> np.ndarray:
+    words = _c(words, np.uint32)
+    n = words.shape[0]
+    out = np.empty((n, k), np.uint8)
+    _lib().sq_unpack4(_p(words), _p(out), n, k)
+    return out
+
+
+def w4_quantize(w, group_size: int, dtype: int = BF16):
+    w = _c(w, np.float32)
+    n, k = w.shape
+    wq = np.empty((n, k // 8), np.uint32)
+    s = np.empty((n, k // group_size), np.uint16)
+    b = np.empty_like(s)
+    _lib().sq_w4_quantize(_p(w), n, k, group_size, dtype, _p(wq), _p(s), _p(b))
+    return wq, s, b
+
+
+def w4_quantize_converter(w, group_size: int = 32):
+    w = _c(w, np.float32)
+    n, k = w.shape
+    wq = np.empty((n, k // 8), np.uint32)
+    s = np.empty((n, k // group_size), np.uint16)
+    b = np.empty_like(s)
+    _lib().sq_w4_quantize_converter(_p(w), n, k, group_size, _p(wq), _p(s), _p(b))
+    return wq, s, b
+
+
+def w4_dequantize(wq, s, b, group_size: int, dtype: int = BF16) -> np.ndarray:
+    wq, s, b = _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
+    n = wq.shape[0]
+    k = wq.shape[1] * 8
+    out = np.empty((n, k), np.float32)
+    _lib().sq_w4_dequantize(_p(wq), _p(s), _p(b), n, k, group_size, dtype, _p(out))
+    return out
+
+
+def w4a16_matmul(x16, wq, s, b, group_size: int, dtype: int = BF16) -> np.ndarray:
+    x16 = _c(x16, np.uint16)
+    wq, s, b = _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
+    m, k = x16.shape
+    n = wq.shape[0]
+    y = np.empty((m, n), np.float64)
+    _lib().sq_w4a16_matmul(_p(x16), dtype, _p(wq), _p(s), _p(b), m, n, k,
+                           group_size, _p(y))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# W8A8
+# ---------------------------------------------------------------------------
+
+def a8_quantize(x):
+    x = _c(x, np.float32)
+    m, k = x.shape
+    q = np.empty((m, k), np.int8)
+    sc = np.empty(m, np.float32)
+    _lib().sq_a8_quantize(_p(x), m, k, _p(q), _p(sc))
+    return q, sc
+
+
+def w8_quantize_channel(w):
+    w = _c(w, np.float32)
+    n, k = w.shape
+    q = np.empty((n, k), np.int8)
+    sc = np.empty(n, np.float32)
+    _lib().sq_w8_quantize_channel(_p(w), n, k, _p(q), _p(sc))
+    return q, sc
+
+
+def w8_unpack_affine(words) -> np.ndarray:
+    words = _c(words, np.uint32)
+    n, k4 = words.shape
+    out = np.empty((n, k4 * 4), np.int8)
+    _lib().sq_w8_unpack_affine(_p(words), n, k4 * 4, _p(out))
+    return out
+
+
+def int8_matmul(a, b) -> np.ndarray:
+    a, b = _c(a, np.int8), _c(b, np.int8)
+    m, k = a.shape
+    n = b.shape[0]
+    c = np.empty((m, n), np.int32)
+    if _lib().sq_int8_matmul(_p(a), _p(b), m, n, k, _p(c)) != 0:
+        raise OverflowError("int8 matmul sum leaves int32")
+    return c
+
+
+def w8a8_epilogue(acc, sa, sw, bias=None) -> np.ndarray:
+    acc = _c(acc, np.int32)
+    sa, sw = _c(sa, np.float32), _c(sw, np.float32)
+    m, n = acc.shape
+    y = np.empty((m, n), np.float32)
+    bias_p = None if bias is None else _p(_c(bias, np.float32))
+    if bias is not None:
+        bias = _c(bias, np.float32)
+        bias_p = _p(bias)
+    _lib().sq_w8a8_epilogue(_p(acc), _p(sa), _p(sw), bias_p, m, n, _p(y))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# INT8 KV and decode attention
+# ---------------------------------------------------------------------------
+
+def kv_quantize_s8(x):
+    x = _c(x, np.float32)
+    d = x.shape[-1]
+    r = x.size // d
+    codes = np.empty(x.shape, np.int8)
+    sc = np.empty(x.shape[:-1], np.uint16)
+    _lib().sq_kv_quantize_s8(_p(x), r, d, _p(codes), _p(sc))
+    return codes, sc
+
+
+def kv_quantize_affine_u8(x, group_size: int, dtype: int = BF16):
+    x = _c(x, np.float32)
+    d = x.shape[-1]
+    r = x.size // d
+    packed = np.empty((*x.shape[:-1], d // 4), np.uint32)
+    s = np.empty((*x.shape[:-1], d // group_size), np.uint16)
+    b = np.empty_like(s)
+    _lib().sq_kv_quantize_affine_u8(_p(x), r, d, group_size, dtype, _p(packed),
+                                    _p(s), _p(b))
+    return packed, s, b
+
+
+def kv_dequantize_s8(codes, scales) -> np.ndarray:
+    codes, scales = _c(codes, np.int8), _c(scales, np.uint16)
+    d = codes.shape[-1]
+    r = codes.size // d
+    out = np.empty(codes.shape, np.float32)
+    _lib().sq_kv_dequantize_s8(_p(codes), _p(scales), r, d, _p(out))
+    return out
+
+
+def kv_dequantize_affine_u8(packed, s, b, group_size: int,
+                            dtype: int = BF16) -> np.ndarray:
+    packed, s, b = _c(packed, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
+    d = packed.shape[-1] * 4
+    r = packed.size // packed.shape[-1]
+    out = np.empty((*packed.shape[:-1], d), np.float32)
+    _lib().sq_kv_dequantize_affine_u8(_p(packed), _p(s), _p(b), r, d,
+                                      group_size, dtype, _p(out))
+    return out
+
+
+def sdpa_decode(q, kdq, vdq, scale: float) -> np.ndarray:
+    """q [B,Hq,D]; kdq/vdq [B,Hkv,N,D] dequantized -> out [B,Hq,D] fp64."""
+    q, kdq, vdq = _c(q, np.float32), _c(kdq, np.float32), _c(vdq, np.float32)
+    bsz, hq, d = q.shape
+    hkv, n = kdq.shape[1], kdq.shape[2]
+    out = np.empty((bsz, hq, d), np.float64)
+    _lib().sq_sdpa_decode(_p(q), _p(kdq), _p(vdq), bsz, hq, hkv, n, d,
+                          float(scale), _p(out))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (bench.py only)
+# ---------------------------------------------------------------------------
+
+def cpu_w4a16_gemv(x16, wq, s, b, group_size: int, threads: int = 0):
+    """Multi-threaded fp32 dequantize-then-dot; returns (y fp32, threads)."""
+    x16 = _c(x16, np.uint16)
+    wq, s, b = _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
+    m, k = x16.shape
+    n = wq.shape[0]
+    y = np.empty((m, n), np.float32)
+    used = _cpu().sq_cpu_w4a16_gemv(_p(x16), _p(wq), _p(s), _p(b), m, n, k,
+                                    group_size, _p(y), threads)
+    if used < 0:
+        raise ValueError("unsupported CPU baseline shape")
+    return y, used

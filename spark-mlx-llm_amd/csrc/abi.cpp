@@ -1,0 +1,280 @@
+// abi.cpp -- the extern "C" entry points of libsparkq.so: argument
+// validation with the reference's error categories, device capability check,
+// and dispatch to the kernel launchers. No entry point allocates device
+// memory or synchronises the stream.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "common.h"
+#include "sparkq.h"
+
+namespace sparkq {
+
+// launchers (w4a16.hip, w8a8.hip, sdpa.hip)
+size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G);
+int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
+                 int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, void* ws,
+                 size_t wsb, hipStream_t st);
+int w4a16_dequantize(const uint32_t* w, const void* s, const void* b, float* out, int64_t N,
+                     int64_t K, int G, int sdt, hipStream_t st);
+int w4_quantize(const void* w, uint32_t* wq, void* s, void* b, int64_t N, int64_t K, int G,
+                int dt, hipStream_t st);
+int a8_quantize(const void* x, int8_t* q, float* scales, int64_t M, int64_t K, int xdt,
+                hipStream_t st);
+size_t i8_matmul_workspace(int64_t M, int64_t N, int64_t K);
+int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N,
+                    int64_t K, void* ws, size_t wsb, hipStream_t st);
+size_t w8a8_workspace(int64_t M, int64_t N, int64_t K);
+int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bias,
+                int bias_dtype, void* y, int64_t M, int64_t N, int64_t K, int xdt, int ydt,
+                void* ws, size_t wsb, hipStream_t st);
+size_t sdpa_workspace(int64_t B, int64_t Hq, int64_t N, int64_t D);
+int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void* kb,
+                       const void* vc, const void* vs, const void* vb, void* out, int64_t B,
+                       int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int G, int fmt,
+                       int qdt, int odt, float scale, const int64_t* strides, void* ws,
+                       size_t wsb, hipStream_t st);
+int kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_t D, int xdt,
+                   hipStream_t st);
+
+static thread_local char g_last_error[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(SPARKQ_ERR_DEVICE, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return SPARKQ_OK;
+}
+
+// Per-device capability cache: 0 unknown, 1 gfx950, -1 other.
+static int g_device_ok[64];
+static std::mutex g_device_mu;
+
+int device_check() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(SPARKQ_ERR_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return set_error(SPARKQ_ERR_DEVICE, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_device_mu);
+  if (g_device_ok[dev] == 0) {
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess)
+      return set_error(SPARKQ_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    g_device_ok[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    if (g_device_ok[dev] < 0)
+      return set_error(SPARKQ_ERR_UNSUPPORTED,
+                       "sparkq kernels require an MI355X (gfx950) device, found %s",
+                       prop.gcnArchName);
+  }
+  if (g_device_ok[dev] < 0)
+    return set_error(SPARKQ_ERR_UNSUPPORTED, "sparkq kernels require an MI355X (gfx950) device");
+  return SPARKQ_OK;
+}
+
+}  // namespace sparkq
+
+using namespace sparkq;
+
+#define REQUIRE(cond, ...)                                 \
+  do {                                                     \
+    if (!(cond)) return set_error(SPARKQ_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+#define REQUIRE_SUPPORTED(cond, ...)                       \
+  do {                                                     \
+    if (!(cond)) return set_error(SPARKQ_ERR_UNSUPPORTED, __VA_ARGS__); \
+  } while (0)
+#define DEVICE_OK()                          \
+  do {                                       \
+    if (int rc_ = device_check()) return rc_; \
+  } while (0)
+
+static bool is_float_dtype(int dt) { return dt == SPARKQ_F32 || dt == SPARKQ_F16 || dt == SPARKQ_BF16; }
+static bool is_half_dtype(int dt) { return dt == SPARKQ_F16 || dt == SPARKQ_BF16; }
+static constexpr int64_t kI32Max = 2147483647LL;
+
+extern "C" {
+
+const char* sparkq_last_error(void) { return g_last_error; }
+
+int sparkq_abi_version(void) { return 1; }
+
+int sparkq_is_available(void) { return device_check() == SPARKQ_OK ? 1 : 0; }
+
+size_t sparkq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size) {
+  return w4a16_workspace(M, N, K, group_size);
+}
+
+int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, void* y, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, int x_dtype, int y_dtype, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  REQUIRE(x && w && scales && biases && y, "w4a16_linear: null tensor pointer");
+  REQUIRE(M > 0 && N > 0 && K > 0, "w4a16_linear: M, N and K must be positive");
+  REQUIRE(M <= kI32Max && N <= kI32Max && K <= kI32Max, "w4a16_linear: dimension too large");
+  REQUIRE_SUPPORTED(bits == 4, "w4a16_linear: only bits=4 is supported (got %d)", bits);
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "w4a16_linear: group_size must be 32, 64 or 128 (got %d)", group_size);
+  REQUIRE(K % group_size == 0, "w4a16_linear: K=%lld is not a multiple of group_size=%d",
+          (long long)K, group_size);
+  REQUIRE_SUPPORTED(K % 64 == 0, "w4a16_linear: K must be a multiple of 64 (got %lld)",
+                    (long long)K);
+  REQUIRE_SUPPORTED(is_half_dtype(x_dtype), "w4a16_linear: x must be bfloat16 or float16");
+  REQUIRE(y_dtype == x_dtype || y_dtype == SPARKQ_F32,
+          "w4a16_linear: y dtype must equal x dtype or be float32");
+  REQUIRE(aligned(x, 16) && aligned(w, 16), "w4a16_linear: x and w must be 16-byte aligned");
+  REQUIRE(aligned(scales, 4) && aligned(biases, 4) && aligned(y, 4),
+          "w4a16_linear: scales, biases and y must be 4-byte aligned");
+  DEVICE_OK();
+  return w4a16_linear(x, w, scales, biases, y, M, N, K, group_size, x_dtype, y_dtype, workspace,
+                      workspace_bytes, (hipStream_t)stream);
+}
+
+int sparkq_w4a16_dequantize(const uint32_t* w, const void* scales, const void* biases, float* out,
+                            int64_t N, int64_t K, int group_size, int scale_dtype, void* stream) {
+  REQUIRE(w && scales && biases && out, "w4a16_dequantize: null tensor pointer");
+  REQUIRE(N > 0 && K > 0 && N * K / 8 <= kI32Max * 64LL, "w4a16_dequantize: bad shape");
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "w4a16_dequantize: group_size must be 32, 64 or 128");
+  REQUIRE(K % group_size == 0, "w4a16_dequantize: K not a multiple of group_size");
+  REQUIRE_SUPPORTED(is_half_dtype(scale_dtype), "w4a16_dequantize: scales must be bf16 or f16");
+  REQUIRE(aligned(out, 16) && aligned(w, 4), "w4a16_dequantize: misaligned pointer");
+  DEVICE_OK();
+  return w4a16_dequantize(w, scales, biases, out, N, K, group_size, scale_dtype,
+                          (hipStream_t)stream);
+}
+
+int sparkq_w4_quantize(const void* w, uint32_t* wq, void* scales, void* biases, int64_t N,
+                       int64_t K, int group_size, int dtype, void* stream) {
+  REQUIRE(w && wq && scales && biases, "w4_quantize: null tensor pointer");
+  REQUIRE(N > 0 && K > 0, "w4_quantize: N and K must be positive");
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "w4_quantize: group_size must be 32, 64 or 128");
+  REQUIRE(K % group_size == 0, "w4_quantize: K not a multiple of group_size");
+  REQUIRE_SUPPORTED(is_half_dtype(dtype), "w4_quantize: weights must be bf16 or f16");
+  DEVICE_OK();
+  return w4_quantize(w, wq, scales, biases, N, K, group_size, dtype, (hipStream_t)stream);
+}
+
+int sparkq_a8_quantize_per_token(const void* x, int8_t* q, float* scales, int64_t M, int64_t K,
+                                 int x_dtype, void* stream) {
+  REQUIRE(x && q && scales, "a8_quantize_per_token: null tensor pointer");
+  REQUIRE(M > 0 && K > 0 && M <= kI32Max, "a8_quantize_per_token: bad shape");
+  REQUIRE(is_float_dtype(x_dtype), "x must have dtype float16, bfloat16, or float32.");
+  DEVICE_OK();
+  return a8_quantize(x, q, scales, M, K, x_dtype, (hipStream_t)stream);
+}
+
+size_t sparkq_int8_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return i8_matmul_workspace(M, N, K);
+}
+
+// Mirrors validate_dimensions, X/src/spark_w8a8.cpp:51-65
+static int validate_i8_dims(const char* op, int64_t M, int64_t N, int64_t K) {
+  REQUIRE(M > 0 && N > 0 && K > 0, "%s: Expected nonempty x[..., K] and weight[N, K] with matching K.", op);
+  REQUIRE(K % 32 == 0 && K <= 131040, "%s: K must be a multiple of 32 in [32, 131040].", op);
+  REQUIRE(M <= kI32Max && N <= kI32Max, "%s: dimension too large", op);
+  return SPARKQ_OK;
+}
+
+int sparkq_int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N,
+                           int64_t K, void* workspace, size_t workspace_bytes, void* stream) {
+  REQUIRE(a && b && c, "int8_matmul_i32: null tensor pointer");
+  if (int rc = validate_i8_dims("int8_matmul_i32", M, N, K)) return rc;
+  REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(c, 4),
+          "int8_matmul_i32: a and b must be 16-byte aligned");
+  DEVICE_OK();
+  return int8_matmul_i32(a, b, c, M, N, K, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+size_t sparkq_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return w8a8_workspace(M, N, K);
+}
+
+int sparkq_w8a8_linear(const void* x, const int8_t* w, const float* w_scales, const void* bias,
+                       int bias_dtype, void* y, int64_t M, int64_t N, int64_t K, int x_dtype,
+                       int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  REQUIRE(x && w && w_scales && y, "w8a8_linear: null tensor pointer");
+  if (int rc = validate_i8_dims("w8a8_linear", M, N, K)) return rc;
+  REQUIRE(is_float_dtype(x_dtype), "x must have dtype float16, bfloat16, or float32.");
+  REQUIRE(y_dtype == x_dtype || y_dtype == SPARKQ_F32,
+          "w8a8_linear: y dtype must equal x dtype or be float32");
+  REQUIRE(bias == nullptr || is_float_dtype(bias_dtype),
+          "bias must have shape [N] and a real floating dtype.");
+  REQUIRE(aligned(w, 16) && aligned(w_scales, 4), "w8a8_linear: misaligned weight pointer");
+  REQUIRE(aligned(workspace, 256), "w8a8_linear: workspace must be 256-byte aligned");
+  DEVICE_OK();
+  return w8a8_linear(x, w, w_scales, bias, bias_dtype, y, M, N, K, x_dtype, y_dtype, workspace,
+                     workspace_bytes, (hipStream_t)stream);
+}
+
+size_t sparkq_int8kv_sdpa_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int64_t D) {
+  return sdpa_workspace(B, Hq, N, D);
+}
+
+int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes, const void* k_scales,
+                              const void* k_biases, const void* v_codes, const void* v_scales,
+                              const void* v_biases, void* out, int64_t B, int64_t Hq,
+                              int64_t Hkv, int64_t N, int64_t D, int group_size, int kv_format,
+                              int q_dtype, int out_dtype, float scale, const int64_t* strides,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  REQUIRE(q && k_codes && k_scales && v_codes && v_scales && out && strides,
+          "int8kv_sdpa_decode: null tensor pointer");
+  REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && N > 0 && D > 0,
+          "Nonempty inputs and query heads divisible by KV heads required");
+  REQUIRE(Hq % Hkv == 0, "Nonempty inputs and query heads divisible by KV heads required");
+  REQUIRE(B * Hkv <= 65535 && N <= kI32Max && B * Hq <= kI32Max, "int8kv_sdpa_decode: shape too large");
+  const int64_t gqa = Hq / Hkv;
+  REQUIRE_SUPPORTED(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8,
+                    "int8kv_sdpa_decode: query heads per KV head must be 1, 2, 4 or 8");
+  REQUIRE_SUPPORTED(D == 64 || D == 128 || D == 256,
+                    "int8kv_sdpa_decode: head dim must be 64, 128 or 256");
+  REQUIRE(std::isfinite(scale), "scale must be a finite Python number");
+  REQUIRE(is_float_dtype(q_dtype), "Q and metadata must be float16, bfloat16 or float32");
+  REQUIRE(out_dtype == q_dtype || out_dtype == SPARKQ_F32,
+          "int8kv_sdpa_decode: out dtype must equal q dtype or be float32");
+  REQUIRE(kv_format == SPARKQ_KV_S8_F16SCALE || kv_format == SPARKQ_KV_AFFINE_U8,
+          "int8kv_sdpa_decode: unknown kv_format %d", kv_format);
+  if (kv_format == SPARKQ_KV_AFFINE_U8) {
+    REQUIRE(k_biases && v_biases, "int8kv_sdpa_decode: affine format needs biases");
+    REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+            "Supported affine formats: bits 2/4/8, group size 32/64/128");
+    REQUIRE(D % group_size == 0, "Incompatible key packed shape, affine metadata or dtype");
+  }
+  for (int i : {0, 1, 2, 6, 7, 8})
+    REQUIRE(strides[i] % 8 == 0 && strides[i] >= 0,
+            "int8kv_sdpa_decode: code strides must be non-negative multiples of 8 bytes");
+  for (int i : {3, 4, 5, 9, 10, 11})
+    REQUIRE(strides[i] >= 0, "int8kv_sdpa_decode: negative scale stride");
+  REQUIRE(aligned(k_codes, 8) && aligned(v_codes, 8), "int8kv_sdpa_decode: codes must be 8-byte aligned");
+  DEVICE_OK();
+  return int8kv_sdpa_decode(q, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases, out, B,
+                            Hq, Hkv, N, D, group_size, kv_format, q_dtype, out_dtype, scale,
+                            strides, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int sparkq_kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_t D,
+                          int x_dtype, void* stream) {
+  REQUIRE(x && codes && scales, "kv_quantize_s8: null tensor pointer");
+  REQUIRE(R > 0 && D > 0, "kv_quantize_s8: R and D must be positive");
+  REQUIRE(is_float_dtype(x_dtype), "kv_quantize_s8: x must be float16, bfloat16 or float32");
+  DEVICE_OK();
+  return kv_quantize_s8(x, codes, scales, R, D, x_dtype, (hipStream_t)stream);
+}
+
+}  // extern "C"

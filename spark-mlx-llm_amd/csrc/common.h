@@ -1,0 +1,121 @@
+// common.h -- device helpers shared by the gfx950 kernels of libsparkq.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sparkq.h"
+
+namespace sparkq {
+
+// ---------------------------------------------------------------------------
+// vector types used as MFMA operands (gfx950, wave64)
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// 16-bit float <-> fp32 (bit-level, round-to-nearest-even)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float((uint32_t)h << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Element traits of the 16-bit activation types. OFFSET/MAGIC give the
+// exponent pattern under which a 4-bit code q placed in the low mantissa bits
+// reads as exactly OFFSET + q.
+struct BF16 {
+  static constexpr int code = SPARKQ_BF16;
+  static constexpr uint32_t MAGIC = 0x43004300u;  // bf16 128.0 in each half
+  static constexpr float OFFSET = 128.0f;
+  __device__ static __forceinline__ float to_f32(uint16_t h) { return bf16_to_f32(h); }
+  __device__ static __forceinline__ uint16_t from_f32(float f) { return f32_to_bf16(f); }
+};
+struct F16 {
+  static constexpr int code = SPARKQ_F16;
+  static constexpr uint32_t MAGIC = 0x64006400u;  // fp16 1024.0 in each half
+  static constexpr float OFFSET = 1024.0f;
+  __device__ static __forceinline__ float to_f32(uint16_t h) { return f16_to_f32(h); }
+  __device__ static __forceinline__ uint16_t from_f32(float f) { return f32_to_f16(f); }
+};
+
+// 32x32x16 MFMA on 16-bit operands held as four packed uint32 registers.
+template <typename T>
+__device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c);
+template <>
+__device__ __forceinline__ f32x16_t mfma32x32x16<BF16>(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16_t mfma32x32x16<F16>(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Decode one uint32 of eight 4-bit codes (code j at bits 4j) into the four
+// packed 16-bit pairs (OFFSET+q[2i], OFFSET+q[2i+1]), i = 0..3, in natural k
+// order: a byte permute pulls code 2i from w and code 2i+1 from w>>4 into the
+// low nibble of each half, and one and-or masks the nibble under MAGIC.
+template <typename T>
+__device__ __forceinline__ u32x4_t decode_w4(uint32_t w) {
+  const uint32_t ws = w >> 4;
+  u32x4_t r;
+  r.x = (__builtin_amdgcn_perm(ws, w, 0x0C040C00u) & 0x000F000Fu) | T::MAGIC;
+  r.y = (__builtin_amdgcn_perm(ws, w, 0x0C050C01u) & 0x000F000Fu) | T::MAGIC;
+  r.z = (__builtin_amdgcn_perm(ws, w, 0x0C060C02u) & 0x000F000Fu) | T::MAGIC;
+  r.w = (__builtin_amdgcn_perm(ws, w, 0x0C070C03u) & 0x000F000Fu) | T::MAGIC;
+  return r;
+}
+
+// Output row of accumulator v held by lane l for a 32x32 MFMA tile.
+__device__ __forceinline__ int mfma32_row(int lane, int v) {
+  return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+}
+
+// Store one fp32 as the requested output dtype.
+__device__ __forceinline__ void store_out(void* y, int64_t idx, float v, int dtype) {
+  if (dtype == SPARKQ_F32) {
+    reinterpret_cast<float*>(y)[idx] = v;
+  } else if (dtype == SPARKQ_BF16) {
+    reinterpret_cast<uint16_t*>(y)[idx] = f32_to_bf16(v);
+  } else {
+    reinterpret_cast<uint16_t*>(y)[idx] = f32_to_f16(v);
+  }
+}
+
+__device__ __forceinline__ float load_in(const void* p, int64_t idx, int dtype) {
+  if (dtype == SPARKQ_F32) return reinterpret_cast<const float*>(p)[idx];
+  uint16_t h = reinterpret_cast<const uint16_t*>(p)[idx];
+  return dtype == SPARKQ_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+}  // namespace sparkq
+
+// ---------------------------------------------------------------------------
+// host-side helpers shared by the launchers (defined in abi.cpp)
+// ---------------------------------------------------------------------------
+namespace sparkq {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+int device_check();
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
+}  // namespace sparkq

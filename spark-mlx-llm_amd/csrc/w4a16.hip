@@ -1,0 +1,627 @@
+// w4a16.hip -- MLX-affine W4A16 quantized linear on gfx950.
+//
+// y[m,n] = sum_g s[n,g] * (sum_{k in g} x[m,k] * q[n,k]) + b[n,g] * X_g[m]
+// with X_g[m] = sum_{k in g} x[m,k]. The MFMA consumes the 4-bit codes as the
+// exact 16-bit values OFFSET+q (one byte-permute and one and-or per pair), so
+// the per-group epilogue uses b' = b - OFFSET*s in place of b. Products of
+// codes and activations are exact; accumulation and the epilogue are fp32.
+//
+// Kernels
+//   w4_dequant_kernel   exact fp32 q*s+b (debug / bit-exact check entry)
+//   w4_quantize_kernel  affine 4-bit quantizer (format producer)
+//   w4_skinny_kernel    M <= 32: weight streaming, 32 rows x 64 k per wave
+//                       step, MFMA 32x32x16, in-workgroup split-K over waves,
+//                       optional cross-workgroup split-K into fp32 partials
+//   splitk_reduce_kernel  sums the partials in a fixed order -> y
+//   xsum_kernel         group sums X_g[m] for the GEMM, layout [K/G][M]
+//   w4_gemm_kernel      M > 32: 128x128x64 LDS tiles (A bf16/f16, B decoded
+//                       to OFFSET+q), double-buffered, MFMA 32x32x16
+#include "common.h"
+
+namespace sparkq {
+
+// ---------------------------------------------------------------------------
+// exact dequantization
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void w4_dequant_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+    const uint16_t* __restrict__ b, float* __restrict__ out, int64_t N,
+    int64_t K, int G) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t kw = K / 8;
+  if (idx >= N * kw) return;
+  const int64_t n = idx / kw;
+  const int64_t k0 = (idx - n * kw) * 8;
+  const int64_t gi = n * (K / G) + k0 / G;
+  const float sv = T::to_f32(s[gi]);
+  const float bv = T::to_f32(b[gi]);
+  const uint32_t v = w[idx];
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = (float)((v >> (4 * j)) & 15u) * sv + bv;
+  f32x4_t* dst = reinterpret_cast<f32x4_t*>(out + n * K + k0);
+  dst[0] = f32x4_t{o[0], o[1], o[2], o[3]};
+  dst[1] = f32x4_t{o[4], o[5], o[6], o[7]};
+}
+
+// ---------------------------------------------------------------------------
+// affine 4-bit quantizer: one thread per group
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void w4_quantize_kernel(
+    const uint16_t* __restrict__ w, uint32_t* __restrict__ wq,
+    uint16_t* __restrict__ s, uint16_t* __restrict__ b, int64_t N, int64_t K,
+    int G) {
+  const int64_t ng = K / G;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= N * ng) return;
+  const int64_t n = gid / ng, g = gid - n * ng;
+  const uint16_t* v = w + n * K + g * G;
+  float mn = T::to_f32(v[0]), mx = mn;
+  for (int i = 1; i < G; ++i) {
+    const float f = T::to_f32(v[i]);
+    mn = f < mn ? f : mn;
+    mx = f > mx ? f : mx;
+  }
+  const uint16_t s16 = T::from_f32((mx - mn) / 15.0f);
+  const uint16_t b16 = T::from_f32(mn);
+  s[gid] = s16;
+  b[gid] = b16;
+  const float sf = T::to_f32(s16), bf = T::to_f32(b16);
+  uint32_t* dst = wq + n * (K / 8) + g * (G / 8);
+  for (int i = 0; i < G / 8; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float q = 0.0f;
+      if (sf != 0.0f) {
+        q = __builtin_rintf((T::to_f32(v[8 * i + j]) - bf) / sf);
+        q = q < 0.0f ? 0.0f : (q > 15.0f ? 15.0f : q);
+      }
+      word |= (uint32_t)q << (4 * j);
+    }
+    dst[i] = word;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// skinny kernel (M <= MB <= 32)
+// ---------------------------------------------------------------------------
+// Workgroup = 4 waves; tile = 32 weight rows; the workgroup's K range
+// (a split of cps 64-k chunks) is shared round-robin by its waves.
+// Wave step: lane (n = l%32, j = l/32) holds 16 bytes = 32 codes of row n at
+// k = 64c + 32j, i.e. four MFMA k-slots of 8; the A operand is the matching
+// 16 bytes of x row m = l%32 read from an LDS copy of the split's x slab.
+// Each 64-k chunk ends with the per-group epilogue in fp32.
+constexpr int kSkinnyU = 4;  // chunks a wave keeps in flight per batch
+
+template <typename T, int G>
+struct ChunkMeta {
+  // (s, b) of the group(s) covering chunk c for a lane's row; for G = 32 the
+  // low half is group 2c and the high half group 2c+1.
+  __device__ static __forceinline__ void load(const uint16_t* srow,
+                                              const uint16_t* brow, int c,
+                                              uint32_t& s, uint32_t& b) {
+    if constexpr (G == 32) {
+      s = *reinterpret_cast<const uint32_t*>(srow + 2 * c);
+      b = *reinterpret_cast<const uint32_t*>(brow + 2 * c);
+    } else if constexpr (G == 64) {
+      s = srow[c];
+      b = brow[c];
+    } else {
+      s = srow[c >> 1];
+      b = brow[c >> 1];
+    }
+  }
+};
+
+template <typename T, int G, int MB>
+__global__ __launch_bounds__(256, 2) void w4_skinny_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ sc, const uint16_t* __restrict__ bi,
+    float* __restrict__ part, void* __restrict__ y, int y_dtype, int M, int N,
+    int K, int cps) {
+  constexpr int VM = MB / 2;  // accumulators per lane holding rows < MB
+  constexpr int U = kSkinnyU;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane >> 5;
+  const int n0 = blockIdx.x * 32;
+  const int split = blockIdx.y;
+  const int nchunks = K >> 6;
+  const int c_begin = split * cps;
+  const int nc = min(cps, nchunks - c_begin);
+  const int ngroups = K / G;
+
+  // LDS: x slab [M][nc*64 + 8] (16-bit), then half-chunk sums [2*nc][MB] fp32
+  const int xpitch = nc * 64 + 8;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  float* xh = reinterpret_cast<float*>(smem + (size_t)M * xpitch * 2);
+  float* red = reinterpret_cast<float*>(smem);  // reused after the main loop
+
+  const int n = n0 + (lane & 31);
+  const int nr = n < N ? n : N - 1;
+  const uint32_t* wrow = w + (int64_t)nr * (K >> 3) + (int64_t)c_begin * 8 + 4 * j;
+  const uint16_t* srow = sc + (int64_t)nr * ngroups;
+  const uint16_t* brow = bi + (int64_t)nr * ngroups;
+
+  u32x4_t wa[U], wb[U];
+  uint32_t sa[U], ba[U], sb[U], bbv[U];
+
+  auto load_batch = [&](int cl0, u32x4_t* wv, uint32_t* sv, uint32_t* bv) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cl = cl0 + 4 * u;
+      if (cl < nc) {
+        wv[u] = *reinterpret_cast<const u32x4_t*>(wrow + (int64_t)cl * 8);
+        ChunkMeta<T, G>::load(srow, brow, c_begin + cl, sv[u], bv[u]);
+      }
+    }
+  };
+
+  // issue the first weight batch before staging x
+  load_batch(wave, wa, sa, ba);
+
+  // stage x[0:M][c_begin*64 : +nc*64] into LDS (16-byte pieces)
+  {
+    const int pieces_per_row = nc * 8;
+    const int total = M * pieces_per_row;
+    for (int p = tid; p < total; p += 256) {
+      const int m = p / pieces_per_row, pc = p - m * pieces_per_row;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(
+          x + (int64_t)m * K + (int64_t)c_begin * 64 + pc * 8);
+      *reinterpret_cast<u32x4_t*>(xs + m * xpitch + pc * 8) = v;
+    }
+  }
+  __syncthreads();
+  // half-chunk (32 k) sums of x, rows >= M are zero
+  for (int p = tid; p < 2 * nc * MB; p += 256) {
+    const int h = p / MB, m = p - h * MB;
+    float s = 0.0f;
+    if (m < M) {
+      const uint16_t* src = xs + m * xpitch + h * 32;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) s += T::to_f32(src[i]);
+    }
+    xh[h * MB + m] = s;
+  }
+  __syncthreads();
+
+  float acc[VM];
+#pragma unroll
+  for (int v = 0; v < VM; ++v) acc[v] = 0.0f;
+
+  const int am = lane & 31;
+  const bool a_ok = am < M;
+  const uint16_t* arow = xs + (a_ok ? am : 0) * xpitch + 32 * j;
+
+  auto compute_batch = [&](int cl0, const u32x4_t* wv, const uint32_t* sv,
+                           const uint32_t* bv) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cl = cl0 + 4 * u;
+      if (cl < nc) {
+        f32x16_t t0 = {}, t1 = {};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const u32x4_t bq = decode_w4<T>(wv[u][t]);
+          u32x4_t a = {0u, 0u, 0u, 0u};
+          if (a_ok) a = *reinterpret_cast<const u32x4_t*>(arow + cl * 64 + 8 * t);
+          if constexpr (G == 32) {
+            const u32x4_t z = {0u, 0u, 0u, 0u};
+            t0 = mfma32x32x16<T>(j == 0 ? a : z, bq, t0);
+            t1 = mfma32x32x16<T>(j == 1 ? a : z, bq, t1);
+          } else {
+            t0 = mfma32x32x16<T>(a, bq, t0);
+          }
+        }
+        const float s0 = T::to_f32((uint16_t)(sv[u] & 0xFFFFu));
+        const float b0 = fmaf(-T::OFFSET, s0, T::to_f32((uint16_t)(bv[u] & 0xFFFFu)));
+        const float* h0 = xh + (2 * cl) * MB + 4 * j;
+        const float* h1 = h0 + MB;
+        if constexpr (G == 32) {
+          const float s1 = T::to_f32((uint16_t)(sv[u] >> 16));
+          const float b1 = fmaf(-T::OFFSET, s1, T::to_f32((uint16_t)(bv[u] >> 16)));
+#pragma unroll
+          for (int q4 = 0; q4 < VM / 4; ++q4) {
+            const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(h0 + 8 * q4);
+            const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(h1 + 8 * q4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int v = 4 * q4 + r;
+              float a0 = fmaf(s0, t0[v], acc[v]);
+              a0 = fmaf(b0, x0[r], a0);
+              a0 = fmaf(s1, t1[v], a0);
+              acc[v] = fmaf(b1, x1[r], a0);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int q4 = 0; q4 < VM / 4; ++q4) {
+            const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(h0 + 8 * q4);
+            const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(h1 + 8 * q4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int v = 4 * q4 + r;
+              const float a0 = fmaf(s0, t0[v], acc[v]);
+              acc[v] = fmaf(b0, x0[r] + x1[r], a0);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  for (int base = wave; base < nc; base += 8 * U) {
+    load_batch(base + 4 * U, wb, sb, bbv);
+    compute_batch(base, wa, sa, ba);
+    load_batch(base + 8 * U, wa, sa, ba);
+    compute_batch(base + 4 * U, wb, sb, bbv);
+  }
+
+  // cross-wave reduction through LDS (aliases the x slab)
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < VM; ++v) red[(wave * VM + v) * 64 + lane] = acc[v];
+  __syncthreads();
+  for (int e = tid; e < VM * 64; e += 256) {
+    const int v = e >> 6, l = e & 63;
+    const float s = red[(0 * VM + v) * 64 + l] + red[(1 * VM + v) * 64 + l] +
+                    red[(2 * VM + v) * 64 + l] + red[(3 * VM + v) * 64 + l];
+    const int m = mfma32_row(l, v);
+    const int nn = n0 + (l & 31);
+    if (m < M && nn < N) {
+      if (part)
+        part[((int64_t)split * M + m) * N + nn] = s;
+      else
+        store_out(y, (int64_t)m * N + nn, s, y_dtype);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const float* __restrict__ part, void* __restrict__ y, int y_dtype,
+    int64_t MN, int S) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  float s = 0.0f;
+  for (int k = 0; k < S; ++k) s += part[(int64_t)k * MN + i];
+  store_out(y, i, s, y_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// GEMM (M > 32)
+// ---------------------------------------------------------------------------
+// group sums X_g[m] in fp32, stored [K/G][M]; one thread per (m, g)
+template <typename T>
+__global__ __launch_bounds__(256) void xsum_kernel(const uint16_t* __restrict__ x,
+                                                   float* __restrict__ xsum,
+                                                   int M, int K, int G) {
+  const int ng = K / G;
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= (int64_t)M * ng) return;
+  const int m = (int)(id / ng), g = (int)(id - (int64_t)m * ng);
+  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(x + (int64_t)m * K + (int64_t)g * G);
+  float s = 0.0f;
+  for (int i = 0; i < G / 8; ++i) {
+    const u32x4_t v = src[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s += T::to_f32((uint16_t)(v[e] & 0xFFFFu));
+      s += T::to_f32((uint16_t)(v[e] >> 16));
+    }
+  }
+  xsum[(int64_t)g * M + m] = s;
+}
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+
+// element offset of the 16-byte piece (row, kc) in a swizzled [128][64] tile
+__device__ __forceinline__ int tile_off(int row, int kc) {
+  return row * 64 + ((kc ^ (row & 7)) << 3);
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(256, 2) void w4_gemm_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ sc, const uint16_t* __restrict__ bi,
+    const float* __restrict__ xsum, void* __restrict__ y, int y_dtype, int M,
+    int N, int K) {
+  constexpr int GPS = G == 32 ? 2 : 1;  // groups starting inside one k-step
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM * kBK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kBN * kBK];
+  __shared__ __attribute__((aligned(16))) float SBs[2][GPS][kBN][2];
+  __shared__ __attribute__((aligned(16))) float XSs[2][GPS][kBM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+  const int ngroups = K / G;
+  const int nsteps = K / kBK;
+
+  // global -> register staging
+  u32x4_t ra[4], rb;
+  float rs = 0.0f, rbias = 0.0f, rx = 0.0f;
+
+  auto load = [&](int step) {
+    const int k0 = step * kBK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i, row = p >> 3, kc = p & 7;
+      const int gm = m0 + row;
+      ra[i] = u32x4_t{0u, 0u, 0u, 0u};
+      if (gm < M) ra[i] = *reinterpret_cast<const u32x4_t*>(x + (int64_t)gm * K + k0 + kc * 8);
+    }
+    {
+      const int row = tid >> 1, half = tid & 1, gn = n0 + row;
+      rb = u32x4_t{0u, 0u, 0u, 0u};
+      if (gn < N) rb = *reinterpret_cast<const u32x4_t*>(w + (int64_t)gn * (K >> 3) + (k0 >> 3) + 4 * half);
+    }
+    if (tid < 128 * GPS) {
+      const int gi = tid >> 7, row = tid & 127;
+      const int g = (G == 32) ? 2 * step + gi : (k0 / G);
+      const int gn = n0 + row, gm = m0 + row;
+      rs = 0.0f;
+      rbias = 0.0f;
+      rx = 0.0f;
+      if (gn < N) {
+        rs = T::to_f32(sc[(int64_t)gn * ngroups + g]);
+        rbias = T::to_f32(bi[(int64_t)gn * ngroups + g]);
+      }
+      if (gm < M) rx = xsum[(int64_t)g * M + gm];
+    }
+  };
+  auto store = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i, row = p >> 3, kc = p & 7;
+      *reinterpret_cast<u32x4_t*>(&As[st][tile_off(row, kc)]) = ra[i];
+    }
+    {
+      const int row = tid >> 1, half = tid & 1;
+#pragma unroll
+      for (int wi = 0; wi < 4; ++wi)
+        *reinterpret_cast<u32x4_t*>(&Bs[st][tile_off(row, 4 * half + wi)]) = decode_w4<T>(rb[wi]);
+    }
+    if (tid < 128 * GPS) {
+      const int gi = tid >> 7, row = tid & 127;
+      SBs[st][gi][row][0] = rs;
+      SBs[st][gi][row][1] = fmaf(-T::OFFSET, rs, rbias);
+      XSs[st][gi][row] = rx;
+    }
+  };
+
+  f32x16_t acc[2][2], tmp[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      acc[a][b] = f32x16_t{};
+      tmp[a][b] = f32x16_t{};
+    }
+
+  load(0);
+  store(0);
+  __syncthreads();
+
+  for (int step = 0; step < nsteps; ++step) {
+    const int st = step & 1;
+    if (step + 1 < nsteps) load(step + 1);
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+      const int kc = 2 * ss + j;
+      u32x4_t af[2], bf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int ar = wm * 64 + t * 32 + (lane & 31);
+        const int br = wn * 64 + t * 32 + (lane & 31);
+        af[t] = *reinterpret_cast<const u32x4_t*>(&As[st][tile_off(ar, kc)]);
+        bf[t] = *reinterpret_cast<const u32x4_t*>(&Bs[st][tile_off(br, kc)]);
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) tmp[a][b] = mfma32x32x16<T>(af[a], bf[b], tmp[a][b]);
+
+      const bool group_end =
+          (G == 32) ? (ss == 1 || ss == 3) : (G == 64 ? ss == 3 : (ss == 3 && (step & 1)));
+      if (group_end) {
+        const int gi = (G == 32) ? (ss >> 1) : 0;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int br = wn * 64 + b * 32 + (lane & 31);
+          const float s = SBs[st][gi][br][0], bp = SBs[st][gi][br][1];
+#pragma unroll
+          for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const int mr = wm * 64 + a * 32 + 8 * q4 + 4 * j;
+              const f32x4_t xv = *reinterpret_cast<const f32x4_t*>(&XSs[st][gi][mr]);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int v = 4 * q4 + r;
+                const float t = fmaf(s, tmp[a][b][v], acc[a][b][v]);
+                acc[a][b][v] = fmaf(bp, xv[r], t);
+              }
+            }
+            tmp[a][b] = f32x16_t{};
+          }
+        }
+      }
+    }
+    if (step + 1 < nsteps) store(st ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int gn = n0 + wn * 64 + b * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gm = m0 + wm * 64 + a * 32 + mfma32_row(lane, v);
+        if (gm < M && gn < N) store_out(y, (int64_t)gm * N + gn, acc[a][b][v], y_dtype);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct SkinnyPlan {
+  int MB;     // 8, 16 or 32
+  int S;      // workgroup splits of K
+  int cps;    // 64-k chunks per split
+  size_t lds;
+};
+
+static SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K) {
+  SkinnyPlan p;
+  p.MB = M <= 8 ? 8 : (M <= 16 ? 16 : 32);
+  const int64_t tiles = cdiv(N, 32);
+  const int64_t nchunks = K / 64;
+  // x slab in LDS <= 32 KB
+  int64_t max_cps = (32768 / (M * 2) - 8) / 64;
+  if (max_cps < 1) max_cps = 1;
+  int64_t S = cdiv(1024, tiles);                  // aim at ~1024 workgroups
+  const int64_t s_cap = nchunks / 4 > 0 ? nchunks / 4 : 1;  // >= 4 chunks each
+  if (S > s_cap) S = s_cap;
+  if (S < 1) S = 1;
+  int64_t cps = cdiv(nchunks, S);
+  if (cps > max_cps) cps = max_cps;
+  S = cdiv(nchunks, cps);
+  p.S = (int)S;
+  p.cps = (int)cps;
+  const size_t slab = (size_t)M * (size_t)(cps * 64 + 8) * 2;
+  const size_t sums = (size_t)2 * cps * p.MB * 4;
+  const size_t red = (size_t)4 * (p.MB / 2) * 64 * 4;
+  p.lds = slab + sums > red ? slab + sums : red;
+  return p;
+}
+
+size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
+  if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
+  if (M <= 32) {
+    const SkinnyPlan p = plan_skinny(M, N, K);
+    return p.S > 1 ? round_up((size_t)p.S * M * N * 4, 256) : 0;
+  }
+  return round_up((size_t)(K / G) * M * 4, 256);
+}
+
+template <typename T, int G, int MB>
+static void launch_skinny_t(const SkinnyPlan& p, const void* x, const uint32_t* w,
+                            const void* s, const void* b, float* part, void* y,
+                            int ydt, int M, int N, int K, hipStream_t st) {
+  dim3 grid((unsigned)cdiv(N, 32), (unsigned)p.S);
+  hipLaunchKernelGGL((w4_skinny_kernel<T, G, MB>), grid, dim3(256), p.lds, st,
+                     (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b,
+                     part, y, ydt, M, N, K, p.cps);
+}
+
+template <typename T, int G>
+static void launch_skinny_g(const SkinnyPlan& p, const void* x, const uint32_t* w,
+                            const void* s, const void* b, float* part, void* y,
+                            int ydt, int M, int N, int K, hipStream_t st) {
+  if (p.MB == 8)
+    launch_skinny_t<T, G, 8>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+  else if (p.MB == 16)
+    launch_skinny_t<T, G, 16>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+  else
+    launch_skinny_t<T, G, 32>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+}
+
+template <typename T>
+static void launch_skinny(const SkinnyPlan& p, int G, const void* x, const uint32_t* w,
+                          const void* s, const void* b, float* part, void* y, int ydt,
+                          int M, int N, int K, hipStream_t st) {
+  if (G == 32)
+    launch_skinny_g<T, 32>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+  else if (G == 64)
+    launch_skinny_g<T, 64>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+  else
+    launch_skinny_g<T, 128>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+}
+
+template <typename T>
+static void launch_gemm(int G, const void* x, const uint32_t* w, const void* s,
+                        const void* b, float* xs, void* y, int ydt, int M, int N,
+                        int K, hipStream_t st) {
+  const int64_t nxs = (int64_t)M * (K / G);
+  hipLaunchKernelGGL(xsum_kernel<T>, dim3((unsigned)cdiv(nxs, 256)), dim3(256), 0, st,
+                     (const uint16_t*)x, xs, M, K, G);
+  dim3 grid((unsigned)cdiv(N, kBN), (unsigned)cdiv(M, kBM));
+#define SPARKQ_GEMM(GG)                                                              \
+  hipLaunchKernelGGL((w4_gemm_kernel<T, GG>), grid, dim3(256), 0, st, (const uint16_t*)x, \
+                     w, (const uint16_t*)s, (const uint16_t*)b, xs, y, ydt, M, N, K)
+  if (G == 32)
+    SPARKQ_GEMM(32);
+  else if (G == 64)
+    SPARKQ_GEMM(64);
+  else
+    SPARKQ_GEMM(128);
+#undef SPARKQ_GEMM
+}
+
+int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
+                 void* y, int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt,
+                 void* ws, size_t wsb, hipStream_t st) {
+  const size_t need = w4a16_workspace(M, N, K, G);
+  if (need > 0 && (ws == nullptr || wsb < need))
+    return set_error(SPARKQ_ERR_WORKSPACE,
+                     "w4a16_linear needs a workspace of %zu bytes (got %zu)", need, wsb);
+  if (M <= 32) {
+    const SkinnyPlan p = plan_skinny(M, N, K);
+    float* part = p.S > 1 ? reinterpret_cast<float*>(ws) : nullptr;
+    if (xdt == SPARKQ_BF16)
+      launch_skinny<BF16>(p, G, x, w, s, b, part, y, ydt, (int)M, (int)N, (int)K, st);
+    else
+      launch_skinny<F16>(p, G, x, w, s, b, part, y, ydt, (int)M, (int)N, (int)K, st);
+    if (int rc = check_launch("w4_skinny_kernel")) return rc;
+    if (p.S > 1) {
+      const int64_t MN = M * N;
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(MN, 256)), dim3(256), 0,
+                         st, part, y, ydt, MN, p.S);
+      if (int rc = check_launch("splitk_reduce_kernel")) return rc;
+    }
+    return SPARKQ_OK;
+  }
+  float* xs = reinterpret_cast<float*>(ws);
+  if (xdt == SPARKQ_BF16)
+    launch_gemm<BF16>(G, x, w, s, b, xs, y, ydt, (int)M, (int)N, (int)K, st);
+  else
+    launch_gemm<F16>(G, x, w, s, b, xs, y, ydt, (int)M, (int)N, (int)K, st);
+  return check_launch("w4_gemm_kernel");
+}
+
+int w4a16_dequantize(const uint32_t* w, const void* s, const void* b, float* out,
+                     int64_t N, int64_t K, int G, int sdt, hipStream_t st) {
+  const int64_t words = N * K / 8;
+  dim3 grid((unsigned)cdiv(words, 256));
+  if (sdt == SPARKQ_BF16)
+    hipLaunchKernelGGL(w4_dequant_kernel<BF16>, grid, dim3(256), 0, st, w,
+                       (const uint16_t*)s, (const uint16_t*)b, out, N, K, G);
+  else
+    hipLaunchKernelGGL(w4_dequant_kernel<F16>, grid, dim3(256), 0, st, w,
+                       (const uint16_t*)s, (const uint16_t*)b, out, N, K, G);
+  return check_launch("w4_dequant_kernel");
+}
+
+int w4_quantize(const void* w, uint32_t* wq, void* s, void* b, int64_t N, int64_t K,
+                int G, int dt, hipStream_t st) {
+  const int64_t groups = N * (K / G);
+  dim3 grid((unsigned)cdiv(groups, 256));
+  if (dt == SPARKQ_BF16)
+    hipLaunchKernelGGL(w4_quantize_kernel<BF16>, grid, dim3(256), 0, st,
+                       (const uint16_t*)w, wq, (uint16_t*)s, (uint16_t*)b, N, K, G);
+  else
+    hipLaunchKernelGGL(w4_quantize_kernel<F16>, grid, dim3(256), 0, st,
+                       (const uint16_t*)w, wq, (uint16_t*)s, (uint16_t*)b, N, K, G);
+  return check_launch("w4_quantize_kernel");
+}
+
+}  // namespace sparkq

@@ -1,0 +1,315 @@
+// w8a8.hip -- W8A8 projection on gfx950: per-token int8 activations,
+// per-channel int8 weights, exact int32 accumulation on the int8 MFMA.
+//
+// Kernels
+//   a8_quantize_kernel   one workgroup per token row: amax, scale = amax/127
+//                        (1 when 0), q = clamp(rint(x/scale), -127, 127);
+//                        bit-exact with X/src/kernels/w8a8_quantize.metal:11-27
+//   i8_skinny_kernel     32 weight rows per workgroup, 4 waves split K; lane
+//                        (n = l%32, j = l/32) feeds 16 bytes of row n straight
+//                        into v_mfma_i32_32x32x32_i8; the A operand is the
+//                        matching 16 bytes of the int8 activations from LDS;
+//                        m-blocks of 32 rows go to grid.z. Output is either the
+//                        raw int32 sums, int32 split-K partials, or the fused
+//                        epilogue fmaf(float(acc)*sa[m], sw[n], bias[n]).
+//   i8_reduce_raw_kernel / i8_reduce_epilogue_kernel
+//                        fixed-order int32 sum of the split-K partials, then
+//                        the raw store or the epilogue
+#include "common.h"
+
+namespace sparkq {
+
+// ---------------------------------------------------------------------------
+// per-token quantizer
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void a8_quantize_kernel(
+    const void* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales,
+    int64_t K, int x_dtype) {
+  __shared__ float wmax[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  float amax = 0.0f;
+  for (int64_t k = tid; k < K; k += 256) amax = fmaxf(amax, fabsf(load_in(x, row * K + k, x_dtype)));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+  if (tid == 0) scales[row] = scale;
+  for (int64_t k = tid; k < K; k += 256) {
+    float v = __builtin_rintf(load_in(x, row * K + k, x_dtype) / scale);
+    v = fminf(fmaxf(v, -127.0f), 127.0f);
+    q[row * K + k] = (int8_t)v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// int8 weight-streaming MFMA kernel
+// ---------------------------------------------------------------------------
+enum I8Out { kOutRaw = 0, kOutPartial = 1, kOutEpilogue = 2 };
+
+struct I8Args {
+  const int8_t* a;      // [M,K] int8 activations
+  const int8_t* b;      // [N,K] int8 weights
+  int32_t* c_raw;       // [M,N] (kOutRaw) or partials [S][M][N] (kOutPartial)
+  void* y;              // [M,N] (kOutEpilogue)
+  const float* sa;      // [M]
+  const float* sw;      // [N]
+  const void* bias;     // [N] or null
+  int bias_dtype;
+  int y_dtype;
+  int M, N, K;
+  int cps;              // 32-k chunks per split
+  int mode;
+};
+
+__device__ __forceinline__ i32x16_t mfma_i8(u32x4_t a, u32x4_t b, i32x16_t c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, a),
+                                               __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
+}
+
+constexpr int kI8U = 8;
+
+__global__ __launch_bounds__(256, 2) void i8_skinny_kernel(I8Args args) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int U = kI8U;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane >> 5;
+  const int M = args.M, N = args.N, K = args.K;
+  const int n0 = blockIdx.x * 32;
+  const int split = blockIdx.y;
+  const int m0 = blockIdx.z * 32;
+  const int mrows = min(32, M - m0);
+  const int nchunks = K >> 5;
+  const int c_begin = split * args.cps;
+  const int nc = min(args.cps, nchunks - c_begin);
+
+  const int pitch = nc * 32 + 16;
+  int8_t* xs = reinterpret_cast<int8_t*>(smem);
+  int32_t* red = reinterpret_cast<int32_t*>(smem);
+
+  const int n = n0 + (lane & 31);
+  const int nr = n < N ? n : N - 1;
+  const int8_t* brow = args.b + (int64_t)nr * K + (int64_t)c_begin * 32 + 16 * j;
+
+  u32x4_t wa[U], wb[U];
+  auto load_batch = [&](int cl0, u32x4_t* wv) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cl = cl0 + 4 * u;
+      if (cl < nc) wv[u] = *reinterpret_cast<const u32x4_t*>(brow + (int64_t)cl * 32);
+    }
+  };
+  load_batch(wave, wa);
+
+  {
+    const int pieces = nc * 2;  // 16-byte pieces per row
+    for (int p = tid; p < mrows * pieces; p += 256) {
+      const int m = p / pieces, pc = p - m * pieces;
+      *reinterpret_cast<u32x4_t*>(xs + m * pitch + pc * 16) = *reinterpret_cast<const u32x4_t*>(
+          args.a + (int64_t)(m0 + m) * K + (int64_t)c_begin * 32 + pc * 16);
+    }
+  }
+  __syncthreads();
+
+  const int am = lane & 31;
+  const bool a_ok = am < mrows;
+  const int8_t* arow = xs + (a_ok ? am : 0) * pitch + 16 * j;
+  i32x16_t acc = {};
+
+  auto compute_batch = [&](int cl0, const u32x4_t* wv) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cl = cl0 + 4 * u;
+      if (cl < nc) {
+        u32x4_t a = {0u, 0u, 0u, 0u};
+        if (a_ok) a = *reinterpret_cast<const u32x4_t*>(arow + cl * 32);
+        acc = mfma_i8(a, wv[u], acc);
+      }
+    }
+  };
+  for (int base = wave; base < nc; base += 8 * U) {
+    load_batch(base + 4 * U, wb);
+    compute_batch(base, wa);
+    load_batch(base + 8 * U, wa);
+    compute_batch(base + 4 * U, wb);
+  }
+
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < 16; ++v) red[(wave * 16 + v) * 64 + lane] = acc[v];
+  __syncthreads();
+  for (int e = tid; e < 16 * 64; e += 256) {
+    const int v = e >> 6, l = e & 63;
+    const int m = mfma32_row(l, v);
+    const int nn = n0 + (l & 31);
+    if (m < mrows && nn < N) {
+      const int32_t s = red[(0 * 16 + v) * 64 + l] + red[(1 * 16 + v) * 64 + l] +
+                        red[(2 * 16 + v) * 64 + l] + red[(3 * 16 + v) * 64 + l];
+      const int gm = m0 + m;
+      if (args.mode == kOutRaw) {
+        args.c_raw[(int64_t)gm * N + nn] = s;
+      } else if (args.mode == kOutPartial) {
+        args.c_raw[((int64_t)split * M + gm) * N + nn] = s;
+      } else {
+        const float bias = args.bias ? load_in(args.bias, nn, args.bias_dtype) : 0.0f;
+        const float t = (float)s * args.sa[gm];
+        store_out(args.y, (int64_t)gm * N + nn, fmaf(t, args.sw[nn], bias), args.y_dtype);
+      }
+    }
+  }
+}
+
+// fixed-order int32 sums of S partials [S][M][N]: raw store, or the epilogue
+__global__ __launch_bounds__(256) void i8_reduce_raw_kernel(const int32_t* __restrict__ part,
+                                                            int32_t* __restrict__ c,
+                                                            int64_t MN, int S) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  int32_t s = 0;
+  for (int k = 0; k < S; ++k) s += part[(int64_t)k * MN + i];
+  c[i] = s;
+}
+
+__global__ __launch_bounds__(256) void i8_reduce_epilogue_kernel(I8Args args, int S) {
+  const int64_t MN = (int64_t)args.M * args.N;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  int32_t s = 0;
+  for (int k = 0; k < S; ++k) s += args.c_raw[(int64_t)k * MN + i];
+  const int m = (int)(i / args.N), nn = (int)(i - (int64_t)m * args.N);
+  const float bias = args.bias ? load_in(args.bias, nn, args.bias_dtype) : 0.0f;
+  const float t = (float)s * args.sa[m];
+  store_out(args.y, i, fmaf(t, args.sw[nn], bias), args.y_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct I8Plan {
+  int S, cps;
+  size_t lds;
+};
+
+static I8Plan plan_i8(int64_t M, int64_t N, int64_t K) {
+  I8Plan p;
+  const int64_t mrows = M < 32 ? M : 32;
+  const int64_t tiles = cdiv(N, 32) * cdiv(M, 32);
+  const int64_t nchunks = K / 32;
+  int64_t max_cps = (32768 / mrows - 16) / 32;
+  if (max_cps < 1) max_cps = 1;
+  int64_t S = cdiv(1024, tiles);
+  const int64_t s_cap = nchunks / 8 > 0 ? nchunks / 8 : 1;
+  if (S > s_cap) S = s_cap;
+  if (S < 1) S = 1;
+  int64_t cps = cdiv(nchunks, S);
+  if (cps > max_cps) cps = max_cps;
+  S = cdiv(nchunks, cps);
+  p.S = (int)S;
+  p.cps = (int)cps;
+  const size_t slab = (size_t)mrows * (size_t)(cps * 32 + 16);
+  const size_t red = (size_t)4 * 16 * 64 * 4;
+  p.lds = slab > red ? slab : red;
+  return p;
+}
+
+static size_t i8_partial_bytes(int64_t M, int64_t N, int64_t K) {
+  const I8Plan p = plan_i8(M, N, K);
+  return p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
+}
+
+size_t w8a8_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  // int8 activations, fp32 scales, int32 partials (each 256-byte aligned)
+  return round_up((size_t)M * K, 256) + round_up((size_t)M * 4, 256) +
+         round_up(i8_partial_bytes(M, N, K), 256);
+}
+
+size_t i8_matmul_workspace(int64_t M, int64_t N, int64_t K) {
+  const size_t part = i8_partial_bytes(M, N, K);
+  return part ? round_up(part, 256) : 0;
+}
+
+static int launch_i8(const I8Args& args, const I8Plan& p, hipStream_t st) {
+  dim3 grid((unsigned)cdiv(args.N, 32), (unsigned)p.S, (unsigned)cdiv(args.M, 32));
+  hipLaunchKernelGGL(i8_skinny_kernel, grid, dim3(256), p.lds, st, args);
+  return check_launch("i8_skinny_kernel");
+}
+
+int a8_quantize(const void* x, int8_t* q, float* scales, int64_t M, int64_t K, int xdt,
+                hipStream_t st) {
+  hipLaunchKernelGGL(a8_quantize_kernel, dim3((unsigned)M), dim3(256), 0, st, x, q, scales,
+                     K, xdt);
+  return check_launch("a8_quantize_kernel");
+}
+
+int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N,
+                    int64_t K, void* ws, size_t wsb, hipStream_t st) {
+  const I8Plan p = plan_i8(M, N, K);
+  I8Args args{};
+  args.a = a;
+  args.b = b;
+  args.M = (int)M;
+  args.N = (int)N;
+  args.K = (int)K;
+  args.cps = p.cps;
+  if (p.S == 1) {
+    args.mode = kOutRaw;
+    args.c_raw = c;
+    return launch_i8(args, p, st);
+  }
+  const size_t need = i8_matmul_workspace(M, N, K);
+  if (ws == nullptr || wsb < need)
+    return set_error(SPARKQ_ERR_WORKSPACE,
+                     "int8_matmul_i32 needs a workspace of %zu bytes (got %zu)", need, wsb);
+  args.mode = kOutPartial;
+  args.c_raw = reinterpret_cast<int32_t*>(ws);
+  if (int rc = launch_i8(args, p, st)) return rc;
+  const int64_t MN = M * N;
+  hipLaunchKernelGGL(i8_reduce_raw_kernel, dim3((unsigned)cdiv(MN, 256)), dim3(256), 0, st,
+                     args.c_raw, c, MN, p.S);
+  return check_launch("i8_reduce_raw_kernel");
+}
+
+int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bias,
+                int bias_dtype, void* y, int64_t M, int64_t N, int64_t K, int xdt, int ydt,
+                void* ws, size_t wsb, hipStream_t st) {
+  const size_t need = w8a8_workspace(M, N, K);
+  if (ws == nullptr || wsb < need)
+    return set_error(SPARKQ_ERR_WORKSPACE,
+                     "w8a8_linear needs a workspace of %zu bytes (got %zu)", need, wsb);
+  unsigned char* base = reinterpret_cast<unsigned char*>(ws);
+  int8_t* q = reinterpret_cast<int8_t*>(base);
+  float* sa = reinterpret_cast<float*>(base + round_up((size_t)M * K, 256));
+  int32_t* part = reinterpret_cast<int32_t*>(base + round_up((size_t)M * K, 256) +
+                                             round_up((size_t)M * 4, 256));
+  if (int rc = a8_quantize(x, q, sa, M, K, xdt, st)) return rc;
+  const I8Plan p = plan_i8(M, N, K);
+  I8Args args{};
+  args.a = q;
+  args.b = w;
+  args.sa = sa;
+  args.sw = wsc;
+  args.bias = bias;
+  args.bias_dtype = bias_dtype;
+  args.y = y;
+  args.y_dtype = ydt;
+  args.M = (int)M;
+  args.N = (int)N;
+  args.K = (int)K;
+  args.cps = p.cps;
+  if (p.S == 1) {
+    args.mode = kOutEpilogue;
+    return launch_i8(args, p, st);
+  }
+  args.mode = kOutPartial;
+  args.c_raw = part;
+  if (int rc = launch_i8(args, p, st)) return rc;
+  const int64_t MN = M * N;
+  hipLaunchKernelGGL(i8_reduce_epilogue_kernel, dim3((unsigned)cdiv(MN, 256)), dim3(256), 0,
+                     st, args, p.S);
+  return check_launch("i8_reduce_epilogue_kernel");
+}
+
+}  // namespace sparkq

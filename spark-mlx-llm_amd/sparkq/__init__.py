@@ -1,0 +1,38 @@
+"""sparkq: MI355X (gfx950) kernels for Spark-MLX-LLM's quantized-linear hot path.
+
+sparkq.ext mirrors the extension API (spark_mlx_ext); sparkq.ops mirrors the
+operator dispatch layer (spark_mlx_llm/ops). Kernels live in libsparkq.so,
+called over the C-ABI declared in include/sparkq.h.
+"""
+
+from .ext import (
+    W8A8Linear,
+    affine_dequantize,
+    affine_quantize,
+    affine_quantized_matmul,
+    int8_matmul_int32,
+    int8_quantized_sdpa,
+    is_w8a8_available,
+    kv_quantize_s8,
+    prepare_w4a16_nax4,
+    quantize_per_token,
+    w4a16_multirow,
+    w4a16_qmv,
+    w8a8_linear,
+)
+
+__all__ = [
+    "W8A8Linear",
+    "affine_dequantize",
+    "affine_quantize",
+    "affine_quantized_matmul",
+    "int8_matmul_int32",
+    "int8_quantized_sdpa",
+    "is_w8a8_available",
+    "kv_quantize_s8",
+    "prepare_w4a16_nax4",
+    "quantize_per_token",
+    "w4a16_multirow",
+    "w4a16_qmv",
+    "w8a8_linear",
+]

@@ -1,0 +1,118 @@
+"""ctypes binding of libsparkq.so (include/sparkq.h).
+
+The library is loaded from this package directory. A missing or unloadable
+library raises ImportError-style RuntimeError at first use: there is no
+fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+__all__ = [
+    "F32", "F16", "BF16", "KV_S8_F16SCALE", "KV_AFFINE_U8",
+    "lib", "library_path", "dtype_code", "call", "stream_handle", "workspace",
+    "SparkqError",
+]
+
+F32, F16, BF16 = 0, 1, 2
+KV_S8_F16SCALE, KV_AFFINE_U8 = 0, 1
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_WORKSPACE = 0, -1, -2, -3, -4
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_LOCK = threading.Lock()
+
+P, I64, I, F, SZ = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float,
+                    ctypes.c_size_t)
+
+# name -> (restype, argtypes); mirrors include/sparkq.h
+SIGNATURES = {
+    "sparkq_last_error": (ctypes.c_char_p, []),
+    "sparkq_abi_version": (I, []),
+    "sparkq_is_available": (I, []),
+    "sparkq_w4a16_workspace_bytes": (SZ, [I64, I64, I64, I]),
+    "sparkq_w4a16_linear": (I, [P, P, P, P, P, I64, I64, I64, I, I, I, I, P, SZ, P]),
+    "sparkq_w4a16_dequantize": (I, [P, P, P, P, I64, I64, I, I, P]),
+    "sparkq_w4_quantize": (I, [P, P, P, P, I64, I64, I, I, P]),
+    "sparkq_a8_quantize_per_token": (I, [P, P, P, I64, I64, I, P]),
+    "sparkq_int8_matmul_workspace_bytes": (SZ, [I64, I64, I64]),
+    "sparkq_int8_matmul_i32": (I, [P, P, P, I64, I64, I64, P, SZ, P]),
+    "sparkq_w8a8_workspace_bytes": (SZ, [I64, I64, I64]),
+    "sparkq_w8a8_linear": (I, [P, P, P, P, I, P, I64, I64, I64, I, I, P, SZ, P]),
+    "sparkq_int8kv_sdpa_workspace_bytes": (SZ, [I64, I64, I64, I64]),
+    "sparkq_int8kv_sdpa_decode": (I, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64,
+                                      I, I, I, I, F, P, P, SZ, P]),
+    "sparkq_kv_quantize_s8": (I, [P, P, P, I64, I64, I, P]),
+}
+
+
+class SparkqError(RuntimeError):
+    """A HIP runtime failure reported by libsparkq."""
+
+
+def library_path() -> str:
+    return os.path.join(_HERE, "libsparkq.so")
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        with _LOCK:
+            if _LIB is None:
+                path = library_path()
+                if not os.path.exists(path):
+                    raise RuntimeError(
+                        f"libsparkq.so is not built ({path}); run "
+                        "python spark-mlx-llm_amd/build.py")
+                handle = ctypes.CDLL(path)
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _LIB = handle
+    return _LIB
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported floating dtype {dtype}") from None
+
+
+def stream_handle(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and map its status to the reference's exception types
+    (validation -> ValueError, runtime -> SparkqError)."""
+    rc = getattr(lib(), name)(*args)
+    if rc == OK:
+        return
+    msg = (lib().sparkq_last_error() or b"").decode(errors="replace")
+    if rc in (ERR_INVALID, ERR_UNSUPPORTED):
+        raise ValueError(msg)
+    raise SparkqError(f"{name}: {msg}")
+
+
+_WS: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int):
+    """Per (device, stream) scratch buffer; reuse is safe because every user
+    enqueues on that same stream."""
+    if nbytes <= 0:
+        return None, 0
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index, stream)
+    buf = _WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WS[key] = buf
+    return ctypes.c_void_p(buf.data_ptr()), buf.numel()

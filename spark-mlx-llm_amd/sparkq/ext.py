@@ -1,0 +1,431 @@
+"""Operator API of the MI355X kernels, mirroring spark_mlx_ext on torch tensors.
+
+Every op validates like its reference wrapper (TypeError/ValueError), then
+calls libsparkq on the current HIP stream of the input's device. Ops return
+without synchronising; inputs are never modified; non-contiguous inputs are
+copied (the reference's ensure_row_contiguous behaviour). There is no CPU or
+eager fallback: tensors must live on a gfx950 device.
+
+Reference: extensions/spark-mlx-ext/spark_mlx_ext/__init__.py:12-44.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from math import prod
+
+import torch
+from torch import nn
+
+from . import _lib
+from ._lib import BF16, F16, F32, KV_AFFINE_U8, KV_S8_F16SCALE
+
+__all__ = [
+    "W8A8Linear",
+    "affine_dequantize",
+    "affine_quantize",
+    "affine_quantized_matmul",
+    "int8_matmul_int32",
+    "int8_quantized_sdpa",
+    "is_w8a8_available",
+    "kv_quantize_s8",
+    "prepare_w4a16_nax4",
+    "quantize_per_token",
+    "w4a16_multirow",
+    "w4a16_qmv",
+    "w8a8_linear",
+]
+
+_PACKED = (torch.uint32, torch.int32)
+_HALF = (torch.bfloat16, torch.float16)
+_REAL = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _out_buffer(out, shape, dtype, device):
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if (out.dtype != dtype or out.device != device or not out.is_contiguous()
+            or out.numel() != prod(shape)):
+        raise ValueError(f"out must be a contiguous {dtype} tensor with {prod(shape)} elements")
+    return out.view(shape)
+
+
+def _require_device(op: str, *tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(f"{op} requires GPU execution")
+
+
+def is_w8a8_available() -> bool:
+    """True on a gfx950 device (X/src/spark_w8a8.cpp:204-216 answers the same
+    question for Apple M5+)."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        return bool(_lib.lib().sparkq_is_available())
+    except (RuntimeError, OSError):
+        return False
+
+
+# ---------------------------------------------------------------------------
+# W4A16
+# ---------------------------------------------------------------------------
+
+def _w4_check(op, x, weight, scales, biases, group_size, bits):
+    if any(not isinstance(v, torch.Tensor) for v in (x, weight, scales, biases)):
+        raise TypeError("x, weight, scales and biases must be tensors")
+    if bits != 4:
+        raise ValueError(f"{op}: only 4-bit affine weights are supported (bits={bits})")
+    if weight.dtype not in _PACKED or weight.ndim != 2:
+        raise ValueError(f"{op} requires UINT32-packed W4 weights of shape [N,K/8]")
+    if x.dtype not in _HALF or scales.dtype != x.dtype or biases.dtype != x.dtype:
+        raise ValueError(f"{op} requires BF16 or F16 x with scales and biases of the same dtype")
+    if x.ndim < 1 or x.shape[-1] <= 0:
+        raise ValueError(f"{op} requires x[..., K] with positive K")
+    k = x.shape[-1]
+    n = weight.shape[0]
+    if n <= 0 or weight.shape[1] * 8 != k:
+        raise ValueError(f"{op}: weight must have shape [N,K/8] with K={k}")
+    if group_size not in (32, 64, 128) or k % group_size:
+        raise ValueError(f"{op}: group_size must be 32, 64 or 128 and divide K")
+    if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
+        raise ValueError(f"{op} requires scales and biases with shape [N,K/{group_size}]")
+    if k % 64:
+        raise ValueError(f"{op} requires K divisible by 64")
+    _require_device(op, x, weight, scales, biases)
+
+
+def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
+                            bits: int = 4, transpose: bool = True, out_dtype=None, out=None):
+    """y = x @ dequantize(weight)^T for MLX affine packed weights.
+
+    The equivalent of mx.quantized_matmul(x, weight, scales, biases,
+    transpose=True, group_size, bits, mode="affine") as called by
+    AffineParameters.native (spark_mlx_llm/ops/linear.py:181-191). Any number
+    of rows: up to 32 rows stream the weights (decode, speculative verify),
+    more rows use the tiled MFMA GEMM (prefill). out_dtype may be
+    torch.float32 to read the unrounded fp32 epilogue; out, when given, is a
+    contiguous [..., N] tensor written in place.
+    """
+    if not transpose:
+        raise ValueError("only transpose=True (x @ W^T) is supported")
+    op = "affine_quantized_matmul"
+    _w4_check(op, x, weight, scales, biases, group_size, bits)
+    k = x.shape[-1]
+    n = weight.shape[0]
+    lead = x.shape[:-1]
+    m = prod(lead)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (x.dtype, torch.float32):
+        raise ValueError("out_dtype must be x.dtype or torch.float32")
+    y = _out_buffer(out, (m, n), out_dtype, x.device)
+    if m == 0:
+        return y.reshape(*lead, n)
+    x2 = x.reshape(m, k).contiguous()
+    weight, scales, biases = weight.contiguous(), scales.contiguous(), biases.contiguous()
+    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_w4a16_workspace_bytes(m, n, k, group_size))
+    _lib.call("sparkq_w4a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
+              _ptr(y), m, n, k, group_size, bits, _lib.dtype_code(x.dtype),
+              _lib.dtype_code(out_dtype), ws, wsb, _lib.stream_handle(x.device))
+    return y.reshape(*lead, n)
+
+
+def w4a16_qmv(x, weight, scales, biases, *, stream=None):
+    """One-row affine W4 GEMV (X/spark_mlx_ext/w4a16_qmv.py:37-98).
+
+    Widened from the reference's BF16/G32/K%512 specialisation: group size is
+    read from the scales shape (32, 64 or 128), K % 64 == 0, BF16 or F16.
+    """
+    if any(not isinstance(v, torch.Tensor) for v in (x, weight, scales, biases)):
+        raise TypeError("x, weight, scales and biases must be tensors")
+    if x.ndim < 1 or prod(x.shape[:-1]) != 1:
+        raise ValueError("W4A16 QMV requires exactly one activation row")
+    if weight.ndim != 2:
+        raise ValueError("W4A16 packed weight must have shape [N,K/8]")
+    if scales.ndim != 2 or scales.shape[1] <= 0:
+        raise ValueError("W4A16 QMV requires scales and biases with shape [N,K/G]")
+    group_size = x.shape[-1] // scales.shape[1]
+    return affine_quantized_matmul(x, weight, scales, biases, group_size=group_size, bits=4)
+
+
+_MULTIROW_ALGORITHMS = ("wide", "p2", "mma", "mma2", "nax", "nax2", "nax4", "split_p2")
+
+
+def w4a16_multirow(x, weight, scales, biases, *, algorithm: str = "wide", **tuning):
+    """Multi-row (speculative verify) affine W4 projection
+    (X/spark_mlx_ext/w4a16_multirow.py:238-437).
+
+    The reference selects among eight Apple-specific algorithms; on gfx950 a
+    single MFMA weight-streaming kernel serves every row count up to 32, so the
+    algorithm name is validated and the tuning keywords are accepted unused.
+    """
+    if algorithm not in _MULTIROW_ALGORITHMS:
+        raise ValueError(f"Unknown multirow algorithm {algorithm!r}")
+    if x.ndim < 1 or not 1 <= prod(x.shape[:-1]) <= 32:
+        raise ValueError("W4A16 multirow requires between 1 and 32 activation rows")
+    group_size = x.shape[-1] // scales.shape[1]
+    return affine_quantized_matmul(x, weight, scales, biases, group_size=group_size, bits=4)
+
+
+def prepare_w4a16_nax4(weight, scales, biases):
+    """The reference repacks nibbles into [N/256][K/32][32k][256n] tiles for its
+    tensor-op kernel (X/spark_mlx_ext/w4a16_multirow.py:181-222). The gfx950
+    kernels read the converter's native [N,K/8] layout with 16-byte loads, so
+    the prepared form is the input itself."""
+    return weight, scales, biases
+
+
+def affine_quantize(w, *, group_size: int = 64, bits: int = 4):
+    """Quantize BF16/F16 weights [N,K] to the MLX affine 4-bit layout on the GPU
+    (mx.quantize(bits=4) producer, spark_mlx_llm/dspark/draft_quantization.py:119):
+    scale = (max-min)/15, bias = min per group, rounded to w.dtype."""
+    if bits != 4:
+        raise ValueError("only 4-bit affine quantization is supported")
+    if w.ndim != 2 or w.dtype not in _HALF:
+        raise ValueError("w must be a BF16 or F16 matrix [N,K]")
+    n, k = w.shape
+    if group_size not in (32, 64, 128) or k % group_size:
+        raise ValueError("group_size must be 32, 64 or 128 and divide K")
+    _require_device("affine_quantize", w)
+    w = w.contiguous()
+    wq = torch.empty((n, k // 8), dtype=torch.uint32, device=w.device)
+    s = torch.empty((n, k // group_size), dtype=w.dtype, device=w.device)
+    b = torch.empty_like(s)
+    _lib.call("sparkq_w4_quantize", _ptr(w), _ptr(wq), _ptr(s), _ptr(b), n, k, group_size,
+              _lib.dtype_code(w.dtype), _lib.stream_handle(w.device))
+    return wq, s, b
+
+
+def affine_dequantize(weight, scales, biases, *, group_size: int = 64, bits: int = 4):
+    """Exact fp32 dequantization q*s+b of MLX affine 4-bit weights."""
+    if bits != 4 or weight.dtype not in _PACKED or weight.ndim != 2:
+        raise ValueError("expected UINT32-packed 4-bit weights [N,K/8]")
+    n, k = weight.shape[0], weight.shape[1] * 8
+    if scales.dtype not in _HALF or biases.dtype != scales.dtype:
+        raise ValueError("scales and biases must be BF16 or F16")
+    if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
+        raise ValueError("scales and biases must have shape [N,K/group_size]")
+    _require_device("affine_dequantize", weight, scales, biases)
+    out = torch.empty((n, k), dtype=torch.float32, device=weight.device)
+    weight, scales, biases = weight.contiguous(), scales.contiguous(), biases.contiguous()
+    _lib.call("sparkq_w4a16_dequantize", _ptr(weight), _ptr(scales),
+              _ptr(biases), _ptr(out), n, k, group_size,
+              _lib.dtype_code(scales.dtype), _lib.stream_handle(weight.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# W8A8
+# ---------------------------------------------------------------------------
+
+def _validate_dimensions(x, weight):
+    """X/src/spark_w8a8.cpp:51-65"""
+    if (x.ndim < 1 or weight.ndim != 2 or x.shape[-1] <= 0 or weight.shape[0] <= 0
+            or x.numel() == 0 or x.shape[-1] != weight.shape[1]):
+        raise ValueError("Expected nonempty x[..., K] and weight[N, K] with matching K.")
+    if x.shape[-1] % 32 or x.shape[-1] > 131040:
+        raise ValueError("K must be a multiple of 32 in [32, 131040].")
+    if weight.dtype != torch.int8:
+        raise ValueError("weight must contain signed INT8 values.")
+
+
+def quantize_per_token(x):
+    """Per-token symmetric int8 activations (X/src/kernels/w8a8_quantize.metal):
+    returns (q int8 [M,K], scales fp32 [M]) for x [..., K]."""
+    if x.dtype not in _REAL:
+        raise ValueError("x must have dtype float16, bfloat16, or float32.")
+    _require_device("quantize_per_token", x)
+    k = x.shape[-1]
+    m = x.numel() // k
+    x2 = x.reshape(m, k).contiguous()
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    sc = torch.empty((m,), dtype=torch.float32, device=x.device)
+    _lib.call("sparkq_a8_quantize_per_token", _ptr(x2), _ptr(q), _ptr(sc), m, k,
+              _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+    return q, sc
+
+
+def int8_matmul_int32(x, weight, *, stream=None):
+    """Raw int32 x[M,K] @ weight[N,K]^T (X/src/spark_w8a8.cpp:218-228)."""
+    _validate_dimensions(x, weight)
+    if x.ndim != 2 or x.dtype != torch.int8:
+        raise ValueError("int8_matmul_int32 requires x[M, K] with dtype int8.")
+    _require_device("int8_matmul_int32", x, weight)
+    m, k = x.shape
+    n = weight.shape[0]
+    c = torch.empty((m, n), dtype=torch.int32, device=x.device)
+    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_int8_matmul_workspace_bytes(m, n, k))
+    x, weight = x.contiguous(), weight.contiguous()
+    _lib.call("sparkq_int8_matmul_i32", _ptr(x), _ptr(weight),
+              _ptr(c), m, n, k, ws, wsb, _lib.stream_handle(x.device))
+    return c
+
+
+def w8a8_linear(x, weight, scales, bias=None, *, stream=None, out_dtype=None, out=None):
+    """Per-token int8 activations x per-channel int8 weights, int32 MACs, then
+    T(float(acc)*sa[m]*sw[n] + bias[n]) (X/src/spark_w8a8.cpp:230-257)."""
+    _validate_dimensions(x, weight)
+    n, k = weight.shape
+    if x.dtype not in _REAL:
+        raise ValueError("x must have dtype float16, bfloat16, or float32.")
+    if scales.dtype != torch.float32 or tuple(scales.shape) not in ((n,), (n, 1)):
+        raise ValueError("scales must have shape [N] or [N, 1] and dtype float32.")
+    if bias is not None and (tuple(bias.shape) != (n,) or bias.dtype not in _REAL):
+        raise ValueError("bias must have shape [N] and a real floating dtype.")
+    _require_device("w8a8_linear", x, weight, scales, bias)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    lead = x.shape[:-1]
+    m = prod(lead)
+    x2 = x.reshape(m, k).contiguous()
+    y = _out_buffer(out, (m, n), out_dtype, x.device)
+    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_w8a8_workspace_bytes(m, n, k))
+    bias_c = bias.contiguous() if bias is not None else None
+    weight, scales = weight.contiguous(), scales.reshape(n).contiguous()
+    _lib.call("sparkq_w8a8_linear", _ptr(x2), _ptr(weight),
+              _ptr(scales), _ptr(bias_c),
+              _lib.dtype_code(bias.dtype) if bias is not None else F32, _ptr(y), m, n, k,
+              _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), ws, wsb,
+              _lib.stream_handle(x.device))
+    return y.reshape(*lead, n)
+
+
+class W8A8Linear(nn.Module):
+    """Linear layer over existing symmetric per-channel INT8 weights
+    (X/spark_mlx_ext/linear.py:9-55): weight int8 [N,K], scales fp32 [N] or
+    [N,1], optional floating bias [N]. Inference only."""
+
+    def __init__(self, weight, scales, bias=None):
+        super().__init__()
+        if weight.ndim != 2 or weight.dtype != torch.int8:
+            raise ValueError("weight must be an INT8 matrix [N, K]")
+        n, k = weight.shape
+        if n <= 0 or k <= 0 or k % 32 or k > 131040:
+            raise ValueError("N must be positive; K must be a multiple of 32 in [32, 131040]")
+        if scales.dtype != torch.float32 or tuple(scales.shape) not in ((n,), (n, 1)):
+            raise ValueError("scales must be FP32 with shape [N] or [N, 1]")
+        if bias is not None and (tuple(bias.shape) != (n,) or bias.dtype not in _REAL):
+            raise ValueError("bias must be a floating array of shape [N]")
+        self.register_buffer("weight", weight)
+        self.register_buffer("scales", scales)
+        self.register_buffer("bias", bias)
+        self.requires_grad_(False)
+
+    @property
+    def input_dims(self) -> int:
+        return self.weight.shape[1]
+
+    @property
+    def output_dims(self) -> int:
+        return self.weight.shape[0]
+
+    def forward(self, x):
+        return w8a8_linear(x, self.weight, self.scales, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"input_dims={self.input_dims}, output_dims={self.output_dims}, "
+                f"bias={self.bias is not None}")
+
+
+# ---------------------------------------------------------------------------
+# INT8-KV decode attention
+# ---------------------------------------------------------------------------
+
+def kv_quantize_s8(x):
+    """Symmetric int8 KV rows: codes int8 [..., D] and fp16 scales [...] with
+    scale = fp16(amax/127) (1 when zero) and codes from the rounded scale."""
+    if x.dtype not in _REAL:
+        raise ValueError("x must be float16, bfloat16 or float32")
+    _require_device("kv_quantize_s8", x)
+    d = x.shape[-1]
+    r = x.numel() // d
+    x2 = x.reshape(r, d).contiguous()
+    codes = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    sc = torch.empty(x.shape[:-1], dtype=torch.float16, device=x.device)
+    _lib.call("sparkq_kv_quantize_s8", _ptr(x2), _ptr(codes), _ptr(sc), r, d,
+              _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+    return codes, sc
+
+
+def _kv_strides(codes, scales, elem_bytes_codes):
+    st = codes.stride()
+    ss = scales.stride()
+    return [st[0] * elem_bytes_codes, st[1] * elem_bytes_codes, st[2] * elem_bytes_codes,
+            ss[0], ss[1], ss[2]]
+
+
+def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, bits: int = 8,
+                        mask=None, single_pass_max_length: int = 1023, out_dtype=None,
+                        out=None):
+    """Decode attention over an INT8 KV cache
+    (X/spark_mlx_ext/int8_quantized_sdpa.py:156-287).
+
+    queries [B,Hq,1,D]. keys/values are either the MLX affine 8-bit tuple
+    (packed uint32 [B,Hkv,N,D/4], scales [B,Hkv,N,D/G], biases) with scales in
+    the query dtype, or the symmetric pair (codes int8 [B,Hkv,N,D], scales fp16
+    [B,Hkv,N]). Views with a sliced token capacity are read in place (strides
+    are passed through); the innermost axis must be contiguous. All N tokens
+    are visible, so mask None and "causal" are the same for one query token.
+    single_pass_max_length is validated for signature compatibility; the split
+    policy is the kernel's own.
+    """
+    if type(single_pass_max_length) is not int or single_pass_max_length < 0:
+        raise ValueError("single_pass_max_length must be a nonnegative Python int")
+    if queries.ndim != 4 or len(keys) not in (2, 3) or len(values) != len(keys):
+        raise ValueError("Expected Q[B,H,L,D] and affine (packed, scales, biases) KV tuples")
+    batch, heads, length, dim = queries.shape
+    if any(t.ndim != 4 for t in (keys[0], values[0])):
+        raise ValueError("Every packed KV and metadata array must have four dimensions")
+    kv_heads, n = keys[0].shape[1:3]
+    if min(batch, heads, length, dim, kv_heads, n) <= 0 or heads % kv_heads:
+        raise ValueError("Nonempty inputs and query heads divisible by KV heads required")
+    if not isinstance(scale, (float, int)) or not math.isfinite(scale):
+        raise ValueError("scale must be a finite Python number")
+    if mask is not None and not (isinstance(mask, str) and mask == "causal"):
+        raise ValueError("only mask=None or mask='causal' is supported")
+    if length != 1:
+        raise ValueError("int8_quantized_sdpa on gfx950 serves single-token decode (L=1)")
+    if queries.dtype not in _REAL:
+        raise ValueError("Q and metadata must be float16, bfloat16 or float32")
+    fmt = KV_AFFINE_U8 if len(keys) == 3 else KV_S8_F16SCALE
+    if fmt == KV_AFFINE_U8:
+        if bits != 8 or group_size not in (32, 64, 128):
+            raise ValueError("Supported affine formats: bits 8, group size 32/64/128")
+        for name, (packed, s, b) in (("key", keys), ("value", values)):
+            if (dim % group_size or packed.shape != (batch, kv_heads, n, dim // 4)
+                    or s.shape != (batch, kv_heads, n, dim // group_size)
+                    or b.shape != s.shape or packed.dtype not in _PACKED
+                    or s.dtype != queries.dtype or b.dtype != queries.dtype
+                    or s.stride() != b.stride()):
+                raise ValueError(f"Incompatible {name} packed shape, affine metadata or dtype")
+            if packed.stride(3) != 1 or s.stride(3) != 1:
+                raise ValueError(f"{name} innermost axis must be contiguous")
+        strides = (_kv_strides(keys[0], keys[1], 4) + _kv_strides(values[0], values[1], 4))
+        kc, ks, kb = keys
+        vc, vs, vb = values
+    else:
+        for name, (codes, s) in (("key", keys), ("value", values)):
+            if (codes.shape != (batch, kv_heads, n, dim) or codes.dtype != torch.int8
+                    or s.shape != (batch, kv_heads, n) or s.dtype != torch.float16):
+                raise ValueError(f"Incompatible {name} int8 codes or fp16 scales")
+            if codes.stride(3) != 1:
+                raise ValueError(f"{name} innermost axis must be contiguous")
+        strides = (_kv_strides(keys[0], keys[1], 1) + _kv_strides(values[0], values[1], 1))
+        (kc, ks), (vc, vs) = keys, values
+        kb = vb = None
+    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    out_dtype = queries.dtype if out_dtype is None else out_dtype
+    q = queries.reshape(batch, heads, dim).contiguous()
+    out = _out_buffer(out, (batch, heads, 1, dim), out_dtype, queries.device)
+    st = (ctypes.c_int64 * 12)(*strides)
+    ws, wsb = _lib.workspace(queries.device,
+                             _lib.lib().sparkq_int8kv_sdpa_workspace_bytes(batch, heads, n, dim))
+    _lib.call("sparkq_int8kv_sdpa_decode", _ptr(q), _ptr(kc), _ptr(ks), _ptr(kb), _ptr(vc),
+              _ptr(vs), _ptr(vb), _ptr(out), batch, heads, kv_heads, n, dim, group_size, fmt,
+              _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), float(scale), st,
+              ws, wsb, _lib.stream_handle(queries.device))
+    return out

@@ -1,0 +1,89 @@
+"""SDPA configuration and dispatch for INT8 KV caches on torch.
+
+Mirrors spark_mlx_llm/ops/sdpa.py: SDPAConfig (:13-20), dispatch_sdpa
+(:39-78), _supports_int8 (:81-103) and _int8_attention (:149-163). The
+predicate is widened from the reference's D=256/G32 affine format to the
+formats and head sizes the gfx950 decode kernel serves (D in 64/128/256,
+affine G in 32/64/128, or symmetric s8 codes with fp16 per-token scales).
+Unquantized caches go to torch's scaled_dot_product_attention, the analogue
+of the reference's mlx-lm native path.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .. import ext
+from .base import OperatorConfig
+
+__all__ = ["SDPAConfig", "dispatch_sdpa"]
+
+
+@dataclass(kw_only=True)
+class SDPAConfig(OperatorConfig):
+    """Prefer available kernels; KV cache quantization is configured separately."""
+
+    fused_quantized_sdpa: bool = True
+    fused_quantized_sdpa_prefill: bool = False
+    tuned_bf16_sdpa: bool = False
+    verification_bf16_sdpa: bool = False
+
+
+def dispatch_sdpa(queries, keys, values, *, cache, scale, mask, config: SDPAConfig | None = None,
+                  is_sliding=False):
+    config = config if config is not None else SDPAConfig()
+    if config.fused_quantized_sdpa and _supports_int8(queries, keys, values, cache=cache,
+                                                      mask=mask):
+        return _int8_attention(queries, keys, values, cache=cache, scale=scale, mask=mask)
+    if isinstance(keys, (tuple, list)):
+        raise ValueError("quantized KV cache outside the gfx950 decode kernel's formats")
+    return _native_attention(queries, keys, values, scale=scale, mask=mask)
+
+
+def _supports_int8(queries, keys, values, *, cache, mask):
+    if not (isinstance(keys, (tuple, list)) and isinstance(values, (tuple, list))
+            and len(keys) == len(values) and len(keys) in (2, 3)):
+        return False
+    if getattr(cache, "bits", None) != 8:
+        return False
+    affine = len(keys) == 3
+    dim = queries.shape[-1] if queries.ndim == 4 else -1
+    return (
+        queries.ndim == 4
+        and queries.shape[-2] == 1
+        and dim in (64, 128, 256)
+        and keys[0].ndim == values[0].ndim == 4
+        and keys[0].shape[1] > 0
+        and queries.shape[1] % keys[0].shape[1] == 0
+        and queries.shape[1] // keys[0].shape[1] in (1, 2, 4, 8)
+        and queries.dtype in (torch.float16, torch.bfloat16, torch.float32)
+        and (
+            (affine and getattr(cache, "group_size", None) in (32, 64, 128)
+             and keys[0].shape[-1] * 4 == dim
+             and all(t.dtype == queries.dtype for t in (*keys[1:], *values[1:])))
+            or (not affine and keys[0].dtype == torch.int8 and keys[0].shape[-1] == dim
+                and keys[1].dtype == values[1].dtype == torch.float16)
+        )
+        and (mask is None or (isinstance(mask, str) and mask == "causal"))
+        and queries.device.type == "cuda"
+        and ext.is_w8a8_available()
+    )
+
+
+def _int8_attention(queries, keys, values, *, cache, scale, mask):
+    return ext.int8_quantized_sdpa(queries, keys, values, scale=scale,
+                                   group_size=getattr(cache, "group_size", 32),
+                                   bits=cache.bits, mask=mask)
+
+
+def _native_attention(queries, keys, values, *, scale, mask):
+    heads, kv_heads = queries.shape[1], keys.shape[1]
+    if heads != kv_heads:
+        keys = keys.repeat_interleave(heads // kv_heads, dim=1)
+        values = values.repeat_interleave(heads // kv_heads, dim=1)
+    causal = isinstance(mask, str) and mask == "causal" and queries.shape[2] > 1
+    attn_mask = None if isinstance(mask, str) or mask is None else mask
+    return torch.nn.functional.scaled_dot_product_attention(
+        queries, keys, values, attn_mask=attn_mask, is_causal=causal, scale=scale)

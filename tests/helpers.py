@@ -1,0 +1,69 @@
+"""Shared helpers for the parity tests: seeded inputs from the oracle's
+generator, uploads to the device, and the comparison metrics."""
+
+import numpy as np
+import torch
+
+import oracle as o
+
+TORCH16 = {o.BF16: torch.bfloat16, o.F16: torch.float16}
+
+
+def up16(bits, dtype, device):
+    """uint16 bit patterns -> device tensor of the 16-bit float dtype."""
+    t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16))
+    return t.view(TORCH16[dtype]).to(device)
+
+
+def up32(words, device):
+    return torch.from_numpy(np.ascontiguousarray(words).view(np.int32)).to(device)
+
+
+def down16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def w4_problem(m, n, k, g, dtype=o.BF16, seed=0, wstd=0.02):
+    """Weights N(0, wstd) rounded to dtype and quantized with the benchmark's
+    affine formula; activations N(0,1) rounded to dtype."""
+    w = o.bits_to_f32(o.randn16(seed, 1000 + n, n * k, wstd, dtype), dtype).reshape(n, k)
+    wq, s, b = o.w4_quantize(w, g, dtype)
+    x = o.randn16(seed, 2000 + m, m * k, 1.0, dtype).reshape(m, k)
+    return x, wq, s, b
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def max_abs(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def ulp_distance16(a_bits, b_bits, dtype):
+    """Distance in units of the 16-bit format between two bit arrays."""
+    def ordered(x):
+        x = x.astype(np.int64)
+        return np.where(x & 0x8000, -(x & 0x7FFF), x)
+
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+def check_fp32(out, ref, atol=2e-2, rtol_l2=1e-3):
+    """The north-star tolerance applied to an unrounded fp32 epilogue."""
+    ma, rl = max_abs(out, ref), rel_l2(out, ref)
+    assert ma <= atol and rl <= rtol_l2, f"max_abs={ma:.3e} rel_l2={rl:.3e}"
+    return ma, rl
+
+
+def check_rounded16(out_bits, ref64, dtype, atol=2e-2, max_flip_frac=0.02):
+    """A 16-bit output against the correctly rounded oracle: every element
+    within one unit of the format, and few 1-unit boundary flips."""
+    ref_bits = o.round16(np.asarray(ref64, np.float32), dtype)
+    d = ulp_distance16(out_bits, ref_bits, dtype)
+    assert d.max() <= 1, f"max ulp distance {d.max()}"
+    frac = float((d > 0).mean())
+    assert frac <= max_flip_frac, f"1-ulp flips {frac:.4f}"
+    return frac

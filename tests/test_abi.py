@@ -1,0 +1,105 @@
+"""CPU checks of the C-ABI boundary: libsparkq.so loads, exports every entry
+point include/sparkq.h declares, and rejects bad arguments with the right
+status before touching a device (no compute calls without a GPU)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "sparkq.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sparkq_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = _declared()
+    for required in ("sparkq_w4a16_linear", "sparkq_w4a16_dequantize", "sparkq_w4_quantize",
+                     "sparkq_a8_quantize_per_token", "sparkq_int8_matmul_i32",
+                     "sparkq_w8a8_linear", "sparkq_int8kv_sdpa_decode", "sparkq_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from sparkq import _lib
+
+    handle = ctypes.CDLL(_lib.library_path())
+    missing = [n for n in _declared() if not hasattr(handle, n)]
+    assert not missing, missing
+    # the Python binding covers the whole header too
+    assert set(_declared()) <= set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_workspace_queries():
+    from sparkq import _lib
+
+    lib = _lib.lib()
+    assert lib.sparkq_abi_version() == 1
+    assert lib.sparkq_w4a16_workspace_bytes(0, 1, 1, 64) == 0
+    # decode GEMV at the down-projection shape splits K across workgroups
+    assert lib.sparkq_w4a16_workspace_bytes(1, 2560, 9728, 64) > 0
+    # prefill: the group-sum prologue buffer [K/G][M] fp32
+    assert lib.sparkq_w4a16_workspace_bytes(2048, 19456, 2560, 64) >= 2048 * 40 * 4
+    assert lib.sparkq_w8a8_workspace_bytes(16, 2560, 9728) >= 16 * 9728 + 16 * 4
+    assert lib.sparkq_int8kv_sdpa_workspace_bytes(1, 32, 1, 128) == 0
+
+
+P = ctypes.c_void_p
+
+
+def _rc(name, *args):
+    from sparkq import _lib
+
+    rc = getattr(_lib.lib(), name)(*args)
+    return rc, _lib.lib().sparkq_last_error().decode()
+
+
+def test_invalid_arguments_rejected_without_a_device():
+    dummy = P(4096)
+    # null pointer
+    rc, msg = _rc("sparkq_w4a16_linear", None, dummy, dummy, dummy, dummy, 1, 64, 64, 64, 4,
+                  2, 2, None, 0, None)
+    assert rc == -1 and "null" in msg
+    # bits other than 4 is unsupported
+    rc, msg = _rc("sparkq_w4a16_linear", dummy, dummy, dummy, dummy, dummy, 1, 64, 64, 64, 8,
+                  2, 2, None, 0, None)
+    assert rc == -2 and "bits" in msg
+    # bad group size
+    rc, msg = _rc("sparkq_w4a16_linear", dummy, dummy, dummy, dummy, dummy, 1, 64, 64, 48, 4,
+                  2, 2, None, 0, None)
+    assert rc == -1 and "group_size" in msg
+    # K not a multiple of 32 for the int8 path (X/src/spark_w8a8.cpp:58-60)
+    rc, msg = _rc("sparkq_int8_matmul_i32", dummy, dummy, dummy, 1, 64, 48, None, 0, None)
+    assert rc == -1 and "multiple of 32" in msg
+    rc, msg = _rc("sparkq_int8_matmul_i32", dummy, dummy, dummy, 1, 64, 131072, None, 0, None)
+    assert rc == -1 and "131040" in msg
+    # fp32 activations are not a W4A16 input
+    rc, msg = _rc("sparkq_w4a16_linear", dummy, dummy, dummy, dummy, dummy, 1, 64, 64, 64, 4,
+                  0, 0, None, 0, None)
+    assert rc == -2
+    # attention: heads not divisible by KV heads
+    st = (ctypes.c_int64 * 12)(*([128] * 12))
+    rc, msg = _rc("sparkq_int8kv_sdpa_decode", dummy, dummy, dummy, None, dummy, dummy, None,
+                  dummy, 1, 6, 4, 16, 128, 32, 0, 2, 2, ctypes.c_float(0.1), st, None, 0, None)
+    assert rc == -1 and "divisible" in msg
+    # attention: unsupported head dim
+    rc, msg = _rc("sparkq_int8kv_sdpa_decode", dummy, dummy, dummy, None, dummy, dummy, None,
+                  dummy, 1, 8, 8, 16, 96, 32, 0, 2, 2, ctypes.c_float(0.1), st, None, 0, None)
+    assert rc == -2 and "head dim" in msg
+    # attention: non-finite scale
+    rc, msg = _rc("sparkq_int8kv_sdpa_decode", dummy, dummy, dummy, None, dummy, dummy, None,
+                  dummy, 1, 8, 8, 16, 128, 32, 0, 2, 2, ctypes.c_float(float("inf")), st,
+                  None, 0, None)
+    assert rc == -1 and "finite" in msg
+
+
+def test_status_maps_to_reference_exceptions():
+    from sparkq import _lib
+
+    with pytest.raises(ValueError, match="null"):
+        _lib.call("sparkq_a8_quantize_per_token", None, None, None, 1, 32, 2, None)

@@ -1,0 +1,182 @@
+"""GPU parity of the W4A16 path (libsparkq via sparkq.ext) against the oracle.
+
+Bars: dequantized weights and the quantizer bit-exact; the fp32 epilogue
+within max-abs 2e-2 and rel-L2 1e-3 of the fp64 dequantize-then-matmul; the
+16-bit output within one unit of the correctly rounded oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from helpers import (check_fp32, check_rounded16, down16, up16, up32, w4_problem)
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(dev, x, wq, s, b, g, dtype, out_dtype=None):
+    import sparkq
+
+    return sparkq.affine_quantized_matmul(
+        up16(x, dtype, dev), up32(wq, dev), up16(s, dtype, dev), up16(b, dtype, dev),
+        group_size=g, out_dtype=out_dtype)
+
+
+@pytest.mark.parametrize("dtype", [o.BF16, o.F16])
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_dequantize_bit_exact(gpu, g, dtype):
+    import sparkq
+
+    n, k = 64, 512
+    rng = np.random.default_rng(g)
+    codes = rng.integers(0, 16, (n, k), dtype=np.uint8)
+    wq = o.pack4(codes)
+    sv = (rng.standard_normal((n, k // g)) * 10 ** rng.uniform(-5, 2, (n, k // g))).astype(np.float32)
+    bv = (rng.standard_normal((n, k // g)) * 10 ** rng.uniform(-5, 2, (n, k // g))).astype(np.float32)
+    s16, b16 = o.round16(sv, dtype), o.round16(bv, dtype)
+    s16[0, 0], b16[0, 0] = 0x0000, 0x8000
+    if dtype == o.BF16:
+        s16[1, 0], b16[1, 0] = 0x0003, 0x8005   # subnormals
+        s16[2, 0], b16[2, 0] = 0x7F00, 0xFE00   # large exponents
+    ref = o.w4_dequantize(wq, s16, b16, g, dtype)
+    out = sparkq.affine_dequantize(up32(wq, gpu), up16(s16, dtype, gpu), up16(b16, dtype, gpu),
+                                   group_size=g).cpu().numpy()
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [o.BF16, o.F16])
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_quantizer_bit_exact(gpu, g, dtype):
+    import sparkq
+
+    n, k = 96, 512
+    w16 = o.randn16(7, g, n * k, 0.02, dtype).reshape(n, k)
+    w16[0, :g] = o.round16(np.full(g, 0.5, np.float32), dtype)   # constant group
+    wq, s, b = sparkq.affine_quantize(up16(w16, dtype, gpu), group_size=g)
+    rwq, rs, rb = o.w4_quantize(o.bits_to_f32(w16, dtype), g, dtype)
+    assert np.array_equal(wq.cpu().view(torch.int32).numpy().view(np.uint32), rwq)
+    assert np.array_equal(down16(s), rs)
+    assert np.array_equal(down16(b), rb)
+
+
+SKINNY = [1, 2, 3, 8, 13, 16, 17, 32]
+
+
+@pytest.mark.parametrize("m", SKINNY)
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_linear_skinny(gpu, m, g):
+    n, k = 96, 1024
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    check_fp32(y32, ref)
+    y16 = down16(_run(gpu, x, wq, s, b, g, o.BF16))
+    check_rounded16(y16, ref, o.BF16)
+
+
+@pytest.mark.parametrize("m", [1, 8, 40])
+def test_linear_f16(gpu, m):
+    n, k, g = 160, 512, 64
+    x, wq, s, b = w4_problem(m, n, k, g, dtype=o.F16, seed=3)
+    ref = o.w4a16_matmul(x, wq, s, b, g, o.F16)
+    y32 = _run(gpu, x, wq, s, b, g, o.F16, out_dtype=torch.float32).cpu().numpy()
+    check_fp32(y32, ref)
+    check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.F16)), ref, o.F16)
+
+
+@pytest.mark.parametrize("m", [33, 130, 256])
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_linear_gemm(gpu, m, g):
+    n, k = 200, 512   # N tail inside a 128-wide tile
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m + g)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    check_fp32(y32, ref)
+    check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 4096), (4, 8192, 256), (16, 40, 2048)])
+def test_split_plans(gpu, m, n, k):
+    """Cross-workgroup split-K (few row tiles, long K) and a single split."""
+    g = 64
+    x, wq, s, b = w4_problem(m, n, k, g, seed=5)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    check_fp32(y32, ref)
+
+
+def test_one_hot_rows_pick_weight_columns(gpu):
+    import sparkq
+
+    n, k, g = 64, 256, 64
+    _, wq, s, b = w4_problem(1, n, k, g, seed=9)
+    x = np.zeros((3, k), np.float32)
+    x[0, 0], x[1, 77], x[2, 255] = 1.0, 1.0, 1.0
+    y = _run(gpu, o.bf16_bits(x), wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    deq = o.w4_dequantize(wq, s, b, g)
+    assert np.array_equal(y[0], deq[:, 0]) and np.array_equal(y[1], deq[:, 77])
+    assert np.array_equal(y[2], deq[:, 255])
+    # the qmv / multirow entry points reach the same kernel
+    xt = up16(o.bf16_bits(x[:1]), o.BF16, gpu)
+    args = (up32(wq, gpu), up16(s, o.BF16, gpu), up16(b, o.BF16, gpu))
+    assert torch.equal(sparkq.w4a16_qmv(xt, *args), _run(gpu, o.bf16_bits(x[:1]), wq, s, b, g, o.BF16))
+
+
+def test_deterministic(gpu):
+    x, wq, s, b = w4_problem(4, 512, 2560, 64, seed=11)
+    a = _run(gpu, x, wq, s, b, 64, o.BF16, out_dtype=torch.float32)
+    c = _run(gpu, x, wq, s, b, 64, o.BF16, out_dtype=torch.float32)
+    assert torch.equal(a, c)
+
+
+# ---------------------------------------------------------------------------
+# benchmark shapes: full kernels, oracle on sampled rows/columns
+# ---------------------------------------------------------------------------
+
+PROJ = {"qkv": (3584, 2560), "gate_up": (19456, 2560), "down": (2560, 9728)}
+
+
+def _gpu_weights(dev, n, k, g, seed):
+    """Benchmark-style weights: N(0,0.02) bf16 quantized on the device."""
+    import sparkq
+
+    w16 = o.randn16(seed, n, n * k, 0.02, o.BF16).reshape(n, k)
+    wq, s, b = sparkq.affine_quantize(up16(w16, o.BF16, dev), group_size=g)
+    return wq, s, b
+
+
+@pytest.mark.parametrize("proj", list(PROJ))
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 512, 2048])
+def test_benchmark_shapes_sampled(gpu, proj, m):
+    import sparkq
+
+    n, k = PROJ[proj]
+    g = 64
+    wq, s, b = _gpu_weights(gpu, n, k, g, seed=1)
+    x16 = o.randn16(0, 77 + m, m * k).reshape(m, k)
+    y = sparkq.affine_quantized_matmul(up16(x16, o.BF16, gpu), wq, s, b, group_size=g,
+                                       out_dtype=torch.float32).cpu().numpy()
+    assert np.isfinite(y).all()
+    rng = np.random.default_rng(m)
+    rows = np.sort(rng.choice(m, size=min(m, 24), replace=False))
+    cols = np.sort(rng.choice(n, size=256, replace=False))
+    wq_h = wq.cpu().numpy().view(np.uint32)[cols]
+    s_h, b_h = down16(s)[cols], down16(b)[cols]
+    ref = o.w4a16_matmul(x16[rows], wq_h, s_h, b_h, g)
+    check_fp32(y[np.ix_(rows, cols)], ref)
+
+
+def test_linearity_full_size(gpu):
+    """y(x1 + x2) = y(x1) + y(x2) at the largest prefill shape (fp32 epilogue);
+    x1, x2 are chosen so that x1 + x2 is exact in bf16."""
+    import sparkq
+
+    n, k, g, m = 19456, 2560, 64, 2048
+    wq, s, b = _gpu_weights(gpu, n, k, g, seed=2)
+    x1 = torch.randint(-8, 8, (m, k), device=gpu).to(torch.bfloat16) / 8
+    x2 = torch.randint(-8, 8, (m, k), device=gpu).to(torch.bfloat16) / 8
+    f = lambda x: sparkq.affine_quantized_matmul(x, wq, s, b, group_size=g, out_dtype=torch.float32)
+    lhs, rhs = f(x1 + x2), f(x1) + f(x2)
+    rel = (torch.linalg.norm(lhs - rhs) / torch.linalg.norm(rhs)).item()
+    assert rel < 1e-5, rel

@@ -1,0 +1,122 @@
+"""GPU parity of the W8A8 path against the oracle: the per-token quantizer and
+the int32 accumulators bit-exact, and (because the epilogue is the same
+fmaf in both) the fp32 output bit-exact too; 16-bit outputs are its
+correctly rounded value."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from helpers import TORCH16, down16, up16
+
+pytestmark = pytest.mark.gpu
+
+
+def _x(m, k, dtype, seed=0):
+    return o.randn16(seed, 300 + m, m * k, 1.0, dtype).reshape(m, k)
+
+
+@pytest.mark.parametrize("dtype", [o.BF16, o.F16, o.F32])
+@pytest.mark.parametrize("m,k", [(1, 2560), (8, 9728), (16, 2560), (5, 32), (3, 131040)])
+def test_quantize_per_token_bit_exact(gpu, m, k, dtype):
+    import sparkq
+
+    if dtype == o.F32:
+        xf = o.randn(1, m, m * k).reshape(m, k)
+        xt = torch.from_numpy(xf).to(gpu)
+    else:
+        x16 = _x(m, k, dtype)
+        xf = o.bits_to_f32(x16, dtype)
+        xt = up16(x16, dtype, gpu)
+    if m >= 3:
+        xf[2] = 0.0
+        xt[2] = 0.0
+    q, sc = sparkq.quantize_per_token(xt)
+    rq, rsc = o.a8_quantize(xf)
+    assert np.array_equal(q.cpu().numpy(), rq)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), rsc.view(np.uint32))
+
+
+def test_quantize_ties_round_to_even(gpu):
+    import sparkq
+
+    x = np.zeros((1, 64), np.float32)
+    x[0, :5] = [127.0, 2.5, 1.5, -0.5, -2.5]   # scale 1: ties at .5
+    q, sc = sparkq.quantize_per_token(torch.from_numpy(x).to(gpu))
+    assert sc.item() == 1.0
+    assert q[0, :5].tolist() == [127, 2, 2, 0, -2]
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 3584, 2560), (8, 2560, 9728), (16, 19456, 2560),
+                                   (33, 96, 256), (70, 130, 512), (2, 40, 32)])
+def test_int8_matmul_int32_bit_exact(gpu, m, n, k):
+    import sparkq
+
+    rng = np.random.default_rng(m * 7 + n)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    c = sparkq.int8_matmul_int32(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    if m * n * k > 2e8:
+        cols = np.sort(rng.choice(n, 256, replace=False))
+        assert np.array_equal(c.cpu().numpy()[:, cols], o.int8_matmul(a, b[cols]))
+    else:
+        assert np.array_equal(c.cpu().numpy(), o.int8_matmul(a, b))
+
+
+def test_int8_matmul_extreme_range(gpu):
+    import sparkq
+
+    k = 131040
+    a = np.full((2, k), -128, np.int8)
+    b = np.full((33, k), -128, np.int8)
+    b[1] = 127
+    c = sparkq.int8_matmul_int32(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    assert c[0, 0].item() == 16384 * k and c[0, 1].item() == -128 * 127 * k
+
+
+def _w8(n, k, seed=0):
+    w = o.randn(seed, 500 + n, n * k, 0.02).reshape(n, k)
+    return o.w8_quantize_channel(w)
+
+
+@pytest.mark.parametrize("dtype", [o.BF16, o.F16, o.F32])
+@pytest.mark.parametrize("m,n,k", [(1, 3584, 2560), (8, 2560, 9728), (16, 19456, 2560),
+                                   (40, 100, 256)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_w8a8_linear_bit_exact(gpu, m, n, k, dtype, with_bias):
+    import sparkq
+
+    wq, wsc = _w8(n, k)
+    if dtype == o.F32:
+        xf = o.randn(2, m, m * k).reshape(m, k)
+        xt = torch.from_numpy(xf).to(gpu)
+    else:
+        x16 = _x(m, k, dtype, seed=1)
+        xf = o.bits_to_f32(x16, dtype)
+        xt = up16(x16, dtype, gpu)
+    bias = o.randn(3, n, n) if with_bias else None
+    bias_t = torch.from_numpy(bias).to(gpu) if with_bias else None
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    y32 = sparkq.w8a8_linear(xt, wt, st, bias_t, out_dtype=torch.float32).cpu().numpy()
+    qa, sa = o.a8_quantize(xf)
+    rng = np.random.default_rng(0)
+    cols = np.sort(rng.choice(n, min(n, 512), replace=False))
+    acc = o.int8_matmul(qa, wq[cols])
+    ref = o.w8a8_epilogue(acc, sa, wsc[cols], bias[cols] if with_bias else None)
+    assert np.array_equal(y32[:, cols].view(np.uint32), ref.view(np.uint32))
+    y = sparkq.w8a8_linear(xt, wt, st, bias_t)
+    assert y.dtype == (torch.float32 if dtype == o.F32 else TORCH16[dtype])
+    if dtype != o.F32:
+        assert np.array_equal(down16(y)[:, cols], o.round16(ref, dtype))
+
+
+def test_readme_known_answer(gpu):
+    """ones(32) activations x ones(4,32) int8 weights, scale 1 -> 32
+    (X/README.md:41-46, adapted from W8A16 to W8A8)."""
+    import sparkq
+
+    lin = sparkq.W8A8Linear(torch.ones((4, 32), dtype=torch.int8, device=gpu),
+                            torch.ones(4, dtype=torch.float32, device=gpu))
+    y = lin(torch.ones((1, 32), dtype=torch.bfloat16, device=gpu))
+    assert y.float().cpu().tolist() == [[32.0] * 4]

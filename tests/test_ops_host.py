@@ -1,0 +1,124 @@
+"""CPU tests of the host layer: configuration contracts, dispatch predicates
+and the validation the operators perform before any device call."""
+
+import pytest
+import torch
+
+import sparkq
+from sparkq import ext
+from sparkq.ops import (AffineParameters, LinearConfig, QuantizedLinear, SDPAConfig,
+                        dispatch_linear, dispatch_sdpa)
+from sparkq.ops.linear import unpack_affine_w8
+
+
+def test_linear_config_contract():
+    assert LinearConfig().w4_qmv_backend == "native"
+    assert LinearConfig.choices("w4_qmv_backend") == ("native", "splitk", "multirow",
+                                                       "multirow_packed")
+    assert LinearConfig.choices("w8_qmv_backend") == ("auto", "native", "w8a16", "w8a8",
+                                                       "multirow")
+    with pytest.raises(ValueError, match="must be one of"):
+        LinearConfig(w4_qmv_backend="fast")
+    with pytest.raises(ValueError, match="renamed"):
+        LinearConfig.validate_values({"qmv_backend": "native"})
+    cfg = LinearConfig.from_dict({"w4_qmv_backend": "splitk", "hidden_size": 2560})
+    assert cfg.w4_qmv_backend == "splitk"
+
+
+def test_sdpa_config_contract():
+    with pytest.raises(ValueError, match="boolean"):
+        SDPAConfig.validate_values({"fused_quantized_sdpa": 1})
+    assert SDPAConfig().fused_quantized_sdpa is True
+
+
+def _layer(n=64, k=256, g=64):
+    wq = torch.zeros((n, k // 8), dtype=torch.int32)
+    s = torch.ones((n, k // g), dtype=torch.bfloat16)
+    b = torch.zeros((n, k // g), dtype=torch.bfloat16)
+    return QuantizedLinear(wq, s, b, group_size=g, bits=4)
+
+
+def test_affine_predicates_on_cpu_tensors_are_false():
+    layer = _layer()
+    p = AffineParameters.from_module(layer)
+    assert AffineParameters.accepts(layer)
+    assert not AffineParameters.supports_splitk((1, 256), torch.bfloat16, *p)
+    assert not AffineParameters.supports_multirow((1, 8, 256), torch.bfloat16, *p)
+    # the native projection runs only on the device: no CPU fallback
+    with pytest.raises(ValueError, match="GPU"):
+        dispatch_linear(torch.zeros((1, 256), dtype=torch.bfloat16), layer,
+                        config=LinearConfig(w4_qmv_backend="splitk"))
+
+
+def test_affine_validation_errors():
+    wq = torch.zeros((64, 32), dtype=torch.int32)
+    s = torch.ones((64, 4), dtype=torch.bfloat16)
+    x = torch.zeros((2, 256), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="exactly one activation row"):
+        ext.w4a16_qmv(x, wq, s, s)
+    with pytest.raises(ValueError, match="BF16 or F16"):
+        ext.affine_quantized_matmul(x.float(), wq, s, s, group_size=64)
+    with pytest.raises(ValueError, match="UINT32"):
+        ext.affine_quantized_matmul(x, wq.float(), s, s, group_size=64)
+    with pytest.raises(ValueError, match="shape"):
+        ext.affine_quantized_matmul(x, wq, s[:, :2], s[:, :2], group_size=64)
+    with pytest.raises(TypeError):
+        ext.w4a16_qmv(x[:1], None, s, s)
+    with pytest.raises(ValueError, match="algorithm"):
+        ext.w4a16_multirow(x, wq, s, s, algorithm="nope")
+
+
+def test_w8a8_validation_errors():
+    w = torch.zeros((16, 64), dtype=torch.int8)
+    sc = torch.ones(16)
+    with pytest.raises(ValueError, match="matching K"):
+        ext.w8a8_linear(torch.zeros((1, 32)), w, sc)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ext.w8a8_linear(torch.zeros((1, 48)), torch.zeros((16, 48), dtype=torch.int8), sc)
+    with pytest.raises(ValueError, match="scales"):
+        ext.w8a8_linear(torch.zeros((1, 64)), w, sc.double())
+    with pytest.raises(ValueError, match="INT8"):
+        ext.W8A8Linear(w.float(), sc)
+    with pytest.raises(ValueError, match="int8"):
+        ext.int8_matmul_int32(torch.zeros((1, 64)), w)
+
+
+def test_unpack_affine_w8_on_host():
+    # unsigned codes 0,128,255,1 -> signed -128,0,127,-127; scale repeated, bias -128*s
+    words = torch.tensor([[0x01FF8000]], dtype=torch.int32)
+    s = torch.full((1, 1), 0.5, dtype=torch.bfloat16)
+    b = torch.full((1, 1), -64.0, dtype=torch.bfloat16)
+    w8, sc = unpack_affine_w8(words, s, b, group_size=4)
+    assert w8.tolist() == [[-128, 0, 127, -127]] and sc.tolist() == [0.5]
+    with pytest.raises(ValueError, match="biases=-128"):
+        unpack_affine_w8(words, s, torch.zeros_like(b), group_size=4)
+    assert unpack_affine_w8(words, s, torch.zeros_like(b), group_size=4,
+                            allow_fallback=True) is None
+
+
+def test_sdpa_dispatch_validation():
+    class Cache:
+        bits, group_size = 8, 32
+
+    q = torch.zeros((1, 8, 1, 128))
+    keys = (torch.zeros((1, 2, 16, 128), dtype=torch.int8), torch.ones((1, 2, 16), dtype=torch.float16))
+    # CPU tensors never take the fused route, and a quantized cache has no
+    # other route
+    with pytest.raises(ValueError, match="quantized KV cache"):
+        dispatch_sdpa(q, keys, keys, cache=Cache(), scale=0.1, mask=None)
+    with pytest.raises(ValueError, match="single_pass_max_length"):
+        ext.int8_quantized_sdpa(q, keys, keys, scale=0.1, single_pass_max_length=-1)
+    with pytest.raises(ValueError, match="finite"):
+        ext.int8_quantized_sdpa(q, keys, keys, scale=float("nan"))
+    with pytest.raises(ValueError, match="L=1"):
+        ext.int8_quantized_sdpa(torch.zeros((1, 8, 2, 128)), keys, keys, scale=0.1)
+    # unquantized caches take torch's attention
+    out = dispatch_sdpa(torch.ones((1, 8, 1, 64)), torch.ones((1, 2, 5, 64)),
+                        torch.ones((1, 2, 5, 64)), cache=None, scale=0.125, mask=None)
+    assert torch.allclose(out, torch.ones_like(out))
+
+
+def test_package_surface():
+    for name in sparkq.__all__:
+        assert callable(getattr(sparkq, name))
+    assert sparkq.prepare_w4a16_nax4(1, 2, 3) == (1, 2, 3)

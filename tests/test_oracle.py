@@ -1,0 +1,307 @@
+"""Pins the CPU oracle (oracle/sparkq_oracle.c) with checks that do not retype
+its formulas: library conversions (torch, numpy), closed forms, invariants,
+extremes and brute force on tiny inputs. The reference ships no golden
+vectors or tests for this path (its tests/ directory is excluded from the
+repository), so these checks are the oracle's anchor.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+
+
+# ---------------------------------------------------------------------------
+# 16-bit conversions
+# ---------------------------------------------------------------------------
+
+def _specials():
+    v = [0.0, -0.0, 1.0, -1.0, 1.00390625, 1.01171875, 3.0e38, -3.0e38, 1e-40, -1e-40,
+         65504.0, 65519.0, 65520.0, 6.1e-5, 5.96e-8, 2.98e-8, 1e-8, float("inf"),
+         float("-inf"), 0.1, 1.0 / 3.0]
+    rng = np.random.default_rng(0)
+    v += list(rng.standard_normal(2000).astype(np.float32) * 10 ** rng.uniform(-8, 8, 2000))
+    # exact bf16 ties: halfway between two bf16 values
+    ties = (np.arange(1, 200, dtype=np.uint32) << 16) | 0x8000
+    v += list(ties.view(np.float32))
+    # exact f16 ties
+    h = np.arange(0x3C00, 0x3D00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    v += list((h[:-1] + (h[1:] - h[:-1]) / 2).astype(np.float32))
+    return np.array(v, dtype=np.float32)
+
+
+def test_bf16_rounding_matches_torch():
+    x = _specials()
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(o.bf16_bits(x), ref)
+    for f in x[:300]:
+        assert o.scalar_f32_to_bf16(float(f)) == int(o.bf16_bits(np.float32(f)).reshape(-1)[0])
+
+
+def test_f16_rounding_matches_numpy():
+    x = _specials()
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    ours = np.array([o.scalar_f32_to_f16(float(f)) for f in x], dtype=np.uint16)
+    assert np.array_equal(ours, ref)
+    back = np.array([o.scalar_f16_to_f32(int(h)) for h in ref[np.isfinite(x)]], np.float32)
+    assert np.array_equal(back, ref[np.isfinite(x)].view(np.float16).astype(np.float32))
+
+
+def test_generator_deterministic_and_normal():
+    a = o.randn(0, 7, 200001)
+    assert np.array_equal(a, o.randn(0, 7, 200001))
+    assert not np.array_equal(a[:100], o.randn(0, 8, 100))
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1.0) < 0.01
+    assert np.array_equal(o.randn16(0, 7, 1001, 0.02, o.BF16), o.bf16_bits(o.randn(0, 7, 1001, 0.02)))
+    assert np.array_equal(o.randn16(0, 7, 999, 1.0, o.F16), o.f16_bits(o.randn(0, 7, 999)))
+
+
+# ---------------------------------------------------------------------------
+# W4 layout, quantizers, dequantization, matmul
+# ---------------------------------------------------------------------------
+
+def test_pack4_layout_known_answer():
+    # code k of a word sits at bits 4*(k%8): codes 1..8 -> 0x87654321
+    codes = np.array([[1, 2, 3, 4, 5, 6, 7, 8, 15, 0, 0, 0, 0, 0, 0, 9]], np.uint8)
+    w = o.pack4(codes)
+    assert w.tolist() == [[0x87654321, 0x9000000F]]
+    # little-endian byte view: byte k/2, even k in the low nibble
+    b = w.view(np.uint8)[0]
+    assert b[0] == 0x21 and b[4] == 0x0F and b[7] == 0x90
+
+
+def test_pack4_round_trip():
+    rng = np.random.default_rng(1)
+    codes = rng.integers(0, 16, (7, 64), dtype=np.uint8)
+    assert np.array_equal(o.unpack4(o.pack4(codes), 64), codes)
+
+
+def _w(shape, seed=0, std=0.02):
+    return o.bits_to_f32(o.randn16(seed, 11, int(np.prod(shape)), std, o.BF16), o.BF16).reshape(shape)
+
+
+@pytest.mark.parametrize("g", [32, 64, 128])
+@pytest.mark.parametrize("dt", [o.BF16, o.F16])
+def test_w4_quantize_properties(g, dt):
+    w = _w((16, 256), seed=g)
+    if dt == o.F16:
+        w = o.bits_to_f32(o.f16_bits(w), o.F16).reshape(w.shape)
+    wq, s16, b16 = o.w4_quantize(w, g, dt)
+    codes = o.unpack4(wq, 256).reshape(16, -1, g).astype(np.int64)
+    s = o.bits_to_f32(s16, dt)[..., None]
+    b = o.bits_to_f32(b16, dt)[..., None]
+    grp = w.reshape(16, -1, g)
+    # scale and bias are the stated statistics rounded to the storage dtype
+    assert np.array_equal(s16, o.round16((grp.max(-1) - grp.min(-1)) / np.float32(15), dt))
+    assert np.array_equal(b16, o.round16(grp.min(-1), dt))
+    assert codes.min() >= 0 and codes.max() <= 15
+    # codes are monotone in w within a group
+    order = np.argsort(grp, axis=-1, kind="stable")
+    assert np.all(np.diff(np.take_along_axis(codes, order, -1), axis=-1) >= 0)
+    # reconstruction error is at most half a step (plus the bias rounding)
+    err = np.abs(codes * s + b - grp)
+    assert np.all(err <= s / 2 + np.abs(b - grp.min(-1, keepdims=True)) + 1e-7)
+    # the group minimum is code 0
+    assert np.all(np.take_along_axis(codes, grp.argmin(-1)[..., None], -1) == 0)
+
+
+def test_w4_quantize_constant_group():
+    w = np.full((1, 64), 0.25, np.float32)
+    wq, s, b = o.w4_quantize(w, 64, o.BF16)
+    assert wq.max() == 0 and s[0, 0] == 0 and o.bits_to_f32(b, o.BF16)[0, 0] == 0.25
+
+
+def test_converter_quantizer_properties():
+    w = _w((8, 128), seed=3, std=0.05)
+    w[0, :32] = 0.0
+    wq, s16, b16 = o.w4_quantize_converter(w, 32)
+    codes = o.unpack4(wq, 128).reshape(8, 4, 32).astype(np.float64)
+    s = o.bits_to_f32(s16, o.BF16)[..., None].astype(np.float64)
+    b = o.bits_to_f32(b16, o.BF16)[..., None].astype(np.float64)
+    grp = w.reshape(8, 4, 32).astype(np.float64)
+    # an all-zero group has scale 1, zero point 0 and reconstructs to 0
+    assert o.bits_to_f32(s16, o.BF16)[0, 0] == 1.0 and np.all(codes[0, 0] == 0)
+    assert np.all(codes[0, 0] * s[0, 0] + b[0, 0] == 0)
+    # zero lies in the representable range and values reconstruct to <= s/2
+    # (+ the bf16 rounding of the scale and of the offset -zero*s)
+    err = np.abs(codes * s + b - grp)
+    slack = s * (2.0 ** -8) * 16 + np.abs(b) * 2.0 ** -8
+    assert np.all(err <= s / 2 + slack)
+
+
+@pytest.mark.parametrize("dt", [o.BF16, o.F16])
+def test_w4_dequantize_is_single_rounding(dt):
+    rng = np.random.default_rng(5)
+    n, k, g = 6, 128, 32
+    codes = rng.integers(0, 16, (n, k), dtype=np.uint8)
+    codes[0, :16] = np.arange(16)
+    wq = o.pack4(codes)
+    sv = (rng.standard_normal((n, k // g)) * 10 ** rng.uniform(-6, 3, (n, k // g))).astype(np.float32)
+    bv = (rng.standard_normal((n, k // g)) * 10 ** rng.uniform(-6, 3, (n, k // g))).astype(np.float32)
+    sv[1, 0], bv[1, 0], sv[1, 1], bv[1, 1] = 0.0, -0.0, -0.0, 0.0
+    s16, b16 = o.round16(sv, dt), o.round16(bv, dt)
+    if dt == o.BF16:
+        s16[2, 0], b16[2, 0] = 0x0001, 0x8001  # subnormal bf16
+    out = o.w4_dequantize(wq, s16, b16, g, dt)
+    s = np.repeat(o.bits_to_f32(s16, dt).astype(np.float64), g, axis=1)
+    b = np.repeat(o.bits_to_f32(b16, dt).astype(np.float64), g, axis=1)
+    exact = codes.astype(np.float64) * s + b  # exact product, one rounding below
+    assert np.array_equal(out, exact.astype(np.float32))
+
+
+def test_w4a16_matmul_against_numpy_and_special_cases():
+    m, n, k, g = 3, 5, 128, 64
+    w = _w((n, k), seed=9)
+    wq, s, b = o.w4_quantize(w, g)
+    deq = o.w4_dequantize(wq, s, b, g).astype(np.float64)
+    x16 = o.randn16(0, 21, m * k).reshape(m, k)
+    xf = o.bits_to_f32(x16, o.BF16).astype(np.float64)
+    y = o.w4a16_matmul(x16, wq, s, b, g)
+    assert np.allclose(y, xf @ deq.T, rtol=1e-12, atol=1e-12)
+    # one-hot rows select dequantized weight columns exactly
+    onehot = np.zeros((2, k), np.float32)
+    onehot[0, 7] = 1.0
+    onehot[1, 100] = 1.0
+    yh = o.w4a16_matmul(o.bf16_bits(onehot), wq, s, b, g)
+    assert np.array_equal(yh[0], deq[:, 7]) and np.array_equal(yh[1], deq[:, 100])
+    # zero scales: y = b * sum(x) per group
+    s0 = np.zeros_like(s)
+    y0 = o.w4a16_matmul(x16, wq, s0, b, g)
+    bf = o.bits_to_f32(b, o.BF16).astype(np.float64)
+    xs = xf.reshape(m, k // g, g).sum(-1)
+    assert np.allclose(y0, xs @ bf.T, rtol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# W8A8
+# ---------------------------------------------------------------------------
+
+def test_a8_quantize_known_answers():
+    x = np.zeros((4, 32), np.float32)
+    x[1] = 1.0                                   # amax 1 -> scale 1/127 -> 127
+    x[2, 0], x[2, 1], x[2, 2] = 2.54, -2.54, 0.01  # exact +-amax -> +-127
+    x[3, :3] = [2.5, 1.5, -127.0]                # ties at .5 go to even
+    q, sc = o.a8_quantize(x)
+    assert sc[0] == 1.0 and np.all(q[0] == 0)    # all-zero row: scale 1
+    assert sc[1] == np.float32(1.0) / np.float32(127) and np.all(q[1] == 127)
+    assert q[2, 0] == 127 and q[2, 1] == -127 and q[2, 2] == 0
+    assert sc[3] == np.float32(127.0) / np.float32(127.0)
+    assert q[3, 0] == 2 and q[3, 1] == 2 and q[3, 2] == -127
+
+
+def test_a8_quantize_properties():
+    x = o.randn(3, 1, 4 * 2560).reshape(4, 2560)
+    q, sc = o.a8_quantize(x)
+    assert np.all(np.abs(q) <= 127)
+    assert np.all(np.abs(q).max(1) == 127)
+    err = np.abs(q.astype(np.float64) * sc[:, None] - x)
+    assert np.all(err <= sc[:, None] * (0.5 + 1e-6))
+
+
+def test_int8_matmul_exact_and_extremes():
+    rng = np.random.default_rng(2)
+    a = rng.integers(-128, 128, (5, 96), dtype=np.int8)
+    b = rng.integers(-128, 128, (7, 96), dtype=np.int8)
+    assert np.array_equal(o.int8_matmul(a, b), a.astype(np.int64) @ b.astype(np.int64).T)
+    # K = 131040 at (-128)*(-128) is the largest sum that still fits int32
+    k = 131040
+    big = np.full((1, k), -128, np.int8)
+    c = o.int8_matmul(big, big)
+    assert int(c[0, 0]) == 16384 * k
+    with pytest.raises(OverflowError):
+        o.int8_matmul(np.full((1, k + 32), -128, np.int8), np.full((1, k + 32), -128, np.int8))
+
+
+def test_w8a8_epilogue_is_fused():
+    rng = np.random.default_rng(4)
+    acc = rng.integers(-2 ** 30, 2 ** 30, (3, 9)).astype(np.int32)
+    sa = rng.random(3).astype(np.float32) * 0.02
+    sw = rng.random(9).astype(np.float32) * 0.01
+    bias = rng.standard_normal(9).astype(np.float32)
+    y = o.w8a8_epilogue(acc, sa, sw, bias)
+    t = (acc.astype(np.float32) * sa[:, None]).astype(np.float64)
+    exact = t * sw.astype(np.float64)[None] + bias[None]  # t*sw exact in fp64
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(y - exact) <= 0.5 * ulp + 1e-30)
+    # README known answer adapted to W8A8: ones(32) x ones(4,32), scale 1 -> 32
+    q, sc = o.a8_quantize(np.ones((1, 32), np.float32))
+    acc1 = o.int8_matmul(q, np.ones((4, 32), np.int8))
+    y1 = o.w8a8_epilogue(acc1, sc, np.ones(4, np.float32))
+    assert np.all(o.bf16_bits(y1) == o.bf16_bits(np.float32(32.0)))
+
+
+def test_w8_unpack_affine():
+    codes = np.array([[0, 1, 127, 128, 129, 255, 200, 55]], np.uint8)  # unsigned storage
+    words = codes.view(np.uint32).reshape(1, 2)
+    assert o.w8_unpack_affine(words).tolist() == [[-128, -127, -1, 0, 1, 127, 72, -73]]
+
+
+# ---------------------------------------------------------------------------
+# INT8 KV and decode attention
+# ---------------------------------------------------------------------------
+
+def test_kv_quantize_s8_properties():
+    x = o.randn(5, 2, 64 * 128).reshape(64, 128)
+    x[3] = 0.0
+    codes, sc = o.kv_quantize_s8(x)
+    s = sc.view(np.float16).astype(np.float32)
+    assert s[3] == 1.0 and np.all(codes[3] == 0)
+    live = np.arange(64) != 3
+    assert np.array_equal(sc[live], (np.abs(x[live]).max(1) / np.float32(127)).astype(np.float16).view(np.uint16))
+    assert np.all(np.abs(codes) <= 127)
+    err = np.abs(codes[live] * s[live, None] - x[live])
+    assert np.all(err <= s[live, None] * 0.5 + np.abs(x[live]).max(1, keepdims=True) * 2 ** -10)
+
+
+def test_kv_affine_u8_round_trip():
+    x = o.randn(6, 2, 16 * 128).reshape(16, 128)
+    packed, s, b = o.kv_quantize_affine_u8(x, 32, o.BF16)
+    deq = o.kv_dequantize_affine_u8(packed, s, b, 32, o.BF16)
+    sf = np.repeat(o.bits_to_f32(s, o.BF16), 32, axis=1)
+    assert np.all(np.abs(deq - x) <= sf * 0.5 + np.abs(x) * 2 ** -7 + 1e-6)
+
+
+def _sdpa_np(q, k, v, scale):
+    rep = q.shape[1] // k.shape[1]
+    k = np.repeat(k.astype(np.float64), rep, axis=1)
+    v = np.repeat(v.astype(np.float64), rep, axis=1)
+    s = np.einsum("bhd,bhnd->bhn", q.astype(np.float64), k) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("bhn,bhnd->bhd", p, v)
+
+
+def test_sdpa_decode_against_numpy_and_invariants():
+    b, hq, hkv, n, d = 2, 8, 2, 37, 64
+    q = o.randn(1, 1, b * hq * d).reshape(b, hq, d)
+    k = o.randn(1, 2, b * hkv * n * d).reshape(b, hkv, n, d)
+    v = o.randn(1, 3, b * hkv * n * d).reshape(b, hkv, n, d)
+    scale = 1 / math.sqrt(d)
+    out = o.sdpa_decode(q, k, v, scale)
+    assert np.allclose(out, _sdpa_np(q, k, v, scale), rtol=1e-12, atol=1e-12)
+    # a single token returns its value row
+    o1 = o.sdpa_decode(q, k[:, :, :1].copy(), v[:, :, :1].copy(), scale)
+    assert np.allclose(o1, np.repeat(v[:, :, 0], hq // hkv, axis=1), atol=1e-7)
+    # identical keys average the values
+    kk = np.repeat(k[:, :, :1], n, axis=2)
+    om = o.sdpa_decode(q, kk, v, scale)
+    assert np.allclose(om, np.repeat(v.mean(2), hq // hkv, axis=1), atol=1e-6)
+    # token order does not matter
+    perm = np.random.default_rng(0).permutation(n)
+    op = o.sdpa_decode(q, k[:, :, perm].copy(), v[:, :, perm].copy(), scale)
+    assert np.allclose(op, out, atol=1e-12)
+
+
+def test_cpu_baseline_matches_oracle():
+    m, n, k, g = 2, 96, 256, 64
+    w = _w((n, k), seed=12)
+    wq, s, b = o.w4_quantize(w, g)
+    x16 = o.randn16(0, 13, m * k).reshape(m, k)
+    y, used = o.cpu_w4a16_gemv(x16, wq, s, b, g)
+    assert used >= 1
+    ref = o.w4a16_matmul(x16, wq, s, b, g)
+    assert np.abs(y - ref).max() < 1e-4
