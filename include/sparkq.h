@@ -74,8 +74,13 @@ int sparkq_is_available(void);
  *   y       [M,N]   y_dtype (x_dtype, or F32 for the unrounded epilogue)
  * group_size in {32, 64, 128}; bits must be 4; K % 64 == 0; K % G == 0.
  * Dispatches internally: M <= 32 runs the weight-streaming skinny kernel
- * (MFMA 32x32x16, split-K with a reduction pass when the shape needs it),
+ * (MFMA 32x32x16; when the shape splits K across workgroups the last
+ * workgroup of each 32-row tile combines the partials in the same launch),
  * larger M runs the LDS-tiled MFMA GEMM behind a group-sum prologue.
+ * Workspace: the first 16384 bytes hold per-tile counters and must be zero
+ * before the first call; every call leaves them zero again. Give each entry
+ * point its own workspace buffer, and do not share one buffer between
+ * streams.
  *
  * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True,
  * group_size, bits, mode="affine") as called by AffineParameters.native
@@ -91,9 +96,9 @@ int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
                         int y_dtype, void* workspace, size_t workspace_bytes,
                         void* stream);
 
-/* Exact dequantization to fp32: out[n,k] = q[n,k] * s[n,k/G] + b[n,k/G].
- * The product of a 4-bit code and a 16-bit float is exact in fp32, so the
- * result has one rounding and is bit-identical however it is computed.
+/* Dequantization to fp32: out[n,k] = fmaf(q[n,k], s[n,k/G], b[n,k/G]), the
+ * exact q*s+b rounded once. (The product of a 4-bit code and a 16-bit float
+ * is exact in fp32 unless it overflows, so mul-then-add agrees except there.)
  * Debug entry; the reference's equivalent is the per-element decode of the
  * affine kernels (X/spark_mlx_ext/_w4a16_multirow_sources.py:31-39). */
 int sparkq_w4a16_dequantize(const uint32_t* w, const void* scales,
@@ -125,14 +130,16 @@ int sparkq_a8_quantize_per_token(const void* x, int8_t* q, float* scales,
 /* Raw int32 C[M,N] = A[M,K] . B[N,K]^T, exact. Replaces int8_matmul_int32
  * (X/src/spark_w8a8.cpp:218-228, X/src/bindings.cpp:33-35).
  * K % 32 == 0 and K <= 131040 so that no int32 sum can overflow. The
- * workspace holds int32 split-K partials when the shape uses them. */
+ * workspace holds split-K tile counters (first 16384 bytes, zero before the
+ * first call and left zero by every call) and int32 partials. */
 size_t sparkq_int8_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int sparkq_int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c,
                            int64_t M, int64_t N, int64_t K, void* workspace,
                            size_t workspace_bytes, void* stream);
 
-/* Workspace for sparkq_w8a8_linear: the int8 activations, their fp32 scales
- * and any split-K int32 partials. */
+/* Workspace for sparkq_w8a8_linear: split-K tile counters (first 16384
+ * bytes, zero before the first call and left zero by every call), the int8
+ * activations, their fp32 scales and any split-K int32 partials. */
 size_t sparkq_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* y[m,n] = to_dtype(fmaf(float(acc[m,n]) * sa[m], sw[n], bias[n])) with acc

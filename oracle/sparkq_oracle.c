@@ -216,7 +216,7 @@ void sq_w4_dequantize(const uint32_t* wq, const uint16_t* scales,
       float q = (float)((wq[n * (K / 8) + k / 8] >> (4 * (k % 8))) & 15u);
       float s = sq_widen16(scales[n * ng + k / G], sdtype);
       float b = sq_widen16(biases[n * ng + k / G], sdtype);
-      out[n * K + k] = q * s + b; /* q*s exact: one rounding */
+      out[n * K + k] = fmaf(q, s, b); /* one rounding, also at overflow */
     }
 }
 
@@ -231,7 +231,7 @@ void sq_w4a16_matmul(const uint16_t* x, int xdtype, const uint32_t* wq,
         float q = (float)((wq[n * (K / 8) + k / 8] >> (4 * (k % 8))) & 15u);
         float s = sq_widen16(scales[n * ng + k / G], xdtype);
         float b = sq_widen16(biases[n * ng + k / G], xdtype);
-        float wv = q * s + b;
+        float wv = fmaf(q, s, b);
         acc += (double)sq_widen16(x[m * K + k], xdtype) * (double)wv;
       }
       y[m * N + n] = acc;

@@ -71,8 +71,9 @@ void sq_w4_quantize_converter(const float* w, int64_t N, int64_t K, int G,
                               uint32_t* wq, uint16_t* scales,
                               uint16_t* biases);
 
-/* Exact fp32 dequantization q*s+b (the product is exact, so one rounding):
- * per-element decode of X/spark_mlx_ext/_w4a16_multirow_sources.py:31-39. */
+/* fp32 dequantization fmaf(q, s, b): the exact q*s+b rounded once. (q*s is
+ * exact unless it overflows, so mul-then-add agrees except there.)
+ * Per-element decode of X/spark_mlx_ext/_w4a16_multirow_sources.py:31-39. */
 void sq_w4_dequantize(const uint32_t* wq, const uint16_t* scales,
                       const uint16_t* biases, int64_t N, int64_t K, int G,
                       int sdtype, float* out);

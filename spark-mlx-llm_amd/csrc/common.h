@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "sparkq.h"
 
@@ -37,12 +38,16 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-// Element traits of the 16-bit activation types. OFFSET/MAGIC give the
-// exponent pattern under which a 4-bit code q placed in the low mantissa bits
-// reads as exactly OFFSET + q.
+// Element traits of the 16-bit activation types. MAGIC is the exponent
+// pattern under which a 4-bit code q placed in the low mantissa bits reads as
+// exactly MAGIC_VALUE + q; OFFSET is what remains in the decoded operand.
+// fp16 removes its 1024 exactly with a packed fp16 subtract (OFFSET 0);
+// bf16 has no packed subtract and keeps 128 + q, which the per-group epilogue
+// corrects with b' = b - 128*s.
 struct BF16 {
   static constexpr int code = SPARKQ_BF16;
   static constexpr uint32_t MAGIC = 0x43004300u;  // bf16 128.0 in each half
+  static constexpr bool kExactDecode = false;
   static constexpr float OFFSET = 128.0f;
   __device__ static __forceinline__ float to_f32(uint16_t h) { return bf16_to_f32(h); }
   __device__ static __forceinline__ uint16_t from_f32(float f) { return f32_to_bf16(f); }
@@ -50,7 +55,8 @@ struct BF16 {
 struct F16 {
   static constexpr int code = SPARKQ_F16;
   static constexpr uint32_t MAGIC = 0x64006400u;  // fp16 1024.0 in each half
-  static constexpr float OFFSET = 1024.0f;
+  static constexpr bool kExactDecode = true;
+  static constexpr float OFFSET = 0.0f;
   __device__ static __forceinline__ float to_f32(uint16_t h) { return f16_to_f32(h); }
   __device__ static __forceinline__ uint16_t from_f32(float f) { return f32_to_f16(f); }
 };
@@ -69,10 +75,17 @@ __device__ __forceinline__ f32x16_t mfma32x32x16<F16>(u32x4_t a, u32x4_t b, f32x
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
 // Decode one uint32 of eight 4-bit codes (code j at bits 4j) into the four
 // packed 16-bit pairs (OFFSET+q[2i], OFFSET+q[2i+1]), i = 0..3, in natural k
 // order: a byte permute pulls code 2i from w and code 2i+1 from w>>4 into the
 // low nibble of each half, and one and-or masks the nibble under MAGIC.
+__device__ __forceinline__ uint32_t exact_f16_pair(uint32_t r) {
+  const f16x2_t v = __builtin_bit_cast(f16x2_t, r) - f16x2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 template <typename T>
 __device__ __forceinline__ u32x4_t decode_w4(uint32_t w) {
   const uint32_t ws = w >> 4;
@@ -81,6 +94,12 @@ __device__ __forceinline__ u32x4_t decode_w4(uint32_t w) {
   r.y = (__builtin_amdgcn_perm(ws, w, 0x0C050C01u) & 0x000F000Fu) | T::MAGIC;
   r.z = (__builtin_amdgcn_perm(ws, w, 0x0C060C02u) & 0x000F000Fu) | T::MAGIC;
   r.w = (__builtin_amdgcn_perm(ws, w, 0x0C070C03u) & 0x000F000Fu) | T::MAGIC;
+  if constexpr (T::kExactDecode) {
+    r.x = exact_f16_pair(r.x);
+    r.y = exact_f16_pair(r.y);
+    r.z = exact_f16_pair(r.z);
+    r.w = exact_f16_pair(r.w);
+  }
   return r;
 }
 
@@ -106,6 +125,58 @@ __device__ __forceinline__ float load_in(const void* p, int64_t idx, int dtype) 
   return dtype == SPARKQ_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
 
+// ---------------------------------------------------------------------------
+// split-K handshake: combine per-workgroup partials in the same launch
+// ---------------------------------------------------------------------------
+// Partials are written and read with device-scope relaxed atomics, which take
+// the coherent path between the XCDs' L2 caches without the L2 writeback and
+// invalidate that a device-scope fence costs. A workgroup waits until its own
+// partial stores are performed (s_waitcnt 0) before bumping the tile counter,
+// so the workgroup that sees the count reach S-1 finds every partial in
+// place; it resets the counter to zero for the next launch.
+template <typename V>
+__device__ __forceinline__ void splitk_store(V* p, V v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V>
+__device__ __forceinline__ V splitk_load(const V* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Returns true in the last workgroup to arrive at *counter (all threads).
+__device__ __forceinline__ bool splitk_arrive(unsigned* counter, int S, int* s_last) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (unsigned)(S - 1);
+  __syncthreads();
+  return *s_last != 0;
+}
+
+__device__ __forceinline__ void splitk_reset(unsigned* counter) {
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum of S partials p[0], p[stride], ... in split order, loads issued in
+// batches of eight so that they overlap.
+template <typename V>
+__device__ __forceinline__ V splitk_sum(const V* p, int64_t stride, int S) {
+  V s = 0;
+  int k = 0;
+  for (; k + 8 <= S; k += 8) {
+    V v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = splitk_load(p + (k + u) * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; k < S; ++k) s += splitk_load(p + k * stride);
+  return s;
+}
+
 }  // namespace sparkq
 
 // ---------------------------------------------------------------------------
@@ -117,5 +188,18 @@ int check_launch(const char* what);
 int device_check();
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// positive integer from the environment, or dflt
+inline int64_t env_int(const char* name, int64_t dflt) {
+  const char* e = getenv(name);
+  const long long v = e ? atoll(e) : 0;
+  return v > 0 ? (int64_t)v : dflt;
+}
 inline size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
+
+// Split-K workspaces start with a fixed block of tile counters: zero before
+// the first call, and every call leaves them zero. The block has the same
+// size for every shape so that one call's partials never overlap another
+// call's counters; shapes with more tiles than it holds do not split K.
+constexpr size_t kCounterBytes = 16384;
+constexpr int64_t kMaxCounterTiles = (int64_t)(kCounterBytes / 4);
 }  // namespace sparkq

@@ -7,15 +7,17 @@
 // codes and activations are exact; accumulation and the epilogue are fp32.
 //
 // Kernels
-//   w4_dequant_kernel   exact fp32 q*s+b (debug / bit-exact check entry)
+//   w4_dequant_kernel   fp32 fmaf(q, s, b) (debug / bit-exact check entry)
 //   w4_quantize_kernel  affine 4-bit quantizer (format producer)
 //   w4_skinny_kernel    M <= 32: weight streaming, 32 rows x 64 k per wave
 //                       step, MFMA 32x32x16, in-workgroup split-K over waves,
-//                       optional cross-workgroup split-K into fp32 partials
-//   splitk_reduce_kernel  sums the partials in a fixed order -> y
+//                       cross-workgroup split-K combined in the same launch by
+//                       the last workgroup of each tile
 //   xsum_kernel         group sums X_g[m] for the GEMM, layout [K/G][M]
 //   w4_gemm_kernel      M > 32: 128x128x64 LDS tiles (A bf16/f16, B decoded
 //                       to OFFSET+q), double-buffered, MFMA 32x32x16
+#include <cstdlib>
+
 #include "common.h"
 
 namespace sparkq {
@@ -39,7 +41,7 @@ __global__ __launch_bounds__(256) void w4_dequant_kernel(
   const uint32_t v = w[idx];
   float o[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = (float)((v >> (4 * j)) & 15u) * sv + bv;
+  for (int j = 0; j < 8; ++j) o[j] = fmaf((float)((v >> (4 * j)) & 15u), sv, bv);
   f32x4_t* dst = reinterpret_cast<f32x4_t*>(out + n * K + k0);
   dst[0] = f32x4_t{o[0], o[1], o[2], o[3]};
   dst[1] = f32x4_t{o[4], o[5], o[6], o[7]};
@@ -88,13 +90,34 @@ __global__ __launch_bounds__(256) void w4_quantize_kernel(
 // ---------------------------------------------------------------------------
 // skinny kernel (M <= MB <= 32)
 // ---------------------------------------------------------------------------
-// Workgroup = 4 waves; tile = 32 weight rows; the workgroup's K range
-// (a split of cps 64-k chunks) is shared round-robin by its waves.
-// Wave step: lane (n = l%32, j = l/32) holds 16 bytes = 32 codes of row n at
+// Workgroup = 4 waves; tile = 32 weight rows; the workgroup's K range (a
+// split of cps 64-k chunks) is shared round-robin by its waves, each keeping
+// two batches of kSkinnyU chunk loads in flight.
+// Chunk step: lane (n = l%32, j = l/32) holds 16 bytes = 32 codes of row n at
 // k = 64c + 32j, i.e. four MFMA k-slots of 8; the A operand is the matching
-// 16 bytes of x row m = l%32 read from an LDS copy of the split's x slab.
-// Each 64-k chunk ends with the per-group epilogue in fp32.
-constexpr int kSkinnyU = 4;  // chunks a wave keeps in flight per batch
+// 16 bytes of x row m = l%32 from an LDS copy of the split's x slab. Per
+// chunk, four MFMAs accumulate x.(OFFSET+q) and four more accumulate x.1 (a
+// constant all-ones B operand), which lands the group sums X_g[m] directly in
+// the output lane layout; the chunk then ends with the fp32 epilogue
+// acc += s*T + (b - OFFSET*s)*X. Splits of K combine in the same launch:
+// every workgroup writes its fp32 partial, and the last one to arrive at the
+// tile's counter sums the partials in split order (deterministic) and resets
+// the counter to zero.
+constexpr int kSkinnyU = 4;  // chunks per batch; two batches in flight
+
+struct SkinnyArgs {
+  const uint16_t* x;
+  const uint32_t* w;
+  const uint16_t* sc;
+  const uint16_t* bi;
+  float* part;          // [S][M][N] fp32 partials (S > 1)
+  unsigned* counters;   // [ceil(N/32)] zero on entry, zero on exit (S > 1)
+  void* y;
+  int y_dtype;
+  int M, N, K;
+  int cps;              // 64-k chunks per split
+  int S;
+};
 
 template <typename T, int G>
 struct ChunkMeta {
@@ -116,36 +139,51 @@ struct ChunkMeta {
   }
 };
 
+template <typename T>
+struct Ones;
+template <>
+struct Ones<BF16> {
+  static constexpr uint32_t pair = 0x3F803F80u;  // bf16 1.0, 1.0
+};
+template <>
+struct Ones<F16> {
+  static constexpr uint32_t pair = 0x3C003C00u;  // fp16 1.0, 1.0
+};
+
+// Rows of the 32x32 output a lane holds for row-bucket MB: accumulators v <
+// VM cover rows 8*(v/4) + 4*(l/32) + v%4 < MB (MB = 1 keeps v = 0 only).
+template <int MB>
+struct RowBucket {
+  static constexpr int VM = MB >= 8 ? MB / 2 : 1;
+};
+
 template <typename T, int G, int MB>
-__global__ __launch_bounds__(256, 2) void w4_skinny_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
-    const uint16_t* __restrict__ sc, const uint16_t* __restrict__ bi,
-    float* __restrict__ part, void* __restrict__ y, int y_dtype, int M, int N,
-    int K, int cps) {
-  constexpr int VM = MB / 2;  // accumulators per lane holding rows < MB
+__global__ __launch_bounds__(256, 2) void w4_skinny_kernel(SkinnyArgs a) {
+  constexpr int VM = RowBucket<MB>::VM;
   constexpr int U = kSkinnyU;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ float red[4][VM][64];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane >> 5;
+  const int M = a.M, N = a.N, K = a.K;
   const int n0 = blockIdx.x * 32;
   const int split = blockIdx.y;
   const int nchunks = K >> 6;
-  const int c_begin = split * cps;
-  const int nc = min(cps, nchunks - c_begin);
+  const int c_begin = split * a.cps;
+  const int nc = min(a.cps, nchunks - c_begin);
   const int ngroups = K / G;
 
-  // LDS: x slab [M][nc*64 + 8] (16-bit), then half-chunk sums [2*nc][MB] fp32
+  // LDS x slab [M][nc*64 + 8] (16-bit)
   const int xpitch = nc * 64 + 8;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  float* xh = reinterpret_cast<float*>(smem + (size_t)M * xpitch * 2);
-  float* red = reinterpret_cast<float*>(smem);  // reused after the main loop
 
   const int n = n0 + (lane & 31);
   const int nr = n < N ? n : N - 1;
-  const uint32_t* wrow = w + (int64_t)nr * (K >> 3) + (int64_t)c_begin * 8 + 4 * j;
-  const uint16_t* srow = sc + (int64_t)nr * ngroups;
-  const uint16_t* brow = bi + (int64_t)nr * ngroups;
+  const uint32_t* wrow = a.w + (int64_t)nr * (K >> 3) + (int64_t)c_begin * 8 + 4 * j;
+  const uint16_t* srow = a.sc + (int64_t)nr * ngroups;
+  const uint16_t* brow = a.bi + (int64_t)nr * ngroups;
 
   u32x4_t wa[U], wb[U];
   uint32_t sa[U], ba[U], sb[U], bbv[U];
@@ -161,31 +199,17 @@ __global__ __launch_bounds__(256, 2) void w4_skinny_kernel(
     }
   };
 
-  // issue the first weight batch before staging x
+  // both weight batches go out before the x slab is staged
   load_batch(wave, wa, sa, ba);
-
-  // stage x[0:M][c_begin*64 : +nc*64] into LDS (16-byte pieces)
+  load_batch(wave + 4 * U, wb, sb, bbv);
   {
     const int pieces_per_row = nc * 8;
     const int total = M * pieces_per_row;
     for (int p = tid; p < total; p += 256) {
       const int m = p / pieces_per_row, pc = p - m * pieces_per_row;
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(
-          x + (int64_t)m * K + (int64_t)c_begin * 64 + pc * 8);
-      *reinterpret_cast<u32x4_t*>(xs + m * xpitch + pc * 8) = v;
+      *reinterpret_cast<u32x4_t*>(xs + m * xpitch + pc * 8) = *reinterpret_cast<const u32x4_t*>(
+          a.x + (int64_t)m * K + (int64_t)c_begin * 64 + pc * 8);
     }
-  }
-  __syncthreads();
-  // half-chunk (32 k) sums of x, rows >= M are zero
-  for (int p = tid; p < 2 * nc * MB; p += 256) {
-    const int h = p / MB, m = p - h * MB;
-    float s = 0.0f;
-    if (m < M) {
-      const uint16_t* src = xs + m * xpitch + h * 32;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) s += T::to_f32(src[i]);
-    }
-    xh[h * MB + m] = s;
   }
   __syncthreads();
 
@@ -196,99 +220,87 @@ __global__ __launch_bounds__(256, 2) void w4_skinny_kernel(
   const int am = lane & 31;
   const bool a_ok = am < M;
   const uint16_t* arow = xs + (a_ok ? am : 0) * xpitch + 32 * j;
+  const u32x4_t ones = {Ones<T>::pair, Ones<T>::pair, Ones<T>::pair, Ones<T>::pair};
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
 
-  auto compute_batch = [&](int cl0, const u32x4_t* wv, const uint32_t* sv,
-                           const uint32_t* bv) {
+  auto compute_batch = [&](int cl0, const u32x4_t* wv, const uint32_t* sv, const uint32_t* bv) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int cl = cl0 + 4 * u;
       if (cl < nc) {
-        f32x16_t t0 = {}, t1 = {};
+        f32x16_t t0 = {}, t1 = {}, x0 = {}, x1 = {};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const u32x4_t bq = decode_w4<T>(wv[u][t]);
-          u32x4_t a = {0u, 0u, 0u, 0u};
-          if (a_ok) a = *reinterpret_cast<const u32x4_t*>(arow + cl * 64 + 8 * t);
+          u32x4_t av = zero;
+          if (a_ok) av = *reinterpret_cast<const u32x4_t*>(arow + cl * 64 + 8 * t);
           if constexpr (G == 32) {
-            const u32x4_t z = {0u, 0u, 0u, 0u};
-            t0 = mfma32x32x16<T>(j == 0 ? a : z, bq, t0);
-            t1 = mfma32x32x16<T>(j == 1 ? a : z, bq, t1);
+            const u32x4_t a0 = j == 0 ? av : zero, a1 = j == 1 ? av : zero;
+            t0 = mfma32x32x16<T>(a0, bq, t0);
+            t1 = mfma32x32x16<T>(a1, bq, t1);
+            x0 = mfma32x32x16<T>(a0, ones, x0);
+            x1 = mfma32x32x16<T>(a1, ones, x1);
           } else {
-            t0 = mfma32x32x16<T>(a, bq, t0);
+            t0 = mfma32x32x16<T>(av, bq, t0);
+            x0 = mfma32x32x16<T>(av, ones, x0);
           }
         }
         const float s0 = T::to_f32((uint16_t)(sv[u] & 0xFFFFu));
         const float b0 = fmaf(-T::OFFSET, s0, T::to_f32((uint16_t)(bv[u] & 0xFFFFu)));
-        const float* h0 = xh + (2 * cl) * MB + 4 * j;
-        const float* h1 = h0 + MB;
         if constexpr (G == 32) {
           const float s1 = T::to_f32((uint16_t)(sv[u] >> 16));
           const float b1 = fmaf(-T::OFFSET, s1, T::to_f32((uint16_t)(bv[u] >> 16)));
 #pragma unroll
-          for (int q4 = 0; q4 < VM / 4; ++q4) {
-            const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(h0 + 8 * q4);
-            const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(h1 + 8 * q4);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int v = 4 * q4 + r;
-              float a0 = fmaf(s0, t0[v], acc[v]);
-              a0 = fmaf(b0, x0[r], a0);
-              a0 = fmaf(s1, t1[v], a0);
-              acc[v] = fmaf(b1, x1[r], a0);
-            }
+          for (int v = 0; v < VM; ++v) {
+            float r = fmaf(s0, t0[v], acc[v]);
+            r = fmaf(b0, x0[v], r);
+            r = fmaf(s1, t1[v], r);
+            acc[v] = fmaf(b1, x1[v], r);
           }
         } else {
 #pragma unroll
-          for (int q4 = 0; q4 < VM / 4; ++q4) {
-            const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(h0 + 8 * q4);
-            const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(h1 + 8 * q4);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int v = 4 * q4 + r;
-              const float a0 = fmaf(s0, t0[v], acc[v]);
-              acc[v] = fmaf(b0, x0[r] + x1[r], a0);
-            }
-          }
+          for (int v = 0; v < VM; ++v) acc[v] = fmaf(b0, x0[v], fmaf(s0, t0[v], acc[v]));
         }
       }
     }
   };
 
   for (int base = wave; base < nc; base += 8 * U) {
-    load_batch(base + 4 * U, wb, sb, bbv);
     compute_batch(base, wa, sa, ba);
     load_batch(base + 8 * U, wa, sa, ba);
     compute_batch(base + 4 * U, wb, sb, bbv);
+    load_batch(base + 12 * U, wb, sb, bbv);
   }
 
-  // cross-wave reduction through LDS (aliases the x slab)
-  __syncthreads();
+  // cross-wave reduction through LDS
 #pragma unroll
-  for (int v = 0; v < VM; ++v) red[(wave * VM + v) * 64 + lane] = acc[v];
+  for (int v = 0; v < VM; ++v) red[wave][v][lane] = acc[v];
   __syncthreads();
   for (int e = tid; e < VM * 64; e += 256) {
     const int v = e >> 6, l = e & 63;
-    const float s = red[(0 * VM + v) * 64 + l] + red[(1 * VM + v) * 64 + l] +
-                    red[(2 * VM + v) * 64 + l] + red[(3 * VM + v) * 64 + l];
+    const float s = red[0][v][l] + red[1][v][l] + red[2][v][l] + red[3][v][l];
     const int m = mfma32_row(l, v);
     const int nn = n0 + (l & 31);
     if (m < M && nn < N) {
-      if (part)
-        part[((int64_t)split * M + m) * N + nn] = s;
+      if (a.S == 1)
+        store_out(a.y, (int64_t)m * N + nn, s, a.y_dtype);
       else
-        store_out(y, (int64_t)m * N + nn, s, y_dtype);
+        splitk_store(&a.part[((int64_t)split * M + m) * N + nn], s);
     }
   }
-}
+  if (a.S == 1) return;
 
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(
-    const float* __restrict__ part, void* __restrict__ y, int y_dtype,
-    int64_t MN, int S) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= MN) return;
-  float s = 0.0f;
-  for (int k = 0; k < S; ++k) s += part[(int64_t)k * MN + i];
-  store_out(y, i, s, y_dtype);
+  // split-K: the last workgroup of this tile sums the partials in split order
+  if (!splitk_arrive(&a.counters[blockIdx.x], a.S, &s_last)) return;
+  const int64_t MN = (int64_t)M * N;
+  for (int e = tid; e < M * 32; e += 256) {
+    const int m = e >> 5, nn = n0 + (e & 31);
+    if (nn < N) {
+      const float s = splitk_sum(a.part + (int64_t)m * N + nn, MN, a.S);
+      store_out(a.y, (int64_t)m * N + nn, s, a.y_dtype);
+    }
+  }
+  splitk_reset(&a.counters[blockIdx.x]);
 }
 
 // ---------------------------------------------------------------------------
@@ -474,21 +486,26 @@ __global__ __launch_bounds__(256, 2) void w4_gemm_kernel(
 // host side
 // ---------------------------------------------------------------------------
 struct SkinnyPlan {
-  int MB;     // 8, 16 or 32
-  int S;      // workgroup splits of K
-  int cps;    // 64-k chunks per split
-  size_t lds;
+  int MB;      // row bucket: 1, 8, 16 or 32
+  int S;       // workgroup splits of K
+  int cps;     // 64-k chunks per split
+  size_t lds;  // dynamic LDS: the x slab
+  size_t counter_bytes, part_bytes;
 };
+
+// Workgroups aimed at per launch (about four per CU); SPARKQ_W4_TARGET_WGS
+// overrides it for tuning.
+static int64_t skinny_target_wgs() { return env_int("SPARKQ_W4_TARGET_WGS", 1024); }
 
 static SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K) {
   SkinnyPlan p;
-  p.MB = M <= 8 ? 8 : (M <= 16 ? 16 : 32);
+  p.MB = M == 1 ? 1 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
   const int64_t tiles = cdiv(N, 32);
   const int64_t nchunks = K / 64;
   // x slab in LDS <= 32 KB
   int64_t max_cps = (32768 / (M * 2) - 8) / 64;
   if (max_cps < 1) max_cps = 1;
-  int64_t S = cdiv(1024, tiles);                  // aim at ~1024 workgroups
+  int64_t S = tiles > kMaxCounterTiles ? 1 : cdiv(skinny_target_wgs(), tiles);
   const int64_t s_cap = nchunks / 4 > 0 ? nchunks / 4 : 1;  // >= 4 chunks each
   if (S > s_cap) S = s_cap;
   if (S < 1) S = 1;
@@ -497,54 +514,47 @@ static SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K) {
   S = cdiv(nchunks, cps);
   p.S = (int)S;
   p.cps = (int)cps;
-  const size_t slab = (size_t)M * (size_t)(cps * 64 + 8) * 2;
-  const size_t sums = (size_t)2 * cps * p.MB * 4;
-  const size_t red = (size_t)4 * (p.MB / 2) * 64 * 4;
-  p.lds = slab + sums > red ? slab + sums : red;
+  p.lds = (size_t)M * (size_t)(cps * 64 + 8) * 2;
+  p.counter_bytes = S > 1 ? kCounterBytes : 0;
+  p.part_bytes = S > 1 ? round_up((size_t)S * M * N * 4, 256) : 0;
   return p;
 }
 
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
+  // every workspace of this entry point starts with the counter block, so a
+  // GEMM call never writes over the counters a later split-K call relies on
   if (M <= 32) {
     const SkinnyPlan p = plan_skinny(M, N, K);
-    return p.S > 1 ? round_up((size_t)p.S * M * N * 4, 256) : 0;
+    return p.S > 1 ? kCounterBytes + p.part_bytes : 0;
   }
-  return round_up((size_t)(K / G) * M * 4, 256);
+  return kCounterBytes + round_up((size_t)(K / G) * M * 4, 256);
 }
 
 template <typename T, int G, int MB>
-static void launch_skinny_t(const SkinnyPlan& p, const void* x, const uint32_t* w,
-                            const void* s, const void* b, float* part, void* y,
-                            int ydt, int M, int N, int K, hipStream_t st) {
-  dim3 grid((unsigned)cdiv(N, 32), (unsigned)p.S);
-  hipLaunchKernelGGL((w4_skinny_kernel<T, G, MB>), grid, dim3(256), p.lds, st,
-                     (const uint16_t*)x, w, (const uint16_t*)s, (const uint16_t*)b,
-                     part, y, ydt, M, N, K, p.cps);
+static void launch_skinny_t(const SkinnyPlan& p, const SkinnyArgs& a, hipStream_t st) {
+  dim3 grid((unsigned)cdiv(a.N, 32), (unsigned)p.S);
+  hipLaunchKernelGGL((w4_skinny_kernel<T, G, MB>), grid, dim3(256), p.lds, st, a);
 }
 
 template <typename T, int G>
-static void launch_skinny_g(const SkinnyPlan& p, const void* x, const uint32_t* w,
-                            const void* s, const void* b, float* part, void* y,
-                            int ydt, int M, int N, int K, hipStream_t st) {
-  if (p.MB == 8)
-    launch_skinny_t<T, G, 8>(p, x, w, s, b, part, y, ydt, M, N, K, st);
-  else if (p.MB == 16)
-    launch_skinny_t<T, G, 16>(p, x, w, s, b, part, y, ydt, M, N, K, st);
-  else
-    launch_skinny_t<T, G, 32>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+static void launch_skinny_g(const SkinnyPlan& p, const SkinnyArgs& a, hipStream_t st) {
+  switch (p.MB) {
+    case 1: launch_skinny_t<T, G, 1>(p, a, st); break;
+    case 8: launch_skinny_t<T, G, 8>(p, a, st); break;
+    case 16: launch_skinny_t<T, G, 16>(p, a, st); break;
+    default: launch_skinny_t<T, G, 32>(p, a, st); break;
+  }
 }
 
 template <typename T>
-static void launch_skinny(const SkinnyPlan& p, int G, const void* x, const uint32_t* w,
-                          const void* s, const void* b, float* part, void* y, int ydt,
-                          int M, int N, int K, hipStream_t st) {
+static void launch_skinny(const SkinnyPlan& p, int G, const SkinnyArgs& a, hipStream_t st) {
   if (G == 32)
-    launch_skinny_g<T, 32>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+    launch_skinny_g<T, 32>(p, a, st);
   else if (G == 64)
-    launch_skinny_g<T, 64>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+    launch_skinny_g<T, 64>(p, a, st);
   else
-    launch_skinny_g<T, 128>(p, x, w, s, b, part, y, ydt, M, N, K, st);
+    launch_skinny_g<T, 128>(p, a, st);
 }
 
 template <typename T>
@@ -576,21 +586,34 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
                      "w4a16_linear needs a workspace of %zu bytes (got %zu)", need, wsb);
   if (M <= 32) {
     const SkinnyPlan p = plan_skinny(M, N, K);
-    float* part = p.S > 1 ? reinterpret_cast<float*>(ws) : nullptr;
-    if (xdt == SPARKQ_BF16)
-      launch_skinny<BF16>(p, G, x, w, s, b, part, y, ydt, (int)M, (int)N, (int)K, st);
-    else
-      launch_skinny<F16>(p, G, x, w, s, b, part, y, ydt, (int)M, (int)N, (int)K, st);
-    if (int rc = check_launch("w4_skinny_kernel")) return rc;
+    if (p.S > 1 && cdiv(N, 32) > kMaxCounterTiles)
+      return set_error(SPARKQ_ERR_UNSUPPORTED,
+                       "w4a16_linear: N=%lld with M=%lld and K=%lld needs more split-K tile "
+                       "counters than the workspace holds (N <= %lld)",
+                       (long long)N, (long long)M, (long long)K, (long long)(32 * kMaxCounterTiles));
+    SkinnyArgs a{};
+    a.x = (const uint16_t*)x;
+    a.w = w;
+    a.sc = (const uint16_t*)s;
+    a.bi = (const uint16_t*)b;
+    a.y = y;
+    a.y_dtype = ydt;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.cps = p.cps;
+    a.S = p.S;
     if (p.S > 1) {
-      const int64_t MN = M * N;
-      hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(MN, 256)), dim3(256), 0,
-                         st, part, y, ydt, MN, p.S);
-      if (int rc = check_launch("splitk_reduce_kernel")) return rc;
+      a.counters = reinterpret_cast<unsigned*>(ws);
+      a.part = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
     }
-    return SPARKQ_OK;
+    if (xdt == SPARKQ_BF16)
+      launch_skinny<BF16>(p, G, a, st);
+    else
+      launch_skinny<F16>(p, G, a, st);
+    return check_launch("w4_skinny_kernel");
   }
-  float* xs = reinterpret_cast<float*>(ws);
+  float* xs = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
   if (xdt == SPARKQ_BF16)
     launch_gemm<BF16>(G, x, w, s, b, xs, y, ydt, (int)M, (int)N, (int)K, st);
   else

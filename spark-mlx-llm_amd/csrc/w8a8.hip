@@ -10,11 +10,10 @@
 //                        into v_mfma_i32_32x32x32_i8; the A operand is the
 //                        matching 16 bytes of the int8 activations from LDS;
 //                        m-blocks of 32 rows go to grid.z. Output is either the
-//                        raw int32 sums, int32 split-K partials, or the fused
-//                        epilogue fmaf(float(acc)*sa[m], sw[n], bias[n]).
-//   i8_reduce_raw_kernel / i8_reduce_epilogue_kernel
-//                        fixed-order int32 sum of the split-K partials, then
-//                        the raw store or the epilogue
+//                        raw int32 sums or the fused epilogue
+//                        fmaf(float(acc)*sa[m], sw[n], bias[n]); splits of K
+//                        combine in the same launch (the last workgroup of a
+//                        tile sums the int32 partials).
 #include "common.h"
 
 namespace sparkq {
@@ -47,12 +46,14 @@ __global__ __launch_bounds__(256) void a8_quantize_kernel(
 // ---------------------------------------------------------------------------
 // int8 weight-streaming MFMA kernel
 // ---------------------------------------------------------------------------
-enum I8Out { kOutRaw = 0, kOutPartial = 1, kOutEpilogue = 2 };
+enum I8Out { kOutRaw = 0, kOutEpilogue = 1 };
 
 struct I8Args {
   const int8_t* a;      // [M,K] int8 activations
   const int8_t* b;      // [N,K] int8 weights
-  int32_t* c_raw;       // [M,N] (kOutRaw) or partials [S][M][N] (kOutPartial)
+  int32_t* c_raw;       // [M,N] (kOutRaw)
+  int32_t* part;        // [S][M][N] partials (S > 1)
+  unsigned* counters;   // per (m-block, n-tile), zero on entry and exit (S > 1)
   void* y;              // [M,N] (kOutEpilogue)
   const float* sa;      // [M]
   const float* sw;      // [N]
@@ -61,6 +62,8 @@ struct I8Args {
   int y_dtype;
   int M, N, K;
   int cps;              // 32-k chunks per split
+  int slab;             // 32-k chunks per LDS slab of activations
+  int S;
   int mode;
 };
 
@@ -69,10 +72,22 @@ __device__ __forceinline__ i32x16_t mfma_i8(u32x4_t a, u32x4_t b, i32x16_t c) {
                                                __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ void i8_store(const I8Args& args, int gm, int nn, int32_t s) {
+  if (args.mode == kOutRaw) {
+    args.c_raw[(int64_t)gm * args.N + nn] = s;
+  } else {
+    const float bias = args.bias ? load_in(args.bias, nn, args.bias_dtype) : 0.0f;
+    const float t = (float)s * args.sa[gm];
+    store_out(args.y, (int64_t)gm * args.N + nn, fmaf(t, args.sw[nn], bias), args.y_dtype);
+  }
+}
+
 constexpr int kI8U = 8;
 
 __global__ __launch_bounds__(256, 2) void i8_skinny_kernel(I8Args args) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ int32_t red[4][16][64];
+  __shared__ int s_last;
   constexpr int U = kI8U;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane >> 5;
@@ -85,111 +100,97 @@ __global__ __launch_bounds__(256, 2) void i8_skinny_kernel(I8Args args) {
   const int c_begin = split * args.cps;
   const int nc = min(args.cps, nchunks - c_begin);
 
-  const int pitch = nc * 32 + 16;
+  // the split's x rows live in LDS in slabs of at most args.slab chunks
+  const int pitch = min(nc, args.slab) * 32 + 16;
   int8_t* xs = reinterpret_cast<int8_t*>(smem);
-  int32_t* red = reinterpret_cast<int32_t*>(smem);
 
   const int n = n0 + (lane & 31);
   const int nr = n < N ? n : N - 1;
   const int8_t* brow = args.b + (int64_t)nr * K + (int64_t)c_begin * 32 + 16 * j;
 
   u32x4_t wa[U], wb[U];
+  int lim = 0;  // end (exclusive) of the chunks of the current slab
   auto load_batch = [&](int cl0, u32x4_t* wv) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int cl = cl0 + 4 * u;
-      if (cl < nc) wv[u] = *reinterpret_cast<const u32x4_t*>(brow + (int64_t)cl * 32);
+      if (cl < lim) wv[u] = *reinterpret_cast<const u32x4_t*>(brow + (int64_t)cl * 32);
     }
   };
-  load_batch(wave, wa);
-
-  {
-    const int pieces = nc * 2;  // 16-byte pieces per row
-    for (int p = tid; p < mrows * pieces; p += 256) {
-      const int m = p / pieces, pc = p - m * pieces;
-      *reinterpret_cast<u32x4_t*>(xs + m * pitch + pc * 16) = *reinterpret_cast<const u32x4_t*>(
-          args.a + (int64_t)(m0 + m) * K + (int64_t)c_begin * 32 + pc * 16);
-    }
-  }
-  __syncthreads();
 
   const int am = lane & 31;
   const bool a_ok = am < mrows;
-  const int8_t* arow = xs + (a_ok ? am : 0) * pitch + 16 * j;
   i32x16_t acc = {};
 
-  auto compute_batch = [&](int cl0, const u32x4_t* wv) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int cl = cl0 + 4 * u;
-      if (cl < nc) {
-        u32x4_t a = {0u, 0u, 0u, 0u};
-        if (a_ok) a = *reinterpret_cast<const u32x4_t*>(arow + cl * 32);
-        acc = mfma_i8(a, wv[u], acc);
+  for (int s0 = 0; s0 < nc; s0 += args.slab) {
+    lim = min(nc, s0 + args.slab);
+    load_batch(s0 + wave, wa);
+    load_batch(s0 + wave + 4 * U, wb);
+    {
+      const int pieces = (lim - s0) * 2;  // 16-byte pieces per row
+      for (int p = tid; p < mrows * pieces; p += 256) {
+        const int m = p / pieces, pc = p - m * pieces;
+        *reinterpret_cast<u32x4_t*>(xs + m * pitch + pc * 16) = *reinterpret_cast<const u32x4_t*>(
+            args.a + (int64_t)(m0 + m) * K + (int64_t)(c_begin + s0) * 32 + pc * 16);
       }
     }
-  };
-  for (int base = wave; base < nc; base += 8 * U) {
-    load_batch(base + 4 * U, wb);
-    compute_batch(base, wa);
-    load_batch(base + 8 * U, wa);
-    compute_batch(base + 4 * U, wb);
+    __syncthreads();
+    const int8_t* arow = xs + (a_ok ? am : 0) * pitch + 16 * j - s0 * 32;
+    auto compute_batch = [&](int cl0, const u32x4_t* wv) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int cl = cl0 + 4 * u;
+        if (cl < lim) {
+          u32x4_t av = {0u, 0u, 0u, 0u};
+          if (a_ok) av = *reinterpret_cast<const u32x4_t*>(arow + cl * 32);
+          acc = mfma_i8(av, wv[u], acc);
+        }
+      }
+    };
+    for (int base = s0 + wave; base < lim; base += 8 * U) {
+      compute_batch(base, wa);
+      load_batch(base + 8 * U, wa);
+      compute_batch(base + 4 * U, wb);
+      load_batch(base + 12 * U, wb);
+    }
+    __syncthreads();  // the slab is consumed before the next one is staged
   }
 
-  __syncthreads();
 #pragma unroll
-  for (int v = 0; v < 16; ++v) red[(wave * 16 + v) * 64 + lane] = acc[v];
+  for (int v = 0; v < 16; ++v) red[wave][v][lane] = acc[v];
   __syncthreads();
+  const int64_t MN = (int64_t)M * N;
   for (int e = tid; e < 16 * 64; e += 256) {
     const int v = e >> 6, l = e & 63;
     const int m = mfma32_row(l, v);
     const int nn = n0 + (l & 31);
     if (m < mrows && nn < N) {
-      const int32_t s = red[(0 * 16 + v) * 64 + l] + red[(1 * 16 + v) * 64 + l] +
-                        red[(2 * 16 + v) * 64 + l] + red[(3 * 16 + v) * 64 + l];
-      const int gm = m0 + m;
-      if (args.mode == kOutRaw) {
-        args.c_raw[(int64_t)gm * N + nn] = s;
-      } else if (args.mode == kOutPartial) {
-        args.c_raw[((int64_t)split * M + gm) * N + nn] = s;
-      } else {
-        const float bias = args.bias ? load_in(args.bias, nn, args.bias_dtype) : 0.0f;
-        const float t = (float)s * args.sa[gm];
-        store_out(args.y, (int64_t)gm * N + nn, fmaf(t, args.sw[nn], bias), args.y_dtype);
-      }
+      const int32_t s = red[0][v][l] + red[1][v][l] + red[2][v][l] + red[3][v][l];
+      if (args.S == 1)
+        i8_store(args, m0 + m, nn, s);
+      else
+        splitk_store(&args.part[split * MN + (int64_t)(m0 + m) * N + nn], s);
     }
   }
-}
+  if (args.S == 1) return;
 
-// fixed-order int32 sums of S partials [S][M][N]: raw store, or the epilogue
-__global__ __launch_bounds__(256) void i8_reduce_raw_kernel(const int32_t* __restrict__ part,
-                                                            int32_t* __restrict__ c,
-                                                            int64_t MN, int S) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= MN) return;
-  int32_t s = 0;
-  for (int k = 0; k < S; ++k) s += part[(int64_t)k * MN + i];
-  c[i] = s;
-}
-
-__global__ __launch_bounds__(256) void i8_reduce_epilogue_kernel(I8Args args, int S) {
-  const int64_t MN = (int64_t)args.M * args.N;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= MN) return;
-  int32_t s = 0;
-  for (int k = 0; k < S; ++k) s += args.c_raw[(int64_t)k * MN + i];
-  const int m = (int)(i / args.N), nn = (int)(i - (int64_t)m * args.N);
-  const float bias = args.bias ? load_in(args.bias, nn, args.bias_dtype) : 0.0f;
-  const float t = (float)s * args.sa[m];
-  store_out(args.y, i, fmaf(t, args.sw[nn], bias), args.y_dtype);
+  // split-K: the last workgroup of this (m-block, n-tile) sums the partials
+  const int tile = blockIdx.z * gridDim.x + blockIdx.x;
+  if (!splitk_arrive(&args.counters[tile], args.S, &s_last)) return;
+  for (int e = tid; e < mrows * 32; e += 256) {
+    const int gm = m0 + (e >> 5), nn = n0 + (e & 31);
+    if (nn < N) i8_store(args, gm, nn, splitk_sum(args.part + (int64_t)gm * N + nn, MN, args.S));
+  }
+  splitk_reset(&args.counters[tile]);
 }
 
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 struct I8Plan {
-  int S, cps;
+  int S, cps, slab;
   size_t lds;
+  size_t counter_bytes, part_bytes;
 };
 
 static I8Plan plan_i8(int64_t M, int64_t N, int64_t K) {
@@ -197,38 +198,36 @@ static I8Plan plan_i8(int64_t M, int64_t N, int64_t K) {
   const int64_t mrows = M < 32 ? M : 32;
   const int64_t tiles = cdiv(N, 32) * cdiv(M, 32);
   const int64_t nchunks = K / 32;
-  int64_t max_cps = (32768 / mrows - 16) / 32;
-  if (max_cps < 1) max_cps = 1;
-  int64_t S = cdiv(1024, tiles);
+  // activation slab in LDS <= 32 KB
+  int64_t slab = (32768 / mrows - 16) / 32;
+  if (slab < 1) slab = 1;
+  // about four workgroups per CU; SPARKQ_I8_TARGET_WGS overrides it for tuning
+  int64_t S = tiles > kMaxCounterTiles ? 1 : cdiv(env_int("SPARKQ_I8_TARGET_WGS", 1024), tiles);
   const int64_t s_cap = nchunks / 8 > 0 ? nchunks / 8 : 1;
   if (S > s_cap) S = s_cap;
   if (S < 1) S = 1;
-  int64_t cps = cdiv(nchunks, S);
-  if (cps > max_cps) cps = max_cps;
+  const int64_t cps = cdiv(nchunks, S);
   S = cdiv(nchunks, cps);
   p.S = (int)S;
   p.cps = (int)cps;
-  const size_t slab = (size_t)mrows * (size_t)(cps * 32 + 16);
-  const size_t red = (size_t)4 * 16 * 64 * 4;
-  p.lds = slab > red ? slab : red;
+  p.slab = (int)(slab < cps ? slab : cps);
+  p.lds = (size_t)mrows * (size_t)(p.slab * 32 + 16);
+  p.counter_bytes = S > 1 ? kCounterBytes : 0;
+  p.part_bytes = S > 1 ? round_up((size_t)S * M * N * 4, 256) : 0;
   return p;
-}
-
-static size_t i8_partial_bytes(int64_t M, int64_t N, int64_t K) {
-  const I8Plan p = plan_i8(M, N, K);
-  return p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
 }
 
 size_t w8a8_workspace(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  // int8 activations, fp32 scales, int32 partials (each 256-byte aligned)
-  return round_up((size_t)M * K, 256) + round_up((size_t)M * 4, 256) +
-         round_up(i8_partial_bytes(M, N, K), 256);
+  const I8Plan p = plan_i8(M, N, K);
+  // counters, int8 activations, fp32 scales, int32 partials
+  return kCounterBytes + round_up((size_t)M * K, 256) + round_up((size_t)M * 4, 256) +
+         p.part_bytes;
 }
 
 size_t i8_matmul_workspace(int64_t M, int64_t N, int64_t K) {
-  const size_t part = i8_partial_bytes(M, N, K);
-  return part ? round_up(part, 256) : 0;
+  const I8Plan p = plan_i8(M, N, K);
+  return p.counter_bytes + p.part_bytes;
 }
 
 static int launch_i8(const I8Args& args, const I8Plan& p, hipStream_t st) {
@@ -247,29 +246,26 @@ int a8_quantize(const void* x, int8_t* q, float* scales, int64_t M, int64_t K, i
 int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N,
                     int64_t K, void* ws, size_t wsb, hipStream_t st) {
   const I8Plan p = plan_i8(M, N, K);
+  const size_t need = p.counter_bytes + p.part_bytes;
+  if (need > 0 && (ws == nullptr || wsb < need))
+    return set_error(SPARKQ_ERR_WORKSPACE,
+                     "int8_matmul_i32 needs a workspace of %zu bytes (got %zu)", need, wsb);
   I8Args args{};
   args.a = a;
   args.b = b;
+  args.c_raw = c;
   args.M = (int)M;
   args.N = (int)N;
   args.K = (int)K;
   args.cps = p.cps;
-  if (p.S == 1) {
-    args.mode = kOutRaw;
-    args.c_raw = c;
-    return launch_i8(args, p, st);
+  args.slab = p.slab;
+  args.S = p.S;
+  args.mode = kOutRaw;
+  if (p.S > 1) {
+    args.counters = reinterpret_cast<unsigned*>(ws);
+    args.part = reinterpret_cast<int32_t*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
   }
-  const size_t need = i8_matmul_workspace(M, N, K);
-  if (ws == nullptr || wsb < need)
-    return set_error(SPARKQ_ERR_WORKSPACE,
-                     "int8_matmul_i32 needs a workspace of %zu bytes (got %zu)", need, wsb);
-  args.mode = kOutPartial;
-  args.c_raw = reinterpret_cast<int32_t*>(ws);
-  if (int rc = launch_i8(args, p, st)) return rc;
-  const int64_t MN = M * N;
-  hipLaunchKernelGGL(i8_reduce_raw_kernel, dim3((unsigned)cdiv(MN, 256)), dim3(256), 0, st,
-                     args.c_raw, c, MN, p.S);
-  return check_launch("i8_reduce_raw_kernel");
+  return launch_i8(args, p, st);
 }
 
 int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bias,
@@ -280,9 +276,9 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
     return set_error(SPARKQ_ERR_WORKSPACE,
                      "w8a8_linear needs a workspace of %zu bytes (got %zu)", need, wsb);
   unsigned char* base = reinterpret_cast<unsigned char*>(ws);
-  int8_t* q = reinterpret_cast<int8_t*>(base);
-  float* sa = reinterpret_cast<float*>(base + round_up((size_t)M * K, 256));
-  int32_t* part = reinterpret_cast<int32_t*>(base + round_up((size_t)M * K, 256) +
+  int8_t* q = reinterpret_cast<int8_t*>(base + kCounterBytes);
+  float* sa = reinterpret_cast<float*>(base + kCounterBytes + round_up((size_t)M * K, 256));
+  int32_t* part = reinterpret_cast<int32_t*>(base + kCounterBytes + round_up((size_t)M * K, 256) +
                                              round_up((size_t)M * 4, 256));
   if (int rc = a8_quantize(x, q, sa, M, K, xdt, st)) return rc;
   const I8Plan p = plan_i8(M, N, K);
@@ -299,17 +295,14 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
   args.N = (int)N;
   args.K = (int)K;
   args.cps = p.cps;
-  if (p.S == 1) {
-    args.mode = kOutEpilogue;
-    return launch_i8(args, p, st);
+  args.slab = p.slab;
+  args.S = p.S;
+  args.mode = kOutEpilogue;
+  if (p.S > 1) {
+    args.counters = reinterpret_cast<unsigned*>(base);
+    args.part = part;
   }
-  args.mode = kOutPartial;
-  args.c_raw = part;
-  if (int rc = launch_i8(args, p, st)) return rc;
-  const int64_t MN = M * N;
-  hipLaunchKernelGGL(i8_reduce_epilogue_kernel, dim3((unsigned)cdiv(MN, 256)), dim3(256), 0,
-                     st, args, p.S);
-  return check_launch("i8_reduce_epilogue_kernel");
+  return launch_i8(args, p, st);
 }
 
 }  // namespace sparkq

@@ -104,15 +104,17 @@ def call(name: str, *args) -> None:
 _WS: dict = {}
 
 
-def workspace(device: torch.device, nbytes: int):
-    """Per (device, stream) scratch buffer; reuse is safe because every user
-    enqueues on that same stream."""
+def workspace(device: torch.device, nbytes: int, kind: str):
+    """Scratch buffer per (device, stream, entry-point kind). Reuse is safe
+    because every user enqueues on that same stream. Buffers start zeroed:
+    split-K entry points keep tile counters at the front of their workspace,
+    which must be zero before the first call (every call leaves them zero)."""
     if nbytes <= 0:
         return None, 0
     stream = torch.cuda.current_stream(device).cuda_stream
-    key = (device.index, stream)
+    key = (device.index, stream, kind)
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WS[key] = buf
     return ctypes.c_void_p(buf.data_ptr()), buf.numel()

@@ -128,7 +128,8 @@ def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
         return y.reshape(*lead, n)
     x2 = x.reshape(m, k).contiguous()
     weight, scales, biases = weight.contiguous(), scales.contiguous(), biases.contiguous()
-    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_w4a16_workspace_bytes(m, n, k, group_size))
+    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_w4a16_workspace_bytes(m, n, k, group_size),
+                             "w4a16")
     _lib.call("sparkq_w4a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
               _ptr(y), m, n, k, group_size, bits, _lib.dtype_code(x.dtype),
               _lib.dtype_code(out_dtype), ws, wsb, _lib.stream_handle(x.device))
@@ -259,7 +260,8 @@ def int8_matmul_int32(x, weight, *, stream=None):
     m, k = x.shape
     n = weight.shape[0]
     c = torch.empty((m, n), dtype=torch.int32, device=x.device)
-    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_int8_matmul_workspace_bytes(m, n, k))
+    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_int8_matmul_workspace_bytes(m, n, k),
+                             "i8mm")
     x, weight = x.contiguous(), weight.contiguous()
     _lib.call("sparkq_int8_matmul_i32", _ptr(x), _ptr(weight),
               _ptr(c), m, n, k, ws, wsb, _lib.stream_handle(x.device))
@@ -283,7 +285,7 @@ def w8a8_linear(x, weight, scales, bias=None, *, stream=None, out_dtype=None, ou
     m = prod(lead)
     x2 = x.reshape(m, k).contiguous()
     y = _out_buffer(out, (m, n), out_dtype, x.device)
-    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_w8a8_workspace_bytes(m, n, k))
+    ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_w8a8_workspace_bytes(m, n, k), "w8a8")
     bias_c = bias.contiguous() if bias is not None else None
     weight, scales = weight.contiguous(), scales.reshape(n).contiguous()
     _lib.call("sparkq_w8a8_linear", _ptr(x2), _ptr(weight),
@@ -423,7 +425,8 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
     out = _out_buffer(out, (batch, heads, 1, dim), out_dtype, queries.device)
     st = (ctypes.c_int64 * 12)(*strides)
     ws, wsb = _lib.workspace(queries.device,
-                             _lib.lib().sparkq_int8kv_sdpa_workspace_bytes(batch, heads, n, dim))
+                             _lib.lib().sparkq_int8kv_sdpa_workspace_bytes(batch, heads, n, dim),
+                             "sdpa")
     _lib.call("sparkq_int8kv_sdpa_decode", _ptr(q), _ptr(kc), _ptr(ks), _ptr(kb), _ptr(vc),
               _ptr(vs), _ptr(vb), _ptr(out), batch, heads, kv_heads, n, dim, group_size, fmt,
               _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), float(scale), st,

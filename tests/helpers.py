@@ -52,18 +52,32 @@ def ulp_distance16(a_bits, b_bits, dtype):
 
 
 def check_fp32(out, ref, atol=2e-2, rtol_l2=1e-3):
-    """The north-star tolerance applied to an unrounded fp32 epilogue."""
+    """The north-star tolerance (max-abs 2e-2, relative L2 1e-3 against the
+    fp64 dequantize-then-matmul) applied to the unrounded fp32 epilogue."""
     ma, rl = max_abs(out, ref), rel_l2(out, ref)
+    print(f"[fp32] max_abs={ma:.3e} rel_l2={rl:.3e}")
     assert ma <= atol and rl <= rtol_l2, f"max_abs={ma:.3e} rel_l2={rl:.3e}"
     return ma, rl
 
 
-def check_rounded16(out_bits, ref64, dtype, atol=2e-2, max_flip_frac=0.02):
-    """A 16-bit output against the correctly rounded oracle: every element
-    within one unit of the format, and few 1-unit boundary flips."""
-    ref_bits = o.round16(np.asarray(ref64, np.float32), dtype)
+def check_rounded16(out_bits, ref64, dtype, atol=2e-2, near_zero=2.0 ** -7,
+                    max_flip_frac=0.05):
+    """A 16-bit output against the correctly rounded oracle: max-abs within
+    atol; every element whose magnitude is at least near_zero * rms(ref)
+    within one unit of the format (an fp32 accumulation error of ~1e-6*rms is
+    many units of a near-zero result, so those are held to atol only); and
+    the fraction of 1-unit boundary flips bounded and reported."""
+    ref = np.asarray(ref64, np.float64)
+    ref_bits = o.round16(ref.astype(np.float32), dtype)
+    ma = max_abs(o.bits_to_f32(out_bits, dtype), o.bits_to_f32(ref_bits, dtype))
     d = ulp_distance16(out_bits, ref_bits, dtype)
-    assert d.max() <= 1, f"max ulp distance {d.max()}"
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    big = np.abs(ref) >= near_zero * rms
     frac = float((d > 0).mean())
+    print(f"[16-bit] max_abs_vs_rounded={ma:.3e} max_ulp(|y|>={near_zero:g}rms)="
+          f"{int(d[big].max()) if big.any() else 0} flips={frac:.4f} "
+          f"max_ulp_all={int(d.max())}")
+    assert ma <= atol, f"max_abs vs rounded oracle {ma:.3e}"
+    assert not big.any() or d[big].max() <= 1, f"max ulp distance {d[big].max()}"
     assert frac <= max_flip_frac, f"1-ulp flips {frac:.4f}"
     return frac

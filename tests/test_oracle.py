@@ -146,11 +146,19 @@ def test_w4_dequantize_is_single_rounding(dt):
     s16, b16 = o.round16(sv, dt), o.round16(bv, dt)
     if dt == o.BF16:
         s16[2, 0], b16[2, 0] = 0x0001, 0x8001  # subnormal bf16
+        # 2*2^127 overflows as a product, but 2^128 - 2^125 is finite: the
+        # dequantization rounds the exact q*s+b once
+        s16[3, 0], b16[3, 0] = 0x7F00, 0xFE00
+        codes[3, :8] = 2
+        wq = o.pack4(codes)
     out = o.w4_dequantize(wq, s16, b16, g, dt)
     s = np.repeat(o.bits_to_f32(s16, dt).astype(np.float64), g, axis=1)
     b = np.repeat(o.bits_to_f32(b16, dt).astype(np.float64), g, axis=1)
     exact = codes.astype(np.float64) * s + b  # exact product, one rounding below
-    assert np.array_equal(out, exact.astype(np.float32))
+    with np.errstate(over="ignore"):
+        assert np.array_equal(out, exact.astype(np.float32))
+    if dt == o.BF16:
+        assert np.isfinite(out[3, :8]).all() and out[3, 0] == np.float32(2.0 ** 128 - 2.0 ** 125)
 
 
 def test_w4a16_matmul_against_numpy_and_special_cases():
