@@ -86,14 +86,32 @@ __device__ __forceinline__ uint32_t exact_f16_pair(uint32_t r) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// A 32-bit constant held in a VGPR. gfx9 VALU instructions read at most one
+// SGPR or literal, so (x & mask) | magic with both constants as literals
+// splits into two instructions; with them in VGPRs it is one v_bitop3.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
+}
+
+// The two decode constants, materialised once per kernel.
+struct DecodeConsts {
+  uint32_t mask, magic;
+};
 template <typename T>
-__device__ __forceinline__ u32x4_t decode_w4(uint32_t w) {
+__device__ __forceinline__ DecodeConsts decode_consts() {
+  return DecodeConsts{vgpr_const(0x000F000Fu), vgpr_const(T::MAGIC)};
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4_t decode_w4(uint32_t w, DecodeConsts c) {
   const uint32_t ws = w >> 4;
   u32x4_t r;
-  r.x = (__builtin_amdgcn_perm(ws, w, 0x0C040C00u) & 0x000F000Fu) | T::MAGIC;
-  r.y = (__builtin_amdgcn_perm(ws, w, 0x0C050C01u) & 0x000F000Fu) | T::MAGIC;
-  r.z = (__builtin_amdgcn_perm(ws, w, 0x0C060C02u) & 0x000F000Fu) | T::MAGIC;
-  r.w = (__builtin_amdgcn_perm(ws, w, 0x0C070C03u) & 0x000F000Fu) | T::MAGIC;
+  r.x = (__builtin_amdgcn_perm(ws, w, 0x0C040C00u) & c.mask) | c.magic;
+  r.y = (__builtin_amdgcn_perm(ws, w, 0x0C050C01u) & c.mask) | c.magic;
+  r.z = (__builtin_amdgcn_perm(ws, w, 0x0C060C02u) & c.mask) | c.magic;
+  r.w = (__builtin_amdgcn_perm(ws, w, 0x0C070C03u) & c.mask) | c.magic;
   if constexpr (T::kExactDecode) {
     r.x = exact_f16_pair(r.x);
     r.y = exact_f16_pair(r.y);

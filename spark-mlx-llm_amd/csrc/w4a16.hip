@@ -16,6 +16,7 @@
 //   xsum_kernel         group sums X_g[m] for the GEMM, layout [K/G][M]
 //   w4_gemm_kernel      M > 32: 128x128x64 LDS tiles (A bf16/f16, B decoded
 //                       to OFFSET+q), double-buffered, MFMA 32x32x16
+#include <cmath>
 #include <cstdlib>
 
 #include "common.h"
@@ -91,19 +92,19 @@ __global__ __launch_bounds__(256) void w4_quantize_kernel(
 // skinny kernel (M <= MB <= 32)
 // ---------------------------------------------------------------------------
 // Workgroup = 4 waves; tile = 32 weight rows; the workgroup's K range (a
-// split of cps 64-k chunks) is shared round-robin by its waves, each keeping
-// two batches of kSkinnyU chunk loads in flight.
+// split of 4*CPW 64-k chunks) is dealt to the waves round-robin, CPW chunks
+// each. The code is straight-line: every wave issues all of its weight and
+// scale loads first (unconditionally, so the compiler waits for exactly the
+// load each chunk needs), then stages x and the group sums of x into LDS
+// behind one barrier, then computes its chunks in order.
 // Chunk step: lane (n = l%32, j = l/32) holds 16 bytes = 32 codes of row n at
 // k = 64c + 32j, i.e. four MFMA k-slots of 8; the A operand is the matching
-// 16 bytes of x row m = l%32 from an LDS copy of the split's x slab. Per
-// chunk, four MFMAs accumulate x.(OFFSET+q) and four more accumulate x.1 (a
-// constant all-ones B operand), which lands the group sums X_g[m] directly in
-// the output lane layout; the chunk then ends with the fp32 epilogue
-// acc += s*T + (b - OFFSET*s)*X. Splits of K combine in the same launch:
-// every workgroup writes its fp32 partial, and the last one to arrive at the
-// tile's counter sums the partials in split order (deterministic) and resets
-// the counter to zero.
-constexpr int kSkinnyU = 4;  // chunks per batch; two batches in flight
+// 16 bytes of x row m = l%32 from the LDS slab (rows past M read a zero row).
+// Four MFMAs accumulate x.(OFFSET+q); the chunk ends with the fp32 epilogue
+// acc += s*T + (b - OFFSET*s)*X over its group(s), X being the group sums.
+// Splits of K combine in the same launch: every workgroup writes its fp32
+// partial, and the last one to arrive at the tile's counter sums the partials
+// in split order (deterministic) and resets the counter to zero.
 
 struct SkinnyArgs {
   const uint16_t* x;
@@ -115,7 +116,7 @@ struct SkinnyArgs {
   void* y;
   int y_dtype;
   int M, N, K;
-  int cps;              // 64-k chunks per split
+  int cps;              // 64-k chunks per split (4 * CPW)
   int S;
 };
 
@@ -139,33 +140,24 @@ struct ChunkMeta {
   }
 };
 
-template <typename T>
-struct Ones;
-template <>
-struct Ones<BF16> {
-  static constexpr uint32_t pair = 0x3F803F80u;  // bf16 1.0, 1.0
-};
-template <>
-struct Ones<F16> {
-  static constexpr uint32_t pair = 0x3C003C00u;  // fp16 1.0, 1.0
-};
-
 // Rows of the 32x32 output a lane holds for row-bucket MB: accumulators v <
 // VM cover rows 8*(v/4) + 4*(l/32) + v%4 < MB (MB = 1 keeps v = 0 only).
 template <int MB>
 struct RowBucket {
   static constexpr int VM = MB >= 8 ? MB / 2 : 1;
+  static constexpr int ROWS = MB >= 8 ? MB : 8;  // group-sum rows kept in LDS
 };
 
-template <typename T, int G, int MB>
+template <typename T, int G, int MB, int CPW>
 __global__ __launch_bounds__(256, 2) void w4_skinny_kernel(SkinnyArgs a) {
   constexpr int VM = RowBucket<MB>::VM;
-  constexpr int U = kSkinnyU;
+  constexpr int XR = RowBucket<MB>::ROWS;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ float red[4][VM][64];
   __shared__ int s_last;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane >> 5;
   const int M = a.M, N = a.N, K = a.K;
   const int n0 = blockIdx.x * 32;
@@ -174,10 +166,15 @@ __global__ __launch_bounds__(256, 2) void w4_skinny_kernel(SkinnyArgs a) {
   const int c_begin = split * a.cps;
   const int nc = min(a.cps, nchunks - c_begin);
   const int ngroups = K / G;
+  // this wave's chunks are wave, wave+4, ...: my_n <= CPW of them (fewer
+  // only in a tail split)
+  const int my_n = nc > wave ? min(CPW, (nc - wave + 3) >> 2) : 0;
 
-  // LDS x slab [M][nc*64 + 8] (16-bit)
+  // LDS: x slab [M+1][nc*64 + 8] (16-bit, row M zero), then the half-chunk
+  // (32-k) sums of x [2*nc][XR] fp32 (rows past M zero)
   const int xpitch = nc * 64 + 8;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  float* xh = reinterpret_cast<float*>(smem + (size_t)(M + 1) * xpitch * 2);
 
   const int n = n0 + (lane & 31);
   const int nr = n < N ? n : N - 1;
@@ -185,30 +182,43 @@ __global__ __launch_bounds__(256, 2) void w4_skinny_kernel(SkinnyArgs a) {
   const uint16_t* srow = a.sc + (int64_t)nr * ngroups;
   const uint16_t* brow = a.bi + (int64_t)nr * ngroups;
 
-  u32x4_t wa[U], wb[U];
-  uint32_t sa[U], ba[U], sb[U], bbv[U];
-
-  auto load_batch = [&](int cl0, u32x4_t* wv, uint32_t* sv, uint32_t* bv) {
+  u32x4_t wv[CPW];
+  uint32_t sv[CPW], bv[CPW];
+  if (my_n > 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int cl = cl0 + 4 * u;
-      if (cl < nc) {
-        wv[u] = *reinterpret_cast<const u32x4_t*>(wrow + (int64_t)cl * 8);
-        ChunkMeta<T, G>::load(srow, brow, c_begin + cl, sv[u], bv[u]);
-      }
+    for (int i = 0; i < CPW; ++i) {
+      // past the wave's last chunk (tail split only) re-read that chunk
+      const int cl = wave + 4 * min(i, my_n - 1);
+      wv[i] = *reinterpret_cast<const u32x4_t*>(wrow + (int64_t)cl * 8);
+      ChunkMeta<T, G>::load(srow, brow, c_begin + cl, sv[i], bv[i]);
     }
-  };
+  }
 
-  // both weight batches go out before the x slab is staged
-  load_batch(wave, wa, sa, ba);
-  load_batch(wave + 4 * U, wb, sb, bbv);
+  // stage x (plus the zero row) and the half-chunk sums, behind one barrier
   {
-    const int pieces_per_row = nc * 8;
-    const int total = M * pieces_per_row;
-    for (int p = tid; p < total; p += 256) {
-      const int m = p / pieces_per_row, pc = p - m * pieces_per_row;
-      *reinterpret_cast<u32x4_t*>(xs + m * xpitch + pc * 8) = *reinterpret_cast<const u32x4_t*>(
-          a.x + (int64_t)m * K + (int64_t)c_begin * 64 + pc * 8);
+    const int ppr = nc * 8;
+    for (int p = tid; p < (M + 1) * ppr; p += 256) {
+      const int m = p / ppr, pc = p - m * ppr;
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (m < M)
+        v = *reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * K + (int64_t)c_begin * 64 + pc * 8);
+      *reinterpret_cast<u32x4_t*>(xs + m * xpitch + pc * 8) = v;
+    }
+    for (int p = tid; p < 2 * nc * XR; p += 256) {
+      const int h = p / XR, m = p - h * XR;
+      float sum = 0.0f;
+      if (m < M) {
+        const u32x4_t* src = reinterpret_cast<const u32x4_t*>(
+            a.x + (int64_t)m * K + (int64_t)c_begin * 64 + h * 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4_t v = src[q];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            sum += T::to_f32((uint16_t)(v[e] & 0xFFFFu)) + T::to_f32((uint16_t)(v[e] >> 16));
+        }
+      }
+      xh[h * XR + m] = sum;
     }
   }
   __syncthreads();
@@ -218,58 +228,50 @@ __global__ __launch_bounds__(256, 2) void w4_skinny_kernel(SkinnyArgs a) {
   for (int v = 0; v < VM; ++v) acc[v] = 0.0f;
 
   const int am = lane & 31;
-  const bool a_ok = am < M;
-  const uint16_t* arow = xs + (a_ok ? am : 0) * xpitch + 32 * j;
-  const u32x4_t ones = {Ones<T>::pair, Ones<T>::pair, Ones<T>::pair, Ones<T>::pair};
+  const uint16_t* arow = xs + (am < M ? am : M) * xpitch + 32 * j;
+  const DecodeConsts dc = decode_consts<T>();
   const u32x4_t zero = {0u, 0u, 0u, 0u};
 
-  auto compute_batch = [&](int cl0, const u32x4_t* wv, const uint32_t* sv, const uint32_t* bv) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int cl = cl0 + 4 * u;
-      if (cl < nc) {
-        f32x16_t t0 = {}, t1 = {}, x0 = {}, x1 = {};
+  for (int i = 0; i < CPW; ++i) {
+    if (i < my_n) {
+      const int cl = wave + 4 * i;
+      f32x16_t t0 = {}, t1 = {};
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const u32x4_t bq = decode_w4<T>(wv[u][t]);
-          u32x4_t av = zero;
-          if (a_ok) av = *reinterpret_cast<const u32x4_t*>(arow + cl * 64 + 8 * t);
-          if constexpr (G == 32) {
-            const u32x4_t a0 = j == 0 ? av : zero, a1 = j == 1 ? av : zero;
-            t0 = mfma32x32x16<T>(a0, bq, t0);
-            t1 = mfma32x32x16<T>(a1, bq, t1);
-            x0 = mfma32x32x16<T>(a0, ones, x0);
-            x1 = mfma32x32x16<T>(a1, ones, x1);
-          } else {
-            t0 = mfma32x32x16<T>(av, bq, t0);
-            x0 = mfma32x32x16<T>(av, ones, x0);
-          }
-        }
-        const float s0 = T::to_f32((uint16_t)(sv[u] & 0xFFFFu));
-        const float b0 = fmaf(-T::OFFSET, s0, T::to_f32((uint16_t)(bv[u] & 0xFFFFu)));
+      for (int t = 0; t < 4; ++t) {
+        const u32x4_t bq = decode_w4<T>(wv[i][t], dc);
+        const u32x4_t av = *reinterpret_cast<const u32x4_t*>(arow + cl * 64 + 8 * t);
         if constexpr (G == 32) {
-          const float s1 = T::to_f32((uint16_t)(sv[u] >> 16));
-          const float b1 = fmaf(-T::OFFSET, s1, T::to_f32((uint16_t)(bv[u] >> 16)));
-#pragma unroll
-          for (int v = 0; v < VM; ++v) {
-            float r = fmaf(s0, t0[v], acc[v]);
-            r = fmaf(b0, x0[v], r);
-            r = fmaf(s1, t1[v], r);
-            acc[v] = fmaf(b1, x1[v], r);
-          }
+          t0 = mfma32x32x16<T>(j == 0 ? av : zero, bq, t0);
+          t1 = mfma32x32x16<T>(j == 1 ? av : zero, bq, t1);
         } else {
+          t0 = mfma32x32x16<T>(av, bq, t0);
+        }
+      }
+      const float s0 = T::to_f32((uint16_t)(sv[i] & 0xFFFFu));
+      const float b0 = fmaf(-T::OFFSET, s0, T::to_f32((uint16_t)(bv[i] & 0xFFFFu)));
+      // group sums of the rows this lane holds: rows 8*(v/4) + 4*j + v%4
+      const float* h0 = xh + (2 * cl) * XR + 4 * j;
+      const float* h1 = h0 + XR;
+      if constexpr (G == 32) {
+        const float s1 = T::to_f32((uint16_t)(sv[i] >> 16));
+        const float b1 = fmaf(-T::OFFSET, s1, T::to_f32((uint16_t)(bv[i] >> 16)));
 #pragma unroll
-          for (int v = 0; v < VM; ++v) acc[v] = fmaf(b0, x0[v], fmaf(s0, t0[v], acc[v]));
+        for (int v = 0; v < VM; ++v) {
+          const int off = 8 * (v >> 2) + (v & 3);
+          float r = fmaf(s0, t0[v], acc[v]);
+          r = fmaf(b0, h0[off], r);
+          r = fmaf(s1, t1[v], r);
+          acc[v] = fmaf(b1, h1[off], r);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < VM; ++v) {
+          const int off = 8 * (v >> 2) + (v & 3);
+          acc[v] = fmaf(b0, h0[off] + h1[off], fmaf(s0, t0[v], acc[v]));
         }
       }
     }
-  };
-
-  for (int base = wave; base < nc; base += 8 * U) {
-    compute_batch(base, wa, sa, ba);
-    load_batch(base + 8 * U, wa, sa, ba);
-    compute_batch(base + 4 * U, wb, sb, bbv);
-    load_batch(base + 12 * U, wb, sb, bbv);
   }
 
   // cross-wave reduction through LDS
@@ -354,6 +356,7 @@ __global__ __launch_bounds__(256, 2) void w4_gemm_kernel(
   const int ngroups = K / G;
   const int nsteps = K / kBK;
 
+  const DecodeConsts dc = decode_consts<T>();
   // global -> register staging
   u32x4_t ra[4], rb;
   float rs = 0.0f, rbias = 0.0f, rx = 0.0f;
@@ -396,7 +399,7 @@ __global__ __launch_bounds__(256, 2) void w4_gemm_kernel(
       const int row = tid >> 1, half = tid & 1;
 #pragma unroll
       for (int wi = 0; wi < 4; ++wi)
-        *reinterpret_cast<u32x4_t*>(&Bs[st][tile_off(row, 4 * half + wi)]) = decode_w4<T>(rb[wi]);
+        *reinterpret_cast<u32x4_t*>(&Bs[st][tile_off(row, 4 * half + wi)]) = decode_w4<T>(rb[wi], dc);
     }
     if (tid < 128 * GPS) {
       const int gi = tid >> 7, row = tid & 127;
@@ -487,36 +490,48 @@ __global__ __launch_bounds__(256, 2) void w4_gemm_kernel(
 // ---------------------------------------------------------------------------
 struct SkinnyPlan {
   int MB;      // row bucket: 1, 8, 16 or 32
+  int CPW;     // chunks per wave: 1, 2, 4, 5 or 8
   int S;       // workgroup splits of K
-  int cps;     // 64-k chunks per split
-  size_t lds;  // dynamic LDS: the x slab
-  size_t counter_bytes, part_bytes;
+  int cps;     // 64-k chunks per split (4 * CPW)
+  size_t lds;  // dynamic LDS: the x slab and its group sums
+  size_t part_bytes;
 };
 
-// Workgroups aimed at per launch (about four per CU); SPARKQ_W4_TARGET_WGS
-// overrides it for tuning.
-static int64_t skinny_target_wgs() { return env_int("SPARKQ_W4_TARGET_WGS", 1024); }
-
+// Workgroups aimed at per launch; SPARKQ_W4_TARGET_WGS overrides it and
+// SPARKQ_W4_CPW forces the chunks per wave, both for tuning.
 static SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K) {
+  static const int kCpw[] = {1, 2, 4, 5, 8};
   SkinnyPlan p;
   p.MB = M == 1 ? 1 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32));
   const int64_t tiles = cdiv(N, 32);
   const int64_t nchunks = K / 64;
-  // x slab in LDS <= 32 KB
-  int64_t max_cps = (32768 / (M * 2) - 8) / 64;
-  if (max_cps < 1) max_cps = 1;
-  int64_t S = tiles > kMaxCounterTiles ? 1 : cdiv(skinny_target_wgs(), tiles);
-  const int64_t s_cap = nchunks / 4 > 0 ? nchunks / 4 : 1;  // >= 4 chunks each
-  if (S > s_cap) S = s_cap;
-  if (S < 1) S = 1;
-  int64_t cps = cdiv(nchunks, S);
-  if (cps > max_cps) cps = max_cps;
-  S = cdiv(nchunks, cps);
-  p.S = (int)S;
-  p.cps = (int)cps;
-  p.lds = (size_t)M * (size_t)(cps * 64 + 8) * 2;
-  p.counter_bytes = S > 1 ? kCounterBytes : 0;
-  p.part_bytes = S > 1 ? round_up((size_t)S * M * N * 4, 256) : 0;
+  const int64_t target = env_int("SPARKQ_W4_TARGET_WGS", 1024);
+  const int64_t forced = env_int("SPARKQ_W4_CPW", 0);
+  const int64_t xr = M >= 8 ? (M <= 16 ? 16 : 32) : 8;
+  double best = 1e30;
+  p.CPW = 1;
+  for (int cpw : kCpw) {
+    if (forced && cpw != forced) continue;
+    const int64_t cps = 4 * (int64_t)cpw;
+    // x slab (M rows + a zero row) and the sums in LDS <= 40 KB
+    const size_t lds = (size_t)(M + 1) * (cps * 64 + 8) * 2 + (size_t)2 * cps * xr * 4;
+    if (lds > 40960 && !forced) continue;
+    const int64_t S = cdiv(nchunks, cps);
+    if (S > 1 && tiles > kMaxCounterTiles) continue;
+    const int64_t wgs = tiles * S;
+    // distance from the target workgroup count, plus idle slots of a tail
+    const int64_t tail = S * cps - nchunks;
+    const double cost = std::fabs(std::log((double)wgs / (double)target)) +
+                        (double)tail / (double)(S * cps);
+    if (cost < best) {
+      best = cost;
+      p.CPW = cpw;
+    }
+  }
+  p.cps = 4 * p.CPW;
+  p.S = (int)cdiv(nchunks, p.cps);
+  p.lds = (size_t)(M + 1) * (p.cps * 64 + 8) * 2 + (size_t)2 * p.cps * xr * 4;
+  p.part_bytes = p.S > 1 ? round_up((size_t)p.S * M * N * 4, 256) : 0;
   return p;
 }
 
@@ -531,10 +546,21 @@ size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   return kCounterBytes + round_up((size_t)(K / G) * M * 4, 256);
 }
 
+template <typename T, int G, int MB, int CPW>
+static void launch_skinny_c(const SkinnyPlan& p, const SkinnyArgs& a, hipStream_t st) {
+  dim3 grid((unsigned)cdiv(a.N, 32), (unsigned)p.S);
+  hipLaunchKernelGGL((w4_skinny_kernel<T, G, MB, CPW>), grid, dim3(256), p.lds, st, a);
+}
+
 template <typename T, int G, int MB>
 static void launch_skinny_t(const SkinnyPlan& p, const SkinnyArgs& a, hipStream_t st) {
-  dim3 grid((unsigned)cdiv(a.N, 32), (unsigned)p.S);
-  hipLaunchKernelGGL((w4_skinny_kernel<T, G, MB>), grid, dim3(256), p.lds, st, a);
+  switch (p.CPW) {
+    case 1: launch_skinny_c<T, G, MB, 1>(p, a, st); break;
+    case 2: launch_skinny_c<T, G, MB, 2>(p, a, st); break;
+    case 4: launch_skinny_c<T, G, MB, 4>(p, a, st); break;
+    case 5: launch_skinny_c<T, G, MB, 5>(p, a, st); break;
+    default: launch_skinny_c<T, G, MB, 8>(p, a, st); break;
+  }
 }
 
 template <typename T, int G>
