@@ -73,9 +73,11 @@ int sparkq_is_available(void);
  *   biases  [N,K/G] x_dtype
  *   y       [M,N]   y_dtype (x_dtype, or F32 for the unrounded epilogue)
  * group_size in {32, 64, 128}; bits must be 4; K % 64 == 0; K % G == 0.
- * Dispatches internally: M <= 32 runs the weight-streaming skinny kernel
- * (MFMA 32x32x16; when the shape splits K across workgroups the last
- * workgroup of each 32-row tile combines the partials in the same launch),
+ * Dispatches internally: M <= 4 runs the decode GEMV (whole rows per
+ * workgroup, 4x4x4 MFMA blocks, no workspace) when the shape fits its LDS
+ * budget (K <= 10240 for M = 1); other M <= 32 run the weight-streaming skinny
+ * kernel (MFMA 32x32x16; when the shape splits K across workgroups the last
+ * workgroup of each 32-row tile combines the partials in the same launch);
  * larger M runs the LDS-tiled MFMA GEMM behind a group-sum prologue.
  * Workspace: the first 16384 bytes hold per-tile counters and must be zero
  * before the first call; every call leaves them zero again. Give each entry

@@ -121,6 +121,25 @@ __device__ __forceinline__ u32x4_t decode_w4(uint32_t w, DecodeConsts c) {
   return r;
 }
 
+// ---------------------------------------------------------------------------
+// buffer loads: a load whose offset lies outside the buffer returns zero and
+// touches no memory, so a lane that has nothing to read gets zeros without a
+// branch (a branch around a load makes the compiler wait for the load where
+// the branch rejoins). Buffers must be smaller than kOob bytes.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOob = 0x80000000u;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // dword 3 = 0x00020000: 32-bit data format, as raw loads require on gfx9
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load2(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
 // Output row of accumulator v held by lane l for a 32x32 MFMA tile.
 __device__ __forceinline__ int mfma32_row(int lane, int v) {
   return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);

@@ -9,6 +9,10 @@
 // Kernels
 //   w4_dequant_kernel   fp32 fmaf(q, s, b) (debug / bit-exact check entry)
 //   w4_quantize_kernel  affine 4-bit quantizer (format producer)
+//   w4_gemv_kernel      M <= 4 decode: 4 rows x 256 contiguous bytes per load
+//                       instruction, v_mfma_f32_4x4x4_16b blocks, activations
+//                       and (scale, bias) staged once per workgroup in LDS,
+//                       whole rows per workgroup (no split-K)
 //   w4_skinny_kernel    M <= 32: weight streaming, 32 rows x 64 k per wave
 //                       step, MFMA 32x32x16, in-workgroup split-K over waves,
 //                       cross-workgroup split-K combined in the same launch by
@@ -85,6 +89,344 @@ __global__ __launch_bounds__(256) void w4_quantize_kernel(
       word |= (uint32_t)q << (4 * j);
     }
     dst[i] = word;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode GEMV (M <= 4): 4x4x4 MFMA blocks over 256-byte row spans
+// ---------------------------------------------------------------------------
+// The weight rows are read in spans of 256 bytes (512 k). Lane l = 4b + j
+// (block b = l/4, quad row j = l%4) loads the 16 bytes at byte 16b of a span
+// of weight row 4q+j, so one load instruction covers 4 rows x 256 contiguous
+// bytes (whole cache lines). v_mfma_f32_4x4x4_16b runs 16 independent 4x4x4
+// products: block b multiplies the activation rows (A: lane 4b+i holds
+// x[i]) by the 4 weight rows (B: lane 4b+j holds row j) over 4 k of the 32 k
+// in that 16-byte piece; eight of them cover the piece, and lane 4b+j ends
+// with D[i] = sum over the piece of x[i,k] * (OFFSET + q[4q+j,k]) for i = 0..3.
+// A 16-byte piece never straddles a group (G >= 32), so the lane applies its
+// own group's scale and bias: acc[i] += s*D[i] + (b - OFFSET*s)*X[i] with X[i]
+// the sum of x[i] over the piece. The sixteen blocks are summed by lane
+// shuffles once per row quad.
+//
+// A vector memory instruction costs the texture unit about the same whatever
+// its width, so the weights are the only per-wave global loads. The
+// activations, their per-piece sums and the (scale, bias) pairs of the
+// workgroup's rows are staged in LDS once per workgroup: the activations in
+// the k order of the decoded pairs, the pairs interleaved into one dword.
+// Work split: a workgroup owns R rows over the whole K; each wave owns one
+// span group (SG groups of up to US consecutive spans per row) for RQW row
+// quads and keeps that group's activations in registers. With SG > 1 the SG
+// waves of a row quad add their sums through LDS. Every global load is a
+// buffer load issued before any compute; lanes with nothing to read use an
+// out-of-range offset and read zeros.
+struct GemvArgs {
+  const uint16_t* x;
+  const uint32_t* w;
+  const uint16_t* sc;
+  const uint16_t* bi;
+  void* y;
+  int y_dtype;
+  int M, N, K;
+  int SG;       // span groups per row (1, 2 or 4)
+  int USr;      // spans per group (the last group may have fewer)
+  int R;        // rows per workgroup
+};
+
+constexpr int kGemvXP = 2;   // staged activation pieces (64 B) per thread, at most
+constexpr int kGemvSP = 4;   // staged (scale, bias) pieces (16 B each) per thread, at most
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma4x4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
+                                           f32x4_t c);
+template <>
+__device__ __forceinline__ f32x4_t mfma4x4<BF16>(uint32_t a0, uint32_t a1, uint32_t b0,
+                                                 uint32_t b1, f32x4_t c) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4_t, u32x2_t{a0, a1}),
+                                                __builtin_bit_cast(s16x4_t, u32x2_t{b0, b1}), c,
+                                                0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4_t mfma4x4<F16>(uint32_t a0, uint32_t a1, uint32_t b0,
+                                                uint32_t b1, f32x4_t c) {
+  typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4_t, u32x2_t{a0, a1}),
+                                            __builtin_bit_cast(f16x4_t, u32x2_t{b0, b1}), c, 0,
+                                            0, 0);
+}
+
+// sum of the two 16-bit values of a packed pair, in fp32
+template <typename T>
+__device__ __forceinline__ float pair_sum(uint32_t p, float acc);
+template <>
+__device__ __forceinline__ float pair_sum<BF16>(uint32_t p, float acc) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, p),
+                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
+template <>
+__device__ __forceinline__ float pair_sum<F16>(uint32_t p, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, p),
+                                __builtin_bit_cast(f16x2_t, 0x3C003C00u), acc, false);
+}
+
+// Decode one word of eight codes into the pairs (q[j], q[j+4]), j = 0..3, as
+// OFFSET+q 16-bit values: pair j is ((w >> 4j) & 0x000F000F) | MAGIC.
+template <typename T>
+__device__ __forceinline__ void decode_w4_strided(uint32_t w, DecodeConsts c, uint32_t p[4]) {
+  p[0] = (w & c.mask) | c.magic;
+  p[1] = ((w >> 4) & c.mask) | c.magic;
+  p[2] = ((w >> 8) & c.mask) | c.magic;
+  p[3] = ((w >> 12) & c.mask) | c.magic;
+  if constexpr (T::kExactDecode) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = exact_f16_pair(p[i]);
+  }
+}
+
+// LDS layout of the decode GEMV (byte offsets)
+struct GemvLds {
+  int xp;    // activations [M][K] in pair order (2 B each)
+  int xs;    // sums of each 32-k piece: [K/32][4] fp32 (rows past M unused)
+  int sb;    // (scale, bias) of the workgroup's rows: [R][K/G] dwords
+  int red;   // cross-wave partial sums: [NW][RQW][4][4] fp32
+  int bytes;
+};
+__host__ __device__ __forceinline__ GemvLds gemv_lds(int M, int K, int R, int G, int NW, int RQW) {
+  GemvLds l;
+  l.xp = 0;
+  l.xs = l.xp + ((M * K * 2 + 15) & ~15);
+  l.sb = l.xs + (K / 32) * 16;
+  l.red = l.sb + ((R * (K / G) * 4 + 15) & ~15);
+  l.bytes = l.red + NW * RQW * 64;
+  return l;
+}
+
+template <typename T, int G, int MQ, int US, int RQW, int NW>
+__global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NT = 64 * NW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, j = lane & 3;
+  const int M = a.M, N = a.N, K = a.K, SG = a.SG, R = a.R;
+  const int RB = K >> 1;                       // bytes per weight row
+  const int U = (RB + 255) >> 8;               // spans per row
+  const int ng = K / G;                        // groups per row
+  const int r0 = blockIdx.x * R;               // first row of the workgroup
+  const int sg = wave % SG;
+  const int q0 = (r0 >> 2) + (wave / SG) * RQW;  // first row quad of the wave
+  const int u0 = sg * a.USr;
+  const int ns = min(a.USr, U - u0);           // spans of this wave (wave-uniform)
+  const GemvLds L = gemv_lds(M, K, R, G, NW, RQW);
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+
+  // 1. staging loads: activation pieces (64 B) and (scale, bias) pieces
+  const int nxp = M * (K >> 5);                // activation pieces
+  const int nsp = (R * ng) >> 3;               // 16-byte scale pieces of the workgroup
+  u32x4_t xr[kGemvXP][4];
+  u32x4_t sr[kGemvSP], br[kGemvSP];
+#pragma unroll
+  for (int i = 0; i < kGemvXP; ++i) {
+    const int pi = tid + i * NT;
+    const uint32_t off = pi < nxp ? 64u * pi : kOob;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
+  }
+#pragma unroll
+  for (int i = 0; i < kGemvSP; ++i) {
+    const int pi = tid + i * NT;
+    const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
+    sr[i] = buf_load16(rs, off);
+    br[i] = buf_load16(rb, off);
+  }
+
+  // 2. the wave's weights: RQW row quads x US spans
+  u32x4_t wv[RQW][US];
+#pragma unroll
+  for (int r = 0; r < RQW; ++r) {
+    const int row = 4 * (q0 + r) + j;
+#pragma unroll
+    for (int s = 0; s < US; ++s) {
+      const int p = 256 * (u0 + s) + 16 * b;
+      const bool ok = row < N && s < ns && p + 16 <= RB;
+      wv[r][s] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
+    }
+  }
+
+  // keep every load above ahead of the arithmetic below
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. write the staged data to LDS
+  {
+    uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
+    float* xs = reinterpret_cast<float*>(smem + L.xs);
+#pragma unroll
+    for (int i = 0; i < kGemvXP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nxp) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const u32x4_t r = xr[i][w];
+          const u32x4_t o = {__builtin_amdgcn_perm(r.z, r.x, 0x05040100u),   // (x0, x4)
+                             __builtin_amdgcn_perm(r.z, r.x, 0x07060302u),   // (x1, x5)
+                             __builtin_amdgcn_perm(r.w, r.y, 0x05040100u),   // (x2, x6)
+                             __builtin_amdgcn_perm(r.w, r.y, 0x07060302u)};  // (x3, x7)
+          *reinterpret_cast<u32x4_t*>(xp + 16 * pi + 4 * w) = o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[e], sum);
+        }
+        const int m = pi / (K >> 5), piece = pi - m * (K >> 5);
+        xs[4 * piece + m] = sum;
+      }
+    }
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+#pragma unroll
+    for (int i = 0; i < kGemvSP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nsp) {
+        const u32x4_t s = sr[i], c = br[i];
+        u32x4_t lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = __builtin_amdgcn_perm(c[e], s[e], 0x05040100u);  // (s0, b0)
+          hi[e] = __builtin_amdgcn_perm(c[e], s[e], 0x07060302u);                 // (s1, b1)
+        }
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. the wave's activations (pair order) and piece sums, from LDS
+  uint32_t xa[US][4][4];
+  float xm[US][MQ];
+  {
+    const unsigned char* xp = smem + L.xp;
+    const float* xs = reinterpret_cast<const float*>(smem + L.xs);
+#pragma unroll
+    for (int s = 0; s < US; ++s) {
+      const int piece = min(16 * (u0 + s) + b, (K >> 5) - 1);
+      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(xp + 2 * ((int64_t)min(j, M - 1) * K + 32 * piece));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const u32x4_t v = src[w];
+        xa[s][w][0] = v.x;
+        xa[s][w][1] = v.y;
+        xa[s][w][2] = v.z;
+        xa[s][w][3] = v.w;
+      }
+      if constexpr (MQ == 1) {
+        xm[s][0] = xs[4 * piece];
+      } else {
+        const f32x4_t v = *reinterpret_cast<const f32x4_t*>(xs + 4 * piece);
+        xm[s][0] = v.x;
+        xm[s][1] = v.y;
+        xm[s][2] = v.z;
+        xm[s][3] = v.w;
+      }
+    }
+  }
+
+  // 5. per row quad: decode and 8 MFMAs per span, then the group epilogue.
+  // A 4x4x4 MFMA takes ~48 cycles to feed its result to the next one, but
+  // issues every ~10 cycles when independent: the spans of a row quad keep
+  // separate accumulators (two each when there are fewer than three spans)
+  // and their MFMAs are interleaved. Template spans beyond the wave's group
+  // (s >= ns) are computed too and dropped by the epilogue.
+  const uint32_t* sb = reinterpret_cast<const uint32_t*>(smem + L.sb);
+  const DecodeConsts dc = decode_consts<T>();
+  constexpr int NA = US < 3 ? 2 : 1;     // accumulators per span
+  float out[RQW][MQ];
+#pragma unroll
+  for (int r = 0; r < RQW; ++r) {
+    const int rl = 4 * (q0 + r) + j - r0;      // row within the workgroup
+    f32x4_t d[US][NA];
+#pragma unroll
+    for (int s = 0; s < US; ++s)
+#pragma unroll
+      for (int h = 0; h < NA; ++h) d[s][h] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t pr[US][4];
+#pragma unroll
+      for (int s = 0; s < US; ++s) decode_w4_strided<T>(wv[r][s][w], dc, pr[s]);
+#pragma unroll
+      for (int s = 0; s < US; ++s)
+        d[s][0] = mfma4x4<T>(xa[s][w][0], xa[s][w][1], pr[s][0], pr[s][1], d[s][0]);
+#pragma unroll
+      for (int s = 0; s < US; ++s)
+        d[s][NA - 1] = mfma4x4<T>(xa[s][w][2], xa[s][w][3], pr[s][2], pr[s][3], d[s][NA - 1]);
+    }
+    float acc[MQ];
+#pragma unroll
+    for (int m = 0; m < MQ; ++m) acc[m] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < US; ++s) {
+      const int p = 256 * (u0 + s) + 16 * b;
+      const bool ok = s < ns && p + 16 <= RB;
+      // pieces past the row end carry zero codes and unrelated activations
+      const uint32_t pair = ok ? sb[rl * ng + (2 * p) / G] : 0u;
+      const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
+      const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) {
+        const float dm = NA == 2 ? d[s][0][m] + d[s][NA - 1][m] : d[s][0][m];
+        const float t = fmaf(sf, dm, fmaf(bf, xm[s][m], acc[m]));
+        acc[m] = ok ? t : acc[m];
+      }
+    }
+    // sum the sixteen blocks (lanes j, j+4, ..., j+60)
+#pragma unroll
+    for (int m = 0; m < MQ; ++m) {
+      float v = acc[m];
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      out[r][m] = v;
+    }
+  }
+
+  if (SG > 1) {
+    float* red = reinterpret_cast<float*>(smem + L.red);
+    if (lane < 4) {
+#pragma unroll
+      for (int r = 0; r < RQW; ++r)
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) red[((wave * RQW + r) * 4 + lane) * 4 + m] = out[r][m];
+    }
+    __syncthreads();
+    if (sg != 0) return;
+    if (lane < 4) {
+#pragma unroll
+      for (int r = 0; r < RQW; ++r)
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) {
+          float v = out[r][m];
+          for (int o = 1; o < SG; ++o) v += red[(((wave + o) * RQW + r) * 4 + lane) * 4 + m];
+          out[r][m] = v;
+        }
+    }
+  }
+  if (lane < 4) {
+#pragma unroll
+    for (int r = 0; r < RQW; ++r) {
+      const int row = 4 * (q0 + r) + lane;
+      if (row < N) {
+#pragma unroll
+        for (int m = 0; m < MQ; ++m)
+          if (m < M) store_out(a.y, (int64_t)m * N + row, out[r][m], a.y_dtype);
+      }
+    }
   }
 }
 
@@ -535,8 +877,101 @@ static SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K) {
   return p;
 }
 
+// Decode GEMV plan. A row has U = ceil(K/512) spans; a wave keeps at most 5
+// spans of activations in registers, so rows of up to 20 spans (K <= 10240)
+// split into SG = 1, 2 or 4 span groups. Workgroups of 4 waves (8 when
+// SG = 4) cover R = 4 * (waves / SG) * RQW rows; two row quads per wave once
+// that still leaves >= 2048 waves. The staged activations, (scale, bias)
+// pieces and LDS must fit the kernel's fixed budgets, and the scale tensors
+// must end on a 16-byte boundary (they are staged in 16-byte loads).
+struct GemvPlan {
+  bool ok;
+  int SG, USr, US, RQW, MQ, NW, R;
+  size_t lds;
+  int64_t wgs;
+};
+
+static GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int G) {
+  GemvPlan p{};
+  if (M > 4 || env_int("SPARKQ_W4_NO_GEMV", 0)) return p;
+  // every tensor must stay below the out-of-range offset of the buffer loads
+  if (N * (K / 2) >= (int64_t)kOob || M * K * 2 >= (int64_t)kOob) return p;
+  const int64_t ng = K / G;
+  if ((N * ng * 2) % 16 != 0) return p;
+  const int64_t U = cdiv(K / 2, 256);
+  if (U <= 5)
+    p.SG = 1;
+  else if (U <= 10)
+    p.SG = 2;
+  else if (U <= 20)
+    p.SG = 4;
+  else
+    return p;
+  p.USr = (int)cdiv(U, p.SG);
+  p.US = p.USr <= 1 ? 1 : (p.USr <= 2 ? 2 : 5);
+  p.NW = p.SG == 4 ? 8 : 4;
+  const int64_t nq = cdiv(N, 4);
+  p.RQW = cdiv(nq, 2) * p.SG >= 2048 ? 2 : 1;
+  p.MQ = M == 1 ? 1 : 4;
+  p.R = 4 * (p.NW / p.SG) * p.RQW;
+  const int64_t nt = 64 * p.NW;
+  if (M * (K / 32) > kGemvXP * nt || p.R * ng / 8 > kGemvSP * nt) return p;
+  const GemvLds l = gemv_lds((int)M, (int)K, p.R, G, p.NW, p.RQW);
+  if (l.bytes > 65536) return p;
+  p.lds = (size_t)l.bytes;
+  p.wgs = cdiv(N, p.R);
+  p.ok = true;
+  return p;
+}
+
+template <typename T, int G, int MQ, int US, int RQW, int NW>
+static void launch_gemv_w(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((w4_gemv_kernel<T, G, MQ, US, RQW, NW>), dim3((unsigned)p.wgs),
+                     dim3(64 * NW), p.lds, st, a);
+}
+template <typename T, int G, int MQ, int US, int RQW>
+static void launch_gemv_r(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
+  if (p.NW == 4)
+    launch_gemv_w<T, G, MQ, US, RQW, 4>(p, a, st);
+  else
+    launch_gemv_w<T, G, MQ, US, RQW, 8>(p, a, st);
+}
+template <typename T, int G, int MQ, int US>
+static void launch_gemv_u(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
+  if (p.RQW == 1)
+    launch_gemv_r<T, G, MQ, US, 1>(p, a, st);
+  else
+    launch_gemv_r<T, G, MQ, US, 2>(p, a, st);
+}
+template <typename T, int G, int MQ>
+static void launch_gemv_m(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
+  if (p.US == 1)
+    launch_gemv_u<T, G, MQ, 1>(p, a, st);
+  else if (p.US == 2)
+    launch_gemv_u<T, G, MQ, 2>(p, a, st);
+  else
+    launch_gemv_u<T, G, MQ, 5>(p, a, st);
+}
+template <typename T, int G>
+static void launch_gemv_g(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
+  if (p.MQ == 1)
+    launch_gemv_m<T, G, 1>(p, a, st);
+  else
+    launch_gemv_m<T, G, 4>(p, a, st);
+}
+template <typename T>
+static void launch_gemv(const GemvPlan& p, int G, const GemvArgs& a, hipStream_t st) {
+  if (G == 32)
+    launch_gemv_g<T, 32>(p, a, st);
+  else if (G == 64)
+    launch_gemv_g<T, 64>(p, a, st);
+  else
+    launch_gemv_g<T, 128>(p, a, st);
+}
+
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
+  if (plan_gemv(M, N, K, G).ok) return 0;
   // every workspace of this entry point starts with the counter block, so a
   // GEMM call never writes over the counters a later split-K call relies on
   if (M <= 32) {
@@ -610,6 +1045,27 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
   if (need > 0 && (ws == nullptr || wsb < need))
     return set_error(SPARKQ_ERR_WORKSPACE,
                      "w4a16_linear needs a workspace of %zu bytes (got %zu)", need, wsb);
+  const GemvPlan gp = plan_gemv(M, N, K, G);
+  if (gp.ok) {
+    GemvArgs a{};
+    a.x = (const uint16_t*)x;
+    a.w = w;
+    a.sc = (const uint16_t*)s;
+    a.bi = (const uint16_t*)b;
+    a.y = y;
+    a.y_dtype = ydt;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.SG = gp.SG;
+    a.USr = gp.USr;
+    a.R = gp.R;
+    if (xdt == SPARKQ_BF16)
+      launch_gemv<BF16>(gp, G, a, st);
+    else
+      launch_gemv<F16>(gp, G, a, st);
+    return check_launch("w4_gemv_kernel");
+  }
   if (M <= 32) {
     const SkinnyPlan p = plan_skinny(M, N, K);
     if (p.S > 1 && cdiv(N, 32) > kMaxCounterTiles)

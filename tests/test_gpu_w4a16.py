@@ -106,6 +106,18 @@ def test_split_plans(gpu, m, n, k):
     check_fp32(y32, ref)
 
 
+@pytest.mark.parametrize("m,n,k,g", [(1, 37, 576, 32), (3, 41, 576, 64), (2, 4, 64, 32),
+                                     (4, 130, 9728, 32), (1, 5, 10240, 128), (3, 9, 4608, 64)])
+def test_decode_ragged_shapes(gpu, m, n, k, g):
+    """Row counts that leave a partial row quad, rows whose last 512-k span is
+    partial, the longest rows the decode kernel takes, and K = 64."""
+    x, wq, s, b = w4_problem(m, n, k, g, seed=n + k)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    check_fp32(y32, ref)
+    check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
+
+
 def test_one_hot_rows_pick_weight_columns(gpu):
     import sparkq
 
