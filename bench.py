@@ -188,6 +188,48 @@ def bench_sdpa(torch, sparkq, dev, b, n, iters):
             "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": kv_bytes}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w4_gemv_gate_up_m1_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed PMC
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters
+    on a copy kernel of known size), or None when there is none."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1].strip()))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def only_dominant(torch, sparkq, dev, iters):
+    """Driver for rocprofv3 --pmc runs: the dominant kernel alone (gate+up
+    GEMV at M=1 over 36 distinct weight sets), then a 256 MiB device copy whose
+    byte count calibrates the counters."""
+    n, k = PROJ["gate_up"]
+    layers = []
+    gen = torch.Generator(device=dev).manual_seed(0)
+    for _ in range(LAYERS):
+        w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        layers.append(sparkq.affine_quantize(w, group_size=G))
+        del w
+    x = torch.randn((1, k), device=dev).to(torch.bfloat16)
+    y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        for wq, s, b in layers:
+            sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y)
+    torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"dominant kernel x {iters * LAYERS} launches, then 5 copies of {256 << 20} bytes")
+
+
 def cpu_baseline(layer_host, budget_s=12.0):
     """The oracle's OpenMP fp32 dequantize-then-dot GEMV on this host, M=1,
     one layer's three projections per pass, repeated for ~budget_s."""
@@ -224,6 +266,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only-dominant", action="store_true",
+                    help="run only the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of "
@@ -238,6 +282,9 @@ def main():
     dev = torch.device("cuda:0")
     if not sparkq.is_w8a8_available():
         raise RuntimeError("libsparkq unusable on cuda:0 (needs gfx950)")
+    if args.only_dominant:
+        only_dominant(torch, sparkq, dev, max(args.steps, 1))
+        return
     log("generating 36 layers of W4A16 G64 weights")
     layers = make_w4_layers(torch, sparkq, dev, LAYERS)
     sweep_bytes = LAYERS * sum(w4_bytes(*PROJ[n]) for n in PROJ)
@@ -251,8 +298,9 @@ def main():
     gu_bytes = w4_bytes(*PROJ["gate_up"])
     achieved = gu_bytes / (gu_ms / 1e3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "w4_skinny_kernel<BF16,64,8> (gate+up 19456x2560, M=1)",
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(),
+                "kernel": "w4_gemv_kernel<BF16,64,1,5,2,4> (gate+up 19456x2560, M=1)",
                 "bytes_per_launch": gu_bytes, "avg_launch_ms": round(gu_ms, 5)}
 
     extras = {}
