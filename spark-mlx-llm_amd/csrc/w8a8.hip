@@ -2,6 +2,9 @@
 // per-channel int8 weights, exact int32 accumulation on the int8 MFMA.
 //
 // Kernels
+//   i8_gemv_kernel       M <= 4 decode: whole rows per workgroup, 4 rows x
+//                        256 bytes per load, v_dot4_i32_i8, activation
+//                        quantizer fused (one launch per projection)
 //   a8_quantize_kernel   one workgroup per token row: amax, scale = amax/127
 //                        (1 when 0), q = clamp(rint(x/scale), -127, 127);
 //                        bit-exact with X/src/kernels/w8a8_quantize.metal:11-27
@@ -185,8 +188,279 @@ __global__ __launch_bounds__(256, 2) void i8_skinny_kernel(I8Args args) {
 }
 
 // ---------------------------------------------------------------------------
+// decode GEMV (M <= 4), activation quantizer fused
+// ---------------------------------------------------------------------------
+// A workgroup owns R whole weight rows. Lane l = 4b + j loads the 16 bytes at
+// byte 16b of a 256-byte span of weight row 4q+j (4 rows x 256 contiguous
+// bytes per load instruction) and multiplies them by the 16 matching int8
+// activations of each row m with four v_dot4_i32_i8; int32 sums are exact in
+// any order, so the sixteen lanes of a row and the span groups of a row quad
+// are added by shuffles and LDS. The workgroup quantizes the activations
+// itself (per-token amax over the whole row, scale = amax/127 with IEEE
+// division, rint, clamp to +-127, as a8_quantize_kernel), so one launch does
+// the whole projection. The weights are the only per-wave global loads; the
+// activations are staged once per workgroup through LDS. All loads are
+// bounds-checked buffer loads issued before any arithmetic.
+struct I8GemvArgs {
+  const void* x;        // [M,K] activations in x_dtype, or int8 for the raw mode
+  const int8_t* w;      // [N,K]
+  const float* sw;      // [N]
+  const void* bias;     // [N] or null
+  void* y;              // [M,N] (epilogue)
+  int32_t* c_raw;       // [M,N] (raw)
+  int x_dtype, bias_dtype, y_dtype;
+  int M, N, K;
+  int SG, USr, R;
+  int mode;
+};
+
+constexpr int kI8XP = 4;  // staged 16-byte activation pieces per thread, at most
+
+// x element e of a 16-byte piece as fp32 (XT: 0 bf16, 1 f16, 2 f32)
+template <int XT>
+__device__ __forceinline__ float piece_elem(const u32x4_t& v, int e) {
+  if constexpr (XT == 2) return __uint_as_float(v[e]);
+  const uint32_t word = v[e >> 1];
+  const uint16_t h = (e & 1) ? (uint16_t)(word >> 16) : (uint16_t)(word & 0xFFFFu);
+  return XT == 0 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+template <int MQ, int US, int NW, int XT>  // XT 3: int8 activations (raw int32 mode)
+__global__ __launch_bounds__(64 * NW) void i8_gemv_kernel(I8GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NT = 64 * NW;
+  constexpr int ES = XT == 2 ? 4 : (XT == 3 ? 1 : 2);   // activation element bytes
+  constexpr int EP = 16 / ES;                            // elements per piece
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, j = lane & 3;
+  const int M = a.M, N = a.N, K = a.K, SG = a.SG, R = a.R;
+  const int U = (K + 255) >> 8;
+  const int r0 = blockIdx.x * R;
+  const int sg = wave % SG;
+  const int q = (r0 >> 2) + wave / SG;
+  const int u0 = sg * a.USr;
+  const int ns = min(a.USr, U - u0);
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);                     // [M][K]
+  unsigned* amax = reinterpret_cast<unsigned*>(smem + ((M * K + 15) & ~15));
+  int32_t* red = reinterpret_cast<int32_t*>(amax + 4);               // [NW][4][4]
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * ES);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * K);
+
+  // 1. staging loads of the activations
+  const int nxp = (M * K * ES) >> 4;
+  u32x4_t xr[kI8XP];
+#pragma unroll
+  for (int i = 0; i < kI8XP; ++i) {
+    const int pi = tid + i * NT;
+    xr[i] = buf_load16(rx, pi < nxp ? 16u * pi : kOob);
+  }
+  // 2. the wave's weights: one row quad x US spans
+  u32x4_t wv[US];
+  {
+    const int row = 4 * q + j;
+#pragma unroll
+    for (int s = 0; s < US; ++s) {
+      const int p = 256 * (u0 + s) + 16 * b;
+      const bool ok = row < N && s < ns && p + 16 <= K;
+      wv[s] = buf_load16(rw, ok ? (uint32_t)row * K + p : kOob);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. per-token amax (exact in any order), then the quantized rows in LDS
+  if (tid < 4) amax[tid] = 0u;
+  __syncthreads();
+  if constexpr (XT != 3) {
+#pragma unroll
+    for (int i = 0; i < kI8XP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nxp) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EP; ++e) mx = fmaxf(mx, fabsf(piece_elem<XT>(xr[i], e)));
+        __hip_atomic_fetch_max(&amax[(pi * EP) / K], __float_as_uint(mx), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < kI8XP; ++i) {
+    const int pi = tid + i * NT;
+    if (pi < nxp) {
+      if constexpr (XT == 3) {
+        *reinterpret_cast<u32x4_t*>(xq + 16 * pi) = xr[i];
+      } else {
+        const float am = __uint_as_float(amax[(pi * EP) / K]);
+        const float scale = am > 0.0f ? am / 127.0f : 1.0f;
+        uint32_t packed[EP / 4];
+#pragma unroll
+        for (int e = 0; e < EP / 4; ++e) packed[e] = 0u;
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+          float v = __builtin_rintf(piece_elem<XT>(xr[i], e) / scale);
+          v = fminf(fmaxf(v, -127.0f), 127.0f);
+          packed[e >> 2] |= ((uint32_t)(int32_t)v & 0xFFu) << (8 * (e & 3));
+        }
+        if constexpr (EP == 8) {
+          *reinterpret_cast<uint2*>(xq + 8 * pi) = uint2{packed[0], packed[1]};
+        } else {
+          *reinterpret_cast<uint32_t*>(xq + 4 * pi) = packed[0];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. int8 dot products, 16 activations x 16 weights per lane per span
+  int32_t acc[MQ];
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) acc[m] = 0;
+#pragma unroll
+  for (int s = 0; s < US; ++s) {
+    const int p = 256 * (u0 + s) + 16 * b;
+    if (s < ns && p + 16 <= K) {
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) {
+        if (m < M) {
+          const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xq + m * K + p);
+          int32_t t = acc[m];
+          t = __builtin_amdgcn_sdot4((int)wv[s].x, (int)xv.x, t, false);
+          t = __builtin_amdgcn_sdot4((int)wv[s].y, (int)xv.y, t, false);
+          t = __builtin_amdgcn_sdot4((int)wv[s].z, (int)xv.z, t, false);
+          t = __builtin_amdgcn_sdot4((int)wv[s].w, (int)xv.w, t, false);
+          acc[m] = t;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) {
+    int32_t v = acc[m];
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 8);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    acc[m] = v;
+  }
+  if (SG > 1) {
+    if (lane < 4) {
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) red[(wave * 4 + lane) * 4 + m] = acc[m];
+    }
+    __syncthreads();
+    if (sg != 0) return;
+    if (lane < 4) {
+#pragma unroll
+      for (int m = 0; m < MQ; ++m)
+        for (int o = 1; o < SG; ++o) acc[m] += red[((wave + o) * 4 + lane) * 4 + m];
+    }
+  }
+  // 5. epilogue: lanes 0..3 hold rows 4q..4q+3
+  if (lane < 4) {
+    const int row = 4 * q + lane;
+    if (row < N) {
+      float sw = 0.0f, bias = 0.0f;
+      if (a.mode == kOutEpilogue) {
+        sw = a.sw[row];
+        bias = a.bias ? load_in(a.bias, row, a.bias_dtype) : 0.0f;
+      }
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) {
+        if (m < M) {
+          if (a.mode == kOutRaw) {
+            a.c_raw[(int64_t)m * N + row] = acc[m];
+          } else {
+            const float am = __uint_as_float(amax[m]);
+            const float sa = am > 0.0f ? am / 127.0f : 1.0f;
+            store_out(a.y, (int64_t)m * N + row, fmaf((float)acc[m] * sa, sw, bias), a.y_dtype);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
+// Decode GEMV plan: a row has U = ceil(K/256) spans; a wave keeps at most 10
+// spans of weights in flight, so rows of up to 40 spans (K <= 10240) split
+// into SG = 1, 2 or 4 span groups; workgroups of 4 waves (8 when SG = 4)
+// cover R = 4 * waves / SG rows. The staged activations must fit the fixed
+// per-thread budget and the tensors the buffer loads' offset range.
+struct I8GemvPlan {
+  bool ok;
+  int SG, USr, US, NW, MQ, R;
+  size_t lds;
+  int64_t wgs;
+};
+
+static I8GemvPlan plan_i8_gemv(int64_t M, int64_t N, int64_t K, int esize) {
+  I8GemvPlan p{};
+  if (M > 4 || env_int("SPARKQ_I8_NO_GEMV", 0)) return p;
+  if (N * K >= (int64_t)kOob || M * K * esize >= (int64_t)kOob) return p;
+  const int64_t U = cdiv(K, 256);
+  if (U <= 10)
+    p.SG = 1;
+  else if (U <= 20)
+    p.SG = 2;
+  else if (U <= 40)
+    p.SG = 4;
+  else
+    return p;
+  p.USr = (int)cdiv(U, p.SG);
+  p.US = p.USr <= 2 ? 2 : (p.USr <= 5 ? 5 : 10);
+  p.NW = p.SG == 4 ? 8 : 4;
+  p.MQ = M == 1 ? 1 : 4;
+  p.R = 4 * (p.NW / p.SG);
+  if (M * K * esize > (int64_t)kI8XP * 16 * 64 * p.NW) return p;
+  p.lds = round_up((size_t)M * K, 16) + 16 + (size_t)p.NW * 64;
+  p.wgs = cdiv(N, p.R);
+  p.ok = true;
+  return p;
+}
+
+template <int MQ, int US, int NW>
+static void launch_i8_gemv_x(const I8GemvPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  dim3 grid((unsigned)p.wgs), block(64 * NW);
+  switch (xt) {
+    case 0: hipLaunchKernelGGL((i8_gemv_kernel<MQ, US, NW, 0>), grid, block, p.lds, st, a); break;
+    case 1: hipLaunchKernelGGL((i8_gemv_kernel<MQ, US, NW, 1>), grid, block, p.lds, st, a); break;
+    case 2: hipLaunchKernelGGL((i8_gemv_kernel<MQ, US, NW, 2>), grid, block, p.lds, st, a); break;
+    default: hipLaunchKernelGGL((i8_gemv_kernel<MQ, US, NW, 3>), grid, block, p.lds, st, a); break;
+  }
+}
+template <int MQ, int US>
+static void launch_i8_gemv_w(const I8GemvPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  if (p.NW == 4)
+    launch_i8_gemv_x<MQ, US, 4>(p, a, xt, st);
+  else
+    launch_i8_gemv_x<MQ, US, 8>(p, a, xt, st);
+}
+template <int MQ>
+static void launch_i8_gemv_u(const I8GemvPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  if (p.US == 2)
+    launch_i8_gemv_w<MQ, 2>(p, a, xt, st);
+  else if (p.US == 5)
+    launch_i8_gemv_w<MQ, 5>(p, a, xt, st);
+  else
+    launch_i8_gemv_w<MQ, 10>(p, a, xt, st);
+}
+static int launch_i8_gemv(const I8GemvPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  if (p.MQ == 1)
+    launch_i8_gemv_u<1>(p, a, xt, st);
+  else
+    launch_i8_gemv_u<4>(p, a, xt, st);
+  return check_launch("i8_gemv_kernel");
+}
+
+// activation type code of the GEMV kernel (3 = int8) and its element size
+static int i8_xt(int xdt) { return xdt == SPARKQ_BF16 ? 0 : (xdt == SPARKQ_F16 ? 1 : 2); }
+static int esize_of(int xdt) { return xdt == SPARKQ_F32 ? 4 : 2; }
+
 struct I8Plan {
   int S, cps, slab;
   size_t lds;
@@ -219,6 +493,8 @@ static I8Plan plan_i8(int64_t M, int64_t N, int64_t K) {
 
 size_t w8a8_workspace(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
+  // the fused decode GEMV needs no workspace for any activation dtype
+  if (plan_i8_gemv(M, N, K, 4).ok && plan_i8_gemv(M, N, K, 2).ok) return 0;
   const I8Plan p = plan_i8(M, N, K);
   // counters, int8 activations, fp32 scales, int32 partials
   return kCounterBytes + round_up((size_t)M * K, 256) + round_up((size_t)M * 4, 256) +
@@ -226,6 +502,7 @@ size_t w8a8_workspace(int64_t M, int64_t N, int64_t K) {
 }
 
 size_t i8_matmul_workspace(int64_t M, int64_t N, int64_t K) {
+  if (plan_i8_gemv(M, N, K, 1).ok) return 0;
   const I8Plan p = plan_i8(M, N, K);
   return p.counter_bytes + p.part_bytes;
 }
@@ -245,6 +522,21 @@ int a8_quantize(const void* x, int8_t* q, float* scales, int64_t M, int64_t K, i
 
 int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int64_t N,
                     int64_t K, void* ws, size_t wsb, hipStream_t st) {
+  const I8GemvPlan gp = plan_i8_gemv(M, N, K, 1);
+  if (gp.ok) {
+    I8GemvArgs g{};
+    g.x = a;
+    g.w = b;
+    g.c_raw = c;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.SG = gp.SG;
+    g.USr = gp.USr;
+    g.R = gp.R;
+    g.mode = kOutRaw;
+    return launch_i8_gemv(gp, g, 3, st);
+  }
   const I8Plan p = plan_i8(M, N, K);
   const size_t need = p.counter_bytes + p.part_bytes;
   if (need > 0 && (ws == nullptr || wsb < need))
@@ -271,6 +563,26 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
 int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bias,
                 int bias_dtype, void* y, int64_t M, int64_t N, int64_t K, int xdt, int ydt,
                 void* ws, size_t wsb, hipStream_t st) {
+  const I8GemvPlan gp = plan_i8_gemv(M, N, K, esize_of(xdt));
+  if (gp.ok) {
+    I8GemvArgs g{};
+    g.x = x;
+    g.w = w;
+    g.sw = wsc;
+    g.bias = bias;
+    g.bias_dtype = bias_dtype;
+    g.y = y;
+    g.y_dtype = ydt;
+    g.x_dtype = xdt;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.SG = gp.SG;
+    g.USr = gp.USr;
+    g.R = gp.R;
+    g.mode = kOutEpilogue;
+    return launch_i8_gemv(gp, g, i8_xt(xdt), st);
+  }
   const size_t need = w8a8_workspace(M, N, K);
   if (ws == nullptr || wsb < need)
     return set_error(SPARKQ_ERR_WORKSPACE,

@@ -49,7 +49,9 @@ def test_quantize_ties_round_to_even(gpu):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 3584, 2560), (8, 2560, 9728), (16, 19456, 2560),
-                                   (33, 96, 256), (70, 130, 512), (2, 40, 32)])
+                                   (33, 96, 256), (70, 130, 512), (2, 40, 32),
+                                   (3, 37, 32), (4, 130, 9728), (2, 5, 10240), (1, 9, 4864),
+                                   (4, 2560, 2560)])
 def test_int8_matmul_int32_bit_exact(gpu, m, n, k):
     import sparkq
 
@@ -82,7 +84,8 @@ def _w8(n, k, seed=0):
 
 @pytest.mark.parametrize("dtype", [o.BF16, o.F16, o.F32])
 @pytest.mark.parametrize("m,n,k", [(1, 3584, 2560), (8, 2560, 9728), (16, 19456, 2560),
-                                   (40, 100, 256)])
+                                   (40, 100, 256), (1, 2560, 9728), (3, 37, 32), (4, 130, 4096),
+                                   (2, 21, 10240)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_w8a8_linear_bit_exact(gpu, m, n, k, dtype, with_bias):
     import sparkq
@@ -109,6 +112,26 @@ def test_w8a8_linear_bit_exact(gpu, m, n, k, dtype, with_bias):
     assert y.dtype == (torch.float32 if dtype == o.F32 else TORCH16[dtype])
     if dtype != o.F32:
         assert np.array_equal(down16(y)[:, cols], o.round16(ref, dtype))
+
+
+def test_w8a8_decode_zero_row_and_repeat(gpu):
+    """Decode GEMV with an all-zero activation row (scale 1, zero codes) and a
+    second call on the same buffers giving identical bits."""
+    import sparkq
+
+    m, n, k = 3, 260, 2560
+    wq, wsc = _w8(n, k, seed=4)
+    x16 = _x(m, k, o.BF16, seed=5)
+    x16[1] = 0
+    xt = up16(x16, o.BF16, gpu)
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    y1 = sparkq.w8a8_linear(xt, wt, st, out_dtype=torch.float32)
+    y2 = sparkq.w8a8_linear(xt, wt, st, out_dtype=torch.float32)
+    assert torch.equal(y1, y2)
+    qa, sa = o.a8_quantize(o.bits_to_f32(x16, o.BF16))
+    ref = o.w8a8_epilogue(o.int8_matmul(qa, wq), sa, wsc)
+    assert np.array_equal(y1.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert np.all(y1[1].cpu().numpy() == 0)
 
 
 def test_readme_known_answer(gpu):
