@@ -17,9 +17,16 @@
 //                       step, MFMA 32x32x16, in-workgroup split-K over waves,
 //                       cross-workgroup split-K combined in the same launch by
 //                       the last workgroup of each tile
-//   xsum_kernel         group sums X_g[m] for the GEMM, layout [K/G][M]
-//   w4_gemm_kernel      M > 32: 128x128x64 LDS tiles (A bf16/f16, B decoded
-//                       to OFFSET+q), double-buffered, MFMA 32x32x16
+//   gemm_prep_kernel    bf16 GEMM prologue: fp16 activations and scales
+//                       under per-row power-of-two shifts, bias slots
+//   w4_gemm_x16_kernel  bf16, M > 32: 128x128x64 LDS tiles of exact fp16
+//                       operands (weights decoded to s'*(q-8)), fp16 MFMA
+//                       32x32x16 with no per-group epilogue, then the bias
+//                       slots on the bf16 MFMA
+//   xsum_kernel         group sums X_g[m] for the fp16 GEMM, layout [K/G][M]
+//   w4_gemm_kernel      fp16, M > 32: 128x128x64 LDS tiles (B decoded to the
+//                       exact q), per-group fp32 scale and bias epilogue
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 
@@ -679,6 +686,281 @@ __device__ __forceinline__ int tile_off(int row, int kc) {
   return row * 64 + ((kc ^ (row & 7)) << 3);
 }
 
+// ---------------------------------------------------------------------------
+// bf16 prefill GEMM on exact fp16 operands
+// ---------------------------------------------------------------------------
+// With w = s*q + b = s*(q-8) + b', b' = b + 8s, the affine dot splits into
+//   y[m,n] = sum_k x[m,k] * s[n,g(k)]*(q-8)  +  sum_g b'[n,g] * X_g[m]
+// (X_g[m] the sum of x[m,:] over group g). Both parts run on the MFMA with
+// products that are exact in fp32:
+//  * s*(q-8) is a bf16 significand (8 bits) times |q-8| <= 8: at most 11
+//    significant bits, exact in fp16. A per-row power of two 2^-es[n] brings
+//    max_g |s[n,g]| into [2^12, 2^13), so |s'*(q-8)| <= 65280 stays finite.
+//    Activations scale the same way per row, 2^-ex[m] putting max_k |x[m,k]|
+//    into [2^15, 2^16). The fp16 MFMA then accumulates exact products and the
+//    epilogue multiplies by 2^(ex[m]+es[n]) (an exponent add). The only
+//    rounding this adds is for values below 2^-24 after the shift (fp16
+//    subnormals): scales under 2^-30 of their row's largest and activations
+//    under 2^-39 of theirs.
+//  * the bias part is a GEMM over K2 = 3*K/G "bias slots" on the bf16 MFMA,
+//    with both factors split into bf16 pairs so that the three products
+//    Xh*bh + Xh*bl + Xl*bh reproduce X*b' to ~2^-17 relative:
+//      A2[m][3g .. 3g+2] = (Xh, Xh, Xl),  B2[n][3g .. 3g+2] = (bh, bl, bh),
+//    zero-padded to K2p = a multiple of 16 slots.
+// Weights decode per uint32 word as dword i = (code i, code i+4) (one shift
+// and one and-or under the fp16 1024 pattern, then a packed subtract of 1032
+// and a packed multiply by s'); the prologue stores x' with the same
+// in-chunk order, dword i = (x[8c+i], x[8c+i+4]), so the MFMA pairs them.
+__host__ __device__ __forceinline__ int bias_slots(int K, int G) { return (3 * (K / G) + 15) & ~15; }
+
+struct GemmPrepArgs {
+  const uint16_t* x;   // [M][K] bf16
+  const uint16_t* sc;  // [N][K/G] bf16
+  const uint16_t* bi;  // [N][K/G] bf16
+  uint16_t* xh;        // [M][K] fp16, scaled and chunk-permuted
+  int* ex;             // [M]
+  uint16_t* a2;        // [M][K2p] bf16
+  uint16_t* sp;        // [N][K/G] fp16 scaled scales
+  int* es;             // [N]
+  uint16_t* b2;        // [N][K2p] bf16
+  int M, N, K, G, K2p;
+};
+
+__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
+  hi = f32_to_bf16(v);
+  lo = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+// exponent that brings a positive finite maximum into [2^top, 2^(top+1))
+__device__ __forceinline__ int row_shift(float amax, int top) {
+  return (amax > 0.0f && amax <= 3.4028235e38f) ? ilogbf(amax) - top : 0;
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  return v;
+}
+
+// blocks [0, M): one activation row each; blocks [M, M + N/4): four weight
+// rows each, one per wave
+__global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ng = a.K / a.G;
+  if ((int)blockIdx.x < a.M) {
+    const int m = blockIdx.x;
+    const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.K);
+    const int nc = a.K / 8;
+    float amax = 0.0f;
+    for (int c = tid; c < nc; c += 256) {
+      const u32x4_t v = xr[c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32((uint16_t)v[e])),
+                                 fabsf(bf16_to_f32((uint16_t)(v[e] >> 16)))));
+    }
+    const int e = row_shift(block_max256(amax, red), 15);
+    if (tid == 0) a.ex[m] = e;
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(a.xh + (int64_t)m * a.K);
+    uint16_t* a2 = a.a2 + (int64_t)m * a.K2p;
+    const int cpg = a.G / 8;  // chunks per group: 4, 8 or 16 consecutive lanes
+    for (int c = tid; c < nc; c += 256) {
+      const u32x4_t v = xr[c];
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = bf16_to_f32((uint16_t)v[i]);
+        f[2 * i + 1] = bf16_to_f32((uint16_t)(v[i] >> 16));
+      }
+      u32x4_t o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)f32_to_f16(ldexpf(f[i], -e)) |
+               ((uint32_t)f32_to_f16(ldexpf(f[i + 4], -e)) << 16);
+      dst[c] = o;
+      float s = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+      for (int o2 = 1; o2 < cpg; o2 <<= 1) s += __shfl_xor(s, o2);
+      if ((c & (cpg - 1)) == 0) {
+        const int g = c / cpg;
+        uint16_t hi, lo;
+        split_bf16(s, hi, lo);
+        a2[3 * g] = hi;
+        a2[3 * g + 1] = hi;
+        a2[3 * g + 2] = lo;
+      }
+    }
+    for (int sl = 3 * ng + tid; sl < a.K2p; sl += 256) a2[sl] = 0;
+    return;
+  }
+  const int n = 4 * ((int)blockIdx.x - a.M) + (tid >> 6);
+  if (n >= a.N) return;
+  const uint16_t* sr = a.sc + (int64_t)n * ng;
+  const uint16_t* br = a.bi + (int64_t)n * ng;
+  float smax = 0.0f;
+  for (int g = lane; g < ng; g += 64) smax = fmaxf(smax, fabsf(bf16_to_f32(sr[g])));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) smax = fmaxf(smax, __shfl_xor(smax, o));
+  const int e = row_shift(smax, 12);
+  if (lane == 0) a.es[n] = e;
+  uint16_t* spr = a.sp + (int64_t)n * ng;
+  uint16_t* b2 = a.b2 + (int64_t)n * a.K2p;
+  for (int g = lane; g < ng; g += 64) {
+    const float s = bf16_to_f32(sr[g]);
+    spr[g] = f32_to_f16(ldexpf(s, -e));
+    uint16_t hi, lo;
+    split_bf16(fmaf(8.0f, s, bf16_to_f32(br[g])), hi, lo);
+    b2[3 * g] = hi;
+    b2[3 * g + 1] = lo;
+    b2[3 * g + 2] = hi;
+  }
+  for (int sl = 3 * ng + lane; sl < a.K2p; sl += 64) b2[sl] = 0;
+}
+
+struct GemmX16Args {
+  const uint16_t* xh;  // [M][K] fp16 from the prologue
+  const uint32_t* w;   // [N][K/8]
+  const uint16_t* sp;  // [N][K/G] fp16
+  const int* ex;       // [M]
+  const int* es;       // [N]
+  const uint16_t* a2;  // [M][K2p]
+  const uint16_t* b2;  // [N][K2p]
+  void* y;
+  int y_dtype, M, N, K, K2p;
+};
+
+template <int G>
+__global__ __launch_bounds__(256, 2) void w4_gemm_x16_kernel(GemmX16Args a) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM * kBK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kBN * kBK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
+  const int K = a.K, ng = K / G, nsteps = K / kBK;
+  const int mrows = min(kBM, a.M - m0), nrows = min(kBN, a.N - n0);
+  // rows past the tile's last one read as zero
+  const rsrc_t rx = make_rsrc(a.xh + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 2u);
+  const rsrc_t rw = make_rsrc(a.w + (int64_t)n0 * (K / 8), (uint32_t)nrows * (uint32_t)K / 2u);
+  const rsrc_t rs = make_rsrc(a.sp + (int64_t)n0 * ng, (uint32_t)(nrows * ng) * 2u);
+  const uint32_t mask = vgpr_const(0x000F000Fu), magic = vgpr_const(0x64006400u);
+
+  u32x4_t ra[4], rb;
+  uint32_t rsv;
+  auto load = [&](int step) {
+    const int k0 = step * kBK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i, row = p >> 3, kc = p & 7;
+      ra[i] = buf_load16(rx, (uint32_t)(row * K + k0 + kc * 8) * 2u);
+    }
+    const int row = tid >> 1, half = tid & 1;
+    rb = buf_load16(rw, (uint32_t)(row * (K / 2) + k0 / 2 + 16 * half));
+    rsv = buf_load2(rs, (uint32_t)(row * ng + (k0 + 32 * half) / G) * 2u);
+  };
+  auto store = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + 256 * i, row = p >> 3, kc = p & 7;
+      *reinterpret_cast<u32x4_t*>(&As[st][tile_off(row, kc)]) = ra[i];
+    }
+    const int row = tid >> 1, half = tid & 1;
+    const f16x2_t s2 = __builtin_bit_cast(f16x2_t, rsv | (rsv << 16));
+    const f16x2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+      const uint32_t w = rb[wi];
+      u32x4_t o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t t = ((w >> (4 * i)) & mask) | magic;
+        o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2_t, t) - off) * s2);
+      }
+      *reinterpret_cast<u32x4_t*>(&Bs[st][tile_off(row, 4 * half + wi)]) = o;
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16_t{};
+
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int step = 0; step < nsteps; ++step) {
+    const int st = step & 1;
+    if (step + 1 < nsteps) load(step + 1);
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+      const int kc = 2 * ss + j;
+      u32x4_t af[2], bf[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        af[t] = *reinterpret_cast<const u32x4_t*>(&As[st][tile_off(wm * 64 + t * 32 + (lane & 31), kc)]);
+        bf[t] = *reinterpret_cast<const u32x4_t*>(&Bs[st][tile_off(wn * 64 + t * 32 + (lane & 31), kc)]);
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) acc[x][y] = mfma32x32x16<F16>(af[x], bf[y], acc[x][y]);
+    }
+    if (step + 1 < nsteps) store(st ^ 1);
+    __syncthreads();
+  }
+
+  // undo the row shifts: y = 2^(ex[m] + es[n]) * acc
+  const rsrc_t rex = make_rsrc(a.ex + m0, (uint32_t)mrows * 4u);
+  const rsrc_t res = make_rsrc(a.es + n0, (uint32_t)nrows * 4u);
+#pragma unroll
+  for (int y = 0; y < 2; ++y) {
+    const int esn = (int)__builtin_amdgcn_raw_buffer_load_b32(
+        res, (wn * 64 + y * 32 + (lane & 31)) * 4, 0, 0);
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const u32x4_t e4 = buf_load16(rex, (uint32_t)(wm * 64 + x * 32 + 8 * q4 + 4 * j) * 4u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[x][y][4 * q4 + r] = ldexpf(acc[x][y][4 * q4 + r], (int)e4[r] + esn);
+      }
+  }
+  // bias slots: acc += A2 * B2^T on the bf16 MFMA
+  const int K2p = a.K2p;
+  const rsrc_t ra2 = make_rsrc(a.a2 + (int64_t)m0 * K2p, (uint32_t)mrows * (uint32_t)K2p * 2u);
+  const rsrc_t rb2 = make_rsrc(a.b2 + (int64_t)n0 * K2p, (uint32_t)nrows * (uint32_t)K2p * 2u);
+  for (int ks = 0; ks < K2p; ks += 16) {
+    u32x4_t af[2], bf[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      af[t] = buf_load16(ra2, (uint32_t)((wm * 64 + t * 32 + (lane & 31)) * K2p + ks + 8 * j) * 2u);
+      bf[t] = buf_load16(rb2, (uint32_t)((wn * 64 + t * 32 + (lane & 31)) * K2p + ks + 8 * j) * 2u);
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) acc[x][y] = mfma32x32x16<BF16>(af[x], bf[y], acc[x][y]);
+  }
+
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int gn = n0 + wn * 64 + y * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gm = m0 + wm * 64 + x * 32 + mfma32_row(lane, v);
+        if (gm < a.M && gn < a.N) store_out(a.y, (int64_t)gm * a.N + gn, acc[x][y][v], a.y_dtype);
+      }
+    }
+}
+
 template <typename T, int G>
 __global__ __launch_bounds__(256, 2) void w4_gemm_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
@@ -969,6 +1251,24 @@ static void launch_gemv(const GemvPlan& p, int G, const GemvArgs& a, hipStream_t
     launch_gemv_g<T, 128>(p, a, st);
 }
 
+// Workspace of the bf16 GEMM after the counter block: the prologue's
+// scaled fp16 activations, row shifts, scaled scales and bias slots.
+struct GemmX16Layout {
+  size_t xh, ex, a2, sp, es, b2, bytes;
+};
+static GemmX16Layout gemm_x16_layout(int64_t M, int64_t N, int64_t K, int G) {
+  const int64_t ng = K / G, k2p = bias_slots((int)K, G);
+  GemmX16Layout l;
+  l.xh = 0;
+  l.ex = l.xh + round_up((size_t)(M * K * 2), 256);
+  l.a2 = l.ex + round_up((size_t)(M * 4), 256);
+  l.sp = l.a2 + round_up((size_t)(M * k2p * 2), 256);
+  l.es = l.sp + round_up((size_t)(N * ng * 2), 256);
+  l.b2 = l.es + round_up((size_t)(N * 4), 256);
+  l.bytes = l.b2 + round_up((size_t)(N * k2p * 2), 256);
+  return l;
+}
+
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
   if (plan_gemv(M, N, K, G).ok) return 0;
@@ -978,7 +1278,8 @@ size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
     const SkinnyPlan p = plan_skinny(M, N, K);
     return p.S > 1 ? kCounterBytes + p.part_bytes : 0;
   }
-  return kCounterBytes + round_up((size_t)(K / G) * M * 4, 256);
+  const GemmX16Layout l = gemm_x16_layout(M, N, K, G);
+  return kCounterBytes + std::max(round_up((size_t)(K / G) * M * 4, 256), l.bytes);
 }
 
 template <typename T, int G, int MB, int CPW>
@@ -1038,6 +1339,49 @@ static void launch_gemm(int G, const void* x, const uint32_t* w, const void* s,
 #undef SPARKQ_GEMM
 }
 
+static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void* s,
+                            const void* b, unsigned char* ws, void* y, int ydt, int M, int N,
+                            int K, hipStream_t st) {
+  const GemmX16Layout l = gemm_x16_layout(M, N, K, G);
+  GemmPrepArgs p{};
+  p.x = (const uint16_t*)x;
+  p.sc = (const uint16_t*)s;
+  p.bi = (const uint16_t*)b;
+  p.xh = reinterpret_cast<uint16_t*>(ws + l.xh);
+  p.ex = reinterpret_cast<int*>(ws + l.ex);
+  p.a2 = reinterpret_cast<uint16_t*>(ws + l.a2);
+  p.sp = reinterpret_cast<uint16_t*>(ws + l.sp);
+  p.es = reinterpret_cast<int*>(ws + l.es);
+  p.b2 = reinterpret_cast<uint16_t*>(ws + l.b2);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.G = G;
+  p.K2p = bias_slots(K, G);
+  hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)(M + cdiv(N, 4))), dim3(256), 0, st, p);
+  GemmX16Args a{};
+  a.xh = p.xh;
+  a.w = w;
+  a.sp = p.sp;
+  a.ex = p.ex;
+  a.es = p.es;
+  a.a2 = p.a2;
+  a.b2 = p.b2;
+  a.y = y;
+  a.y_dtype = ydt;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.K2p = p.K2p;
+  dim3 grid((unsigned)cdiv(N, kBN), (unsigned)cdiv(M, kBM));
+  if (G == 32)
+    hipLaunchKernelGGL(w4_gemm_x16_kernel<32>, grid, dim3(256), 0, st, a);
+  else if (G == 64)
+    hipLaunchKernelGGL(w4_gemm_x16_kernel<64>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(w4_gemm_x16_kernel<128>, grid, dim3(256), 0, st, a);
+}
+
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
                  void* y, int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt,
                  void* ws, size_t wsb, hipStream_t st) {
@@ -1095,7 +1439,12 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
       launch_skinny<F16>(p, G, a, st);
     return check_launch("w4_skinny_kernel");
   }
-  float* xs = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
+  unsigned char* wsp = reinterpret_cast<unsigned char*>(ws) + kCounterBytes;
+  if (xdt == SPARKQ_BF16 && !env_int("SPARKQ_W4_NO_X16", 0)) {
+    launch_gemm_x16(G, x, w, s, b, wsp, y, ydt, (int)M, (int)N, (int)K, st);
+    return check_launch("w4_gemm_x16_kernel");
+  }
+  float* xs = reinterpret_cast<float*>(wsp);
   if (xdt == SPARKQ_BF16)
     launch_gemm<BF16>(G, x, w, s, b, xs, y, ydt, (int)M, (int)N, (int)K, st);
   else

@@ -118,6 +118,42 @@ def test_decode_ragged_shapes(gpu, m, n, k, g):
     check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
 
 
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_gemm_row_shifts(gpu, g):
+    """The bf16 GEMM runs on fp16 operands after per-row power-of-two shifts
+    of the activations and of the scales. Rows far outside the fp16 range in
+    either direction, an all-zero row, a row of zero scales and a row whose
+    scales span 2^20 must keep the fp32 dot-product error bound: |err| <=
+    2^-14 * sum_k |x_k| * (|w_k| + 8|s_g(k)|) per element."""
+    m, n, k = 40, 72, 512
+    x, wq, s, b = w4_problem(m, n, k, g, seed=g)
+    xf = o.bits_to_f32(x, o.BF16).copy()
+    xf[0] *= 2.0 ** 40
+    xf[1] *= 2.0 ** -60
+    xf[2] = 0.0
+    xf[3, ::7] *= 2.0 ** 30
+    sf, bf = o.bits_to_f32(s, o.BF16).copy(), o.bits_to_f32(b, o.BF16).copy()
+    sf[0] *= 2.0 ** -40
+    bf[0] *= 2.0 ** -40
+    sf[1] *= 2.0 ** 40
+    bf[1] *= 2.0 ** 40
+    sf[2] = 0.0
+    sf[3, 1] *= 2.0 ** 20
+    x, s, b = o.round16(xf, o.BF16), o.round16(sf, o.BF16), o.round16(bf, o.BF16)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy().astype(np.float64)
+    xa = np.abs(o.bits_to_f32(x, o.BF16).astype(np.float64))
+    deq = np.abs(o.w4_dequantize(wq, s, b, g).astype(np.float64))
+    s8 = np.repeat(8.0 * np.abs(o.bits_to_f32(s, o.BF16).astype(np.float64)), g, axis=1)
+    bound = 2.0 ** -14 * (xa @ (deq + s8).T)
+    err = np.abs(y - ref)
+    assert np.isfinite(y).all()
+    worst = float(np.max(err / np.maximum(bound, 1e-300)))
+    print(f"worst err/bound = {worst:.3e}")
+    assert (err <= bound).all(), worst
+    assert np.all(y[2] == 0.0)
+
+
 def test_one_hot_rows_pick_weight_columns(gpu):
     import sparkq
 
