@@ -27,6 +27,7 @@
 //   w4_gemm_kernel      fp16, M > 32: 128x128x64 LDS tiles (B decoded to the
 //                       exact q), per-group fp32 scale and bias epilogue
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <cstdlib>
 
@@ -695,12 +696,12 @@ __device__ __forceinline__ int tile_off(int row, int kc) {
 // products that are exact in fp32:
 //  * s*(q-8) is a bf16 significand (8 bits) times |q-8| <= 8: at most 11
 //    significant bits, exact in fp16. A per-row power of two 2^-es[n] brings
-//    max_g |s[n,g]| into [2^12, 2^13), so |s'*(q-8)| <= 65280 stays finite.
+//    max_g |s[n,g]| into [2^10, 2^11), so |s'*(q-8)| and |24*s'| stay finite.
 //    Activations scale the same way per row, 2^-ex[m] putting max_k |x[m,k]|
 //    into [2^15, 2^16). The fp16 MFMA then accumulates exact products and the
 //    epilogue multiplies by 2^(ex[m]+es[n]) (an exponent add). The only
 //    rounding this adds is for values below 2^-24 after the shift (fp16
-//    subnormals): scales under 2^-30 of their row's largest and activations
+//    subnormals): scales under 2^-27 of their row's largest and activations
 //    under 2^-39 of theirs.
 //  * the bias part is a GEMM over K2 = 3*K/G "bias slots" on the bf16 MFMA,
 //    with both factors split into bf16 pairs so that the three products
@@ -804,7 +805,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
   for (int g = lane; g < ng; g += 64) smax = fmaxf(smax, fabsf(bf16_to_f32(sr[g])));
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) smax = fmaxf(smax, __shfl_xor(smax, o));
-  const int e = row_shift(smax, 12);
+  const int e = row_shift(smax, 10);
   if (lane == 0) a.es[n] = e;
   uint16_t* spr = a.sp + (int64_t)n * ng;
   uint16_t* b2 = a.b2 + (int64_t)n * a.K2p;
@@ -957,6 +958,193 @@ __global__ __launch_bounds__(256, 2) void w4_gemm_x16_kernel(GemmX16Args a) {
       for (int v = 0; v < 16; ++v) {
         const int gm = m0 + wm * 64 + x * 32 + mfma32_row(lane, v);
         if (gm < a.M && gn < a.N) store_out(a.y, (int64_t)gm * a.N + gn, acc[x][y][v], a.y_dtype);
+      }
+    }
+}
+
+// Wide variant: a 128 x (64*NWV) tile per workgroup of NWV waves, each wave
+// owning 128 rows x 64 columns. Activations go through LDS (shared by the
+// waves); each wave loads its own packed weights straight into registers and
+// decodes them there. The k order inside a 64-k step is permuted so that one
+// 16-byte load per lane covers the whole step: lane half j of sub-step ss
+// reads chunk 4j+ss (the A fragments use the same chunk), so a lane's four
+// consecutive weight words are its operands of sub-steps 0..3. Every lane
+// scales its own words, so any group size works with this order.
+//
+// Decode, three VALU ops per pair of weights: code q goes to fp16 mantissa
+// bits 9..6 under exponent 4, which reads as exactly 16+q, and one packed fma
+// (16+q)*s' + (-24*s') = s'*(q-8) is exact (the exact product sum is
+// representable, so its single rounding changes nothing). Pair i of a word
+// holds codes i and i+4, 16 bits apart, so one shift places both.
+//
+// LDS rows are 128 bytes; chunk c of row r sits at c ^ ((t ^ (t >> 3)) & 7)
+// with t = r mod 32, which keeps any 16 consecutive rows of an aligned block
+// at one chunk index on distinct banks, and repeats every 32 rows so that a
+// fragment 32*x rows further down is a constant offset away.
+__device__ __forceinline__ int atile_off(int row, int kc) {
+  const int t = row & 31;
+  return row * 64 + ((kc ^ ((t ^ (t >> 3)) & 7)) << 3);
+}
+
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <int G, int NWV>
+__global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a) {
+  constexpr int NT = 64 * NWV;
+  constexpr int AL = kBM * kBK / 8 / NT;  // 16-byte A pieces per thread per step
+  __shared__ __attribute__((aligned(16))) uint16_t As[2 * kBM * kBK];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave-uniform, so that the per-wave buffer descriptors live in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane >> 5, l32 = lane & 31;
+  const int n0 = blockIdx.x * (64 * NWV), m0 = blockIdx.y * kBM;
+  const int K = a.K, ng = K / G, nsteps = K / kBK;
+  const int mrows = min(kBM, a.M - m0);
+  const int wn0 = n0 + 64 * wave;  // this wave's first column
+  const int nrows = __builtin_amdgcn_readfirstlane(max(0, min(64, a.N - wn0)));
+  // rows past the tile's last one read as zero
+  const rsrc_t rx = make_rsrc(a.xh + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 2u);
+  const rsrc_t rw = make_rsrc(a.w + (int64_t)wn0 * (K / 8), (uint32_t)nrows * (uint32_t)K / 2u);
+  const rsrc_t rs = make_rsrc(a.sp + (int64_t)wn0 * ng, (uint32_t)(nrows * ng) * 2u);
+  const uint32_t mask = vgpr_const(0x03C003C0u), magic = vgpr_const(0x4C004C00u);
+
+  // loop-invariant per-lane offsets; the k offset of a step is a scalar
+  uint32_t xoff[AL], lds_w[AL];
+#pragma unroll
+  for (int i = 0; i < AL; ++i) {
+    const int p = tid + NT * i, row = p >> 3, kc = p & 7;
+    xoff[i] = (uint32_t)(row * K + kc * 8) * 2u;
+    lds_w[i] = (uint32_t)atile_off(row, kc) * 2u;
+  }
+  uint32_t woff[2], soff[2], lds_r[4];
+#pragma unroll
+  for (int y = 0; y < 2; ++y) {
+    const int col = 32 * y + l32;
+    woff[y] = (uint32_t)(col * (K / 2) + 16 * j);
+    soff[y] = (uint32_t)(col * ng + (G == 32 ? j : 0)) * 2u;
+  }
+#pragma unroll
+  for (int ss = 0; ss < 4; ++ss) lds_r[ss] = (uint32_t)atile_off(l32, 4 * j + ss) * 2u;
+
+  u32x4_t ra[AL], rb[2];
+  uint32_t rsv[2];
+  auto load = [&](int step) {
+    const int k0 = step * kBK;
+#pragma unroll
+    for (int i = 0; i < AL; ++i)
+      ra[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], 2 * k0, 0));
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      rb[y] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff[y], k0 / 2, 0));
+      rsv[y] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff[y], 2 * (k0 / G), 0);
+    }
+  };
+  auto lds_at = [&](uint32_t byte_off) -> u32x4_t* {
+    return reinterpret_cast<u32x4_t*>(reinterpret_cast<unsigned char*>(As) + byte_off);
+  };
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16_t{};
+
+  auto body = [&](int step, auto stc) {
+    constexpr int st = decltype(stc)::value;
+    const u32x4_t wb0 = rb[0], wb1 = rb[1];
+    const f16x2_t s0 = __builtin_bit_cast(f16x2_t, rsv[0] * 0x10001u);
+    const f16x2_t s1 = __builtin_bit_cast(f16x2_t, rsv[1] * 0x10001u);
+    const f16x2_t c0 = s0 * f16x2_t{(_Float16)-24.0f, (_Float16)-24.0f};
+    const f16x2_t c1 = s1 * f16x2_t{(_Float16)-24.0f, (_Float16)-24.0f};
+    if (step + 1 < nsteps) load(step + 1);
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+      u32x4_t bf0, bf1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sh = 6 - 4 * i;
+        const uint32_t t0 = ((sh >= 0 ? wb0[ss] << sh : wb0[ss] >> -sh) & mask) | magic;
+        const uint32_t t1 = ((sh >= 0 ? wb1[ss] << sh : wb1[ss] >> -sh) & mask) | magic;
+        bf0[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, t0), s0, c0));
+        bf1[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, t1), s1, c1));
+      }
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const u32x4_t af = *lds_at(lds_r[ss] + (uint32_t)(st * kBM * kBK * 2 + x * 32 * 128));
+        acc[x][0] = mfma32x32x16<F16>(af, bf0, acc[x][0]);
+        acc[x][1] = mfma32x32x16<F16>(af, bf1, acc[x][1]);
+      }
+    }
+    if (step + 1 < nsteps) {
+#pragma unroll
+      for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)((st ^ 1) * kBM * kBK * 2)) = ra[i];
+    }
+    __syncthreads();
+  };
+
+  load(0);
+#pragma unroll
+  for (int i = 0; i < AL; ++i) *lds_at(lds_w[i]) = ra[i];
+  __syncthreads();
+  for (int step = 0; step < nsteps; step += 2) {
+    body(step, std::integral_constant<int, 0>{});
+    if (step + 1 < nsteps) body(step + 1, std::integral_constant<int, 1>{});
+  }
+
+  // undo the row shifts: y = 2^(ex[m] + es[n]) * acc
+  const rsrc_t rex = make_rsrc(a.ex + m0, (uint32_t)mrows * 4u);
+  const rsrc_t res = make_rsrc(a.es + wn0, (uint32_t)nrows * 4u);
+#pragma unroll
+  for (int y = 0; y < 2; ++y) {
+    const int esn = (int)__builtin_amdgcn_raw_buffer_load_b32(res, (32 * y + l32) * 4, 0, 0);
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const u32x4_t e4 = buf_load16(rex, (uint32_t)(x * 32 + 8 * q4 + 4 * j) * 4u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[x][y][4 * q4 + r] = ldexpf(acc[x][y][4 * q4 + r], (int)e4[r] + esn);
+      }
+  }
+  // bias slots: acc += A2 * B2^T on the bf16 MFMA
+  const int K2p = a.K2p;
+  const rsrc_t ra2 = make_rsrc(a.a2 + (int64_t)m0 * K2p, (uint32_t)mrows * (uint32_t)K2p * 2u);
+  const rsrc_t rb2 = make_rsrc(a.b2 + (int64_t)wn0 * K2p, (uint32_t)nrows * (uint32_t)K2p * 2u);
+  for (int ks = 0; ks < K2p; ks += 16) {
+    u32x4_t bf[2];
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+      bf[y] = buf_load16(rb2, (uint32_t)((32 * y + l32) * K2p + ks + 8 * j) * 2u);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const u32x4_t af = buf_load16(ra2, (uint32_t)((32 * x + l32) * K2p + ks + 8 * j) * 2u);
+      acc[x][0] = mfma32x32x16<BF16>(af, bf[0], acc[x][0]);
+      acc[x][1] = mfma32x32x16<BF16>(af, bf[1], acc[x][1]);
+    }
+  }
+
+  const int gn0 = wn0 + l32;
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int gn = gn0 + 32 * y;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gm = m0 + 32 * x + mfma32_row(lane, v);
+        if (gm < a.M && gn < a.N) {
+          const int64_t idx = (int64_t)gm * a.N + gn;
+          if (a.y_dtype == SPARKQ_BF16)
+            reinterpret_cast<uint16_t*>(a.y)[idx] = (uint16_t)bf16x2_rne(acc[x][y][v], 0.0f);
+          else
+            store_out(a.y, idx, acc[x][y][v], a.y_dtype);
+        }
       }
     }
 }
@@ -1373,6 +1561,27 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   a.N = N;
   a.K = K;
   a.K2p = p.K2p;
+  const int wide = (int)env_int("SPARKQ_W4_WIDE", 4);
+  if (wide == 4) {
+    dim3 gw((unsigned)cdiv(N, 256), (unsigned)cdiv(M, kBM));
+    if (G == 32)
+      hipLaunchKernelGGL((w4_gemm_x16w_kernel<32, 4>), gw, dim3(256), 0, st, a);
+    else if (G == 64)
+      hipLaunchKernelGGL((w4_gemm_x16w_kernel<64, 4>), gw, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((w4_gemm_x16w_kernel<128, 4>), gw, dim3(256), 0, st, a);
+    return;
+  }
+  if (wide == 2) {
+    dim3 gw((unsigned)cdiv(N, 128), (unsigned)cdiv(M, kBM));
+    if (G == 32)
+      hipLaunchKernelGGL((w4_gemm_x16w_kernel<32, 2>), gw, dim3(128), 0, st, a);
+    else if (G == 64)
+      hipLaunchKernelGGL((w4_gemm_x16w_kernel<64, 2>), gw, dim3(128), 0, st, a);
+    else
+      hipLaunchKernelGGL((w4_gemm_x16w_kernel<128, 2>), gw, dim3(128), 0, st, a);
+    return;
+  }
   dim3 grid((unsigned)cdiv(N, kBN), (unsigned)cdiv(M, kBM));
   if (G == 32)
     hipLaunchKernelGGL(w4_gemm_x16_kernel<32>, grid, dim3(256), 0, st, a);

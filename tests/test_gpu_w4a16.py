@@ -171,6 +171,26 @@ def test_one_hot_rows_pick_weight_columns(gpu):
     assert torch.equal(sparkq.w4a16_qmv(xt, *args), _run(gpu, o.bf16_bits(x[:1]), wq, s, b, g, o.BF16))
 
 
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_gemm_one_hot_rows_pick_weight_columns(gpu, g):
+    """M > 32 takes the bf16 GEMM. A one-hot activation row picks one column
+    of the dequantized weights: the s*(q-8) part is exact, so the only error
+    left is the bf16-pair split of the bias b + 8s, under 2^-15 |b + 8s|."""
+    n, k, m = 300, 1024, 64
+    _, wq, s, b = w4_problem(1, n, k, g, seed=21 + g)
+    ks = np.random.default_rng(g).choice(k, m, replace=False)
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), ks] = 1.0
+    y = _run(gpu, o.bf16_bits(x), wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    deq = o.w4_dequantize(wq, s, b, g).astype(np.float64)
+    ref = deq[:, ks].T
+    sf = o.bits_to_f32(s, o.BF16).astype(np.float64)[:, ks // g].T
+    bf = o.bits_to_f32(b, o.BF16).astype(np.float64)[:, ks // g].T
+    err = np.abs(y - ref)
+    bound = 2.0 ** -15 * np.abs(bf + 8.0 * sf)
+    assert (err <= bound).all(), float(np.max(err - bound))
+
+
 def test_deterministic(gpu):
     x, wq, s, b = w4_problem(4, 512, 2560, 64, seed=11)
     a = _run(gpu, x, wq, s, b, 64, o.BF16, out_dtype=torch.float32)
