@@ -240,19 +240,25 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   const int nsp = (R * ng) >> 3;               // 16-byte scale pieces of the workgroup
   u32x4_t xr[kGemvXP][4];
   u32x4_t sr[kGemvSP], br[kGemvSP];
+  // a wave with no piece to fetch skips the instruction (the texture unit
+  // charges per instruction, lanes or not); the condition is wave-uniform
 #pragma unroll
   for (int i = 0; i < kGemvXP; ++i) {
     const int pi = tid + i * NT;
-    const uint32_t off = pi < nxp ? 64u * pi : kOob;
+    if (i * NT + 64 * wave < nxp) {
+      const uint32_t off = pi < nxp ? 64u * pi : kOob;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
+      for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
+    }
   }
 #pragma unroll
   for (int i = 0; i < kGemvSP; ++i) {
     const int pi = tid + i * NT;
-    const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
-    sr[i] = buf_load16(rs, off);
-    br[i] = buf_load16(rb, off);
+    if (i * NT + 64 * wave < nsp) {
+      const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
+      sr[i] = buf_load16(rs, off);
+      br[i] = buf_load16(rb, off);
+    }
   }
 
   // 2. the wave's weights: RQW row quads x US spans
@@ -1349,8 +1355,9 @@ static SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K) {
 
 // Decode GEMV plan. A row has U = ceil(K/512) spans; a wave keeps at most 5
 // spans of activations in registers, so rows of up to 20 spans (K <= 10240)
-// split into SG = 1, 2 or 4 span groups. Workgroups of 4 waves (8 when
-// SG = 4) cover R = 4 * (waves / SG) * RQW rows; two row quads per wave once
+// split into SG = 1, 2 or 4 span groups. Workgroups of 4 waves (8 when the
+// activations need the larger staging budget) cover R = 4 * (waves / SG) *
+// RQW rows; two row quads per wave once
 // that still leaves >= 2048 waves. The staged activations, (scale, bias)
 // pieces and LDS must fit the kernel's fixed budgets, and the scale tensors
 // must end on a 16-byte boundary (they are staged in 16-byte loads).
@@ -1379,9 +1386,14 @@ static GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int G) {
     return p;
   p.USr = (int)cdiv(U, p.SG);
   p.US = p.USr <= 1 ? 1 : (p.USr <= 2 ? 2 : 5);
-  p.NW = p.SG == 4 ? 8 : 4;
+  // 4 waves: three workgroups fit a CU, so the whole grid is resident at
+  // once (8-wave workgroups fit one per CU and ran long rows in two rounds);
+  // 8 only when the activations need the larger staging budget
+  p.NW = M * (K / 32) > kGemvXP * 256 ? 8 : 4;
+  if (env_int("SPARKQ_W4_GEMV_NW", 0)) p.NW = env_int("SPARKQ_W4_GEMV_NW", 4) == 8 ? 8 : 4;
   const int64_t nq = cdiv(N, 4);
   p.RQW = cdiv(nq, 2) * p.SG >= 2048 ? 2 : 1;
+  if (env_int("SPARKQ_W4_GEMV_RQW", 0)) p.RQW = env_int("SPARKQ_W4_GEMV_RQW", 1) == 2 ? 2 : 1;
   p.MQ = M == 1 ? 1 : 4;
   p.R = 4 * (p.NW / p.SG) * p.RQW;
   const int64_t nt = 64 * p.NW;
