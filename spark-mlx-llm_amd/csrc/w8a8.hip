@@ -254,7 +254,8 @@ __global__ __launch_bounds__(64 * NW) void i8_gemv_kernel(I8GemvArgs a) {
 #pragma unroll
   for (int i = 0; i < kI8XP; ++i) {
     const int pi = tid + i * NT;
-    xr[i] = buf_load16(rx, pi < nxp ? 16u * pi : kOob);
+    // waves with no piece skip the instruction (wave-uniform condition)
+    if (i * NT + 64 * wave < nxp) xr[i] = buf_load16(rx, pi < nxp ? 16u * pi : kOob);
   }
   // 2. the wave's weights: one row quad x US spans
   u32x4_t wv[US];
