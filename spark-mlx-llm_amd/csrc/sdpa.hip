@@ -15,8 +15,13 @@
 //                       Slots merge by shuffles, waves through LDS, and the
 //                       workgroup writes either the final output (one split)
 //                       or its (max, sum, acc) partial.
+//   sdpa_mfma_kernel    the s8 + fp16-scale format with a 16-bit query: both
+//                       products on the fp16 MFMA (see its comment)
 //   sdpa_merge_kernel   log-sum-exp merge of the split partials.
 //   kv_quantize_s8_kernel  s8 + fp16-scale quantizer (one wave per row).
+#include <algorithm>
+#include <type_traits>
+
 #include "common.h"
 
 namespace sparkq {
@@ -226,24 +231,357 @@ __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA decode attention for the symmetric s8 + fp16-scale format
+// ---------------------------------------------------------------------------
+// A workgroup (4 waves) owns one (sequence, KV head) and one split of the
+// context; each wave walks blocks of 32 tokens with 16-byte loads. Both
+// products run on v_mfma_f32_16x16x32_f16, with the GQA query heads as the
+// (zero-padded) 16-row side:
+//  * QK: A = the query heads, B = 16 tokens x 32 dims of K. The int8 codes
+//    become exact fp16 values 1152 + k with one byte permute and one xor
+//    under the fp16 1024 pattern (code ^ 0x80 = k + 128); the 1152 * sum(q)
+//    the offset adds is subtracted in fp32. The query is shifted per head by
+//    a power of two so that it is an exact fp16 operand.
+//  * PV: A = p * v_scale over 32 tokens as an fp16 hi/lo pair (two MFMAs,
+//    ~22 significant bits), transposed to head-major through per-wave LDS
+//    strips; B = 16 dims x 32 tokens of V, read from an
+//    LDS copy of the block with ds_read_b64_tr_b8 (the 8 bytes of a lane are
+//    one dim of 8 consecutive tokens) and decoded like K; the 1152 offset is
+//    removed with the running sum of the fp16 weights.
+// Online softmax in the log2 domain: a block max across the 16 token lanes,
+// per-lane partial sums reduced once at the end. Waves combine through LDS;
+// the workgroup writes the output (one split) or its (max, sum, acc) partial.
+__device__ __forceinline__ u32x4_t s8x8_to_f16(uint32_t lo, uint32_t hi) {
+  // bytes b0..b7 -> fp16 pairs (1152 + b0, 1152 + b1), ... in byte order
+  const uint32_t m = 0x64806480u;
+  return u32x4_t{__builtin_amdgcn_perm(0u, lo, 0x0C010C00u) ^ m,
+                 __builtin_amdgcn_perm(0u, lo, 0x0C030C02u) ^ m,
+                 __builtin_amdgcn_perm(0u, hi, 0x0C010C00u) ^ m,
+                 __builtin_amdgcn_perm(0u, hi, 0x0C030C02u) ^ m};
+}
+
+__device__ __forceinline__ f32x4_t mfma16x16x32_f16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <int D>
+struct SdpaMfmaLds {
+  static constexpr int VROW = D + 16;                 // padded token row of the V copy
+  static constexpr int VT = 32 * VROW;                // one wave's V block
+  static constexpr int PT = 2 * 16 * 32 * 2;          // one wave's P strips (hi, lo) [16 heads][32 tokens] fp16
+  static constexpr int LOOP = 4 * (VT + PT);
+  static constexpr int MERGE = 4 * 8 * 4 * 2 + 4 * 8 * D * 4;
+  static constexpr int BYTES = LOOP > MERGE ? LOOP : MERGE;
+};
+
+template <int D, int GQA>
+__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaArgs a) {
+  constexpr int NC = D / 32;   // k chunks of QK
+  constexpr int PL = D / 64;   // 16-byte K pieces per lane per 16-token group
+  constexpr int NJ = D / 16;   // 16-dim column groups of PV
+  constexpr int VL = D / 32;   // 16-byte V pieces per lane per block
+  using L = SdpaMfmaLds<D>;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[L::BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, grp = lane >> 4;
+  const int split = blockIdx.x;
+  const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
+  const int t_begin = split * a.tps;
+  const int t_end = min(a.N, t_begin + a.tps);
+  unsigned char* vtile = smem + wave * L::VT;
+  uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + 4 * L::VT + wave * L::PT);
+
+  // query operand: lane (head n16, k quarter grp); chunk c covers dims
+  // 16*(grp + 4*(c/2)) + 8*(c%2) .. +8, matching the K piece order below
+  u32x4_t qa[NC];
+  float qmax = 0.0f, qs = 0.0f;
+  {
+    const int h = n16;
+    float qv[NC][8];
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) +
+                           ((int64_t)b * a.Hq + kh * GQA + min(h, GQA - 1)) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d0 = 16 * (grp + 4 * (c >> 1)) + 8 * (c & 1);
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(qrow + d0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t bits = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+        const float v = a.q_dtype == SPARKQ_BF16 ? bf16_to_f32(bits) : f16_to_f32(bits);
+        qv[c][i] = h < GQA ? v : 0.0f;
+        qmax = fmaxf(qmax, fabsf(qv[c][i]));
+      }
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    const int e = (qmax > 0.0f && qmax <= 3.4028235e38f) ? ilogbf(qmax) - 14 : 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const _Float16 lo = (_Float16)ldexpf(qv[c][2 * i], -e), hi = (_Float16)ldexpf(qv[c][2 * i + 1], -e);
+        qs += (float)lo + (float)hi;
+        qa[c][i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
+    }
+    qs += __shfl_xor(qs, 16);
+    qs += __shfl_xor(qs, 32);
+    qmax = ldexpf(a.scale_log2, e);  // reused: per-head score multiplier
+  }
+  // score lanes: head 4*grp + r, token n16 (+16 for the second token group)
+  float qcorr[4], qmul[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * grp + r;
+    qcorr[r] = 1152.0f * __shfl(qs, h & 15);
+    qmul[r] = __shfl(qmax, h & 15);
+  }
+
+  // P strip rows past GQA stay zero
+  for (int i = lane; i < 2 * 16 * 32; i += 64)
+    if ((i & 511) / 32 >= GQA) pstrip[i] = 0;
+
+  const rsrc_t rk = make_rsrc(a.kc + b * a.kc_b + kh * a.kc_h, (uint32_t)(t_end * a.kc_t));
+  const rsrc_t rv = make_rsrc(a.vc + b * a.vc_b + kh * a.vc_h, (uint32_t)(t_end * a.vc_t));
+  const rsrc_t rks = make_rsrc(reinterpret_cast<const uint16_t*>(a.ks) + b * a.ks_b + kh * a.ks_h,
+                               (uint32_t)(t_end * a.ks_t * 2));
+  const rsrc_t rvs = make_rsrc(reinterpret_cast<const uint16_t*>(a.vs) + b * a.vs_b + kh * a.vs_h,
+                               (uint32_t)(t_end * a.vs_t * 2));
+
+  // block registers, two sets (the next two blocks are in flight while one
+  // is computed): K pieces [token group][piece], V pieces, one scale
+  u32x4_t kr[2][2][PL], vr[2][VL];
+  uint32_t sr[2];
+  auto load = [&](int set, int t0) {
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        kr[set][g2][i] = buf_load16(rk, (uint32_t)((t0 + 16 * g2 + n16) * a.kc_t + 16 * (grp + 4 * i)));
+#pragma unroll
+    for (int v = 0; v < VL; ++v) {
+      const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
+      vr[set][v] = buf_load16(rv, (uint32_t)((t0 + tok) * a.vc_t + 16 * pc));
+    }
+    sr[set] = lane < 32 ? buf_load2(rks, (uint32_t)((t0 + lane) * a.ks_t * 2))
+                        : buf_load2(rvs, (uint32_t)((t0 + lane - 32) * a.vs_t * 2));
+  };
+
+  float mrun[4], zl[4], psl[4];
+  f32x4_t acc[NJ];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mrun[r] = kNegInf;
+    zl[r] = 0.0f;
+    psl[r] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int stride = 4 * 32;
+  auto block = [&](int t0, auto setc) {
+    constexpr int set = decltype(setc)::value;
+    // this block's data, then the loads of the block two ahead into its set
+    u32x4_t kb[2][PL], vb[VL];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int i = 0; i < PL; ++i) kb[g2][i] = kr[set][g2][i];
+#pragma unroll
+    for (int v = 0; v < VL; ++v) vb[v] = vr[set][v];
+    const uint32_t sb = sr[set];
+    if (t0 + 2 * stride < t_end) load(set, t0 + 2 * stride);
+    // V block to this wave's LDS copy (padded rows)
+#pragma unroll
+    for (int v = 0; v < VL; ++v) {
+      const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
+      *reinterpret_cast<u32x4_t*>(vtile + tok * L::VROW + 16 * pc) = vb[v];
+    }
+
+    // scores: 2 token groups x NC chunks
+    f32x4_t sc[2];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      sc[g2] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const u32x4_t kp = kb[g2][c >> 1];
+        const u32x4_t kf = (c & 1) ? s8x8_to_f16(kp.z, kp.w) : s8x8_to_f16(kp.x, kp.y);
+        sc[g2] = mfma16x16x32_f16(qa[c], kf, sc[g2]);
+      }
+    }
+    const float ksc0 = f16_to_f32((uint16_t)__shfl(sb, n16));
+    const float ksc1 = f16_to_f32((uint16_t)__shfl(sb, 16 + n16));
+    const float vsc0 = f16_to_f32((uint16_t)__shfl(sb, 32 + n16));
+    const float vsc1 = f16_to_f32((uint16_t)__shfl(sb, 48 + n16));
+    const bool ok0 = t0 + n16 < t_end, ok1 = t0 + 16 + n16 < t_end;
+
+    float alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float s0 = ok0 ? (sc[0][r] - qcorr[r]) * ksc0 * qmul[r] : kNegInf;
+      const float s1 = ok1 ? (sc[1][r] - qcorr[r]) * ksc1 * qmul[r] : kNegInf;
+      float mb = fmaxf(s0, s1);
+      mb = fmaxf(mb, __shfl_xor(mb, 1));
+      mb = fmaxf(mb, __shfl_xor(mb, 2));
+      mb = fmaxf(mb, __shfl_xor(mb, 4));
+      mb = fmaxf(mb, __shfl_xor(mb, 8));
+      mb = fmaxf(mb, mrun[r]);
+      alpha[r] = exp2_guarded(mrun[r] - mb, mrun[r] != kNegInf);
+      mrun[r] = mb;
+      const float p0 = exp2_guarded(s0 - mb, ok0), p1 = exp2_guarded(s1 - mb, ok1);
+      const float f0 = p0 * vsc0, f1 = p1 * vsc1;
+      const _Float16 w0 = (_Float16)f0, w1 = (_Float16)f1;
+      const _Float16 u0 = (_Float16)(f0 - (float)w0), u1 = (_Float16)(f1 - (float)w1);
+      zl[r] = fmaf(zl[r], alpha[r], p0 + p1);
+      psl[r] = fmaf(psl[r], alpha[r], ((float)w0 + (float)u0) + ((float)w1 + (float)u1));
+      const int h = 4 * grp + r;
+      if (h < GQA) {
+        pstrip[h * 32 + n16] = __builtin_bit_cast(uint16_t, w0);
+        pstrip[h * 32 + 16 + n16] = __builtin_bit_cast(uint16_t, w1);
+        pstrip[512 + h * 32 + n16] = __builtin_bit_cast(uint16_t, u0);
+        pstrip[512 + h * 32 + 16 + n16] = __builtin_bit_cast(uint16_t, u1);
+      }
+    }
+    // PV: A = P strip row n16, tokens 8*grp .. +8
+    const u32x4_t pa = *reinterpret_cast<const u32x4_t*>(pstrip + n16 * 32 + 8 * grp);
+    const u32x4_t pl = *reinterpret_cast<const u32x4_t*>(pstrip + 512 + n16 * 32 + 8 * grp);
+    const unsigned char* vaddr = vtile + (8 * grp + (n16 >> 1)) * L::VROW + 8 * (n16 & 1);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      acc[j][0] *= alpha[0];
+      acc[j][1] *= alpha[1];
+      acc[j][2] *= alpha[2];
+      acc[j][3] *= alpha[3];
+      typedef int v2i_t __attribute__((ext_vector_type(2)));
+      const v2i_t t8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (__attribute__((address_space(3))) v2i_t*)(vaddr + 16 * j));
+      const u32x4_t vf = s8x8_to_f16((uint32_t)t8.x, (uint32_t)t8.y);
+      acc[j] = mfma16x16x32_f16(pa, vf, acc[j]);
+      acc[j] = mfma16x16x32_f16(pl, vf, acc[j]);
+    }
+  };
+  int t0 = t_begin + 32 * wave;
+  if (t0 < t_end) load(0, t0);
+  if (t0 + stride < t_end) load(1, t0 + stride);
+  for (; t0 < t_end; t0 += 2 * stride) {
+    block(t0, std::integral_constant<int, 0>{});
+    if (t0 + stride < t_end) block(t0 + stride, std::integral_constant<int, 1>{});
+  }
+
+  // per-lane partial sums -> the 16 token lanes of each head group
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      zl[r] += __shfl_xor(zl[r], o);
+      psl[r] += __shfl_xor(psl[r], o);
+    }
+  }
+
+  // combine the waves through LDS (the loop's LDS is free after the barrier)
+  __syncthreads();
+  float* wm = reinterpret_cast<float*>(smem);            // [4][8]
+  float* wz = wm + 32;                                   // [4][8]
+  float* wacc = wz + 32;                                 // [4][8][D]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * grp + r;
+    if (h < GQA) {
+      if (n16 == 0) {
+        wm[wave * 8 + h] = mrun[r];
+        wz[wave * 8 + h] = zl[r];
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) wacc[(wave * 8 + h) * D + 16 * j + n16] = acc[j][r] - 1152.0f * psl[r];
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < GQA * D; e += 256) {
+    const int h = e / D, d = e - h * D;
+    float mm = kNegInf;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mm = fmaxf(mm, wm[w * 8 + h]);
+    float z = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float wt = exp2_guarded(wm[w * 8 + h] - mm, wm[w * 8 + h] != kNegInf);
+      z = fmaf(wz[w * 8 + h], wt, z);
+      o = fmaf(wacc[(w * 8 + h) * D + d], wt, o);
+    }
+    const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
+    if (a.S == 1) {
+      store_out(a.out, bh * D + d, z > 0.0f ? o / z : 0.0f, a.out_dtype);
+    } else {
+      a.pacc[(bh * a.S + split) * D + d] = o;
+      if (d == 0) {
+        a.pm[bh * a.S + split] = mm;
+        a.pz[bh * a.S + split] = z;
+      }
+    }
+  }
+}
+
+// Log-sum-exp merge of the split partials of one (sequence, query head) row:
+// the split maxima and sums reduce across the workgroup, then thread
+// (d, part) sums the weighted partial outputs of every 256/D-th split with
+// eight loads in flight.
 __global__ __launch_bounds__(256) void sdpa_merge_kernel(const float* __restrict__ pm,
                                                          const float* __restrict__ pz,
                                                          const float* __restrict__ pacc,
                                                          void* __restrict__ out, int out_dtype,
                                                          int S, int D) {
+  __shared__ float wts[1024];
+  __shared__ float red[8];
+  __shared__ float part[256];
   const int64_t bh = blockIdx.x;
-  const int d = threadIdx.x;
-  if (d >= D) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // 1. global max over the splits
   float mm = kNegInf;
-  for (int s = 0; s < S; ++s) mm = fmaxf(mm, pm[bh * S + s]);
-  float z = 0.0f, o = 0.0f;
-  for (int s = 0; s < S; ++s) {
+  for (int s = tid; s < S; s += 256) mm = fmaxf(mm, pm[bh * S + s]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+  if (lane == 0) red[wave] = mm;
+  __syncthreads();
+  mm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // 2. split weights and the normalizer
+  float z = 0.0f;
+  for (int s = tid; s < S; s += 256) {
     const float m = pm[bh * S + s];
-    const float wt = exp2_guarded(m - mm, m != kNegInf);
-    z = fmaf(pz[bh * S + s], wt, z);
-    o = fmaf(pacc[(bh * S + s) * D + d], wt, o);
+    const float w = exp2_guarded(m - mm, m != kNegInf);
+    wts[s] = w;
+    z = fmaf(pz[bh * S + s], w, z);
   }
-  store_out(out, bh * D + d, z > 0.0f ? o / z : 0.0f, out_dtype);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o);
+  if (lane == 0) red[4 + wave] = z;
+  __syncthreads();
+  z = (red[4] + red[5]) + (red[6] + red[7]);
+  // 3. weighted sum of the partial outputs
+  const int parts = 256 / D, d = tid % D, pi = tid / D;
+  float o = 0.0f;
+  if (pi < parts) {
+    int s = pi;
+    for (; s + 7 * parts < S; s += 8 * parts) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = pacc[(bh * S + s + u * parts) * D + d];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o = fmaf(v[u], wts[s + u * parts], o);
+    }
+    for (; s < S; s += parts) o = fmaf(pacc[(bh * S + s) * D + d], wts[s], o);
+  }
+  part[tid] = o;
+  __syncthreads();
+  if (tid < D) {
+    float t = 0.0f;
+    for (int q = 0; q < parts; ++q) t += part[q * D + tid];
+    store_out(out, bh * D + tid, z > 0.0f ? t / z : 0.0f, out_dtype);
+  }
 }
 
 __global__ __launch_bounds__(256) void kv_quantize_s8_kernel(const void* __restrict__ x,
@@ -271,11 +609,12 @@ __global__ __launch_bounds__(256) void kv_quantize_s8_kernel(const void* __restr
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-// Context splits: about 128 workgroups per sequence batch-wide, at least 64
-// tokens per split, and no empty split.
+// Context splits: about 64 per sequence batch-wide (512 workgroups with 8 KV
+// heads), at least 128 tokens per split (one 32-token block per wave), at
+// most 1024 splits, and no empty split.
 static int sdpa_splits(int64_t B, int64_t N, int64_t* tps_out = nullptr) {
-  int64_t S = cdiv(128, B);
-  const int64_t cap = cdiv(N, 64);
+  int64_t S = cdiv(64, B);
+  const int64_t cap = std::min<int64_t>(cdiv(N, 128), 1024);
   if (S > cap) S = cap;
   if (S < 1) S = 1;
   const int64_t tps = cdiv(N, S);
@@ -307,6 +646,16 @@ static void launch_decode_d(const SdpaArgs& a, int gqa, int fmt, dim3 grid, hipS
     case 2: launch_decode_g<D, 2>(a, fmt, grid, st); break;
     case 4: launch_decode_g<D, 4>(a, fmt, grid, st); break;
     default: launch_decode_g<D, 8>(a, fmt, grid, st); break;
+  }
+}
+
+template <int D>
+static void launch_mfma_d(const SdpaArgs& a, int gqa, dim3 grid, hipStream_t st) {
+  switch (gqa) {
+    case 1: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 1>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 2>), grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 4>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 8>), grid, dim3(256), 0, st, a); break;
   }
 }
 
@@ -361,7 +710,15 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
   }
   const int gqa = (int)(Hq / Hkv);
   dim3 grid((unsigned)S, (unsigned)(B * Hkv));
-  if (D == 64)
+  if (fmt == SPARKQ_KV_S8_F16SCALE && (qdt == SPARKQ_BF16 || qdt == SPARKQ_F16) &&
+      !env_int("SPARKQ_SDPA_NO_MFMA", 0)) {
+    if (D == 64)
+      launch_mfma_d<64>(a, gqa, grid, st);
+    else if (D == 128)
+      launch_mfma_d<128>(a, gqa, grid, st);
+    else
+      launch_mfma_d<256>(a, gqa, grid, st);
+  } else if (D == 64)
     launch_decode_d<64>(a, gqa, fmt, grid, st);
   else if (D == 128)
     launch_decode_d<128>(a, gqa, fmt, grid, st);
