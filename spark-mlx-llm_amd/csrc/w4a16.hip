@@ -19,10 +19,11 @@
 //                       the last workgroup of each tile
 //   gemm_prep_kernel    bf16 GEMM prologue: fp16 activations and scales
 //                       under per-row power-of-two shifts, bias slots
-//   w4_gemm_x16_kernel  bf16, M > 32: 128x128x64 LDS tiles of exact fp16
-//                       operands (weights decoded to s'*(q-8)), fp16 MFMA
-//                       32x32x16 with no per-group epilogue, then the bias
-//                       slots on the bf16 MFMA
+//   w4_gemm_x16w_kernel bf16, M > 32: 128x256 tiles of exact fp16 operands
+//                       (weights decoded to s'*(q-8) in registers, activations
+//                       through LDS), fp16 MFMA 32x32x16 with no per-group
+//                       epilogue, the bias slots on the bf16 MFMA, split-K
+//                       combined in the same launch when tiles are few
 //   xsum_kernel         group sums X_g[m] for the fp16 GEMM, layout [K/G][M]
 //   w4_gemm_kernel      fp16, M > 32: 128x128x64 LDS tiles (B decoded to the
 //                       exact q), per-group fp32 scale and bias epilogue
@@ -837,136 +838,12 @@ struct GemmX16Args {
   const uint16_t* b2;  // [N][K2p]
   void* y;
   int y_dtype, M, N, K, K2p;
+  // split-K (wide kernel): grid z = split, S splits of the 64-k steps; the
+  // fp32 tile partials and one counter per output tile live in the workspace
+  int S;
+  float* part;
+  unsigned* counters;
 };
-
-template <int G>
-__global__ __launch_bounds__(256, 2) void w4_gemm_x16_kernel(GemmX16Args a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM * kBK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][kBN * kBK];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int j = lane >> 5;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * kBM;
-  const int K = a.K, ng = K / G, nsteps = K / kBK;
-  const int mrows = min(kBM, a.M - m0), nrows = min(kBN, a.N - n0);
-  // rows past the tile's last one read as zero
-  const rsrc_t rx = make_rsrc(a.xh + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 2u);
-  const rsrc_t rw = make_rsrc(a.w + (int64_t)n0 * (K / 8), (uint32_t)nrows * (uint32_t)K / 2u);
-  const rsrc_t rs = make_rsrc(a.sp + (int64_t)n0 * ng, (uint32_t)(nrows * ng) * 2u);
-  const uint32_t mask = vgpr_const(0x000F000Fu), magic = vgpr_const(0x64006400u);
-
-  u32x4_t ra[4], rb;
-  uint32_t rsv;
-  auto load = [&](int step) {
-    const int k0 = step * kBK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + 256 * i, row = p >> 3, kc = p & 7;
-      ra[i] = buf_load16(rx, (uint32_t)(row * K + k0 + kc * 8) * 2u);
-    }
-    const int row = tid >> 1, half = tid & 1;
-    rb = buf_load16(rw, (uint32_t)(row * (K / 2) + k0 / 2 + 16 * half));
-    rsv = buf_load2(rs, (uint32_t)(row * ng + (k0 + 32 * half) / G) * 2u);
-  };
-  auto store = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = tid + 256 * i, row = p >> 3, kc = p & 7;
-      *reinterpret_cast<u32x4_t*>(&As[st][tile_off(row, kc)]) = ra[i];
-    }
-    const int row = tid >> 1, half = tid & 1;
-    const f16x2_t s2 = __builtin_bit_cast(f16x2_t, rsv | (rsv << 16));
-    const f16x2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-#pragma unroll
-    for (int wi = 0; wi < 4; ++wi) {
-      const uint32_t w = rb[wi];
-      u32x4_t o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t t = ((w >> (4 * i)) & mask) | magic;
-        o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2_t, t) - off) * s2);
-      }
-      *reinterpret_cast<u32x4_t*>(&Bs[st][tile_off(row, 4 * half + wi)]) = o;
-    }
-  };
-
-  f32x16_t acc[2][2];
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) acc[x][y] = f32x16_t{};
-
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int step = 0; step < nsteps; ++step) {
-    const int st = step & 1;
-    if (step + 1 < nsteps) load(step + 1);
-#pragma unroll
-    for (int ss = 0; ss < 4; ++ss) {
-      const int kc = 2 * ss + j;
-      u32x4_t af[2], bf[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        af[t] = *reinterpret_cast<const u32x4_t*>(&As[st][tile_off(wm * 64 + t * 32 + (lane & 31), kc)]);
-        bf[t] = *reinterpret_cast<const u32x4_t*>(&Bs[st][tile_off(wn * 64 + t * 32 + (lane & 31), kc)]);
-      }
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int y = 0; y < 2; ++y) acc[x][y] = mfma32x32x16<F16>(af[x], bf[y], acc[x][y]);
-    }
-    if (step + 1 < nsteps) store(st ^ 1);
-    __syncthreads();
-  }
-
-  // undo the row shifts: y = 2^(ex[m] + es[n]) * acc
-  const rsrc_t rex = make_rsrc(a.ex + m0, (uint32_t)mrows * 4u);
-  const rsrc_t res = make_rsrc(a.es + n0, (uint32_t)nrows * 4u);
-#pragma unroll
-  for (int y = 0; y < 2; ++y) {
-    const int esn = (int)__builtin_amdgcn_raw_buffer_load_b32(
-        res, (wn * 64 + y * 32 + (lane & 31)) * 4, 0, 0);
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const u32x4_t e4 = buf_load16(rex, (uint32_t)(wm * 64 + x * 32 + 8 * q4 + 4 * j) * 4u);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc[x][y][4 * q4 + r] = ldexpf(acc[x][y][4 * q4 + r], (int)e4[r] + esn);
-      }
-  }
-  // bias slots: acc += A2 * B2^T on the bf16 MFMA
-  const int K2p = a.K2p;
-  const rsrc_t ra2 = make_rsrc(a.a2 + (int64_t)m0 * K2p, (uint32_t)mrows * (uint32_t)K2p * 2u);
-  const rsrc_t rb2 = make_rsrc(a.b2 + (int64_t)n0 * K2p, (uint32_t)nrows * (uint32_t)K2p * 2u);
-  for (int ks = 0; ks < K2p; ks += 16) {
-    u32x4_t af[2], bf[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      af[t] = buf_load16(ra2, (uint32_t)((wm * 64 + t * 32 + (lane & 31)) * K2p + ks + 8 * j) * 2u);
-      bf[t] = buf_load16(rb2, (uint32_t)((wn * 64 + t * 32 + (lane & 31)) * K2p + ks + 8 * j) * 2u);
-    }
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int y = 0; y < 2; ++y) acc[x][y] = mfma32x32x16<BF16>(af[x], bf[y], acc[x][y]);
-  }
-
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int gn = n0 + wn * 64 + y * 32 + (lane & 31);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int gm = m0 + wm * 64 + x * 32 + mfma32_row(lane, v);
-        if (gm < a.M && gn < a.N) store_out(a.y, (int64_t)gm * a.N + gn, acc[x][y][v], a.y_dtype);
-      }
-    }
-}
 
 // Wide variant: a 128 x (64*NWV) tile per workgroup of NWV waves, each wave
 // owning 128 rows x 64 columns. Activations go through LDS (shared by the
@@ -1009,7 +886,10 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane >> 5, l32 = lane & 31;
   const int n0 = blockIdx.x * (64 * NWV), m0 = blockIdx.y * kBM;
-  const int K = a.K, ng = K / G, nsteps = K / kBK;
+  const int K = a.K, ng = K / G;
+  // this workgroup's 64-k steps [s_begin, nsteps)
+  const int s_begin = (int)((int64_t)blockIdx.z * (K / kBK) / a.S);
+  const int nsteps = (int)((int64_t)(blockIdx.z + 1) * (K / kBK) / a.S);
   const int mrows = min(kBM, a.M - m0);
   const int wn0 = n0 + 64 * wave;  // this wave's first column
   const int nrows = __builtin_amdgcn_readfirstlane(max(0, min(64, a.N - wn0)));
@@ -1093,13 +973,47 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     __syncthreads();
   };
 
-  load(0);
+  load(s_begin);
 #pragma unroll
   for (int i = 0; i < AL; ++i) *lds_at(lds_w[i]) = ra[i];
   __syncthreads();
-  for (int step = 0; step < nsteps; step += 2) {
+  for (int step = s_begin; step < nsteps; step += 2) {
     body(step, std::integral_constant<int, 0>{});
     if (step + 1 < nsteps) body(step + 1, std::integral_constant<int, 1>{});
+  }
+
+  if (a.S > 1) {
+    // every split stores its raw tile; the last to arrive sums them in split
+    // order (deterministic), resets the counter and finishes the tile
+    constexpr int TV = 4 * 2 * 16;  // accumulators per lane
+    const int ntiles = gridDim.x * gridDim.y, tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const size_t tsz = (size_t)TV * NT;
+    float* mine = a.part + ((size_t)blockIdx.z * ntiles + tile) * tsz + tid;
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) splitk_store(mine + (size_t)((x * 2 + y) * 16 + v) * NT, acc[x][y][v]);
+    __shared__ int s_last;
+    if (!splitk_arrive(a.counters + tile, a.S, &s_last)) return;
+    const float* base = a.part + (size_t)tile * tsz + tid;
+    const size_t zstride = (size_t)ntiles * tsz;
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        f32x16_t t = f32x16_t{};
+        for (int z = 0; z < a.S; ++z) {
+          float v16[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) v16[v] = splitk_load(base + z * zstride + (size_t)((x * 2 + y) * 16 + v) * NT);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) t[v] += v16[v];
+        }
+        acc[x][y] = t;
+      }
+    splitk_reset(a.counters + tile);
   }
 
   // undo the row shifts: y = 2^(ex[m] + es[n]) * acc
@@ -1469,6 +1383,27 @@ static GemmX16Layout gemm_x16_layout(int64_t M, int64_t N, int64_t K, int G) {
   return l;
 }
 
+// Split-K of the wide GEMM, for long rows only (K >= 4096; measured: at
+// K = 2560 the partial round trip costs more than the extra waves bring):
+// about two waves per SIMD (2048 waves of one 128x64 tile each) when the
+// output tiles alone are too few, at least twelve 64-k steps per split, and
+// only while the tile counters fit.
+struct WidePlan {
+  int S;
+  size_t part_bytes;
+};
+static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
+  WidePlan p{1, 0};
+  const int64_t tiles = cdiv(N, 256) * cdiv(M, kBM), nsteps = K / kBK;
+  if (tiles > kMaxCounterTiles) return p;
+  int64_t S = nsteps >= 64 ? (2048 + 2 * tiles) / (4 * tiles) : 1;
+  S = std::min<int64_t>(S, nsteps / 12);
+  if (env_int("SPARKQ_W4_SPLITS", 0)) S = std::min<int64_t>(env_int("SPARKQ_W4_SPLITS", 1), nsteps);
+  p.S = (int)std::max<int64_t>(S, 1);
+  if (p.S > 1) p.part_bytes = round_up((size_t)p.S * tiles * kBM * 256 * 4, 256);
+  return p;
+}
+
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
   if (plan_gemv(M, N, K, G).ok) return 0;
@@ -1479,7 +1414,8 @@ size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
     return p.S > 1 ? kCounterBytes + p.part_bytes : 0;
   }
   const GemmX16Layout l = gemm_x16_layout(M, N, K, G);
-  return kCounterBytes + std::max(round_up((size_t)(K / G) * M * 4, 256), l.bytes);
+  return kCounterBytes +
+         std::max(round_up((size_t)(K / G) * M * 4, 256), l.bytes + plan_wide(M, N, K).part_bytes);
 }
 
 template <typename T, int G, int MB, int CPW>
@@ -1540,8 +1476,8 @@ static void launch_gemm(int G, const void* x, const uint32_t* w, const void* s,
 }
 
 static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void* s,
-                            const void* b, unsigned char* ws, void* y, int ydt, int M, int N,
-                            int K, hipStream_t st) {
+                            const void* b, unsigned* counters, unsigned char* ws, void* y,
+                            int ydt, int M, int N, int K, hipStream_t st) {
   const GemmX16Layout l = gemm_x16_layout(M, N, K, G);
   GemmPrepArgs p{};
   p.x = (const uint16_t*)x;
@@ -1573,34 +1509,17 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   a.N = N;
   a.K = K;
   a.K2p = p.K2p;
-  const int wide = (int)env_int("SPARKQ_W4_WIDE", 4);
-  if (wide == 4) {
-    dim3 gw((unsigned)cdiv(N, 256), (unsigned)cdiv(M, kBM));
-    if (G == 32)
-      hipLaunchKernelGGL((w4_gemm_x16w_kernel<32, 4>), gw, dim3(256), 0, st, a);
-    else if (G == 64)
-      hipLaunchKernelGGL((w4_gemm_x16w_kernel<64, 4>), gw, dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL((w4_gemm_x16w_kernel<128, 4>), gw, dim3(256), 0, st, a);
-    return;
-  }
-  if (wide == 2) {
-    dim3 gw((unsigned)cdiv(N, 128), (unsigned)cdiv(M, kBM));
-    if (G == 32)
-      hipLaunchKernelGGL((w4_gemm_x16w_kernel<32, 2>), gw, dim3(128), 0, st, a);
-    else if (G == 64)
-      hipLaunchKernelGGL((w4_gemm_x16w_kernel<64, 2>), gw, dim3(128), 0, st, a);
-    else
-      hipLaunchKernelGGL((w4_gemm_x16w_kernel<128, 2>), gw, dim3(128), 0, st, a);
-    return;
-  }
-  dim3 grid((unsigned)cdiv(N, kBN), (unsigned)cdiv(M, kBM));
+  const WidePlan wp = plan_wide(M, N, K);
+  a.S = wp.S;
+  a.part = reinterpret_cast<float*>(ws + l.bytes);
+  a.counters = counters;
+  dim3 gw((unsigned)cdiv(N, 256), (unsigned)cdiv(M, kBM), (unsigned)wp.S);
   if (G == 32)
-    hipLaunchKernelGGL(w4_gemm_x16_kernel<32>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((w4_gemm_x16w_kernel<32, 4>), gw, dim3(256), 0, st, a);
   else if (G == 64)
-    hipLaunchKernelGGL(w4_gemm_x16_kernel<64>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((w4_gemm_x16w_kernel<64, 4>), gw, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL(w4_gemm_x16_kernel<128>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((w4_gemm_x16w_kernel<128, 4>), gw, dim3(256), 0, st, a);
 }
 
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
@@ -1662,8 +1581,9 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
   }
   unsigned char* wsp = reinterpret_cast<unsigned char*>(ws) + kCounterBytes;
   if (xdt == SPARKQ_BF16 && !env_int("SPARKQ_W4_NO_X16", 0)) {
-    launch_gemm_x16(G, x, w, s, b, wsp, y, ydt, (int)M, (int)N, (int)K, st);
-    return check_launch("w4_gemm_x16_kernel");
+    launch_gemm_x16(G, x, w, s, b, reinterpret_cast<unsigned*>(ws), wsp, y, ydt, (int)M, (int)N,
+                    (int)K, st);
+    return check_launch("w4_gemm_x16w_kernel");
   }
   float* xs = reinterpret_cast<float*>(wsp);
   if (xdt == SPARKQ_BF16)

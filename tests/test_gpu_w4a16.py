@@ -106,6 +106,20 @@ def test_split_plans(gpu, m, n, k):
     check_fp32(y32, ref)
 
 
+@pytest.mark.parametrize("m,n,k,g", [(33, 200, 4096, 32), (300, 520, 4096, 64), (130, 90, 9728, 128),
+                                     (2048, 256, 4096, 64)])
+def test_gemm_split_k(gpu, m, n, k, g):
+    """Few output tiles and long K: the bf16 GEMM splits K across workgroups
+    and the last one of each tile sums the partials (ragged M and N tiles)."""
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m + n)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    check_fp32(y32.cpu().numpy(), ref)
+    check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
+    # repeated calls on the same workspace are bit-identical (counters reset)
+    assert torch.equal(y32, _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32))
+
+
 @pytest.mark.parametrize("m,n,k,g", [(1, 37, 576, 32), (3, 41, 576, 64), (2, 4, 64, 32),
                                      (4, 130, 9728, 32), (1, 5, 10240, 128), (3, 9, 4608, 64)])
 def test_decode_ragged_shapes(gpu, m, n, k, g):
