@@ -78,7 +78,10 @@ int sparkq_is_available(void);
  * budget (K <= 10240 for M = 1); other M <= 32 run the weight-streaming skinny
  * kernel (MFMA 32x32x16; when the shape splits K across workgroups the last
  * workgroup of each 32-row tile combines the partials in the same launch);
- * larger M runs the LDS-tiled MFMA GEMM behind a group-sum prologue.
+ * larger M runs the MFMA GEMM behind a prologue (bf16: exact fp16 operands
+ * under power-of-two row shifts, with the bias term as extra MFMA slots, and
+ * an in-launch split-K for long rows; fp16: a group-sum prologue and a
+ * per-group fp32 epilogue).
  * Workspace: the first 16384 bytes hold per-tile counters and must be zero
  * before the first call; every call leaves them zero again. Give each entry
  * point its own workspace buffer, and do not share one buffer between

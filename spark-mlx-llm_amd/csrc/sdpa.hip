@@ -613,7 +613,7 @@ __global__ __launch_bounds__(256) void kv_quantize_s8_kernel(const void* __restr
 // heads), at least 128 tokens per split (one 32-token block per wave), at
 // most 1024 splits, and no empty split.
 static int sdpa_splits(int64_t B, int64_t N, int64_t* tps_out = nullptr) {
-  int64_t S = cdiv(64, B);
+  int64_t S = cdiv(env_int("SPARKQ_SDPA_SPLITS", 64), B);
   const int64_t cap = std::min<int64_t>(cdiv(N, 128), 1024);
   if (S > cap) S = cap;
   if (S < 1) S = 1;
