@@ -66,7 +66,9 @@ void sq_w4_quantize(const float* w, int64_t N, int64_t K, int G, int dtype,
 /* The converter's BF16 -> W4 quantizer (spark_mlx_llm/conversion.py:564-583):
  * groups of G; lower = min(min,0), upper = max(max,0); scale = (upper-lower)/15
  * (1 if 0) rounded to bf16; zero = clip(rint(-lower/s), 0, 15);
- * code = clip(rint(w/s) + zero, 0, 15); bias = bf16(-zero*s). */
+ * code = clip(rint(w/s) + zero, 0, 15); bias = bf16(-zero*s).
+ * Pinned at G32 against vectors the converter itself wrote
+ * (tests/golden/converter_vectors.npz, tests/golden/make_converter_vectors.py). */
 void sq_w4_quantize_converter(const float* w, int64_t N, int64_t K, int G,
                               uint32_t* wq, uint16_t* scales,
                               uint16_t* biases);

@@ -6,6 +6,7 @@ repository), so these checks are the oracle's anchor.
 """
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -313,3 +314,51 @@ def test_cpu_baseline_matches_oracle():
     assert used >= 1
     ref = o.w4a16_matmul(x16, wq, s, b, g)
     assert np.abs(y - ref).max() < 1e-4
+
+
+# ---------------------------------------------------------------------------
+# golden vectors written by the reference converter (tests/golden/)
+# ---------------------------------------------------------------------------
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "converter_vectors.npz")
+
+
+def _golden():
+    return np.load(GOLDEN)  # plain arrays, no pickle
+
+
+def test_converter_w4_quantizer_matches_reference_vectors():
+    """The oracle's G32 converter quantizer against `_rows` (scheme
+    bf16-int4, conversion.py:551-608) on 34 rows of edge cases: codes,
+    scales and biases bit for bit."""
+    g = _golden()
+    wq, s, b = o.w4_quantize_converter(o.bits_to_f32(g["w16"], o.BF16), 32)
+    assert np.array_equal(wq, g["w4_words"])
+    assert np.array_equal(s, g["w4_scales"])
+    assert np.array_equal(b, g["w4_biases"])
+
+
+def test_converter_w8_format_unpacks_to_symmetric_codes():
+    """The converter's W8 rows (scheme bf16-int8) unpack, through the oracle
+    and through the operator layer's unpack (ops/linear.py:299-324), to
+    rint(w / scale) clipped to +-127 with one repeated per-row scale and
+    biases -128 * scale."""
+    from sparkq.ops.linear import unpack_affine_w8
+
+    g = _golden()
+    w = o.bits_to_f32(g["w16"], o.BF16).astype(np.float64)
+    sc = o.bits_to_f32(g["w8_scales"], o.BF16)
+    assert np.all(sc == sc[:, :1])
+    expect = np.clip(np.rint(w / sc[:, :1].astype(np.float64)), -127, 127).astype(np.int8)
+    assert np.array_equal(o.w8_unpack_affine(g["w8_words"]), expect)
+    assert np.array_equal(g["w8_biases"], o.bf16_bits(-128.0 * sc))
+    w8, ch = unpack_affine_w8(torch.from_numpy(g["w8_words"].view(np.int32)),
+                              torch.from_numpy(g["w8_scales"].view(np.int16)).view(torch.bfloat16),
+                              torch.from_numpy(g["w8_biases"].view(np.int16)).view(torch.bfloat16),
+                              group_size=32)
+    assert np.array_equal(w8.numpy(), expect)
+    assert np.array_equal(ch.numpy(), sc[:, 0])
+
+
+def test_bf16_rounding_matches_reference_vectors():
+    g = _golden()
+    assert np.array_equal(o.bf16_bits(g["bf16_in"]), g["bf16_out"])
