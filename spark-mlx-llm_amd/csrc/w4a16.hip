@@ -1271,8 +1271,8 @@ static SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K) {
 // spans of activations in registers, so rows of up to 20 spans (K <= 10240)
 // split into SG = 1, 2 or 4 span groups. Workgroups of 4 waves (8 when the
 // activations need the larger staging budget) cover R = 4 * (waves / SG) *
-// RQW rows; two row quads per wave once
-// that still leaves >= 2048 waves. The staged activations, (scale, bias)
+// RQW rows; two row quads per wave (M = 1 only) once that still leaves
+// >= 2048 waves. The staged activations, (scale, bias)
 // pieces and LDS must fit the kernel's fixed budgets, and the scale tensors
 // must end on a 16-byte boundary (they are staged in 16-byte loads).
 struct GemvPlan {
@@ -1306,7 +1306,10 @@ static GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int G) {
   p.NW = M * (K / 32) > kGemvXP * 256 ? 8 : 4;
   if (env_int("SPARKQ_W4_GEMV_NW", 0)) p.NW = env_int("SPARKQ_W4_GEMV_NW", 4) == 8 ? 8 : 4;
   const int64_t nq = cdiv(N, 4);
-  p.RQW = cdiv(nq, 2) * p.SG >= 2048 ? 2 : 1;
+  // two row quads per wave only at M = 1: with four activation rows the
+  // second quad's registers spill at three waves per SIMD (measured: gate+up
+  // at M = 4 takes 15.4 us with two, 11.1 us with one)
+  p.RQW = M == 1 && cdiv(nq, 2) * p.SG >= 2048 ? 2 : 1;
   if (env_int("SPARKQ_W4_GEMV_RQW", 0)) p.RQW = env_int("SPARKQ_W4_GEMV_RQW", 1) == 2 ? 2 : 1;
   p.MQ = M == 1 ? 1 : 4;
   p.R = 4 * (p.NW / p.SG) * p.RQW;
@@ -1409,7 +1412,7 @@ size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (plan_gemv(M, N, K, G).ok) return 0;
   // every workspace of this entry point starts with the counter block, so a
   // GEMM call never writes over the counters a later split-K call relies on
-  if (M <= 32) {
+  if (M <= 32 && M < env_int("SPARKQ_W4_GEMM_FROM", 33)) {
     const SkinnyPlan p = plan_skinny(M, N, K);
     return p.S > 1 ? kCounterBytes + p.part_bytes : 0;
   }
@@ -1550,7 +1553,7 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
       launch_gemv<F16>(gp, G, a, st);
     return check_launch("w4_gemv_kernel");
   }
-  if (M <= 32) {
+  if (M <= 32 && M < env_int("SPARKQ_W4_GEMM_FROM", 33)) {
     const SkinnyPlan p = plan_skinny(M, N, K);
     if (p.S > 1 && cdiv(N, 32) > kMaxCounterTiles)
       return set_error(SPARKQ_ERR_UNSUPPORTED,
