@@ -86,6 +86,21 @@ int device_check() {
   return SPARKQ_OK;
 }
 
+static int g_device_cus[64];
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(g_device_mu);
+  if (g_device_cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256;
+    g_device_cus[dev] = n;
+  }
+  return g_device_cus[dev];
+}
+
 }  // namespace sparkq
 
 using namespace sparkq;

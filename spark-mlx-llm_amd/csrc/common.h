@@ -223,6 +223,8 @@ namespace sparkq {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int device_check();
+// CUs of the current device (256 when it cannot be queried)
+int device_cus();
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // positive integer from the environment, or dflt

@@ -195,6 +195,14 @@ __device__ __forceinline__ void decode_w4_strided(uint32_t w, DecodeConsts c, ui
   }
 }
 
+// LDS slot (dword index) of 16-byte chunk w of activation piece pi. The
+// pieces of a span sit chunk-major (16 pieces x 16 B per chunk), so the 16
+// lane blocks of a wave, which read 16 consecutive pieces, hit 256
+// contiguous bytes per read instead of 16 addresses at a 64-byte stride.
+__device__ __forceinline__ int gemv_xslot(int pi, int w) {
+  return 256 * (pi >> 4) + 64 * w + 4 * (pi & 15);
+}
+
 // LDS layout of the decode GEMV (byte offsets)
 struct GemvLds {
   int xp;    // activations [M][K] in pair order (2 B each)
@@ -206,7 +214,7 @@ struct GemvLds {
 __host__ __device__ __forceinline__ GemvLds gemv_lds(int M, int K, int R, int G, int NW, int RQW) {
   GemvLds l;
   l.xp = 0;
-  l.xs = l.xp + ((M * K * 2 + 15) & ~15);
+  l.xs = l.xp + ((M * K * 2 + 1023) & ~1023);
   l.sb = l.xs + (K / 32) * 16;
   l.red = l.sb + ((R * (K / G) * 4 + 15) & ~15);
   l.bytes = l.red + NW * RQW * 64;
@@ -294,7 +302,7 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
                              __builtin_amdgcn_perm(r.z, r.x, 0x07060302u),   // (x1, x5)
                              __builtin_amdgcn_perm(r.w, r.y, 0x05040100u),   // (x2, x6)
                              __builtin_amdgcn_perm(r.w, r.y, 0x07060302u)};  // (x3, x7)
-          *reinterpret_cast<u32x4_t*>(xp + 16 * pi + 4 * w) = o;
+          *reinterpret_cast<u32x4_t*>(xp + gemv_xslot(pi, w)) = o;
 #pragma unroll
           for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[e], sum);
         }
@@ -330,10 +338,10 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int s = 0; s < US; ++s) {
       const int piece = min(16 * (u0 + s) + b, (K >> 5) - 1);
-      const u32x4_t* src = reinterpret_cast<const u32x4_t*>(xp + 2 * ((int64_t)min(j, M - 1) * K + 32 * piece));
+      const int pi = min(j, M - 1) * (K >> 5) + piece;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const u32x4_t v = src[w];
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xp + 4 * gemv_xslot(pi, w));
         xa[s][w][0] = v.x;
         xa[s][w][1] = v.y;
         xa[s][w][2] = v.z;
@@ -442,6 +450,229 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
           if (m < M) store_out(a.y, (int64_t)m * N + row, out[r][m], a.y_dtype);
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// streaming decode GEMV (M = 1)
+// ---------------------------------------------------------------------------
+// One workgroup of 16 waves per CU. Workgroup w owns the row quads
+// [w*nq/P, (w+1)*nq/P) (sizes differ by at most one), so every CU streams
+// the same number of bytes. Its work items are (row quad, span) pairs in
+// quad-major order, dealt to the waves round-robin: each wave gets NI or
+// fewer 1 KB items whatever the row length. The activations (pair order,
+// chunk-major spans) with their piece sums, and the (scale, bias) pairs of
+// the workgroup's rows, are staged in LDS once per workgroup.
+// Every wave issues all of its weight loads at the start, right after the
+// staging loads, and computes its items in issue order, each as soon as its
+// own load has landed: the decode and MFMAs of early items overlap the
+// arrival of later ones, and the work left after the last byte lands is one
+// item per wave.
+// An item is the w4_gemv_kernel step for one span of one row quad: one
+// 16-byte piece per lane (activations read from LDS), eight 4x4x4 MFMAs and
+// the lane's group epilogue. Its 64 lane sums go to an LDS slot; at the end
+// each row adds its slots over the spans in order, then over the 16 blocks
+// by a fixed shuffle tree.
+struct GemvStreamArgs {
+  const uint16_t* x;
+  const uint32_t* w;
+  const uint16_t* sc;
+  const uint16_t* bi;
+  void* y;
+  int y_dtype;
+  int N, K;
+  int nq;  // row quads
+  int P;   // workgroups
+  int QW;  // row quads of the largest workgroup
+};
+
+constexpr int kStreamXP = 1;   // staged activation pieces (64 B) per thread, at most
+constexpr int kStreamSP = 2;   // staged (scale, bias) pieces (16 B each) per thread, at most
+
+// LDS layout of the streaming GEMV (byte offsets)
+struct StreamLds {
+  int xp;    // activations [K], gemv_xslot order
+  int xs;    // piece sums [K/32] fp32
+  int sb;    // (scale, bias) of the workgroup's rows: [4*QW][K/G] dwords
+  int part;  // lane sums of the items: [QW*U][64] fp32
+  int bytes;
+};
+__host__ __device__ __forceinline__ StreamLds stream_lds(int K, int QW, int G) {
+  const int U = ((K >> 1) + 255) >> 8;
+  StreamLds l;
+  l.xp = 0;
+  l.xs = (K * 2 + 1023) & ~1023;
+  l.sb = l.xs + ((K / 32) * 4 + 15) / 16 * 16;
+  l.part = l.sb + ((4 * QW * (K / G) * 4 + 15) & ~15);
+  l.bytes = l.part + QW * U * 64 * 4;
+  return l;
+}
+
+// FULL: K % 512 == 0 and N % 4 == 0 (every piece of every item is in range)
+template <typename T, int G, int NI, int NW, bool FULL>
+__global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NT = 64 * NW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, j = lane & 3;
+  const int N = a.N, K = a.K;
+  const int RB = K >> 1;             // bytes per weight row
+  const int U = (RB + 255) >> 8;     // spans per row
+  const int ng = K / G;              // groups per row
+  const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
+  const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
+  const int nitems = nql * U;
+  const StreamLds L = stream_lds(K, a.QW, G);
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)K * 2);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+
+  // 1. staging loads: activation pieces and (scale, bias) pieces; a wave
+  // with no piece to fetch skips the instruction
+  const int nxp = K >> 5;
+  const int nsp = (4 * nql * ng) >> 3;
+  u32x4_t xr[kStreamXP][4];
+  u32x4_t sr[kStreamSP], br[kStreamSP];
+#pragma unroll
+  for (int i = 0; i < kStreamXP; ++i) {
+    const int pi = tid + i * NT;
+    if (i * NT + 64 * wave < nxp) {
+      const uint32_t off = pi < nxp ? 64u * pi : kOob;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kStreamSP; ++i) {
+    const int pi = tid + i * NT;
+    if (i * NT + 64 * wave < nsp) {
+      const uint32_t off = pi < nsp ? 8u * (uint32_t)qa * ng + 16u * pi : kOob;
+      sr[i] = buf_load16(rs, off);
+      br[i] = buf_load16(rb, off);
+    }
+  }
+
+  // 2. every weight load of the wave: item wave + 16 i is (row quad ql[i],
+  // span sp[i]); slots past the wave's last item read nothing
+  const int nmy = nitems > wave ? (nitems - wave + NW - 1) / NW : 0;
+  int ql[NI], sp[NI];
+  u32x4_t wv[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int it = wave + i * NW;
+    ql[i] = it / U;
+    sp[i] = it - ql[i] * U;
+    const int row = 4 * (qa + ql[i]) + j, p = 256 * sp[i] + 16 * b;
+    const bool ok = i < nmy && (FULL || (row < N && p + 16 <= RB));
+    wv[i] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
+  }
+
+  // keep every load above ahead of the arithmetic below
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. write the staged data to LDS
+  {
+    uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
+    float* xs = reinterpret_cast<float*>(smem + L.xs);
+#pragma unroll
+    for (int i = 0; i < kStreamXP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nxp) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const u32x4_t r = xr[i][w];
+          const u32x4_t o = {__builtin_amdgcn_perm(r.z, r.x, 0x05040100u),   // (x0, x4)
+                             __builtin_amdgcn_perm(r.z, r.x, 0x07060302u),   // (x1, x5)
+                             __builtin_amdgcn_perm(r.w, r.y, 0x05040100u),   // (x2, x6)
+                             __builtin_amdgcn_perm(r.w, r.y, 0x07060302u)};  // (x3, x7)
+          *reinterpret_cast<u32x4_t*>(xp + gemv_xslot(pi, w)) = o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[e], sum);
+        }
+        xs[pi] = sum;
+      }
+    }
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+#pragma unroll
+    for (int i = 0; i < kStreamSP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nsp) {
+        const u32x4_t s = sr[i], c = br[i];
+        u32x4_t lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = __builtin_amdgcn_perm(c[e], s[e], 0x05040100u);  // (s0, b0)
+          hi[e] = __builtin_amdgcn_perm(c[e], s[e], 0x07060302u);  // (s1, b1)
+        }
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. the wave's items, in issue order
+  const unsigned char* xp = smem + L.xp;
+  const float* xs = reinterpret_cast<const float*>(smem + L.xs);
+  const uint32_t* sb = reinterpret_cast<const uint32_t*>(smem + L.sb);
+  float* part = reinterpret_cast<float*>(smem + L.part);
+  const DecodeConsts dc = decode_consts<T>();
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    if (i < nmy) {
+      const int s = sp[i];
+      const int p = 256 * s + 16 * b;
+      const bool ok = FULL || (4 * (qa + ql[i]) + j < N && p + 16 <= RB);
+      const int piece = FULL ? 16 * s + b : min(16 * s + b, (K >> 5) - 1);
+      uint32_t xa[4][4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xp + 4 * gemv_xslot(piece, w));
+        xa[w][0] = v.x;
+        xa[w][1] = v.y;
+        xa[w][2] = v.z;
+        xa[w][3] = v.w;
+      }
+      const float xm = xs[piece];
+      // pieces past the row end carry zero codes and unrelated activations
+      const uint32_t pair = ok ? sb[(4 * ql[i] + j) * ng + (2 * p) / G] : 0u;
+      f32x4_t d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = d0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        uint32_t pr[4];
+        decode_w4_strided<T>(wv[i][w], dc, pr);
+        d0 = mfma4x4<T>(xa[w][0], xa[w][1], pr[0], pr[1], d0);
+        d1 = mfma4x4<T>(xa[w][2], xa[w][3], pr[2], pr[3], d1);
+      }
+      const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
+      const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
+      const float v = fmaf(sf, d0[0] + d1[0], bf * xm);
+      part[(ql[i] * U + s) * 64 + lane] = ok ? v : 0.0f;
+    }
+  }
+  __syncthreads();
+
+  // 5. row r of the workgroup, block bb: the sum of its slots over the spans
+  // in order, then over the 16 blocks by a shuffle tree (lanes 16t..16t+15
+  // hold the blocks of one row)
+  for (int t0 = 0; t0 < 64 * nql; t0 += NT) {
+    const int t = t0 + tid;
+    const int rl = t >> 4, bb = t & 15;
+    float v = 0.0f;
+    if (rl < 4 * nql) {
+      const float* src = part + (rl >> 2) * U * 64 + 4 * bb + (rl & 3);
+      for (int s = 0; s < U; ++s) v += src[s * 64];
+    }
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 8);
+    const int row = 4 * qa + rl;
+    if (bb == 0 && rl < 4 * nql && row < N) store_out(a.y, row, v, a.y_dtype);
   }
 }
 
@@ -1368,6 +1599,85 @@ static void launch_gemv(const GemvPlan& p, int G, const GemvArgs& a, hipStream_t
     launch_gemv_g<T, 128>(p, a, st);
 }
 
+// Streaming GEMV plan (M = 1, rows longer than 5 spans): one workgroup per
+// CU, each owning a contiguous range of row quads, its items dealt NI or
+// fewer to a wave. The
+// staged activations and the (scale, bias) pieces of the largest workgroup
+// must fit the staging budgets and LDS; the scale tensors must end on a
+// 16-byte boundary and every workgroup's first scale on one (K/G even),
+// since they are staged in 16-byte loads.
+struct StreamPlan {
+  bool ok;
+  int P, QW, NI, NW;
+  bool full;
+  size_t lds;
+};
+
+static StreamPlan plan_stream(int64_t M, int64_t N, int64_t K, int G) {
+  StreamPlan p{};
+  if (M != 1 || env_int("SPARKQ_W4_NO_STREAM", 0)) return p;
+  if (N * (K / 2) >= (int64_t)kOob || K * 2 >= (int64_t)kOob) return p;
+  const int64_t ng = K / G;
+  if (ng % 2 != 0 || (N * ng * 2) % 16 != 0) return p;
+  const int64_t nq = cdiv(N, 4), U = cdiv(K / 2, 256);
+  // Rows of up to 5 spans (K <= 2560) keep w4_gemv_kernel, whose
+  // activations fit one wave's registers and are staged by many small
+  // workgroups at little cost (measured: gate+up 19456x2560 8.5 us there
+  // against 9.1 us here). Longer rows stage up to 20 KB of activations per
+  // workgroup there, once per CU here (down 2560x9728: 6.9 -> 6.1 us).
+  if (U <= 5 && !env_int("SPARKQ_W4_STREAM_ALL", 0)) return p;
+  p.NW = env_int("SPARKQ_W4_STREAM_NW", 16) == 8 ? 8 : 16;
+  p.P = (int)std::min<int64_t>(nq, device_cus() * (16 / p.NW));
+  p.QW = (int)cdiv(nq, p.P);
+  const int64_t ni = cdiv(p.QW * U, p.NW);
+  if (ni > 8) return p;
+  p.NI = ni <= 2 ? 2 : (ni <= 4 ? (int)ni : (ni <= 6 ? 6 : 8));
+  const int64_t nt = 64 * p.NW;
+  if (K / 32 > kStreamXP * nt || 4 * p.QW * ng / 8 > kStreamSP * nt) return p;
+  const StreamLds l = stream_lds((int)K, p.QW, G);
+  if (l.bytes > 65536) return p;
+  p.lds = (size_t)l.bytes;
+  p.full = K % 512 == 0 && N % 4 == 0;
+  p.ok = true;
+  return p;
+}
+
+template <typename T, int G, int NI, int NW>
+static void launch_stream_w(const StreamPlan& p, const GemvStreamArgs& a, hipStream_t st) {
+  if (p.full)
+    hipLaunchKernelGGL((w4_gemv_stream_kernel<T, G, NI, NW, true>), dim3((unsigned)p.P),
+                       dim3(64 * NW), p.lds, st, a);
+  else
+    hipLaunchKernelGGL((w4_gemv_stream_kernel<T, G, NI, NW, false>), dim3((unsigned)p.P),
+                       dim3(64 * NW), p.lds, st, a);
+}
+template <typename T, int G, int NI>
+static void launch_stream_n(const StreamPlan& p, const GemvStreamArgs& a, hipStream_t st) {
+  if (p.NW == 16)
+    launch_stream_w<T, G, NI, 16>(p, a, st);
+  else
+    launch_stream_w<T, G, NI, 8>(p, a, st);
+}
+template <typename T, int G>
+static void launch_stream_g(const StreamPlan& p, const GemvStreamArgs& a, hipStream_t st) {
+  switch (p.NI) {
+    case 2: launch_stream_n<T, G, 2>(p, a, st); break;
+    case 3: launch_stream_n<T, G, 3>(p, a, st); break;
+    case 4: launch_stream_n<T, G, 4>(p, a, st); break;
+    case 6: launch_stream_n<T, G, 6>(p, a, st); break;
+    default: launch_stream_n<T, G, 8>(p, a, st); break;
+  }
+}
+template <typename T>
+static void launch_stream(const StreamPlan& p, int G, const GemvStreamArgs& a, hipStream_t st) {
+  if (G == 32)
+    launch_stream_g<T, 32>(p, a, st);
+  else if (G == 64)
+    launch_stream_g<T, 64>(p, a, st);
+  else
+    launch_stream_g<T, 128>(p, a, st);
+}
+
 // Workspace of the bf16 GEMM after the counter block: the prologue's
 // scaled fp16 activations, row shifts, scaled scales and bias slots.
 struct GemmX16Layout {
@@ -1409,7 +1719,7 @@ static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
 
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
-  if (plan_gemv(M, N, K, G).ok) return 0;
+  if (plan_stream(M, N, K, G).ok || plan_gemv(M, N, K, G).ok) return 0;
   // every workspace of this entry point starts with the counter block, so a
   // GEMM call never writes over the counters a later split-K call relies on
   if (M <= 32 && M < env_int("SPARKQ_W4_GEMM_FROM", 33)) {
@@ -1532,6 +1842,26 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
   if (need > 0 && (ws == nullptr || wsb < need))
     return set_error(SPARKQ_ERR_WORKSPACE,
                      "w4a16_linear needs a workspace of %zu bytes (got %zu)", need, wsb);
+  const StreamPlan sp = plan_stream(M, N, K, G);
+  if (sp.ok) {
+    GemvStreamArgs a{};
+    a.x = (const uint16_t*)x;
+    a.w = w;
+    a.sc = (const uint16_t*)s;
+    a.bi = (const uint16_t*)b;
+    a.y = y;
+    a.y_dtype = ydt;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.nq = (int)cdiv(N, 4);
+    a.P = sp.P;
+    a.QW = sp.QW;
+    if (xdt == SPARKQ_BF16)
+      launch_stream<BF16>(sp, G, a, st);
+    else
+      launch_stream<F16>(sp, G, a, st);
+    return check_launch("w4_gemv_stream_kernel");
+  }
   const GemvPlan gp = plan_gemv(M, N, K, G);
   if (gp.ok) {
     GemvArgs a{};

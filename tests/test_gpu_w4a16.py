@@ -132,6 +132,21 @@ def test_decode_ragged_shapes(gpu, m, n, k, g):
     check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
 
 
+@pytest.mark.parametrize("n,k,g", [(37, 5632, 64), (36, 3712, 64), (1030, 6144, 128),
+                                   (2600, 3072, 32), (4, 9728, 64)])
+def test_decode_long_rows(gpu, n, k, g):
+    """M = 1 with rows longer than 2560 k takes the streaming kernel (one
+    workgroup per CU, row quads split evenly, items dealt round-robin): a
+    partial last row quad, a partial last span, more row quads than CUs
+    (uneven split) and fewer row quads than CUs."""
+    for dtype in (o.BF16, o.F16):
+        x, wq, s, b = w4_problem(1, n, k, g, dtype=dtype, seed=n + g)
+        ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
+        y32 = _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32).cpu().numpy()
+        check_fp32(y32, ref)
+        check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
+
+
 @pytest.mark.parametrize("g", [32, 64, 128])
 def test_gemm_row_shifts(gpu, g):
     """The bf16 GEMM runs on fp16 operands after per-row power-of-two shifts
