@@ -677,6 +677,253 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
 }
 
 // ---------------------------------------------------------------------------
+// streaming decode GEMV, several activation rows (2 <= M <= 16)
+// ---------------------------------------------------------------------------
+// The M = 1 streaming layout (one workgroup of 16 waves per CU, a contiguous
+// range of row quads per workgroup, 1 KB (row quad, span) items, every
+// weight load issued at the start) with the activation rows taken four at a
+// time: each decoded piece feeds eight 4x4x4 MFMAs per row quartet (MQ
+// quartets), so the decode is shared by all M rows. A wave takes a
+// contiguous run of items in quad-major order and keeps per-lane sums in
+// registers while the row quad stays the same; when it changes (and at the
+// end) the sixteen blocks are added by lane shuffles and the quad's sums go
+// to the LDS slot of the run's first span (the other slots of the run stay
+// zero). Each output is the sum of its quad's slots in span order.
+struct DecodeStreamArgs {
+  const uint16_t* x;
+  const uint32_t* w;
+  const uint16_t* sc;
+  const uint16_t* bi;
+  void* y;
+  int y_dtype;
+  int M, N, K;
+  int nq;  // row quads
+  int P;   // workgroups
+  int QW;  // row quads of the largest workgroup
+};
+
+constexpr int kDecNW = 16;  // waves per workgroup
+constexpr int kDecXP = 2;   // staged activation pieces (64 B) per thread, at most
+constexpr int kDecSP = 2;   // staged (scale, bias) pieces (16 B each) per thread, at most
+
+// LDS layout of the multi-row streaming GEMV (byte offsets)
+struct DecLds {
+  int xp;    // activations [M][K], gemv_xslot order
+  int xs;    // piece sums [K/32][4*MQ] fp32
+  int sb;    // (scale, bias) of the workgroup's rows: [4*QW][K/G] dwords
+  int part;  // quad sums: [QW][U][4][4*MQ] fp32
+  int bytes;
+};
+__host__ __device__ __forceinline__ DecLds dec_lds(int M, int K, int QW, int G, int MQ) {
+  const int U = ((K >> 1) + 255) >> 8;
+  DecLds l;
+  l.xp = 0;
+  l.xs = (M * K * 2 + 1023) & ~1023;
+  l.sb = l.xs + (K / 32) * 16 * MQ;
+  l.part = l.sb + ((4 * QW * (K / G) * 4 + 15) & ~15);
+  l.bytes = l.part + QW * U * 4 * 4 * MQ * 4;
+  return l;
+}
+
+// Sum over the sixteen 4-lane blocks of a wave (lanes j, j+4, ..., j+60):
+// two row rotations inside each 16-lane row (DPP), then the row pairs and the
+// wave halves exchanged with v_permlane16/32_swap (a swap of v with itself
+// leaves each lane's value and its partner's in the two results). Every lane
+// ends with the sum of its j.
+__device__ __forceinline__ float sum_blocks(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+template <typename T, int G, int MQ, int NI, bool FULL>
+__global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStreamArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NT = 64 * kDecNW;
+  constexpr int MR = 4 * MQ;         // activation rows held (rows past M repeat row M-1)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, j = lane & 3;
+  const int M = a.M, N = a.N, K = a.K;
+  const int RB = K >> 1;             // bytes per weight row
+  const int U = (RB + 255) >> 8;     // spans per row
+  const int ng = K / G;              // groups per row
+  const int np = K >> 5;             // 32-k pieces per row
+  const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
+  const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
+  const int nitems = nql * U;
+  const int i0 = (int)((int64_t)wave * nitems / kDecNW);
+  const int nmy = (int)((int64_t)(wave + 1) * nitems / kDecNW) - i0;
+  const DecLds L = dec_lds(M, K, a.QW, G, MQ);
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+
+  // 1. staging loads (a wave with no piece to fetch skips the instruction)
+  const int nxp = M * np;
+  const int nsp = (4 * nql * ng) >> 3;
+  u32x4_t xr[kDecXP][4];
+  u32x4_t sr[kDecSP], br[kDecSP];
+#pragma unroll
+  for (int i = 0; i < kDecXP; ++i) {
+    const int pi = tid + i * NT;
+    if (i * NT + 64 * wave < nxp) {
+      const uint32_t off = pi < nxp ? 64u * pi : kOob;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kDecSP; ++i) {
+    const int pi = tid + i * NT;
+    if (i * NT + 64 * wave < nsp) {
+      const uint32_t off = pi < nsp ? 8u * (uint32_t)qa * ng + 16u * pi : kOob;
+      sr[i] = buf_load16(rs, off);
+      br[i] = buf_load16(rb, off);
+    }
+  }
+
+  // 2. every weight load of the wave (slots past its last item read nothing)
+  int ql[NI], sp[NI];
+  u32x4_t wv[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int it = i0 + i;
+    ql[i] = it / U;
+    sp[i] = it - ql[i] * U;
+    const int row = 4 * (qa + ql[i]) + j, p = 256 * sp[i] + 16 * b;
+    const bool ok = i < nmy && (FULL || (row < N && p + 16 <= RB));
+    wv[i] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
+  }
+
+  // keep every load above ahead of the arithmetic below
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. write the staged data to LDS; clear the quad slots
+  {
+    float* part = reinterpret_cast<float*>(smem + L.part);
+    const int nslot = nql * U * 16 * MQ;
+    for (int e = tid; e < nslot; e += NT) part[e] = 0.0f;
+    uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
+    float* xs = reinterpret_cast<float*>(smem + L.xs);
+#pragma unroll
+    for (int i = 0; i < kDecXP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nxp) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const u32x4_t r = xr[i][w];
+          const u32x4_t o = {__builtin_amdgcn_perm(r.z, r.x, 0x05040100u),   // (x0, x4)
+                             __builtin_amdgcn_perm(r.z, r.x, 0x07060302u),   // (x1, x5)
+                             __builtin_amdgcn_perm(r.w, r.y, 0x05040100u),   // (x2, x6)
+                             __builtin_amdgcn_perm(r.w, r.y, 0x07060302u)};  // (x3, x7)
+          *reinterpret_cast<u32x4_t*>(xp + gemv_xslot(pi, w)) = o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[e], sum);
+        }
+        const int m = pi / np, piece = pi - m * np;
+        xs[piece * MR + m] = sum;
+      }
+    }
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+#pragma unroll
+    for (int i = 0; i < kDecSP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nsp) {
+        const u32x4_t s = sr[i], c = br[i];
+        u32x4_t lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = __builtin_amdgcn_perm(c[e], s[e], 0x05040100u);  // (s0, b0)
+          hi[e] = __builtin_amdgcn_perm(c[e], s[e], 0x07060302u);  // (s1, b1)
+        }
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. the wave's items in order; per-lane sums while the row quad stays
+  const unsigned char* xp = smem + L.xp;
+  const float* xs = reinterpret_cast<const float*>(smem + L.xs);
+  const uint32_t* sb = reinterpret_cast<const uint32_t*>(smem + L.sb);
+  float* part = reinterpret_cast<float*>(smem + L.part);
+  const DecodeConsts dc = decode_consts<T>();
+  f32x4_t acc[MQ];
+#pragma unroll
+  for (int q = 0; q < MQ; ++q) acc[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  int first = nmy > 0 ? sp[0] : 0;   // first span of the current run
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    if (i < nmy) {
+      const int s = sp[i];
+      const int p = 256 * s + 16 * b;
+      const bool ok = FULL || (4 * (qa + ql[i]) + j < N && p + 16 <= RB);
+      const int piece = FULL ? 16 * s + b : min(16 * s + b, np - 1);
+      // pieces past the row end carry zero codes and unrelated activations
+      const uint32_t pair = ok ? sb[(4 * ql[i] + j) * ng + (2 * p) / G] : 0u;
+      const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
+      const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
+      uint32_t pr[4][4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) decode_w4_strided<T>(wv[i][w], dc, pr[w]);
+#pragma unroll
+      for (int q = 0; q < MQ; ++q) {
+        const int pi = min(4 * q + j, M - 1) * np + piece;
+        f32x4_t d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = d0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xp + 4 * gemv_xslot(pi, w));
+          d0 = mfma4x4<T>(v.x, v.y, pr[w][0], pr[w][1], d0);
+          d1 = mfma4x4<T>(v.z, v.w, pr[w][2], pr[w][3], d1);
+        }
+        const f32x4_t xm = *reinterpret_cast<const f32x4_t*>(xs + piece * MR + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float t = fmaf(sf, d0[e] + d1[e], bf * xm[e]);
+          acc[q][e] += ok ? t : 0.0f;
+        }
+      }
+      // end of a run: next item in another row quad, or the wave's last
+      const bool last = i + 1 >= nmy || (i + 1 < NI && ql[i + 1] != ql[i]);
+      if (last) {
+        float* dst = part + ((ql[i] * U + first) * 4) * MR;
+#pragma unroll
+        for (int q = 0; q < MQ; ++q) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = sum_blocks(acc[q][e]);
+            if (lane < 4) dst[lane * MR + 4 * q + e] = v;
+          }
+          acc[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (i + 1 < NI) first = sp[i + 1];
+      }
+    }
+  }
+  __syncthreads();
+
+  // 5. each output: the sum of its quad's slots in span order
+  for (int t = tid; t < 4 * nql * M; t += NT) {
+    const int rl = t / M, m = t - rl * M;
+    const int row = 4 * qa + rl;
+    if (row < N) {
+      const float* src = part + (((rl >> 2) * U) * 4 + (rl & 3)) * MR + m;
+      float v = 0.0f;
+      for (int s = 0; s < U; ++s) v += src[s * 4 * MR];
+      store_out(a.y, (int64_t)m * N + row, v, a.y_dtype);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // skinny kernel (M <= MB <= 32)
 // ---------------------------------------------------------------------------
 // Workgroup = 4 waves; tile = 32 weight rows; the workgroup's K range (a
@@ -1678,6 +1925,82 @@ static void launch_stream(const StreamPlan& p, int G, const GemvStreamArgs& a, h
     launch_stream_g<T, 128>(p, a, st);
 }
 
+// Multi-row streaming plan (2 <= M <= 16): the layout of plan_stream with
+// all M activation rows staged per workgroup. K % 512 == 0 and N % 4 == 0
+// (whole spans and row quads); LDS up to 160 KB.
+struct DecPlan {
+  bool ok;
+  int P, QW, MQ, NI;
+  size_t lds;
+};
+
+constexpr int kDecMaxLds = 160 * 1024;
+
+static DecPlan plan_dec(int64_t M, int64_t N, int64_t K, int G) {
+  DecPlan p{};
+  if (M < 2 || M > 16 || env_int("SPARKQ_W4_NO_DEC", 0)) return p;
+  if (K % 512 != 0 || N % 4 != 0) return p;
+  // Up to four rows of at most 5 spans keep w4_gemv_kernel (measured at
+  // M = 4: QKV 3584x2560 4.5 against 5.2 us here, gate+up 19456x2560 11.1
+  // against 11.4 us); longer rows (down 2560x9728: 12.0 -> 9.0 us) and more
+  // rows (M = 8: QKV 8.6 -> 6.8 us, gate+up 17.9 -> 16.4 us) come here.
+  if (M <= 4 && K <= 2560 && !env_int("SPARKQ_W4_DEC_ALL", 0)) return p;
+  if (N * (K / 2) >= (int64_t)kOob || M * K * 2 >= (int64_t)kOob) return p;
+  const int64_t ng = K / G;
+  if (ng % 2 != 0 || (N * ng * 2) % 16 != 0) return p;
+  const int64_t nq = N / 4, U = K / 512;
+  p.P = (int)std::min<int64_t>(nq, device_cus());
+  p.QW = (int)cdiv(nq, p.P);
+  p.MQ = (int)cdiv(M, 4);
+  const int64_t ni = cdiv(p.QW * U, kDecNW);
+  if (ni > 8) return p;
+  p.NI = ni <= 2 ? 2 : (ni <= 4 ? 4 : 8);
+  const int64_t nt = 64 * kDecNW;
+  if (M * (K / 32) > kDecXP * nt || 4 * p.QW * ng / 8 > kDecSP * nt) return p;
+  const DecLds l = dec_lds((int)M, (int)K, p.QW, G, p.MQ);
+  if (l.bytes > kDecMaxLds) return p;
+  p.lds = (size_t)l.bytes;
+  p.ok = true;
+  return p;
+}
+
+template <typename T, int G, int MQ, int NI>
+static void launch_dec_n(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {
+  auto* k = w4_decode_stream_kernel<T, G, MQ, NI, true>;
+  // dynamic LDS above 64 KB must be enabled per kernel
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, kDecMaxLds);
+  (void)attr;
+  hipLaunchKernelGGL(k, dim3((unsigned)p.P), dim3(64 * kDecNW), p.lds, st, a);
+}
+template <typename T, int G, int MQ>
+static void launch_dec_m(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {
+  if (p.NI == 2)
+    launch_dec_n<T, G, MQ, 2>(p, a, st);
+  else if (p.NI == 4)
+    launch_dec_n<T, G, MQ, 4>(p, a, st);
+  else
+    launch_dec_n<T, G, MQ, 8>(p, a, st);
+}
+template <typename T, int G>
+static void launch_dec_g(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {
+  switch (p.MQ) {
+    case 1: launch_dec_m<T, G, 1>(p, a, st); break;
+    case 2: launch_dec_m<T, G, 2>(p, a, st); break;
+    case 3: launch_dec_m<T, G, 3>(p, a, st); break;
+    default: launch_dec_m<T, G, 4>(p, a, st); break;
+  }
+}
+template <typename T>
+static void launch_dec(const DecPlan& p, int G, const DecodeStreamArgs& a, hipStream_t st) {
+  if (G == 32)
+    launch_dec_g<T, 32>(p, a, st);
+  else if (G == 64)
+    launch_dec_g<T, 64>(p, a, st);
+  else
+    launch_dec_g<T, 128>(p, a, st);
+}
+
 // Workspace of the bf16 GEMM after the counter block: the prologue's
 // scaled fp16 activations, row shifts, scaled scales and bias slots.
 struct GemmX16Layout {
@@ -1719,7 +2042,7 @@ static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
 
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
-  if (plan_stream(M, N, K, G).ok || plan_gemv(M, N, K, G).ok) return 0;
+  if (plan_stream(M, N, K, G).ok || plan_dec(M, N, K, G).ok || plan_gemv(M, N, K, G).ok) return 0;
   // every workspace of this entry point starts with the counter block, so a
   // GEMM call never writes over the counters a later split-K call relies on
   if (M <= 32 && M < env_int("SPARKQ_W4_GEMM_FROM", 33)) {
@@ -1861,6 +2184,27 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     else
       launch_stream<F16>(sp, G, a, st);
     return check_launch("w4_gemv_stream_kernel");
+  }
+  const DecPlan dp = plan_dec(M, N, K, G);
+  if (dp.ok) {
+    DecodeStreamArgs a{};
+    a.x = (const uint16_t*)x;
+    a.w = w;
+    a.sc = (const uint16_t*)s;
+    a.bi = (const uint16_t*)b;
+    a.y = y;
+    a.y_dtype = ydt;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.nq = (int)(N / 4);
+    a.P = dp.P;
+    a.QW = dp.QW;
+    if (xdt == SPARKQ_BF16)
+      launch_dec<BF16>(dp, G, a, st);
+    else
+      launch_dec<F16>(dp, G, a, st);
+    return check_launch("w4_decode_stream_kernel");
   }
   const GemvPlan gp = plan_gemv(M, N, K, G);
   if (gp.ok) {

@@ -147,6 +147,19 @@ def test_decode_long_rows(gpu, n, k, g):
         check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
 
 
+@pytest.mark.parametrize("m,n,k,g", [(3, 1100, 4096, 64), (5, 1100, 3072, 32), (12, 260, 1536, 128),
+                                     (16, 1028, 2048, 64), (2, 8, 9728, 64)])
+def test_decode_multirow_stream(gpu, m, n, k, g):
+    """2 <= M <= 16 on the multi-row streaming kernel: more row quads than
+    CUs (uneven split), fewer, a row-quad count below the wave count, M not a
+    multiple of 4 (the last row quartet repeats row M-1) and long rows."""
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m * n)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    check_fp32(y32, ref)
+    check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
+
+
 @pytest.mark.parametrize("g", [32, 64, 128])
 def test_gemm_row_shifts(gpu, g):
     """The bf16 GEMM runs on fp16 operands after per-row power-of-two shifts
