@@ -221,6 +221,30 @@ __host__ __device__ __forceinline__ GemvLds gemv_lds(int M, int K, int R, int G,
   return l;
 }
 
+// Sum over the sixteen 4-lane blocks of a wave (lanes j, j+4, ..., j+60):
+// two row rotations inside each 16-lane row (DPP), then the row pairs and the
+// wave halves exchanged with v_permlane16/32_swap (a swap of v with itself
+// leaves each lane's value and its partner's in the two results). Every lane
+// ends with the sum of its j.
+__device__ __forceinline__ float sum_blocks(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// Sum over the 16 lanes of each 16-lane row: four DPP row rotations, each
+// doubling the window.
+__device__ __forceinline__ float sum_row16(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  return v;
+}
+
 template <typename T, int G, int MQ, int US, int RQW, int NW>
 __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -409,14 +433,7 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
     }
     // sum the sixteen blocks (lanes j, j+4, ..., j+60)
 #pragma unroll
-    for (int m = 0; m < MQ; ++m) {
-      float v = acc[m];
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      out[r][m] = v;
-    }
+    for (int m = 0; m < MQ; ++m) out[r][m] = sum_blocks(acc[m]);
   }
 
   if (SG > 1) {
@@ -667,10 +684,7 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
       const float* src = part + (rl >> 2) * U * 64 + 4 * bb + (rl & 3);
       for (int s = 0; s < U; ++s) v += src[s * 64];
     }
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 8);
+    v = sum_row16(v);
     const int row = 4 * qa + rl;
     if (bb == 0 && rl < 4 * nql && row < N) store_out(a.y, row, v, a.y_dtype);
   }
@@ -723,20 +737,6 @@ __host__ __device__ __forceinline__ DecLds dec_lds(int M, int K, int QW, int G, 
   l.part = l.sb + ((4 * QW * (K / G) * 4 + 15) & ~15);
   l.bytes = l.part + QW * U * 4 * 4 * MQ * 4;
   return l;
-}
-
-// Sum over the sixteen 4-lane blocks of a wave (lanes j, j+4, ..., j+60):
-// two row rotations inside each 16-lane row (DPP), then the row pairs and the
-// wave halves exchanged with v_permlane16/32_swap (a swap of v with itself
-// leaves each lane's value and its partner's in the two results). Every lane
-// ends with the sum of its j.
-__device__ __forceinline__ float sum_blocks(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
-  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
 template <typename T, int G, int MQ, int NI, bool FULL>
