@@ -122,6 +122,30 @@ __device__ __forceinline__ u32x4_t decode_w4(uint32_t w, DecodeConsts c) {
 }
 
 // ---------------------------------------------------------------------------
+// reductions over the 16 lanes of each 16-lane row (DPP row rotations by 1,
+// 2, 4 and 8, each doubling the window; every lane ends with the result).
+// All lanes of the wave must be active.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum_row16(float v) {
+  v += dpp_row<0x121>(v);
+  v += dpp_row<0x122>(v);
+  v += dpp_row<0x124>(v);
+  v += dpp_row<0x128>(v);
+  return v;
+}
+__device__ __forceinline__ float max_row16(float v) {
+  v = fmaxf(v, dpp_row<0x121>(v));
+  v = fmaxf(v, dpp_row<0x122>(v));
+  v = fmaxf(v, dpp_row<0x124>(v));
+  v = fmaxf(v, dpp_row<0x128>(v));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
 // buffer loads: a load whose offset lies outside the buffer returns zero and
 // touches no memory, so a lane that has nothing to read gets zeros without a
 // branch (a branch around a load makes the compiler wait for the load where

@@ -425,11 +425,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
     for (int r = 0; r < 4; ++r) {
       const float s0 = ok0 ? (sc[0][r] - qcorr[r]) * ksc0 * qmul[r] : kNegInf;
       const float s1 = ok1 ? (sc[1][r] - qcorr[r]) * ksc1 * qmul[r] : kNegInf;
-      float mb = fmaxf(s0, s1);
-      mb = fmaxf(mb, __shfl_xor(mb, 1));
-      mb = fmaxf(mb, __shfl_xor(mb, 2));
-      mb = fmaxf(mb, __shfl_xor(mb, 4));
-      mb = fmaxf(mb, __shfl_xor(mb, 8));
+      float mb = max_row16(fmaxf(s0, s1));
       mb = fmaxf(mb, mrun[r]);
       alpha[r] = exp2_guarded(mrun[r] - mb, mrun[r] != kNegInf);
       mrun[r] = mb;
@@ -476,11 +472,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
   // per-lane partial sums -> the 16 token lanes of each head group
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      zl[r] += __shfl_xor(zl[r], o);
-      psl[r] += __shfl_xor(psl[r], o);
-    }
+    zl[r] = sum_row16(zl[r]);
+    psl[r] = sum_row16(psl[r]);
   }
 
   // combine the waves through LDS (the loop's LDS is free after the barrier)

@@ -235,16 +235,6 @@ __device__ __forceinline__ float sum_blocks(float v) {
   return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
-// Sum over the 16 lanes of each 16-lane row: four DPP row rotations, each
-// doubling the window.
-__device__ __forceinline__ float sum_row16(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
-  return v;
-}
-
 template <typename T, int G, int MQ, int US, int RQW, int NW>
 __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
