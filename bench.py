@@ -165,6 +165,33 @@ def bench_w8a8(torch, sparkq, dev, m, iters, copies=36):
     return res
 
 
+def bench_w8a16(torch, sparkq, dev, iters):
+    """W8A16 per-channel GEMV at M=1: the projections (36 distinct weight
+    sets) and the W8 lm_head 131072 x 2560 (335 MB, 3 distinct copies)."""
+    res = {}
+    gen = torch.Generator(device=dev).manual_seed(2)
+    shapes = dict(PROJ)
+    shapes["lm_head"] = (131072, 2560)
+    for name, (n, k) in shapes.items():
+        copies = 3 if name == "lm_head" else 36
+        ws = [(torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=gen),
+               torch.rand(n, device=dev, generator=gen) * 1e-3) for _ in range(copies)]
+        x = torch.randn((1, k), device=dev).to(torch.bfloat16)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+
+        def fn():
+            for q, sc in ws:
+                sparkq.w8a16_per_channel(x, q, sc, out=y)
+
+        graph = capture(torch, fn)
+        ms = Timer(torch).time(graph.replay, iters, 2) / copies
+        nbytes = n * k + 4 * n
+        res[name] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+                     "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        del ws, graph
+    return res
+
+
 def bench_sdpa(torch, sparkq, dev, b, n, iters):
     hq, hkv, d = 32, 8, 128
     kv_bytes = 2 * b * hkv * n * d + 2 * b * hkv * n * 2
@@ -329,6 +356,8 @@ def main():
         extras["w4a16_prefill_gemm"] = gemm
         log("W8A8")
         extras["w8a8"] = {f"M={m}": bench_w8a8(torch, sparkq, dev, m, 5) for m in (1, 8, 16)}
+        log("W8A16")
+        extras["w8a16_m1"] = bench_w8a16(torch, sparkq, dev, 5)
         log("INT8-KV decode attention")
         extras["int8kv_sdpa_decode"] = {f"B={b} N={n}": bench_sdpa(torch, sparkq, dev, b, n, 5)
                                         for b in (1, 8) for n in (4096, 32768)}

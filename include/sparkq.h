@@ -159,6 +159,22 @@ int sparkq_w8a8_linear(const void* x, const int8_t* w, const float* w_scales,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * W8A16: per-channel int8 weights, 16-bit activations (decode, M <= 4)
+ * y[m,n] = to_dtype(scale[n] * sum_k x[m,k] * w[n,k]), the dot in fp32.
+ *   x       [M,K]  x_dtype (BF16 or F16)
+ *   w       [N,K]  int8
+ *   scales  [N]    fp32
+ *   y       [M,N]  y_dtype (x_dtype, or F32 for the unrounded epilogue)
+ * K % 16 == 0 and M*K <= 32768. Replaces w8a16_per_channel
+ * (X/src/spark_w8a16.cpp:80-110, bindings X/src/bindings.cpp:17; kernel
+ * X/src/kernels/w8a16_matvec.metal:12-31), which takes one activation row;
+ * rows 2..4 are this build's extension for short verify batches.
+ * ---------------------------------------------------------------------- */
+int sparkq_w8a16_linear(const void* x, const int8_t* w, const float* scales,
+                        void* y, int64_t M, int64_t N, int64_t K, int x_dtype,
+                        int y_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * INT8-KV GQA decode attention (one query token per sequence)
  *   q    [B,Hq,D] (the L=1 axis of [B,Hq,1,D] dropped), q_dtype
  *   out  [B,Hq,D], out_dtype (q_dtype, or F32 for the unrounded epilogue)

@@ -18,7 +18,7 @@ __all__ = [
     "bf16_bits", "bits_to_f32", "f16_bits", "round16",
     "randn", "randn16",
     "pack4", "unpack4", "w4_quantize", "w4_quantize_converter",
-    "w4_dequantize", "w4a16_matmul",
+    "w4_dequantize", "w4a16_matmul", "w8a16_matmul",
     "a8_quantize", "w8_quantize_channel", "w8_unpack_affine",
     "int8_matmul", "w8a8_epilogue",
     "kv_quantize_s8", "kv_quantize_affine_u8", "kv_dequantize_s8",
@@ -77,6 +77,7 @@ def _declare(lib):
         "sq_w4_quantize_converter": (None, [P, I64, I64, I, P, P, P]),
         "sq_w4_dequantize": (None, [P, P, P, I64, I64, I, I, P]),
         "sq_w4a16_matmul": (None, [P, I, P, P, P, I64, I64, I64, I, P]),
+        "sq_w8a16_matmul": (None, [P, I, P, P, I64, I64, I64, P]),
         "sq_a8_quantize": (None, [P, I64, I64, P, P]),
         "sq_w8_quantize_channel": (None, [P, I64, I64, P, P]),
         "sq_w8_unpack_affine": (None, [P, I64, I64, P]),
@@ -215,6 +216,16 @@ def w4a16_matmul(x16, wq, s, b, group_size: int, dtype: int = BF16) -> np.ndarra
     y = np.empty((m, n), np.float64)
     _lib().sq_w4a16_matmul(_p(x16), dtype, _p(wq), _p(s), _p(b), m, n, k,
                            group_size, _p(y))
+    return y
+
+
+def w8a16_matmul(x16, w8, scales, dtype: int = BF16) -> np.ndarray:
+    """scale[n] * sum_k x[m,k] * w[n,k] in float64 (w8a16_per_channel)."""
+    x16, w8, sc = _c(x16, np.uint16), _c(w8, np.int8), _c(scales, np.float32)
+    m, k = x16.shape
+    n = w8.shape[0]
+    y = np.empty((m, n), np.float64)
+    _lib().sq_w8a16_matmul(_p(x16), dtype, _p(w8), _p(sc), m, n, k, _p(y))
     return y
 
 

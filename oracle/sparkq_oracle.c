@@ -239,6 +239,20 @@ void sq_w4a16_matmul(const uint16_t* x, int xdtype, const uint32_t* wq,
   }
 }
 
+/* X/src/kernels/w8a16_matvec.metal:12-31 (sum, then times the scale) */
+void sq_w8a16_matmul(const uint16_t* x, int xdtype, const int8_t* w,
+                     const float* scales, int64_t M, int64_t N, int64_t K,
+                     double* y) {
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t m = 0; m < M; ++m) {
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k)
+        acc += (double)sq_widen16(x[m * K + k], xdtype) * (double)w[n * K + k];
+      y[m * N + n] = acc * (double)scales[n];
+    }
+  }
+}
+
 /* ------------------------------------------------------------------------ */
 /* W8A8                                                                      */
 /* ------------------------------------------------------------------------ */

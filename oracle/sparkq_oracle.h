@@ -87,6 +87,15 @@ void sq_w4a16_matmul(const uint16_t* x, int xdtype, const uint32_t* wq,
                      const uint16_t* scales, const uint16_t* biases,
                      int64_t M, int64_t N, int64_t K, int G, double* y);
 
+/* --- W8A16 ------------------------------------------------------------- */
+/* y[m,n] = scale[n] * sum_k x[m,k] * w[n,k] in fp64: the fp32 dot times the
+ * channel scale of w8a16_per_channel (X/src/kernels/w8a16_matvec.metal:
+ * 12-31), computed exactly enough to serve as its reference. x is [M,K]
+ * 16-bit in xdtype, w [N,K] int8, scales [N] fp32. */
+void sq_w8a16_matmul(const uint16_t* x, int xdtype, const int8_t* w,
+                     const float* scales, int64_t M, int64_t N, int64_t K,
+                     double* y);
+
 /* --- W8A8 -------------------------------------------------------------- */
 /* Per-token quantizer, X/src/kernels/w8a8_quantize.metal:11-27:
  * amax = max|x|; scale = amax > 0 ? amax/127 : 1; q = clamp(rint(x/scale),

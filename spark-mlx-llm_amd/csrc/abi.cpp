@@ -41,6 +41,8 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
                        size_t wsb, hipStream_t st);
 int kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_t D, int xdt,
                    hipStream_t st);
+int w8a16_linear(const void* x, const int8_t* w, const float* scales, void* y, int64_t M,
+                 int64_t N, int64_t K, int xdt, int ydt, hipStream_t st);
 
 static thread_local char g_last_error[512] = "";
 
@@ -290,6 +292,26 @@ int sparkq_kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R,
   REQUIRE(is_float_dtype(x_dtype), "kv_quantize_s8: x must be float16, bfloat16 or float32");
   DEVICE_OK();
   return kv_quantize_s8(x, codes, scales, R, D, x_dtype, (hipStream_t)stream);
+}
+
+// Mirrors the checks of w8a16_per_channel (X/src/spark_w8a16.cpp:80-104).
+int sparkq_w8a16_linear(const void* x, const int8_t* w, const float* scales, void* y, int64_t M,
+                        int64_t N, int64_t K, int x_dtype, int y_dtype, void* stream) {
+  REQUIRE(x && w && scales && y, "w8a16_linear: null tensor pointer");
+  REQUIRE(M > 0 && N > 0 && K > 0,
+          "w8a16_per_channel requires one activation row x[..., K] with singleton leading "
+          "dimensions and nonempty weight[N, K].");
+  REQUIRE(N <= kI32Max && K <= kI32Max, "w8a16_linear: dimension too large");
+  REQUIRE(is_half_dtype(x_dtype), "w8a16_per_channel x must have dtype bfloat16 or float16.");
+  REQUIRE(y_dtype == x_dtype || y_dtype == SPARKQ_F32,
+          "w8a16_linear: y dtype must equal x dtype or be float32");
+  REQUIRE_SUPPORTED(M <= 4, "w8a16_linear: at most 4 activation rows (got %lld)", (long long)M);
+  REQUIRE_SUPPORTED(K % 16 == 0, "w8a16_linear: K must be a multiple of 16 (got %lld)",
+                    (long long)K);
+  REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(scales, 4) && aligned(y, 4),
+          "w8a16_linear: x and w must be 16-byte aligned");
+  DEVICE_OK();
+  return w8a16_linear(x, w, scales, y, M, N, K, x_dtype, y_dtype, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -146,6 +146,75 @@ __device__ __forceinline__ float max_row16(float v) {
 }
 
 // ---------------------------------------------------------------------------
+// 4x4x4 MFMA blocks, pair sums and the strided 4-bit decode shared by the
+// decode GEMVs
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma4x4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
+                                           f32x4_t c);
+template <>
+__device__ __forceinline__ f32x4_t mfma4x4<BF16>(uint32_t a0, uint32_t a1, uint32_t b0,
+                                                 uint32_t b1, f32x4_t c) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4_t, u32x2_t{a0, a1}),
+                                                __builtin_bit_cast(s16x4_t, u32x2_t{b0, b1}), c,
+                                                0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4_t mfma4x4<F16>(uint32_t a0, uint32_t a1, uint32_t b0,
+                                                uint32_t b1, f32x4_t c) {
+  typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4_t, u32x2_t{a0, a1}),
+                                            __builtin_bit_cast(f16x4_t, u32x2_t{b0, b1}), c, 0,
+                                            0, 0);
+}
+
+// sum of the two 16-bit values of a packed pair, in fp32
+template <typename T>
+__device__ __forceinline__ float pair_sum(uint32_t p, float acc);
+template <>
+__device__ __forceinline__ float pair_sum<BF16>(uint32_t p, float acc) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, p),
+                                         __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
+template <>
+__device__ __forceinline__ float pair_sum<F16>(uint32_t p, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, p),
+                                __builtin_bit_cast(f16x2_t, 0x3C003C00u), acc, false);
+}
+
+// Decode one word of eight codes into the pairs (q[j], q[j+4]), j = 0..3, as
+// OFFSET+q 16-bit values: pair j is ((w >> 4j) & 0x000F000F) | MAGIC.
+template <typename T>
+__device__ __forceinline__ void decode_w4_strided(uint32_t w, DecodeConsts c, uint32_t p[4]) {
+  p[0] = (w & c.mask) | c.magic;
+  p[1] = ((w >> 4) & c.mask) | c.magic;
+  p[2] = ((w >> 8) & c.mask) | c.magic;
+  p[3] = ((w >> 12) & c.mask) | c.magic;
+  if constexpr (T::kExactDecode) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = exact_f16_pair(p[i]);
+  }
+}
+
+// Sum over the sixteen 4-lane blocks of a wave (lanes j, j+4, ..., j+60):
+// two row rotations inside each 16-lane row (DPP), then the row pairs and the
+// wave halves exchanged with v_permlane16/32_swap (a swap of v with itself
+// leaves each lane's value and its partner's in the two results). Every lane
+// ends with the sum of its j.
+__device__ __forceinline__ float sum_blocks(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// ---------------------------------------------------------------------------
 // buffer loads: a load whose offset lies outside the buffer returns zero and
 // touches no memory, so a lane that has nothing to read gets zeros without a
 // branch (a branch around a load makes the compiler wait for the load where

@@ -18,6 +18,7 @@ from .ext import (
     quantize_per_token,
     w4a16_multirow,
     w4a16_qmv,
+    w8a16_per_channel,
     w8a8_linear,
 )
 
@@ -34,5 +35,6 @@ __all__ = [
     "quantize_per_token",
     "w4a16_multirow",
     "w4a16_qmv",
+    "w8a16_per_channel",
     "w8a8_linear",
 ]

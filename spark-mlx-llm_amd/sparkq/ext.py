@@ -34,6 +34,7 @@ __all__ = [
     "quantize_per_token",
     "w4a16_multirow",
     "w4a16_qmv",
+    "w8a16_per_channel",
     "w8a8_linear",
 ]
 
@@ -331,6 +332,42 @@ class W8A8Linear(nn.Module):
     def extra_repr(self) -> str:
         return (f"input_dims={self.input_dims}, output_dims={self.output_dims}, "
                 f"bias={self.bias is not None}")
+
+
+# ---------------------------------------------------------------------------
+# W8A16
+# ---------------------------------------------------------------------------
+
+def w8a16_per_channel(x, weight, scales, *, stream=None, out_dtype=None, out=None):
+    """Signed int8 weights [N,K] with an fp32 scale per output channel times
+    16-bit activations: y = T(scale[n] * sum_k x[k] * w[n,k])
+    (X/src/spark_w8a16.cpp:80-110; checks as there). The reference takes one
+    activation row; up to 4 rows are accepted here (short verify batches)."""
+    if (x.ndim < 1 or weight.ndim != 2 or x.shape[-1] <= 0 or weight.shape[0] <= 0
+            or weight.shape[1] != x.shape[-1] or not 1 <= x.numel() // x.shape[-1] <= 4):
+        raise ValueError(
+            "w8a16_per_channel requires one activation row x[..., K] with singleton leading "
+            "dimensions and nonempty weight[N, K].")
+    if x.dtype not in _HALF:
+        raise ValueError("w8a16_per_channel x must have dtype bfloat16 or float16.")
+    if weight.dtype != torch.int8:
+        raise ValueError("w8a16_per_channel weight must have dtype int8.")
+    n, k = weight.shape
+    if scales.dtype != torch.float32 or tuple(scales.shape) not in ((n,), (n, 1)):
+        raise ValueError(
+            "w8a16_per_channel scales must have dtype float32 and shape [N] or [N, 1].")
+    _require_device("w8a16_per_channel", x, weight, scales)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (x.dtype, torch.float32):
+        raise ValueError("out_dtype must be x.dtype or torch.float32")
+    lead = x.shape[:-1]
+    m = prod(lead)
+    x2 = x.reshape(m, k).contiguous()
+    y = _out_buffer(out, (m, n), out_dtype, x.device)
+    weight, scales = weight.contiguous(), scales.reshape(n).contiguous()
+    _lib.call("sparkq_w8a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(y), m, n, k,
+              _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), _lib.stream_handle(x.device))
+    return y.reshape(*lead, n)
 
 
 # ---------------------------------------------------------------------------

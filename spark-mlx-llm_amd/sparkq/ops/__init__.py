@@ -5,6 +5,7 @@ from .linear import (
     AffineParameters,
     LinearConfig,
     QuantizedLinear,
+    W8A16PerChannelLinear,
     W8A8Projection,
     W8A8QuantizedLinear,
     dispatch_linear,
@@ -17,6 +18,7 @@ __all__ = [
     "OperatorConfig",
     "QuantizedLinear",
     "SDPAConfig",
+    "W8A16PerChannelLinear",
     "W8A8Projection",
     "W8A8QuantizedLinear",
     "dispatch_linear",

@@ -24,6 +24,7 @@ __all__ = [
     "AffineParameters",
     "LinearConfig",
     "QuantizedLinear",
+    "W8A16PerChannelLinear",
     "W8A8Projection",
     "W8A8QuantizedLinear",
     "dispatch_linear",
@@ -254,6 +255,44 @@ class W8A8QuantizedLinear(nn.Module):
     def forward(self, x):
         w8, sc = self.prepare_parameters()
         return ext.w8a8_linear(x, w8, sc, self.bias)
+
+
+class W8A16PerChannelLinear(nn.Module):
+    """Single-row W8A16 projection with the affine W8 layer kept as the
+    fallback for other inputs (spark_mlx_llm/ops/linear.py:413-476): signed
+    int8 weight [N,K] and fp32 channel scales [N] or [N,1] derived from the
+    fallback's packed weights (unpack_affine_w8)."""
+
+    def __init__(self, fallback, weight, scales):
+        super().__init__()
+        fb_w = getattr(fallback, "weight", None)
+        if (getattr(fallback, "mode", None) != "affine" or getattr(fallback, "bits", None) != 8
+                or getattr(fallback, "biases", None) is None
+                or getattr(fallback, "bias", None) is not None):
+            raise ValueError("W8A16 fallback must be a bias-free affine W8 QuantizedLinear")
+        if (weight.ndim != 2 or weight.dtype != torch.int8 or fb_w is None
+                or tuple(weight.shape) != (fb_w.shape[0], fb_w.shape[1] * 4)
+                or scales.dtype != torch.float32
+                or tuple(scales.shape) not in ((weight.shape[0],), (weight.shape[0], 1))):
+            raise ValueError("W8A16 needs matching signed INT8 [N,K] and FP32 [N] scales")
+        self.fallback = fallback
+        self.register_buffer("weight", weight.contiguous())
+        self.register_buffer("scales", scales.reshape(-1).contiguous())
+        self.requires_grad_(False)
+
+    def forward(self, x):
+        if x.ndim >= 1 and x.shape[-1] > 0 and self.supports_rows(x.numel() // x.shape[-1],
+                                                                    x.dtype, x):
+            return self.matmul(x, self.weight, self.scales)
+        return self.fallback(x)
+
+    @staticmethod
+    def supports_rows(num_rows, dtype, x=None):
+        return num_rows == 1 and dtype in _HALF and (x is None or _on_gfx950(x))
+
+    @staticmethod
+    def matmul(x, weight, scales):
+        return ext.w8a16_per_channel(x, weight, scales)
 
 
 class W8A8Projection(nn.Module):

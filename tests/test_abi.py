@@ -99,6 +99,13 @@ def test_invalid_arguments_rejected_without_a_device():
                   dummy, 1, 8, 8, 16, 128, 32, 0, 2, 2, ctypes.c_float(float("inf")), st,
                   None, 0, None)
     assert rc == -1 and "finite" in msg
+    # W8A16: fp32 activations, more than 4 rows, K not a multiple of 16
+    rc, msg = _rc("sparkq_w8a16_linear", dummy, dummy, dummy, dummy, 1, 64, 64, 0, 0, None)
+    assert rc == -1 and "bfloat16 or float16" in msg
+    rc, msg = _rc("sparkq_w8a16_linear", dummy, dummy, dummy, dummy, 5, 64, 64, 2, 2, None)
+    assert rc == -2 and "4 activation rows" in msg
+    rc, msg = _rc("sparkq_w8a16_linear", dummy, dummy, dummy, dummy, 1, 64, 40, 2, 2, None)
+    assert rc == -2 and "multiple of 16" in msg
 
 
 def test_status_maps_to_reference_exceptions():

@@ -122,3 +122,31 @@ def test_package_surface():
     for name in sparkq.__all__:
         assert callable(getattr(sparkq, name))
     assert sparkq.prepare_w4a16_nax4(1, 2, 3) == (1, 2, 3)
+
+
+def test_w8a16_layer_contract():
+    """W8A16PerChannelLinear (spark_mlx_llm/ops/linear.py:413-476): needs a
+    bias-free affine W8 fallback and matching int8 [N,K] / fp32 [N] inputs;
+    serves single 16-bit rows on the device only."""
+    from sparkq.ops import W8A16PerChannelLinear
+
+    n, k = 16, 64
+    fb = QuantizedLinear(torch.zeros((n, k // 4), dtype=torch.int32),
+                         torch.ones((n, k // 32), dtype=torch.bfloat16),
+                         torch.full((n, k // 32), -128.0, dtype=torch.bfloat16),
+                         group_size=32, bits=8)
+    w8 = torch.zeros((n, k), dtype=torch.int8)
+    sc = torch.ones(n, dtype=torch.float32)
+    layer = W8A16PerChannelLinear(fb, w8, sc)
+    assert layer.scales.shape == (n,)
+    with pytest.raises(ValueError, match="matching signed INT8"):
+        W8A16PerChannelLinear(fb, w8.to(torch.int16), sc)
+    with pytest.raises(ValueError, match="matching signed INT8"):
+        W8A16PerChannelLinear(fb, torch.zeros((n, k + 4), dtype=torch.int8), sc)
+    with pytest.raises(ValueError, match="bias-free affine W8"):
+        W8A16PerChannelLinear(_layer(), w8, sc)
+    assert W8A16PerChannelLinear.supports_rows(1, torch.bfloat16)
+    assert not W8A16PerChannelLinear.supports_rows(2, torch.bfloat16)
+    assert not W8A16PerChannelLinear.supports_rows(1, torch.float32)
+    assert not W8A16PerChannelLinear.supports_rows(1, torch.bfloat16,
+                                                   torch.zeros(1, k, dtype=torch.bfloat16))
