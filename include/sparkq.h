@@ -73,15 +73,20 @@ int sparkq_is_available(void);
  *   biases  [N,K/G] x_dtype
  *   y       [M,N]   y_dtype (x_dtype, or F32 for the unrounded epilogue)
  * group_size in {32, 64, 128}; bits must be 4; K % 64 == 0; K % G == 0.
- * Dispatches internally: M <= 4 runs the decode GEMV (whole rows per
- * workgroup, 4x4x4 MFMA blocks, no workspace) when the shape fits its LDS
- * budget (K <= 10240 for M = 1); other M <= 32 run the weight-streaming skinny
- * kernel (MFMA 32x32x16; when the shape splits K across workgroups the last
- * workgroup of each 32-row tile combines the partials in the same launch);
- * larger M runs the MFMA GEMM behind a prologue (bf16: exact fp16 operands
- * under power-of-two row shifts, with the bias term as extra MFMA slots, and
- * an in-launch split-K for long rows; fp16: a group-sum prologue and a
- * per-group fp32 epilogue).
+ * Dispatches internally (no workspace for the first three):
+ *   - M = 1, rows longer than 2560 k: the streaming GEMV (one workgroup per
+ *     CU, 4x4x4 MFMA blocks, activations staged once per CU);
+ *   - 2 <= M <= 16 with K % 512 == 0 and N % 4 == 0 (except M <= 4 with
+ *     K <= 2560), when the M activation rows fit LDS: the multi-row
+ *     streaming GEMV (one decode shared by all row quartets);
+ *   - otherwise M <= 4 within the LDS budget: the whole-row decode GEMV;
+ *   - other M <= 32: the weight-streaming skinny kernel (MFMA 32x32x16; when
+ *     the shape splits K across workgroups the last workgroup of each 32-row
+ *     tile combines the partials in the same launch);
+ *   - larger M: the MFMA GEMM behind a prologue (bf16: exact fp16 operands
+ *     under power-of-two row shifts, with the bias term as extra MFMA slots,
+ *     and an in-launch split-K for long rows; fp16: a group-sum prologue and
+ *     a per-group fp32 epilogue).
  * Workspace: the first 16384 bytes hold per-tile counters and must be zero
  * before the first call; every call leaves them zero again. Give each entry
  * point its own workspace buffer, and do not share one buffer between

@@ -13,6 +13,13 @@
 //                       instruction, v_mfma_f32_4x4x4_16b blocks, activations
 //                       and (scale, bias) staged once per workgroup in LDS,
 //                       whole rows per workgroup (no split-K)
+//   w4_gemv_stream_kernel  M = 1, rows over 2560 k: one 16-wave workgroup per
+//                       CU over a contiguous range of row quads, (row quad,
+//                       span) items dealt evenly, every load issued at the
+//                       start, per-item lane sums through LDS
+//   w4_decode_stream_kernel  2 <= M <= 16: the same layout with each decoded
+//                       piece feeding eight MFMAs per row quartet and lane
+//                       sums kept in registers over a run of spans
 //   w4_skinny_kernel    M <= 32: weight streaming, 32 rows x 64 k per wave
 //                       step, MFMA 32x32x16, in-workgroup split-K over waves,
 //                       cross-workgroup split-K combined in the same launch by
@@ -1864,7 +1871,8 @@ constexpr int kDecMaxLds = 160 * 1024;
 
 static DecPlan plan_dec(int64_t M, int64_t N, int64_t K, int G) {
   DecPlan p{};
-  if (M < 2 || M > 16 || env_int("SPARKQ_W4_NO_DEC", 0)) return p;
+  if (M < (env_int("SPARKQ_W4_DEC_M1", 0) ? 1 : 2) || M > 16 || env_int("SPARKQ_W4_NO_DEC", 0))
+    return p;
   if (K % 512 != 0 || N % 4 != 0) return p;
   // Up to four rows of at most 5 spans keep w4_gemv_kernel (measured at
   // M = 4: QKV 3584x2560 4.5 against 5.2 us here, gate+up 19456x2560 11.1

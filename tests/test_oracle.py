@@ -362,3 +362,21 @@ def test_converter_w8_format_unpacks_to_symmetric_codes():
 def test_bf16_rounding_matches_reference_vectors():
     g = _golden()
     assert np.array_equal(o.bf16_bits(g["bf16_in"]), g["bf16_out"])
+
+
+def test_w8a16_oracle_matches_numpy():
+    """sq_w8a16_matmul against a float64 numpy matmul (random and extreme
+    codes), and one-hot activations picking w[:, k] * scale."""
+    rng = np.random.default_rng(8)
+    m, n, k = 3, 17, 96
+    x = o.randn16(8, 1, m * k).reshape(m, k)
+    w8 = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    w8[0] = -128
+    sc = rng.random(n).astype(np.float32)
+    y = o.w8a16_matmul(x, w8, sc)
+    ref = (o.bits_to_f32(x, o.BF16).astype(np.float64) @ w8.T.astype(np.float64)) * sc
+    assert np.allclose(y, ref, rtol=1e-14, atol=0)
+    e = np.zeros((1, k), np.float32)
+    e[0, 5] = 1.0
+    assert np.array_equal(o.w8a16_matmul(o.bf16_bits(e), w8, sc)[0],
+                          w8[:, 5].astype(np.float64) * sc.astype(np.float64))
