@@ -219,6 +219,46 @@ int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes,
 int sparkq_kv_quantize_s8(const void* x, int8_t* codes, void* scales,
                           int64_t R, int64_t D, int x_dtype, void* stream);
 
+/* INT8-KV GQA prefill attention (L > 1 query tokens per sequence) over the
+ * symmetric S8_F16SCALE cache: q [B,Hq,L,D] contiguous in q_dtype (BF16 or
+ * F16), out [B,Hq,L,D] in out_dtype (q_dtype or F32); K/V codes and scales
+ * and strides[0..11] as for sparkq_int8kv_sdpa_decode. causal = 1 applies
+ * the bottom-right causal mask (query position i of L sees tokens
+ * 0 .. N-L+i, L <= N); 0 lets every query see all N tokens. fp32 online
+ * softmax; QK and PV on the fp16 MFMA with exact operands.
+ * Replaces the L > 1 branch of int8_quantized_sdpa
+ * (X/spark_mlx_ext/int8_quantized_sdpa.py:236-245) and its kernel
+ * spark_affine_u8_sdpa_prefill (X/spark_mlx_ext/int8_quantized_sdpa_prefill.py:
+ * 44-57, X/spark_mlx_ext/_int8_prefill_sources.py:7-154), which serves the
+ * MLX affine u8/G32 cache at D=256; this entry point serves the symmetric s8
+ * format at D in {64,128,256}. */
+int sparkq_int8kv_sdpa_prefill(const void* q, const void* k_codes,
+                               const void* k_scales, const void* v_codes,
+                               const void* v_scales, void* out, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
+                               int64_t D, int causal, int q_dtype,
+                               int out_dtype, float scale,
+                               const int64_t* strides, void* stream);
+
+/* Quantize-on-append into a preallocated INT8 KV cache (mlx-lm
+ * QuantizedKVCache.update_and_fetch as used by spark_mlx_llm/generation.py:
+ * 13,316-329,339-384): row (b, h, l) of x [B,H,L,D] (contiguous, x_dtype) is
+ * quantized and written to token offset+l of the cache.
+ *   S8_F16SCALE: codes int8 [B,H,Ncap,D], scales fp16 [B,H,Ncap]; the
+ *     sparkq_kv_quantize_s8 formula. biases unused (may be NULL).
+ *   AFFINE_U8: packed uint32 [B,H,Ncap,D/4] (dim 4w+j in byte j of word w),
+ *     scales and biases [B,H,Ncap,D/G] in x_dtype (BF16 or F16); per group of
+ *     G dims scale = to_dtype((max-min)/255), bias = to_dtype(min), code =
+ *     clamp(rint((x - bias)/scale), 0, 255) with the rounded scale and bias
+ *     (code 0 when the scale is 0): the mx.quantize(bits=8) formula.
+ * strides[0..2] codes (batch, head, token) in bytes; strides[3..5] scales and
+ * biases (batch, head, token) in elements. The cache is written in place;
+ * tokens outside [offset, offset+L) are untouched. */
+int sparkq_kv_append(const void* x, void* codes, void* scales, void* biases,
+                     int64_t B, int64_t H, int64_t L, int64_t D,
+                     int64_t offset, int group_size, int kv_format,
+                     int x_dtype, const int64_t* strides, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

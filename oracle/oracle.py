@@ -22,7 +22,7 @@ __all__ = [
     "a8_quantize", "w8_quantize_channel", "w8_unpack_affine",
     "int8_matmul", "w8a8_epilogue",
     "kv_quantize_s8", "kv_quantize_affine_u8", "kv_dequantize_s8",
-    "kv_dequantize_affine_u8", "sdpa_decode",
+    "kv_dequantize_affine_u8", "sdpa_decode", "sdpa_prefill",
     "cpu_w4a16_gemv", "scalar_f32_to_bf16", "scalar_f32_to_f16",
     "scalar_f16_to_f32",
 ]
@@ -337,6 +337,29 @@ def sdpa_decode(q, kdq, vdq, scale: float) -> np.ndarray:
     _lib().sq_sdpa_decode(_p(q), _p(kdq), _p(vdq), bsz, hq, hkv, n, d,
                           float(scale), _p(out))
     return out
+
+
+def sdpa_prefill(q, kdq, vdq, scale: float, causal: bool) -> np.ndarray:
+    """Staged attention in float64 over dequantized K/V, the reference's
+    _fallback (X/spark_mlx_ext/int8_quantized_sdpa.py:122-153): q*scale,
+    scores = q K^T, the bottom-right causal mask arange(N-L, N)[:, None] >=
+    arange(N)[None, :] when causal, softmax, probs V. q [B,Hq,L,D]; kdq/vdq
+    [B,Hkv,N,D] -> out [B,Hq,L,D]."""
+    q = np.asarray(q, np.float64)
+    kdq, vdq = np.asarray(kdq, np.float64), np.asarray(vdq, np.float64)
+    bsz, hq, length, d = q.shape
+    hkv, n = kdq.shape[1], kdq.shape[2]
+    rep = hq // hkv
+    k = np.repeat(kdq, rep, axis=1)
+    v = np.repeat(vdq, rep, axis=1)
+    scores = (q * scale) @ np.swapaxes(k, -1, -2)
+    if causal:
+        vis = np.arange(n - length, n)[:, None] >= np.arange(n)[None, :]
+        scores = np.where(vis, scores, -np.inf)
+    scores -= scores.max(axis=-1, keepdims=True)
+    p = np.exp(scores)
+    p /= p.sum(axis=-1, keepdims=True)
+    return p @ v
 
 
 # ---------------------------------------------------------------------------

@@ -41,6 +41,13 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
                        size_t wsb, hipStream_t st);
 int kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_t D, int xdt,
                    hipStream_t st);
+int kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B, int64_t H,
+              int64_t L, int64_t D, int64_t offset, int G, int fmt, int xdt,
+              const int64_t* strides, hipStream_t st);
+int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const void* vc,
+                        const void* vs, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                        int64_t N, int64_t D, int causal, int qdt, int odt, float scale,
+                        const int64_t* strides, hipStream_t st);
 int w8a16_linear(const void* x, const int8_t* w, const float* scales, void* y, int64_t M,
                  int64_t N, int64_t K, int xdt, int ydt, hipStream_t st);
 
@@ -292,6 +299,66 @@ int sparkq_kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R,
   REQUIRE(is_float_dtype(x_dtype), "kv_quantize_s8: x must be float16, bfloat16 or float32");
   DEVICE_OK();
   return kv_quantize_s8(x, codes, scales, R, D, x_dtype, (hipStream_t)stream);
+}
+
+int sparkq_int8kv_sdpa_prefill(const void* q, const void* k_codes, const void* k_scales,
+                               const void* v_codes, const void* v_scales, void* out, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t L, int64_t N, int64_t D,
+                               int causal, int q_dtype, int out_dtype, float scale,
+                               const int64_t* strides, void* stream) {
+  REQUIRE(q && k_codes && k_scales && v_codes && v_scales && out && strides,
+          "int8kv_sdpa_prefill: null tensor pointer");
+  REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && L > 0 && N > 0 && D > 0 && Hq % Hkv == 0,
+          "Nonempty inputs and query heads divisible by KV heads required");
+  REQUIRE(B * Hkv <= 65535 && N <= kI32Max && L * Hq <= kI32Max,
+          "int8kv_sdpa_prefill: shape too large");
+  REQUIRE(!causal || L <= N, "int8kv_sdpa_prefill: a causal mask needs L <= N");
+  const int64_t gqa = Hq / Hkv;
+  REQUIRE_SUPPORTED(gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8,
+                    "int8kv_sdpa_prefill: query heads per KV head must be 1, 2, 4 or 8");
+  REQUIRE_SUPPORTED(D == 64 || D == 128 || D == 256,
+                    "int8kv_sdpa_prefill: head dim must be 64, 128 or 256");
+  REQUIRE(std::isfinite(scale), "scale must be a finite Python number");
+  REQUIRE_SUPPORTED(is_half_dtype(q_dtype),
+                    "int8kv_sdpa_prefill: queries must be float16 or bfloat16");
+  REQUIRE(out_dtype == q_dtype || out_dtype == SPARKQ_F32,
+          "int8kv_sdpa_prefill: out dtype must equal q dtype or be float32");
+  for (int i : {0, 1, 2, 6, 7, 8})
+    REQUIRE(strides[i] % 16 == 0 && strides[i] >= 0,
+            "int8kv_sdpa_prefill: code strides must be non-negative multiples of 16 bytes");
+  for (int i : {3, 4, 5, 9, 10, 11})
+    REQUIRE(strides[i] >= 0, "int8kv_sdpa_prefill: negative scale stride");
+  REQUIRE(aligned(q, 16) && aligned(k_codes, 16) && aligned(v_codes, 16),
+          "int8kv_sdpa_prefill: q and codes must be 16-byte aligned");
+  DEVICE_OK();
+  return int8kv_sdpa_prefill(q, k_codes, k_scales, v_codes, v_scales, out, B, Hq, Hkv, L, N, D,
+                             causal, q_dtype, out_dtype, scale, strides, (hipStream_t)stream);
+}
+
+int sparkq_kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B,
+                     int64_t H, int64_t L, int64_t D, int64_t offset, int group_size,
+                     int kv_format, int x_dtype, const int64_t* strides, void* stream) {
+  REQUIRE(x && codes && scales && strides, "kv_append: null tensor pointer");
+  REQUIRE(B > 0 && H > 0 && L > 0 && D > 0 && offset >= 0, "kv_append: bad shape or offset");
+  REQUIRE(B * H * L * D <= kI32Max * 4LL && offset + L <= kI32Max, "kv_append: shape too large");
+  REQUIRE(kv_format == SPARKQ_KV_S8_F16SCALE || kv_format == SPARKQ_KV_AFFINE_U8,
+          "kv_append: unknown kv_format %d", kv_format);
+  for (int i = 0; i < 6; ++i) REQUIRE(strides[i] >= 0, "kv_append: negative stride");
+  if (kv_format == SPARKQ_KV_S8_F16SCALE) {
+    REQUIRE(is_float_dtype(x_dtype), "kv_append: x must be float16, bfloat16 or float32");
+  } else {
+    REQUIRE(biases, "kv_append: affine format needs biases");
+    REQUIRE(is_half_dtype(x_dtype), "kv_append: affine KV needs float16 or bfloat16 x");
+    REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+            "Supported affine formats: bits 2/4/8, group size 32/64/128");
+    REQUIRE(D % group_size == 0, "kv_append: head dim not a multiple of group_size");
+    REQUIRE(strides[0] % 4 == 0 && strides[1] % 4 == 0 && strides[2] % 4 == 0,
+            "kv_append: packed code strides must be multiples of 4 bytes");
+    REQUIRE(aligned(codes, 4), "kv_append: packed codes must be 4-byte aligned");
+  }
+  DEVICE_OK();
+  return kv_append(x, codes, scales, biases, B, H, L, D, offset, group_size, kv_format, x_dtype,
+                   strides, (hipStream_t)stream);
 }
 
 // Mirrors the checks of w8a16_per_channel (X/src/spark_w8a16.cpp:80-104).

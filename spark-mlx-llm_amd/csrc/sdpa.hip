@@ -19,6 +19,10 @@
 //                       products on the fp16 MFMA (see its comment)
 //   sdpa_merge_kernel   log-sum-exp merge of the split partials.
 //   kv_quantize_s8_kernel  s8 + fp16-scale quantizer (one wave per row).
+//   sdpa_prefill_kernel    L > 1 queries, s8 + fp16 scale: the MFMA block step
+//                          with (position, head) rows, bottom-right causal.
+//   kv_append_s8_kernel, kv_append_u8_kernel  quantize-on-append into a
+//                          strided cache (s8 + fp16 scale; MLX affine u8).
 #include <algorithm>
 #include <type_traits>
 
@@ -45,6 +49,7 @@ struct SdpaArgs {
   int B, Hq, Hkv, N, G;
   int q_dtype, out_dtype;
   int tps, S;
+  int L, causal;     // prefill: query length, bottom-right causal mask
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -519,6 +524,236 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA prefill attention for the symmetric s8 + fp16-scale format (L > 1)
+// ---------------------------------------------------------------------------
+// The decode kernel's block step with the 16 MFMA rows of a wave taken by 16
+// (query position, head) rows of one KV head: row rr of L*GQA is position
+// rr / GQA of head rr % GQA, so a wave's rows cover 16/GQA adjacent positions
+// and share most of their visible context. Each wave walks every 32-token
+// block up to the last one its rows see (bottom-right causal: position i of
+// L sees tokens 0 .. N-L+i; without the mask all N), two blocks in flight,
+// masking each score row at its own limit, and writes its rows' outputs
+// itself (no context split, no merge). A workgroup is 4 waves = 64 rows.
+template <int D, int GQA>
+__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(SdpaArgs a) {
+  constexpr int NC = D / 32;   // k chunks of QK
+  constexpr int PL = D / 64;   // 16-byte K pieces per lane per 16-token group
+  constexpr int NJ = D / 16;   // 16-dim column groups of PV
+  constexpr int VL = D / 32;   // 16-byte V pieces per lane per block
+  using L = SdpaMfmaLds<D>;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[L::BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, grp = lane >> 4;
+  const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
+  const int R = a.L * GQA;                     // query rows (position, head) of this KV head
+  const int row0 = blockIdx.x * 64 + wave * 16;  // the wave's first row
+  // last visible token of row rr (bottom-right causal), -1 for rows past R
+  auto last_tok = [&](int rr) -> int {
+    return rr >= R ? -1 : (a.causal ? a.N - a.L + rr / GQA : a.N - 1);
+  };
+  const int t_end = row0 < R ? min(a.N, last_tok(min(row0 + 15, R - 1)) + 1) : 0;
+  const int t_begin = 0;
+  unsigned char* vtile = smem + wave * L::VT;
+  uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + 4 * L::VT + wave * L::PT);
+
+  // query operand: lane (head n16, k quarter grp); chunk c covers dims
+  // 16*(grp + 4*(c/2)) + 8*(c%2) .. +8, matching the K piece order below
+  u32x4_t qa[NC];
+  float qmax = 0.0f, qs = 0.0f;
+  {
+    const int rr = min(row0 + n16, R - 1);
+    const bool live = row0 + n16 < R;
+    float qv[NC][8];
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) +
+                           (((int64_t)b * a.Hq + kh * GQA + rr % GQA) * a.L + rr / GQA) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d0 = 16 * (grp + 4 * (c >> 1)) + 8 * (c & 1);
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(qrow + d0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t bits = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+        const float v = a.q_dtype == SPARKQ_BF16 ? bf16_to_f32(bits) : f16_to_f32(bits);
+        qv[c][i] = live ? v : 0.0f;
+        qmax = fmaxf(qmax, fabsf(qv[c][i]));
+      }
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    const int e = (qmax > 0.0f && qmax <= 3.4028235e38f) ? ilogbf(qmax) - 14 : 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const _Float16 lo = (_Float16)ldexpf(qv[c][2 * i], -e), hi = (_Float16)ldexpf(qv[c][2 * i + 1], -e);
+        qs += (float)lo + (float)hi;
+        qa[c][i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
+    }
+    qs += __shfl_xor(qs, 16);
+    qs += __shfl_xor(qs, 32);
+    qmax = ldexpf(a.scale_log2, e);  // reused: per-head score multiplier
+  }
+  // score lanes: head 4*grp + r, token n16 (+16 for the second token group)
+  float qcorr[4], qmul[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * grp + r;
+    qcorr[r] = 1152.0f * __shfl(qs, h & 15);
+    qmul[r] = __shfl(qmax, h & 15);
+  }
+
+  // last visible token of the four score rows of this lane
+  int lim[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) lim[r] = last_tok(row0 + 4 * grp + r);
+
+  const rsrc_t rk = make_rsrc(a.kc + b * a.kc_b + kh * a.kc_h, (uint32_t)(t_end * a.kc_t));
+  const rsrc_t rv = make_rsrc(a.vc + b * a.vc_b + kh * a.vc_h, (uint32_t)(t_end * a.vc_t));
+  const rsrc_t rks = make_rsrc(reinterpret_cast<const uint16_t*>(a.ks) + b * a.ks_b + kh * a.ks_h,
+                               (uint32_t)(t_end * a.ks_t * 2));
+  const rsrc_t rvs = make_rsrc(reinterpret_cast<const uint16_t*>(a.vs) + b * a.vs_b + kh * a.vs_h,
+                               (uint32_t)(t_end * a.vs_t * 2));
+
+  // block registers, two sets (the next two blocks are in flight while one
+  // is computed): K pieces [token group][piece], V pieces, one scale
+  u32x4_t kr[2][2][PL], vr[2][VL];
+  uint32_t sr[2];
+  auto load = [&](int set, int t0) {
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        kr[set][g2][i] = buf_load16(rk, (uint32_t)((t0 + 16 * g2 + n16) * a.kc_t + 16 * (grp + 4 * i)));
+#pragma unroll
+    for (int v = 0; v < VL; ++v) {
+      const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
+      vr[set][v] = buf_load16(rv, (uint32_t)((t0 + tok) * a.vc_t + 16 * pc));
+    }
+    sr[set] = lane < 32 ? buf_load2(rks, (uint32_t)((t0 + lane) * a.ks_t * 2))
+                        : buf_load2(rvs, (uint32_t)((t0 + lane - 32) * a.vs_t * 2));
+  };
+
+  float mrun[4], zl[4], psl[4];
+  f32x4_t acc[NJ];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mrun[r] = kNegInf;
+    zl[r] = 0.0f;
+    psl[r] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int stride = 32;
+  auto block = [&](int t0, auto setc) {
+    constexpr int set = decltype(setc)::value;
+    // this block's data, then the loads of the block two ahead into its set
+    u32x4_t kb[2][PL], vb[VL];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int i = 0; i < PL; ++i) kb[g2][i] = kr[set][g2][i];
+#pragma unroll
+    for (int v = 0; v < VL; ++v) vb[v] = vr[set][v];
+    const uint32_t sb = sr[set];
+    if (t0 + 2 * stride < t_end) load(set, t0 + 2 * stride);
+    // V block to this wave's LDS copy (padded rows)
+#pragma unroll
+    for (int v = 0; v < VL; ++v) {
+      const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
+      *reinterpret_cast<u32x4_t*>(vtile + tok * L::VROW + 16 * pc) = vb[v];
+    }
+
+    // scores: 2 token groups x NC chunks
+    f32x4_t sc[2];
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      sc[g2] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const u32x4_t kp = kb[g2][c >> 1];
+        const u32x4_t kf = (c & 1) ? s8x8_to_f16(kp.z, kp.w) : s8x8_to_f16(kp.x, kp.y);
+        sc[g2] = mfma16x16x32_f16(qa[c], kf, sc[g2]);
+      }
+    }
+    const float ksc0 = f16_to_f32((uint16_t)__shfl(sb, n16));
+    const float ksc1 = f16_to_f32((uint16_t)__shfl(sb, 16 + n16));
+    const float vsc0 = f16_to_f32((uint16_t)__shfl(sb, 32 + n16));
+    const float vsc1 = f16_to_f32((uint16_t)__shfl(sb, 48 + n16));
+
+    float alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok0 = t0 + n16 <= lim[r], ok1 = t0 + 16 + n16 <= lim[r];
+      const float s0 = ok0 ? (sc[0][r] - qcorr[r]) * ksc0 * qmul[r] : kNegInf;
+      const float s1 = ok1 ? (sc[1][r] - qcorr[r]) * ksc1 * qmul[r] : kNegInf;
+      float mb = max_row16(fmaxf(s0, s1));
+      mb = fmaxf(mb, mrun[r]);
+      alpha[r] = exp2_guarded(mrun[r] - mb, mrun[r] != kNegInf);
+      mrun[r] = mb;
+      const float p0 = exp2_guarded(s0 - mb, ok0), p1 = exp2_guarded(s1 - mb, ok1);
+      const float f0 = p0 * vsc0, f1 = p1 * vsc1;
+      const _Float16 w0 = (_Float16)f0, w1 = (_Float16)f1;
+      const _Float16 u0 = (_Float16)(f0 - (float)w0), u1 = (_Float16)(f1 - (float)w1);
+      zl[r] = fmaf(zl[r], alpha[r], p0 + p1);
+      psl[r] = fmaf(psl[r], alpha[r], ((float)w0 + (float)u0) + ((float)w1 + (float)u1));
+      const int h = 4 * grp + r;
+      pstrip[h * 32 + n16] = __builtin_bit_cast(uint16_t, w0);
+      pstrip[h * 32 + 16 + n16] = __builtin_bit_cast(uint16_t, w1);
+      pstrip[512 + h * 32 + n16] = __builtin_bit_cast(uint16_t, u0);
+      pstrip[512 + h * 32 + 16 + n16] = __builtin_bit_cast(uint16_t, u1);
+    }
+    // PV: A = P strip row n16, tokens 8*grp .. +8
+    const u32x4_t pa = *reinterpret_cast<const u32x4_t*>(pstrip + n16 * 32 + 8 * grp);
+    const u32x4_t pl = *reinterpret_cast<const u32x4_t*>(pstrip + 512 + n16 * 32 + 8 * grp);
+    const unsigned char* vaddr = vtile + (8 * grp + (n16 >> 1)) * L::VROW + 8 * (n16 & 1);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      acc[j][0] *= alpha[0];
+      acc[j][1] *= alpha[1];
+      acc[j][2] *= alpha[2];
+      acc[j][3] *= alpha[3];
+      typedef int v2i_t __attribute__((ext_vector_type(2)));
+      const v2i_t t8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (__attribute__((address_space(3))) v2i_t*)(vaddr + 16 * j));
+      const u32x4_t vf = s8x8_to_f16((uint32_t)t8.x, (uint32_t)t8.y);
+      acc[j] = mfma16x16x32_f16(pa, vf, acc[j]);
+      acc[j] = mfma16x16x32_f16(pl, vf, acc[j]);
+    }
+  };
+  int t0 = t_begin;
+  if (t0 < t_end) load(0, t0);
+  if (t0 + stride < t_end) load(1, t0 + stride);
+  for (; t0 < t_end; t0 += 2 * stride) {
+    block(t0, std::integral_constant<int, 0>{});
+    if (t0 + stride < t_end) block(t0 + stride, std::integral_constant<int, 1>{});
+  }
+
+  // per-lane partial sums -> the 16 token lanes of each head group
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    zl[r] = sum_row16(zl[r]);
+    psl[r] = sum_row16(psl[r]);
+  }
+
+  // each wave owns its 16 rows: out = (acc - 1152 * sum of fp16 weights) / z
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int rr = row0 + 4 * grp + r;
+    if (rr < R) {
+      const int64_t orow = ((int64_t)b * a.Hq + kh * GQA + rr % GQA) * a.L + rr / GQA;
+      const float inv = zl[r] > 0.0f ? 1.0f / zl[r] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        store_out(a.out, orow * D + 16 * j + n16, (acc[j][r] - 1152.0f * psl[r]) * inv, a.out_dtype);
+    }
+  }
+}
+
 // Log-sum-exp merge of the split partials of one (sequence, query head) row:
 // the split maxima and sums reduce across the workgroup, then thread
 // (d, part) sums the weighted partial outputs of every 256/D-th split with
@@ -596,6 +831,84 @@ __global__ __launch_bounds__(256) void kv_quantize_s8_kernel(const void* __restr
     float v = __builtin_rintf(load_in(x, row * D + d, xdt) / s);
     v = fminf(fmaxf(v, -127.0f), 127.0f);
     codes[row * D + d] = (int8_t)v;
+  }
+}
+
+// Quantize-on-append: row (b, h, l) of x [B,H,L,D] to cache token offset+l.
+// S8 format: one wave per row, the kv_quantize_s8_kernel formula. Affine u8
+// format: one thread per group of G values, scale = to_dtype((max-min)/255),
+// bias = to_dtype(min), code = clamp(rint((x - bias) / scale), 0, 255) with
+// the rounded scale and bias (0 for a zero scale), four codes per uint32
+// (dim 4w+j in byte j of word w).
+struct KvAppendArgs {
+  const void* x;
+  void* codes;
+  void* scales;
+  void* biases;
+  int64_t c_b, c_h, c_t;  // code strides (bytes)
+  int64_t s_b, s_h, s_t;  // scale/bias strides (elements)
+  int B, H, L, D, G, offset, x_dtype;
+};
+
+__global__ __launch_bounds__(256) void kv_append_s8_kernel(KvAppendArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.H * a.L) return;
+  const int l = (int)(row % a.L), bh = (int)(row / a.L), h = bh % a.H, b = bh / a.H;
+  const int D = a.D;
+  float amax = 0.0f;
+  for (int d = lane; d < D; d += 64) amax = fmaxf(amax, fabsf(load_in(a.x, row * D + d, a.x_dtype)));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  uint16_t s16 = f32_to_f16(amax / 127.0f);
+  if (f16_to_f32(s16) == 0.0f) s16 = 0x3C00u;
+  const float s = f16_to_f32(s16);
+  const int64_t t = (int64_t)a.offset + l;
+  if (lane == 0)
+    reinterpret_cast<uint16_t*>(a.scales)[b * a.s_b + h * a.s_h + t * a.s_t] = s16;
+  int8_t* dst = reinterpret_cast<int8_t*>(a.codes) + b * a.c_b + h * a.c_h + t * a.c_t;
+  for (int d = lane; d < D; d += 64) {
+    float v = __builtin_rintf(load_in(a.x, row * D + d, a.x_dtype) / s);
+    v = fminf(fmaxf(v, -127.0f), 127.0f);
+    dst[d] = (int8_t)v;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void kv_append_u8_kernel(KvAppendArgs a) {
+  const int ng = a.D / a.G;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (int64_t)a.B * a.H * a.L * ng) return;
+  const int g = (int)(gid % ng);
+  const int64_t row = gid / ng;
+  const int l = (int)(row % a.L), bh = (int)(row / a.L), h = bh % a.H, b = bh / a.H;
+  const int64_t t = (int64_t)a.offset + l;
+  const uint16_t* v = reinterpret_cast<const uint16_t*>(a.x) + row * a.D + (int64_t)g * a.G;
+  float mn = T::to_f32(v[0]), mx = mn;
+  for (int i = 1; i < a.G; ++i) {
+    const float f = T::to_f32(v[i]);
+    mn = f < mn ? f : mn;
+    mx = f > mx ? f : mx;
+  }
+  const uint16_t s16 = T::from_f32((mx - mn) / 255.0f), b16 = T::from_f32(mn);
+  const int64_t si = b * a.s_b + h * a.s_h + t * a.s_t + g;
+  reinterpret_cast<uint16_t*>(a.scales)[si] = s16;
+  reinterpret_cast<uint16_t*>(a.biases)[si] = b16;
+  const float sf = T::to_f32(s16), bf = T::to_f32(b16);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(a.codes) +
+                                              b * a.c_b + h * a.c_h + t * a.c_t) + g * a.G / 4;
+  for (int w = 0; w < a.G / 4; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float q = 0.0f;
+      if (sf != 0.0f) {
+        q = __builtin_rintf((T::to_f32(v[4 * w + j]) - bf) / sf);
+        q = q < 0.0f ? 0.0f : (q > 255.0f ? 255.0f : q);
+      }
+      word |= (uint32_t)q << (8 * j);
+    }
+    dst[w] = word;
   }
 }
 
@@ -724,6 +1037,95 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
     if (int rc = check_launch("sdpa_merge_kernel")) return rc;
   }
   return SPARKQ_OK;
+}
+
+template <int D>
+static void launch_prefill_d(const SdpaArgs& a, int gqa, dim3 grid, hipStream_t st) {
+  switch (gqa) {
+    case 1: hipLaunchKernelGGL((sdpa_prefill_kernel<D, 1>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((sdpa_prefill_kernel<D, 2>), grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((sdpa_prefill_kernel<D, 4>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((sdpa_prefill_kernel<D, 8>), grid, dim3(256), 0, st, a); break;
+  }
+}
+
+int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const void* vc,
+                        const void* vs, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                        int64_t N, int64_t D, int causal, int qdt, int odt, float scale,
+                        const int64_t* strides, hipStream_t st) {
+  SdpaArgs a{};
+  a.q = q;
+  a.kc = reinterpret_cast<const uint8_t*>(kc);
+  a.ks = ks;
+  a.vc = reinterpret_cast<const uint8_t*>(vc);
+  a.vs = vs;
+  a.out = out;
+  a.kc_b = strides[0];
+  a.kc_h = strides[1];
+  a.kc_t = strides[2];
+  a.ks_b = strides[3];
+  a.ks_h = strides[4];
+  a.ks_t = strides[5];
+  a.vc_b = strides[6];
+  a.vc_h = strides[7];
+  a.vc_t = strides[8];
+  a.vs_b = strides[9];
+  a.vs_h = strides[10];
+  a.vs_t = strides[11];
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.N = (int)N;
+  a.L = (int)L;
+  a.causal = causal ? 1 : 0;
+  a.q_dtype = qdt;
+  a.out_dtype = odt;
+  a.S = 1;
+  a.tps = (int)N;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int gqa = (int)(Hq / Hkv);
+  dim3 grid((unsigned)cdiv(L * gqa, 64), (unsigned)(B * Hkv));
+  if (D == 64)
+    launch_prefill_d<64>(a, gqa, grid, st);
+  else if (D == 128)
+    launch_prefill_d<128>(a, gqa, grid, st);
+  else
+    launch_prefill_d<256>(a, gqa, grid, st);
+  return check_launch("sdpa_prefill_kernel");
+}
+
+int kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B, int64_t H,
+              int64_t L, int64_t D, int64_t offset, int G, int fmt, int xdt,
+              const int64_t* strides, hipStream_t st) {
+  KvAppendArgs a{};
+  a.x = x;
+  a.codes = codes;
+  a.scales = scales;
+  a.biases = biases;
+  a.c_b = strides[0];
+  a.c_h = strides[1];
+  a.c_t = strides[2];
+  a.s_b = strides[3];
+  a.s_h = strides[4];
+  a.s_t = strides[5];
+  a.B = (int)B;
+  a.H = (int)H;
+  a.L = (int)L;
+  a.D = (int)D;
+  a.G = G;
+  a.offset = (int)offset;
+  a.x_dtype = xdt;
+  const int64_t rows = B * H * L;
+  if (fmt == SPARKQ_KV_S8_F16SCALE) {
+    hipLaunchKernelGGL(kv_append_s8_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, st, a);
+  } else {
+    const unsigned grid = (unsigned)cdiv(rows * (D / G), 256);
+    if (xdt == SPARKQ_BF16)
+      hipLaunchKernelGGL(kv_append_u8_kernel<BF16>, dim3(grid), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(kv_append_u8_kernel<F16>, dim3(grid), dim3(256), 0, st, a);
+  }
+  return check_launch("kv_append_kernel");
 }
 
 int kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_t D, int xdt,

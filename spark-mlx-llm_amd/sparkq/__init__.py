@@ -6,6 +6,7 @@ called over the C-ABI declared in include/sparkq.h.
 """
 
 from .ext import (
+    QuantizedKVCache,
     W8A8Linear,
     affine_dequantize,
     affine_quantize,
@@ -13,6 +14,7 @@ from .ext import (
     int8_matmul_int32,
     int8_quantized_sdpa,
     is_w8a8_available,
+    kv_append,
     kv_quantize_s8,
     prepare_w4a16_nax4,
     quantize_per_token,
@@ -23,6 +25,7 @@ from .ext import (
 )
 
 __all__ = [
+    "QuantizedKVCache",
     "W8A8Linear",
     "affine_dequantize",
     "affine_quantize",
@@ -30,6 +33,7 @@ __all__ = [
     "int8_matmul_int32",
     "int8_quantized_sdpa",
     "is_w8a8_available",
+    "kv_append",
     "kv_quantize_s8",
     "prepare_w4a16_nax4",
     "quantize_per_token",

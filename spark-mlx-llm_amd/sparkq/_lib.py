@@ -49,6 +49,9 @@ SIGNATURES = {
     "sparkq_int8kv_sdpa_decode": (I, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64,
                                       I, I, I, I, F, P, P, SZ, P]),
     "sparkq_kv_quantize_s8": (I, [P, P, P, I64, I64, I, P]),
+    "sparkq_kv_append": (I, [P, P, P, P, I64, I64, I64, I64, I64, I, I, I, P, P]),
+    "sparkq_int8kv_sdpa_prefill": (I, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I, I,
+                                       I, F, P, P]),
 }
 
 

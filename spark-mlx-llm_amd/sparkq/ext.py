@@ -30,6 +30,8 @@ __all__ = [
     "int8_quantized_sdpa",
     "is_w8a8_available",
     "kv_quantize_s8",
+    "QuantizedKVCache",
+    "kv_append",
     "prepare_w4a16_nax4",
     "quantize_per_token",
     "w4a16_multirow",
@@ -390,6 +392,140 @@ def kv_quantize_s8(x):
     return codes, sc
 
 
+def _int8_prefill(queries, keys, values, *, scale, causal, fmt, out_dtype, out):
+    """L > 1 queries over the symmetric s8 cache (the prefill branch of
+    X/spark_mlx_ext/int8_quantized_sdpa.py:236-245): tiled QK, online softmax
+    and PV in one launch, bottom-right causal or unmasked."""
+    batch, heads, length, dim = queries.shape
+    kv_heads, n = keys[0].shape[1:3]
+    if fmt != KV_S8_F16SCALE:
+        raise ValueError("multi-token INT8-KV attention on gfx950 needs the symmetric int8 cache "
+                         "(codes int8 [B,Hkv,N,D], fp16 scales [B,Hkv,N])")
+    if queries.dtype not in _HALF:
+        raise ValueError("multi-token INT8-KV attention needs float16 or bfloat16 queries")
+    if causal and length > n:
+        raise ValueError("a causal mask needs L <= N")
+    for name, (codes, s) in (("key", keys), ("value", values)):
+        if (codes.shape != (batch, kv_heads, n, dim) or codes.dtype != torch.int8
+                or s.shape != (batch, kv_heads, n) or s.dtype != torch.float16):
+            raise ValueError(f"Incompatible {name} int8 codes or fp16 scales")
+        if codes.stride(3) != 1:
+            raise ValueError(f"{name} innermost axis must be contiguous")
+    (kc, ks), (vc, vs) = keys, values
+    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    out_dtype = queries.dtype if out_dtype is None else out_dtype
+    q = queries.contiguous()
+    y = _out_buffer(out, (batch, heads, length, dim), out_dtype, queries.device)
+    st = (ctypes.c_int64 * 12)(*(_kv_strides(kc, ks, 1) + _kv_strides(vc, vs, 1)))
+    _lib.call("sparkq_int8kv_sdpa_prefill", _ptr(q), _ptr(kc), _ptr(ks), _ptr(vc), _ptr(vs),
+              _ptr(y), batch, heads, kv_heads, length, n, dim, 1 if causal else 0,
+              _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), float(scale), st,
+              _lib.stream_handle(queries.device))
+    return y
+
+
+def kv_append(x, cache, offset: int, *, group_size: int = 32):
+    """Quantize x [B,H,L,D] into tokens [offset, offset+L) of a preallocated
+    cache, in place: cache is (codes int8 [B,H,Ncap,D], scales fp16
+    [B,H,Ncap]) for the symmetric format, or the MLX affine 8-bit tuple
+    (packed uint32 [B,H,Ncap,D/4], scales, biases [B,H,Ncap,D/G] in x.dtype).
+    The quantize-on-append step of mlx-lm's QuantizedKVCache."""
+    if x.ndim != 4 or x.numel() == 0:
+        raise ValueError("x must be a nonempty [B,H,L,D] tensor")
+    b, h, length, d = x.shape
+    fmt = KV_AFFINE_U8 if len(cache) == 3 else KV_S8_F16SCALE
+    codes, scales = cache[0], cache[1]
+    biases = cache[2] if fmt == KV_AFFINE_U8 else None
+    ncap = codes.shape[2]
+    if offset < 0 or offset + length > ncap:
+        raise ValueError(f"tokens [{offset}, {offset + length}) exceed the cache capacity {ncap}")
+    if fmt == KV_AFFINE_U8:
+        if x.dtype not in _HALF or scales.dtype != x.dtype or biases.dtype != x.dtype:
+            raise ValueError("affine KV needs float16 or bfloat16 x, scales and biases")
+        if (codes.shape != (b, h, ncap, d // 4) or codes.dtype not in _PACKED
+                or scales.shape != (b, h, ncap, d // group_size) or biases.shape != scales.shape
+                or scales.stride() != biases.stride() or d % group_size):
+            raise ValueError("Incompatible affine KV cache for this input")
+        strides = _kv_strides(codes, scales, 4)
+    else:
+        if x.dtype not in _REAL:
+            raise ValueError("x must be float16, bfloat16 or float32")
+        if (codes.shape != (b, h, ncap, d) or codes.dtype != torch.int8
+                or scales.shape != (b, h, ncap) or scales.dtype != torch.float16):
+            raise ValueError("Incompatible int8 KV cache for this input")
+        strides = _kv_strides(codes, scales, 1)
+    if codes.stride(3) != 1 or (fmt == KV_AFFINE_U8 and scales.stride(-1) != 1):
+        raise ValueError("the cache's innermost axes must be contiguous")
+    _require_device("kv_append", x, codes, scales, biases)
+    st = (ctypes.c_int64 * 6)(*strides)
+    _lib.call("sparkq_kv_append", _ptr(x.contiguous()), _ptr(codes), _ptr(scales), _ptr(biases),
+              b, h, length, d, offset, group_size, fmt, _lib.dtype_code(x.dtype), st,
+              _lib.stream_handle(x.device))
+
+
+class QuantizedKVCache:
+    """Quantize-on-append INT8 KV cache with the interface of mlx-lm 0.31.3's
+    QuantizedKVCache (used by spark_mlx_llm/generation.py:13,377):
+    update_and_fetch(keys, values) quantizes [B,Hkv,L,D] keys and values on the
+    device into storage that grows in steps of 256 tokens and returns views of
+    tokens [0, offset), ready for int8_quantized_sdpa. kv_format "affine_u8"
+    keeps MLX's (packed, scales, biases) tuples with group_size; "s8" the
+    symmetric (codes, fp16 scale) pairs of the decode benchmark."""
+
+    step = 256
+
+    def __init__(self, group_size: int = 32, bits: int = 8, kv_format: str = "affine_u8"):
+        if bits != 8:
+            raise ValueError("only 8-bit KV quantization is supported")
+        if kv_format not in ("affine_u8", "s8"):
+            raise ValueError("kv_format must be 'affine_u8' or 's8'")
+        if kv_format == "affine_u8" and group_size not in (32, 64, 128):
+            raise ValueError("group_size must be 32, 64 or 128")
+        self.group_size, self.bits, self.kv_format = group_size, bits, kv_format
+        self.keys = self.values = None
+        self.offset = 0
+
+    def _alloc(self, x, capacity):
+        b, h, _, d = x.shape
+        dev = x.device
+        if self.kv_format == "s8":
+            return (torch.zeros((b, h, capacity, d), dtype=torch.int8, device=dev),
+                    torch.zeros((b, h, capacity), dtype=torch.float16, device=dev))
+        g = self.group_size
+        return (torch.zeros((b, h, capacity, d // 4), dtype=torch.int32, device=dev),
+                torch.zeros((b, h, capacity, d // g), dtype=x.dtype, device=dev),
+                torch.zeros((b, h, capacity, d // g), dtype=x.dtype, device=dev))
+
+    def _grow(self, old, x, capacity):
+        new = self._alloc(x, capacity)
+        if old is not None:
+            for dst, src in zip(new, old):
+                dst[:, :, : self.offset] = src[:, :, : self.offset]
+        return new
+
+    def update_and_fetch(self, keys, values):
+        if keys.ndim != 4 or values.ndim != 4 or keys.shape[:3] != values.shape[:3]:
+            raise ValueError("keys and values must be [B,Hkv,L,D] with matching B, Hkv and L")
+        length = keys.shape[2]
+        if self.kv_format == "affine_u8" and (keys.shape[-1] % self.group_size
+                                              or values.shape[-1] % self.group_size):
+            raise ValueError("head dims must be multiples of group_size")
+        cap = self.keys[0].shape[2] if self.keys is not None else 0
+        if self.keys is None or self.offset + length > cap:
+            capacity = -(-(self.offset + length) // self.step) * self.step
+            self.keys = self._grow(self.keys, keys, capacity)
+            self.values = self._grow(self.values, values, capacity)
+        kv_append(keys, self.keys, self.offset, group_size=self.group_size)
+        kv_append(values, self.values, self.offset, group_size=self.group_size)
+        self.offset += length
+        n = self.offset
+        return (tuple(t[:, :, :n] for t in self.keys), tuple(t[:, :, :n] for t in self.values))
+
+    @property
+    def state(self):
+        return self.keys, self.values
+
+
 def _kv_strides(codes, scales, elem_bytes_codes):
     st = codes.stride()
     ss = scales.stride()
@@ -426,11 +562,12 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
         raise ValueError("scale must be a finite Python number")
     if mask is not None and not (isinstance(mask, str) and mask == "causal"):
         raise ValueError("only mask=None or mask='causal' is supported")
-    if length != 1:
-        raise ValueError("int8_quantized_sdpa on gfx950 serves single-token decode (L=1)")
     if queries.dtype not in _REAL:
         raise ValueError("Q and metadata must be float16, bfloat16 or float32")
     fmt = KV_AFFINE_U8 if len(keys) == 3 else KV_S8_F16SCALE
+    if length > 1:
+        return _int8_prefill(queries, keys, values, scale=scale, causal=mask is not None,
+                             fmt=fmt, out_dtype=out_dtype, out=out)
     if fmt == KV_AFFINE_U8:
         if bits != 8 or group_size not in (32, 64, 128):
             raise ValueError("Supported affine formats: bits 8, group size 32/64/128")

@@ -4,7 +4,9 @@ Mirrors spark_mlx_llm/ops/sdpa.py: SDPAConfig (:13-20), dispatch_sdpa
 (:39-78), _supports_int8 (:81-103) and _int8_attention (:149-163). The
 predicate is widened from the reference's D=256/G32 affine format to the
 formats and head sizes the gfx950 decode kernel serves (D in 64/128/256,
-affine G in 32/64/128, or symmetric s8 codes with fp16 per-token scales).
+affine G in 32/64/128, or symmetric s8 codes with fp16 per-token scales);
+multi-token queries (the opt-in fused_quantized_sdpa_prefill) are served on
+the symmetric s8 cache.
 Unquantized caches go to torch's scaled_dot_product_attention, the analogue
 of the reference's mlx-lm native path.
 """
@@ -35,14 +37,15 @@ def dispatch_sdpa(queries, keys, values, *, cache, scale, mask, config: SDPAConf
                   is_sliding=False):
     config = config if config is not None else SDPAConfig()
     if config.fused_quantized_sdpa and _supports_int8(queries, keys, values, cache=cache,
-                                                      mask=mask):
+                                                      mask=mask,
+                                                      prefill=config.fused_quantized_sdpa_prefill):
         return _int8_attention(queries, keys, values, cache=cache, scale=scale, mask=mask)
     if isinstance(keys, (tuple, list)):
         raise ValueError("quantized KV cache outside the gfx950 decode kernel's formats")
     return _native_attention(queries, keys, values, scale=scale, mask=mask)
 
 
-def _supports_int8(queries, keys, values, *, cache, mask):
+def _supports_int8(queries, keys, values, *, cache, mask, prefill=False):
     if not (isinstance(keys, (tuple, list)) and isinstance(values, (tuple, list))
             and len(keys) == len(values) and len(keys) in (2, 3)):
         return False
@@ -50,9 +53,14 @@ def _supports_int8(queries, keys, values, *, cache, mask):
         return False
     affine = len(keys) == 3
     dim = queries.shape[-1] if queries.ndim == 4 else -1
+    length = queries.shape[-2] if queries.ndim == 4 else 0
+    # multi-token queries (prefill, opt-in as in the reference) run on the
+    # symmetric s8 cache with 16-bit queries and L <= N under a causal mask
+    multi_ok = (prefill and not affine and queries.dtype in (torch.float16, torch.bfloat16)
+                and (mask is None or length <= keys[0].shape[2]))
     return (
         queries.ndim == 4
-        and queries.shape[-2] == 1
+        and (length == 1 or (length > 1 and multi_ok))
         and dim in (64, 128, 256)
         and keys[0].ndim == values[0].ndim == 4
         and keys[0].shape[1] > 0

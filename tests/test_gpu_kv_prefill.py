@@ -1,0 +1,140 @@
+"""GPU parity of the INT8 KV cache producer and of multi-token attention:
+quantize-on-append (QuantizedKVCache / kv_append) bit-exact with the oracle's
+quantizers for both formats across appends that cross the cache's 256-token
+growth steps, decode attention on the fetched views, and the prefill
+attention (L > 1, bottom-right causal or unmasked) against the fp64 staged
+attention of the reference's _fallback."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from helpers import check_fp32, check_rounded16, down16, up16
+
+pytestmark = pytest.mark.gpu
+
+
+def _x16(seed, stream, shape, dtype=o.BF16):
+    return o.randn16(seed, stream, int(np.prod(shape)), 1.0, dtype).reshape(shape)
+
+
+@pytest.mark.parametrize("fmt,d,g", [("s8", 128, 32), ("s8", 64, 32), ("affine_u8", 128, 32),
+                                     ("affine_u8", 256, 64), ("affine_u8", 128, 128)])
+def test_append_matches_oracle(gpu, fmt, d, g):
+    import sparkq
+
+    b, h = 2, 4
+    cache = sparkq.QuantizedKVCache(group_size=g, kv_format=fmt)
+    chunks = [5, 1, 300, 2]
+    ks, vs = [], []
+    for i, length in enumerate(chunks):
+        k16 = _x16(i, 10, (b, h, length, d))
+        v16 = _x16(i, 20, (b, h, length, d))
+        ks.append(k16)
+        vs.append(v16)
+        keys, values = cache.update_and_fetch(up16(k16, o.BF16, gpu), up16(v16, o.BF16, gpu))
+    n = sum(chunks)
+    assert cache.offset == n and keys[0].shape[2] == n
+    assert cache.keys[0].shape[2] == 512          # grown in steps of 256
+    kf = o.bits_to_f32(np.concatenate(ks, axis=2), o.BF16)
+    vf = o.bits_to_f32(np.concatenate(vs, axis=2), o.BF16)
+    for got, want in ((keys, kf), (values, vf)):
+        if fmt == "s8":
+            codes, sc = o.kv_quantize_s8(want)
+            assert np.array_equal(got[0].cpu().numpy(), codes)
+            assert np.array_equal(got[1].cpu().numpy().view(np.uint16), sc)
+        else:
+            packed, s, bb = o.kv_quantize_affine_u8(want, g, o.BF16)
+            assert np.array_equal(got[0].cpu().numpy().view(np.uint32), packed)
+            assert np.array_equal(down16(got[1]), s)
+            assert np.array_equal(down16(got[2]), bb)
+    # decode attention straight on the fetched views
+    q16 = _x16(7, 30, (b, 2 * h, d))
+    y = sparkq.int8_quantized_sdpa(up16(q16[:, :, None], o.BF16, gpu), keys, values,
+                                   scale=1.0 / math.sqrt(d), group_size=g,
+                                   out_dtype=torch.float32)
+    if fmt == "s8":
+        kd = o.kv_dequantize_s8(*o.kv_quantize_s8(kf))
+        vd = o.kv_dequantize_s8(*o.kv_quantize_s8(vf))
+    else:
+        kd = o.kv_dequantize_affine_u8(*o.kv_quantize_affine_u8(kf, g, o.BF16), g, o.BF16)
+        vd = o.kv_dequantize_affine_u8(*o.kv_quantize_affine_u8(vf, g, o.BF16), g, o.BF16)
+    ref = o.sdpa_decode(o.bits_to_f32(q16, o.BF16), kd, vd, 1.0 / math.sqrt(d))
+    check_fp32(y.cpu().numpy().reshape(ref.shape), ref)
+
+
+def _prefill(dev, b, hq, hkv, length, n, d, causal, seed, qdtype=o.BF16, out_dtype=None):
+    import sparkq
+
+    q16 = _x16(seed, 40, (b, hq, length, d), qdtype)
+    k = o.randn(seed, 41, b * hkv * n * d).reshape(b, hkv, n, d)
+    v = o.randn(seed, 42, b * hkv * n * d).reshape(b, hkv, n, d)
+    kc, ks = o.kv_quantize_s8(k)
+    vc, vs = o.kv_quantize_s8(v)
+    keys = (torch.from_numpy(kc).to(dev), torch.from_numpy(ks.view(np.float16)).to(dev))
+    vals = (torch.from_numpy(vc).to(dev), torch.from_numpy(vs.view(np.float16)).to(dev))
+    scale = 1.0 / math.sqrt(d)
+    y = sparkq.int8_quantized_sdpa(up16(q16, qdtype, dev), keys, vals, scale=scale,
+                                   mask="causal" if causal else None, out_dtype=out_dtype)
+    ref = o.sdpa_prefill(o.bits_to_f32(q16, qdtype), o.kv_dequantize_s8(kc, ks),
+                         o.kv_dequantize_s8(vc, vs), scale, causal)
+    return y, ref
+
+
+@pytest.mark.parametrize("b,hq,hkv,length,n,d,causal", [
+    (1, 32, 8, 16, 16, 128, True), (1, 32, 8, 100, 300, 128, True),
+    (2, 32, 8, 257, 257, 128, True), (1, 32, 8, 64, 200, 128, False),
+    (1, 8, 8, 33, 90, 64, True), (1, 16, 2, 40, 129, 256, True), (2, 16, 8, 7, 7, 64, True),
+    (1, 4, 2, 1000, 1000, 128, True)])
+def test_prefill_matches_oracle(gpu, b, hq, hkv, length, n, d, causal):
+    y32, ref = _prefill(gpu, b, hq, hkv, length, n, d, causal, seed=length + n,
+                        out_dtype=torch.float32)
+    check_fp32(y32.cpu().numpy(), ref)
+    y16, _ = _prefill(gpu, b, hq, hkv, length, n, d, causal, seed=length + n)
+    # the fp32 result is within ~2e-5 absolute (the 1152 code offset costs
+    # ~1152 * 2^-24 of the value scale); that is several bf16 units of the
+    # smallest outputs, so the one-unit bound applies from rms/16 up
+    check_rounded16(down16(y16), ref, o.BF16, near_zero=2.0 ** -4)
+
+
+def test_prefill_f16_queries(gpu):
+    y32, ref = _prefill(gpu, 1, 32, 8, 48, 80, 128, True, seed=3, qdtype=o.F16,
+                        out_dtype=torch.float32)
+    check_fp32(y32.cpu().numpy(), ref)
+
+
+def test_prefill_last_row_is_decode(gpu):
+    """Under the causal mask the last query position sees all N tokens, so its
+    output must equal single-token decode of that query."""
+    import sparkq
+
+    b, hq, hkv, length, n, d = 1, 32, 8, 20, 150, 128
+    q16 = _x16(5, 50, (b, hq, length, d))
+    k = o.randn(5, 51, b * hkv * n * d).reshape(b, hkv, n, d)
+    v = o.randn(5, 52, b * hkv * n * d).reshape(b, hkv, n, d)
+    kc, ks = o.kv_quantize_s8(k)
+    vc, vs = o.kv_quantize_s8(v)
+    keys = (torch.from_numpy(kc).to(gpu), torch.from_numpy(ks.view(np.float16)).to(gpu))
+    vals = (torch.from_numpy(vc).to(gpu), torch.from_numpy(vs.view(np.float16)).to(gpu))
+    qt = up16(q16, o.BF16, gpu)
+    yp = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=0.1, mask="causal",
+                                    out_dtype=torch.float32)
+    yd = sparkq.int8_quantized_sdpa(qt[:, :, -1:].contiguous(), keys, vals, scale=0.1,
+                                    out_dtype=torch.float32)
+    # different summation orders (decode splits the context over waves and
+    # workgroups), each within ~2e-5 of the exact value
+    assert torch.allclose(yp[:, :, -1], yd[:, :, 0], rtol=1e-4, atol=1e-4)
+    # identical keys: every visible token has the same score, so position i
+    # returns the mean of V over its N-L+i+1 visible tokens
+    kc1 = np.repeat(kc[:, :, :1], n, axis=2)
+    ks1 = np.repeat(ks[:, :, :1], n, axis=2)
+    keys1 = (torch.from_numpy(kc1).to(gpu), torch.from_numpy(ks1.view(np.float16)).to(gpu))
+    y = sparkq.int8_quantized_sdpa(qt, keys1, vals, scale=0.1, mask="causal",
+                                   out_dtype=torch.float32).cpu().numpy()
+    vd = o.kv_dequantize_s8(vc, vs).astype(np.float64)
+    for i in (0, length // 2, length - 1):
+        mean = vd[:, :, : n - length + i + 1].mean(axis=2)
+        assert np.allclose(y[:, :, i], np.repeat(mean, hq // hkv, axis=1), rtol=1e-4, atol=1e-4)

@@ -110,8 +110,17 @@ def test_sdpa_dispatch_validation():
         ext.int8_quantized_sdpa(q, keys, keys, scale=0.1, single_pass_max_length=-1)
     with pytest.raises(ValueError, match="finite"):
         ext.int8_quantized_sdpa(q, keys, keys, scale=float("nan"))
-    with pytest.raises(ValueError, match="L=1"):
+    # multi-token queries: 16-bit queries over the symmetric cache, L <= N
+    # under a causal mask; the affine tuple serves single-token decode only
+    with pytest.raises(ValueError, match="float16 or bfloat16 queries"):
         ext.int8_quantized_sdpa(torch.zeros((1, 8, 2, 128)), keys, keys, scale=0.1)
+    q2 = torch.zeros((1, 8, 32, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="L <= N"):
+        ext.int8_quantized_sdpa(q2, keys, keys, scale=0.1, mask="causal")
+    aff = (torch.zeros((1, 2, 16, 32), dtype=torch.int32), torch.ones((1, 2, 16, 4), dtype=torch.bfloat16),
+           torch.zeros((1, 2, 16, 4), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="symmetric int8 cache"):
+        ext.int8_quantized_sdpa(q2[:, :, :2], aff, aff, scale=0.1)
     # unquantized caches take torch's attention
     out = dispatch_sdpa(torch.ones((1, 8, 1, 64)), torch.ones((1, 2, 5, 64)),
                         torch.ones((1, 2, 5, 64)), cache=None, scale=0.125, mask=None)
@@ -150,3 +159,20 @@ def test_w8a16_layer_contract():
     assert not W8A16PerChannelLinear.supports_rows(1, torch.float32)
     assert not W8A16PerChannelLinear.supports_rows(1, torch.bfloat16,
                                                    torch.zeros(1, k, dtype=torch.bfloat16))
+
+
+def test_quantized_kv_cache_contract():
+    """QuantizedKVCache mirrors mlx-lm's interface: 8 bits only, the two
+    formats, capacity in steps of 256; appends run on the device only."""
+    with pytest.raises(ValueError, match="8-bit"):
+        sparkq.QuantizedKVCache(bits=4)
+    with pytest.raises(ValueError, match="kv_format"):
+        sparkq.QuantizedKVCache(kv_format="fp8")
+    cache = sparkq.QuantizedKVCache(group_size=64)
+    assert cache.offset == 0 and cache.step == 256 and cache.state == (None, None)
+    x = torch.zeros((1, 2, 3, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        cache.update_and_fetch(x, x)
+    with pytest.raises(ValueError, match="capacity"):
+        ext.kv_append(x, (torch.zeros((1, 2, 2, 128), dtype=torch.int8),
+                          torch.zeros((1, 2, 2), dtype=torch.float16)), 0)
