@@ -215,6 +215,50 @@ def bench_sdpa(torch, sparkq, dev, b, n, iters):
             "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": kv_bytes}
 
 
+def bench_prefill(torch, sparkq, dev, length, n, iters):
+    """INT8-KV prefill attention, s8 cache: B=1, 32 query / 8 KV heads,
+    D=128, bottom-right causal. Useful flop: 4*Hq*D per visible (query,
+    token) pair."""
+    b, hq, hkv, d = 1, 32, 8, 128
+    kc, ks = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
+    vc, vs = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
+    q = torch.randn((b, hq, length, d), device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(d)
+
+    def fn():
+        sparkq.int8_quantized_sdpa(q, (kc, ks), (vc, vs), scale=scale, mask="causal", out=out)
+
+    graph = capture(torch, fn)
+    ms = Timer(torch).time(graph.replay, iters, 2)
+    pairs = sum(n - length + i + 1 for i in range(length))
+    flop = 4.0 * b * hq * d * pairs
+    return {"ms": round(ms, 4), "TFLOP/s": round(flop / ms / 1e9, 1),
+            "frac_f16_peak": round(flop / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}
+
+
+def bench_kv_append(torch, sparkq, dev, iters):
+    """Quantize-on-append of one decode token and of a 2048-token prefill
+    chunk into 8 KV heads of D=128 (both formats): bytes read + written."""
+    res = {}
+    for fmt, g in (("s8", 32), ("affine_u8", 32)):
+        for length in (1, 2048):
+            cache = sparkq.QuantizedKVCache(group_size=g, kv_format=fmt)
+            x = torch.randn((1, 8, length, 128), device=dev).to(torch.bfloat16)
+            cache.update_and_fetch(x, x)
+            store = cache.keys
+
+            def fn():
+                for _ in range(32):
+                    sparkq.kv_append(x, store, 0, group_size=g)
+
+            graph = capture(torch, fn)
+            ms = Timer(torch).time(graph.replay, iters, 2) / 32
+            nbytes = x.numel() * 2 + x.numel() + (8 * length * (2 if fmt == "s8" else 2 * 2 * 128 // g))
+            res[f"{fmt} L={length}"] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1)}
+    return res
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w4_gemv_gate_up_m1_pmc.md")
 
 
@@ -361,6 +405,11 @@ def main():
         log("INT8-KV decode attention")
         extras["int8kv_sdpa_decode"] = {f"B={b} N={n}": bench_sdpa(torch, sparkq, dev, b, n, 5)
                                         for b in (1, 8) for n in (4096, 32768)}
+        log("INT8-KV prefill attention and KV append")
+        extras["int8kv_sdpa_prefill_causal"] = {
+            f"L={l} N={n}": bench_prefill(torch, sparkq, dev, l, n, 5)
+            for l, n in ((2048, 2048), (512, 4096))}
+        extras["kv_append"] = bench_kv_append(torch, sparkq, dev, 10)
 
     cpu = None
     if not args.skip_cpu:
