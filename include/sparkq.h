@@ -259,6 +259,73 @@ int sparkq_kv_append(const void* x, void* codes, void* scales, void* biases,
                      int64_t offset, int group_size, int kv_format,
                      int x_dtype, const int64_t* strides, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Decoder-layer steps around the W4 projections (16-bit graph semantics:
+ * every operation computes in fp32 and rounds to dtype, BF16 or F16; all
+ * tensors contiguous, weights in the W4 affine layout of
+ * sparkq_w4a16_linear, group_size in {32,64,128}).
+ * ---------------------------------------------------------------------- */
+
+/* FFN block of the decoder layer: compiled_ffn (spark_mlx_llm/ops/ffn.py:
+ * 83-105, dispatched by dispatch_ffn :17-80):
+ *   hidden = x + attn
+ *   normed = rms_norm(hidden, norm_w, eps) = w * to_dtype(hidden * rsqrt(
+ *            mean(hidden^2) + eps))                    (mx.fast.rms_norm)
+ *   act    = gelu(gate(normed)) * up(normed),  gelu(v) = v * (1 +
+ *            erf(v / sqrt(2))) / 2                     (mlx.nn.gelu)
+ *   out    = hidden + down(act)
+ *   x, attn, out [M,K]; norm_w [K]; gate, up: weights [I,K/8] and scales,
+ *   biases [I,K/G]; down: [K,I/8] and [K,I/G]. K and I multiples of 64.
+ * One launch does the residual, the norm, both projections and the
+ * activation for M <= 4 rows, and the down projection adds the residual in
+ * its epilogue. The workspace (sparkq_ffn_workspace_bytes) holds the
+ * projections' split-K counters first (zero before the first call, left
+ * zero) and then hidden, the normed rows and act. */
+size_t sparkq_ffn_workspace_bytes(int64_t M, int64_t K, int64_t I, int group_size);
+int sparkq_ffn(const void* x, const void* attn, const void* norm_w, float eps,
+               const uint32_t* gate_w, const void* gate_scales, const void* gate_biases,
+               const uint32_t* up_w, const void* up_scales, const void* up_biases,
+               const uint32_t* down_w, const void* down_scales, const void* down_biases,
+               void* out, int64_t M, int64_t K, int64_t I, int group_size, int dtype,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused QKV projection + RoPE of one token: spark_qkv_rope
+ * (X/src/spark_qkv_rope.cpp:14-102; bindings X/src/bindings.cpp:73-74;
+ * caller spark_mlx_llm/ops/qkv.py:41-53,110-137):
+ *   qkv = quantized_matmul(x, w, scales, biases) [N], N = q_size + 2*kv_size
+ *   q [n_heads,head_dim], k [n_kv_heads,head_dim] = mx.fast.rope(.,
+ *     rope_dims, traditional=false, rope_base, scale=1, offset); v as is.
+ * x [hidden] (the [1,1,hidden] token). q, k, v are contiguous [heads,
+ * head_dim], i.e. [1,heads,1,head_dim]. One launch when head_dim and
+ * rope_dims are multiples of 8 and hidden >= 1536; otherwise the projection
+ * and a rope pass through the workspace (sparkq_qkv_rope_workspace_bytes;
+ * counters first, as above). Only bits == 4 is run. */
+size_t sparkq_qkv_rope_workspace_bytes(int64_t hidden, int num_heads, int num_kv_heads,
+                                       int head_dim, int group_size);
+int sparkq_qkv_rope(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                    void* q, void* k, void* v, int64_t hidden, int q_size, int kv_size,
+                    int num_heads, int num_kv_heads, int head_dim, int rope_dims,
+                    float rope_base, int64_t offset, int group_size, int bits, int dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* mx.fast.rms_norm with an optional residual (spark_mlx_llm/ops/ffn.py:98-99
+ * and the decoder's input_layernorm, spark_mlx_llm/model.py:240-254): per row
+ * of x [M,K], hidden = x (+ residual), out = weight * to_dtype(hidden *
+ * rsqrt(mean(hidden^2) + eps)); hidden is also written to hidden_out when
+ * that is not NULL. residual may be NULL. */
+int sparkq_rms_norm(const void* x, const void* residual, const void* weight, float eps,
+                    void* hidden_out, void* out, int64_t M, int64_t K, int dtype, void* stream);
+
+/* mx.fast.rope over x [rows,D] (rows = B*H*L, token l = row % L at position
+ * offset + l), as applied by _apply_rope (spark_mlx_llm/ops/qkv.py:176-177)
+ * and spark_qkv_rope (X/src/spark_qkv_rope.cpp:99-100): pairs (i, i+dims/2)
+ * (or (2i, 2i+1) when traditional) for i < dims/2 rotated by theta =
+ * (scale * position) * base^(-2i/dims); dims past `dims` copied. out may
+ * equal x. */
+int sparkq_rope(const void* x, void* out, int64_t rows, int64_t L, int64_t D, int dims,
+                int traditional, float base, float scale, int64_t offset, int dtype,
+                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,7 @@ __all__ = [
     "kv_dequantize_affine_u8", "sdpa_decode", "sdpa_prefill",
     "cpu_w4a16_gemv", "scalar_f32_to_bf16", "scalar_f32_to_f16",
     "scalar_f16_to_f32",
+    "add16", "rms_norm16", "gelu16", "gelu_mul16", "rope16", "ffn_block", "qkv_rope",
 ]
 
 F32, F16, BF16 = 0, 1, 2
@@ -360,6 +361,123 @@ def sdpa_prefill(q, kdq, vdq, scale: float, causal: bool) -> np.ndarray:
     p = np.exp(scores)
     p /= p.sum(axis=-1, keepdims=True)
     return p @ v
+
+
+# ---------------------------------------------------------------------------
+# Decoder-layer steps around the projections, in the 16-bit graph's rounding.
+# MLX 0.32.4 (un-vendored; pinned by X/spark_mlx_ext/__init__.py:6-7) runs
+# each operation of a bf16/f16 graph in fp32 and rounds its result to the
+# array dtype; under mx.compile the intermediates keep their dtype. The
+# functions below restate that arithmetic; the 16-bit inputs and outputs are
+# bit patterns.
+# ---------------------------------------------------------------------------
+
+def add16(a16, b16, dtype: int = BF16) -> np.ndarray:
+    """a + b of two 16-bit arrays: the fp32 sum rounded to the dtype
+    (hidden = x + attention_output and hidden + mlp_output,
+    spark_mlx_llm/ops/ffn.py:98,105)."""
+    return round16(bits_to_f32(a16, dtype) + bits_to_f32(b16, dtype), dtype)
+
+
+def rms_norm16(h16, w16, eps: float, dtype: int = BF16) -> np.ndarray:
+    """mx.fast.rms_norm(h, w, eps) over the last axis (spark_mlx_llm/ops/
+    ffn.py:99): inv = rsqrt(mean(h^2) + eps) (float64 here, rounded to fp32),
+    out = w * T(h * inv), each product rounded to the dtype."""
+    h = bits_to_f32(h16, dtype)
+    w = bits_to_f32(w16, dtype)
+    h64 = h.astype(np.float64)
+    ms = (h64 * h64).mean(axis=-1, keepdims=True)
+    inv = (1.0 / np.sqrt(ms + np.float64(np.float32(eps)))).astype(np.float32)
+    n = bits_to_f32(round16(h * inv, dtype), dtype)
+    return round16(w * n, dtype)
+
+
+def gelu16(g16, dtype: int = BF16) -> np.ndarray:
+    """mlx.nn.gelu on a 16-bit array, x * (1 + erf(x / sqrt(2))) / 2
+    (spark_mlx_llm/ops/ffn.py:102): the Python constant sqrt(2) takes the
+    array dtype; every operation rounds to the dtype; erf of the 16-bit value
+    is rounded to fp32 before the dtype."""
+    from scipy.special import erf
+
+    def r(v):
+        return bits_to_f32(round16(np.asarray(v, np.float32), dtype), dtype)
+
+    g = bits_to_f32(g16, dtype)
+    c = r(np.float32(np.sqrt(2.0)))
+    t1 = r(g / c)
+    e = r(erf(t1.astype(np.float64)).astype(np.float32))
+    t3 = r(np.float32(1.0) + e)
+    t4 = r(g * t3)
+    return round16(t4 / np.float32(2.0), dtype)
+
+
+def gelu_mul16(g16, u16, dtype: int = BF16) -> np.ndarray:
+    """gelu(gate) * up, the product rounded to the dtype (ffn.py:102)."""
+    return round16(bits_to_f32(gelu16(g16, dtype), dtype) * bits_to_f32(u16, dtype), dtype)
+
+
+def rope16(x16, dims: int, base: float, offset: int, dtype: int = BF16,
+           traditional: bool = False, scale: float = 1.0) -> np.ndarray:
+    """mx.fast.rope on x [..., L, D] (X/src/spark_qkv_rope.cpp:99-100;
+    spark_mlx_llm/ops/qkv.py:176-177). Token l sits at position offset + l.
+    For pair i < dims/2: d = fp32(i) / fp32(dims/2), inv_freq = 2^(-d *
+    log2(base)) (fp32 exponent, the power correctly rounded to fp32), theta =
+    fp32(scale * position) * inv_freq in fp32; x1 = x[i], x2 = x[i + dims/2]
+    (x[2i], x[2i+1] when traditional); out1 = x1 cos - x2 sin, out2 = x1 sin
+    + x2 cos (float64 here), rounded to the dtype; dims past `dims` unchanged."""
+    x = bits_to_f32(x16, dtype).astype(np.float64)
+    length = x.shape[-2]
+    half = dims // 2
+    l2b = np.float32(np.log2(np.float64(np.float32(base))))
+    d = np.arange(half, dtype=np.float32) / np.float32(half)
+    inv = np.exp2((-d * l2b).astype(np.float64)).astype(np.float32)
+    pos = (np.float32(scale) * (np.float32(offset) + np.arange(length, dtype=np.float32)))
+    theta = (pos[:, None] * inv[None, :]).astype(np.float32).astype(np.float64)
+    c, s = np.cos(theta), np.sin(theta)
+    if traditional:
+        i1, i2 = np.arange(0, dims, 2), np.arange(1, dims, 2)
+    else:
+        i1, i2 = np.arange(half), np.arange(half, dims)
+    x1, x2 = x[..., i1], x[..., i2]
+    out = np.array(bits_to_f32(x16, dtype), np.float64)
+    out[..., i1] = x1 * c - x2 * s
+    out[..., i2] = x1 * s + x2 * c
+    res = round16(out.astype(np.float32), dtype)
+    return np.where(np.arange(x.shape[-1]) < dims, res, np.asarray(x16, np.uint16))
+
+
+def ffn_block(x16, attn16, norm16, eps, gate, up, down, group_size: int,
+              dtype: int = BF16) -> dict:
+    """compiled_ffn (spark_mlx_llm/ops/ffn.py:96-105) in stages: hidden =
+    x + attn; normed = rms_norm(hidden); gate/up = the W4 projections of
+    normed (float64, rounded to the dtype as mx.quantized_matmul returns
+    them); act = gelu(gate) * up; mlp = down(act); out = hidden + mlp.
+    gate, up, down are (packed weight, scales, biases)."""
+    hidden = add16(x16, attn16, dtype)
+    normed = rms_norm16(hidden, norm16, eps, dtype)
+    g = w4a16_matmul(normed, *gate, group_size, dtype)
+    u = w4a16_matmul(normed, *up, group_size, dtype)
+    act = gelu_mul16(round16(g, dtype), round16(u, dtype), dtype)
+    mlp = w4a16_matmul(act, *down, group_size, dtype)
+    out = add16(hidden, round16(mlp, dtype), dtype)
+    return {"hidden": hidden, "normed": normed, "gate": g, "up": u, "act": act, "mlp": mlp,
+            "out": out}
+
+
+def qkv_rope(x16, wq, s, b, group_size: int, n_heads: int, n_kv: int, head_dim: int,
+             rope_dims: int, base: float, offset: int, dtype: int = BF16):
+    """spark_qkv_rope (X/src/spark_qkv_rope.cpp:83-101) for one token x [K]:
+    qkv = the W4 projection rounded to the dtype; split into q, k, v
+    [heads, head_dim]; q and k through rope16 at position offset. Returns
+    (q, k, v, qkv) with qkv the float64 projection."""
+    qkv = w4a16_matmul(np.asarray(x16, np.uint16).reshape(1, -1), wq, s, b, group_size, dtype)[0]
+    r = round16(qkv, dtype)
+    qs, ks = n_heads * head_dim, n_kv * head_dim
+    q = r[:qs].reshape(n_heads, 1, head_dim)
+    k = r[qs:qs + ks].reshape(n_kv, 1, head_dim)
+    v = r[qs + ks:].reshape(n_kv, head_dim)
+    return (rope16(q, rope_dims, base, offset, dtype)[:, 0],
+            rope16(k, rope_dims, base, offset, dtype)[:, 0], v, qkv)
 
 
 # ---------------------------------------------------------------------------

@@ -19,7 +19,8 @@ namespace sparkq {
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G);
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
                  int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, void* ws,
-                 size_t wsb, hipStream_t st);
+                 size_t wsb, hipStream_t st, const void* res = nullptr,
+                 bool* res_done = nullptr);
 int w4a16_dequantize(const uint32_t* w, const void* s, const void* b, float* out, int64_t N,
                      int64_t K, int G, int sdt, hipStream_t st);
 int w4_quantize(const void* w, uint32_t* wq, void* s, void* b, int64_t N, int64_t K, int G,
@@ -50,6 +51,20 @@ int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const voi
                         const int64_t* strides, hipStream_t st);
 int w8a16_linear(const void* x, const int8_t* w, const float* scales, void* y, int64_t M,
                  int64_t N, int64_t K, int xdt, int ydt, hipStream_t st);
+// launchers (layer.hip)
+size_t ffn_workspace(int64_t M, int64_t K, int64_t I, int G);
+int ffn(const void* x, const void* attn, const void* nw, float eps, const uint32_t* wg,
+        const void* sg, const void* bg, const uint32_t* wu, const void* su, const void* bu,
+        const uint32_t* wd, const void* sd, const void* bd, void* out, int64_t M, int64_t K,
+        int64_t I, int G, int dt, void* ws, size_t wsb, hipStream_t st);
+size_t qkv_rope_workspace(int64_t K, int nh, int nkv, int hd, int G);
+int qkv_rope(const void* x, const uint32_t* w, const void* s, const void* b, void* q, void* k,
+             void* v, int64_t K, int nh, int nkv, int hd, int rd, float base, int64_t offset,
+             int G, int dt, void* ws, size_t wsb, hipStream_t st);
+int rope(const void* x, void* out, int64_t rows, int64_t L, int64_t D, int dims, int traditional,
+         float base, float scale, int64_t offset, int dt, hipStream_t st);
+int rms_norm(const void* x, const void* xres, const void* w, float eps, void* hid, void* out,
+             int64_t M, int64_t K, int dt, hipStream_t st);
 
 static thread_local char g_last_error[512] = "";
 
@@ -379,6 +394,125 @@ int sparkq_w8a16_linear(const void* x, const int8_t* w, const float* scales, voi
           "w8a16_linear: x and w must be 16-byte aligned");
   DEVICE_OK();
   return w8a16_linear(x, w, scales, y, M, N, K, x_dtype, y_dtype, (hipStream_t)stream);
+}
+
+size_t sparkq_ffn_workspace_bytes(int64_t M, int64_t K, int64_t I, int group_size) {
+  if (M <= 0 || K <= 0 || I <= 0 || group_size <= 0) return 0;
+  return ffn_workspace(M, K, I, group_size);
+}
+
+int sparkq_ffn(const void* x, const void* attn, const void* norm_w, float eps,
+               const uint32_t* gate_w, const void* gate_scales, const void* gate_biases,
+               const uint32_t* up_w, const void* up_scales, const void* up_biases,
+               const uint32_t* down_w, const void* down_scales, const void* down_biases,
+               void* out, int64_t M, int64_t K, int64_t I, int group_size, int dtype,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  REQUIRE(x && attn && norm_w && gate_w && gate_scales && gate_biases && up_w && up_scales &&
+              up_biases && down_w && down_scales && down_biases && out,
+          "ffn: null tensor pointer");
+  REQUIRE(M > 0 && K > 0 && I > 0, "ffn: M, K and I must be positive");
+  REQUIRE(M <= kI32Max && K <= kI32Max && I <= kI32Max && M * K <= kI32Max && M * I <= kI32Max,
+          "ffn: dimension too large");
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "ffn: group_size must be 32, 64 or 128 (got %d)", group_size);
+  REQUIRE_SUPPORTED(K % 64 == 0 && I % 64 == 0,
+                    "ffn: hidden and intermediate sizes must be multiples of 64 (got %lld, %lld)",
+                    (long long)K, (long long)I);
+  REQUIRE(K % group_size == 0 && I % group_size == 0,
+          "ffn: hidden and intermediate sizes must be multiples of group_size=%d", group_size);
+  REQUIRE_SUPPORTED(is_half_dtype(dtype), "ffn: dtype must be bfloat16 or float16");
+  REQUIRE(std::isfinite(eps) && eps >= 0.0f, "ffn: eps must be finite and non-negative");
+  REQUIRE(aligned(x, 16) && aligned(attn, 16) && aligned(norm_w, 16) && aligned(out, 4) &&
+              aligned(gate_w, 16) && aligned(up_w, 16) && aligned(down_w, 16),
+          "ffn: x, attn, norm_w and the weights must be 16-byte aligned");
+  REQUIRE(aligned(gate_scales, 4) && aligned(gate_biases, 4) && aligned(up_scales, 4) &&
+              aligned(up_biases, 4) && aligned(down_scales, 4) && aligned(down_biases, 4),
+          "ffn: scales and biases must be 4-byte aligned");
+  REQUIRE(aligned(workspace, 256), "ffn: workspace must be 256-byte aligned");
+  DEVICE_OK();
+  return ffn(x, attn, norm_w, eps, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
+             down_w, down_scales, down_biases, out, M, K, I, group_size, dtype, workspace,
+             workspace_bytes, (hipStream_t)stream);
+}
+
+size_t sparkq_qkv_rope_workspace_bytes(int64_t hidden, int num_heads, int num_kv_heads,
+                                       int head_dim, int group_size) {
+  if (hidden <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || group_size <= 0)
+    return 0;
+  return qkv_rope_workspace(hidden, num_heads, num_kv_heads, head_dim, group_size);
+}
+
+int sparkq_qkv_rope(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                    void* q, void* k, void* v, int64_t hidden, int q_size, int kv_size,
+                    int num_heads, int num_kv_heads, int head_dim, int rope_dims,
+                    float rope_base, int64_t offset, int group_size, int bits, int dtype,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  // the checks and messages of X/src/spark_qkv_rope.cpp:29-81
+  REQUIRE(x && w && scales && biases && q && k && v, "[spark_qkv_rope] null tensor pointer.");
+  REQUIRE(hidden > 0 && hidden <= kI32Max,
+          "[spark_qkv_rope] x must have shape [1, 1, hidden] with hidden > 0.");
+  REQUIRE(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
+              num_heads % num_kv_heads == 0 &&
+              (int64_t)q_size == (int64_t)num_heads * head_dim &&
+              (int64_t)kv_size == (int64_t)num_kv_heads * head_dim,
+          "[spark_qkv_rope] Invalid head counts, head_dim, q_size, or kv_size.");
+  REQUIRE(rope_dims > 0 && rope_dims % 2 == 0 && rope_dims <= head_dim &&
+              std::isfinite(rope_base) && rope_base > 0.0f,
+          "[spark_qkv_rope] rope_dims must be positive, even, and no larger than head_dim; "
+          "rope_base must be positive and finite.");
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "[spark_qkv_rope] group_size must be 32, 64, or 128.");
+  REQUIRE(bits == 1 || bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8,
+          "[spark_qkv_rope] bits must be 1, 2, 3, 4, 5, 6, or 8.");
+  REQUIRE_SUPPORTED(bits == 4, "[spark_qkv_rope] only bits=4 is supported here (got %d)", bits);
+  REQUIRE(hidden % group_size == 0,
+          "[spark_qkv_rope] Packed weight and quantization metadata shapes do not match x, "
+          "q_size, kv_size, group_size, and bits.");
+  REQUIRE((int64_t)q_size + 2LL * kv_size <= kI32Max, "[spark_qkv_rope] q_size + 2*kv_size too large");
+  REQUIRE_SUPPORTED(hidden % 64 == 0, "[spark_qkv_rope] hidden must be a multiple of 64 (got %lld)",
+                    (long long)hidden);
+  REQUIRE_SUPPORTED(is_half_dtype(dtype), "[spark_qkv_rope] x must be bfloat16 or float16");
+  REQUIRE(offset >= 0 && offset < (1LL << 24), "[spark_qkv_rope] offset must be in [0, 2^24)");
+  REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(scales, 4) && aligned(biases, 4) &&
+              aligned(q, 2) && aligned(k, 2) && aligned(v, 2) && aligned(workspace, 256),
+          "[spark_qkv_rope] x and w must be 16-byte aligned");
+  DEVICE_OK();
+  return qkv_rope(x, w, scales, biases, q, k, v, hidden, num_heads, num_kv_heads, head_dim,
+                  rope_dims, rope_base, offset, group_size, dtype, workspace, workspace_bytes,
+                  (hipStream_t)stream);
+}
+
+int sparkq_rope(const void* x, void* out, int64_t rows, int64_t L, int64_t D, int dims,
+                int traditional, float base, float scale, int64_t offset, int dtype,
+                void* stream) {
+  REQUIRE(x && out, "rope: null tensor pointer");
+  REQUIRE(rows >= 0 && L > 0 && D > 0 && rows % L == 0, "rope: rows must be a multiple of L > 0");
+  REQUIRE(rows * D <= (1LL << 40) && D <= kI32Max && L <= kI32Max, "rope: dimension too large");
+  REQUIRE(dims > 0 && dims % 2 == 0 && dims <= D,
+          "rope: dims must be positive, even and no larger than the last axis");
+  REQUIRE(std::isfinite(base) && base > 0.0f && std::isfinite(scale),
+          "rope: base must be positive and finite");
+  REQUIRE(offset >= 0 && offset + L <= (1LL << 24), "rope: positions must lie in [0, 2^24)");
+  REQUIRE_SUPPORTED(is_half_dtype(dtype), "rope: dtype must be bfloat16 or float16");
+  REQUIRE(aligned(x, 2) && aligned(out, 2), "rope: tensors must be 2-byte aligned");
+  DEVICE_OK();
+  return rope(x, out, rows, L, D, dims, traditional ? 1 : 0, base, scale, offset, dtype,
+              (hipStream_t)stream);
+}
+
+int sparkq_rms_norm(const void* x, const void* residual, const void* weight, float eps,
+                    void* hidden_out, void* out, int64_t M, int64_t K, int dtype, void* stream) {
+  REQUIRE(x && weight && out, "rms_norm: null tensor pointer");
+  REQUIRE(M >= 0 && K > 0 && M <= kI32Max && K <= kI32Max && M * K <= (1LL << 40),
+          "rms_norm: bad shape");
+  REQUIRE(std::isfinite(eps) && eps >= 0.0f, "rms_norm: eps must be finite and non-negative");
+  REQUIRE_SUPPORTED(is_half_dtype(dtype), "rms_norm: dtype must be bfloat16 or float16");
+  REQUIRE(aligned(x, 2) && aligned(weight, 2) && aligned(out, 2) && aligned(residual, 2) &&
+              aligned(hidden_out, 2),
+          "rms_norm: tensors must be 2-byte aligned");
+  if (M == 0) return 0;
+  DEVICE_OK();
+  return rms_norm(x, residual, weight, eps, hidden_out, out, M, K, dtype, (hipStream_t)stream);
 }
 
 }  // extern "C"

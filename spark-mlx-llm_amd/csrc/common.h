@@ -249,6 +249,44 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, float v, int dty
   }
 }
 
+// ---------------------------------------------------------------------------
+// elementwise steps of the decoder layer around the projections, each with
+// the rounding points of the reference's 16-bit graph: every operation of the
+// bf16/fp16 graph computes in fp32 and rounds to the 16-bit type.
+// ---------------------------------------------------------------------------
+// Round v to T, then add a 16-bit residual (hidden + mlp_output,
+// spark_mlx_llm/ops/ffn.py:105). The caller rounds the sum when it stores.
+template <typename T>
+__device__ __forceinline__ float add_rounded(float v, uint16_t res) {
+  return T::to_f32(T::from_f32(v)) + T::to_f32(res);
+}
+
+// gelu(gate) * up as mlx.nn.gelu computes it on a 16-bit array,
+// x * (1 + erf(x / sqrt(2))) / 2 (spark_mlx_llm/ops/ffn.py:102): the constant
+// sqrt(2) is rounded to T (1.4140625 for both types) and each operation's
+// result is rounded to T. erf runs in double and is rounded to fp32 first,
+// as a float erf would deliver it. g and u are the projections' fp32 sums;
+// the result is the product's fp32 value, which the caller rounds to T.
+template <typename T>
+__device__ __forceinline__ float gelu_mul(float g, float u) {
+  auto r = [](float v) { return T::to_f32(T::from_f32(v)); };
+  const float gate = r(g), up = r(u);
+  const float c = r(1.41421356237309515f);
+  const float t1 = r(gate / c);
+  const float e = r((float)erf((double)t1));
+  const float t3 = r(1.0f + e);
+  const float t5 = r(r(gate * t3) / 2.0f);
+  return t5 * up;
+}
+
+// Inverse frequency of rotary pair i of mx.fast.rope (non-traditional):
+// 2^(-(i / half) * log2(base)), d and the exponent in fp32 and the power
+// correctly rounded to fp32 (through double).
+__device__ __forceinline__ float rope_inv_freq(int i, int half, float log2_base) {
+  const float d = (float)i / (float)half;
+  return (float)exp2((double)(-d * log2_base));
+}
+
 __device__ __forceinline__ float load_in(const void* p, int64_t idx, int dtype) {
   if (dtype == SPARKQ_F32) return reinterpret_cast<const float*>(p)[idx];
   uint16_t h = reinterpret_cast<const uint16_t*>(p)[idx];

@@ -146,7 +146,46 @@ struct GemvArgs {
   int SG;       // span groups per row (1, 2 or 4)
   int USr;      // spans per group (the last group may have fewer)
   int R;        // rows per workgroup
+  // plain GEMV: 16-bit residual [M][N] added to the rounded output (or null)
+  const uint16_t* res;
+  // fused layer steps (GemvFuse)
+  const uint16_t* xr;   // kFfnGateUp: residual added to x before the norm (or null)
+  const uint16_t* nw;   // kFfnGateUp: RMSNorm weight [K]
+  uint16_t* hid;        // kFfnGateUp: x + xr [M][K], written by workgroup 0 (or null)
+  uint16_t* nrm;        // kFfnGateUp: the normed activations [M][K], workgroup 0 (or null)
+  float eps;
+  const uint32_t* w2;   // kFfnGateUp: the up projection's weights, scales, biases
+  const uint16_t* sc2;
+  const uint16_t* bi2;
+  void* y2;             // kQkvRope: key and value outputs
+  void* y3;
+  int heads;            // kQkvRope: heads of the query and key sections
+  int hd, rd;           // kQkvRope: head_dim and rope_dims
+  int q_rows, kv_rows;  // kQkvRope: q_size and kv_size
+  float log2_base;      // kQkvRope: log2 of the RoPE base
+  float pos;            // kQkvRope: the token's position (the cache offset)
 };
+
+// Decoder-layer steps fused into the GEMV (template parameter FUSE):
+//  kFfnGateUp  the residual add and RMSNorm of the FFN input in the prologue;
+//              gate and up row quads interleaved (even virtual quad t -> gate
+//              quad t/2, odd -> up quad t/2) and gelu(gate) * up written as
+//              the output (spark_mlx_llm/ops/ffn.py:98-102);
+//  kQkvRope    the QKV projection of one token with rotary embedding of the
+//              query and key heads in the epilogue: within each head the row
+//              quad of dims i..i+3 and the one of i + rope_dims/2 are an
+//              even/odd virtual pair (X/src/spark_qkv_rope.cpp:83-101).
+enum GemvFuse { kPlain = 0, kFfnGateUp = 1, kQkvRope = 2 };
+
+// Real row quad of virtual quad vq under the kQkvRope pairing: head h of the
+// query and key sections holds hd/4 quads; its first rope_dims/4 virtual
+// quads are the pairs (p, p + rope_dims/8), the rest keep their place, and so
+// do the value rows.
+__device__ __forceinline__ int qkv_real_quad(int vq, int hq, int P, int heads) {
+  const int h = vq / hq, w = vq - h * hq;
+  if (h >= heads || w >= 2 * P) return vq;
+  return h * hq + (w >> 1) + (w & 1) * P;
+}
 
 constexpr int kGemvXP = 2;   // staged activation pieces (64 B) per thread, at most
 constexpr int kGemvSP = 4;   // staged (scale, bias) pieces (16 B each) per thread, at most
@@ -165,6 +204,7 @@ struct GemvLds {
   int xs;    // sums of each 32-k piece: [K/32][4] fp32 (rows past M unused)
   int sb;    // (scale, bias) of the workgroup's rows: [R][K/G] dwords
   int red;   // cross-wave partial sums: [NW][RQW][4][4] fp32
+  int fz;    // fused epilogues: final sums of the workgroup's rows [R][4] fp32
   int bytes;
 };
 __host__ __device__ __forceinline__ GemvLds gemv_lds(int M, int K, int R, int G, int NW, int RQW) {
@@ -173,19 +213,25 @@ __host__ __device__ __forceinline__ GemvLds gemv_lds(int M, int K, int R, int G,
   l.xs = l.xp + ((M * K * 2 + 1023) & ~1023);
   l.sb = l.xs + (K / 32) * 16;
   l.red = l.sb + ((R * (K / G) * 4 + 15) & ~15);
-  l.bytes = l.red + NW * RQW * 64;
+  l.fz = l.red + NW * RQW * 64;
+  l.bytes = l.fz + R * 16;
   return l;
 }
 
 
-template <typename T, int G, int MQ, int US, int RQW, int NW>
+template <typename T, int G, int MQ, int US, int RQW, int NW, int FUSE = kPlain>
 __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int NT = 64 * NW;
+  // staged activation pieces per thread: the FFN prologue also holds the
+  // residual and norm weight pieces, so at one row it stages one piece each
+  constexpr int XP = FUSE == kFfnGateUp && MQ == 1 ? 1 : kGemvXP;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = lane >> 2, j = lane & 3;
   const int M = a.M, N = a.N, K = a.K, SG = a.SG, R = a.R;
+  // rows of one weight matrix (the gate and up matrices each hold N/2)
+  const int NR = FUSE == kFfnGateUp ? N >> 1 : N;
   const int RB = K >> 1;                       // bytes per weight row
   const int U = (RB + 255) >> 8;               // spans per row
   const int ng = K / G;                        // groups per row
@@ -197,33 +243,75 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   const GemvLds L = gemv_lds(M, K, R, G, NW, RQW);
 
   const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
-  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)NR * RB);
   const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
   const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
 
   // 1. staging loads: activation pieces (64 B) and (scale, bias) pieces
   const int nxp = M * (K >> 5);                // activation pieces
   const int nsp = (R * ng) >> 3;               // 16-byte scale pieces of the workgroup
-  u32x4_t xr[kGemvXP][4];
+  u32x4_t xr[XP][4];
+  constexpr int XF = FUSE == kFfnGateUp ? XP : 1;
+  u32x4_t rr[XF][4], nr[XF][4];                // residual and norm weight pieces
   u32x4_t sr[kGemvSP], br[kGemvSP];
   // a wave with no piece to fetch skips the instruction (the texture unit
   // charges per instruction, lanes or not); the condition is wave-uniform
 #pragma unroll
-  for (int i = 0; i < kGemvXP; ++i) {
+  for (int i = 0; i < XP; ++i) {
     const int pi = tid + i * NT;
     if (i * NT + 64 * wave < nxp) {
       const uint32_t off = pi < nxp ? 64u * pi : kOob;
 #pragma unroll
       for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
+      if constexpr (FUSE == kFfnGateUp) {
+        const rsrc_t rr_ = make_rsrc(a.xr, a.xr ? (uint32_t)M * K * 2 : 0u);
+        const rsrc_t rn_ = make_rsrc(a.nw, (uint32_t)K * 2);
+        const uint32_t noff = pi < nxp ? 64u * (pi % (K >> 5)) : kOob;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          rr[i][w] = buf_load16(rr_, off + 16 * w);
+          nr[i][w] = buf_load16(rn_, noff + 16 * w);
+        }
+      }
     }
   }
+  if constexpr (FUSE == kPlain) {
 #pragma unroll
-  for (int i = 0; i < kGemvSP; ++i) {
-    const int pi = tid + i * NT;
-    if (i * NT + 64 * wave < nsp) {
-      const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
-      sr[i] = buf_load16(rs, off);
-      br[i] = buf_load16(rb, off);
+    for (int i = 0; i < kGemvSP; ++i) {
+      const int pi = tid + i * NT;
+      if (i * NT + 64 * wave < nsp) {
+        const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
+        sr[i] = buf_load16(rs, off);
+        br[i] = buf_load16(rb, off);
+      }
+    }
+  } else {
+    // the workgroup's virtual quads are not contiguous rows: piece pi is
+    // piece pi % (ng/2) of the 4 contiguous rows of virtual quad pi / (ng/2),
+    // read from that quad's matrix through a per-lane address
+    const int hp = ng >> 1;
+#pragma unroll
+    for (int i = 0; i < kGemvSP; ++i) {
+      const int pi = tid + i * NT;
+      if (i * NT + 64 * wave < nsp) {
+        const int pc = min(pi, nsp - 1);
+        const int vq = min((r0 >> 2) + pc / hp, (N >> 2) - 1), po = pc % hp;
+        const uint16_t* ps = a.sc;
+        const uint16_t* pb = a.bi;
+        int rq;
+        if constexpr (FUSE == kFfnGateUp) {
+          rq = vq >> 1;
+          if (vq & 1) {
+            ps = a.sc2;
+            pb = a.bi2;
+          }
+        } else {
+          rq = qkv_real_quad(vq, a.hd >> 2, a.rd >> 3, a.heads);
+        }
+        const int64_t e = (int64_t)rq * 4 * ng + 8 * po;
+        sr[i] = *reinterpret_cast<const u32x4_t*>(ps + e);
+        br[i] = *reinterpret_cast<const u32x4_t*>(pb + e);
+      }
     }
   }
 
@@ -231,24 +319,116 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   u32x4_t wv[RQW][US];
 #pragma unroll
   for (int r = 0; r < RQW; ++r) {
-    const int row = 4 * (q0 + r) + j;
+    const int vq = q0 + r;
+    int rq = vq;
+    rsrc_t rwr = rw;
+    if constexpr (FUSE == kFfnGateUp) {
+      rq = vq >> 1;
+      if (vq & 1) rwr = make_rsrc(a.w2, (uint32_t)NR * RB);
+    } else if constexpr (FUSE == kQkvRope) {
+      rq = qkv_real_quad(vq, a.hd >> 2, a.rd >> 3, a.heads);
+    }
+    const int row = 4 * rq + j;
 #pragma unroll
     for (int s = 0; s < US; ++s) {
       const int p = 256 * (u0 + s) + 16 * b;
-      const bool ok = row < N && s < ns && p + 16 <= RB;
-      wv[r][s] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
+      const bool ok = row < NR && s < ns && p + 16 <= RB;
+      wv[r][s] = buf_load16(rwr, ok ? (uint32_t)row * RB + p : kOob);
     }
   }
 
   // keep every load above ahead of the arithmetic below
   __builtin_amdgcn_sched_barrier(0);
 
+  // 2b. FFN prologue: hidden = x + residual and its RMSNorm,
+  // w * T(hidden * rsqrt(mean(hidden^2) + eps)) (mx.fast.rms_norm,
+  // spark_mlx_llm/ops/ffn.py:98-99), replacing the staged activations. Every
+  // workgroup reduces the sums of squares in the same order, so all of them
+  // normalise with the same factor.
+  if constexpr (FUSE == kFfnGateUp) {
+    float ss[MQ];
+#pragma unroll
+    for (int m = 0; m < MQ; ++m) ss[m] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nxp) {
+        float q = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t xv = xr[i][w][e];
+            float h0 = T::to_f32((uint16_t)(xv & 0xFFFFu));
+            float h1 = T::to_f32((uint16_t)(xv >> 16));
+            if (a.xr) {
+              const uint32_t rv = rr[i][w][e];
+              h0 = T::to_f32(T::from_f32(h0 + T::to_f32((uint16_t)(rv & 0xFFFFu))));
+              h1 = T::to_f32(T::from_f32(h1 + T::to_f32((uint16_t)(rv >> 16))));
+              xr[i][w][e] = (uint32_t)T::from_f32(h0) | ((uint32_t)T::from_f32(h1) << 16);
+            }
+            q = fmaf(h0, h0, q);
+            q = fmaf(h1, h1, q);
+          }
+        const int m = MQ == 1 ? 0 : pi / (K >> 5);
+#pragma unroll
+        for (int mm = 0; mm < MQ; ++mm) ss[mm] += mm == m ? q : 0.0f;
+      }
+    }
+    float* red = reinterpret_cast<float*>(smem + L.red);
+#pragma unroll
+    for (int m = 0; m < MQ; ++m) {
+      float v = ss[m];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      if (lane == 0) red[wave * 4 + m] = v;
+    }
+    __syncthreads();
+    float inv[MQ];
+#pragma unroll
+    for (int m = 0; m < MQ; ++m) {
+      float t = 0.0f;
+      for (int w = 0; w < NW; ++w) t += red[w * 4 + m];
+      inv[m] = (float)(1.0 / sqrt((double)(t / (float)K + a.eps)));
+    }
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nxp) {
+        const int m = MQ == 1 ? 0 : pi / (K >> 5);
+        float im = inv[0];
+#pragma unroll
+        for (int mm = 1; mm < MQ; ++mm) im = mm == m ? inv[mm] : im;
+        u32x4_t nv[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t xv = xr[i][w][e], wt = nr[i][w][e];
+            const float n0 = T::to_f32(T::from_f32(T::to_f32((uint16_t)(xv & 0xFFFFu)) * im));
+            const float n1 = T::to_f32(T::from_f32(T::to_f32((uint16_t)(xv >> 16)) * im));
+            nv[w][e] = (uint32_t)T::from_f32(T::to_f32((uint16_t)(wt & 0xFFFFu)) * n0) |
+                       ((uint32_t)T::from_f32(T::to_f32((uint16_t)(wt >> 16)) * n1) << 16);
+          }
+        if (blockIdx.x == 0) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            if (a.hid) *reinterpret_cast<u32x4_t*>(a.hid + 32 * pi + 8 * w) = xr[i][w];
+            if (a.nrm) *reinterpret_cast<u32x4_t*>(a.nrm + 32 * pi + 8 * w) = nv[w];
+          }
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) xr[i][w] = nv[w];
+      }
+    }
+  }
+
   // 3. write the staged data to LDS
   {
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
     float* xs = reinterpret_cast<float*>(smem + L.xs);
 #pragma unroll
-    for (int i = 0; i < kGemvXP; ++i) {
+    for (int i = 0; i < XP; ++i) {
       const int pi = tid + i * NT;
       if (pi < nxp) {
         float sum = 0.0f;
@@ -378,8 +558,7 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
         for (int m = 0; m < MQ; ++m) red[((wave * RQW + r) * 4 + lane) * 4 + m] = out[r][m];
     }
     __syncthreads();
-    if (sg != 0) return;
-    if (lane < 4) {
+    if (sg == 0 && lane < 4) {
 #pragma unroll
       for (int r = 0; r < RQW; ++r)
 #pragma unroll
@@ -390,6 +569,65 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
         }
     }
   }
+
+  if constexpr (FUSE != kPlain) {
+    // the partner of virtual quad vq is vq ^ 1: the wave's other quad, or
+    // (one quad per wave) the neighbouring wave's, exchanged through LDS
+    float pv[RQW][MQ];
+    if constexpr (RQW == 2) {
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) {
+        pv[0][m] = out[1][m];
+        pv[1][m] = out[0][m];
+      }
+    } else {
+      float* fz = reinterpret_cast<float*>(smem + L.fz);
+      const int ql = q0 - (r0 >> 2);
+      if (sg == 0 && lane < 4) {
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) fz[(ql * 4 + lane) * 4 + m] = out[0][m];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) pv[0][m] = fz[((ql ^ 1) * 4 + lane) * 4 + m];
+    }
+    if (sg != 0 || lane >= 4) return;
+#pragma unroll
+    for (int r = 0; r < RQW; ++r) {
+      const int vq = q0 + r;
+      if constexpr (FUSE == kFfnGateUp) {
+        // the gate quad's lanes write gelu(gate) * up for rows 4*(vq/2) + lane
+        const int row = 2 * (vq & ~1) + lane;
+        if ((vq & 1) == 0 && row < NR) {
+#pragma unroll
+          for (int m = 0; m < MQ; ++m)
+            if (m < M) store_out(a.y, (int64_t)m * NR + row, gelu_mul<T>(out[r][m], pv[r][m]), a.y_dtype);
+        }
+      } else {
+        const int hq = a.hd >> 2, P = a.rd >> 3;
+        const int h = vq / hq, w = vq - h * hq;
+        const int row = 4 * qkv_real_quad(vq, hq, P, a.heads) + lane;
+        float v = out[r][0];
+        if (h < a.heads && w < 2 * P) {
+          // mx.fast.rope on the 16-bit projections (non-traditional):
+          // x1 = dim i, x2 = dim i + rope_dims/2 of the head
+          const float inv = rope_inv_freq(4 * (w >> 1) + lane, a.rd >> 1, a.log2_base);
+          float sn, cs;
+          sincosf(a.pos * inv, &sn, &cs);
+          const float self = T::to_f32(T::from_f32(v)), other = T::to_f32(T::from_f32(pv[r][0]));
+          v = (w & 1) == 0 ? self * cs - other * sn : other * sn + self * cs;
+        }
+        if (row < a.q_rows)
+          store_out(a.y, row, v, a.y_dtype);
+        else if (row < a.q_rows + a.kv_rows)
+          store_out(a.y2, row - a.q_rows, v, a.y_dtype);
+        else if (row < N)
+          store_out(a.y3, row - a.q_rows - a.kv_rows, v, a.y_dtype);
+      }
+    }
+    return;
+  }
+  if (sg != 0) return;
   if (lane < 4) {
 #pragma unroll
     for (int r = 0; r < RQW; ++r) {
@@ -397,7 +635,11 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
       if (row < N) {
 #pragma unroll
         for (int m = 0; m < MQ; ++m)
-          if (m < M) store_out(a.y, (int64_t)m * N + row, out[r][m], a.y_dtype);
+          if (m < M) {
+            const int64_t idx = (int64_t)m * N + row;
+            const float v = out[r][m];
+            store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
+          }
       }
     }
   }
@@ -434,6 +676,7 @@ struct GemvStreamArgs {
   int nq;  // row quads
   int P;   // workgroups
   int QW;  // row quads of the largest workgroup
+  const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
 };
 
 constexpr int kStreamXP = 1;   // staged activation pieces (64 B) per thread, at most
@@ -619,7 +862,8 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
     }
     v = sum_row16(v);
     const int row = 4 * qa + rl;
-    if (bb == 0 && rl < 4 * nql && row < N) store_out(a.y, row, v, a.y_dtype);
+    if (bb == 0 && rl < 4 * nql && row < N)
+      store_out(a.y, row, a.res ? add_rounded<T>(v, a.res[row]) : v, a.y_dtype);
   }
 }
 
@@ -647,6 +891,7 @@ struct DecodeStreamArgs {
   int nq;  // row quads
   int P;   // workgroups
   int QW;  // row quads of the largest workgroup
+  const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
 };
 
 constexpr int kDecNW = 16;  // waves per workgroup
@@ -851,7 +1096,8 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
       const float* src = part + (((rl >> 2) * U) * 4 + (rl & 3)) * MR + m;
       float v = 0.0f;
       for (int s = 0; s < U; ++s) v += src[s * 4 * MR];
-      store_out(a.y, (int64_t)m * N + row, v, a.y_dtype);
+      const int64_t idx = (int64_t)m * N + row;
+      store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
     }
   }
 }
@@ -1734,9 +1980,9 @@ static GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int G) {
   return p;
 }
 
-template <typename T, int G, int MQ, int US, int RQW, int NW>
+template <typename T, int G, int MQ, int US, int RQW, int NW, int F = kPlain>
 static void launch_gemv_w(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((w4_gemv_kernel<T, G, MQ, US, RQW, NW>), dim3((unsigned)p.wgs),
+  hipLaunchKernelGGL((w4_gemv_kernel<T, G, MQ, US, RQW, NW, F>), dim3((unsigned)p.wgs),
                      dim3(64 * NW), p.lds, st, a);
 }
 template <typename T, int G, int MQ, int US, int RQW>
@@ -1777,6 +2023,147 @@ static void launch_gemv(const GemvPlan& p, int G, const GemvArgs& a, hipStream_t
     launch_gemv_g<T, 64>(p, a, st);
   else
     launch_gemv_g<T, 128>(p, a, st);
+}
+
+// Plan of a fused GEMV (w4_gemv_kernel with FUSE != kPlain) over NV
+// virtual rows: the plain plan, with rows of 3 or more spans per wave (US 5,
+// every K >= 1536 up to the plain limit), an even number of groups per row
+// (scale pieces are staged per row quad), and workgroups of whole virtual
+// quad pairs (R % 8 == 0; eight waves when four would give R = 4).
+static GemvPlan plan_fused(int64_t M, int64_t NV, int64_t K, int G, int fuse) {
+  GemvPlan p = plan_gemv(M, NV, K, G);
+  const GemvPlan bad{};
+  if (!p.ok || p.US != 5 || (K / G) % 2 != 0 || NV % 8 != 0) return bad;
+  if (p.R % 8 != 0) {
+    p.NW = 8;
+    p.R = 4 * (p.NW / p.SG) * p.RQW;
+    if (p.R % 8 != 0) return bad;
+  }
+  const int64_t nt = 64 * p.NW, ng = K / G;
+  const int xp = fuse == kFfnGateUp && p.MQ == 1 ? 1 : kGemvXP;
+  if (M * (K / 32) > xp * nt || p.R * ng / 8 > kGemvSP * nt) return bad;
+  const GemvLds l = gemv_lds((int)M, (int)K, p.R, G, p.NW, p.RQW);
+  if (l.bytes > 65536) return bad;
+  p.lds = (size_t)l.bytes;
+  p.wgs = cdiv(NV, p.R);
+  return p;
+}
+
+template <typename T, int G, int MQ, int F>
+static void launch_fused_g(const GemvPlan& p, const GemvArgs& a, hipStream_t st) {
+  // two row quads per wave only at one activation row (plan_gemv)
+  if (MQ > 1 || p.RQW == 1) {
+    if (p.NW == 4)
+      launch_gemv_w<T, G, MQ, 5, 1, 4, F>(p, a, st);
+    else
+      launch_gemv_w<T, G, MQ, 5, 1, 8, F>(p, a, st);
+  } else if constexpr (MQ == 1) {
+    if (p.NW == 4)
+      launch_gemv_w<T, G, MQ, 5, 2, 4, F>(p, a, st);
+    else
+      launch_gemv_w<T, G, MQ, 5, 2, 8, F>(p, a, st);
+  }
+}
+template <typename T, int MQ, int F>
+static void launch_fused(const GemvPlan& p, int G, const GemvArgs& a, hipStream_t st) {
+  if (G == 32)
+    launch_fused_g<T, 32, MQ, F>(p, a, st);
+  else if (G == 64)
+    launch_fused_g<T, 64, MQ, F>(p, a, st);
+  else
+    launch_fused_g<T, 128, MQ, F>(p, a, st);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Residual add, RMSNorm and the gate/up projections of the FFN with
+// gelu(gate) * up in one launch, for M <= 4 rows (spark_mlx_llm/ops/ffn.py:
+// 98-102). Writes act [M][I]; workgroup 0 also writes hidden = x + xres and
+// the normed rows [M][K] when those pointers are given. Returns 1 when no
+// fused plan serves the shape (the caller composes the steps instead).
+int w4_ffn_gate_up(const void* x, const void* xres, const void* nw, float eps,
+                   const uint32_t* wg, const void* sg, const void* bg, const uint32_t* wu,
+                   const void* su, const void* bu, void* act, void* hid, void* nrm, int64_t M,
+                   int64_t K, int64_t I, int G, int dt, hipStream_t st) {
+  if (M < 1 || M > 4 || env_int("SPARKQ_NO_FUSED_FFN", 0)) return 1;
+  if (!aligned16(sg) || !aligned16(bg) || !aligned16(su) || !aligned16(bu)) return 1;
+  if (I * (K / 2) >= (int64_t)kOob) return 1;
+  const GemvPlan p = plan_fused(M, 2 * I, K, G, kFfnGateUp);
+  if (!p.ok) return 1;
+  GemvArgs a{};
+  a.x = (const uint16_t*)x;
+  a.w = wg;
+  a.sc = (const uint16_t*)sg;
+  a.bi = (const uint16_t*)bg;
+  a.w2 = wu;
+  a.sc2 = (const uint16_t*)su;
+  a.bi2 = (const uint16_t*)bu;
+  a.xr = (const uint16_t*)xres;
+  a.nw = (const uint16_t*)nw;
+  a.hid = (uint16_t*)hid;
+  a.nrm = (uint16_t*)nrm;
+  a.eps = eps;
+  a.y = act;
+  a.y_dtype = dt;
+  a.M = (int)M;
+  a.N = (int)(2 * I);
+  a.K = (int)K;
+  a.SG = p.SG;
+  a.USr = p.USr;
+  a.R = p.R;
+  if (dt == SPARKQ_BF16) {
+    if (p.MQ == 1)
+      launch_fused<BF16, 1, kFfnGateUp>(p, G, a, st);
+    else
+      launch_fused<BF16, 4, kFfnGateUp>(p, G, a, st);
+  } else {
+    if (p.MQ == 1)
+      launch_fused<F16, 1, kFfnGateUp>(p, G, a, st);
+    else
+      launch_fused<F16, 4, kFfnGateUp>(p, G, a, st);
+  }
+  return check_launch("w4_gemv_kernel<ffn gate/up>");
+}
+
+// QKV projection of one token with RoPE on the query and key heads in one
+// launch (X/src/spark_qkv_rope.cpp:83-101). q, k, v receive the [heads][D]
+// rows of each section. Returns 1 when no fused plan serves the shape.
+int w4_qkv_rope(const void* x, const uint32_t* w, const void* s, const void* b, void* q,
+                void* k, void* v, int64_t K, int nh, int nkv, int hd, int rd, float log2_base,
+                int64_t pos, int G, int dt, hipStream_t st) {
+  if (env_int("SPARKQ_NO_FUSED_QKV", 0)) return 1;
+  if (hd % 8 != 0 || rd % 8 != 0 || !aligned16(s) || !aligned16(b)) return 1;
+  const int64_t N = (int64_t)(nh + 2 * nkv) * hd;
+  if (N * (K / 2) >= (int64_t)kOob) return 1;
+  const GemvPlan p = plan_fused(1, N, K, G, kQkvRope);
+  if (!p.ok) return 1;
+  GemvArgs a{};
+  a.x = (const uint16_t*)x;
+  a.w = w;
+  a.sc = (const uint16_t*)s;
+  a.bi = (const uint16_t*)b;
+  a.y = q;
+  a.y2 = k;
+  a.y3 = v;
+  a.y_dtype = dt;
+  a.M = 1;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.SG = p.SG;
+  a.USr = p.USr;
+  a.R = p.R;
+  a.heads = nh + nkv;
+  a.hd = hd;
+  a.rd = rd;
+  a.q_rows = nh * hd;
+  a.kv_rows = nkv * hd;
+  a.log2_base = log2_base;
+  a.pos = (float)pos;
+  if (dt == SPARKQ_BF16)
+    launch_fused<BF16, 1, kQkvRope>(p, G, a, st);
+  else
+    launch_fused<F16, 1, kQkvRope>(p, G, a, st);
+  return check_launch("w4_gemv_kernel<qkv rope>");
 }
 
 // Streaming GEMV plan (M = 1, rows longer than 5 spans): one workgroup per
@@ -2094,7 +2481,10 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
 
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
                  void* y, int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt,
-                 void* ws, size_t wsb, hipStream_t st) {
+                 void* ws, size_t wsb, hipStream_t st, const void* res, bool* res_done) {
+  // res (16-bit [M][N], y of the same type) is added to the rounded output by
+  // the decode kernels; *res_done says whether the chosen kernel did it
+  if (res_done) *res_done = false;
   const size_t need = w4a16_workspace(M, N, K, G);
   if (need > 0 && (ws == nullptr || wsb < need))
     return set_error(SPARKQ_ERR_WORKSPACE,
@@ -2113,6 +2503,8 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     a.nq = (int)cdiv(N, 4);
     a.P = sp.P;
     a.QW = sp.QW;
+    a.res = (const uint16_t*)res;
+    if (res_done) *res_done = res != nullptr;
     if (xdt == SPARKQ_BF16)
       launch_stream<BF16>(sp, G, a, st);
     else
@@ -2134,6 +2526,8 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     a.nq = (int)(N / 4);
     a.P = dp.P;
     a.QW = dp.QW;
+    a.res = (const uint16_t*)res;
+    if (res_done) *res_done = res != nullptr;
     if (xdt == SPARKQ_BF16)
       launch_dec<BF16>(dp, G, a, st);
     else
@@ -2155,6 +2549,8 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     a.SG = gp.SG;
     a.USr = gp.USr;
     a.R = gp.R;
+    a.res = (const uint16_t*)res;
+    if (res_done) *res_done = res != nullptr;
     if (xdt == SPARKQ_BF16)
       launch_gemv<BF16>(gp, G, a, st);
     else

@@ -11,6 +11,7 @@ from .ext import (
     affine_dequantize,
     affine_quantize,
     affine_quantized_matmul,
+    fused_ffn,
     int8_matmul_int32,
     int8_quantized_sdpa,
     is_w8a8_available,
@@ -18,6 +19,9 @@ from .ext import (
     kv_quantize_s8,
     prepare_w4a16_nax4,
     quantize_per_token,
+    rms_norm,
+    rope,
+    spark_qkv_rope,
     w4a16_multirow,
     w4a16_qmv,
     w8a16_per_channel,
@@ -30,6 +34,7 @@ __all__ = [
     "affine_dequantize",
     "affine_quantize",
     "affine_quantized_matmul",
+    "fused_ffn",
     "int8_matmul_int32",
     "int8_quantized_sdpa",
     "is_w8a8_available",
@@ -37,6 +42,9 @@ __all__ = [
     "kv_quantize_s8",
     "prepare_w4a16_nax4",
     "quantize_per_token",
+    "rms_norm",
+    "rope",
+    "spark_qkv_rope",
     "w4a16_multirow",
     "w4a16_qmv",
     "w8a16_per_channel",

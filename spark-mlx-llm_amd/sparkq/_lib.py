@@ -52,6 +52,13 @@ SIGNATURES = {
     "sparkq_kv_append": (I, [P, P, P, P, I64, I64, I64, I64, I64, I, I, I, P, P]),
     "sparkq_int8kv_sdpa_prefill": (I, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I, I,
                                        I, F, P, P]),
+    "sparkq_ffn_workspace_bytes": (SZ, [I64, I64, I64, I]),
+    "sparkq_ffn": (I, [P, P, P, F, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I, I, P, SZ, P]),
+    "sparkq_qkv_rope_workspace_bytes": (SZ, [I64, I, I, I, I]),
+    "sparkq_qkv_rope": (I, [P, P, P, P, P, P, P, I64, I, I, I, I, I, I, F, I64, I, I, I, P, SZ,
+                            P]),
+    "sparkq_rope": (I, [P, P, I64, I64, I64, I, I, F, F, I64, I, P]),
+    "sparkq_rms_norm": (I, [P, P, P, F, P, P, I64, I64, I, P]),
 }
 
 
@@ -106,6 +113,12 @@ def call(name: str, *args) -> None:
 
 
 _WS: dict = {}
+
+
+def workspace_buffer(device: torch.device, nbytes: int, kind: str) -> torch.Tensor:
+    """The uint8 buffer behind workspace() (at least nbytes)."""
+    workspace(device, nbytes, kind)
+    return _WS[(device.index, torch.cuda.current_stream(device).cuda_stream, kind)]
 
 
 def workspace(device: torch.device, nbytes: int, kind: str):

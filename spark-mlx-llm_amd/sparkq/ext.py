@@ -26,6 +26,7 @@ __all__ = [
     "affine_dequantize",
     "affine_quantize",
     "affine_quantized_matmul",
+    "fused_ffn",
     "int8_matmul_int32",
     "int8_quantized_sdpa",
     "is_w8a8_available",
@@ -34,6 +35,9 @@ __all__ = [
     "kv_append",
     "prepare_w4a16_nax4",
     "quantize_per_token",
+    "rms_norm",
+    "rope",
+    "spark_qkv_rope",
     "w4a16_multirow",
     "w4a16_qmv",
     "w8a16_per_channel",
@@ -606,3 +610,184 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
               _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), float(scale), st,
               ws, wsb, _lib.stream_handle(queries.device))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Decoder-layer steps around the projections
+# ---------------------------------------------------------------------------
+
+def _round_up(v: int, a: int) -> int:
+    return (v + a - 1) // a * a
+
+
+def rms_norm(x, weight, eps: float, *, residual=None, return_hidden: bool = False):
+    """mx.fast.rms_norm(x (+ residual), weight, eps) over the last axis:
+    weight * T(h * rsqrt(mean(h^2) + eps)) with h = x (+ residual) rounded to
+    x's dtype (spark_mlx_llm/ops/ffn.py:98-99). With return_hidden, returns
+    (normed, h)."""
+    if not isinstance(x, torch.Tensor) or not isinstance(weight, torch.Tensor):
+        raise TypeError("x and weight must be tensors")
+    if x.dtype not in _HALF or weight.dtype != x.dtype:
+        raise ValueError("rms_norm requires BF16 or F16 x and a weight of the same dtype")
+    k = x.shape[-1]
+    if weight.shape != (k,):
+        raise ValueError(f"rms_norm weight must have shape [{k}]")
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype):
+        raise ValueError("rms_norm residual must match x in shape and dtype")
+    _require_device("rms_norm", x, weight, residual)
+    m = prod(x.shape[:-1])
+    x2 = x.reshape(m, k).contiguous()
+    r2 = residual.reshape(m, k).contiguous() if residual is not None else None
+    out = torch.empty_like(x2)
+    hid = torch.empty_like(x2) if return_hidden else None
+    _lib.call("sparkq_rms_norm", _ptr(x2), _ptr(r2), _ptr(weight.contiguous()), float(eps),
+              _ptr(hid), _ptr(out), m, k, _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+    if return_hidden:
+        return out.view(x.shape), (hid.view(x.shape) if residual is not None else x)
+    return out.view(x.shape)
+
+
+def rope(x, dims: int, *, traditional: bool = False, base: float = 10000.0,
+         scale: float = 1.0, offset: int = 0):
+    """mx.fast.rope on x [..., L, D]: position of token l is offset + l; the
+    first `dims` features rotate in pairs (i, i + dims/2) (or (2i, 2i+1) when
+    traditional) by (scale * position) * base^(-2i/dims); the rest pass
+    through (spark_mlx_llm/ops/qkv.py:176-177; X/src/spark_qkv_rope.cpp:
+    99-100)."""
+    if not isinstance(x, torch.Tensor):
+        raise TypeError("x must be a tensor")
+    if x.dtype not in _HALF:
+        raise ValueError("rope requires a BF16 or F16 input")
+    if x.ndim < 2:
+        raise ValueError("rope requires x[..., L, D]")
+    if not isinstance(offset, int) or isinstance(offset, bool):
+        raise ValueError("rope offset must be an int")
+    _require_device("rope", x)
+    length, d = x.shape[-2], x.shape[-1]
+    rows = prod(x.shape[:-1])
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    if rows == 0:
+        return out
+    _lib.call("sparkq_rope", _ptr(xc), _ptr(out), rows, length, d, int(dims), int(bool(traditional)),
+              float(base), float(scale), int(offset), _lib.dtype_code(x.dtype),
+              _lib.stream_handle(x.device))
+    return out
+
+
+def spark_qkv_rope(x, weight, scales, biases, q_size: int, kv_size: int, num_heads: int,
+                   num_key_value_heads: int, head_dim: int, rope_dims: int, rope_base: float,
+                   offset: int, group_size: int, bits: int):
+    """Fused QKV projection + RoPE of one token, spark_qkv_rope
+    (X/src/spark_qkv_rope.cpp:14-102) with its argument checks: x [1,1,hidden]
+    -> (queries [1,H,1,D], keys [1,Hkv,1,D], values [1,Hkv,1,D]); queries and
+    keys rotated by mx.fast.rope(rope_dims, traditional=False, rope_base,
+    scale=1, offset)."""
+    if not isinstance(x, torch.Tensor) or x.ndim != 3 or x.shape[0] != 1 or x.shape[1] != 1 \
+            or x.shape[2] <= 0:
+        raise ValueError("[spark_qkv_rope] x must have shape [1, 1, hidden] with hidden > 0.")
+    if not x.dtype.is_floating_point:
+        raise ValueError("[spark_qkv_rope] x must have a real floating dtype.")
+    if (num_heads <= 0 or num_key_value_heads <= 0 or head_dim <= 0
+            or num_heads % num_key_value_heads != 0 or q_size != num_heads * head_dim
+            or kv_size != num_key_value_heads * head_dim):
+        raise ValueError("[spark_qkv_rope] Invalid head counts, head_dim, q_size, or kv_size.")
+    if (rope_dims <= 0 or rope_dims % 2 != 0 or rope_dims > head_dim
+            or not math.isfinite(rope_base) or rope_base <= 0):
+        raise ValueError("[spark_qkv_rope] rope_dims must be positive, even, and no larger than "
+                         "head_dim; rope_base must be positive and finite.")
+    if group_size not in (32, 64, 128):
+        raise ValueError("[spark_qkv_rope] group_size must be 32, 64, or 128.")
+    if bits not in (1, 2, 3, 4, 5, 6, 8):
+        raise ValueError("[spark_qkv_rope] bits must be 1, 2, 3, 4, 5, 6, or 8.")
+    for t in (weight, scales, biases):
+        if not isinstance(t, torch.Tensor) or t.ndim != 2:
+            raise ValueError("[spark_qkv_rope] weight, scales, and biases must be matrices.")
+    if (weight.dtype not in _PACKED or not scales.dtype.is_floating_point
+            or not biases.dtype.is_floating_point):
+        raise ValueError("[spark_qkv_rope] weight must be uint32; scales and biases must have "
+                         "real floating dtypes.")
+    hidden = x.shape[2]
+    if (hidden % group_size or weight.shape[0] != q_size + 2 * kv_size
+            or weight.shape[1] * 32 != hidden * bits or scales.shape != biases.shape
+            or scales.shape[0] != weight.shape[0] or scales.shape[1] != hidden // group_size):
+        raise ValueError("[spark_qkv_rope] Packed weight and quantization metadata shapes do "
+                         "not match x, q_size, kv_size, group_size, and bits.")
+    if x.dtype not in _HALF or scales.dtype != x.dtype or biases.dtype != x.dtype:
+        raise ValueError("[spark_qkv_rope] x, scales and biases must share a BF16 or F16 dtype")
+    if not isinstance(offset, int) or isinstance(offset, bool):
+        raise ValueError("[spark_qkv_rope] offset must be an int")
+    _require_device("spark_qkv_rope", x, weight, scales, biases)
+    dev = x.device
+    q = torch.empty((1, num_heads, 1, head_dim), dtype=x.dtype, device=dev)
+    k = torch.empty((1, num_key_value_heads, 1, head_dim), dtype=x.dtype, device=dev)
+    v = torch.empty_like(k)
+    need = _lib.lib().sparkq_qkv_rope_workspace_bytes(hidden, num_heads, num_key_value_heads,
+                                                       head_dim, group_size)
+    ws, wsb = _lib.workspace(dev, need, "qkv_rope")
+    _lib.call("sparkq_qkv_rope", _ptr(x.contiguous()), _ptr(weight.contiguous()),
+              _ptr(scales.contiguous()), _ptr(biases.contiguous()), _ptr(q), _ptr(k), _ptr(v),
+              hidden, q_size, kv_size, num_heads, num_key_value_heads, head_dim, rope_dims,
+              float(rope_base), int(offset), group_size, bits, _lib.dtype_code(x.dtype), ws, wsb,
+              _lib.stream_handle(dev))
+    return q, k, v
+
+
+def fused_ffn(x, attention_output, norm_weight, eps: float, gate, up, down, *,
+              group_size: int = 64, bits: int = 4, return_intermediates: bool = False):
+    """The decoder's FFN block, compiled_ffn (spark_mlx_llm/ops/ffn.py:83-105):
+    hidden = x + attention_output; normed = rms_norm(hidden, norm_weight, eps);
+    out = hidden + down(gelu(gate(normed)) * up(normed)), in the 16-bit
+    graph's rounding. gate, up and down are (weight, scales, biases) of W4
+    affine projections. With return_intermediates, returns (out, hidden,
+    normed, act)."""
+    tensors = (x, attention_output, norm_weight)
+    if any(not isinstance(t, torch.Tensor) for t in tensors):
+        raise TypeError("x, attention_output and norm_weight must be tensors")
+    if bits != 4:
+        raise ValueError("fused_ffn: only 4-bit affine projections are supported")
+    if x.dtype not in _HALF or attention_output.dtype != x.dtype or norm_weight.dtype != x.dtype:
+        raise ValueError("fused_ffn requires BF16 or F16 x, attention_output and norm weight")
+    if attention_output.shape != x.shape:
+        raise ValueError("fused_ffn: attention_output must have the shape of x")
+    k = x.shape[-1]
+    if norm_weight.shape != (k,):
+        raise ValueError(f"fused_ffn: norm weight must have shape [{k}]")
+    (gw, gs, gb), (uw, us, ub), (dw, ds, db) = gate, up, down
+    inter = gw.shape[0]
+    for name, (w, s, b), n, kk in (("gate", gate, inter, k), ("up", up, inter, k),
+                                   ("down", down, k, inter)):
+        if (w.dtype not in _PACKED or w.shape != (n, kk // 8) or s.dtype != x.dtype
+                or b.dtype != x.dtype or kk % group_size
+                or s.shape != (n, kk // group_size) or b.shape != s.shape):
+            raise ValueError(f"fused_ffn: {name} projection has the wrong packed shape or dtype")
+    if group_size not in (32, 64, 128) or k % 64 or inter % 64:
+        raise ValueError("fused_ffn: group_size 32/64/128 and sizes divisible by 64 required")
+    _require_device("fused_ffn", x, attention_output, norm_weight, gw, uw, dw)
+    m = prod(x.shape[:-1])
+    x2 = x.reshape(m, k).contiguous()
+    a2 = attention_output.reshape(m, k).contiguous()
+    out = torch.empty_like(x2)
+    if m == 0:
+        return out.view(x.shape)
+    dev = x.device
+    need = _lib.lib().sparkq_ffn_workspace_bytes(m, k, inter, group_size)
+    buf = _lib.workspace_buffer(dev, need, "ffn")
+    c = [t.contiguous() for t in (gw, gs, gb, uw, us, ub, dw, ds, db)]
+    _lib.call("sparkq_ffn", _ptr(x2), _ptr(a2), _ptr(norm_weight.contiguous()), float(eps),
+              *[_ptr(t) for t in c], _ptr(out), m, k, inter, group_size,
+              _lib.dtype_code(x.dtype), ctypes.c_void_p(buf.data_ptr()), buf.numel(),
+              _lib.stream_handle(dev))
+    if not return_intermediates:
+        return out.view(x.shape)
+    lin = _round_up(max(_lib.lib().sparkq_w4a16_workspace_bytes(m, inter, k, group_size),
+                        _lib.lib().sparkq_w4a16_workspace_bytes(m, k, inter, group_size)), 256)
+    hk = _round_up(m * k * 2, 256)
+
+    def view(off, n, cols):
+        return buf[off:off + 2 * n].view(x.dtype).view(m, cols).clone()
+
+    hidden = view(lin, m * k, k)
+    normed = view(lin + hk, m * k, k)
+    act = view(lin + 2 * hk, m * inter, inter)
+    return out.view(x.shape), hidden, normed, act

@@ -108,6 +108,60 @@ def test_invalid_arguments_rejected_without_a_device():
     assert rc == -2 and "multiple of 16" in msg
 
 
+def test_layer_entry_points_validate_without_a_device():
+    dummy = P(4096)
+    f = ctypes.c_float
+    ffn = lambda m, k, i, g, dt, eps=1e-6: _rc(  # noqa: E731
+        "sparkq_ffn", dummy, dummy, dummy, f(eps), *([dummy] * 9), dummy, m, k, i, g, dt,
+        None, 0, None)
+    rc, msg = ffn(1, 2560, 9728, 48, 2)
+    assert rc == -1 and "group_size" in msg
+    rc, msg = ffn(1, 2560, 9700, 64, 2)
+    assert rc == -2 and "multiples of 64" in msg
+    rc, msg = ffn(1, 2560, 9728, 64, 0)
+    assert rc == -2 and "bfloat16 or float16" in msg
+    rc, msg = ffn(1, 2560, 9728, 64, 2, eps=float("nan"))
+    assert rc == -1 and "eps" in msg
+    from sparkq import _lib
+
+    lib = _lib.lib()
+    # workspace: counters of the projections, hidden, normed, act, gate, up
+    assert lib.sparkq_ffn_workspace_bytes(1, 2560, 9728, 64) >= 2 * 2560 * 2 + 3 * 9728 * 2
+    assert lib.sparkq_ffn_workspace_bytes(0, 2560, 9728, 64) == 0
+    assert lib.sparkq_qkv_rope_workspace_bytes(2560, 32, 8, 128, 64) >= 3584 * 2
+
+    def qkv(q_size=4096, kv_size=1024, nh=32, nkv=8, hd=128, rd=128, base=10000.0, g=64, bits=4,
+            hidden=2560, off=0):
+        return _rc("sparkq_qkv_rope", dummy, dummy, dummy, dummy, dummy, dummy, dummy, hidden,
+                   q_size, kv_size, nh, nkv, hd, rd, f(base), off, g, bits, 2, None, 0, None)
+
+    # the reference's checks and messages (X/src/spark_qkv_rope.cpp:29-81)
+    rc, msg = qkv(nkv=5)
+    assert rc == -1 and "Invalid head counts" in msg
+    rc, msg = qkv(q_size=4000)
+    assert rc == -1 and "Invalid head counts" in msg
+    rc, msg = qkv(rd=7)
+    assert rc == -1 and "rope_dims must be positive, even" in msg
+    rc, msg = qkv(rd=256)
+    assert rc == -1 and "rope_dims" in msg
+    rc, msg = qkv(base=-1.0)
+    assert rc == -1 and "rope_base" in msg
+    rc, msg = qkv(g=16)
+    assert rc == -1 and "group_size must be 32, 64, or 128" in msg
+    rc, msg = qkv(bits=7)
+    assert rc == -1 and "bits must be 1, 2, 3, 4, 5, 6, or 8" in msg
+    rc, msg = qkv(bits=8)
+    assert rc == -2 and "bits=4" in msg
+    rc, msg = qkv(hidden=2500)
+    assert rc == -1 and "metadata shapes" in msg
+    rc, msg = _rc("sparkq_rope", dummy, dummy, 6, 4, 128, 128, 0, f(10000.0), f(1.0), 0, 2, None)
+    assert rc == -1 and "multiple of L" in msg
+    rc, msg = _rc("sparkq_rope", dummy, dummy, 8, 4, 128, 130, 0, f(10000.0), f(1.0), 0, 2, None)
+    assert rc == -1 and "dims" in msg
+    rc, msg = _rc("sparkq_rms_norm", dummy, None, dummy, f(1e-6), None, dummy, 1, 64, 0, None)
+    assert rc == -2 and "bfloat16 or float16" in msg
+
+
 def test_status_maps_to_reference_exceptions():
     from sparkq import _lib
 

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle as o
+from helpers import rel_l2, ulp_distance16
 
 
 # ---------------------------------------------------------------------------
@@ -380,3 +381,154 @@ def test_w8a16_oracle_matches_numpy():
     e[0, 5] = 1.0
     assert np.array_equal(o.w8a16_matmul(o.bf16_bits(e), w8, sc)[0],
                           w8[:, 5].astype(np.float64) * sc.astype(np.float64))
+
+
+# ---------------------------------------------------------------------------
+# decoder-layer steps: residual add, RMSNorm, GELU, RoPE, FFN block, QKV+RoPE
+# ---------------------------------------------------------------------------
+
+def _b(vals):
+    return o.round16(np.asarray(vals, np.float32), o.BF16)
+
+
+def test_add16_rounding_and_identities():
+    x = o.randn16(1, 70, 4096)
+    y = o.randn16(1, 71, 4096)
+    zero = np.zeros_like(x)
+    assert np.array_equal(o.add16(x, zero), x & 0x7FFF | (x & 0x8000) * (x != 0x8000))
+    assert np.array_equal(o.add16(x, y), o.add16(y, x))
+    assert not o.bits_to_f32(o.add16(x, x ^ 0x8000), o.BF16).any()
+    # 1 + 2^-8 is a tie between 1 and 1 + 2^-7: even wins; 1 + 3*2^-9 rounds up
+    one = _b([1.0, 1.0])
+    assert o.bits_to_f32(o.add16(one, _b([2.0 ** -8, 3 * 2.0 ** -9])), o.BF16).tolist() == \
+        [1.0, 1.0078125]
+    # fp16: 1 + 2^-11 ties to 1, 1 + 3*2^-12 rounds up to 1 + 2^-10
+    one16 = o.round16(np.ones(2, np.float32), o.F16)
+    t = o.round16(np.array([2.0 ** -11, 3 * 2.0 ** -12], np.float32), o.F16)
+    assert o.bits_to_f32(o.add16(one16, t, o.F16), o.F16).tolist() == [1.0, 1.0 + 2.0 ** -10]
+
+
+def test_rms_norm16_known_answer_and_invariants():
+    # h = [3, 4]: mean(h^2) = 12.5, 3/sqrt(12.5) = 0.84853 -> 0.84765625,
+    # 4/sqrt(12.5) = 1.13137 -> 1.1328125 (bf16 nearest)
+    out = o.rms_norm16(_b([[3.0, 4.0]]), _b([1.0, 1.0]), 0.0)
+    assert o.bits_to_f32(out, o.BF16).tolist() == [[0.84765625, 1.1328125]]
+    # a weight of 2 doubles exactly; the weight multiplies per feature
+    h = o.randn16(2, 72, 4 * 2560).reshape(4, 2560)
+    one = _b(np.ones(2560))
+    n1 = o.bits_to_f32(o.rms_norm16(h, one, 1e-6), o.BF16)
+    n2 = o.bits_to_f32(o.rms_norm16(h, _b(np.full(2560, 2.0)), 1e-6), o.BF16)
+    assert np.array_equal(n2, 2 * n1)
+    # scale invariance with eps = 0: scaling h by 2 is exact, so is the norm
+    h2 = o.round16(2 * o.bits_to_f32(h, o.BF16), o.BF16)
+    assert np.array_equal(o.rms_norm16(h2, one, 0.0), o.rms_norm16(h, one, 0.0))
+    # unit mean square within the rounding of each element
+    assert np.allclose((n1.astype(np.float64) ** 2).mean(axis=-1), 1.0, atol=5e-3)
+    # eps enters under the root: a zero row stays zero, a tiny row is damped
+    z = o.rms_norm16(_b(np.zeros((1, 64))), _b(np.ones(64)), 1e-6)
+    assert not o.bits_to_f32(z, o.BF16).any()
+    small = o.rms_norm16(_b(np.full((1, 64), 1e-3)), _b(np.ones(64)), 1e-6)
+    assert np.allclose(o.bits_to_f32(small, o.BF16), 1e-3 / np.sqrt(1e-6 + 1e-6), rtol=8e-3)
+
+
+def test_gelu16_against_the_erf_definition():
+    from scipy.special import erf
+
+    x = np.linspace(-6, 6, 4001, dtype=np.float32)
+    for dt, eps in ((o.BF16, 2.0 ** -8), (o.F16, 2.0 ** -11)):
+        g = o.round16(x, dt)
+        xv = o.bits_to_f32(g, dt).astype(np.float64)
+        exact = 0.5 * xv * (1.0 + erf(xv / np.sqrt(2.0)))
+        got = o.bits_to_f32(o.gelu16(g, dt), dt)
+        # the 16-bit 1 + erf(.) loses up to one unit of 1 to cancellation, so
+        # the error is bounded by |x| units of the format (and the result's
+        # own rounding), not by the result's units
+        assert np.all(np.abs(got - exact) <= 1.5 * eps * np.abs(xv) + eps * np.abs(exact) + 1e-30)
+    # hand-derived at the rounding points, x = -3 in bf16: x / 1.4140625 =
+    # -2.1215 -> -2.125; erf(-2.125) = -0.99730 -> -0.99609375; 1 + that =
+    # 2^-8; times x = -0.01171875; halved = -0.005859375 (one fp32 rounding at
+    # the end would give -0.00405)
+    assert o.bits_to_f32(o.gelu16(_b([-3.0])), o.BF16).tolist() == [-0.005859375]
+    assert o.bits_to_f32(o.gelu16(_b([0.0, 8.0, 100.0])), o.BF16).tolist() == [0.0, 8.0, 100.0]
+    assert o.bits_to_f32(o.gelu16(_b([-8.0, -100.0])), o.BF16).tolist() == [0.0, 0.0]
+    gm = o.gelu_mul16(_b([8.0, 8.0]), _b([0.5, -3.0]))
+    assert o.bits_to_f32(gm, o.BF16).tolist() == [4.0, -24.0]
+
+
+def test_rope16_geometry():
+    d, length = 128, 6
+    x = o.randn16(3, 73, 2 * 4 * length * d).reshape(2, 4, length, d)
+    y = o.rope16(x, d, 10000.0, 0)
+    assert np.array_equal(y[:, :, 0], x[:, :, 0])           # position 0 is the identity
+    # one-hot inputs land on cos/sin of the textbook angle p * base^(-2i/d)
+    for i, p in ((0, 1), (5, 7), (63, 4095), (17, 30000)):
+        e = np.zeros((1, 1, d), np.float32)
+        e[0, 0, i] = 1.0
+        r = o.bits_to_f32(o.rope16(o.round16(e, o.BF16), d, 10000.0, p), o.BF16)[0, 0]
+        th = p * 10000.0 ** (-2 * i / d)
+        assert abs(r[i] - np.cos(th)) <= 2 ** -8 and abs(r[i + d // 2] - np.sin(th)) <= 2 ** -8
+        assert np.count_nonzero(r) <= 2
+    # each pair keeps its length
+    xf = o.bits_to_f32(x, o.BF16).astype(np.float64)
+    yf = o.bits_to_f32(o.rope16(x, d, 10000.0, 123), o.BF16).astype(np.float64)
+    n0 = xf[..., :64] ** 2 + xf[..., 64:] ** 2
+    n1 = yf[..., :64] ** 2 + yf[..., 64:] ** 2
+    assert np.allclose(n1, n0, rtol=2e-2, atol=1e-3)
+    # partial rotation: the dims past rope_dims pass through bit for bit
+    yp = o.rope16(x, 32, 10000.0, 5)
+    assert np.array_equal(yp[..., 32:], x[..., 32:])
+    # traditional pairs (2i, 2i+1) are the non-traditional pairs after an
+    # interleaving permutation of the features
+    perm = np.concatenate([np.arange(0, d, 2), np.arange(1, d, 2)])
+    yt = o.rope16(x, d, 10000.0, 9, traditional=True)
+    yn = o.rope16(x[..., perm], d, 10000.0, 9)
+    assert np.array_equal(yt[..., perm], yn)
+    # consecutive tokens: token l at offset a equals token 0 at offset a + l
+    ya = o.rope16(x, d, 500000.0, 40)
+    yb = o.rope16(x[:, :, 3:4], d, 500000.0, 43)
+    assert np.array_equal(ya[:, :, 3:4], yb)
+
+
+def test_ffn_block_against_textbook_float64():
+    """The staged 16-bit FFN against the same formulas in float64 without
+    intermediate rounding: close (bf16 noise), and the known-wrong orders
+    (residual on the normed rows, GELU on up) are far."""
+    from scipy.special import erf
+
+    k, inter, g = 256, 512, 64
+    x = o.randn16(4, 74, 2 * k).reshape(2, k)
+    a = o.randn16(4, 75, 2 * k).reshape(2, k)
+    nw = o.round16(1.0 + 0.1 * o.randn(4, 76, k), o.BF16)
+    mats = []
+    for n, kk, st in ((inter, k, 77), (inter, k, 78), (k, inter, 79)):
+        w = o.bits_to_f32(o.randn16(4, st, n * kk, 0.05), o.BF16).reshape(n, kk)
+        mats.append(o.w4_quantize(w, g, o.BF16))
+    st = o.ffn_block(x, a, nw, 1e-6, *mats, g)
+    wd = [o.w4_dequantize(*m, g).astype(np.float64) for m in mats]
+    h = o.bits_to_f32(x, o.BF16).astype(np.float64) + o.bits_to_f32(a, o.BF16)
+    n = h / np.sqrt((h * h).mean(-1, keepdims=True) + 1e-6) * o.bits_to_f32(nw, o.BF16)
+    gate, up = n @ wd[0].T, n @ wd[1].T
+    act = 0.5 * gate * (1 + erf(gate / np.sqrt(2))) * up
+    out = h + act @ wd[2].T
+    got = o.bits_to_f32(st["out"], o.BF16)
+    assert rel_l2(got, out) < 4e-3
+    assert np.array_equal(st["hidden"], o.add16(x, a))
+    wrong = n + (0.5 * up * (1 + erf(up / np.sqrt(2))) * gate) @ wd[2].T
+    assert rel_l2(got, wrong) > 0.05
+
+
+def test_qkv_rope_split_and_rotation():
+    k, nh, nkv, hd, g = 256, 4, 2, 64, 32
+    w = o.bits_to_f32(o.randn16(5, 80, (nh + 2 * nkv) * hd * k, 0.05), o.BF16).reshape(-1, k)
+    wq, s, b = o.w4_quantize(w, g, o.BF16)
+    x = o.randn16(5, 81, k)
+    q, kk, v, qkv = o.qkv_rope(x, wq, s, b, g, nh, nkv, hd, hd, 10000.0, 0)
+    r = o.round16(qkv, o.BF16)
+    # position 0 rotates nothing: the split alone, queries, keys, values in order
+    assert np.array_equal(q.reshape(-1), r[:nh * hd])
+    assert np.array_equal(kk.reshape(-1), r[nh * hd:(nh + nkv) * hd])
+    assert np.array_equal(v.reshape(-1), r[(nh + nkv) * hd:])
+    q7, k7, v7, _ = o.qkv_rope(x, wq, s, b, g, nh, nkv, hd, 32, 10000.0, 7)
+    assert np.array_equal(v7, v)
+    assert np.array_equal(q7[:, 32:], q[:, 32:]) and not np.array_equal(q7[:, :32], q[:, :32])
+    assert np.array_equal(k7, o.rope16(kk[:, None], 32, 10000.0, 7)[:, 0])
