@@ -262,6 +262,50 @@ def bench_kv_append(torch, sparkq, dev, iters):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "w4_gemv_gate_up_m1_pmc.md")
 
 
+def bench_layer(torch, sparkq, dev, layers, iters):
+    """The fused decoder-layer steps at one token over the 36 layers: the FFN
+    block (residual + RMSNorm + gate/up + gelu*up in one launch, down +
+    residual in another; gate and up are the two halves of the fused
+    gate_up weights) and the QKV projection with RoPE (3584 = 2560 + 2 * 512
+    rows: 20 query and 4 key/value heads of 128, full rotation, position
+    4095)."""
+    inter = PROJ["gate_up"][0] // 2
+    hidden = PROJ["down"][0]
+    x = torch.randn((1, hidden), device=dev).to(torch.bfloat16)
+    a = torch.randn((1, hidden), device=dev).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(hidden, device=dev)).to(torch.bfloat16)
+
+    def halves(t):
+        return t[:inter], t[inter:]
+
+    ffn_args = []
+    for layer in layers:
+        (gw, uw), (gs, us), (gb, ub) = (halves(t) for t in layer["gate_up"])
+        ffn_args.append(((gw, gs, gb), (uw, us, ub), layer["down"]))
+
+    def ffn():
+        for gate, up, down in ffn_args:
+            sparkq.fused_ffn(x, a, nw, 1e-6, gate, up, down, group_size=G)
+
+    xq = x.view(1, 1, hidden)
+
+    def qkv():
+        for layer in layers:
+            wq, s, b = layer["qkv"]
+            sparkq.spark_qkv_rope(xq, wq, s, b, 2560, 512, 20, 4, 128, 128, 500000.0, 4095, G, 4)
+
+    res = {}
+    for name, fn, nbytes in (
+            ("ffn_block", ffn, w4_bytes(*PROJ["gate_up"]) + w4_bytes(*PROJ["down"])),
+            ("qkv_rope", qkv, w4_bytes(*PROJ["qkv"]))):
+        graph = capture(torch, fn)
+        ms = Timer(torch).time(graph.replay, iters, 2) / len(layers)
+        res[name] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+                     "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        del graph
+    return res
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel, from the committed PMC
     summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters
@@ -410,6 +454,8 @@ def main():
             f"L={l} N={n}": bench_prefill(torch, sparkq, dev, l, n, 5)
             for l, n in ((2048, 2048), (512, 4096))}
         extras["kv_append"] = bench_kv_append(torch, sparkq, dev, 10)
+        log("fused FFN block and QKV+RoPE")
+        extras["layer_m1"] = bench_layer(torch, sparkq, dev, layers, 10)
 
     cpu = None
     if not args.skip_cpu:

@@ -261,6 +261,57 @@ __device__ __forceinline__ float add_rounded(float v, uint16_t res) {
   return T::to_f32(T::from_f32(v)) + T::to_f32(res);
 }
 
+// The two 16-bit values of a packed pair as fp32, and two fp32 values rounded
+// (to nearest even) into a packed pair: one v_cvt_pk_bf16_f32 on gfx950.
+template <typename T> __device__ __forceinline__ float lo16(uint32_t p);
+template <typename T> __device__ __forceinline__ float hi16(uint32_t p);
+template <typename T> __device__ __forceinline__ uint32_t pack_round(float a, float b);
+template <> __device__ __forceinline__ float lo16<BF16>(uint32_t p) { return __uint_as_float(p << 16); }
+template <> __device__ __forceinline__ float hi16<BF16>(uint32_t p) {
+  return __uint_as_float(p & 0xFFFF0000u);
+}
+template <> __device__ __forceinline__ uint32_t pack_round<BF16>(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+template <> __device__ __forceinline__ float lo16<F16>(uint32_t p) { return f16_to_f32((uint16_t)p); }
+template <> __device__ __forceinline__ float hi16<F16>(uint32_t p) {
+  return f16_to_f32((uint16_t)(p >> 16));
+}
+template <> __device__ __forceinline__ uint32_t pack_round<F16>(float a, float b) {
+  return (uint32_t)f32_to_f16(a) | ((uint32_t)f32_to_f16(b) << 16);
+}
+
+// Sum over the 64 lanes of a wave, the same value in every lane: pairs and
+// quads by DPP, the sixteen quads by sum_blocks, then lane 0's value.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v = sum_blocks(v);
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+// erf(t) as it rounds to T: the fp32 erff (error of a few units of fp32)
+// decides the 16-bit result unless it lies within 16 fp32 units of a
+// rounding tie of T (or in fp16's subnormal range); those few are redone in
+// double and rounded to fp32, as a correctly rounded float erf would give.
+template <typename T>
+__device__ __forceinline__ float erf_for16(float t) {
+  float e = erff(t);
+  const uint32_t u = __float_as_uint(e);
+  bool redo;
+  if constexpr (T::code == SPARKQ_BF16) {
+    const int low = (int)(u & 0xFFFFu) - 0x8000;
+    redo = low > -16 && low < 16;
+  } else {
+    const int low = (int)(u & 0x1FFFu) - 0x1000;
+    redo = (low > -16 && low < 16) || fabsf(e) < 6.2e-5f;
+  }
+  if (redo) e = (float)erf((double)t);
+  return e;
+}
+
 // gelu(gate) * up as mlx.nn.gelu computes it on a 16-bit array,
 // x * (1 + erf(x / sqrt(2))) / 2 (spark_mlx_llm/ops/ffn.py:102): the constant
 // sqrt(2) is rounded to T (1.4140625 for both types) and each operation's
@@ -273,15 +324,16 @@ __device__ __forceinline__ float gelu_mul(float g, float u) {
   const float gate = r(g), up = r(u);
   const float c = r(1.41421356237309515f);
   const float t1 = r(gate / c);
-  const float e = r((float)erf((double)t1));
+  const float e = r(erf_for16<T>(t1));
   const float t3 = r(1.0f + e);
   const float t5 = r(r(gate * t3) / 2.0f);
   return t5 * up;
 }
 
-// Inverse frequency of rotary pair i of mx.fast.rope (non-traditional):
-// 2^(-(i / half) * log2(base)), d and the exponent in fp32 and the power
-// correctly rounded to fp32 (through double).
+// Inverse frequency of rotary pair i of mx.fast.rope: 2^(-(i / half) *
+// log2(base)), d and the exponent in fp32, the power correctly rounded to
+// fp32 (through double: a unit of fp32 in the frequency is a position-sized
+// error in the angle).
 __device__ __forceinline__ float rope_inv_freq(int i, int half, float log2_base) {
   const float d = (float)i / (float)half;
   return (float)exp2((double)(-d * log2_base));

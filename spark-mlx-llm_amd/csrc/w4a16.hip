@@ -189,6 +189,8 @@ __device__ __forceinline__ int qkv_real_quad(int vq, int hq, int P, int heads) {
 
 constexpr int kGemvXP = 2;   // staged activation pieces (64 B) per thread, at most
 constexpr int kGemvSP = 4;   // staged (scale, bias) pieces (16 B each) per thread, at most
+constexpr int kFfnXC1 = 2;   // FFN prologue chunks (16 B) per thread at one row, at most
+constexpr int kFfnXC4 = 4;   // ... at two to four rows
 
 // LDS slot (dword index) of 16-byte chunk w of activation piece pi. The
 // pieces of a span sit chunk-major (16 pieces x 16 B per chunk), so the 16
@@ -205,16 +207,19 @@ struct GemvLds {
   int sb;    // (scale, bias) of the workgroup's rows: [R][K/G] dwords
   int red;   // cross-wave partial sums: [NW][RQW][4][4] fp32
   int fz;    // fused epilogues: final sums of the workgroup's rows [R][4] fp32
+  int st;    // FFN prologue: the normed rows [M][K] in natural order
   int bytes;
 };
-__host__ __device__ __forceinline__ GemvLds gemv_lds(int M, int K, int R, int G, int NW, int RQW) {
+__host__ __device__ __forceinline__ GemvLds gemv_lds(int M, int K, int R, int G, int NW, int RQW,
+                                                     bool ffn = false) {
   GemvLds l;
   l.xp = 0;
   l.xs = l.xp + ((M * K * 2 + 1023) & ~1023);
   l.sb = l.xs + (K / 32) * 16;
   l.red = l.sb + ((R * (K / G) * 4 + 15) & ~15);
   l.fz = l.red + NW * RQW * 64;
-  l.bytes = l.fz + R * 16;
+  l.st = l.fz + R * 16;
+  l.bytes = l.st + (ffn ? M * K * 2 : 0);
   return l;
 }
 
@@ -223,9 +228,9 @@ template <typename T, int G, int MQ, int US, int RQW, int NW, int FUSE = kPlain>
 __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int NT = 64 * NW;
-  // staged activation pieces per thread: the FFN prologue also holds the
-  // residual and norm weight pieces, so at one row it stages one piece each
-  constexpr int XP = FUSE == kFfnGateUp && MQ == 1 ? 1 : kGemvXP;
+  // FFN prologue: 16-byte chunks of x, the residual and the norm weight per
+  // thread, spread over the whole workgroup
+  constexpr int XC = FUSE == kFfnGateUp ? (MQ == 1 ? kFfnXC1 : kFfnXC4) : 1;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = lane >> 2, j = lane & 3;
@@ -240,38 +245,43 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
   const int q0 = (r0 >> 2) + (wave / SG) * RQW;  // first row quad of the wave
   const int u0 = sg * a.USr;
   const int ns = min(a.USr, U - u0);           // spans of this wave (wave-uniform)
-  const GemvLds L = gemv_lds(M, K, R, G, NW, RQW);
+  const GemvLds L = gemv_lds(M, K, R, G, NW, RQW, FUSE == kFfnGateUp);
 
   const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
   const rsrc_t rw = make_rsrc(a.w, (uint32_t)NR * RB);
-  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
-  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)NR * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)NR * ng * 2);
 
   // 1. staging loads: activation pieces (64 B) and (scale, bias) pieces
   const int nxp = M * (K >> 5);                // activation pieces
   const int nsp = (R * ng) >> 3;               // 16-byte scale pieces of the workgroup
-  u32x4_t xr[XP][4];
-  constexpr int XF = FUSE == kFfnGateUp ? XP : 1;
-  u32x4_t rr[XF][4], nr[XF][4];                // residual and norm weight pieces
+  u32x4_t xr[kGemvXP][4];
+  u32x4_t xc[XC], rc[XC], nc[XC];              // FFN prologue chunks
   u32x4_t sr[kGemvSP], br[kGemvSP];
+  const int nxc = nxp * 4;                     // 16-byte activation chunks
   // a wave with no piece to fetch skips the instruction (the texture unit
   // charges per instruction, lanes or not); the condition is wave-uniform
+  if constexpr (FUSE == kFfnGateUp) {
+    const rsrc_t rr_ = make_rsrc(a.xr, a.xr ? (uint32_t)M * K * 2 : 0u);
+    const rsrc_t rn_ = make_rsrc(a.nw, (uint32_t)K * 2);
 #pragma unroll
-  for (int i = 0; i < XP; ++i) {
-    const int pi = tid + i * NT;
-    if (i * NT + 64 * wave < nxp) {
-      const uint32_t off = pi < nxp ? 64u * pi : kOob;
+    for (int c = 0; c < XC; ++c) {
+      const int ci = tid + c * NT;
+      if (c * NT + 64 * wave < nxc) {
+        const uint32_t off = ci < nxc ? 16u * ci : kOob;
+        xc[c] = buf_load16(rx, off);
+        rc[c] = buf_load16(rr_, off);
+        nc[c] = buf_load16(rn_, ci < nxc ? 16u * (ci % (K >> 3)) : kOob);
+      }
+    }
+  } else {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
-      if constexpr (FUSE == kFfnGateUp) {
-        const rsrc_t rr_ = make_rsrc(a.xr, a.xr ? (uint32_t)M * K * 2 : 0u);
-        const rsrc_t rn_ = make_rsrc(a.nw, (uint32_t)K * 2);
-        const uint32_t noff = pi < nxp ? 64u * (pi % (K >> 5)) : kOob;
+    for (int i = 0; i < kGemvXP; ++i) {
+      const int pi = tid + i * NT;
+      if (i * NT + 64 * wave < nxp) {
+        const uint32_t off = pi < nxp ? 64u * pi : kOob;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          rr[i][w] = buf_load16(rr_, off + 16 * w);
-          nr[i][w] = buf_load16(rn_, noff + 16 * w);
-        }
+        for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
       }
     }
   }
@@ -286,31 +296,30 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
       }
     }
   } else {
-    // the workgroup's virtual quads are not contiguous rows: piece pi is
-    // piece pi % (ng/2) of the 4 contiguous rows of virtual quad pi / (ng/2),
-    // read from that quad's matrix through a per-lane address
+    // the workgroup's virtual quads are not contiguous rows: wave w stages
+    // the scale block of virtual quads w and w + NW (4 contiguous rows, ng/2
+    // pieces of 16 bytes, one per lane), from that quad's matrix; the quad's
+    // matrix and rows are wave-uniform
     const int hp = ng >> 1;
 #pragma unroll
-    for (int i = 0; i < kGemvSP; ++i) {
-      const int pi = tid + i * NT;
-      if (i * NT + 64 * wave < nsp) {
-        const int pc = min(pi, nsp - 1);
-        const int vq = min((r0 >> 2) + pc / hp, (N >> 2) - 1), po = pc % hp;
-        const uint16_t* ps = a.sc;
-        const uint16_t* pb = a.bi;
+    for (int t = 0; t < 2; ++t) {
+      const int vql = wave + t * NW;
+      if (vql < (R >> 2)) {
+        const int vq = min((r0 >> 2) + vql, (N >> 2) - 1);
+        rsrc_t rsq = rs, rbq = rb;
         int rq;
         if constexpr (FUSE == kFfnGateUp) {
           rq = vq >> 1;
           if (vq & 1) {
-            ps = a.sc2;
-            pb = a.bi2;
+            rsq = make_rsrc(a.sc2, (uint32_t)NR * ng * 2);
+            rbq = make_rsrc(a.bi2, (uint32_t)NR * ng * 2);
           }
         } else {
           rq = qkv_real_quad(vq, a.hd >> 2, a.rd >> 3, a.heads);
         }
-        const int64_t e = (int64_t)rq * 4 * ng + 8 * po;
-        sr[i] = *reinterpret_cast<const u32x4_t*>(ps + e);
-        br[i] = *reinterpret_cast<const u32x4_t*>(pb + e);
+        const uint32_t off = lane < hp ? (uint32_t)rq * 8 * ng + 16 * lane : kOob;
+        sr[t] = buf_load16(rsq, off);
+        br[t] = buf_load16(rbq, off);
       }
     }
   }
@@ -342,45 +351,40 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
 
   // 2b. FFN prologue: hidden = x + residual and its RMSNorm,
   // w * T(hidden * rsqrt(mean(hidden^2) + eps)) (mx.fast.rms_norm,
-  // spark_mlx_llm/ops/ffn.py:98-99), replacing the staged activations. Every
-  // workgroup reduces the sums of squares in the same order, so all of them
-  // normalise with the same factor.
+  // spark_mlx_llm/ops/ffn.py:98-99), over 16-byte chunks spread across the
+  // workgroup; the normed rows go to an LDS stage in natural order, from
+  // which the activation pieces are read below. Every workgroup reduces the
+  // sums of squares in the same order, so all of them normalise alike.
   if constexpr (FUSE == kFfnGateUp) {
+    const bool has_res = a.xr != nullptr;
     float ss[MQ];
 #pragma unroll
     for (int m = 0; m < MQ; ++m) ss[m] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < XP; ++i) {
-      const int pi = tid + i * NT;
-      if (pi < nxp) {
+    for (int c = 0; c < XC; ++c) {
+      const int ci = tid + c * NT;
+      if (ci < nxc) {
         float q = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t xv = xr[i][w][e];
-            float h0 = T::to_f32((uint16_t)(xv & 0xFFFFu));
-            float h1 = T::to_f32((uint16_t)(xv >> 16));
-            if (a.xr) {
-              const uint32_t rv = rr[i][w][e];
-              h0 = T::to_f32(T::from_f32(h0 + T::to_f32((uint16_t)(rv & 0xFFFFu))));
-              h1 = T::to_f32(T::from_f32(h1 + T::to_f32((uint16_t)(rv >> 16))));
-              xr[i][w][e] = (uint32_t)T::from_f32(h0) | ((uint32_t)T::from_f32(h1) << 16);
-            }
-            q = fmaf(h0, h0, q);
-            q = fmaf(h1, h1, q);
-          }
-        const int m = MQ == 1 ? 0 : pi / (K >> 5);
+        for (int e = 0; e < 4; ++e) {
+          uint32_t p = xc[c][e];
+          if (has_res)
+            p = pack_round<T>(lo16<T>(p) + lo16<T>(rc[c][e]), hi16<T>(p) + hi16<T>(rc[c][e]));
+          xc[c][e] = p;
+          const float h0 = lo16<T>(p), h1 = hi16<T>(p);
+          q = fmaf(h0, h0, q);
+          q = fmaf(h1, h1, q);
+        }
+        const int m = MQ == 1 ? 0 : ci / (K >> 3);
 #pragma unroll
         for (int mm = 0; mm < MQ; ++mm) ss[mm] += mm == m ? q : 0.0f;
+        if (blockIdx.x == 0 && a.hid) *reinterpret_cast<u32x4_t*>(a.hid + 8 * ci) = xc[c];
       }
     }
     float* red = reinterpret_cast<float*>(smem + L.red);
 #pragma unroll
     for (int m = 0; m < MQ; ++m) {
-      float v = ss[m];
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      const float v = wave_sum(ss[m]);
       if (lane == 0) red[wave * 4 + m] = v;
     }
     __syncthreads();
@@ -391,34 +395,33 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
       for (int w = 0; w < NW; ++w) t += red[w * 4 + m];
       inv[m] = (float)(1.0 / sqrt((double)(t / (float)K + a.eps)));
     }
+    uint16_t* stage = reinterpret_cast<uint16_t*>(smem + L.st);
 #pragma unroll
-    for (int i = 0; i < XP; ++i) {
-      const int pi = tid + i * NT;
-      if (pi < nxp) {
-        const int m = MQ == 1 ? 0 : pi / (K >> 5);
+    for (int c = 0; c < XC; ++c) {
+      const int ci = tid + c * NT;
+      if (ci < nxc) {
+        const int m = MQ == 1 ? 0 : ci / (K >> 3);
         float im = inv[0];
 #pragma unroll
         for (int mm = 1; mm < MQ; ++mm) im = mm == m ? inv[mm] : im;
-        u32x4_t nv[4];
+        u32x4_t nv;
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t xv = xr[i][w][e], wt = nr[i][w][e];
-            const float n0 = T::to_f32(T::from_f32(T::to_f32((uint16_t)(xv & 0xFFFFu)) * im));
-            const float n1 = T::to_f32(T::from_f32(T::to_f32((uint16_t)(xv >> 16)) * im));
-            nv[w][e] = (uint32_t)T::from_f32(T::to_f32((uint16_t)(wt & 0xFFFFu)) * n0) |
-                       ((uint32_t)T::from_f32(T::to_f32((uint16_t)(wt >> 16)) * n1) << 16);
-          }
-        if (blockIdx.x == 0) {
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            if (a.hid) *reinterpret_cast<u32x4_t*>(a.hid + 32 * pi + 8 * w) = xr[i][w];
-            if (a.nrm) *reinterpret_cast<u32x4_t*>(a.nrm + 32 * pi + 8 * w) = nv[w];
-          }
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t p = xc[c][e], wt = nc[c][e];
+          const uint32_t n = pack_round<T>(lo16<T>(p) * im, hi16<T>(p) * im);
+          nv[e] = pack_round<T>(lo16<T>(wt) * lo16<T>(n), hi16<T>(wt) * hi16<T>(n));
         }
+        *reinterpret_cast<u32x4_t*>(stage + 8 * ci) = nv;
+        if (blockIdx.x == 0 && a.nrm) *reinterpret_cast<u32x4_t*>(a.nrm + 8 * ci) = nv;
+      }
+    }
+    __syncthreads();
 #pragma unroll
-        for (int w = 0; w < 4; ++w) xr[i][w] = nv[w];
+    for (int i = 0; i < kGemvXP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nxp) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) xr[i][w] = *reinterpret_cast<const u32x4_t*>(stage + 32 * pi + 8 * w);
       }
     }
   }
@@ -428,7 +431,7 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
     float* xs = reinterpret_cast<float*>(smem + L.xs);
 #pragma unroll
-    for (int i = 0; i < XP; ++i) {
+    for (int i = 0; i < kGemvXP; ++i) {
       const int pi = tid + i * NT;
       if (pi < nxp) {
         float sum = 0.0f;
@@ -448,10 +451,13 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
       }
     }
     uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+    const int hp = ng >> 1;
 #pragma unroll
     for (int i = 0; i < kGemvSP; ++i) {
-      const int pi = tid + i * NT;
-      if (pi < nsp) {
+      // plain: piece tid + i*NT; fused: piece lane of virtual quad wave + i*NW
+      const int pi = FUSE == kPlain ? tid + i * NT : (wave + i * NW) * hp + lane;
+      const bool ok = FUSE == kPlain ? pi < nsp : i < 2 && wave + i * NW < (R >> 2) && lane < hp;
+      if (ok) {
         const u32x4_t s = sr[i], c = br[i];
         u32x4_t lo, hi;
 #pragma unroll
@@ -493,6 +499,25 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
         xm[s][2] = v.z;
         xm[s][3] = v.w;
       }
+    }
+  }
+
+  // 4b. the rotation of each output row of the wave (kQkvRope) does not
+  // depend on the projection: its angle is taken here, while the weights are
+  // still arriving
+  float rcs[RQW], rsn[RQW];
+  if constexpr (FUSE == kQkvRope) {
+#pragma unroll
+    for (int r = 0; r < RQW; ++r) {
+      const int vq = q0 + r, hq = a.hd >> 2, P = a.rd >> 3;
+      const int h = vq / hq, w = vq - h * hq;
+      rcs[r] = 1.0f;
+      rsn[r] = 0.0f;
+      if (lane < 4 && h < a.heads && w < 2 * P)
+        sincosf(a.pos * rope_inv_freq(4 * (w >> 1) + lane, a.rd >> 1, a.log2_base), &rsn[r],
+                &rcs[r]);
+      // materialise the values here rather than where the epilogue uses them
+      asm volatile("" ::"v"(rcs[r]), "v"(rsn[r]));
     }
   }
 
@@ -611,9 +636,7 @@ __global__ __launch_bounds__(64 * NW, 3) void w4_gemv_kernel(GemvArgs a) {
         if (h < a.heads && w < 2 * P) {
           // mx.fast.rope on the 16-bit projections (non-traditional):
           // x1 = dim i, x2 = dim i + rope_dims/2 of the head
-          const float inv = rope_inv_freq(4 * (w >> 1) + lane, a.rd >> 1, a.log2_base);
-          float sn, cs;
-          sincosf(a.pos * inv, &sn, &cs);
+          const float sn = rsn[r], cs = rcs[r];
           const float self = T::to_f32(T::from_f32(v)), other = T::to_f32(T::from_f32(pv[r][0]));
           v = (w & 1) == 0 ? self * cs - other * sn : other * sn + self * cs;
         }
@@ -2039,10 +2062,17 @@ static GemvPlan plan_fused(int64_t M, int64_t NV, int64_t K, int G, int fuse) {
     p.R = 4 * (p.NW / p.SG) * p.RQW;
     if (p.R % 8 != 0) return bad;
   }
+  const int xc = p.MQ == 1 ? kFfnXC1 : kFfnXC4;
+  if (fuse == kFfnGateUp && M * (K / 8) > xc * 64 * p.NW && p.NW == 4 && p.SG == 1) {
+    p.NW = 8;  // more threads for the prologue's chunks
+    p.R = 4 * (p.NW / p.SG) * p.RQW;
+  }
   const int64_t nt = 64 * p.NW, ng = K / G;
-  const int xp = fuse == kFfnGateUp && p.MQ == 1 ? 1 : kGemvXP;
-  if (M * (K / 32) > xp * nt || p.R * ng / 8 > kGemvSP * nt) return bad;
-  const GemvLds l = gemv_lds((int)M, (int)K, p.R, G, p.NW, p.RQW);
+  if (fuse == kFfnGateUp && M * (K / 8) > xc * nt) return bad;
+  // scale staging: one lane per 16-byte piece of a quad, two quads per wave
+  if (ng / 2 > 64 || p.R / 4 > 2 * p.NW) return bad;
+  if (M * (K / 32) > kGemvXP * nt || p.R * ng / 8 > kGemvSP * nt) return bad;
+  const GemvLds l = gemv_lds((int)M, (int)K, p.R, G, p.NW, p.RQW, fuse == kFfnGateUp);
   if (l.bytes > 65536) return bad;
   p.lds = (size_t)l.bytes;
   p.wgs = cdiv(NV, p.R);

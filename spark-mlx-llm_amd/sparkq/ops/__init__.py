@@ -1,6 +1,7 @@
 """Operator dispatch mirroring spark_mlx_llm/ops on torch tensors."""
 
 from .base import OperatorConfig
+from .ffn import RMSNorm, dispatch_ffn
 from .linear import (
     AffineParameters,
     LinearConfig,
@@ -10,6 +11,7 @@ from .linear import (
     W8A8QuantizedLinear,
     dispatch_linear,
 )
+from .qkv import RoPE, dispatch_qkv
 from .sdpa import SDPAConfig, dispatch_sdpa
 
 __all__ = [
@@ -17,10 +19,14 @@ __all__ = [
     "LinearConfig",
     "OperatorConfig",
     "QuantizedLinear",
+    "RMSNorm",
+    "RoPE",
     "SDPAConfig",
     "W8A16PerChannelLinear",
     "W8A8Projection",
     "W8A8QuantizedLinear",
+    "dispatch_ffn",
     "dispatch_linear",
+    "dispatch_qkv",
     "dispatch_sdpa",
 ]

@@ -212,3 +212,59 @@ def test_rms_norm_op(gpu, m, k):
         assert np.array_equal(down16(h), o.add16(x, r, dtype))
         d = ulp_distance16(down16(n), o.rms_norm16(o.add16(x, r, dtype), w, 1e-5, dtype), dtype)
         assert d.max() <= 1 and (d == 0).mean() > 0.99
+
+
+def test_dispatch_routes(gpu):
+    """sparkq.ops.dispatch_ffn / dispatch_qkv take the fused kernels for the
+    standard modules and one token, and the composed route otherwise, with
+    the results of the direct ops."""
+    import sparkq
+    from sparkq.ops import QuantizedLinear, RMSNorm, RoPE, dispatch_ffn, dispatch_qkv
+
+    dtype, g, k, inter = o.BF16, 64, 2560, 2048
+    t16 = torch.bfloat16
+
+    def layer(seed, n, kk):
+        wq, s, b = _dev(_mat(seed, 1, n, kk, g, dtype), gpu, dtype)
+        return QuantizedLinear(wq, s, b, group_size=g, bits=4)
+
+    class MLP(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_proj, self.up_proj, self.down_proj = (
+                layer(1, inter, k), layer(2, inter, k), layer(3, k, inter))
+
+        def forward(self, x):
+            raise AssertionError("the standard MLP must take the fused route")
+
+    mlp = MLP()
+    norm = RMSNorm(k, 1e-6, weight=up16(o.round16(1.0 + 0.1 * o.randn(1, 4, k), dtype), dtype, gpu))
+    x = up16(o.randn16(1, 5, k), dtype, gpu).view(1, 1, k)
+    a = up16(o.randn16(1, 6, k), dtype, gpu).view(1, 1, k)
+    y = dispatch_ffn(x, a, norm, mlp, mlp_type=MLP)
+    p = lambda m: (m.weight, m.scales, m.biases)  # noqa: E731
+    ref = sparkq.fused_ffn(x, a, norm.weight, 1e-6, p(mlp.gate_proj), p(mlp.up_proj),
+                           p(mlp.down_proj), group_size=g)
+    assert torch.equal(y, ref)
+
+    nh, nkv, hd = 8, 2, 128
+    proj = layer(7, (nh + 2 * nkv) * hd, k)
+    rope = RoPE(hd, base=10000.0)
+    kw = dict(q_size=nh * hd, kv_size=nkv * hd, n_heads=nh, n_kv_heads=nkv, head_dim=hd)
+    q1, k1, v1 = dispatch_qkv(x, proj, rope, offset=5, **kw)
+    fq, fk, fv = sparkq.spark_qkv_rope(x, proj.weight, proj.scales, proj.biases, nh * hd,
+                                       nkv * hd, nh, nkv, hd, hd, 10000.0, 5, g, 4)
+    assert torch.equal(q1, fq) and torch.equal(k1, fk) and torch.equal(v1, fv)
+    # four tokens: projection, head split, rope at positions 5..8
+    x4 = up16(o.randn16(1, 8, 4 * k), dtype, gpu).view(1, 4, k)
+    q4, k4, v4 = dispatch_qkv(x4, proj, rope, offset=5, **kw)
+    y4 = sparkq.affine_quantized_matmul(x4, proj.weight, proj.scales, proj.biases, group_size=g)
+    yq = y4[..., :nh * hd].reshape(1, 4, nh, hd).transpose(1, 2)
+    assert q4.shape == (1, nh, 4, hd) and v4.shape == (1, nkv, 4, hd)
+    assert torch.equal(q4, sparkq.rope(yq.contiguous(), hd, base=10000.0, offset=5))
+    assert torch.equal(v4, y4[..., (nh + nkv) * hd:].reshape(1, 4, nkv, hd).transpose(1, 2))
+    # token 3 of the four equals the single-token fused route at offset 8
+    # up to the projection's row count (same per-row arithmetic)
+    s1 = dispatch_qkv(x4[:, 3:4].contiguous(), proj, rope, offset=8, **kw)
+    assert torch.equal(s1[2][:, :, 0], v4[:, :, 3])
+    assert t16 == q4.dtype

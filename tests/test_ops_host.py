@@ -176,3 +176,42 @@ def test_quantized_kv_cache_contract():
     with pytest.raises(ValueError, match="capacity"):
         ext.kv_append(x, (torch.zeros((1, 2, 2, 128), dtype=torch.int8),
                           torch.zeros((1, 2, 2), dtype=torch.float16)), 0)
+
+
+def test_layer_dispatch_contract_on_host():
+    """The FFN/QKV dispatchers keep the reference's module fallback for
+    non-standard modules, and the kernels never run on CPU tensors."""
+    from sparkq import ext
+    from sparkq.ops import RMSNorm, RoPE, dispatch_ffn, dispatch_qkv
+
+    calls = []
+
+    class Custom(torch.nn.Module):
+        def forward(self, h):
+            calls.append(h.shape)
+            return 2 * h
+
+    x = torch.ones(1, 1, 8)
+    a = torch.full((1, 1, 8), 0.5)
+    # custom norm and MLP: module calls, hidden + mlp(norm(hidden))
+    y = dispatch_ffn(x, a, lambda h: h + 1, Custom(), mlp_type=torch.nn.Linear)
+    assert torch.equal(y, 1.5 + 2 * 2.5 * torch.ones(1, 1, 8)) and calls == [(1, 1, 8)]
+    # the kernels refuse host tensors instead of computing elsewhere
+    with pytest.raises(ValueError, match="GPU"):
+        ext.rope(torch.zeros(1, 2, 3, 8, dtype=torch.bfloat16), 8)
+    norm = RMSNorm(8, 1e-6, weight=torch.ones(8, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="GPU"):
+        norm(torch.zeros(2, 8, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="x must have shape"):
+        ext.spark_qkv_rope(torch.zeros(1, 2, 64, dtype=torch.bfloat16), None, None, None,
+                           64, 16, 4, 1, 16, 16, 10000.0, 0, 64, 4)
+    with pytest.raises(ValueError, match="Invalid head counts"):
+        ext.spark_qkv_rope(torch.zeros(1, 1, 64, dtype=torch.bfloat16), None, None, None,
+                           64, 16, 4, 3, 16, 16, 10000.0, 0, 64, 4)
+    # a projection that is not an affine W4 module is called as a module
+    proj = Custom()
+    rope = RoPE(8)
+    with pytest.raises(ValueError, match="GPU"):
+        dispatch_qkv(torch.zeros(1, 2, 24, dtype=torch.bfloat16), proj, rope, q_size=8,
+                     kv_size=8, n_heads=1, n_kv_heads=1, head_dim=8, offset=0)
+    assert calls[-1] == (1, 2, 24)
