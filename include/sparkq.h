@@ -192,7 +192,10 @@ int sparkq_w8a16_linear(const void* x, const int8_t* w, const float* scales,
  *     strides[9..11] value scales (elements; biases share them)
  *   All N tokens are visible (bottom-right causal decode with L=1).
  * out = softmax(scale * q . K^T) . V in fp32 with an online softmax, split
- * over the context and merged by log-sum-exp.
+ * over the context and merged by log-sum-exp (in the same launch, by the
+ * last split to finish, for the symmetric format with a 16-bit query). A
+ * split decode needs the workspace: per-(batch, KV head) counters in its
+ * first 16384 bytes (zero before the first call, left zero), then partials.
  * Replaces int8_quantized_sdpa (X/spark_mlx_ext/int8_quantized_sdpa.py:
  * 156-287) and its kernels spark_affine_u8_sdpa_{decode,merge,short}
  * (X/spark_mlx_ext/_int8_sdpa_sources.py:8-376). D in {64,128,256};

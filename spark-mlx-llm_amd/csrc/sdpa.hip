@@ -42,6 +42,7 @@ struct SdpaArgs {
   float* pm;
   float* pz;
   float* pacc;
+  unsigned* counters;  // per (batch, KV head): the last split's workgroup merges (or null)
   int64_t kc_b, kc_h, kc_t;  // key codes (bytes)
   int64_t ks_b, ks_h, ks_t;  // key scales/biases (elements)
   int64_t vc_b, vc_h, vc_t;  // value codes (bytes)
@@ -281,6 +282,53 @@ struct SdpaMfmaLds {
   static constexpr int BYTES = LOOP > MERGE ? LOOP : MERGE;
 };
 
+// The split merge done by the last workgroup of a (batch, KV head) to finish
+// (the others' partials are read with coherent loads): per query head the
+// maximum over the splits, the split weights and the normalizer (one wave
+// per head), then each output as the weighted sum of the partial outputs in
+// split order, eight loads in flight. sm holds GQA*S + GQA floats.
+template <int D, int GQA>
+__device__ void sdpa_fold_merge(const SdpaArgs& a, int b, int kh, float* sm) {
+  const int S = a.S, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* wts = sm;             // [GQA][S]
+  float* zs = sm + GQA * S;    // [GQA]
+  for (int h = wave; h < GQA; h += 4) {
+    const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
+    float mm = kNegInf;
+    for (int s = lane; s < S; s += 64) mm = fmaxf(mm, splitk_load(a.pm + bh * S + s));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+    float z = 0.0f;
+    for (int s = lane; s < S; s += 64) {
+      const float m = splitk_load(a.pm + bh * S + s);
+      const float w = exp2_guarded(m - mm, m != kNegInf);
+      wts[h * S + s] = w;
+      z = fmaf(splitk_load(a.pz + bh * S + s), w, z);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o);
+    if (lane == 0) zs[h] = z;
+  }
+  __syncthreads();
+  for (int e = tid; e < GQA * D; e += 256) {
+    const int h = e / D, d = e - h * D;
+    const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
+    const float* p = a.pacc + bh * S * D + d;
+    const float* w = wts + h * S;
+    float o = 0.0f;
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = splitk_load(p + (int64_t)(s + u) * D);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o = fmaf(v[u], w[s + u], o);
+    }
+    for (; s < S; ++s) o = fmaf(splitk_load(p + (int64_t)s * D), w[s], o);
+    store_out(a.out, bh * D + d, zs[h] > 0.0f ? o / zs[h] : 0.0f, a.out_dtype);
+  }
+}
+
 template <int D, int GQA>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaArgs a) {
   constexpr int NC = D / 32;   // k chunks of QK
@@ -514,12 +562,26 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
     const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
     if (a.S == 1) {
       store_out(a.out, bh * D + d, z > 0.0f ? o / z : 0.0f, a.out_dtype);
+    } else if (a.counters) {
+      splitk_store(&a.pacc[(bh * a.S + split) * D + d], o);
+      if (d == 0) {
+        splitk_store(&a.pm[bh * a.S + split], mm);
+        splitk_store(&a.pz[bh * a.S + split], z);
+      }
     } else {
       a.pacc[(bh * a.S + split) * D + d] = o;
       if (d == 0) {
         a.pm[bh * a.S + split] = mm;
         a.pz[bh * a.S + split] = z;
       }
+    }
+  }
+  if (a.S > 1 && a.counters) {
+    __shared__ int s_last;
+    if (splitk_arrive(a.counters + blockIdx.y, a.S, &s_last)) {
+      __syncthreads();  // the combine above is done with the LDS it reused
+      sdpa_fold_merge<D, GQA>(a, b, kh, reinterpret_cast<float*>(smem));
+      splitk_reset(a.counters + blockIdx.y);
     }
   }
 }
@@ -929,12 +991,15 @@ static int sdpa_splits(int64_t B, int64_t N, int64_t* tps_out = nullptr) {
   return (int)S;
 }
 
+// Workspace of a split decode: the per-(batch, KV head) counters of the
+// in-kernel merge first (zero before the first call, left zero), then the
+// partial maxima, sums and outputs.
 size_t sdpa_workspace(int64_t B, int64_t Hq, int64_t N, int64_t D) {
   if (B <= 0 || Hq <= 0 || N <= 0 || D <= 0) return 0;
   const int S = sdpa_splits(B, N);
   if (S == 1) return 0;
   const size_t rows = (size_t)B * Hq * S;
-  return round_up(rows * 4, 256) * 2 + round_up(rows * D * 4, 256);
+  return kCounterBytes + round_up(rows * 4, 256) * 2 + round_up(rows * D * 4, 256);
 }
 
 template <int D, int GQA>
@@ -1007,17 +1072,24 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
   a.S = S;
   a.tps = (int)tps;
   a.scale_log2 = scale * 1.4426950408889634f;
+  const int gqa = (int)(Hq / Hkv);
+  const bool mfma = fmt == SPARKQ_KV_S8_F16SCALE && (qdt == SPARKQ_BF16 || qdt == SPARKQ_F16) &&
+                    !env_int("SPARKQ_SDPA_NO_MFMA", 0);
   if (S > 1) {
     const size_t rows = (size_t)B * Hq * S;
     unsigned char* base = reinterpret_cast<unsigned char*>(ws);
+    // the MFMA kernel merges the splits itself when its LDS holds the split
+    // weights and the counters cover every (batch, KV head)
+    if (mfma && (int64_t)gqa * S <= 2048 && B * Hkv <= kMaxCounterTiles &&
+        !env_int("SPARKQ_SDPA_MERGE_KERNEL", 0))
+      a.counters = reinterpret_cast<unsigned*>(base);
+    base += kCounterBytes;
     a.pm = reinterpret_cast<float*>(base);
     a.pz = reinterpret_cast<float*>(base + round_up(rows * 4, 256));
     a.pacc = reinterpret_cast<float*>(base + 2 * round_up(rows * 4, 256));
   }
-  const int gqa = (int)(Hq / Hkv);
   dim3 grid((unsigned)S, (unsigned)(B * Hkv));
-  if (fmt == SPARKQ_KV_S8_F16SCALE && (qdt == SPARKQ_BF16 || qdt == SPARKQ_F16) &&
-      !env_int("SPARKQ_SDPA_NO_MFMA", 0)) {
+  if (mfma) {
     if (D == 64)
       launch_mfma_d<64>(a, gqa, grid, st);
     else if (D == 128)
@@ -1031,7 +1103,7 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
   else
     launch_decode_d<256>(a, gqa, fmt, grid, st);
   if (int rc = check_launch("sdpa_decode_kernel")) return rc;
-  if (S > 1) {
+  if (S > 1 && !a.counters) {
     hipLaunchKernelGGL(sdpa_merge_kernel, dim3((unsigned)(B * Hq)), dim3(256), 0, st, a.pm,
                        a.pz, a.pacc, out, odt, S, (int)D);
     if (int rc = check_launch("sdpa_merge_kernel")) return rc;
