@@ -974,6 +974,61 @@ __global__ __launch_bounds__(256) void kv_append_u8_kernel(KvAppendArgs a) {
   }
 }
 
+// The same quantizer with one wave per row (D = 64*E): lane i holds dims
+// E*i .. E*i+E-1, the G/E lanes of a group reduce its min and max by a
+// butterfly, and each lane writes its own E code bytes (byte j of word w of
+// the packed row is dim 4w+j). Same formula and rounding as above.
+template <typename T, int E>
+__global__ __launch_bounds__(256) void kv_append_u8_wave_kernel(KvAppendArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.H * a.L) return;  // whole waves leave together
+  const int l = (int)(row % a.L), bh = (int)(row / a.L), h = bh % a.H, b = bh / a.H;
+  const int64_t t = (int64_t)a.offset + l;
+  const uint16_t* v = reinterpret_cast<const uint16_t*>(a.x) + row * (64 * E) + E * lane;
+  float f[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) f[e] = T::to_f32(v[e]);
+  float mn = f[0], mx = f[0];
+#pragma unroll
+  for (int e = 1; e < E; ++e) {
+    mn = f[e] < mn ? f[e] : mn;
+    mx = f[e] > mx ? f[e] : mx;
+  }
+  const int LG = a.G / E;  // lanes per group: 8, 16, 32 or 64
+  for (int o = LG >> 1; o > 0; o >>= 1) {
+    const float pn = __shfl_xor(mn, o), px = __shfl_xor(mx, o);
+    mn = pn < mn ? pn : mn;
+    mx = px > mx ? px : mx;
+  }
+  const uint16_t s16 = T::from_f32((mx - mn) / 255.0f), b16 = T::from_f32(mn);
+  const int g = lane / LG;
+  if (lane % LG == 0) {
+    const int64_t si = b * a.s_b + h * a.s_h + t * a.s_t + g;
+    reinterpret_cast<uint16_t*>(a.scales)[si] = s16;
+    reinterpret_cast<uint16_t*>(a.biases)[si] = b16;
+  }
+  const float sf = T::to_f32(s16), bf = T::to_f32(b16);
+  uint32_t bytes = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    float q = 0.0f;
+    if (sf != 0.0f) {
+      q = __builtin_rintf((f[e] - bf) / sf);
+      q = q < 0.0f ? 0.0f : (q > 255.0f ? 255.0f : q);
+    }
+    bytes |= (uint32_t)q << (8 * e);
+  }
+  unsigned char* dst = reinterpret_cast<unsigned char*>(a.codes) + b * a.c_b + h * a.c_h +
+                       t * a.c_t + E * lane;
+  if constexpr (E == 4)
+    *reinterpret_cast<uint32_t*>(dst) = bytes;
+  else if constexpr (E == 2)
+    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)bytes;
+  else
+    *dst = (unsigned char)bytes;
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -1166,6 +1221,16 @@ int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const voi
   return check_launch("sdpa_prefill_kernel");
 }
 
+template <typename T>
+static void launch_append_u8(int D, const KvAppendArgs& a, dim3 grid, hipStream_t st) {
+  if (D == 64)
+    hipLaunchKernelGGL((kv_append_u8_wave_kernel<T, 1>), grid, dim3(256), 0, st, a);
+  else if (D == 128)
+    hipLaunchKernelGGL((kv_append_u8_wave_kernel<T, 2>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((kv_append_u8_wave_kernel<T, 4>), grid, dim3(256), 0, st, a);
+}
+
 int kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B, int64_t H,
               int64_t L, int64_t D, int64_t offset, int G, int fmt, int xdt,
               const int64_t* strides, hipStream_t st) {
@@ -1190,6 +1255,13 @@ int kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B,
   const int64_t rows = B * H * L;
   if (fmt == SPARKQ_KV_S8_F16SCALE) {
     hipLaunchKernelGGL(kv_append_s8_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, st, a);
+  } else if ((D == 64 || D == 128 || D == 256) && G % (D / 64) == 0 && G / (D / 64) <= 64 &&
+             !env_int("SPARKQ_KV_APPEND_THREAD", 0)) {
+    const dim3 grid((unsigned)cdiv(rows, 4));
+    if (xdt == SPARKQ_BF16)
+      launch_append_u8<BF16>((int)D, a, grid, st);
+    else
+      launch_append_u8<F16>((int)D, a, grid, st);
   } else {
     const unsigned grid = (unsigned)cdiv(rows * (D / G), 256);
     if (xdt == SPARKQ_BF16)

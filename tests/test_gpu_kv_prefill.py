@@ -22,7 +22,9 @@ def _x16(seed, stream, shape, dtype=o.BF16):
 
 
 @pytest.mark.parametrize("fmt,d,g", [("s8", 128, 32), ("s8", 64, 32), ("affine_u8", 128, 32),
-                                     ("affine_u8", 256, 64), ("affine_u8", 128, 128)])
+                                     ("affine_u8", 256, 64), ("affine_u8", 128, 128),
+                                     ("affine_u8", 64, 32), ("affine_u8", 64, 64),
+                                     ("affine_u8", 256, 32)])
 def test_append_matches_oracle(gpu, fmt, d, g):
     import sparkq
 
