@@ -1,0 +1,359 @@
+// w4mr.hip -- W4A16 decode GEMV for 9..16 activation rows on the
+// 16x16x32 MFMA (speculative-verify and small-batch decode).
+//
+// The 4x4x4 decode kernels share each decoded weight piece across the
+// activation rows four at a time; at 8..16 rows their activation reads from
+// LDS (16 KB per 1 KB item and wave at M = 16) bound them. Here one
+// v_mfma_f32_16x16x32 takes 16 weight rows x 16 activation rows x 32 k:
+//
+//  * Items: a row tile of 16 weight rows x one 128-k segment (64 bytes a
+//    row). Lane l loads 16 bytes of row l%16 at byte 16*(l/16) of the
+//    segment: one load instruction per item, every load issued at the start.
+//  * A 4x4 transpose of the loaded words across the four 16-lane rows
+//    (v_permlane32_swap, then v_permlane16_swap) leaves in lane (g, r) word
+//    g of each 32-k chunk c, so MFMA c covers exactly chunk c: its k range
+//    lies inside one quantization group (G >= 32) and the group's scale and
+//    bias apply to the MFMA result, s*D + (b - OFFSET*s)*X with X the group
+//    sum of each activation row (the decode of 3.1: codes read as OFFSET + q).
+//  * The A operand is 8 activations of row l%16 read from LDS (rows padded
+//    by 16 bytes); rows past M read row M-1 and their outputs are dropped.
+//  * Layout as the streaming kernels: one workgroup of 16 waves per CU, a
+//    contiguous range of row tiles per workgroup, the (tile, segment) items
+//    dealt to the waves in contiguous runs. A wave sums its run of a tile in
+//    registers and leaves the sum in an LDS slot (a run touches at most two
+//    tiles); each output is the sum of its tile's slots in wave order.
+#include "common.h"
+
+namespace sparkq {
+
+struct MrArgs {
+  const uint16_t* x;
+  const uint32_t* w;
+  const uint16_t* sc;
+  const uint16_t* bi;
+  void* y;
+  const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
+  int y_dtype;
+  int M, N, K;
+  int nt;  // row tiles of 16
+  int P;   // workgroups
+  int TW;  // tiles of the largest workgroup
+  int IW;  // items per wave
+};
+
+constexpr int kMrNW = 16;              // waves per workgroup
+constexpr int kMrXC = 8;               // staged activation chunks (16 B) per thread, at most
+constexpr int kMrSP = 2;               // staged (scale, bias) pieces per thread, at most
+constexpr int kMrMaxLds = 160 * 1024;
+
+// LDS layout (byte offsets)
+struct MrLds {
+  int xrow;  // padded activation row (bytes)
+  int xa;    // activations [M][K]
+  int xs;    // group sums [K/G][16] fp32 (rows past M zero)
+  int sb;    // (scale, bias) of the workgroup's rows [16*TW][K/G] dwords
+  int part;  // run sums [waves][2][16][16] fp32
+  int bytes;
+};
+__host__ __device__ __forceinline__ MrLds mr_lds(int M, int K, int TW, int G) {
+  MrLds l;
+  l.xrow = 2 * K + 16;
+  l.xa = 0;
+  l.xs = (M * l.xrow + 15) & ~15;
+  l.sb = l.xs + (K / G) * 64;
+  l.part = l.sb + ((TW * 16 * (K / G) * 4 + 15) & ~15);
+  l.bytes = l.part + kMrNW * 2 * 256 * 4;
+  return l;
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c);
+template <>
+__device__ __forceinline__ f32x4_t mfma16x16x32<BF16>(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4_t mfma16x16x32<F16>(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// 4x4 transpose of the words of a 16-byte piece across the four 16-lane rows
+// of the wave: afterwards lane (row g) holds in word c what row c held in
+// word g. The 32-lane swap exchanges the off-diagonal 2x2 blocks, the 16-lane
+// swap transposes each block.
+__device__ __forceinline__ u32x4_t transpose_rows(u32x4_t v) {
+  uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
+  auto r = __builtin_amdgcn_permlane32_swap(w0, w2, false, false);
+  w0 = r[0];
+  w2 = r[1];
+  r = __builtin_amdgcn_permlane32_swap(w1, w3, false, false);
+  w1 = r[0];
+  w3 = r[1];
+  r = __builtin_amdgcn_permlane16_swap(w0, w1, false, false);
+  w0 = r[0];
+  w1 = r[1];
+  r = __builtin_amdgcn_permlane16_swap(w2, w3, false, false);
+  w2 = r[0];
+  w3 = r[1];
+  return u32x4_t{w0, w1, w2, w3};
+}
+
+template <typename T, int G, int NI>
+__global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NT = 64 * kMrNW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r16 = lane & 15;
+  const int M = a.M, N = a.N, K = a.K;
+  const int ng = K / G, SEG = K >> 7, RB = K >> 1;
+  const int t0 = blockIdx.x * a.nt / a.P;
+  const int ntl = (blockIdx.x + 1) * a.nt / a.P - t0;  // tiles of this workgroup
+  const int IW = a.IW;
+  const int i0 = wave * IW;
+  const int ni = max(0, min(IW, ntl * SEG - i0));      // items of this wave
+  const MrLds L = mr_lds(M, K, a.TW, G);
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+
+  // 1. staging loads: activation chunks and the (scale, bias) pieces of the
+  // workgroup's rows (16 * ntl contiguous rows)
+  const int nxc = (M * K) >> 3;
+  const int nsp = (ntl * 16 * ng) >> 3;
+  // every thread issues the same loads (lanes with nothing to read use the
+  // out-of-range offset): branches around loads here made the compiler
+  // spill the staging registers
+  u32x4_t xr[kMrXC], sr[kMrSP], br[kMrSP];
+#pragma unroll
+  for (int c = 0; c < kMrXC; ++c) {
+    const int ci = tid + c * NT;
+    xr[c] = buf_load16(rx, ci < nxc ? 16u * ci : kOob);
+  }
+#pragma unroll
+  for (int i = 0; i < kMrSP; ++i) {
+    const int pi = tid + i * NT;
+    const uint32_t off = pi < nsp ? 32u * (uint32_t)t0 * ng + 16u * pi : kOob;
+    sr[i] = buf_load16(rs, off);
+    br[i] = buf_load16(rb, off);
+  }
+  // 2. the wave's weight items
+  u32x4_t wv[NI];
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    const int it = i0 + k, tl = it / SEG, s = it - tl * SEG;
+    const int row = 16 * (t0 + tl) + r16;
+    const bool ok = k < ni && row < N;
+    wv[k] = buf_load16(rw, ok ? (uint32_t)row * RB + 64u * s + 16u * g : kOob);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. activations and (scale, bias) pairs to LDS, then the group sums
+  uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+  float* xs = reinterpret_cast<float*>(smem + L.xs);
+#pragma unroll
+  for (int c = 0; c < kMrXC; ++c) {
+    const int ci = tid + c * NT;
+    if (ci < nxc) {
+      const int m = ci / (K >> 3), kk = (ci - m * (K >> 3)) << 3;
+      *reinterpret_cast<u32x4_t*>(smem + L.xa + m * L.xrow + 2 * kk) = xr[c];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMrSP; ++i) {
+    const int pi = tid + i * NT;
+    if (pi < nsp) {
+      const u32x4_t s = sr[i], c = br[i];
+      u32x4_t lo, hi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = __builtin_amdgcn_perm(c[e], s[e], 0x05040100u);  // (s0, b0)
+        hi[e] = __builtin_amdgcn_perm(c[e], s[e], 0x07060302u);  // (s1, b1)
+      }
+      *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+      *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < ng * 16; e += NT) {
+    const int grp = e >> 4, m = e & 15;
+    float s = 0.0f;
+    if (m < M) {
+      const unsigned char* p = smem + L.xa + m * L.xrow + 2 * G * grp;
+      for (int q = 0; q < G / 8; ++q) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p + 16 * q);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) s = pair_sum<T>(v[h], s);
+      }
+    }
+    xs[e] = s;
+  }
+  __syncthreads();
+
+  // 4. the items: per 32-k chunk one MFMA, per group the scale epilogue
+  float* part = reinterpret_cast<float*>(smem + L.part);
+  const unsigned char* arow = smem + L.xa + min(r16, M - 1) * L.xrow + 16 * g;
+  const DecodeConsts dc = decode_consts<T>();
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  int cur = -1, slot = 0;
+  auto flush = [&]() {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[(wave * 2 + slot) * 256 + (4 * g + r) * 16 + r16] = acc[r];
+  };
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    if (k < ni) {
+      const int it = i0 + k, tl = it / SEG, s = it - tl * SEG;
+      if (tl != cur) {
+        if (cur >= 0) {
+          flush();
+          slot = 1;
+        }
+        cur = tl;
+        acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      const u32x4_t wt = transpose_rows(wv[k]);
+      f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int kb = 128 * s + 32 * c;
+        const u32x4_t bop = decode_w4<T>(wt[c], dc);
+        const u32x4_t aop = *reinterpret_cast<const u32x4_t*>(arow + 2 * kb);
+        d = mfma16x16x32<T>(aop, bop, d);
+        if (((c + 1) * 32) % G == 0) {
+          const int grp = kb / G;
+          const uint32_t pair = sb[(tl * 16 + r16) * ng + grp];
+          const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
+          const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
+          const f32x4_t xg = *reinterpret_cast<const f32x4_t*>(xs + grp * 16 + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(sf, d[r], fmaf(bf, xg[r], acc[r]));
+          d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+      }
+      // one item at a time: hoisting later items' decodes would spill
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (cur >= 0) flush();
+  __syncthreads();
+
+  // 5. each output: the sum of its tile's run slots in wave order
+  for (int e = tid; e < ntl * 256; e += NT) {
+    const int tl = e >> 8, m = (e >> 4) & 15, j = e & 15;
+    const int n = 16 * (t0 + tl) + j;
+    if (m >= M || n >= N) continue;
+    const int v0 = (tl * SEG) / IW, v1 = ((tl + 1) * SEG - 1) / IW;
+    float v = 0.0f;
+    for (int w = v0; w <= v1; ++w) {
+      const int sl = (w * IW) / SEG == tl ? 0 : 1;
+      v += part[(w * 2 + sl) * 256 + m * 16 + j];
+    }
+    const int64_t idx = (int64_t)m * N + n;
+    store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+// Plan: 9..16 rows (from 2 with SPARKQ_W4_MR_MIN), K a multiple of 128, the
+// activations, scales and run slots within 160 KB of LDS, at most 8 items
+// per wave and no wave run longer than a row (so it touches at most two
+// tiles). Measured per projection (bf16, G64): QKV 3584x2560 and gate+up
+// 19456x2560 take 6.9-7.1 and 14.2-14.8 us from 5 to 16 rows, against 6.1
+// and 13.0 us at 5 rows, 6.2 and 14.4 at 8, 7.6 and 18.2 at 12 and 8.8 and
+// 21.8 at 16 on the 4x4x4 multi-row kernel; down 2560x9728 at 5 rows 12.2
+// against 9.2 us.
+struct MrPlan {
+  bool ok;
+  int P, TW, IW, NI;
+  size_t lds;
+};
+
+static MrPlan plan_mr(int64_t M, int64_t N, int64_t K, int G) {
+  MrPlan p{};
+  if (M < env_int("SPARKQ_W4_MR_MIN", 9) || M > 16 || env_int("SPARKQ_W4_NO_MR", 0)) return p;
+  if (K % 128 != 0 || K % G != 0) return p;
+  if (N * (K / 2) >= (int64_t)kOob || M * K * 2 >= (int64_t)kOob) return p;
+  const int64_t ng = K / G;
+  if ((N * ng * 2) % 16 != 0) return p;
+  const int64_t nt = cdiv(N, 16), SEG = K / 128;
+  p.P = (int)std::min<int64_t>(nt, device_cus());
+  p.TW = (int)cdiv(nt, p.P);
+  const int64_t iw = cdiv(p.TW * SEG, kMrNW);
+  if (iw > 8 || iw > SEG) return p;
+  p.IW = (int)iw;
+  p.NI = iw <= 2 ? 2 : (iw <= 4 ? 4 : 8);
+  if (M * K / 8 > (int64_t)kMrXC * 64 * kMrNW) return p;
+  if (p.TW * 16 * ng / 8 > (int64_t)kMrSP * 64 * kMrNW) return p;
+  const MrLds l = mr_lds((int)M, (int)K, p.TW, G);
+  if (l.bytes > kMrMaxLds) return p;
+  p.lds = (size_t)l.bytes;
+  p.ok = true;
+  return p;
+}
+
+template <typename T, int G, int NI>
+static void launch_mr_n(const MrPlan& p, const MrArgs& a, hipStream_t st) {
+  auto* k = w4_mr16_kernel<T, G, NI>;
+  // dynamic LDS above 64 KB must be enabled per kernel
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, kMrMaxLds);
+  (void)attr;
+  hipLaunchKernelGGL(k, dim3((unsigned)p.P), dim3(64 * kMrNW), p.lds, st, a);
+}
+template <typename T, int G>
+static void launch_mr_g(const MrPlan& p, const MrArgs& a, hipStream_t st) {
+  if (p.NI == 2)
+    launch_mr_n<T, G, 2>(p, a, st);
+  else if (p.NI == 4)
+    launch_mr_n<T, G, 4>(p, a, st);
+  else
+    launch_mr_n<T, G, 8>(p, a, st);
+}
+template <typename T>
+static void launch_mr(const MrPlan& p, int G, const MrArgs& a, hipStream_t st) {
+  if (G == 32)
+    launch_mr_g<T, 32>(p, a, st);
+  else if (G == 64)
+    launch_mr_g<T, 64>(p, a, st);
+  else
+    launch_mr_g<T, 128>(p, a, st);
+}
+
+bool w4_mr_supported(int64_t M, int64_t N, int64_t K, int G) { return plan_mr(M, N, K, G).ok; }
+
+// Returns 1 when the shape is not served (the caller picks another kernel).
+int w4_mr_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
+                 int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, hipStream_t st,
+                 const void* res) {
+  const MrPlan p = plan_mr(M, N, K, G);
+  if (!p.ok) return 1;
+  MrArgs a{};
+  a.x = (const uint16_t*)x;
+  a.w = w;
+  a.sc = (const uint16_t*)s;
+  a.bi = (const uint16_t*)b;
+  a.y = y;
+  a.res = (const uint16_t*)res;
+  a.y_dtype = ydt;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.nt = (int)cdiv(N, 16);
+  a.P = p.P;
+  a.TW = p.TW;
+  a.IW = p.IW;
+  if (xdt == SPARKQ_BF16)
+    launch_mr<BF16>(p, G, a, st);
+  else
+    launch_mr<F16>(p, G, a, st);
+  return check_launch("w4_mr16_kernel");
+}
+
+}  // namespace sparkq

@@ -149,15 +149,45 @@ def test_decode_long_rows(gpu, n, k, g):
 
 @pytest.mark.parametrize("m,n,k,g", [(3, 1100, 4096, 64), (5, 1100, 3072, 32), (12, 260, 1536, 128),
                                      (16, 1028, 2048, 64), (2, 8, 9728, 64)])
-def test_decode_multirow_stream(gpu, m, n, k, g):
-    """2 <= M <= 16 on the multi-row streaming kernel: more row quads than
-    CUs (uneven split), fewer, a row-quad count below the wave count, M not a
-    multiple of 4 (the last row quartet repeats row M-1) and long rows."""
+def test_decode_multirow_stream(gpu, m, n, k, g, monkeypatch):
+    """2 <= M <= 16 on the multi-row streaming kernel (the 16x16x32 kernel
+    switched off): more row quads than CUs (uneven split), fewer, a row-quad
+    count below the wave count, M not a multiple of 4 (the last row quartet
+    repeats row M-1) and long rows."""
+    monkeypatch.setenv("SPARKQ_W4_NO_MR", "1")
     x, wq, s, b = w4_problem(m, n, k, g, seed=m * n)
     ref = o.w4a16_matmul(x, wq, s, b, g)
     y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
     check_fp32(y32, ref)
     check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
+
+
+@pytest.mark.parametrize("m,n,k,g", [(5, 1100, 3072, 32), (8, 3584, 2560, 64), (16, 19456, 2560, 64),
+                                     (16, 1000, 1152, 128), (5, 40, 9728, 64), (16, 16, 128, 32),
+                                     (11, 2560, 4096, 64)])
+def test_decode_mfma_rows(gpu, m, n, k, g, monkeypatch):
+    """5 <= M <= 16 on the 16x16x32 kernel (taken from 9 rows by default): a
+    partial last row tile, the benchmark's QKV and gate+up shapes,
+    one-segment rows (K = 128), long rows with one tile per workgroup, both
+    dtypes."""
+    monkeypatch.setenv("SPARKQ_W4_MR_MIN", "5")
+    for dtype in (o.BF16, o.F16):
+        x, wq, s, b = w4_problem(m, n, k, g, dtype=dtype, seed=m + n + k)
+        ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
+        y32 = _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32).cpu().numpy()
+        check_fp32(y32, ref)
+        check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
+
+
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_decode_mfma_rows_few(gpu, m, monkeypatch):
+    """The 16x16x32 kernel below 5 rows stays correct."""
+    monkeypatch.setenv("SPARKQ_W4_MR_MIN", "2")
+    n, k, g = 700, 2560, 64
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
+    check_fp32(y32, ref)
 
 
 @pytest.mark.parametrize("g", [32, 64, 128])
