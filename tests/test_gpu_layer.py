@@ -268,3 +268,45 @@ def test_dispatch_routes(gpu):
     s1 = dispatch_qkv(x4[:, 3:4].contiguous(), proj, rope, offset=8, **kw)
     assert torch.equal(s1[2][:, :, 0], v4[:, :, 3])
     assert t16 == q4.dtype
+
+
+def test_layer_graph_replay_matches_eager(gpu):
+    """The fused FFN block (one token and 16 rows), QKV + RoPE and the KV
+    append captured in one HIP graph: every replay, with eager work and
+    synchronisation between them, equals the eager results bit for bit."""
+    import sparkq
+
+    dtype, g, k, inter = o.BF16, 64, 2560, 9728
+    mats = [_dev(_mat(3, s, n, kk, g, dtype), gpu, dtype)
+            for s, n, kk in ((4, inter, k), (5, inter, k), (6, k, inter))]
+    qkv = _dev(_mat(3, 7, 3584, k, g, dtype), gpu, dtype)
+    nw = up16(o.round16(1.0 + 0.1 * o.randn(3, 3, k), dtype), dtype, gpu)
+    x1 = up16(o.randn16(3, 1, k), dtype, gpu).view(1, k)
+    a1 = up16(o.randn16(3, 2, k), dtype, gpu).view(1, k)
+    x16 = up16(o.randn16(3, 8, 16 * k), dtype, gpu).view(16, k)
+    a16 = up16(o.randn16(3, 9, 16 * k), dtype, gpu).view(16, k)
+    cache = sparkq.QuantizedKVCache(group_size=32, kv_format="affine_u8")
+    kv = up16(o.randn16(3, 10, 4 * 128), dtype, gpu).view(1, 4, 1, 128)
+    cache.update_and_fetch(kv, kv)   # allocate the storage before capture
+
+    def step():
+        f1 = sparkq.fused_ffn(x1, a1, nw, 1e-6, *mats, group_size=g)
+        f16 = sparkq.fused_ffn(x16, a16, nw, 1e-6, *mats, group_size=g)
+        q, kk, v = sparkq.spark_qkv_rope(x1.view(1, 1, k), *qkv, 2560, 512, 20, 4, 128, 128,
+                                         10000.0, 77, g, 4)
+        cache.offset = 1
+        keys, _ = cache.update_and_fetch(kk, v)
+        return [f1, f16, q, kk, v, keys[0]]
+
+    eager = [t.clone() for t in step()]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for _ in range(3):
+        junk = torch.randn(1 << 20, device=gpu).sum()   # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert float(junk) == float(junk)
+        for got, want in zip(outs, eager):
+            assert torch.equal(got, want)
