@@ -267,6 +267,15 @@ __device__ __forceinline__ u32x4_t s8x8_to_f16(uint32_t lo, uint32_t hi) {
                  __builtin_amdgcn_perm(0u, hi, 0x0C030C02u) ^ m};
 }
 
+// fp16 in the low half of a register to fp32. The conversion reads only the
+// low 16 bits; written as one instruction so that no masking of the loaded
+// scale registers is hoisted to where their loads are still in flight.
+__device__ __forceinline__ float f16lo_to_f32(int v) {
+  float r;
+  asm volatile("v_cvt_f32_f16 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
 __device__ __forceinline__ f32x4_t mfma16x16x32_f16(u32x4_t a, u32x4_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
@@ -406,9 +415,13 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
                                (uint32_t)(t_end * a.vs_t * 2));
 
   // block registers, two sets (the next two blocks are in flight while one
-  // is computed): K pieces [token group][piece], V pieces, one scale
+  // is computed): K pieces [token group][piece], V pieces, the K and V
+  // scales of the block's 32 tokens (lane t % 32). Every load is issued
+  // unconditionally (past t_end it reads zeros through the bounded
+  // descriptors), so the loop's wait counts stay exact instead of draining
+  // all loads each block.
   u32x4_t kr[2][2][PL], vr[2][VL];
-  uint32_t sr[2];
+  uint16_t skr[2], svr[2];
   auto load = [&](int set, int t0) {
 #pragma unroll
     for (int g2 = 0; g2 < 2; ++g2)
@@ -420,8 +433,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
       const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
       vr[set][v] = buf_load16(rv, (uint32_t)((t0 + tok) * a.vc_t + 16 * pc));
     }
-    sr[set] = lane < 32 ? buf_load2(rks, (uint32_t)((t0 + lane) * a.ks_t * 2))
-                        : buf_load2(rvs, (uint32_t)((t0 + lane - 32) * a.vs_t * 2));
+    skr[set] = buf_load2(rks, (uint32_t)((t0 + (lane & 31)) * a.ks_t * 2));
+    svr[set] = buf_load2(rvs, (uint32_t)((t0 + (lane & 31)) * a.vs_t * 2));
   };
 
   float mrun[4], zl[4], psl[4];
@@ -436,18 +449,14 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
   for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int stride = 4 * 32;
+  // The block's registers are read in place and refilled with the block two
+  // ahead once the QK product and the scales have been taken from them, so
+  // no register copy waits on the loads still in flight.
   auto block = [&](int t0, auto setc) {
     constexpr int set = decltype(setc)::value;
-    // this block's data, then the loads of the block two ahead into its set
-    u32x4_t kb[2][PL], vb[VL];
-#pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2)
-#pragma unroll
-      for (int i = 0; i < PL; ++i) kb[g2][i] = kr[set][g2][i];
-#pragma unroll
-    for (int v = 0; v < VL; ++v) vb[v] = vr[set][v];
-    const uint32_t sb = sr[set];
-    if (t0 + 2 * stride < t_end) load(set, t0 + 2 * stride);
+    __builtin_amdgcn_sched_barrier(0);  // nothing of this block moves into the previous one
+    const auto& kb = kr[set];
+    const auto& vb = vr[set];
     // V block to this wave's LDS copy (padded rows)
 #pragma unroll
     for (int v = 0; v < VL; ++v) {
@@ -467,10 +476,15 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
         sc[g2] = mfma16x16x32_f16(qa[c], kf, sc[g2]);
       }
     }
-    const float ksc0 = f16_to_f32((uint16_t)__shfl(sb, n16));
-    const float ksc1 = f16_to_f32((uint16_t)__shfl(sb, 16 + n16));
-    const float vsc0 = f16_to_f32((uint16_t)__shfl(sb, 32 + n16));
-    const float vsc1 = f16_to_f32((uint16_t)__shfl(sb, 48 + n16));
+    const float ksc0 = f16lo_to_f32(__shfl((int)skr[set], n16));
+    const float ksc1 = f16lo_to_f32(__shfl((int)skr[set], 16 + n16));
+    const float vsc0 = f16lo_to_f32(__shfl((int)svr[set], n16));
+    const float vsc1 = f16lo_to_f32(__shfl((int)svr[set], 16 + n16));
+    // the refill stays in issue order at this point (the wait counts of the
+    // next blocks rely on it)
+    __builtin_amdgcn_sched_barrier(0);
+    load(set, t0 + 2 * stride);
+    __builtin_amdgcn_sched_barrier(0);
     const bool ok0 = t0 + n16 < t_end, ok1 = t0 + 16 + n16 < t_end;
 
     float alpha[4];
@@ -515,12 +529,17 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
     }
   };
   int t0 = t_begin + 32 * wave;
-  if (t0 < t_end) load(0, t0);
-  if (t0 + stride < t_end) load(1, t0 + stride);
-  for (; t0 < t_end; t0 += 2 * stride) {
+  // blocks in pairs with no branch in the loop body (so the wait counts
+  // carried around it stay exact), then an odd last block
+  const int nb = t0 < t_end ? (t_end - t0 + stride - 1) / stride : 0;
+  load(0, t0);
+  load(1, t0 + stride);
+  int ib = 0;
+  for (; ib + 2 <= nb; ib += 2, t0 += 2 * stride) {
     block(t0, std::integral_constant<int, 0>{});
-    if (t0 + stride < t_end) block(t0 + stride, std::integral_constant<int, 1>{});
+    block(t0 + stride, std::integral_constant<int, 1>{});
   }
+  if (ib < nb) block(t0, std::integral_constant<int, 0>{});
 
   // per-lane partial sums -> the 16 token lanes of each head group
 #pragma unroll
@@ -681,9 +700,13 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
                                (uint32_t)(t_end * a.vs_t * 2));
 
   // block registers, two sets (the next two blocks are in flight while one
-  // is computed): K pieces [token group][piece], V pieces, one scale
+  // is computed): K pieces [token group][piece], V pieces, the K and V
+  // scales of the block's 32 tokens (lane t % 32). Every load is issued
+  // unconditionally (past t_end it reads zeros through the bounded
+  // descriptors), so the loop's wait counts stay exact instead of draining
+  // all loads each block.
   u32x4_t kr[2][2][PL], vr[2][VL];
-  uint32_t sr[2];
+  uint16_t skr[2], svr[2];
   auto load = [&](int set, int t0) {
 #pragma unroll
     for (int g2 = 0; g2 < 2; ++g2)
@@ -695,8 +718,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
       const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
       vr[set][v] = buf_load16(rv, (uint32_t)((t0 + tok) * a.vc_t + 16 * pc));
     }
-    sr[set] = lane < 32 ? buf_load2(rks, (uint32_t)((t0 + lane) * a.ks_t * 2))
-                        : buf_load2(rvs, (uint32_t)((t0 + lane - 32) * a.vs_t * 2));
+    skr[set] = buf_load2(rks, (uint32_t)((t0 + (lane & 31)) * a.ks_t * 2));
+    svr[set] = buf_load2(rvs, (uint32_t)((t0 + (lane & 31)) * a.vs_t * 2));
   };
 
   float mrun[4], zl[4], psl[4];
@@ -711,18 +734,14 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
   for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int stride = 32;
+  // The block's registers are read in place and refilled with the block two
+  // ahead once the QK product and the scales have been taken from them, so
+  // no register copy waits on the loads still in flight.
   auto block = [&](int t0, auto setc) {
     constexpr int set = decltype(setc)::value;
-    // this block's data, then the loads of the block two ahead into its set
-    u32x4_t kb[2][PL], vb[VL];
-#pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2)
-#pragma unroll
-      for (int i = 0; i < PL; ++i) kb[g2][i] = kr[set][g2][i];
-#pragma unroll
-    for (int v = 0; v < VL; ++v) vb[v] = vr[set][v];
-    const uint32_t sb = sr[set];
-    if (t0 + 2 * stride < t_end) load(set, t0 + 2 * stride);
+    __builtin_amdgcn_sched_barrier(0);  // nothing of this block moves into the previous one
+    const auto& kb = kr[set];
+    const auto& vb = vr[set];
     // V block to this wave's LDS copy (padded rows)
 #pragma unroll
     for (int v = 0; v < VL; ++v) {
@@ -742,10 +761,15 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
         sc[g2] = mfma16x16x32_f16(qa[c], kf, sc[g2]);
       }
     }
-    const float ksc0 = f16_to_f32((uint16_t)__shfl(sb, n16));
-    const float ksc1 = f16_to_f32((uint16_t)__shfl(sb, 16 + n16));
-    const float vsc0 = f16_to_f32((uint16_t)__shfl(sb, 32 + n16));
-    const float vsc1 = f16_to_f32((uint16_t)__shfl(sb, 48 + n16));
+    const float ksc0 = f16lo_to_f32(__shfl((int)skr[set], n16));
+    const float ksc1 = f16lo_to_f32(__shfl((int)skr[set], 16 + n16));
+    const float vsc0 = f16lo_to_f32(__shfl((int)svr[set], n16));
+    const float vsc1 = f16lo_to_f32(__shfl((int)svr[set], 16 + n16));
+    // the refill stays in issue order at this point (the wait counts of the
+    // next blocks rely on it)
+    __builtin_amdgcn_sched_barrier(0);
+    load(set, t0 + 2 * stride);
+    __builtin_amdgcn_sched_barrier(0);
 
     float alpha[4];
 #pragma unroll
@@ -788,12 +812,17 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
     }
   };
   int t0 = t_begin;
-  if (t0 < t_end) load(0, t0);
-  if (t0 + stride < t_end) load(1, t0 + stride);
-  for (; t0 < t_end; t0 += 2 * stride) {
+  // blocks in pairs with no branch in the loop body (so the wait counts
+  // carried around it stay exact), then an odd last block
+  const int nb = t0 < t_end ? (t_end - t0 + stride - 1) / stride : 0;
+  load(0, t0);
+  load(1, t0 + stride);
+  int ib = 0;
+  for (; ib + 2 <= nb; ib += 2, t0 += 2 * stride) {
     block(t0, std::integral_constant<int, 0>{});
-    if (t0 + stride < t_end) block(t0 + stride, std::integral_constant<int, 1>{});
+    block(t0 + stride, std::integral_constant<int, 1>{});
   }
+  if (ib < nb) block(t0, std::integral_constant<int, 0>{});
 
   // per-lane partial sums -> the 16 token lanes of each head group
 #pragma unroll
