@@ -215,19 +215,30 @@ def bench_sdpa(torch, sparkq, dev, b, n, iters):
             "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": kv_bytes}
 
 
-def bench_prefill(torch, sparkq, dev, length, n, iters):
-    """INT8-KV prefill attention, s8 cache: B=1, 32 query / 8 KV heads,
-    D=128, bottom-right causal. Useful flop: 4*Hq*D per visible (query,
-    token) pair."""
-    b, hq, hkv, d = 1, 32, 8, 128
-    kc, ks = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
-    vc, vs = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
+def bench_prefill(torch, sparkq, dev, length, n, iters, fmt="s8", hq=32, hkv=8, d=128, g=32):
+    """INT8-KV prefill attention, B=1, bottom-right causal, over the s8 cache
+    or the MLX affine u8 cache (group size g, quantized on append). Useful
+    flop: 4*Hq*D per visible (query, token) pair."""
+    b = 1
+    kv = [torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    if fmt == "s8":
+        keys, vals = (sparkq.kv_quantize_s8(t) for t in kv)
+        group = {}
+    else:
+        def affine(t):
+            cache = (torch.zeros((b, hkv, n, d // 4), device=dev, dtype=torch.int32),
+                     torch.zeros((b, hkv, n, d // g), device=dev, dtype=torch.bfloat16),
+                     torch.zeros((b, hkv, n, d // g), device=dev, dtype=torch.bfloat16))
+            sparkq.kv_append(t, cache, 0, group_size=g)
+            return cache
+        keys, vals = affine(kv[0]), affine(kv[1])
+        group = {"group_size": g}
     q = torch.randn((b, hq, length, d), device=dev).to(torch.bfloat16)
     out = torch.empty_like(q)
     scale = 1.0 / math.sqrt(d)
 
     def fn():
-        sparkq.int8_quantized_sdpa(q, (kc, ks), (vc, vs), scale=scale, mask="causal", out=out)
+        sparkq.int8_quantized_sdpa(q, keys, vals, scale=scale, mask="causal", out=out, **group)
 
     graph = capture(torch, fn)
     ms = Timer(torch).time(graph.replay, iters, 2)
@@ -453,6 +464,10 @@ def main():
         extras["int8kv_sdpa_prefill_causal"] = {
             f"L={l} N={n}": bench_prefill(torch, sparkq, dev, l, n, 5)
             for l, n in ((2048, 2048), (512, 4096))}
+        extras["int8kv_sdpa_prefill_affine_causal"] = {
+            f"L={l} N={n} Hq/Hkv={hq}/{hkv} D={d}": bench_prefill(
+                torch, sparkq, dev, l, n, 5, fmt="affine_u8", hq=hq, hkv=hkv, d=d)
+            for l, n in ((2048, 2048), (512, 4096)) for hq, hkv, d in ((32, 8, 128), (16, 4, 256))}
         extras["kv_append"] = bench_kv_append(torch, sparkq, dev, 10)
         log("fused FFN block and QKV+RoPE")
         extras["layer_m1"] = bench_layer(torch, sparkq, dev, layers, 10)

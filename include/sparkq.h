@@ -233,8 +233,9 @@ int sparkq_kv_quantize_s8(const void* x, int8_t* codes, void* scales,
  * (X/spark_mlx_ext/int8_quantized_sdpa.py:236-245) and its kernel
  * spark_affine_u8_sdpa_prefill (X/spark_mlx_ext/int8_quantized_sdpa_prefill.py:
  * 44-57, X/spark_mlx_ext/_int8_prefill_sources.py:7-154), which serves the
- * MLX affine u8/G32 cache at D=256; this entry point serves the symmetric s8
- * format at D in {64,128,256}. */
+ * MLX affine u8/G32 cache at D=256 (served here by
+ * sparkq_int8kv_sdpa_prefill_affine); this entry point serves the symmetric
+ * s8 format at D in {64,128,256}. */
 int sparkq_int8kv_sdpa_prefill(const void* q, const void* k_codes,
                                const void* k_scales, const void* v_codes,
                                const void* v_scales, void* out, int64_t B,
@@ -242,6 +243,35 @@ int sparkq_int8kv_sdpa_prefill(const void* q, const void* k_codes,
                                int64_t D, int causal, int q_dtype,
                                int out_dtype, float scale,
                                const int64_t* strides, void* stream);
+
+/* INT8-KV GQA prefill attention (L > 1 query tokens per sequence) over the
+ * MLX affine 8-bit cache: q [B,Hq,L,D] contiguous in q_dtype (BF16 or F16),
+ * out [B,Hq,L,D] in out_dtype (q_dtype or F32); packed uint32 codes
+ * [B,Hkv,N,D/4] (dim 4w+j in byte j of word w), scales and biases
+ * [B,Hkv,N,D/group_size] in q_dtype, strides[0..11] as for
+ * sparkq_int8kv_sdpa_decode (packed strides in bytes, multiples of 16).
+ * causal as for sparkq_int8kv_sdpa_prefill. K and V dequantize to q_dtype
+ * as code * scale + bias (one rounding), the softmax weights are rounded to
+ * q_dtype for the PV product; scores, normalizer and output accumulate in
+ * fp32 (the numerics of the reference kernel, except that q is not
+ * pre-multiplied by scale and rounded). Any Hq/Hkv; D in {64,128,256};
+ * group_size in {32,64,128}.
+ * Replaces the L > 1 branch of int8_quantized_sdpa
+ * (X/spark_mlx_ext/int8_quantized_sdpa.py:236-245) and its kernel
+ * spark_affine_u8_sdpa_prefill (X/spark_mlx_ext/int8_quantized_sdpa_prefill.py:
+ * 44-57, X/spark_mlx_ext/_int8_prefill_sources.py:7-154), which the
+ * reference serves at D=256, group size 32 and Hq/Hkv in {1,2,4,8}. */
+int sparkq_int8kv_sdpa_prefill_affine(const void* q, const void* k_packed,
+                                      const void* k_scales,
+                                      const void* k_biases,
+                                      const void* v_packed,
+                                      const void* v_scales,
+                                      const void* v_biases, void* out,
+                                      int64_t B, int64_t Hq, int64_t Hkv,
+                                      int64_t L, int64_t N, int64_t D,
+                                      int group_size, int causal,
+                                      int q_dtype, int out_dtype, float scale,
+                                      const int64_t* strides, void* stream);
 
 /* Quantize-on-append into a preallocated INT8 KV cache (mlx-lm
  * QuantizedKVCache.update_and_fetch as used by spark_mlx_llm/generation.py:

@@ -49,6 +49,11 @@ int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const voi
                         const void* vs, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
                         int64_t N, int64_t D, int causal, int qdt, int odt, float scale,
                         const int64_t* strides, hipStream_t st);
+int int8kv_sdpa_prefill_affine(const void* q, const void* kc, const void* ks, const void* kb,
+                               const void* vc, const void* vs, const void* vb, void* out,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
+                               int64_t D, int G, int causal, int qdt, int odt, float scale,
+                               const int64_t* strides, hipStream_t st);
 int w8a16_linear(const void* x, const int8_t* w, const float* scales, void* y, int64_t M,
                  int64_t N, int64_t K, int xdt, int ydt, hipStream_t st);
 // launchers (layer.hip)
@@ -348,6 +353,48 @@ int sparkq_int8kv_sdpa_prefill(const void* q, const void* k_codes, const void* k
   DEVICE_OK();
   return int8kv_sdpa_prefill(q, k_codes, k_scales, v_codes, v_scales, out, B, Hq, Hkv, L, N, D,
                              causal, q_dtype, out_dtype, scale, strides, (hipStream_t)stream);
+}
+
+int sparkq_int8kv_sdpa_prefill_affine(const void* q, const void* k_packed, const void* k_scales,
+                                      const void* k_biases, const void* v_packed,
+                                      const void* v_scales, const void* v_biases, void* out,
+                                      int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
+                                      int64_t D, int group_size, int causal, int q_dtype,
+                                      int out_dtype, float scale, const int64_t* strides,
+                                      void* stream) {
+  REQUIRE(q && k_packed && k_scales && k_biases && v_packed && v_scales && v_biases && out &&
+              strides,
+          "int8kv_sdpa_prefill_affine: null tensor pointer");
+  REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && L > 0 && N > 0 && D > 0 && Hq % Hkv == 0,
+          "Nonempty inputs and query heads divisible by KV heads required");
+  REQUIRE(B * Hkv <= 65535 && N <= kI32Max && L * Hq <= kI32Max,
+          "int8kv_sdpa_prefill_affine: shape too large");
+  REQUIRE(!causal || L <= N, "int8kv_sdpa_prefill_affine: a causal mask needs L <= N");
+  REQUIRE_SUPPORTED(D == 64 || D == 128 || D == 256,
+                    "int8kv_sdpa_prefill_affine: head dim must be 64, 128 or 256");
+  REQUIRE_SUPPORTED(group_size == 32 || group_size == 64 || group_size == 128,
+                    "Supported affine formats: bits 8, group size 32/64/128");
+  REQUIRE(D % group_size == 0, "int8kv_sdpa_prefill_affine: head dim must be a multiple of group_size");
+  REQUIRE(std::isfinite(scale), "scale must be a finite Python number");
+  REQUIRE_SUPPORTED(is_half_dtype(q_dtype),
+                    "int8kv_sdpa_prefill_affine: queries must be float16 or bfloat16");
+  REQUIRE(out_dtype == q_dtype || out_dtype == SPARKQ_F32,
+          "int8kv_sdpa_prefill_affine: out dtype must equal q dtype or be float32");
+  for (int i : {0, 1, 2, 6, 7, 8})
+    REQUIRE(strides[i] % 16 == 0 && strides[i] >= 0,
+            "int8kv_sdpa_prefill_affine: packed strides must be non-negative multiples of 16 bytes");
+  for (int i : {3, 4, 5, 9, 10, 11})
+    REQUIRE(strides[i] >= 0, "int8kv_sdpa_prefill_affine: negative scale stride");
+  // the per-(sequence, head) token range is addressed with 32-bit offsets
+  REQUIRE(N * std::max(strides[2], strides[8]) <= (int64_t)UINT32_MAX &&
+              N * std::max(strides[5], strides[11]) * 2 <= (int64_t)UINT32_MAX,
+          "int8kv_sdpa_prefill_affine: cache too long for 32-bit offsets");
+  REQUIRE(aligned(q, 16) && aligned(k_packed, 16) && aligned(v_packed, 16),
+          "int8kv_sdpa_prefill_affine: q and packed codes must be 16-byte aligned");
+  DEVICE_OK();
+  return int8kv_sdpa_prefill_affine(q, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases,
+                                    out, B, Hq, Hkv, L, N, D, group_size, causal, q_dtype,
+                                    out_dtype, scale, strides, (hipStream_t)stream);
 }
 
 int sparkq_kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B,

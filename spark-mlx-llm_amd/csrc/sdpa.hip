@@ -21,6 +21,8 @@
 //   kv_quantize_s8_kernel  s8 + fp16-scale quantizer (one wave per row).
 //   sdpa_prefill_kernel    L > 1 queries, s8 + fp16 scale: the MFMA block step
 //                          with (position, head) rows, bottom-right causal.
+//   sdpa_prefill_affine_kernel  L > 1 queries over the MLX affine u8 cache:
+//                          blocks dequantized once per workgroup into LDS.
 //   kv_append_s8_kernel, kv_append_u8_kernel  quantize-on-append into a
 //                          strided cache (s8 + fp16 scale; MLX affine u8).
 #include <algorithm>
@@ -845,6 +847,313 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA prefill attention over the MLX affine u8 cache (L > 1)
+// ---------------------------------------------------------------------------
+// The numerics of spark_affine_u8_sdpa_prefill: K and V dequantize to the
+// query dtype T as T(code * scale + bias) (fp32 fma, one rounding), the
+// softmax weights are rounded to T for the PV product, and the scores, the
+// normalizer and the outputs stay fp32. The query is used as given (the
+// softmax scale multiplies the fp32 scores instead of a rounded q * scale).
+//
+// A workgroup of 4 waves owns 128 consecutive (position, head) rows of one
+// (sequence, KV head), 32 rows per wave, and walks the 32-token blocks up to
+// the last token its last row sees. Each block is dequantized once per
+// workgroup into LDS (double-buffered, one barrier per block): K token-major
+// with the 16-byte chunks of a token row XOR-swizzled by the token, V
+// token-major with its 32-byte runs swizzled. Both products run on the
+// 16x16x32 MFMA in the transposed orientation
+//     S^T (16 tokens x 16 rows) = K (16 tokens x 32 dims) . Q^T
+//     O^T (16 dims x 16 rows)  += V^T (16 dims x 32 tokens) . P^T
+// so that the lane holding row n16's scores for tokens 4g+r and 16+4g+r
+// (lane group g) after QK holds exactly the k-slots of that row in the PV
+// operand: alpha and the normalizer of a row never leave its lane. The V^T
+// operand comes from ds_read_b64_tr_b16 (per 16 lanes a 4-token x 16-dim
+// tile, each lane left with one dim of the 4 tokens).
+template <int D>
+struct AffPrefillLds {
+  static constexpr int ROW = 2 * D;        // bytes of one dequantized token row
+  static constexpr int TILE = 32 * ROW;    // one 32-token K or V block
+  static constexpr int BUF = 2 * TILE;     // K then V
+  static constexpr int BYTES = 2 * BUF;    // double-buffered
+};
+// 16-byte chunk swizzle of K rows and 32-byte run swizzle of V rows: the 16
+// lanes of an MFMA operand read (K: 16 tokens, one chunk; V: 4 tokens x 4
+// lanes per 16 lanes, 8 tokens per half wave) hit distinct banks.
+template <int D>
+__device__ __forceinline__ int aff_kswz(int t) { return D >= 128 ? (t & 15) : ((t >> 1) & 7); }
+template <int D>
+__device__ __forceinline__ int aff_vswz(int t) { return D >= 128 ? (t & 7) : ((t >> 1) & 3); }
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma16_kv(u32x4_t a, u32x4_t b, f32x4_t c);
+template <>
+__device__ __forceinline__ f32x4_t mfma16_kv<BF16>(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4_t mfma16_kv<F16>(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// 16 codes (byte j of word w is code 4w+j) of one group -> 16 values of T in
+// 8 packed words, each T(code * s + b) with one rounding.
+template <typename T>
+__device__ __forceinline__ void dequant_u8x16(u32x4_t c, uint32_t s, uint32_t b, uint32_t o[8]);
+template <>
+__device__ __forceinline__ void dequant_u8x16<BF16>(u32x4_t c, uint32_t s, uint32_t b, uint32_t o[8]) {
+  const float sf = __uint_as_float(s << 16), bf = __uint_as_float(b << 16);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t x = c[w];
+    o[2 * w] = pack_round<BF16>(fmaf((float)(x & 255u), sf, bf), fmaf((float)((x >> 8) & 255u), sf, bf));
+    o[2 * w + 1] =
+        pack_round<BF16>(fmaf((float)((x >> 16) & 255u), sf, bf), fmaf((float)(x >> 24), sf, bf));
+  }
+}
+template <>
+__device__ __forceinline__ void dequant_u8x16<F16>(u32x4_t c, uint32_t s, uint32_t b, uint32_t o[8]) {
+  // a code byte under the fp16 exponent of 1024 reads 1024 + code; the
+  // packed subtract leaves the code exactly, the packed fma rounds once
+  const f16x2_t s2 = __builtin_bit_cast(f16x2_t, (s & 0xFFFFu) * 0x10001u);
+  const f16x2_t b2 = __builtin_bit_cast(f16x2_t, (b & 0xFFFFu) * 0x10001u);
+  const f16x2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t x = c[w];
+    const f16x2_t lo = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) - k1024;
+    const f16x2_t hi = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - k1024;
+    o[2 * w] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(lo, s2, b2));
+    o[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(hi, s2, b2));
+  }
+}
+
+// max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48);
+// every lane ends with the same value
+__device__ __forceinline__ float max_rows4(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_rows4(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D, typename T>
+__global__ __launch_bounds__(256, 1) void sdpa_prefill_affine_kernel(SdpaArgs a) {
+  using LY = AffPrefillLds<D>;
+  constexpr int NK = D / 32;                    // QK k chunks
+  constexpr int NJ = D / 16;                    // PV dim tiles
+  constexpr int PIECES = 2 * D;                 // 16-code pieces of one K (or V) block
+  constexpr int PPT = PIECES >= 256 ? PIECES / 256 : 1;
+  constexpr int NVB = NJ < 8 ? NJ : 8;          // distinct V run offsets of a lane
+  __shared__ __attribute__((aligned(16))) unsigned char smem[LY::BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, grp = lane >> 4;
+  const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
+  const int gqa = a.Hq / a.Hkv;
+  const int R = a.L * gqa;  // (position, head) rows of this KV head
+  // under the causal mask the later (longer) row tiles start first
+  const int tile = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+  const int rw0 = tile * 128;
+  auto last_tok = [&](int rr) -> int {
+    return rr >= R ? -1 : (a.causal ? a.N - a.L + rr / gqa : a.N - 1);
+  };
+  const int t_end = min(a.N, last_tok(min(rw0 + 127, R - 1)) + 1);
+  const int nb = (t_end + 31) / 32;
+
+  // Q^T operand of each 16-row tile: lane (g, n16) holds row n16, dims
+  // 32*kk + 8*g .. +8; rows past R read row R-1 and are masked out
+  u32x4_t qb[2][NK];
+  int lim[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int rr = rw0 + 32 * wave + 16 * rt + n16;
+    lim[rt] = last_tok(rr);
+    const int rq = min(rr, R - 1);
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) +
+                           (((int64_t)b * a.Hq + kh * gqa + rq % gqa) * a.L + rq / gqa) * D;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) qb[rt][kk] = *reinterpret_cast<const u32x4_t*>(qrow + 32 * kk + 8 * grp);
+  }
+
+  // staging: piece p = tid + 256 i is token p / (D/16), codes 16 (p % (D/16)) ..
+  // +16; loads past t_end read zeros through the bounded descriptors
+  const int64_t sbase_k = (int64_t)b * a.ks_b + kh * a.ks_h, sbase_v = (int64_t)b * a.vs_b + kh * a.vs_h;
+  const rsrc_t rk = make_rsrc(a.kc + b * a.kc_b + kh * a.kc_h, (uint32_t)(t_end * a.kc_t));
+  const rsrc_t rv = make_rsrc(a.vc + b * a.vc_b + kh * a.vc_h, (uint32_t)(t_end * a.vc_t));
+  const rsrc_t rks = make_rsrc(reinterpret_cast<const uint16_t*>(a.ks) + sbase_k, (uint32_t)(t_end * a.ks_t * 2));
+  const rsrc_t rkb = make_rsrc(reinterpret_cast<const uint16_t*>(a.kb) + sbase_k, (uint32_t)(t_end * a.ks_t * 2));
+  const rsrc_t rvs = make_rsrc(reinterpret_cast<const uint16_t*>(a.vs) + sbase_v, (uint32_t)(t_end * a.vs_t * 2));
+  const rsrc_t rvb = make_rsrc(reinterpret_cast<const uint16_t*>(a.vb) + sbase_v, (uint32_t)(t_end * a.vs_t * 2));
+  const bool stager = PIECES >= 256 || tid < PIECES;  // wave-uniform
+  u32x4_t kcr[PPT], vcr[PPT];
+  uint32_t ksr[PPT], kbr[PPT], vsr[PPT], vbr[PPT];
+  auto load = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int p = tid + 256 * i, tk = p / (D / 16), jb = p % (D / 16), g = 16 * jb / a.G;
+      kcr[i] = buf_load16(rk, (uint32_t)((t0 + tk) * a.kc_t + 16 * jb));
+      vcr[i] = buf_load16(rv, (uint32_t)((t0 + tk) * a.vc_t + 16 * jb));
+      ksr[i] = buf_load2(rks, (uint32_t)(((t0 + tk) * a.ks_t + g) * 2));
+      kbr[i] = buf_load2(rkb, (uint32_t)(((t0 + tk) * a.ks_t + g) * 2));
+      vsr[i] = buf_load2(rvs, (uint32_t)(((t0 + tk) * a.vs_t + g) * 2));
+      vbr[i] = buf_load2(rvb, (uint32_t)(((t0 + tk) * a.vs_t + g) * 2));
+    }
+  };
+  auto stage = [&](unsigned char* buf) {
+    if (!stager) return;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int p = tid + 256 * i, tk = p / (D / 16), jb = p % (D / 16);
+      uint32_t kw[8], vw[8];
+      dequant_u8x16<T>(kcr[i], ksr[i], kbr[i], kw);
+      dequant_u8x16<T>(vcr[i], vsr[i], vbr[i], vw);
+      unsigned char* kt = buf + tk * LY::ROW;
+      const int ks = aff_kswz<D>(tk);
+      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb) ^ ks) * 16) = u32x4_t{kw[0], kw[1], kw[2], kw[3]};
+      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb + 1) ^ ks) * 16) = u32x4_t{kw[4], kw[5], kw[6], kw[7]};
+      unsigned char* vt = buf + LY::TILE + tk * LY::ROW + (jb ^ aff_vswz<D>(tk)) * 32;
+      *reinterpret_cast<u32x4_t*>(vt) = u32x4_t{vw[0], vw[1], vw[2], vw[3]};
+      *reinterpret_cast<u32x4_t*>(vt + 16) = u32x4_t{vw[4], vw[5], vw[6], vw[7]};
+    }
+  };
+
+  // operand addresses of this lane inside a buffer. K (A of S^T): token
+  // n16 (+16 for the second token tile), chunk 4 kk + g. V (A of O^T): the
+  // lane feeds token 4 g + n16/4 (+16 for slots 4..7), dims 16 j + 4 (n16 % 4)
+  // .. +4; run j = 8 u + v sits at va[v] + 256 u.
+  int ka[NK], va[NVB];
+#pragma unroll
+  for (int kk = 0; kk < NK; ++kk) ka[kk] = n16 * LY::ROW + ((4 * kk + grp) ^ aff_kswz<D>(n16)) * 16;
+  {
+    const int tv = 4 * grp + (n16 >> 2), sw = aff_vswz<D>(tv);
+#pragma unroll
+    for (int v = 0; v < NVB; ++v) va[v] = LY::TILE + tv * LY::ROW + ((v ^ sw) * 32) + 8 * (n16 & 3);
+  }
+
+  float mrun[2] = {kNegInf, kNegInf}, zl[2] = {0.0f, 0.0f};
+  f32x4_t acc[2][NJ];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[rt][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  // One block. The running max of a row moves only when a block's max
+  // exceeds it by more than 8 (log2 units): until then the weights
+  // exp2(s - m) stay below 2^8 and the accumulators are not rescaled, so the
+  // rescale (a wave-uniform branch) runs for few blocks.
+  auto compute = [&](const unsigned char* buf, int t0) {
+    f32x4_t sc[2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) sc[tt][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(buf + ka[kk] + tt * 16 * LY::ROW);
+        sc[tt][0] = mfma16_kv<T>(kf, qb[0][kk], sc[tt][0]);
+        sc[tt][1] = mfma16_kv<T>(kf, qb[1][kk], sc[tt][1]);
+      }
+    u32x4_t pb[2];
+    float alpha[2];
+    bool up[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float s[8];
+      float mb = kNegInf;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        s[i] = sc[i >> 2][rt][i & 3] * a.scale_log2;
+        s[i] = t0 + 16 * (i >> 2) + 4 * grp + (i & 3) <= lim[rt] ? s[i] : kNegInf;
+        mb = fmaxf(mb, s[i]);
+      }
+      mb = max_rows4(mb);
+      up[rt] = mb > mrun[rt] + 8.0f;
+      alpha[rt] = up[rt] ? exp2_guarded(mrun[rt] - mb, mrun[rt] != kNegInf) : 1.0f;
+      mrun[rt] = up[rt] ? mb : mrun[rt];
+      // a row with nothing visible yet keeps m = -inf; its weights are 0
+      const float mu = mrun[rt] == kNegInf ? 0.0f : mrun[rt];
+      float p[8], ps = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(s[i] - mu);
+        ps += p[i];
+      }
+      zl[rt] = fmaf(zl[rt], alpha[rt], ps);
+      pb[rt] = u32x4_t{pack_round<T>(p[0], p[1]), pack_round<T>(p[2], p[3]), pack_round<T>(p[4], p[5]),
+                       pack_round<T>(p[6], p[7])};
+    }
+    if (__builtin_amdgcn_ballot_w64(up[0] || up[1]) != 0) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[rt][j] *= alpha[rt];
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const unsigned char* vp = buf + va[j % NVB] + 256 * (j / NVB);
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4_t*)(vp));
+      const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4_t*)(vp + 16 * LY::ROW));
+      typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+      const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+      const u32x4_t vf = u32x4_t{l2.x, l2.y, h2.x, h2.y};
+      acc[0][j] = mfma16_kv<T>(vf, pb[0], acc[0][j]);
+      acc[1][j] = mfma16_kv<T>(vf, pb[1], acc[1][j]);
+    }
+  };
+  load(0);
+  stage(smem);
+  load(32);
+  __syncthreads();
+  for (int ib = 0; ib < nb; ++ib) {
+    // compute, stage the next block into the other buffer, issue the loads
+    // of the block after it
+    const int t0 = 32 * ib;
+    compute(smem + (ib & 1) * LY::BUF, t0);
+    stage(smem + ((ib + 1) & 1) * LY::BUF);
+    load(t0 + 64);
+    __syncthreads();
+  }
+
+  // O^T lane (g, n16): row n16, dims 16 j + 4 g + r
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const float z = sum_rows4(zl[rt]);
+    const int rr = rw0 + 32 * wave + 16 * rt + n16;
+    if (rr < R) {
+      const int64_t orow = (((int64_t)b * a.Hq + kh * gqa + rr % gqa) * a.L + rr / gqa) * D;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = z > 0.0f ? acc[rt][j][r] / z : 0.0f;
+        const int64_t idx = orow + 16 * j + 4 * grp;
+        if (a.out_dtype == SPARKQ_F32) {
+          *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(a.out) + idx) = f32x4_t{o[0], o[1], o[2], o[3]};
+        } else {
+          typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(a.out) + idx) =
+              u32x2_t{pack_round<T>(o[0], o[1]), pack_round<T>(o[2], o[3])};
+        }
+      }
+    }
+  }
+}
+
 // Log-sum-exp merge of the split partials of one (sequence, query head) row:
 // the split maxima and sums reduce across the workgroup, then thread
 // (d, part) sums the weighted partial outputs of every 256/D-th split with
@@ -1248,6 +1557,62 @@ int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const voi
   else
     launch_prefill_d<256>(a, gqa, grid, st);
   return check_launch("sdpa_prefill_kernel");
+}
+
+template <int D>
+static void launch_prefill_affine_d(const SdpaArgs& a, int qdt, dim3 grid, hipStream_t st) {
+  if (qdt == SPARKQ_BF16)
+    hipLaunchKernelGGL((sdpa_prefill_affine_kernel<D, BF16>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((sdpa_prefill_affine_kernel<D, F16>), grid, dim3(256), 0, st, a);
+}
+
+int int8kv_sdpa_prefill_affine(const void* q, const void* kc, const void* ks, const void* kb,
+                               const void* vc, const void* vs, const void* vb, void* out,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
+                               int64_t D, int G, int causal, int qdt, int odt, float scale,
+                               const int64_t* strides, hipStream_t st) {
+  SdpaArgs a{};
+  a.q = q;
+  a.kc = reinterpret_cast<const uint8_t*>(kc);
+  a.ks = ks;
+  a.kb = kb;
+  a.vc = reinterpret_cast<const uint8_t*>(vc);
+  a.vs = vs;
+  a.vb = vb;
+  a.out = out;
+  a.kc_b = strides[0];
+  a.kc_h = strides[1];
+  a.kc_t = strides[2];
+  a.ks_b = strides[3];
+  a.ks_h = strides[4];
+  a.ks_t = strides[5];
+  a.vc_b = strides[6];
+  a.vc_h = strides[7];
+  a.vc_t = strides[8];
+  a.vs_b = strides[9];
+  a.vs_h = strides[10];
+  a.vs_t = strides[11];
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.N = (int)N;
+  a.G = G;
+  a.L = (int)L;
+  a.causal = causal ? 1 : 0;
+  a.q_dtype = qdt;
+  a.out_dtype = odt;
+  a.S = 1;
+  a.tps = (int)N;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  dim3 grid((unsigned)cdiv(L * (Hq / Hkv), 128), (unsigned)(B * Hkv));
+  if (D == 64)
+    launch_prefill_affine_d<64>(a, qdt, grid, st);
+  else if (D == 128)
+    launch_prefill_affine_d<128>(a, qdt, grid, st);
+  else
+    launch_prefill_affine_d<256>(a, qdt, grid, st);
+  return check_launch("sdpa_prefill_affine_kernel");
 }
 
 template <typename T>

@@ -396,15 +396,58 @@ def kv_quantize_s8(x):
     return codes, sc
 
 
-def _int8_prefill(queries, keys, values, *, scale, causal, fmt, out_dtype, out):
-    """L > 1 queries over the symmetric s8 cache (the prefill branch of
-    X/spark_mlx_ext/int8_quantized_sdpa.py:236-245): tiled QK, online softmax
-    and PV in one launch, bottom-right causal or unmasked."""
+def _int8_prefill_affine(queries, keys, values, *, scale, causal, group_size, bits, out_dtype,
+                         out):
+    """L > 1 queries over the MLX affine 8-bit cache: the prefill branch of
+    X/spark_mlx_ext/int8_quantized_sdpa.py:236-245 and its kernel
+    spark_affine_u8_sdpa_prefill (int8_quantized_sdpa_prefill.py:44-57). K/V
+    dequantize to the query dtype, weights are rounded to it for PV; scores,
+    normalizer and output accumulate in fp32."""
     batch, heads, length, dim = queries.shape
     kv_heads, n = keys[0].shape[1:3]
-    if fmt != KV_S8_F16SCALE:
-        raise ValueError("multi-token INT8-KV attention on gfx950 needs the symmetric int8 cache "
-                         "(codes int8 [B,Hkv,N,D], fp16 scales [B,Hkv,N])")
+    if bits != 8 or group_size not in (32, 64, 128):
+        raise ValueError("Supported affine formats: bits 8, group size 32/64/128")
+    if queries.dtype not in _HALF:
+        raise ValueError("multi-token INT8-KV attention needs float16 or bfloat16 queries")
+    if dim not in (64, 128, 256):
+        raise ValueError("multi-token INT8-KV attention needs a head dim of 64, 128 or 256")
+    if causal and length > n:
+        raise ValueError("a causal mask needs L <= N")
+    for name, (packed, s, b) in (("key", keys), ("value", values)):
+        if (dim % group_size or packed.shape != (batch, kv_heads, n, dim // 4)
+                or s.shape != (batch, kv_heads, n, dim // group_size)
+                or b.shape != s.shape or packed.dtype not in _PACKED
+                or s.dtype != queries.dtype or b.dtype != queries.dtype
+                or s.stride() != b.stride()):
+            raise ValueError(f"Incompatible {name} packed shape, affine metadata or dtype")
+        if packed.stride(3) != 1 or s.stride(3) != 1:
+            raise ValueError(f"{name} innermost axis must be contiguous")
+    (kc, ks, kb), (vc, vs, vb) = keys, values
+    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    out_dtype = queries.dtype if out_dtype is None else out_dtype
+    q = queries.contiguous()
+    y = _out_buffer(out, (batch, heads, length, dim), out_dtype, queries.device)
+    st = (ctypes.c_int64 * 12)(*(_kv_strides(kc, ks, 4) + _kv_strides(vc, vs, 4)))
+    _lib.call("sparkq_int8kv_sdpa_prefill_affine", _ptr(q), _ptr(kc), _ptr(ks), _ptr(kb),
+              _ptr(vc), _ptr(vs), _ptr(vb), _ptr(y), batch, heads, kv_heads, length, n, dim,
+              group_size, 1 if causal else 0, _lib.dtype_code(queries.dtype),
+              _lib.dtype_code(out_dtype), float(scale), st, _lib.stream_handle(queries.device))
+    return y
+
+
+def _int8_prefill(queries, keys, values, *, scale, causal, fmt, out_dtype, out,
+                  group_size=32, bits=8):
+    """L > 1 queries (the prefill branch of
+    X/spark_mlx_ext/int8_quantized_sdpa.py:236-245): tiled QK, online softmax
+    and PV in one launch, bottom-right causal or unmasked. The MLX affine
+    tuple goes to _int8_prefill_affine; this body serves the symmetric s8
+    cache."""
+    if fmt == KV_AFFINE_U8:
+        return _int8_prefill_affine(queries, keys, values, scale=scale, causal=causal,
+                                    group_size=group_size, bits=bits, out_dtype=out_dtype,
+                                    out=out)
+    batch, heads, length, dim = queries.shape
+    kv_heads, n = keys[0].shape[1:3]
     if queries.dtype not in _HALF:
         raise ValueError("multi-token INT8-KV attention needs float16 or bfloat16 queries")
     if causal and length > n:
@@ -571,7 +614,8 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
     fmt = KV_AFFINE_U8 if len(keys) == 3 else KV_S8_F16SCALE
     if length > 1:
         return _int8_prefill(queries, keys, values, scale=scale, causal=mask is not None,
-                             fmt=fmt, out_dtype=out_dtype, out=out)
+                             fmt=fmt, out_dtype=out_dtype, out=out, group_size=group_size,
+                             bits=bits)
     if fmt == KV_AFFINE_U8:
         if bits != 8 or group_size not in (32, 64, 128):
             raise ValueError("Supported affine formats: bits 8, group size 32/64/128")

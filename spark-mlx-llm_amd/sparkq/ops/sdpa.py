@@ -6,7 +6,7 @@ predicate is widened from the reference's D=256/G32 affine format to the
 formats and head sizes the gfx950 decode kernel serves (D in 64/128/256,
 affine G in 32/64/128, or symmetric s8 codes with fp16 per-token scales);
 multi-token queries (the opt-in fused_quantized_sdpa_prefill) are served on
-the symmetric s8 cache.
+both formats with 16-bit queries.
 Unquantized caches go to torch's scaled_dot_product_attention, the analogue
 of the reference's mlx-lm native path.
 """
@@ -54,9 +54,9 @@ def _supports_int8(queries, keys, values, *, cache, mask, prefill=False):
     affine = len(keys) == 3
     dim = queries.shape[-1] if queries.ndim == 4 else -1
     length = queries.shape[-2] if queries.ndim == 4 else 0
-    # multi-token queries (prefill, opt-in as in the reference) run on the
-    # symmetric s8 cache with 16-bit queries and L <= N under a causal mask
-    multi_ok = (prefill and not affine and queries.dtype in (torch.float16, torch.bfloat16)
+    # multi-token queries (prefill, opt-in as in the reference) run on either
+    # cache format with 16-bit queries and L <= N under a causal mask
+    multi_ok = (prefill and queries.dtype in (torch.float16, torch.bfloat16)
                 and (mask is None or length <= keys[0].shape[2]))
     return (
         queries.ndim == 4

@@ -2,8 +2,8 @@
 quantize-on-append (QuantizedKVCache / kv_append) bit-exact with the oracle's
 quantizers for both formats across appends that cross the cache's 256-token
 growth steps, decode attention on the fetched views, and the prefill
-attention (L > 1, bottom-right causal or unmasked) against the fp64 staged
-attention of the reference's _fallback."""
+attention (L > 1, bottom-right causal or unmasked) for both formats against
+the fp64 staged attention of the reference's _fallback."""
 
 import math
 
@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle as o
-from helpers import check_fp32, check_rounded16, down16, up16
+from helpers import check_fp32, check_rounded16, down16, max_abs, rel_l2, up16
 
 pytestmark = pytest.mark.gpu
 
@@ -140,3 +140,104 @@ def test_prefill_last_row_is_decode(gpu):
     for i in (0, length // 2, length - 1):
         mean = vd[:, :, : n - length + i + 1].mean(axis=2)
         assert np.allclose(y[:, :, i], np.repeat(mean, hq // hkv, axis=1), rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------------------
+# prefill over the MLX affine 8-bit cache
+# ---------------------------------------------------------------------------
+def _affine_cache(dev, b, hkv, n, d, g, seed, qdtype):
+    k = o.randn(seed, 61, b * hkv * n * d).reshape(b, hkv, n, d)
+    v = o.randn(seed, 62, b * hkv * n * d).reshape(b, hkv, n, d)
+    kq = o.kv_quantize_affine_u8(k, g, qdtype)
+    vq = o.kv_quantize_affine_u8(v, g, qdtype)
+
+    def dev_tuple(t):
+        packed, s, bias = t
+        return (torch.from_numpy(packed.view(np.int32)).to(dev), up16(s, qdtype, dev),
+                up16(bias, qdtype, dev))
+
+    kd = o.kv_dequantize_affine_u8(*kq, g, qdtype)
+    vd = o.kv_dequantize_affine_u8(*vq, g, qdtype)
+    return dev_tuple(kq), dev_tuple(vq), kd, vd
+
+
+def _row_rel(out, ref):
+    num = np.linalg.norm((out - ref).reshape(-1, ref.shape[-1]), axis=1)
+    den = np.maximum(np.linalg.norm(ref.reshape(-1, ref.shape[-1]), axis=1), 1e-30)
+    return float(np.max(num / den))
+
+
+# K and V dequantized to the query dtype and the weights rounded to it for
+# PV (the reference kernel's rounding points): with bf16 that is ~2^-9 per
+# element, ~2.5e-3 relative L2 on N(0,1) data; fp16 ~2^-12
+_AFF_TOL = {o.BF16: (5e-3, 3e-2), o.F16: (8e-4, 5e-3)}
+
+
+@pytest.mark.parametrize("b,hq,hkv,length,n,d,g,causal,qdtype", [
+    (1, 16, 4, 64, 64, 256, 32, True, o.BF16),
+    (1, 16, 4, 200, 333, 256, 32, True, o.BF16),
+    (2, 8, 2, 37, 100, 128, 64, True, o.F16),
+    (1, 32, 8, 130, 300, 128, 32, False, o.BF16),
+    (1, 4, 4, 45, 45, 64, 32, True, o.BF16),
+    (1, 6, 2, 70, 96, 128, 128, True, o.F16),
+    (2, 8, 1, 300, 300, 256, 64, True, o.F16),
+])
+def test_prefill_affine_matches_oracle(gpu, b, hq, hkv, length, n, d, g, causal, qdtype):
+    import sparkq
+
+    seed = length + n + d
+    keys, vals, kd, vd = _affine_cache(gpu, b, hkv, n, d, g, seed, qdtype)
+    q16 = _x16(seed, 60, (b, hq, length, d), qdtype)
+    qt = up16(q16, qdtype, gpu)
+    scale = 1.0 / math.sqrt(d)
+    mask = "causal" if causal else None
+    print(f"[prefill_affine] b={b} hq={hq} hkv={hkv} L={length} N={n} D={d} G={g} "
+          f"causal={causal} q={'bf16' if qdtype == o.BF16 else 'f16'}", flush=True)
+    y32 = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=scale, group_size=g, mask=mask,
+                                     out_dtype=torch.float32)
+    y16 = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=scale, group_size=g, mask=mask)
+    torch.cuda.synchronize()
+    ref = o.sdpa_prefill(o.bits_to_f32(q16, qdtype), kd, vd, scale, causal)
+    out = y32.cpu().numpy().astype(np.float64)
+    rl, rr, ma = rel_l2(out, ref), _row_rel(out, ref), max_abs(out, ref)
+    print(f"  rel_l2={rl:.3e} worst_row={rr:.3e} max_abs={ma:.3e}")
+    tol_l2, tol_row = _AFF_TOL[qdtype]
+    assert rl <= tol_l2 and rr <= tol_row and ma <= 2e-2
+    # the 16-bit output is the fp32 result rounded once
+    assert np.array_equal(down16(y16), o.round16(y32.cpu().numpy(), qdtype))
+
+
+@pytest.mark.parametrize("d,g,qdtype", [(256, 32, o.BF16), (128, 64, o.F16), (64, 32, o.BF16)])
+def test_prefill_affine_identical_keys_mean_of_values(gpu, d, g, qdtype):
+    """Identical keys give every visible token the weight 1 exactly, so row i
+    returns the mean of the dequantized (query-dtype) V over its N-L+i+1
+    visible tokens: pins the V operand layout and the causal limits."""
+    import sparkq
+
+    b, hq, hkv, length, n = 1, 8, 2, 40, 77
+    keys, vals, kd, vd = _affine_cache(gpu, b, hkv, n, d, g, 7, qdtype)
+    keys1 = tuple(t[:, :, :1].expand(-1, -1, n, -1).contiguous() for t in keys)
+    q16 = _x16(7, 63, (b, hq, length, d), qdtype)
+    y = sparkq.int8_quantized_sdpa(up16(q16, qdtype, gpu), keys1, vals, scale=0.1, group_size=g,
+                                   mask="causal", out_dtype=torch.float32).cpu().numpy()
+    v16 = o.bits_to_f32(o.round16(vd, qdtype), qdtype).astype(np.float64)
+    for i in range(length):
+        mean = v16[:, :, : n - length + i + 1].mean(axis=2)
+        assert np.allclose(y[:, :, i], np.repeat(mean, hq // hkv, axis=1), rtol=1e-5, atol=1e-6), i
+
+
+def test_prefill_affine_dispatch(gpu):
+    """dispatch_sdpa routes multi-token queries over the affine tuple to the
+    fused kernel when fused_quantized_sdpa_prefill is set."""
+    import sparkq
+    from sparkq.ops import SDPAConfig, dispatch_sdpa
+
+    class Cache:
+        bits, group_size = 8, 32
+
+    keys, vals, _, _ = _affine_cache(gpu, 1, 4, 96, 256, 32, 9, o.BF16)
+    qt = up16(_x16(9, 64, (1, 16, 50, 256)), o.BF16, gpu)
+    y = dispatch_sdpa(qt, keys, vals, cache=Cache(), scale=0.0625, mask="causal",
+                      config=SDPAConfig(fused_quantized_sdpa_prefill=True))
+    ref = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=0.0625, mask="causal")
+    assert torch.equal(y, ref)

@@ -110,8 +110,8 @@ def test_sdpa_dispatch_validation():
         ext.int8_quantized_sdpa(q, keys, keys, scale=0.1, single_pass_max_length=-1)
     with pytest.raises(ValueError, match="finite"):
         ext.int8_quantized_sdpa(q, keys, keys, scale=float("nan"))
-    # multi-token queries: 16-bit queries over the symmetric cache, L <= N
-    # under a causal mask; the affine tuple serves single-token decode only
+    # multi-token queries: 16-bit queries, L <= N under a causal mask; the
+    # affine tuple needs bits 8, G in 32/64/128 and metadata in the query dtype
     with pytest.raises(ValueError, match="float16 or bfloat16 queries"):
         ext.int8_quantized_sdpa(torch.zeros((1, 8, 2, 128)), keys, keys, scale=0.1)
     q2 = torch.zeros((1, 8, 32, 128), dtype=torch.bfloat16)
@@ -119,7 +119,14 @@ def test_sdpa_dispatch_validation():
         ext.int8_quantized_sdpa(q2, keys, keys, scale=0.1, mask="causal")
     aff = (torch.zeros((1, 2, 16, 32), dtype=torch.int32), torch.ones((1, 2, 16, 4), dtype=torch.bfloat16),
            torch.zeros((1, 2, 16, 4), dtype=torch.bfloat16))
-    with pytest.raises(ValueError, match="symmetric int8 cache"):
+    with pytest.raises(ValueError, match="group size"):
+        ext.int8_quantized_sdpa(q2[:, :, :2], aff, aff, scale=0.1, group_size=16)
+    with pytest.raises(ValueError, match="Incompatible key packed"):
+        ext.int8_quantized_sdpa(q2[:, :, :2], aff, aff, scale=0.1, group_size=64)
+    with pytest.raises(ValueError, match="head dim"):
+        ext.int8_quantized_sdpa(torch.zeros((1, 8, 2, 96), dtype=torch.bfloat16),
+                                aff, aff, scale=0.1)
+    with pytest.raises(ValueError, match="GPU"):
         ext.int8_quantized_sdpa(q2[:, :, :2], aff, aff, scale=0.1)
     # unquantized caches take torch's attention
     out = dispatch_sdpa(torch.ones((1, 8, 1, 64)), torch.ones((1, 2, 5, 64)),
