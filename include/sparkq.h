@@ -255,7 +255,12 @@ int sparkq_int8kv_sdpa_prefill(const void* q, const void* k_codes,
  * q_dtype for the PV product; scores, normalizer and output accumulate in
  * fp32 (the numerics of the reference kernel, except that q is not
  * pre-multiplied by scale and rounded). Any Hq/Hkv; D in {64,128,256};
- * group_size in {32,64,128}.
+ * group_size in {32,64,128}. When the grid of 128-row tiles is short of the
+ * chip, each tile's context is split over several workgroups merged in the
+ * same launch: that needs the workspace of
+ * sparkq_int8kv_sdpa_prefill_affine_workspace_bytes (0 when no split; tile
+ * counters in its first 16384 bytes, zero before the first call and left
+ * zero, then partials). Calls that share a workspace must not overlap.
  * Replaces the L > 1 branch of int8_quantized_sdpa
  * (X/spark_mlx_ext/int8_quantized_sdpa.py:236-245) and its kernel
  * spark_affine_u8_sdpa_prefill (X/spark_mlx_ext/int8_quantized_sdpa_prefill.py:
@@ -271,7 +276,12 @@ int sparkq_int8kv_sdpa_prefill_affine(const void* q, const void* k_packed,
                                       int64_t L, int64_t N, int64_t D,
                                       int group_size, int causal,
                                       int q_dtype, int out_dtype, float scale,
-                                      const int64_t* strides, void* stream);
+                                      const int64_t* strides, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+size_t sparkq_int8kv_sdpa_prefill_affine_workspace_bytes(int64_t B, int64_t Hq,
+                                                         int64_t Hkv, int64_t L,
+                                                         int64_t N, int64_t D,
+                                                         int causal);
 
 /* Quantize-on-append into a preallocated INT8 KV cache (mlx-lm
  * QuantizedKVCache.update_and_fetch as used by spark_mlx_llm/generation.py:

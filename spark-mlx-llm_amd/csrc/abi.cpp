@@ -49,11 +49,13 @@ int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const voi
                         const void* vs, void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
                         int64_t N, int64_t D, int causal, int qdt, int odt, float scale,
                         const int64_t* strides, hipStream_t st);
+size_t int8kv_sdpa_prefill_affine_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                                            int64_t D, int causal);
 int int8kv_sdpa_prefill_affine(const void* q, const void* kc, const void* ks, const void* kb,
                                const void* vc, const void* vs, const void* vb, void* out,
                                int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
                                int64_t D, int G, int causal, int qdt, int odt, float scale,
-                               const int64_t* strides, hipStream_t st);
+                               const int64_t* strides, void* ws, size_t wsb, hipStream_t st);
 int w8a16_linear(const void* x, const int8_t* w, const float* scales, void* y, int64_t M,
                  int64_t N, int64_t K, int xdt, int ydt, hipStream_t st);
 // launchers (layer.hip)
@@ -361,7 +363,7 @@ int sparkq_int8kv_sdpa_prefill_affine(const void* q, const void* k_packed, const
                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
                                       int64_t D, int group_size, int causal, int q_dtype,
                                       int out_dtype, float scale, const int64_t* strides,
-                                      void* stream) {
+                                      void* workspace, size_t workspace_bytes, void* stream) {
   REQUIRE(q && k_packed && k_scales && k_biases && v_packed && v_scales && v_biases && out &&
               strides,
           "int8kv_sdpa_prefill_affine: null tensor pointer");
@@ -394,7 +396,16 @@ int sparkq_int8kv_sdpa_prefill_affine(const void* q, const void* k_packed, const
   DEVICE_OK();
   return int8kv_sdpa_prefill_affine(q, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases,
                                     out, B, Hq, Hkv, L, N, D, group_size, causal, q_dtype,
-                                    out_dtype, scale, strides, (hipStream_t)stream);
+                                    out_dtype, scale, strides, workspace, workspace_bytes,
+                                    (hipStream_t)stream);
+}
+
+size_t sparkq_int8kv_sdpa_prefill_affine_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv,
+                                                         int64_t L, int64_t N, int64_t D,
+                                                         int causal) {
+  (void)N;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || D <= 0 || Hq % Hkv) return 0;
+  return int8kv_sdpa_prefill_affine_workspace(B, Hq, Hkv, L, D, causal);
 }
 
 int sparkq_kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B,

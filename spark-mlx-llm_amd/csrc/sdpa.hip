@@ -26,6 +26,7 @@
 //   kv_append_s8_kernel, kv_append_u8_kernel  quantize-on-append into a
 //                          strided cache (s8 + fp16 scale; MLX affine u8).
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -53,6 +54,7 @@ struct SdpaArgs {
   int q_dtype, out_dtype;
   int tps, S;
   int L, causal;     // prefill: query length, bottom-right causal mask
+  int pair;          // affine prefill: each workgroup takes row tiles T-1-x and x
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -945,8 +947,8 @@ __device__ __forceinline__ float sum_rows4(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int D, typename T>
-__global__ __launch_bounds__(256, 1) void sdpa_prefill_affine_kernel(SdpaArgs a) {
+template <int D, typename T, bool SPLIT>
+__global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void sdpa_prefill_affine_kernel(SdpaArgs a) {
   using LY = AffPrefillLds<D>;
   constexpr int NK = D / 32;                    // QK k chunks
   constexpr int NJ = D / 16;                    // PV dim tiles
@@ -961,14 +963,27 @@ __global__ __launch_bounds__(256, 1) void sdpa_prefill_affine_kernel(SdpaArgs a)
   const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
   const int gqa = a.Hq / a.Hkv;
   const int R = a.L * gqa;  // (position, head) rows of this KV head
-  // under the causal mask the later (longer) row tiles start first
-  const int tile = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+  // Row tiles of 128. Under the causal mask tile t walks ~t+1 times the
+  // blocks of tile 0: with pairing (when the paired grid still covers the
+  // chip) workgroup x takes tiles T-1-x and x in turn, so every workgroup
+  // walks about the same number of blocks; otherwise the longer tiles start
+  // first.
+  // With a context split (S > 1, no pairing) workgroup x takes chunk x % S
+  // of the blocks of tile x / S and the last chunk to finish merges.
+  const int ntiles = (R + 127) / 128;
+  const int S = SPLIT ? a.S : 1;
+  const int xt = S > 1 ? (int)blockIdx.x / S : (int)blockIdx.x, chunk = (int)blockIdx.x - xt * S;
+  const int npass = D <= 128 && a.pair && ntiles - 1 - xt != xt ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+  const int tile = D <= 128 && a.pair ? (pass == 0 ? ntiles - 1 - xt : xt)
+                                      : (a.causal ? ntiles - 1 - xt : xt);
   const int rw0 = tile * 128;
   auto last_tok = [&](int rr) -> int {
     return rr >= R ? -1 : (a.causal ? a.N - a.L + rr / gqa : a.N - 1);
   };
   const int t_end = min(a.N, last_tok(min(rw0 + 127, R - 1)) + 1);
-  const int nb = (t_end + 31) / 32;
+  const int nb_all = (t_end + 31) / 32;
+  const int ib0 = (int)((int64_t)chunk * nb_all / S), ib1 = (int)((int64_t)(chunk + 1) * nb_all / S);
 
   // Q^T operand of each 16-row tile: lane (g, n16) holds row n16, dims
   // 32*kk + 8*g .. +8; rows past R read row R-1 and are masked out
@@ -1009,21 +1024,47 @@ __global__ __launch_bounds__(256, 1) void sdpa_prefill_affine_kernel(SdpaArgs a)
       vbr[i] = buf_load2(rvb, (uint32_t)(((t0 + tk) * a.vs_t + g) * 2));
     }
   };
+  // D <= 128: the next block dequantized in registers (interleaved with the
+  // PV product), then written to the other buffer
+  uint32_t kw[PPT][8], vw[PPT][8];
+  auto dequant = [&]() {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      dequant_u8x16<T>(kcr[i], ksr[i], kbr[i], kw[i]);
+      dequant_u8x16<T>(vcr[i], vsr[i], vbr[i], vw[i]);
+    }
+  };
+  // dequant and write in one pass, each piece's values short-lived
   auto stage = [&](unsigned char* buf) {
     if (!stager) return;
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int p = tid + 256 * i, tk = p / (D / 16), jb = p % (D / 16);
-      uint32_t kw[8], vw[8];
-      dequant_u8x16<T>(kcr[i], ksr[i], kbr[i], kw);
-      dequant_u8x16<T>(vcr[i], vsr[i], vbr[i], vw);
+      uint32_t kq[8], vq[8];
+      dequant_u8x16<T>(kcr[i], ksr[i], kbr[i], kq);
+      dequant_u8x16<T>(vcr[i], vsr[i], vbr[i], vq);
       unsigned char* kt = buf + tk * LY::ROW;
       const int ks = aff_kswz<D>(tk);
-      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb) ^ ks) * 16) = u32x4_t{kw[0], kw[1], kw[2], kw[3]};
-      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb + 1) ^ ks) * 16) = u32x4_t{kw[4], kw[5], kw[6], kw[7]};
+      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb) ^ ks) * 16) = u32x4_t{kq[0], kq[1], kq[2], kq[3]};
+      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb + 1) ^ ks) * 16) = u32x4_t{kq[4], kq[5], kq[6], kq[7]};
       unsigned char* vt = buf + LY::TILE + tk * LY::ROW + (jb ^ aff_vswz<D>(tk)) * 32;
-      *reinterpret_cast<u32x4_t*>(vt) = u32x4_t{vw[0], vw[1], vw[2], vw[3]};
-      *reinterpret_cast<u32x4_t*>(vt + 16) = u32x4_t{vw[4], vw[5], vw[6], vw[7]};
+      *reinterpret_cast<u32x4_t*>(vt) = u32x4_t{vq[0], vq[1], vq[2], vq[3]};
+      *reinterpret_cast<u32x4_t*>(vt + 16) = u32x4_t{vq[4], vq[5], vq[6], vq[7]};
+    }
+  };
+  auto stage_write = [&](unsigned char* buf) {
+    if (!stager) return;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int p = tid + 256 * i, tk = p / (D / 16), jb = p % (D / 16);
+      unsigned char* kt = buf + tk * LY::ROW;
+      const int ks = aff_kswz<D>(tk);
+      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb) ^ ks) * 16) = u32x4_t{kw[i][0], kw[i][1], kw[i][2], kw[i][3]};
+      *reinterpret_cast<u32x4_t*>(kt + ((2 * jb + 1) ^ ks) * 16) =
+          u32x4_t{kw[i][4], kw[i][5], kw[i][6], kw[i][7]};
+      unsigned char* vt = buf + LY::TILE + tk * LY::ROW + (jb ^ aff_vswz<D>(tk)) * 32;
+      *reinterpret_cast<u32x4_t*>(vt) = u32x4_t{vw[i][0], vw[i][1], vw[i][2], vw[i][3]};
+      *reinterpret_cast<u32x4_t*>(vt + 16) = u32x4_t{vw[i][4], vw[i][5], vw[i][6], vw[i][7]};
     }
   };
 
@@ -1101,6 +1142,9 @@ __global__ __launch_bounds__(256, 1) void sdpa_prefill_affine_kernel(SdpaArgs a)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[rt][j] *= alpha[rt];
     }
+    // the next block's dequant (VALU) goes between the PV MFMAs (at D=256
+    // the registers it holds cost more than the overlap gains)
+    if (D <= 128) dequant();
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const unsigned char* vp = buf + va[j % NVB] + 256 * (j / NVB);
@@ -1114,25 +1158,89 @@ __global__ __launch_bounds__(256, 1) void sdpa_prefill_affine_kernel(SdpaArgs a)
       acc[0][j] = mfma16_kv<T>(vf, pb[0], acc[0][j]);
       acc[1][j] = mfma16_kv<T>(vf, pb[1], acc[1][j]);
     }
+    if (D <= 128) {
+      constexpr int VPM = (PPT * 80) / (2 * NJ);  // dequant VALU per PV MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+        if (j + 2 < NJ) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+    }
   };
-  load(0);
+  load(32 * ib0);
   stage(smem);
-  load(32);
+  load(32 * ib0 + 32);
   __syncthreads();
-  for (int ib = 0; ib < nb; ++ib) {
-    // compute, stage the next block into the other buffer, issue the loads
-    // of the block after it
-    const int t0 = 32 * ib;
-    compute(smem + (ib & 1) * LY::BUF, t0);
-    stage(smem + ((ib + 1) & 1) * LY::BUF);
+  for (int ib = ib0; ib < ib1; ++ib) {
+    // compute (with the next block's dequant), write the next block into
+    // the other buffer, issue the loads of the block after it
+    const int t0 = 32 * ib, cur = (ib - ib0) & 1;
+    compute(smem + cur * LY::BUF, t0);
+    if (D > 128)
+      stage(smem + (cur ^ 1) * LY::BUF);
+    else
+      stage_write(smem + (cur ^ 1) * LY::BUF);
     load(t0 + 64);
     __syncthreads();
+  }
+
+  float zrow[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) zrow[rt] = sum_rows4(zl[rt]);
+  if (SPLIT) {
+    // store this chunk's (max, sum, acc) of its 128 rows, then the last
+    // chunk of the tile to arrive combines all S in chunk order
+    const int64_t tg = ((int64_t)b * a.Hkv + kh) * ntiles + tile;
+    const int64_t pbase = tg * S;
+    constexpr int NV = 2 * NJ * 4;  // accumulators per thread
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      if (grp == 0) {
+        const int64_t ri = (pbase + chunk) * 128 + 32 * wave + 16 * rt + n16;
+        splitk_store(a.pm + ri, mrun[rt]);
+        splitk_store(a.pz + ri, zrow[rt]);
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          splitk_store(a.pacc + ((pbase + chunk) * NV + (rt * NJ + j) * 4 + r) * 256 + tid, acc[rt][j][r]);
+    }
+    __shared__ int s_last;
+    if (!splitk_arrive(a.counters + tg, S, &s_last)) continue;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int64_t rrow = 32 * wave + 16 * rt + n16;
+      float mm = kNegInf;
+      for (int c = 0; c < S; ++c) mm = fmaxf(mm, splitk_load(a.pm + (pbase + c) * 128 + rrow));
+      float z = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[rt][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int c = 0; c < S; ++c) {
+        const float mc = splitk_load(a.pm + (pbase + c) * 128 + rrow);
+        const float w = exp2_guarded(mc - mm, mc != kNegInf);
+        z = fmaf(splitk_load(a.pz + (pbase + c) * 128 + rrow), w, z);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[rt][j][r] =
+                fmaf(splitk_load(a.pacc + ((pbase + c) * NV + (rt * NJ + j) * 4 + r) * 256 + tid), w,
+                     acc[rt][j][r]);
+      }
+      zrow[rt] = z;
+    }
+    splitk_reset(a.counters + tg);
   }
 
   // O^T lane (g, n16): row n16, dims 16 j + 4 g + r
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const float z = sum_rows4(zl[rt]);
+    const float z = zrow[rt];
     const int rr = rw0 + 32 * wave + 16 * rt + n16;
     if (rr < R) {
       const int64_t orow = (((int64_t)b * a.Hq + kh * gqa + rr % gqa) * a.L + rr / gqa) * D;
@@ -1152,6 +1260,7 @@ __global__ __launch_bounds__(256, 1) void sdpa_prefill_affine_kernel(SdpaArgs a)
       }
     }
   }
+  }  // pass
 }
 
 // Log-sum-exp merge of the split partials of one (sequence, query head) row:
@@ -1559,19 +1668,63 @@ int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const voi
   return check_launch("sdpa_prefill_kernel");
 }
 
+template <int D, bool SPLIT>
+static void launch_prefill_affine_s(const SdpaArgs& a, int qdt, dim3 grid, hipStream_t st) {
+  if (qdt == SPARKQ_BF16)
+    hipLaunchKernelGGL((sdpa_prefill_affine_kernel<D, BF16, SPLIT>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((sdpa_prefill_affine_kernel<D, F16, SPLIT>), grid, dim3(256), 0, st, a);
+}
 template <int D>
 static void launch_prefill_affine_d(const SdpaArgs& a, int qdt, dim3 grid, hipStream_t st) {
-  if (qdt == SPARKQ_BF16)
-    hipLaunchKernelGGL((sdpa_prefill_affine_kernel<D, BF16>), grid, dim3(256), 0, st, a);
+  if (a.S > 1)
+    launch_prefill_affine_s<D, true>(a, qdt, grid, st);
   else
-    hipLaunchKernelGGL((sdpa_prefill_affine_kernel<D, F16>), grid, dim3(256), 0, st, a);
+    launch_prefill_affine_s<D, false>(a, qdt, grid, st);
+}
+
+// Launch plan of the affine prefill: causal row tiles are paired when the
+// paired grid still has a workgroup for every CU (D <= 128); a grid short of
+// one workgroup per CU splits each tile's blocks over S <= 8 workgroups,
+// merged in the same launch through the workspace (tile counters, then the
+// per-chunk maxima, sums and accumulators).
+struct AffPrefillPlan {
+  int pair, S;
+  int64_t ntiles_all;
+  size_t bytes;
+};
+static AffPrefillPlan plan_prefill_affine(int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                                          int64_t D, int causal) {
+  AffPrefillPlan p{};
+  const int64_t ntiles = cdiv(L * (Hq / Hkv), 128);
+  p.ntiles_all = ntiles * B * Hkv;
+  p.pair = D <= 128 && causal && ntiles >= 2 && cdiv(ntiles, 2) * B * Hkv >= 256 ? 1 : 0;
+  p.S = 1;
+  static const int64_t target = [] {
+    const char* e = std::getenv("SPARKQ_PREFILL_SPLIT_TARGET");
+    return e ? std::max(1, std::atoi(e)) : 256;
+  }();
+  if (!p.pair && p.ntiles_all < target && p.ntiles_all <= kCounterBytes / 4)
+    p.S = (int)std::min<int64_t>(8, cdiv(target, p.ntiles_all));
+  p.bytes = p.S > 1 ? kCounterBytes + round_up((size_t)p.ntiles_all * p.S * 128 * 4, 256) * 2 +
+                          (size_t)p.ntiles_all * p.S * 128 * D * 4
+                    : 0;
+  return p;
+}
+
+size_t int8kv_sdpa_prefill_affine_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                                            int64_t D, int causal) {
+  return plan_prefill_affine(B, Hq, Hkv, L, D, causal).bytes;
 }
 
 int int8kv_sdpa_prefill_affine(const void* q, const void* kc, const void* ks, const void* kb,
                                const void* vc, const void* vs, const void* vb, void* out,
                                int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
                                int64_t D, int G, int causal, int qdt, int odt, float scale,
-                               const int64_t* strides, hipStream_t st) {
+                               const int64_t* strides, void* ws, size_t wsb, hipStream_t st) {
+  const AffPrefillPlan plan = plan_prefill_affine(B, Hq, Hkv, L, D, causal);
+  if (plan.S > 1 && (ws == nullptr || wsb < plan.bytes))
+    return set_error(SPARKQ_ERR_WORKSPACE, "int8kv_sdpa_prefill_affine: workspace too small");
   SdpaArgs a{};
   a.q = q;
   a.kc = reinterpret_cast<const uint8_t*>(kc);
@@ -1602,10 +1755,20 @@ int int8kv_sdpa_prefill_affine(const void* q, const void* kc, const void* ks, co
   a.causal = causal ? 1 : 0;
   a.q_dtype = qdt;
   a.out_dtype = odt;
-  a.S = 1;
+  a.S = plan.S;
+  a.pair = plan.pair;
   a.tps = (int)N;
   a.scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid((unsigned)cdiv(L * (Hq / Hkv), 128), (unsigned)(B * Hkv));
+  if (plan.S > 1) {
+    unsigned char* base = reinterpret_cast<unsigned char*>(ws);
+    const size_t rows = round_up((size_t)plan.ntiles_all * plan.S * 128 * 4, 256);
+    a.counters = reinterpret_cast<unsigned*>(base);
+    a.pm = reinterpret_cast<float*>(base + kCounterBytes);
+    a.pz = reinterpret_cast<float*>(base + kCounterBytes + rows);
+    a.pacc = reinterpret_cast<float*>(base + kCounterBytes + 2 * rows);
+  }
+  const int64_t ntiles = cdiv(L * (Hq / Hkv), 128);
+  dim3 grid((unsigned)(plan.pair ? cdiv(ntiles, 2) : ntiles * plan.S), (unsigned)(B * Hkv));
   if (D == 64)
     launch_prefill_affine_d<64>(a, qdt, grid, st);
   else if (D == 128)

@@ -53,7 +53,8 @@ SIGNATURES = {
     "sparkq_int8kv_sdpa_prefill": (I, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I, I,
                                        I, F, P, P]),
     "sparkq_int8kv_sdpa_prefill_affine": (I, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64,
-                                              I64, I, I, I, I, F, P, P]),
+                                              I64, I, I, I, I, F, P, P, SZ, P]),
+    "sparkq_int8kv_sdpa_prefill_affine_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I64, I]),
     "sparkq_ffn_workspace_bytes": (SZ, [I64, I64, I64, I]),
     "sparkq_ffn": (I, [P, P, P, F, P, P, P, P, P, P, P, P, P, P, I64, I64, I64, I, I, P, SZ, P]),
     "sparkq_qkv_rope_workspace_bytes": (SZ, [I64, I, I, I, I]),

@@ -428,10 +428,15 @@ def _int8_prefill_affine(queries, keys, values, *, scale, causal, group_size, bi
     q = queries.contiguous()
     y = _out_buffer(out, (batch, heads, length, dim), out_dtype, queries.device)
     st = (ctypes.c_int64 * 12)(*(_kv_strides(kc, ks, 4) + _kv_strides(vc, vs, 4)))
+    c = 1 if causal else 0
+    ws, wsb = _lib.workspace(queries.device,
+                             _lib.lib().sparkq_int8kv_sdpa_prefill_affine_workspace_bytes(
+                                 batch, heads, kv_heads, length, n, dim, c),
+                             "sdpa_prefill")
     _lib.call("sparkq_int8kv_sdpa_prefill_affine", _ptr(q), _ptr(kc), _ptr(ks), _ptr(kb),
               _ptr(vc), _ptr(vs), _ptr(vb), _ptr(y), batch, heads, kv_heads, length, n, dim,
-              group_size, 1 if causal else 0, _lib.dtype_code(queries.dtype),
-              _lib.dtype_code(out_dtype), float(scale), st, _lib.stream_handle(queries.device))
+              group_size, c, _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype),
+              float(scale), st, ws, wsb, _lib.stream_handle(queries.device))
     return y
 
 

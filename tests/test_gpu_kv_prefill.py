@@ -181,6 +181,9 @@ _AFF_TOL = {o.BF16: (5e-3, 3e-2), o.F16: (8e-4, 5e-3)}
     (1, 4, 4, 45, 45, 64, 32, True, o.BF16),
     (1, 6, 2, 70, 96, 128, 128, True, o.F16),
     (2, 8, 1, 300, 300, 256, 64, True, o.F16),
+    # 512 row tiles: paired causal tiles, and the unsplit unmasked grid
+    (4, 32, 8, 512, 512, 64, 32, True, o.BF16),
+    (4, 32, 8, 512, 600, 64, 64, False, o.BF16),
 ])
 def test_prefill_affine_matches_oracle(gpu, b, hq, hkv, length, n, d, g, causal, qdtype):
     import sparkq
@@ -224,6 +227,28 @@ def test_prefill_affine_identical_keys_mean_of_values(gpu, d, g, qdtype):
     for i in range(length):
         mean = v16[:, :, : n - length + i + 1].mean(axis=2)
         assert np.allclose(y[:, :, i], np.repeat(mean, hq // hkv, axis=1), rtol=1e-5, atol=1e-6), i
+
+
+@pytest.mark.parametrize("b,hq,hkv,length,n,d", [(1, 16, 4, 300, 900, 256), (1, 32, 8, 70, 2000, 128)])
+def test_prefill_affine_split_repeats(gpu, b, hq, hkv, length, n, d):
+    """Short prompts over long caches split each row tile's context over
+    several workgroups, merged in the same launch by the last to finish: the
+    result matches the oracle and repeats bit for bit (the tile counters are
+    left zero for the next call)."""
+    import sparkq
+
+    lib = sparkq._lib.lib()
+    assert lib.sparkq_int8kv_sdpa_prefill_affine_workspace_bytes(b, hq, hkv, length, n, d, 1) > 0
+    keys, vals, kd, vd = _affine_cache(gpu, b, hkv, n, d, 32, 11, o.BF16)
+    q16 = _x16(11, 65, (b, hq, length, d))
+    qt = up16(q16, o.BF16, gpu)
+    y1 = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=0.08, mask="causal", out_dtype=torch.float32)
+    y2 = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=0.08, mask="causal", out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    ref = o.sdpa_prefill(o.bits_to_f32(q16, o.BF16), kd, vd, 0.08, True)
+    out = y1.cpu().numpy().astype(np.float64)
+    assert rel_l2(out, ref) <= _AFF_TOL[o.BF16][0] and _row_rel(out, ref) <= _AFF_TOL[o.BF16][1]
 
 
 def test_prefill_affine_dispatch(gpu):
