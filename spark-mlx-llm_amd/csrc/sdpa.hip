@@ -634,7 +634,9 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
   const int n16 = lane & 15, grp = lane >> 4;
   const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
   const int R = a.L * GQA;                     // query rows (position, head) of this KV head
-  const int row0 = blockIdx.x * 64 + wave * 16;  // the wave's first row
+  // the wave's first row; under the causal mask the later (longer) row
+  // tiles start first
+  const int row0 = (a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x) * 64 + wave * 16;
   // last visible token of row rr (bottom-right causal), -1 for rows past R
   auto last_tok = [&](int rr) -> int {
     return rr >= R ? -1 : (a.causal ? a.N - a.L + rr / GQA : a.N - 1);
