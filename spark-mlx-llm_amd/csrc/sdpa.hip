@@ -305,40 +305,74 @@ __device__ void sdpa_fold_merge(const SdpaArgs& a, int b, int kh, float* sm) {
   const int S = a.S, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float* wts = sm;             // [GQA][S]
   float* zs = sm + GQA * S;    // [GQA]
+  // the maxima and sums of a head's splits are loaded together (one round
+  // trip for up to 64 splits)
   for (int h = wave; h < GQA; h += 4) {
     const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
-    float mm = kNegInf;
-    for (int s = lane; s < S; s += 64) mm = fmaxf(mm, splitk_load(a.pm + bh * S + s));
+    float mm = kNegInf, z = 0.0f;
+    if (S <= 64) {
+      const bool live = lane < S;
+      const float m = live ? splitk_load(a.pm + bh * S + lane) : kNegInf;
+      const float zp = live ? splitk_load(a.pz + bh * S + lane) : 0.0f;
+      mm = m;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
-    float z = 0.0f;
-    for (int s = lane; s < S; s += 64) {
-      const float m = splitk_load(a.pm + bh * S + s);
+      for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
       const float w = exp2_guarded(m - mm, m != kNegInf);
-      wts[h * S + s] = w;
-      z = fmaf(splitk_load(a.pz + bh * S + s), w, z);
+      if (live) wts[h * S + lane] = w;
+      z = zp * w;
+    } else {
+      for (int s = lane; s < S; s += 64) mm = fmaxf(mm, splitk_load(a.pm + bh * S + s));
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+      for (int s = lane; s < S; s += 64) {
+        const float m = splitk_load(a.pm + bh * S + s);
+        const float w = exp2_guarded(m - mm, m != kNegInf);
+        wts[h * S + s] = w;
+        z = fmaf(splitk_load(a.pz + bh * S + s), w, z);
+      }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o);
     if (lane == 0) zs[h] = z;
   }
   __syncthreads();
-  for (int e = tid; e < GQA * D; e += 256) {
-    const int h = e / D, d = e - h * D;
+  // each thread's outputs (e = tid + 256 k) summed over the splits in split
+  // order, the loads of all its outputs for eight splits in flight together
+  constexpr int E = GQA * D, EPT = (E + 255) / 256;
+  float o[EPT];
+  const float* p[EPT];
+  const float* w[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = min(tid + 256 * k, E - 1), h = e / D, d = e - h * D;
     const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
-    const float* p = a.pacc + bh * S * D + d;
-    const float* w = wts + h * S;
-    float o = 0.0f;
-    int s = 0;
-    for (; s + 8 <= S; s += 8) {
-      float v[8];
+    o[k] = 0.0f;
+    p[k] = a.pacc + bh * S * D + d;
+    w[k] = wts + h * S;
+  }
+  int s = 0;
+  for (; s + 8 <= S; s += 8) {
+    float v[EPT][8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = splitk_load(p + (int64_t)(s + u) * D);
+    for (int k = 0; k < EPT; ++k)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) o = fmaf(v[u], w[s + u], o);
+      for (int u = 0; u < 8; ++u) v[k][u] = splitk_load(p[k] + (int64_t)(s + u) * D);
+#pragma unroll
+    for (int k = 0; k < EPT; ++k)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o[k] = fmaf(v[k][u], w[k][s + u], o[k]);
+  }
+  for (; s < S; ++s)
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) o[k] = fmaf(splitk_load(p[k] + (int64_t)s * D), w[k][s], o[k]);
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = tid + 256 * k;
+    if (e < E) {
+      const int h = e / D, d = e - h * D;
+      const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
+      store_out(a.out, bh * D + d, zs[h] > 0.0f ? o[k] / zs[h] : 0.0f, a.out_dtype);
     }
-    for (; s < S; ++s) o = fmaf(splitk_load(p + (int64_t)s * D), w[s], o);
-    store_out(a.out, bh * D + d, zs[h] > 0.0f ? o / zs[h] : 0.0f, a.out_dtype);
   }
 }
 
@@ -1485,8 +1519,11 @@ __global__ __launch_bounds__(256) void kv_append_u8_wave_kernel(KvAppendArgs a) 
 // heads), at least 128 tokens per split (one 32-token block per wave), at
 // most 1024 splits, and no empty split.
 static int sdpa_splits(int64_t B, int64_t N, int64_t* tps_out = nullptr) {
+  // 64 splits over the batch, at most 32 per sequence: past 32 the merge of
+  // the partials costs more than the extra workgroups gain (B=1 N=32768:
+  // 28.0 us at 64 splits, 24.2 us at 32)
   int64_t S = cdiv(env_int("SPARKQ_SDPA_SPLITS", 64), B);
-  const int64_t cap = std::min<int64_t>(cdiv(N, 128), 1024);
+  const int64_t cap = std::min<int64_t>(cdiv(N, 128), env_int("SPARKQ_SDPA_SPLITS", 0) ? 1024 : 32);
   if (S > cap) S = cap;
   if (S < 1) S = 1;
   const int64_t tps = cdiv(N, S);
