@@ -17,6 +17,9 @@
 //                        fmaf(float(acc)*sa[m], sw[n], bias[n]); splits of K
 //                        combine in the same launch (the last workgroup of a
 //                        tile sums the int32 partials).
+//   i8_rows16_kernel     5..16 token rows: 16 weight rows per workgroup, 8
+//                        waves split K, both operands straight from global
+//                        memory into v_mfma_i32_16x16x64_i8.
 #include "common.h"
 
 namespace sparkq {
@@ -384,6 +387,73 @@ __global__ __launch_bounds__(64 * NW) void i8_gemv_kernel(I8GemvArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// 5..16 token rows: i8_rows16_kernel
+// ---------------------------------------------------------------------------
+// One workgroup per 16 weight rows; its 8 waves split K into eighths. Both
+// int8 operands go from global memory straight into
+// v_mfma_i32_16x16x64_i8 (lane l: row l%16 of the weights / of the
+// activations, k 16*(l/16) .. +16 of each 64-k chunk); the quantized
+// activations (at most 16 x K bytes) stay in L2 for every workgroup. Each
+// wave issues the loads of eight chunks before their MFMAs; rows past M or N
+// read zeros through the bounded descriptors. The waves' int32 sums are
+// added through LDS (exact in any order) and wave 0 writes the epilogue.
+constexpr int kR16W = 8;   // waves per workgroup (K split)
+constexpr int kR16PD = 8;  // 64-k chunks in flight per wave
+
+__global__ __launch_bounds__(64 * kR16W) void i8_rows16_kernel(I8Args args) {
+  __shared__ i32x4_t red[kR16W - 1][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, grp = lane >> 4;
+  const int K = args.K, N = args.N, M = args.M;
+  const int n0 = blockIdx.x * 16;
+  const int nch = K / 64;
+  const int c0 = wave * nch / kR16W, c1 = (wave + 1) * nch / kR16W;
+  const int nrows = min(16, N - n0);
+  const rsrc_t rb = make_rsrc(args.b + (int64_t)n0 * K, (uint32_t)nrows * (uint32_t)K);
+  const rsrc_t ra = make_rsrc(args.a, (uint32_t)M * (uint32_t)K);
+  const uint32_t off = (uint32_t)(n16 * K + 16 * grp);
+  i32x4_t acc = {0, 0, 0, 0};
+  for (int c = c0; c < c1; c += kR16PD) {
+    u32x4_t av[kR16PD], bv[kR16PD];
+#pragma unroll
+    for (int u = 0; u < kR16PD; ++u) {
+      const bool ok = c + u < c1;  // wave-uniform
+      bv[u] = buf_load16(rb, ok ? off + 64u * (uint32_t)(c + u) : kOob);
+      av[u] = buf_load16(ra, ok ? off + 64u * (uint32_t)(c + u) : kOob);
+    }
+#pragma unroll
+    for (int u = 0; u < kR16PD; ++u)
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, av[u]),
+                                                  __builtin_bit_cast(i32x4_t, bv[u]), acc, 0, 0, 0);
+  }
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < kR16W - 1; ++w) acc += red[w][lane];
+  // lane (g, n16) holds token rows 4g .. 4g+3 of weight row n0 + n16
+  const int nn = n0 + n16;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * grp + r;
+    if (m < M && nn < N) i8_store(args, m, nn, acc[r]);
+  }
+}
+
+static bool use_rows16(int64_t M, int64_t N, int64_t K) {
+  return M > 4 && M <= 16 && K % 64 == 0 && N * K < (int64_t)kOob && M * K < (int64_t)kOob &&
+         !env_int("SPARKQ_I8_NO_ROWS16", 0);
+}
+
+static int launch_rows16(const I8Args& args, hipStream_t st) {
+  hipLaunchKernelGGL(i8_rows16_kernel, dim3((unsigned)cdiv(args.N, 16)), dim3(64 * kR16W), 0, st,
+                     args);
+  return check_launch("i8_rows16_kernel");
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -538,6 +608,17 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
     g.mode = kOutRaw;
     return launch_i8_gemv(gp, g, 3, st);
   }
+  if (use_rows16(M, N, K)) {
+    I8Args r{};
+    r.a = a;
+    r.b = b;
+    r.c_raw = c;
+    r.M = (int)M;
+    r.N = (int)N;
+    r.K = (int)K;
+    r.mode = kOutRaw;
+    return launch_rows16(r, st);
+  }
   const I8Plan p = plan_i8(M, N, K);
   const size_t need = p.counter_bytes + p.part_bytes;
   if (need > 0 && (ws == nullptr || wsb < need))
@@ -594,6 +675,22 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
   int32_t* part = reinterpret_cast<int32_t*>(base + kCounterBytes + round_up((size_t)M * K, 256) +
                                              round_up((size_t)M * 4, 256));
   if (int rc = a8_quantize(x, q, sa, M, K, xdt, st)) return rc;
+  if (use_rows16(M, N, K)) {
+    I8Args r{};
+    r.a = q;
+    r.b = w;
+    r.sa = sa;
+    r.sw = wsc;
+    r.bias = bias;
+    r.bias_dtype = bias_dtype;
+    r.y = y;
+    r.y_dtype = ydt;
+    r.M = (int)M;
+    r.N = (int)N;
+    r.K = (int)K;
+    r.mode = kOutEpilogue;
+    return launch_rows16(r, st);
+  }
   const I8Plan p = plan_i8(M, N, K);
   I8Args args{};
   args.a = q;
