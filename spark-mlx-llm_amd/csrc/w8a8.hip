@@ -5,7 +5,8 @@
 //   i8_gemv_kernel       M <= 4 decode: whole rows per workgroup, 4 rows x
 //                        256 bytes per load, v_dot4_i32_i8, activation
 //                        quantizer fused (one launch per projection)
-//   a8_quantize_kernel   one workgroup per token row: amax, scale = amax/127
+//   a8_quantize_kernel   one workgroup per token row (a8_quantize_reg_kernel
+//                        for rows of up to 32 KB: one load round trip): amax, scale = amax/127
 //                        (1 when 0), q = clamp(rint(x/scale), -127, 127);
 //                        bit-exact with X/src/kernels/w8a8_quantize.metal:11-27
 //   i8_skinny_kernel     32 weight rows per workgroup, 4 waves split K; lane
@@ -388,6 +389,62 @@ __global__ __launch_bounds__(64 * NW) void i8_gemv_kernel(I8GemvArgs a) {
 }
 
 
+// Per-token quantizer for rows of up to 2048 16-byte pieces: every load of
+// the row is issued at once into registers (one round trip instead of one
+// per element), the amax reduced across the workgroup, and the codes
+// written from the same registers. The formula is a8_quantize_kernel's.
+constexpr int kQPieces = 8;  // 16-byte pieces per thread
+
+template <int XT>
+__global__ __launch_bounds__(256) void a8_quantize_reg_kernel(const void* __restrict__ x,
+                                                              int8_t* __restrict__ q,
+                                                              float* __restrict__ scales, int K) {
+  constexpr int ES = XT == 2 ? 4 : 2, EP = 16 / ES;
+  __shared__ float wmax[4];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int np = K * ES / 16;
+  const rsrc_t rx = make_rsrc(reinterpret_cast<const unsigned char*>(x) + (int64_t)row * K * ES,
+                              (uint32_t)(K * ES));
+  u32x4_t v[kQPieces];
+#pragma unroll
+  for (int i = 0; i < kQPieces; ++i) {
+    const int p = tid + 256 * i;
+    v[i] = buf_load16(rx, p < np ? 16u * (uint32_t)p : kOob);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kQPieces; ++i)
+#pragma unroll
+    for (int e = 0; e < EP; ++e) amax = fmaxf(amax, fabsf(piece_elem<XT>(v[i], e)));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+  if (tid == 0) scales[row] = scale;
+  int8_t* qrow = q + (int64_t)row * K;
+#pragma unroll
+  for (int i = 0; i < kQPieces; ++i) {
+    const int p = tid + 256 * i;
+    if (p < np) {
+      uint32_t packed[EP / 4];
+#pragma unroll
+      for (int e = 0; e < EP / 4; ++e) packed[e] = 0u;
+#pragma unroll
+      for (int e = 0; e < EP; ++e) {
+        float t = __builtin_rintf(piece_elem<XT>(v[i], e) / scale);
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        packed[e >> 2] |= ((uint32_t)(int32_t)t & 0xFFu) << (8 * (e & 3));
+      }
+      if constexpr (EP == 8)
+        *reinterpret_cast<uint2*>(qrow + 8 * p) = uint2{packed[0], packed[1]};
+      else
+        *reinterpret_cast<uint32_t*>(qrow + 4 * p) = packed[0];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 5..16 token rows: i8_rows16_kernel
 // ---------------------------------------------------------------------------
@@ -586,6 +643,17 @@ static int launch_i8(const I8Args& args, const I8Plan& p, hipStream_t st) {
 
 int a8_quantize(const void* x, int8_t* q, float* scales, int64_t M, int64_t K, int xdt,
                 hipStream_t st) {
+  const int64_t bytes = K * esize_of(xdt);
+  if (bytes % 16 == 0 && bytes <= 16 * 256 * kQPieces && M <= 65535) {
+    const dim3 grid((unsigned)M), block(256);
+    if (xdt == SPARKQ_BF16)
+      hipLaunchKernelGGL(a8_quantize_reg_kernel<0>, grid, block, 0, st, x, q, scales, (int)K);
+    else if (xdt == SPARKQ_F16)
+      hipLaunchKernelGGL(a8_quantize_reg_kernel<1>, grid, block, 0, st, x, q, scales, (int)K);
+    else
+      hipLaunchKernelGGL(a8_quantize_reg_kernel<2>, grid, block, 0, st, x, q, scales, (int)K);
+    return check_launch("a8_quantize_reg_kernel");
+  }
   hipLaunchKernelGGL(a8_quantize_kernel, dim3((unsigned)M), dim3(256), 0, st, x, q, scales,
                      K, xdt);
   return check_launch("a8_quantize_kernel");
