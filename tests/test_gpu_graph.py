@@ -55,12 +55,25 @@ def test_graph_replay_matches_eager(gpu):
     kc, ks = sparkq.kv_quantize_s8(torch.randn((1, 8, 4096, 128), device=gpu).to(torch.bfloat16))
     vc, vs = sparkq.kv_quantize_s8(torch.randn((1, 8, 4096, 128), device=gpu).to(torch.bfloat16))
     q = torch.randn((1, 32, 1, 128), device=gpu).to(torch.bfloat16)
+    # prefill over the MLX affine cache with a context split (tile counters
+    # reset by the kernel on every call)
+    aff = []
+    for _ in range(2):
+        cache = (torch.zeros((1, 4, 900, 64), dtype=torch.int32, device=gpu),
+                 torch.zeros((1, 4, 900, 8), dtype=torch.bfloat16, device=gpu),
+                 torch.zeros((1, 4, 900, 8), dtype=torch.bfloat16, device=gpu))
+        sparkq.kv_append(torch.randn((1, 4, 900, 256), device=gpu).to(torch.bfloat16), cache, 0)
+        aff.append(cache)
+    qp = torch.randn((1, 16, 300, 256), device=gpu).to(torch.bfloat16)
+    assert sparkq._lib.lib().sparkq_int8kv_sdpa_prefill_affine_workspace_bytes(
+        1, 16, 4, 300, 900, 256, 1) > 0
 
     outs = {
         "w4": torch.empty((1, 3584), dtype=torch.bfloat16, device=gpu),
         "w4b": torch.empty((8, 2560), dtype=torch.bfloat16, device=gpu),
         "w8": torch.empty((8, 2560), dtype=torch.bfloat16, device=gpu),
         "sdpa": torch.empty((1, 32, 1, 128), dtype=torch.bfloat16, device=gpu),
+        "prefill_affine": torch.empty((1, 16, 300, 256), dtype=torch.bfloat16, device=gpu),
     }
 
     def step():
@@ -69,6 +82,8 @@ def test_graph_replay_matches_eager(gpu):
         sparkq.w8a8_linear(x8, w8t, sc8t, out=outs["w8"])
         sparkq.int8_quantized_sdpa(q, (kc, ks), (vc, vs), scale=1 / math.sqrt(128),
                                    out=outs["sdpa"])
+        sparkq.int8_quantized_sdpa(qp, aff[0], aff[1], scale=0.0625, mask="causal",
+                                   out=outs["prefill_affine"])
 
     step()
     torch.cuda.synchronize()
