@@ -1519,11 +1519,13 @@ __global__ __launch_bounds__(256) void kv_append_u8_wave_kernel(KvAppendArgs a) 
 // heads), at least 128 tokens per split (one 32-token block per wave), at
 // most 1024 splits, and no empty split.
 static int sdpa_splits(int64_t B, int64_t N, int64_t* tps_out = nullptr) {
-  // 64 splits over the batch, at most 32 per sequence: past 32 the merge of
-  // the partials costs more than the extra workgroups gain (B=1 N=32768:
-  // 28.0 us at 64 splits, 24.2 us at 32)
+  // 64 splits over the batch, at most 32 per sequence and at least 256
+  // tokens per split: past that the merge of the partials costs more than
+  // the extra workgroups gain (B=1 N=32768: 28.0 us at 64 splits, 23.1 at
+  // 32; B=1 N=4096: 12.2 us at 32, 11.2 at 16)
   int64_t S = cdiv(env_int("SPARKQ_SDPA_SPLITS", 64), B);
-  const int64_t cap = std::min<int64_t>(cdiv(N, 128), env_int("SPARKQ_SDPA_SPLITS", 0) ? 1024 : 32);
+  const int64_t cap = env_int("SPARKQ_SDPA_SPLITS", 0) ? std::min<int64_t>(cdiv(N, 128), 1024)
+                                                       : std::min<int64_t>(cdiv(N, 256), 32);
   if (S > cap) S = cap;
   if (S < 1) S = 1;
   const int64_t tps = cdiv(N, S);
