@@ -116,11 +116,14 @@ int sparkq_w4a16_dequantize(const uint32_t* w, const void* scales,
                             int64_t K, int group_size, int scale_dtype,
                             void* stream);
 
-/* Affine 4-bit quantizer on the device (the mx.quantize(bits=4) producer of
- * the layout above, spark_mlx_llm/dspark/draft_quantization.py:119):
- * per group of G values, scale = to_dtype((max-min)/15), bias = to_dtype(min),
- * code = clamp(rint((w - bias) / scale), 0, 15) with the rounded scale and
- * bias (a zero scale gives code 0). w is [N,K] in dtype (BF16 or F16). */
+/* Affine 4-bit quantizer on the device, writing the layout above with the
+ * benchmark's formula: per group of G values, scale = to_dtype((max-min)/15),
+ * bias = to_dtype(min), code = clamp(rint((w - bias) / scale), 0, 15) with
+ * the rounded scale and bias (a zero scale gives code 0). w is [N,K] in dtype
+ * (BF16 or F16). The reference fills this layout with mx.quantize(bits=4)
+ * (spark_mlx_llm/dspark/draft_quantization.py:119), whose rule differs: it
+ * makes the larger-magnitude edge of the group exact (negative scale when
+ * that edge is the minimum, bias = edge), so its tuples are not these. */
 int sparkq_w4_quantize(const void* w, uint32_t* wq, void* scales, void* biases,
                        int64_t N, int64_t K, int group_size, int dtype,
                        void* stream);
@@ -178,6 +181,29 @@ int sparkq_w8a8_linear(const void* x, const int8_t* w, const float* w_scales,
 int sparkq_w8a16_linear(const void* x, const int8_t* w, const float* scales,
                         void* y, int64_t M, int64_t N, int64_t K, int x_dtype,
                         int y_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * W8 affine quantized linear (MLX layout, groupwise)
+ * y[m,n] = sum_k x[m,k] * (u[n,k] * s[n,k/G] + b[n,k/G]), u the unsigned
+ * byte k%4 of word k/4 of row n:
+ *   x       [M,K]   x_dtype (BF16 or F16)
+ *   w       [N,K/4] uint32
+ *   scales  [N,K/G] scale_dtype (F32, F16 or BF16; biases alike)
+ *   y       [M,N]   y_dtype (x_dtype, or F32)
+ * group_size in {32, 64, 128}; K % group_size == 0; any M. The codes are
+ * exact 16-bit MFMA operands and each group adds s*D + b*X in fp32, with D
+ * the group's dot of x and the codes and X the group's sum of x. No
+ * workspace.
+ * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True,
+ * group_size, bits=8, mode="affine") behind the affine W8 nn.QuantizedLinear
+ * that the W8 adapters keep as their fallback (spark_mlx_llm/ops/linear.py:
+ * 413-476, 531-562) and that 'native' and 'auto' W8 checkpoints run
+ * directly (spark_mlx_llm/ops/linear.py:651-711).
+ * ---------------------------------------------------------------------- */
+int sparkq_w8_affine_linear(const void* x, const uint32_t* w, const void* scales,
+                            const void* biases, void* y, int64_t M, int64_t N, int64_t K,
+                            int group_size, int x_dtype, int scale_dtype, int y_dtype,
+                            void* stream);
 
 /* ------------------------------------------------------------------------
  * INT8-KV GQA decode attention (one query token per sequence)
@@ -293,7 +319,10 @@ size_t sparkq_int8kv_sdpa_prefill_affine_workspace_bytes(int64_t B, int64_t Hq,
  *     scales and biases [B,H,Ncap,D/G] in x_dtype (BF16 or F16); per group of
  *     G dims scale = to_dtype((max-min)/255), bias = to_dtype(min), code =
  *     clamp(rint((x - bias)/scale), 0, 255) with the rounded scale and bias
- *     (code 0 when the scale is 0): the mx.quantize(bits=8) formula.
+ *     (code 0 when the scale is 0). This is the min/max formula of the 4-bit
+ *     quantizer with 255 bins, not mlx-lm's mx.quantize(bits=8) rule (which
+ *     makes the larger-magnitude edge exact), so a cache written here holds
+ *     different codes, scales and biases than mlx-lm's for the same keys.
  * strides[0..2] codes (batch, head, token) in bytes; strides[3..5] scales and
  * biases (batch, head, token) in elements. The cache is written in place;
  * tokens outside [offset, offset+L) are untouched. */

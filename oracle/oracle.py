@@ -18,7 +18,7 @@ __all__ = [
     "bf16_bits", "bits_to_f32", "f16_bits", "round16",
     "randn", "randn16",
     "pack4", "unpack4", "w4_quantize", "w4_quantize_converter",
-    "w4_dequantize", "w4a16_matmul", "w8a16_matmul",
+    "w4_dequantize", "w4a16_matmul", "w8a16_matmul", "unpack8", "w8_affine_matmul",
     "a8_quantize", "w8_quantize_channel", "w8_unpack_affine",
     "int8_matmul", "w8a8_epilogue",
     "kv_quantize_s8", "kv_quantize_affine_u8", "kv_dequantize_s8",
@@ -218,6 +218,30 @@ def w4a16_matmul(x16, wq, s, b, group_size: int, dtype: int = BF16) -> np.ndarra
     _lib().sq_w4a16_matmul(_p(x16), dtype, _p(wq), _p(s), _p(b), m, n, k,
                            group_size, _p(y))
     return y
+
+
+def unpack8(words) -> np.ndarray:
+    """MLX affine 8-bit layout: byte j of word w (little endian) is the
+    unsigned code of k = 4w + j (spark_mlx_llm/conversion.py:429-433 packs
+    32/bits codes per uint32 from the least significant bits up)."""
+    words = np.ascontiguousarray(words, np.uint32)
+    return words.view(np.uint8).reshape(*words.shape[:-1], words.shape[-1] * 4)
+
+
+def w8_affine_matmul(x16, words, s, b, group_size: int, dtype: int = BF16,
+                     scale_dtype: int | None = None) -> np.ndarray:
+    """mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size,
+    bits=8) in float64: y[m,n] = sum_k x[m,k] * (u[n,k]*s[n,k/G] + b[n,k/G])
+    (the affine dequantize of spark_mlx_llm/ops/linear.py:181-191, 299-324
+    with 8-bit codes). x16 holds 16-bit patterns of dtype; s and b are 16-bit
+    patterns of scale_dtype (default dtype) or float32 arrays."""
+    x = bits_to_f32(x16, dtype).astype(np.float64)
+    sd = dtype if scale_dtype is None else scale_dtype
+    sf = (np.asarray(s, np.float64) if sd == F32 else bits_to_f32(s, sd).astype(np.float64))
+    bf = (np.asarray(b, np.float64) if sd == F32 else bits_to_f32(b, sd).astype(np.float64))
+    u = unpack8(words).astype(np.float64)
+    w = u * np.repeat(sf, group_size, axis=1) + np.repeat(bf, group_size, axis=1)
+    return x @ w.T
 
 
 def w8a16_matmul(x16, w8, scales, dtype: int = BF16) -> np.ndarray:

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 
 #include "common.h"
@@ -58,6 +59,9 @@ int int8kv_sdpa_prefill_affine(const void* q, const void* kc, const void* ks, co
                                const int64_t* strides, void* ws, size_t wsb, hipStream_t st);
 int w8a16_linear(const void* x, const int8_t* w, const float* scales, void* y, int64_t M,
                  int64_t N, int64_t K, int xdt, int ydt, hipStream_t st);
+int w8_affine_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
+                     int64_t M, int64_t N, int64_t K, int G, int xdt, int sdt, int ydt,
+                     hipStream_t st);
 // launchers (layer.hip)
 size_t ffn_workspace(int64_t M, int64_t K, int64_t I, int G);
 int ffn(const void* x, const void* attn, const void* nw, float eps, const uint32_t* wg,
@@ -153,6 +157,24 @@ static bool is_float_dtype(int dt) { return dt == SPARKQ_F32 || dt == SPARKQ_F16
 static bool is_half_dtype(int dt) { return dt == SPARKQ_F16 || dt == SPARKQ_BF16; }
 static constexpr int64_t kI32Max = 2147483647LL;
 
+// Kernels address each tensor (or each sequence's slice of a KV cache) through
+// a buffer descriptor with 32-bit offsets, and lanes with nothing to read use
+// the offset kOob = 2^31, which must lie outside every range. A range is a
+// product of shape terms in bytes; a negative value marks an overflow.
+static int64_t range_bytes(std::initializer_list<int64_t> terms) {
+  int64_t r = 1;
+  for (int64_t t : terms) {
+    if (t < 0) return -1;
+    if (t != 0 && r > (int64_t)kOob / t + 1) return -1;
+    r *= t;
+  }
+  return r;
+}
+static bool fits_range(std::initializer_list<int64_t> terms) {
+  const int64_t r = range_bytes(terms);
+  return r >= 0 && r <= (int64_t)kOob;
+}
+
 extern "C" {
 
 const char* sparkq_last_error(void) { return g_last_error; }
@@ -182,6 +204,10 @@ int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
   REQUIRE_SUPPORTED(is_half_dtype(x_dtype), "w4a16_linear: x must be bfloat16 or float16");
   REQUIRE(y_dtype == x_dtype || y_dtype == SPARKQ_F32,
           "w4a16_linear: y dtype must equal x dtype or be float32");
+  REQUIRE_SUPPORTED(fits_range({N, K / 2}) && fits_range({N, K / group_size, 2}) &&
+                        (M > 32 || fits_range({M, K, 2})),
+                    "w4a16_linear: weights, scales or activations exceed the 2 GiB range of "
+                    "one buffer descriptor");
   REQUIRE(aligned(x, 16) && aligned(w, 16), "w4a16_linear: x and w must be 16-byte aligned");
   REQUIRE(aligned(scales, 4) && aligned(biases, 4) && aligned(y, 4),
           "w4a16_linear: scales, biases and y must be 4-byte aligned");
@@ -235,6 +261,9 @@ static int validate_i8_dims(const char* op, int64_t M, int64_t N, int64_t K) {
   REQUIRE(M > 0 && N > 0 && K > 0, "%s: Expected nonempty x[..., K] and weight[N, K] with matching K.", op);
   REQUIRE(K % 32 == 0 && K <= 131040, "%s: K must be a multiple of 32 in [32, 131040].", op);
   REQUIRE(M <= kI32Max && N <= kI32Max, "%s: dimension too large", op);
+  REQUIRE_SUPPORTED(fits_range({N, K}) && (M > 16 || fits_range({M, K, 4})),
+                    "%s: weights or activations exceed the 2 GiB range of one buffer descriptor",
+                    op);
   return SPARKQ_OK;
 }
 
@@ -307,6 +336,12 @@ int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes, const void* k_
             "int8kv_sdpa_decode: code strides must be non-negative multiples of 8 bytes");
   for (int i : {3, 4, 5, 9, 10, 11})
     REQUIRE(strides[i] >= 0, "int8kv_sdpa_decode: negative scale stride");
+  for (int i : {2, 5, 8, 11})
+    REQUIRE(strides[i] > 0, "int8kv_sdpa_decode: token strides must be positive (materialise "
+                            "broadcast views)");
+  REQUIRE_SUPPORTED(fits_range({N, std::max(strides[2], strides[8])}) &&
+                        fits_range({N, std::max(strides[5], strides[11]), 2}),
+                    "int8kv_sdpa_decode: cache too long for 32-bit offsets");
   REQUIRE(aligned(k_codes, 8) && aligned(v_codes, 8), "int8kv_sdpa_decode: codes must be 8-byte aligned");
   DEVICE_OK();
   return int8kv_sdpa_decode(q, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases, out, B,
@@ -350,6 +385,12 @@ int sparkq_int8kv_sdpa_prefill(const void* q, const void* k_codes, const void* k
             "int8kv_sdpa_prefill: code strides must be non-negative multiples of 16 bytes");
   for (int i : {3, 4, 5, 9, 10, 11})
     REQUIRE(strides[i] >= 0, "int8kv_sdpa_prefill: negative scale stride");
+  for (int i : {2, 5, 8, 11})
+    REQUIRE(strides[i] > 0, "int8kv_sdpa_prefill: token strides must be positive (materialise "
+                            "broadcast views)");
+  REQUIRE_SUPPORTED(fits_range({N, std::max(strides[2], strides[8])}) &&
+                        fits_range({N, std::max(strides[5], strides[11]), 2}),
+                    "int8kv_sdpa_prefill: cache too long for 32-bit offsets");
   REQUIRE(aligned(q, 16) && aligned(k_codes, 16) && aligned(v_codes, 16),
           "int8kv_sdpa_prefill: q and codes must be 16-byte aligned");
   DEVICE_OK();
@@ -387,10 +428,13 @@ int sparkq_int8kv_sdpa_prefill_affine(const void* q, const void* k_packed, const
             "int8kv_sdpa_prefill_affine: packed strides must be non-negative multiples of 16 bytes");
   for (int i : {3, 4, 5, 9, 10, 11})
     REQUIRE(strides[i] >= 0, "int8kv_sdpa_prefill_affine: negative scale stride");
+  for (int i : {2, 5, 8, 11})
+    REQUIRE(strides[i] > 0, "int8kv_sdpa_prefill_affine: token strides must be positive "
+                            "(materialise broadcast views)");
   // the per-(sequence, head) token range is addressed with 32-bit offsets
-  REQUIRE(N * std::max(strides[2], strides[8]) <= (int64_t)UINT32_MAX &&
-              N * std::max(strides[5], strides[11]) * 2 <= (int64_t)UINT32_MAX,
-          "int8kv_sdpa_prefill_affine: cache too long for 32-bit offsets");
+  REQUIRE_SUPPORTED(fits_range({N, std::max(strides[2], strides[8])}) &&
+                        fits_range({N, std::max(strides[5], strides[11]), 2}),
+                    "int8kv_sdpa_prefill_affine: cache too long for 32-bit offsets");
   REQUIRE(aligned(q, 16) && aligned(k_packed, 16) && aligned(v_packed, 16),
           "int8kv_sdpa_prefill_affine: q and packed codes must be 16-byte aligned");
   DEVICE_OK();
@@ -448,10 +492,38 @@ int sparkq_w8a16_linear(const void* x, const int8_t* w, const float* scales, voi
   REQUIRE_SUPPORTED(M <= 4, "w8a16_linear: at most 4 activation rows (got %lld)", (long long)M);
   REQUIRE_SUPPORTED(K % 16 == 0, "w8a16_linear: K must be a multiple of 16 (got %lld)",
                     (long long)K);
+  REQUIRE_SUPPORTED(fits_range({N, K}),
+                    "w8a16_linear: weights exceed the 2 GiB range of one buffer descriptor");
   REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(scales, 4) && aligned(y, 4),
           "w8a16_linear: x and w must be 16-byte aligned");
   DEVICE_OK();
   return w8a16_linear(x, w, scales, y, M, N, K, x_dtype, y_dtype, (hipStream_t)stream);
+}
+
+int sparkq_w8_affine_linear(const void* x, const uint32_t* w, const void* scales,
+                            const void* biases, void* y, int64_t M, int64_t N, int64_t K,
+                            int group_size, int x_dtype, int scale_dtype, int y_dtype,
+                            void* stream) {
+  REQUIRE(x && w && scales && biases && y, "w8_affine_linear: null tensor pointer");
+  REQUIRE(M > 0 && N > 0 && K > 0, "w8_affine_linear: M, N and K must be positive");
+  REQUIRE(M <= kI32Max && N <= kI32Max && K <= kI32Max, "w8_affine_linear: dimension too large");
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "w8_affine_linear: group_size must be 32, 64 or 128 (got %d)", group_size);
+  REQUIRE(K % group_size == 0, "w8_affine_linear: K=%lld is not a multiple of group_size=%d",
+          (long long)K, group_size);
+  REQUIRE_SUPPORTED(is_half_dtype(x_dtype), "w8_affine_linear: x must be bfloat16 or float16");
+  REQUIRE(is_float_dtype(scale_dtype), "w8_affine_linear: scales must be a floating dtype");
+  REQUIRE(y_dtype == x_dtype || y_dtype == SPARKQ_F32,
+          "w8_affine_linear: y dtype must equal x dtype or be float32");
+  REQUIRE_SUPPORTED(fits_range({N, K}) && fits_range({M, K, 2}),
+                    "w8_affine_linear: weights or activations exceed the 2 GiB range of one "
+                    "buffer descriptor");
+  REQUIRE(aligned(x, 16) && aligned(w, 16), "w8_affine_linear: x and w must be 16-byte aligned");
+  REQUIRE(aligned(scales, 2) && aligned(biases, 2) && aligned(y, 4),
+          "w8_affine_linear: scales, biases and y must be aligned to their element size");
+  DEVICE_OK();
+  return w8_affine_linear(x, w, scales, biases, y, M, N, K, group_size, x_dtype, scale_dtype,
+                          y_dtype, (hipStream_t)stream);
 }
 
 size_t sparkq_ffn_workspace_bytes(int64_t M, int64_t K, int64_t I, int group_size) {
@@ -486,6 +558,10 @@ int sparkq_ffn(const void* x, const void* attn, const void* norm_w, float eps,
   REQUIRE(aligned(gate_scales, 4) && aligned(gate_biases, 4) && aligned(up_scales, 4) &&
               aligned(up_biases, 4) && aligned(down_scales, 4) && aligned(down_biases, 4),
           "ffn: scales and biases must be 4-byte aligned");
+  REQUIRE_SUPPORTED(fits_range({I, K / 2}) && fits_range({I, K / group_size, 2}) &&
+                        fits_range({K, I / 2}) && fits_range({K, I / group_size, 2}) &&
+                        (M > 32 || fits_range({M, I, 2})),
+                    "ffn: weights exceed the 2 GiB range of one buffer descriptor");
   REQUIRE(aligned(workspace, 256), "ffn: workspace must be 256-byte aligned");
   DEVICE_OK();
   return ffn(x, attn, norm_w, eps, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
@@ -529,6 +605,9 @@ int sparkq_qkv_rope(const void* x, const uint32_t* w, const void* scales, const 
   REQUIRE((int64_t)q_size + 2LL * kv_size <= kI32Max, "[spark_qkv_rope] q_size + 2*kv_size too large");
   REQUIRE_SUPPORTED(hidden % 64 == 0, "[spark_qkv_rope] hidden must be a multiple of 64 (got %lld)",
                     (long long)hidden);
+  REQUIRE_SUPPORTED(fits_range({(int64_t)q_size + 2LL * kv_size, hidden / 2}) &&
+                        fits_range({(int64_t)q_size + 2LL * kv_size, hidden / group_size, 2}),
+                    "[spark_qkv_rope] weights exceed the 2 GiB range of one buffer descriptor");
   REQUIRE_SUPPORTED(is_half_dtype(dtype), "[spark_qkv_rope] x must be bfloat16 or float16");
   REQUIRE(offset >= 0 && offset < (1LL << 24), "[spark_qkv_rope] offset must be in [0, 2^24)");
   REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(scales, 4) && aligned(biases, 4) &&

@@ -1384,7 +1384,8 @@ __global__ __launch_bounds__(256) void kv_quantize_s8_kernel(const void* __restr
 // format: one thread per group of G values, scale = to_dtype((max-min)/255),
 // bias = to_dtype(min), code = clamp(rint((x - bias) / scale), 0, 255) with
 // the rounded scale and bias (0 for a zero scale), four codes per uint32
-// (dim 4w+j in byte j of word w).
+// (dim 4w+j in byte j of word w). This min/max rule is not mx.quantize's,
+// which makes the larger-magnitude edge exact (negative scale, bias = edge).
 struct KvAppendArgs {
   const void* x;
   void* codes;

@@ -69,7 +69,9 @@ __global__ __launch_bounds__(256) void w4_dequant_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// affine 4-bit quantizer: one thread per group
+// affine 4-bit quantizer: one thread per group, the benchmark's min/max
+// formula (scale (max-min)/15, bias min); mx.quantize's rule, which makes the
+// larger-magnitude edge exact, gives different tuples in the same layout
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void w4_quantize_kernel(

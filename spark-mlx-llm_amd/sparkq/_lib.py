@@ -45,6 +45,7 @@ SIGNATURES = {
     "sparkq_w8a8_workspace_bytes": (SZ, [I64, I64, I64]),
     "sparkq_w8a8_linear": (I, [P, P, P, P, I, P, I64, I64, I64, I, I, P, SZ, P]),
     "sparkq_w8a16_linear": (I, [P, P, P, P, I64, I64, I64, I, I, P]),
+    "sparkq_w8_affine_linear": (I, [P, P, P, P, P, I64, I64, I64, I, I, I, I, P]),
     "sparkq_int8kv_sdpa_workspace_bytes": (SZ, [I64, I64, I64, I64]),
     "sparkq_int8kv_sdpa_decode": (I, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64,
                                       I, I, I, I, F, P, P, SZ, P]),

@@ -17,11 +17,15 @@ A quantized module has ``<module>.weight`` (U32 packed codes, [N, K*bits/32]),
 ``<module>.scales`` and ``<module>.biases`` ([N, K/G], BF16; F32 for the LM
 head). This reader memory-maps the shards, builds the tensors on a device and
 wraps each quantized module in the projection its backend selects, the load-time
-policy of QuantizedProjections._configure (spark_mlx_llm/ops/linear.py:
-565-731): W4 modules become QuantizedLinear (sparkq's affine GEMV/GEMM); W8
-modules become W8A8QuantizedLinear for the "w8a8" backend and
-W8A16PerChannelLinear for "w8a16" (both after the W8 unpack, ops/linear.py:
-299-324); "native"/"auto" keep the affine QuantizedLinear.
+policy of QuantizedProjections (spark_mlx_llm/ops/linear.py:565-731): W4
+modules become QuantizedLinear (sparkq's affine GEMV/GEMM). W8 modules keep
+the affine QuantizedLinear (sparkq's groupwise W8 MFMA kernel) and, by
+backend, are wrapped after the W8 unpack (ops/linear.py:299-324):
+"w8a16" in W8A16PerChannelLinear when the scales are per channel (groupwise
+W8 stays affine), "w8a8" in W8A8Projection; "auto" builds
+W8A8QuantizedLinear for a module whose quantization_config entry carries
+input_activations (ops/linear.py:569-583) and keeps the affine module
+otherwise; "native" and "multirow" keep the affine module.
 """
 
 from __future__ import annotations
@@ -35,8 +39,8 @@ from math import prod
 import numpy as np
 import torch
 
-from .ops.linear import (QuantizedLinear, W8A16PerChannelLinear, W8A8QuantizedLinear,
-                         unpack_affine_w8)
+from .ops.linear import (LinearConfig, QuantizedLinear, W8A16PerChannelLinear, W8A8Projection,
+                         W8A8QuantizedLinear, unpack_affine_w8, validate_w8a8_activations)
 
 __all__ = ["TensorInfo", "Checkpoint", "quantization_scheme", "load_projection"]
 
@@ -160,9 +164,11 @@ def load_projection(ckpt: Checkpoint, module: str, device, *, w8_backend: str | 
     """Build the projection for one quantized module on ``device``.
 
     W4 -> QuantizedLinear. W8 -> by backend (the checkpoint's w8_qmv_backend
-    unless overridden): "w8a8" W8A8QuantizedLinear, "w8a16"
-    W8A16PerChannelLinear (affine fallback kept), "native"/"auto" the affine
-    QuantizedLinear (ops/linear.py:651-711)."""
+    unless overridden; ops/linear.py:569-583, 651-711): "w8a16"
+    W8A16PerChannelLinear over the affine module when the W8 is per channel
+    and bias-free, "w8a8" W8A8Projection over it, "auto" W8A8QuantizedLinear
+    when the module's quantization_config entry carries input_activations,
+    otherwise (and for "native"/"multirow") the affine QuantizedLinear."""
     scheme = quantization_scheme(ckpt.config, module)
     bits, g = scheme["bits"], scheme["group_size"]
     w = ckpt.tensor(module + ".weight", device)
@@ -177,9 +183,19 @@ def load_projection(ckpt: Checkpoint, module: str, device, *, w8_backend: str | 
     if bits != 8:
         raise ValueError(f"{module}: unsupported bits={bits}")
     backend = w8_backend or ckpt.config.get("w8_qmv_backend", "native")
+    LinearConfig(w8_qmv_backend=backend)
+    if backend == "auto":
+        scheme = (ckpt.config.get("quantization_config") or {}).get(module, {})
+        if isinstance(scheme, dict) and scheme.get("input_activations") is not None:
+            validate_w8a8_activations(scheme["input_activations"])
+            return W8A8QuantizedLinear(w, s, b, group_size=g, bits=8, bias=bias)
+        return affine
     if backend == "w8a8":
-        return W8A8QuantizedLinear(w, s, b, group_size=g, bits=8, bias=bias)
-    if backend == "w8a16" and bias is None:
         w8, sc = unpack_affine_w8(w, s, b, g, module)
-        return W8A16PerChannelLinear(affine, w8, sc)
+        return W8A8Projection(affine, w8, sc)
+    if backend == "w8a16" and bias is None:
+        unpacked = unpack_affine_w8(w, s, b, g, module, allow_fallback=True)
+        if unpacked is None:
+            return affine
+        return W8A16PerChannelLinear(affine, *unpacked)
     return affine

@@ -115,13 +115,17 @@ def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
     transpose=True, group_size, bits, mode="affine") as called by
     AffineParameters.native (spark_mlx_llm/ops/linear.py:181-191). Any number
     of rows: up to 32 rows stream the weights (decode, speculative verify),
-    more rows use the tiled MFMA GEMM (prefill). out_dtype may be
+    more rows use the tiled MFMA GEMM (prefill). bits=8 (weight [N,K/4]) runs
+    the groupwise W8 affine MFMA kernel that the reference's W8 layers fall
+    back to. out_dtype may be
     torch.float32 to read the unrounded fp32 epilogue; out, when given, is a
     contiguous [..., N] tensor written in place.
     """
     if not transpose:
         raise ValueError("only transpose=True (x @ W^T) is supported")
     op = "affine_quantized_matmul"
+    if bits == 8:
+        return _w8_affine_matmul(op, x, weight, scales, biases, group_size, out_dtype, out)
     _w4_check(op, x, weight, scales, biases, group_size, bits)
     k = x.shape[-1]
     n = weight.shape[0]
@@ -140,6 +144,47 @@ def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
     _lib.call("sparkq_w4a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
               _ptr(y), m, n, k, group_size, bits, _lib.dtype_code(x.dtype),
               _lib.dtype_code(out_dtype), ws, wsb, _lib.stream_handle(x.device))
+    return y.reshape(*lead, n)
+
+
+def _w8_affine_matmul(op, x, weight, scales, biases, group_size, out_dtype, out):
+    """bits=8 branch of affine_quantized_matmul: packed uint32 [N,K/4] codes
+    (byte k%4 of word k/4, unsigned), groupwise scales and biases [N,K/G].
+    The result dtype follows MLX's promotion of x with the scales (fp32
+    scales, as the converter writes for the lm_head, give an fp32 result)."""
+    if any(not isinstance(v, torch.Tensor) for v in (x, weight, scales, biases)):
+        raise TypeError("x, weight, scales and biases must be tensors")
+    if weight.dtype not in _PACKED or weight.ndim != 2:
+        raise ValueError(f"{op} requires UINT32-packed W8 weights of shape [N,K/4]")
+    if x.dtype not in _HALF:
+        raise ValueError(f"{op} requires BF16 or F16 x for 8-bit affine weights")
+    if scales.dtype not in _REAL or biases.dtype != scales.dtype:
+        raise ValueError(f"{op} requires floating scales and biases of one dtype")
+    if x.ndim < 1 or x.shape[-1] <= 0:
+        raise ValueError(f"{op} requires x[..., K] with positive K")
+    k, n = x.shape[-1], weight.shape[0]
+    if n <= 0 or weight.shape[1] * 4 != k:
+        raise ValueError(f"{op}: weight must have shape [N,K/4] with K={k}")
+    if group_size not in (32, 64, 128) or k % group_size:
+        raise ValueError(f"{op}: group_size must be 32, 64 or 128 and divide K")
+    if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
+        raise ValueError(f"{op} requires scales and biases with shape [N,K/{group_size}]")
+    _require_device(op, x, weight, scales, biases)
+    result = torch.promote_types(x.dtype, scales.dtype)
+    out_dtype = result if out_dtype is None else out_dtype
+    if out_dtype not in (result, torch.float32):
+        raise ValueError(f"out_dtype must be {result} or torch.float32")
+    lead = x.shape[:-1]
+    m = prod(lead)
+    y = _out_buffer(out, (m, n), out_dtype, x.device)
+    if m == 0:
+        return y.reshape(*lead, n)
+    x2 = x.reshape(m, k).contiguous()
+    weight, scales, biases = weight.contiguous(), scales.contiguous(), biases.contiguous()
+    _lib.call("sparkq_w8_affine_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
+              _ptr(y), m, n, k, group_size, _lib.dtype_code(x.dtype),
+              _lib.dtype_code(scales.dtype), _lib.dtype_code(out_dtype),
+              _lib.stream_handle(x.device))
     return y.reshape(*lead, n)
 
 
@@ -189,9 +234,16 @@ def prepare_w4a16_nax4(weight, scales, biases):
 
 
 def affine_quantize(w, *, group_size: int = 64, bits: int = 4):
-    """Quantize BF16/F16 weights [N,K] to the MLX affine 4-bit layout on the GPU
-    (mx.quantize(bits=4) producer, spark_mlx_llm/dspark/draft_quantization.py:119):
-    scale = (max-min)/15, bias = min per group, rounded to w.dtype."""
+    """Quantize BF16/F16 weights [N,K] into the MLX affine 4-bit layout on the
+    GPU with the benchmark's formula: per group, scale = (max-min)/15 and
+    bias = min, both rounded to w.dtype, codes rint((w-bias)/scale) clamped
+    to 0..15. The layout is the one mx.quantize(bits=4) fills for the
+    reference (spark_mlx_llm/dspark/draft_quantization.py:119), but the
+    tuple is not MLX's: mx.quantize makes the group's larger-magnitude edge
+    exactly representable (a negative scale when that edge is the minimum,
+    bias equal to the edge), so its codes, scales and biases differ from
+    these. Any tuple in this layout runs through the same kernels; bit
+    identity with mx.quantize is unpinned (MLX is not available here)."""
     if bits != 4:
         raise ValueError("only 4-bit affine quantization is supported")
     if w.ndim != 2 or w.dtype not in _HALF:

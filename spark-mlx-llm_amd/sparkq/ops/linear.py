@@ -197,6 +197,19 @@ class AffineParameters(NamedTuple):
 
 _XOR80 = -2139062144  # 0x80808080 as a signed 32-bit value
 
+_W8A8_ACTIVATIONS = {"num_bits": 8, "type": "int", "strategy": "token", "symmetric": True,
+                     "dynamic": True}
+
+
+def validate_w8a8_activations(activations):
+    """A W8A8 module's input_activations must describe symmetric dynamic
+    per-token int8 (spark_mlx_llm/ops/linear.py:280-296); absent keys take
+    the expected values."""
+    if not isinstance(activations, dict) or activations.get("num_bits") != 8 or any(
+            activations.get(key, want) != want for key, want in _W8A8_ACTIVATIONS.items()):
+        raise ValueError(
+            "W8A8 out_proj requires symmetric dynamic per-token INT8 input_activations")
+
 
 def unpack_affine_w8(weight, scales, biases, group_size: int, name: str = "layer",
                      *, allow_fallback: bool = False):

@@ -86,12 +86,25 @@ def _int8_attention(queries, keys, values, *, cache, scale, mask):
                                    bits=cache.bits, mask=mask)
 
 
+def causal_mask(length: int, n: int, device=None) -> torch.Tensor:
+    """Boolean [length, n] mask of MLX's "causal": aligned bottom-right, so
+    query i of the last ``length`` positions sees tokens 0 .. n-length+i
+    (mlx-lm's create_causal_mask; X/spark_mlx_ext/int8_quantized_sdpa.py:
+    141-142 builds the same mask as arange(n-L, n)[:, None] >= arange(n))."""
+    return torch.ones((length, n), dtype=torch.bool, device=device).tril(n - length)
+
+
 def _native_attention(queries, keys, values, *, scale, mask):
     heads, kv_heads = queries.shape[1], keys.shape[1]
     if heads != kv_heads:
         keys = keys.repeat_interleave(heads // kv_heads, dim=1)
         values = values.repeat_interleave(heads // kv_heads, dim=1)
-    causal = isinstance(mask, str) and mask == "causal" and queries.shape[2] > 1
-    attn_mask = None if isinstance(mask, str) or mask is None else mask
+    length, n = queries.shape[2], keys.shape[2]
+    if isinstance(mask, str):
+        if mask != "causal":
+            raise ValueError("mask string must be 'causal'")
+        # torch's is_causal aligns the mask top-left; MLX aligns it bottom-right,
+        # which differs whenever the cache already holds tokens (length < n)
+        mask = causal_mask(length, n, queries.device) if length > 1 else None
     return torch.nn.functional.scaled_dot_product_attention(
-        queries, keys, values, attn_mask=attn_mask, is_causal=causal, scale=scale)
+        queries, keys, values, attn_mask=mask, scale=scale)

@@ -167,3 +167,49 @@ def test_status_maps_to_reference_exceptions():
 
     with pytest.raises(ValueError, match="null"):
         _lib.call("sparkq_a8_quantize_per_token", None, None, None, 1, 32, 2, None)
+
+
+def test_ranges_beyond_one_buffer_descriptor_are_unsupported():
+    """Kernels address a tensor (or one sequence's KV slice) with 32-bit
+    buffer offsets and use offset 2^31 for lanes with nothing to read, so any
+    such range above 2 GiB must be refused before a launch, not wrapped."""
+    dummy = P(4096)
+    f = ctypes.c_float
+    # W4: a 2^20 x 2^13 weight is 4 GiB of packed codes
+    rc, msg = _rc("sparkq_w4a16_linear", dummy, dummy, dummy, dummy, dummy, 1, 1 << 20,
+                  1 << 13, 64, 4, 2, 2, None, 0, None)
+    assert rc == -2 and "2 GiB" in msg
+    # W8: an int8 head of 262144 x 16384 (4 GiB)
+    rc, msg = _rc("sparkq_w8a16_linear", dummy, dummy, dummy, dummy, 1, 262144, 16384, 2, 2,
+                  None)
+    assert rc == -2 and "2 GiB" in msg
+    rc, msg = _rc("sparkq_int8_matmul_i32", dummy, dummy, dummy, 1, 262144, 16384, None, 0,
+                  None)
+    assert rc == -2 and "2 GiB" in msg
+    rc, msg = _rc("sparkq_w8a8_linear", dummy, dummy, dummy, None, 0, dummy, 1, 262144, 16384,
+                  2, 2, dummy, 0, None)
+    assert rc == -2 and "2 GiB" in msg
+    # exactly 2 GiB is still addressable: 131072 x 16384 int8
+    rc, msg = _rc("sparkq_w8a16_linear", dummy, dummy, dummy, dummy, 1, 131072, 16384, 2, 2,
+                  None)
+    assert "2 GiB" not in msg
+    # attention: a token stride of 64 KiB over 2^16 tokens is a 4 GiB slice
+    big = (ctypes.c_int64 * 12)(0, 0, 65536, 0, 0, 1, 0, 0, 65536, 0, 0, 1)
+    rc, msg = _rc("sparkq_int8kv_sdpa_decode", dummy, dummy, dummy, None, dummy, dummy, None,
+                  dummy, 1, 8, 8, 65536, 128, 32, 0, 2, 2, f(0.1), big, None, 0, None)
+    assert rc == -2 and "32-bit offsets" in msg
+    rc, msg = _rc("sparkq_int8kv_sdpa_prefill", dummy, dummy, dummy, dummy, dummy, dummy, 1, 8,
+                  8, 2, 65536, 128, 1, 2, 2, f(0.1), big, None)
+    assert rc == -2 and "32-bit offsets" in msg
+    # a broadcast (zero) token stride would make the range empty: refused
+    zero = (ctypes.c_int64 * 12)(0, 0, 0, 0, 0, 1, 0, 0, 128, 0, 0, 1)
+    rc, msg = _rc("sparkq_int8kv_sdpa_decode", dummy, dummy, dummy, None, dummy, dummy, None,
+                  dummy, 1, 8, 8, 16, 128, 32, 0, 2, 2, f(0.1), zero, None, 0, None)
+    assert rc == -1 and "token strides must be positive" in msg
+    rc, msg = _rc("sparkq_int8kv_sdpa_prefill", dummy, dummy, dummy, dummy, dummy, dummy, 1, 8,
+                  8, 2, 16, 128, 1, 2, 2, f(0.1), zero, None)
+    assert rc == -1 and "token strides must be positive" in msg
+    aff = (ctypes.c_int64 * 12)(0, 0, 0, 0, 0, 4, 0, 0, 32, 0, 0, 4)
+    rc, msg = _rc("sparkq_int8kv_sdpa_prefill_affine", dummy, dummy, dummy, dummy, dummy, dummy,
+                  dummy, dummy, 1, 8, 8, 2, 16, 128, 32, 1, 2, 2, f(0.1), aff, None, 0, None)
+    assert rc == -1 and "token strides must be positive" in msg

@@ -101,7 +101,7 @@ def test_loaded_projections_match_oracle(gpu, tmp_path, backend):
     each layer's 16-bit output must be the rounding of that fp32 value."""
     import sparkq
     from sparkq.checkpoint import Checkpoint, load_projection
-    from sparkq.ops import W8A16PerChannelLinear, W8A8QuantizedLinear
+    from sparkq.ops import W8A16PerChannelLinear, W8A8Projection
 
     tensors = _write_model(tmp_path, w8_backend=backend)
     ck = Checkpoint(str(tmp_path))
@@ -128,8 +128,8 @@ def test_loaded_projections_match_oracle(gpu, tmp_path, backend):
                                        out_dtype=torch.float32).cpu().numpy()
         close(y32, o.w8a16_matmul(x, w8, sc))
     else:
-        assert isinstance(p8, W8A8QuantizedLinear)
-        w8t, sct = p8.prepare_parameters()
+        assert isinstance(p8, W8A8Projection)
+        w8t, sct = p8.projection.weight, p8.projection.scales
         assert np.array_equal(w8t.cpu().numpy(), w8)
         y32 = sparkq.w8a8_linear(xt, w8t, sct, out_dtype=torch.float32).cpu().numpy()
         q, sa = o.a8_quantize(o.bits_to_f32(x, o.BF16))

@@ -134,6 +134,40 @@ def test_sdpa_dispatch_validation():
     assert torch.allclose(out, torch.ones_like(out))
 
 
+def test_native_causal_mask_is_bottom_right():
+    """mask='causal' over an unquantized cache that already holds tokens
+    (L < S): query i sees tokens 0 .. S-L+i, as MLX aligns it, not torch's
+    top-left is_causal."""
+    from sparkq.ops.sdpa import causal_mask
+
+    g = torch.Generator().manual_seed(0)
+    b, hq, hkv, length, s, d = 1, 4, 2, 3, 7, 16
+    q = torch.randn((b, hq, length, d), generator=g, dtype=torch.float64)
+    k = torch.randn((b, hkv, s, d), generator=g, dtype=torch.float64)
+    v = torch.randn((b, hkv, s, d), generator=g, dtype=torch.float64)
+    out = dispatch_sdpa(q, k, v, cache=None, scale=0.25, mask="causal")
+    # textbook: explicit loops over the visible tokens of each query
+    kk, vv = k.repeat_interleave(2, dim=1), v.repeat_interleave(2, dim=1)
+    ref = torch.empty_like(out)
+    for h in range(hq):
+        for i in range(length):
+            visible = s - length + i + 1
+            w = torch.softmax(0.25 * kk[0, h, :visible] @ q[0, h, i], dim=0)
+            ref[0, h, i] = w @ vv[0, h, :visible]
+    assert torch.allclose(out, ref, atol=1e-12)
+    # the mask itself: last row sees everything, first row sees S-L+1 tokens
+    m = causal_mask(length, s)
+    assert m[-1].all() and int(m[0].sum()) == s - length + 1
+    assert torch.equal(causal_mask(s, s), torch.ones((s, s), dtype=torch.bool).tril())
+    # an explicit boolean mask array is passed through unchanged
+    keep = torch.rand((length, s), generator=g) > 0.3
+    keep[:, 0] = True
+    out2 = dispatch_sdpa(q, k, v, cache=None, scale=0.25, mask=keep)
+    sc = 0.25 * (q @ kk.transpose(-1, -2))
+    ref2 = torch.softmax(sc.masked_fill(~keep, float("-inf")), -1) @ vv
+    assert torch.allclose(out2, ref2, atol=1e-12)
+
+
 def test_package_surface():
     for name in sparkq.__all__:
         assert callable(getattr(sparkq, name))

@@ -532,3 +532,96 @@ def test_qkv_rope_split_and_rotation():
     assert np.array_equal(v7, v)
     assert np.array_equal(q7[:, 32:], q[:, 32:]) and not np.array_equal(q7[:, :32], q[:, :32])
     assert np.array_equal(k7, o.rope16(kk[:, None], 32, 10000.0, 7)[:, 0])
+
+
+# ---------------------------------------------------------------------------
+# W8 affine (groupwise) quantized matmul
+# ---------------------------------------------------------------------------
+
+def test_w8_affine_oracle_against_brute_force_and_special_cases():
+    """w8_affine_matmul: pure-Python loops over the packed bytes on a tiny
+    case; one-hot activations pick u*s+b; a zero scale leaves b * group sum
+    of x; per-channel symmetric W8 (biases -128*s, the converter's layout)
+    equals the independent W8A16 oracle s * sum x*(u-128)."""
+    rng = np.random.default_rng(21)
+    m, n, k, g = 2, 3, 64, 32
+    words = rng.integers(0, 2 ** 32, (n, k // 4), dtype=np.uint64).astype(np.uint32)
+    s = o.bf16_bits(rng.standard_normal((n, k // g)).astype(np.float32) * 0.01)
+    b = o.bf16_bits(rng.standard_normal((n, k // g)).astype(np.float32) * 0.1)
+    x = o.randn16(21, 1, m * k).reshape(m, k)
+    y = o.w8_affine_matmul(x, words, s, b, g)
+    xf, sf, bf = (o.bits_to_f32(a, o.BF16) for a in (x, s, b))
+    for i in range(m):
+        for j in range(n):
+            acc = 0.0
+            for kk in range(k):
+                code = (int(words[j, kk // 4]) >> (8 * (kk % 4))) & 0xFF
+                acc += float(xf[i, kk]) * (code * float(sf[j, kk // g]) + float(bf[j, kk // g]))
+            assert abs(y[i, j] - acc) <= 1e-12 * max(1.0, abs(acc))
+    # one-hot rows
+    e = np.zeros((1, k), np.float32)
+    e[0, 37] = 1.0
+    code = (words[:, 37 // 4] >> np.uint32(8 * (37 % 4))) & 0xFF
+    assert np.array_equal(o.w8_affine_matmul(o.bf16_bits(e), words, s, b, g)[0],
+                          code * sf[:, 1].astype(np.float64) + bf[:, 1].astype(np.float64))
+    # zero scales: b times the group sums of x
+    z = np.zeros_like(s)
+    yz = o.w8_affine_matmul(x, words, z, b, g)
+    gs = xf.astype(np.float64).reshape(m, k // g, g).sum(-1)
+    assert np.allclose(yz, gs @ bf.astype(np.float64).T, rtol=1e-13, atol=1e-13)
+    # converter W8 rows against the W8A16 oracle (fp32 scale per channel)
+    gold = _golden()
+    x8 = o.randn16(22, 1, 3 * 256).reshape(3, 256)
+    sc = o.bits_to_f32(gold["w8_scales"], o.BF16)[:, 0].copy()
+    ya = o.w8_affine_matmul(x8, gold["w8_words"], gold["w8_scales"], gold["w8_biases"], 32)
+    yb = o.w8a16_matmul(x8, o.w8_unpack_affine(gold["w8_words"]), sc)
+    assert np.allclose(ya, yb, rtol=1e-12, atol=1e-9)
+    # fp32 scales (the converter's lm_head coefficients) are taken as is
+    sf32 = rng.random((n, k // g)).astype(np.float32)
+    bf32 = rng.random((n, k // g)).astype(np.float32)
+    y32 = o.w8_affine_matmul(x, words, sf32, bf32, g, o.BF16, o.F32)
+    u = o.unpack8(words).astype(np.float64)
+    w = u * np.repeat(sf32.astype(np.float64), g, 1) + np.repeat(bf32.astype(np.float64), g, 1)
+    assert np.allclose(y32, xf.astype(np.float64) @ w.T, rtol=1e-13)
+    assert np.array_equal(o.unpack8(np.array([[0x04030201]], np.uint32))[0], [1, 2, 3, 4])
+
+
+# ---------------------------------------------------------------------------
+# multi-token (prefill) attention oracle
+# ---------------------------------------------------------------------------
+
+def test_sdpa_prefill_oracle_pins():
+    """oracle.sdpa_prefill against the independent C decode oracle and
+    textbook invariants: each causal row i (of L) equals decode of that query
+    over the first N-L+i+1 tokens, so the last row is decode over all N; an
+    unmasked L-row call equals decode row by row; identical keys give the
+    mean of the visible values; a wrong (top-left) mask alignment fails."""
+    b, hq, hkv, length, n, d = 1, 4, 2, 5, 9, 16
+    q = o.randn(5, 1, b * hq * length * d).reshape(b, hq, length, d)
+    k = o.randn(5, 2, b * hkv * n * d).reshape(b, hkv, n, d)
+    v = o.randn(5, 3, b * hkv * n * d).reshape(b, hkv, n, d)
+    scale = 0.3
+    causal = o.sdpa_prefill(q, k, v, scale, causal=True)
+    full = o.sdpa_prefill(q, k, v, scale, causal=False)
+    for i in range(length):
+        vis = n - length + i + 1
+        dec = o.sdpa_decode(q[:, :, i].copy(), k[:, :, :vis].copy(), v[:, :, :vis].copy(), scale)
+        assert np.allclose(causal[:, :, i], dec, atol=1e-6), i
+        decf = o.sdpa_decode(q[:, :, i].copy(), k, v, scale)
+        assert np.allclose(full[:, :, i], decf, atol=1e-6), i
+    assert np.allclose(causal[:, :, -1], full[:, :, -1], atol=1e-12)
+    # identical keys: uniform weights over each row's visible tokens
+    kk = np.repeat(k[:, :, :1], n, axis=2)
+    same = o.sdpa_prefill(q, kk, v, scale, causal=True)
+    vr = np.repeat(v.astype(np.float64), hq // hkv, axis=1)
+    for i in range(length):
+        vis = n - length + i + 1
+        assert np.allclose(same[:, :, i], vr[:, :, :vis].mean(2), atol=1e-6)
+    # a top-left alignment (query i sees tokens 0..i) would differ
+    vis_tl = np.arange(length)[:, None] >= np.arange(n)[None, :]
+    kr = np.repeat(k.astype(np.float64), hq // hkv, axis=1)
+    sc = (q.astype(np.float64) * scale) @ np.swapaxes(kr, -1, -2)
+    sc = np.where(vis_tl, sc, -np.inf)
+    p = np.exp(sc - sc.max(-1, keepdims=True))
+    wrong = (p / p.sum(-1, keepdims=True)) @ vr
+    assert not np.allclose(wrong, causal, atol=1e-3)
