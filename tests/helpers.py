@@ -62,22 +62,27 @@ def check_fp32(out, ref, atol=2e-2, rtol_l2=1e-3):
 
 def check_rounded16(out_bits, ref64, dtype, atol=2e-2, near_zero=2.0 ** -7,
                     max_flip_frac=0.05):
-    """A 16-bit output against the correctly rounded oracle: max-abs within
-    atol; every element whose magnitude is at least near_zero * rms(ref)
+    """A 16-bit output against the correctly rounded oracle: every element
+    within atol of it or a 1-unit boundary flip (one unit of bf16 is 2^-5 at
+    |y| >= 4, above atol, so flips are allowed and counted rather than held
+    to atol); every element whose magnitude is at least near_zero * rms(ref)
     within one unit of the format (an fp32 accumulation error of ~1e-6*rms is
     many units of a near-zero result, so those are held to atol only); and
-    the fraction of 1-unit boundary flips bounded and reported."""
+    the fraction of 1-unit flips bounded and reported."""
     ref = np.asarray(ref64, np.float64)
     ref_bits = o.round16(ref.astype(np.float32), dtype)
-    ma = max_abs(o.bits_to_f32(out_bits, dtype), o.bits_to_f32(ref_bits, dtype))
+    diff = np.abs(o.bits_to_f32(out_bits, dtype).astype(np.float64)
+                  - o.bits_to_f32(ref_bits, dtype).astype(np.float64))
     d = ulp_distance16(out_bits, ref_bits, dtype)
+    ma = float(diff.max())
+    ma_noflip = float(diff[d > 1].max()) if (d > 1).any() else 0.0
     rms = float(np.sqrt(np.mean(ref ** 2)))
     big = np.abs(ref) >= near_zero * rms
     frac = float((d > 0).mean())
-    print(f"[16-bit] max_abs_vs_rounded={ma:.3e} max_ulp(|y|>={near_zero:g}rms)="
-          f"{int(d[big].max()) if big.any() else 0} flips={frac:.4f} "
-          f"max_ulp_all={int(d.max())}")
-    assert ma <= atol, f"max_abs vs rounded oracle {ma:.3e}"
+    print(f"[16-bit] max_abs_vs_rounded={ma:.3e} (beyond 1-unit flips {ma_noflip:.3e}) "
+          f"max_ulp(|y|>={near_zero:g}rms)={int(d[big].max()) if big.any() else 0} "
+          f"flips={frac:.4f} max_ulp_all={int(d.max())}")
+    assert ma_noflip <= atol, f"max_abs vs rounded oracle beyond 1-unit flips {ma_noflip:.3e}"
     assert not big.any() or d[big].max() <= 1, f"max ulp distance {d[big].max()}"
     assert frac <= max_flip_frac, f"1-ulp flips {frac:.4f}"
     return frac

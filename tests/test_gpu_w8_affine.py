@@ -17,14 +17,21 @@ TORCH = {o.BF16: torch.bfloat16, o.F16: torch.float16}
 
 
 def _problem(m, n, k, g, dtype, sdtype, seed):
-    rng = np.random.default_rng(seed)
-    words = rng.integers(0, 2 ** 32, (n, k // 4), dtype=np.uint64).astype(np.uint32)
-    sf = (rng.random((n, k // g)) * 2e-3 + 1e-4).astype(np.float32)
-    bf = (-(rng.random((n, k // g)) * 0.25)).astype(np.float32)
+    """Weights N(0, 0.02) quantized per group of g with 255 min/max bins
+    (scale (max-min)/255, bias min, as stored; codes rint((w-b)/s)), so the
+    outputs have the magnitudes of a real projection."""
+    w = o.randn(seed, 11, n * k, 0.02).reshape(n, k // g, g).astype(np.float64)
+    lo, hi = w.min(-1), w.max(-1)
+    sf, bf = ((hi - lo) / 255).astype(np.float32), lo.astype(np.float32)
     if sdtype == o.F32:
         s, b = sf, bf
+        s64, b64 = sf.astype(np.float64), bf.astype(np.float64)
     else:
         s, b = o.round16(sf, sdtype), o.round16(bf, sdtype)
+        s64 = o.bits_to_f32(s, sdtype).astype(np.float64)
+        b64 = o.bits_to_f32(b, sdtype).astype(np.float64)
+    u = np.clip(np.rint((w - b64[..., None]) / s64[..., None]), 0, 255).astype(np.uint8)
+    words = np.ascontiguousarray(u.reshape(n, k)).view(np.uint32)
     x = o.randn16(seed, 7, m * k, 1.0, dtype).reshape(m, k)
     return x, words, s, b
 
@@ -114,8 +121,8 @@ def test_loaded_w8_projection_any_rows(gpu, tmp_path, backend, rows):
     x = o.randn16(4, rows, rows * 256).reshape(rows, 256)
     xt = up16(x, o.BF16, gpu)
     y = p8(xt)
-    assert y.shape == (rows, 256) and y.dtype == torch.bfloat16
     words, sb, bb = tensors[W8 + ".weight"], tensors[W8 + ".scales"], tensors[W8 + ".biases"]
+    assert y.shape == (rows, words.shape[0]) and y.dtype == torch.bfloat16
     w8 = o.w8_unpack_affine(words)
     sc = o.bits_to_f32(sb, o.BF16)[:, 0].copy()
     if backend in ("auto", "w8a8"):
