@@ -239,6 +239,29 @@ int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes,
                               const int64_t* strides, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of sparkq_int8kv_sdpa_decode, with the same
+ * arguments, checks, kernels and results, minus the workspace. No
+ * counterpart in the reference: it is for callers that cannot allocate or
+ * hold a workspace (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Its scratch space (split counters and
+ * partials) is a fixed 8 MiB array of device memory per GPU, held until the
+ * process ends; a call whose split decode needs more (the size
+ * sparkq_int8kv_sdpa_workspace_bytes reports: at most 64 splits per batch,
+ * so B=8, Hq=32, N=32768 needs 1.1 MB at D=128, and up to 64 query heads
+ * at D=256 fit for any B and N) returns SPARKQ_ERR_UNSUPPORTED. The first call on a device resolves the array's
+ * address and clears its counters with a kernel on `stream`; every call
+ * leaves the counters zero. All calls on one GPU share the array: calls that
+ * overlap in time on one GPU (different streams or threads) race and give
+ * wrong results; serialise them on one stream. */
+int sparkq_int8kv_sdpa_decode_noalloc(const void* q, const void* k_codes,
+                                      const void* k_scales, const void* k_biases,
+                                      const void* v_codes, const void* v_scales,
+                                      const void* v_biases, void* out, int64_t B,
+                                      int64_t Hq, int64_t Hkv, int64_t N,
+                                      int64_t D, int group_size, int kv_format,
+                                      int q_dtype, int out_dtype, float scale,
+                                      const int64_t* strides, void* stream);
+
 /* Symmetric int8 KV quantizer for the S8_F16SCALE format (the quantize-on-
  * append producer, mlx-lm QuantizedKVCache as configured by
  * spark_mlx_llm/generation.py:316-329,339-384): per row of D values,

@@ -41,6 +41,12 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
                        int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int G, int fmt,
                        int qdt, int odt, float scale, const int64_t* strides, void* ws,
                        size_t wsb, hipStream_t st);
+int int8kv_sdpa_decode_noalloc(const void* q, const void* kc, const void* ks, const void* kb,
+                               const void* vc, const void* vs, const void* vb, void* out,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int G,
+                               int fmt, int qdt, int odt, float scale, const int64_t* strides,
+                               hipStream_t st);
+size_t decode_scratch_bytes();
 int kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_t D, int xdt,
                    hipStream_t st);
 int kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B, int64_t H,
@@ -302,12 +308,13 @@ size_t sparkq_int8kv_sdpa_workspace_bytes(int64_t B, int64_t Hq, int64_t N, int6
   return sdpa_workspace(B, Hq, N, D);
 }
 
-int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes, const void* k_scales,
-                              const void* k_biases, const void* v_codes, const void* v_scales,
-                              const void* v_biases, void* out, int64_t B, int64_t Hq,
-                              int64_t Hkv, int64_t N, int64_t D, int group_size, int kv_format,
-                              int q_dtype, int out_dtype, float scale, const int64_t* strides,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+// Argument checks of the decode entry points (the reference's messages where
+// it has them, X/spark_mlx_ext/int8_quantized_sdpa.py:188-224).
+static int check_sdpa_decode(const void* q, const void* k_codes, const void* k_scales,
+                             const void* k_biases, const void* v_codes, const void* v_scales,
+                             const void* v_biases, const void* out, int64_t B, int64_t Hq,
+                             int64_t Hkv, int64_t N, int64_t D, int group_size, int kv_format,
+                             int q_dtype, int out_dtype, float scale, const int64_t* strides) {
   REQUIRE(q && k_codes && k_scales && v_codes && v_scales && out && strides,
           "int8kv_sdpa_decode: null tensor pointer");
   REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && N > 0 && D > 0,
@@ -343,10 +350,44 @@ int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes, const void* k_
                         fits_range({N, std::max(strides[5], strides[11]), 2}),
                     "int8kv_sdpa_decode: cache too long for 32-bit offsets");
   REQUIRE(aligned(k_codes, 8) && aligned(v_codes, 8), "int8kv_sdpa_decode: codes must be 8-byte aligned");
+  return SPARKQ_OK;
+}
+
+int sparkq_int8kv_sdpa_decode(const void* q, const void* k_codes, const void* k_scales,
+                              const void* k_biases, const void* v_codes, const void* v_scales,
+                              const void* v_biases, void* out, int64_t B, int64_t Hq,
+                              int64_t Hkv, int64_t N, int64_t D, int group_size, int kv_format,
+                              int q_dtype, int out_dtype, float scale, const int64_t* strides,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_sdpa_decode(q, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
+                                 out, B, Hq, Hkv, N, D, group_size, kv_format, q_dtype,
+                                 out_dtype, scale, strides))
+    return rc;
   DEVICE_OK();
   return int8kv_sdpa_decode(q, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases, out, B,
                             Hq, Hkv, N, D, group_size, kv_format, q_dtype, out_dtype, scale,
                             strides, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int sparkq_int8kv_sdpa_decode_noalloc(const void* q, const void* k_codes, const void* k_scales,
+                                      const void* k_biases, const void* v_codes,
+                                      const void* v_scales, const void* v_biases, void* out,
+                                      int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                                      int group_size, int kv_format, int q_dtype, int out_dtype,
+                                      float scale, const int64_t* strides, void* stream) {
+  if (int rc = check_sdpa_decode(q, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
+                                 out, B, Hq, Hkv, N, D, group_size, kv_format, q_dtype,
+                                 out_dtype, scale, strides))
+    return rc;
+  REQUIRE_SUPPORTED(sdpa_workspace(B, Hq, N, D) <= decode_scratch_bytes(),
+                    "int8kv_sdpa_decode_noalloc: B=%lld Hq=%lld N=%lld D=%lld needs %zu bytes of "
+                    "scratch, above the fixed %zu",
+                    (long long)B, (long long)Hq, (long long)N, (long long)D,
+                    sdpa_workspace(B, Hq, N, D), decode_scratch_bytes());
+  DEVICE_OK();
+  return int8kv_sdpa_decode_noalloc(q, k_codes, k_scales, k_biases, v_codes, v_scales, v_biases,
+                                    out, B, Hq, Hkv, N, D, group_size, kv_format, q_dtype,
+                                    out_dtype, scale, strides, (hipStream_t)stream);
 }
 
 int sparkq_kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_t D,

@@ -27,6 +27,7 @@
 //                          strided cache (s8 + fp16 scale; MLX affine u8).
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1876,6 +1877,72 @@ int kv_quantize_s8(const void* x, int8_t* codes, void* scales, int64_t R, int64_
   hipLaunchKernelGGL(kv_quantize_s8_kernel, dim3((unsigned)cdiv(R, 4)), dim3(256), 0, st, x,
                      codes, (uint16_t*)scales, R, D, xdt);
   return check_launch("kv_quantize_s8_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the workspace is a file-scope device array, one
+// copy per GPU, held until the process ends. Its counters start at zero (the
+// first use on a device clears them with a fill kernel) and every decode
+// leaves them zero; the partials need no clearing. The host never passes
+// the array's name to a kernel: it is a host-side stand-in, and the device
+// address comes from hipGetSymbolAddress, resolved once per device.
+// ---------------------------------------------------------------------------
+constexpr size_t kDecodeScratchBytes = 8u << 20;
+static __device__ __align__(256) unsigned char g_decode_scratch[kDecodeScratchBytes];
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t* p, int64_t words) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (int64_t)gridDim.x * 256)
+    p[i] = 0u;
+}
+
+static void* g_decode_scratch_ptr[64];
+static std::mutex g_decode_scratch_mu;
+
+// Device address of this GPU's scratch array, resolved (and its counters
+// cleared on stream st) on the first call per device; null on failure.
+static void* decode_scratch(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_decode_scratch_mu);
+  if (g_decode_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_decode_scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error(SPARKQ_ERR_DEVICE, "hipGetSymbolAddress(decode scratch): %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(16), dim3(256), 0, st, (uint32_t*)ptr,
+                       (int64_t)(kCounterBytes / 4));
+    if (hipGetLastError() != hipSuccess) {
+      set_error(SPARKQ_ERR_DEVICE, "decode scratch: clearing the counters failed");
+      return nullptr;
+    }
+    g_decode_scratch_ptr[dev] = ptr;
+  }
+  return g_decode_scratch_ptr[dev];
+}
+
+size_t decode_scratch_bytes() { return kDecodeScratchBytes; }
+
+int int8kv_sdpa_decode_noalloc(const void* q, const void* kc, const void* ks, const void* kb,
+                               const void* vc, const void* vs, const void* vb, void* out,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int G,
+                               int fmt, int qdt, int odt, float scale, const int64_t* strides,
+                               hipStream_t st) {
+  const size_t need = sdpa_workspace(B, Hq, N, D);
+  if (need > kDecodeScratchBytes)
+    return set_error(SPARKQ_ERR_UNSUPPORTED,
+                     "int8kv_sdpa_decode_noalloc: B=%lld Hq=%lld N=%lld D=%lld needs %zu bytes of "
+                     "scratch, above the fixed %zu",
+                     (long long)B, (long long)Hq, (long long)N, (long long)D, need,
+                     kDecodeScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = decode_scratch(st);
+    if (ws == nullptr) return SPARKQ_ERR_DEVICE;
+  }
+  return int8kv_sdpa_decode(q, kc, ks, kb, vc, vs, vb, out, B, Hq, Hkv, N, D, G, fmt, qdt, odt,
+                            scale, strides, ws, need > 0 ? kDecodeScratchBytes : 0, st);
 }
 
 }  // namespace sparkq

@@ -49,6 +49,8 @@ SIGNATURES = {
     "sparkq_int8kv_sdpa_workspace_bytes": (SZ, [I64, I64, I64, I64]),
     "sparkq_int8kv_sdpa_decode": (I, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64,
                                       I, I, I, I, F, P, P, SZ, P]),
+    "sparkq_int8kv_sdpa_decode_noalloc": (I, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64,
+                                              I, I, I, I, F, P, P]),
     "sparkq_kv_quantize_s8": (I, [P, P, P, I64, I64, I, P]),
     "sparkq_kv_append": (I, [P, P, P, P, I64, I64, I64, I64, I64, I, I, I, P, P]),
     "sparkq_int8kv_sdpa_prefill": (I, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I, I,

@@ -213,3 +213,20 @@ def test_ranges_beyond_one_buffer_descriptor_are_unsupported():
     rc, msg = _rc("sparkq_int8kv_sdpa_prefill_affine", dummy, dummy, dummy, dummy, dummy, dummy,
                   dummy, dummy, 1, 8, 8, 2, 16, 128, 32, 1, 2, 2, f(0.1), aff, None, 0, None)
     assert rc == -1 and "token strides must be positive" in msg
+
+
+def test_noalloc_decode_refuses_oversized_scratch_without_a_device():
+    """The allocation-free decode keeps a fixed 8 MiB scratch per GPU: a
+    split decode that needs more (here 256 query heads of 256 dims) is
+    refused before any device call; 64 heads at D=256 fit."""
+    from sparkq import _lib
+
+    dummy = P(4096)
+    st = (ctypes.c_int64 * 12)(0, 0, 256, 0, 0, 1, 0, 0, 256, 0, 0, 1)
+    need = _lib.lib().sparkq_int8kv_sdpa_workspace_bytes(1, 256, 32768, 256)
+    assert need > 8 << 20
+    rc, msg = _rc("sparkq_int8kv_sdpa_decode_noalloc", dummy, dummy, dummy, None, dummy, dummy,
+                  None, dummy, 1, 256, 32, 32768, 256, 32, 0, 2, 2, ctypes.c_float(0.1), st, None)
+    assert rc == -2 and "scratch" in msg
+    for b in (1, 2, 3, 8, 64):
+        assert _lib.lib().sparkq_int8kv_sdpa_workspace_bytes(b, 64, 32768, 256) <= 8 << 20
