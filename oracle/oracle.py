@@ -22,7 +22,7 @@ __all__ = [
     "a8_quantize", "w8_quantize_channel", "w8_unpack_affine",
     "int8_matmul", "w8a8_epilogue",
     "kv_quantize_s8", "kv_quantize_affine_u8", "kv_dequantize_s8",
-    "kv_dequantize_affine_u8", "sdpa_decode", "sdpa_prefill",
+    "kv_dequantize_affine_u8", "sdpa_decode", "sdpa_prefill", "sdpa_prefill_rounded",
     "cpu_w4a16_gemv", "scalar_f32_to_bf16", "scalar_f32_to_f16",
     "scalar_f16_to_f32",
     "add16", "rms_norm16", "gelu16", "gelu_mul16", "rope16", "ffn_block", "qkv_rope",
@@ -385,6 +385,39 @@ def sdpa_prefill(q, kdq, vdq, scale: float, causal: bool) -> np.ndarray:
     p = np.exp(scores)
     p /= p.sum(axis=-1, keepdims=True)
     return p @ v
+
+
+def sdpa_prefill_rounded(q16, kdq, vdq, scale: float, causal: bool,
+                         dtype: int = BF16) -> np.ndarray:
+    """Multi-token attention with the rounding points of the reference's
+    prefill kernel spark_affine_u8_sdpa_prefill
+    (X/spark_mlx_ext/_int8_prefill_sources.py:60-146): K and V dequantize to
+    the query dtype T (:73, :115), the softmax weights are rounded to T for
+    the PV product while the normalizer sums the unrounded weights (:99-103),
+    and scores, normalizer and output stay wide. Scores are
+    (q . k) * scale * log2(e) in float64 with q exact (the reference also
+    rounds q * scale to T, :38-39, a loss this oracle does not restate); a
+    row's weights are 2^(s - c) with the integer c = ceil(max_row s), and
+    since rounding to T commutes with powers of two, T(2^(s-c)) * 2^c does
+    not depend on the integer chosen. q16 [B,Hq,L,D] 16-bit patterns of
+    dtype; kdq/vdq [B,Hkv,N,D] dequantized values, rounded to T here. Returns
+    float64 [B,Hq,L,D]."""
+    q = bits_to_f32(q16, dtype).astype(np.float64)
+    kt = bits_to_f32(round16(np.asarray(kdq, np.float32), dtype), dtype).astype(np.float64)
+    vt = bits_to_f32(round16(np.asarray(vdq, np.float32), dtype), dtype).astype(np.float64)
+    bsz, hq, length, d = q.shape
+    hkv, n = kt.shape[1], kt.shape[2]
+    rep = hq // hkv
+    k = np.repeat(kt, rep, axis=1)
+    v = np.repeat(vt, rep, axis=1)
+    s2 = (q @ np.swapaxes(k, -1, -2)) * (scale * np.log2(np.e))
+    if causal:
+        vis = np.arange(n - length, n)[:, None] >= np.arange(n)[None, :]
+        s2 = np.where(vis, s2, -np.inf)
+    c = np.ceil(s2.max(axis=-1, keepdims=True))
+    p = np.exp2(s2 - c)
+    pt = bits_to_f32(round16(p.astype(np.float32), dtype), dtype).astype(np.float64)
+    return (pt @ v) / p.sum(axis=-1, keepdims=True)
 
 
 # ---------------------------------------------------------------------------

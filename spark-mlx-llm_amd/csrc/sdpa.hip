@@ -1129,7 +1129,11 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void sdpa_prefill_affine_ker
   // One block. The running max of a row moves only when a block's max
   // exceeds it by more than 8 (log2 units): until then the weights
   // exp2(s - m) stay below 2^8 and the accumulators are not rescaled, so the
-  // rescale (a wave-uniform branch) runs for few blocks.
+  // rescale (a wave-uniform branch) runs for few blocks. It moves to the
+  // ceiling of the block max: with an integer offset the weights rounded to
+  // T are T(exp2(s)) scaled by a power of two (rounding commutes with it), so
+  // they do not depend on the block order, and every rescale factor is an
+  // exact power of two.
   auto compute = [&](const unsigned char* buf, int t0) {
     f32x4_t sc[2][2];
 #pragma unroll
@@ -1159,8 +1163,9 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void sdpa_prefill_affine_ker
       }
       mb = max_rows4(mb);
       up[rt] = mb > mrun[rt] + 8.0f;
-      alpha[rt] = up[rt] ? exp2_guarded(mrun[rt] - mb, mrun[rt] != kNegInf) : 1.0f;
-      mrun[rt] = up[rt] ? mb : mrun[rt];
+      const float mnew = ceilf(mb);
+      alpha[rt] = up[rt] ? exp2_guarded(mrun[rt] - mnew, mrun[rt] != kNegInf) : 1.0f;
+      mrun[rt] = up[rt] ? mnew : mrun[rt];
       // a row with nothing visible yet keeps m = -inf; its weights are 0
       const float mu = mrun[rt] == kNegInf ? 0.0f : mrun[rt];
       float p[8], ps = 0.0f;

@@ -200,10 +200,17 @@ def test_prefill_affine_matches_oracle(gpu, b, hq, hkv, length, n, d, g, causal,
                                      out_dtype=torch.float32)
     y16 = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=scale, group_size=g, mask=mask)
     torch.cuda.synchronize()
-    ref = o.sdpa_prefill(o.bits_to_f32(q16, qdtype), kd, vd, scale, causal)
     out = y32.cpu().numpy().astype(np.float64)
+    # the oracle with the reference kernel's rounding points (K, V and the
+    # softmax weights rounded to the query dtype)
+    refr = o.sdpa_prefill_rounded(q16, kd, vd, scale, causal, qdtype)
+    rl, rr, ma = rel_l2(out, refr), _row_rel(out, refr), max_abs(out, refr)
+    print(f"  vs rounding-faithful oracle: rel_l2={rl:.3e} worst_row={rr:.3e} max_abs={ma:.3e}")
+    assert rl <= 1e-3 and ma <= 2e-2
+    # and against exact float64 attention, where the roundings themselves show
+    ref = o.sdpa_prefill(o.bits_to_f32(q16, qdtype), kd, vd, scale, causal)
     rl, rr, ma = rel_l2(out, ref), _row_rel(out, ref), max_abs(out, ref)
-    print(f"  rel_l2={rl:.3e} worst_row={rr:.3e} max_abs={ma:.3e}")
+    print(f"  vs exact oracle: rel_l2={rl:.3e} worst_row={rr:.3e} max_abs={ma:.3e}")
     tol_l2, tol_row = _AFF_TOL[qdtype]
     assert rl <= tol_l2 and rr <= tol_row and ma <= 2e-2
     # the 16-bit output is the fp32 result rounded once
@@ -212,14 +219,15 @@ def test_prefill_affine_matches_oracle(gpu, b, hq, hkv, length, n, d, g, causal,
 
 @pytest.mark.parametrize("d,g,qdtype", [(256, 32, o.BF16), (128, 64, o.F16), (64, 32, o.BF16)])
 def test_prefill_affine_identical_keys_mean_of_values(gpu, d, g, qdtype):
-    """Identical keys give every visible token the weight 1 exactly, so row i
-    returns the mean of the dequantized (query-dtype) V over its N-L+i+1
-    visible tokens: pins the V operand layout and the causal limits."""
+    """Zero keys (scales and biases 0) give every visible token the score 0
+    and the weight 1 exactly, so row i returns the mean of the dequantized
+    (query-dtype) V over its N-L+i+1 visible tokens: pins the V operand
+    layout and the causal limits."""
     import sparkq
 
     b, hq, hkv, length, n = 1, 8, 2, 40, 77
     keys, vals, kd, vd = _affine_cache(gpu, b, hkv, n, d, g, 7, qdtype)
-    keys1 = tuple(t[:, :, :1].expand(-1, -1, n, -1).contiguous() for t in keys)
+    keys1 = (keys[0], torch.zeros_like(keys[1]), torch.zeros_like(keys[2]))
     q16 = _x16(7, 63, (b, hq, length, d), qdtype)
     y = sparkq.int8_quantized_sdpa(up16(q16, qdtype, gpu), keys1, vals, scale=0.1, group_size=g,
                                    mask="causal", out_dtype=torch.float32).cpu().numpy()
@@ -246,8 +254,12 @@ def test_prefill_affine_split_repeats(gpu, b, hq, hkv, length, n, d):
     y2 = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=0.08, mask="causal", out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
-    ref = o.sdpa_prefill(o.bits_to_f32(q16, o.BF16), kd, vd, 0.08, True)
     out = y1.cpu().numpy().astype(np.float64)
+    # the splits' partials merge exactly (integer offsets, power-of-two
+    # factors), so the split result meets the rounding-faithful oracle too
+    refr = o.sdpa_prefill_rounded(q16, kd, vd, 0.08, True, o.BF16)
+    assert rel_l2(out, refr) <= 1e-3 and max_abs(out, refr) <= 2e-2
+    ref = o.sdpa_prefill(o.bits_to_f32(q16, o.BF16), kd, vd, 0.08, True)
     assert rel_l2(out, ref) <= _AFF_TOL[o.BF16][0] and _row_rel(out, ref) <= _AFF_TOL[o.BF16][1]
 
 

@@ -113,7 +113,7 @@ def test_kv_quantizer_bit_exact(gpu):
     assert np.array_equal(sc.cpu().numpy().view(np.uint16), rs)
 
 
-@pytest.mark.parametrize("b,n", [(1, 32768), (8, 4096)])
+@pytest.mark.parametrize("b,n", [(1, 4096), (1, 32768), (8, 4096), (8, 32768)])
 def test_benchmark_shapes_sampled_heads(gpu, b, n):
     """Full kernels at benchmark sizes; oracle on two KV heads."""
     hq, hkv, d = 32, 8, 128

@@ -274,7 +274,9 @@ def test_deterministic(gpu):
 # benchmark shapes: full kernels, oracle on sampled rows/columns
 # ---------------------------------------------------------------------------
 
-PROJ = {"qkv": (3584, 2560), "gate_up": (19456, 2560), "down": (2560, 9728)}
+# the single 2560x2560 projection and the three projections of one layer
+PROJ = {"square": (2560, 2560), "qkv": (3584, 2560), "gate_up": (19456, 2560),
+        "down": (2560, 9728)}
 
 
 def _gpu_weights(dev, n, k, g, seed):

@@ -114,6 +114,36 @@ def test_w8a8_linear_bit_exact(gpu, m, n, k, dtype, with_bias):
         assert np.array_equal(down16(y)[:, cols], o.round16(ref, dtype))
 
 
+BENCH_PROJ = {"qkv": (3584, 2560), "gate_up": (19456, 2560), "down": (2560, 9728)}
+
+
+@pytest.mark.parametrize("proj", list(BENCH_PROJ))
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_w8a8_benchmark_pairs_bit_exact(gpu, m, proj):
+    """Every (rows, projection) pair of the W8A8 decode benchmark: int32
+    accumulators (through the raw entry point) and the fp32 epilogue bit for
+    bit on sampled columns."""
+    import sparkq
+
+    n, k = BENCH_PROJ[proj]
+    print(f"[case] w8a8 m={m} proj={proj}", flush=True)
+    wq, wsc = _w8(n, k, seed=9)
+    x16 = _x(m, k, o.BF16, seed=m)
+    xf = o.bits_to_f32(x16, o.BF16)
+    xt = up16(x16, o.BF16, gpu)
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    y32 = sparkq.w8a8_linear(xt, wt, st, out_dtype=torch.float32).cpu().numpy()
+    qa, sa = o.a8_quantize(xf)
+    qt, sat = sparkq.quantize_per_token(xt)
+    assert np.array_equal(qt.cpu().numpy(), qa) and np.array_equal(sat.cpu().numpy(), sa)
+    acc_t = sparkq.int8_matmul_int32(qt, wt).cpu().numpy()
+    cols = np.sort(np.random.default_rng(m + n).choice(n, 512, replace=False))
+    acc = o.int8_matmul(qa, wq[cols])
+    assert np.array_equal(acc_t[:, cols], acc)
+    ref = o.w8a8_epilogue(acc, sa, wsc[cols])
+    assert np.array_equal(y32[:, cols].view(np.uint32), ref.view(np.uint32))
+
+
 def test_w8a8_decode_zero_row_and_repeat(gpu):
     """Decode GEMV with an all-zero activation row (scale 1, zero codes) and a
     second call on the same buffers giving identical bits."""

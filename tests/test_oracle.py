@@ -625,3 +625,59 @@ def test_sdpa_prefill_oracle_pins():
     p = np.exp(sc - sc.max(-1, keepdims=True))
     wrong = (p / p.sum(-1, keepdims=True)) @ vr
     assert not np.allclose(wrong, causal, atol=1e-3)
+
+
+def test_sdpa_prefill_rounded_pins():
+    """sdpa_prefill_rounded (the reference prefill kernel's rounding points)
+    against an independent loop that rounds through numpy's float16 on a tiny
+    case; with values exact in T and weights that are powers of two it is
+    the unrounded oracle; identical keys give the mean of the rounded V over
+    each row's visible tokens; its weights' rounding does not depend on the
+    integer offset; and it stays within the bf16 bound of the exact oracle."""
+    b, hq, hkv, length, n, d = 1, 2, 1, 3, 6, 8
+    q = o.randn(6, 1, b * hq * length * d).reshape(b, hq, length, d)
+    k = o.randn(6, 2, b * hkv * n * d).reshape(b, hkv, n, d)
+    v = o.randn(6, 3, b * hkv * n * d).reshape(b, hkv, n, d)
+    q16 = o.f16_bits(q)
+    y = o.sdpa_prefill_rounded(q16, k, v, 0.4, True, o.F16)
+    # independent loop with numpy float16
+    qf = q16.view(np.float16).astype(np.float64)
+    kf = k.astype(np.float16).astype(np.float64)
+    vf = v.astype(np.float16).astype(np.float64)
+    ref = np.zeros_like(y)
+    for h in range(hq):
+        for i in range(length):
+            vis = n - length + i + 1
+            s = np.array([qf[0, h, i] @ kf[0, 0, t] for t in range(vis)]) * 0.4 / math.log(2)
+            c = math.ceil(s.max())
+            p = [2.0 ** (st - c) for st in s]
+            pt = [float(np.float16(np.float32(pp))) for pp in p]
+            ref[0, h, i] = sum(pt[t] * vf[0, 0, t] for t in range(vis)) / sum(p)
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-12)
+    # zero keys: every weight is exactly 1, so each row is the mean of the
+    # T-rounded values it sees (with other identical keys the rounded weight
+    # over the unrounded normalizer scales that mean by T(p)/p, as in the
+    # reference kernel)
+    same = o.sdpa_prefill_rounded(q16, np.zeros_like(k), v, 0.4, True, o.F16)
+    for i in range(length):
+        vis = n - length + i + 1
+        assert np.allclose(same[0, :, i], vf[0, 0, :vis].mean(0), atol=1e-12)
+    # against the exact oracle: values already in T and integer log2 scores
+    # leave nothing to round
+    kk = np.zeros_like(k)
+    kk[..., 0] = np.arange(n)[None, None, :]
+    qq = np.zeros((b, hq, length, d), np.float32)
+    qq[..., 0] = 1.0
+    vv = vf.astype(np.float32)
+    y0 = o.sdpa_prefill_rounded(o.f16_bits(qq), kk, vv, math.log(2), True, o.F16)
+    y1 = o.sdpa_prefill(qq, kk, vv, math.log(2), True)
+    assert np.allclose(y0, y1, rtol=1e-12, atol=1e-12)
+    # bf16 rounding of K, V and the weights moves a N(0,1) problem by ~1e-3
+    bq, l2, n2, d2 = 1, 16, 40, 64
+    q2 = o.randn(7, 1, bq * 4 * l2 * d2).reshape(bq, 4, l2, d2)
+    k2 = o.randn(7, 2, bq * 2 * n2 * d2).reshape(bq, 2, n2, d2)
+    v2 = o.randn(7, 3, bq * 2 * n2 * d2).reshape(bq, 2, n2, d2)
+    q2b = o.bf16_bits(q2)
+    yr = o.sdpa_prefill_rounded(q2b, k2, v2, 0.125, True, o.BF16)
+    ye = o.sdpa_prefill(o.bits_to_f32(q2b, o.BF16), k2, v2, 0.125, True)
+    assert 3e-4 < rel_l2(yr, ye) < 1e-2
