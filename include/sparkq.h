@@ -421,6 +421,22 @@ int sparkq_rope(const void* x, void* out, int64_t rows, int64_t L, int64_t D, in
                 int traditional, float base, float scale, int64_t offset, int dtype,
                 void* stream);
 
+/* Head-wise sigmoid gate of the attention output, the step between the
+ * attention and the output projection in _compiled_affine_output,
+ * _compiled_w8a16_output and _module_output (spark_mlx_llm/ops/
+ * attention_output.py:69-95, called from spark_mlx_llm/model.py:205):
+ *   gate[b,l,h] = T(sigmoid(float(T(x[b,l,:] . gate_w[h,:]))))
+ *   out[b,l,h*D+d] = T(attn[b,h,l,d] * gate[b,l,h])
+ * x [B,L,hidden], attn [B,H,L,D] and gate_w [H,hidden] (the bias-free
+ * g_proj) contiguous in dtype (BF16 or F16); out [B,L,H*D], the transposed
+ * and gated output ready for the output projection; gate_out [B,L,H] or
+ * NULL. hidden % 8 == 0. The sigmoid is that of the rounded
+ * dot, computed so that its rounding to T is the exact sigmoid's. */
+int sparkq_attention_gate(const void* x, const void* attn, const void* gate_w,
+                          void* out, void* gate_out, int64_t B, int64_t L,
+                          int64_t H, int64_t D, int64_t hidden, int dtype,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,7 +25,7 @@ __all__ = [
     "kv_dequantize_affine_u8", "sdpa_decode", "sdpa_prefill", "sdpa_prefill_rounded",
     "cpu_w4a16_gemv", "scalar_f32_to_bf16", "scalar_f32_to_f16",
     "scalar_f16_to_f32",
-    "add16", "rms_norm16", "gelu16", "gelu_mul16", "rope16", "ffn_block", "qkv_rope",
+    "attention_gate16", "add16", "rms_norm16", "gelu16", "gelu_mul16", "rope16", "ffn_block", "qkv_rope",
 ]
 
 F32, F16, BF16 = 0, 1, 2
@@ -553,3 +553,22 @@ def cpu_w4a16_gemv(x16, wq, s, b, group_size: int, threads: int = 0):
     if used < 0:
         raise ValueError("unsupported CPU baseline shape")
     return y, used
+
+
+def attention_gate16(x16, attn16, gw16, dtype: int = BF16):
+    """The head-wise gate of spark_mlx_llm/ops/attention_output.py:69-95 in
+    the 16-bit graph's roundings: gate = T(sigmoid(T(x . g_proj[h]))) with the
+    dot and the sigmoid exact (float64) before each rounding, and
+    out[b,l,h*D+d] = T(attn[b,h,l,d] * gate[b,l,h]). x16 [B,L,hidden],
+    attn16 [B,H,L,D], gw16 [H,hidden] as 16-bit patterns; returns the gate
+    [B,L,H] and out [B,L,H*D] as 16-bit patterns."""
+    x = bits_to_f32(x16, dtype).astype(np.float64)
+    a = bits_to_f32(attn16, dtype).astype(np.float64)
+    w = bits_to_f32(gw16, dtype).astype(np.float64)
+    dot = bits_to_f32(round16((x @ w.T).astype(np.float32), dtype), dtype).astype(np.float64)
+    gate = round16((1.0 / (1.0 + np.exp(-dot))).astype(np.float32), dtype)
+    g = bits_to_f32(gate, dtype).astype(np.float64)
+    b, h, length, d = a.shape
+    prod_ = np.swapaxes(a, 1, 2) * g[..., None]
+    out = round16(prod_.astype(np.float32), dtype).reshape(b, length, h * d)
+    return gate, out

@@ -82,6 +82,9 @@ int rope(const void* x, void* out, int64_t rows, int64_t L, int64_t D, int dims,
          float base, float scale, int64_t offset, int dt, hipStream_t st);
 int rms_norm(const void* x, const void* xres, const void* w, float eps, void* hid, void* out,
              int64_t M, int64_t K, int dt, hipStream_t st);
+int attention_gate(const void* x, const void* attn, const void* gw, void* out, void* gate_out,
+                   int64_t B, int64_t L, int64_t H, int64_t D, int64_t K, int dt,
+                   hipStream_t st);
 
 static thread_local char g_last_error[512] = "";
 
@@ -691,6 +694,24 @@ int sparkq_rms_norm(const void* x, const void* residual, const void* weight, flo
   if (M == 0) return 0;
   DEVICE_OK();
   return rms_norm(x, residual, weight, eps, hidden_out, out, M, K, dtype, (hipStream_t)stream);
+}
+
+int sparkq_attention_gate(const void* x, const void* attn, const void* gate_w, void* out,
+                          void* gate_out, int64_t B, int64_t L, int64_t H, int64_t D,
+                          int64_t hidden, int dtype, void* stream) {
+  REQUIRE(x && attn && gate_w && out, "attention_gate: null tensor pointer");
+  REQUIRE(B > 0 && L > 0 && H > 0 && D > 0 && hidden > 0, "attention_gate: empty shape");
+  REQUIRE(B * L <= kI32Max && H <= 4LL * 65535 && D <= kI32Max && hidden <= kI32Max &&
+              B * L * H * D <= (1LL << 40) && B * L * hidden <= (1LL << 40),
+          "attention_gate: shape too large");
+  REQUIRE_SUPPORTED(hidden % 8 == 0, "attention_gate: hidden size must be a multiple of 8");
+  REQUIRE_SUPPORTED(is_half_dtype(dtype), "attention_gate: dtype must be bfloat16 or float16");
+  REQUIRE(aligned(x, 16) && aligned(gate_w, 16) && aligned(attn, 2) && aligned(out, 2) &&
+              aligned(gate_out, 2),
+          "attention_gate: x and the gate weight must be 16-byte aligned");
+  DEVICE_OK();
+  return attention_gate(x, attn, gate_w, out, gate_out, B, L, H, D, hidden, dtype,
+                        (hipStream_t)stream);
 }
 
 }  // extern "C"

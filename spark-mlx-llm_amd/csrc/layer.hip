@@ -252,4 +252,77 @@ int qkv_rope(const void* x, const uint32_t* w, const void* s, const void* b, voi
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Head-wise sigmoid gate of the attention output (the body of
+// _compiled_affine_output / _compiled_w8a16_output / _module_output,
+// spark_mlx_llm/ops/attention_output.py:69-95):
+//   gate[m, h] = T(sigmoid(float(T(x[m, :] . g_proj[h, :]))))
+//   out[m, h*D + d] = T(attn[b, h, l, d] * gate[m, h]),  m = b*L + l
+// i.e. the transpose of [B,H,L,D] to [B,L,H*D] with each head scaled, ready
+// for the output projection. One wave per (token, head): the dot in fp32 in a
+// fixed order (lanes stride the row in 16-byte pieces, then the wave sum),
+// rounded to T as the 16-bit matmul returns it; sigmoid in fp32, redone in
+// double where the fp32 value lies within 16 units of a T rounding tie, so
+// the gate is the rounding of the exact sigmoid; the product of two T values
+// is exact in fp32 and rounds once.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float sigmoid_for16(float t) {
+  float e = 1.0f / (1.0f + expf(-t));
+  const uint32_t u = __float_as_uint(e);
+  bool redo;
+  if constexpr (T::code == SPARKQ_BF16) {
+    const int low = (int)(u & 0xFFFFu) - 0x8000;
+    redo = low > -16 && low < 16;
+  } else {
+    const int low = (int)(u & 0x1FFFu) - 0x1000;
+    redo = (low > -16 && low < 16) || e < 6.2e-5f;
+  }
+  if (redo) e = (float)(1.0 / (1.0 + exp(-(double)t)));
+  return e;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_gate_kernel(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ attn,
+                                                        const uint16_t* __restrict__ gw,
+                                                        uint16_t* __restrict__ out,
+                                                        uint16_t* __restrict__ gate_out, int L,
+                                                        int H, int D, int K) {
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int64_t m = blockIdx.x;
+  if (h >= H) return;
+  const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(x + m * K);
+  const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(gw + (int64_t)h * K);
+  float acc = 0.0f;
+  for (int c = lane; c < K / 8; c += 64) {
+    const u32x4_t xv = xr[c], wv = wr[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = fmaf(lo16<T>(xv[e]), lo16<T>(wv[e]), acc);
+      acc = fmaf(hi16<T>(xv[e]), hi16<T>(wv[e]), acc);
+    }
+  }
+  const float dot = wave_sum(acc);
+  const uint16_t g16 = T::from_f32(sigmoid_for16<T>(T::to_f32(T::from_f32(dot))));
+  const float g = T::to_f32(g16);
+  if (gate_out && lane == 0) gate_out[m * H + h] = g16;
+  const int64_t b = m / L, l = m - b * L;
+  const uint16_t* src = attn + (((b * H + h) * L + l) * D);
+  uint16_t* dst = out + (m * H + h) * D;
+  for (int d = lane; d < D; d += 64) dst[d] = T::from_f32(T::to_f32(src[d]) * g);
+}
+
+int attention_gate(const void* x, const void* attn, const void* gw, void* out, void* gate_out,
+                   int64_t B, int64_t L, int64_t H, int64_t D, int64_t K, int dt,
+                   hipStream_t st) {
+  const dim3 grid((unsigned)(B * L), (unsigned)cdiv(H, 4));
+  auto* k = dt == SPARKQ_BF16 ? attn_gate_kernel<BF16> : attn_gate_kernel<F16>;
+  hipLaunchKernelGGL(k, grid, dim3(256), 0, st, (const uint16_t*)x, (const uint16_t*)attn,
+                     (const uint16_t*)gw, (uint16_t*)out, (uint16_t*)gate_out, (int)L, (int)H,
+                     (int)D, (int)K);
+  return check_launch("attn_gate_kernel");
+}
+
 }  // namespace sparkq

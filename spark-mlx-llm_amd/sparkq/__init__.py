@@ -9,6 +9,7 @@ from .ext import (
     QuantizedKVCache,
     W8A8Linear,
     affine_dequantize,
+    attention_gate,
     affine_quantize,
     affine_quantized_matmul,
     fused_ffn,
@@ -32,6 +33,7 @@ __all__ = [
     "QuantizedKVCache",
     "W8A8Linear",
     "affine_dequantize",
+    "attention_gate",
     "affine_quantize",
     "affine_quantized_matmul",
     "fused_ffn",

@@ -65,6 +65,7 @@ SIGNATURES = {
                             P]),
     "sparkq_rope": (I, [P, P, I64, I64, I64, I, I, F, F, I64, I, P]),
     "sparkq_rms_norm": (I, [P, P, P, F, P, P, I64, I64, I, P]),
+    "sparkq_attention_gate": (I, [P, P, P, P, P, I64, I64, I64, I64, I64, I, P]),
 }
 
 

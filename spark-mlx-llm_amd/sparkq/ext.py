@@ -23,6 +23,7 @@ from ._lib import BF16, F16, F32, KV_AFFINE_U8, KV_S8_F16SCALE
 
 __all__ = [
     "W8A8Linear",
+    "attention_gate",
     "affine_dequantize",
     "affine_quantize",
     "affine_quantized_matmul",
@@ -892,3 +893,31 @@ def fused_ffn(x, attention_output, norm_weight, eps: float, gate, up, down, *,
     normed = view(lin + hk, m * k, k)
     act = view(lin + 2 * hk, m * inter, inter)
     return out.view(x.shape), hidden, normed, act
+
+
+def attention_gate(x, output, gate_weight, *, return_gate: bool = False):
+    """Head-wise sigmoid gate of the attention output, transposed for the
+    output projection (spark_mlx_llm/ops/attention_output.py:69-95):
+    x [B,L,hidden], output [B,H,L,D], gate_weight [H,hidden] (a bias-free
+    g_proj) -> [B,L,H*D] = (output^T[b,l,h,:] * sigmoid(x[b,l] . g[h])),
+    with the 16-bit graph's roundings (the dot and the sigmoid each rounded
+    to the dtype, the product rounded once). With return_gate the [B,L,H]
+    gate is returned too."""
+    if any(not isinstance(t, torch.Tensor) for t in (x, output, gate_weight)):
+        raise TypeError("x, output and gate_weight must be tensors")
+    if output.ndim != 4 or x.ndim != 3 or gate_weight.ndim != 2:
+        raise ValueError("expected x [B,L,hidden], output [B,H,L,D] and gate_weight [H,hidden]")
+    b, h, length, d = output.shape
+    if x.shape[:2] != (b, length) or gate_weight.shape != (h, x.shape[2]):
+        raise ValueError("x, output and gate_weight shapes disagree")
+    if x.dtype not in _HALF or output.dtype != x.dtype or gate_weight.dtype != x.dtype:
+        raise ValueError("attention_gate requires bfloat16 or float16 tensors of one dtype")
+    _require_device("attention_gate", x, output, gate_weight)
+    hidden = x.shape[2]
+    x, output, gate_weight = x.contiguous(), output.contiguous(), gate_weight.contiguous()
+    out = torch.empty((b, length, h * d), dtype=x.dtype, device=x.device)
+    gate = torch.empty((b, length, h), dtype=x.dtype, device=x.device) if return_gate else None
+    _lib.call("sparkq_attention_gate", _ptr(x), _ptr(output), _ptr(gate_weight), _ptr(out),
+              _ptr(gate), b, length, h, d, hidden, _lib.dtype_code(x.dtype),
+              _lib.stream_handle(x.device))
+    return (out, gate) if return_gate else out

@@ -1,5 +1,6 @@
 """Operator dispatch mirroring spark_mlx_llm/ops on torch tensors."""
 
+from .attention_output import dispatch_attention_output
 from .base import OperatorConfig
 from .ffn import RMSNorm, dispatch_ffn
 from .linear import (
@@ -25,6 +26,7 @@ __all__ = [
     "W8A16PerChannelLinear",
     "W8A8Projection",
     "W8A8QuantizedLinear",
+    "dispatch_attention_output",
     "dispatch_ffn",
     "dispatch_linear",
     "dispatch_qkv",

@@ -681,3 +681,32 @@ def test_sdpa_prefill_rounded_pins():
     yr = o.sdpa_prefill_rounded(q2b, k2, v2, 0.125, True, o.BF16)
     ye = o.sdpa_prefill(o.bits_to_f32(q2b, o.BF16), k2, v2, 0.125, True)
     assert 3e-4 < rel_l2(yr, ye) < 1e-2
+
+
+def test_attention_gate16_against_torch_and_known_answers():
+    """attention_gate16 against the same graph written with torch's own
+    float64 ops and 16-bit casts; a zero dot gives the gate 0.5 exactly (the
+    output halves exactly); a large dot gives 1 (the output passes through);
+    out[b, l, h*D:(h+1)*D] is head h of position l, scaled."""
+    b, h, length, d, hid = 2, 3, 4, 8, 32
+    x16 = o.randn16(31, 1, b * length * hid).reshape(b, length, hid)
+    a16 = o.randn16(31, 2, b * h * length * d).reshape(b, h, length, d)
+    w16 = o.randn16(31, 3, h * hid, 0.3).reshape(h, hid)
+    gate, out = o.attention_gate16(x16, a16, w16, o.BF16)
+    t = lambda u: torch.from_numpy(u.view(np.int16)).view(torch.bfloat16)  # noqa: E731
+    xt, at, wt = t(x16), t(a16), t(w16)
+    dot = (xt.double() @ wt.double().T).float().to(torch.bfloat16)
+    gt = torch.sigmoid(dot.double()).float().to(torch.bfloat16)
+    ot = (at.transpose(1, 2).double() * gt.double()[..., None]).float().to(torch.bfloat16)
+    assert np.array_equal(gate, gt.view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(out, ot.reshape(b, length, h * d).view(torch.int16).numpy()
+                          .view(np.uint16))
+    g0, o0 = o.attention_gate16(np.zeros_like(x16), a16, w16, o.BF16)
+    assert np.all(o.bits_to_f32(g0, o.BF16) == 0.5)
+    half = o.bits_to_f32(a16, o.BF16).transpose(0, 2, 1, 3).reshape(b, length, h * d) / 2
+    assert np.array_equal(o.bits_to_f32(o0, o.BF16), half)
+    big = o.bf16_bits(np.full((h, hid), 4.0, np.float32))
+    ones = o.bf16_bits(np.ones((b, length, hid), np.float32))
+    g1, o1 = o.attention_gate16(ones, a16, big, o.BF16)
+    assert np.all(o.bits_to_f32(g1, o.BF16) == 1.0)
+    assert np.array_equal(o1, a16.transpose(0, 2, 1, 3).reshape(b, length, h * d))
