@@ -43,6 +43,12 @@ enum sparkq_kv_format {
    * [B,Hkv,Ncap,D/4] with byte j of word w holding dim 4w+j, scales and
    * biases [B,Hkv,Ncap,D/G] in the query dtype; value = u8 * scale + bias. */
   SPARKQ_KV_AFFINE_U8 = 1,
+  /* MLX affine 4-bit and 2-bit tuples: packed uint32 [B,Hkv,Ncap,D*bits/32],
+   * code of dim cpw*w+j at bits (bits*j) of word w (cpw = 32/bits), scales
+   * and biases [B,Hkv,Ncap,D/G]. Appended by sparkq_kv_append and read by
+   * sparkq_quantized_sdpa. */
+  SPARKQ_KV_AFFINE_U4 = 2,
+  SPARKQ_KV_AFFINE_U2 = 3,
 };
 
 /* Status codes. */
@@ -349,6 +355,8 @@ size_t sparkq_int8kv_sdpa_prefill_affine_workspace_bytes(int64_t B, int64_t Hq,
  * strides[0..2] codes (batch, head, token) in bytes; strides[3..5] scales and
  * biases (batch, head, token) in elements. The cache is written in place;
  * tokens outside [offset, offset+L) are untouched. */
+/* (kv_format AFFINE_U4 / AFFINE_U2 store the same formula with 15 / 3 bins
+ * and 8 / 16 codes per uint32.) */
 int sparkq_kv_append(const void* x, void* codes, void* scales, void* biases,
                      int64_t B, int64_t H, int64_t L, int64_t D,
                      int64_t offset, int group_size, int kv_format,
@@ -420,6 +428,43 @@ int sparkq_rms_norm(const void* x, const void* residual, const void* weight, flo
 int sparkq_rope(const void* x, void* out, int64_t rows, int64_t L, int64_t D, int dims,
                 int traditional, float base, float scale, int64_t offset, int dtype,
                 void* stream);
+
+/* ------------------------------------------------------------------------
+ * Attention over an MLX affine quantized KV cache of any width: the
+ * reference's staged _fallback (X/spark_mlx_ext/int8_quantized_sdpa.py:
+ * 122-153, validation :188-224), which serves every bits/group/head-dim/mask
+ * combination its fused kernels do not:
+ *   q        [B,Hq,L,D] contiguous, q_dtype (F32, F16 or BF16)
+ *   K        packed uint32 [B,Hkv,N,D*bits/32], scales and biases
+ *            [B,Hkv,N,D/G] in q_dtype; V alike with head dim Dv
+ *   out      [B,Hq,L,Dv] in out_dtype (q_dtype or F32)
+ *   strides  as for sparkq_int8kv_sdpa_decode (packed strides in bytes,
+ *            multiples of 4; token strides positive)
+ *   mask_kind 0: none; 1: "causal", bottom-right (row i of L sees tokens
+ *            0 .. N-L+i); 2: boolean array (uint8, nonzero = visible);
+ *            3: additive array of mask_dtype. mask_strides[0..3] are the
+ *            element strides of the mask over (batch, query head, row,
+ *            token), 0 for broadcast axes.
+ * bits in {2,4,8}; group_size in {32,64,128}; D and Dv multiples of the
+ * group size up to 512; any Hq divisible by Hkv. Masked scores take the
+ * lowest finite value of q_dtype, as mx.where does, so a row that sees
+ * nothing averages all values. Scores, softmax and output run in fp32 (the
+ * reference's staged form rounds q*scale, the scores and the weights to the
+ * query dtype). A long context is split over several workgroups and merged
+ * by a second launch; the workspace (sparkq_quantized_sdpa_workspace_bytes,
+ * 0 without a split) holds the partials.
+ * ---------------------------------------------------------------------- */
+size_t sparkq_quantized_sdpa_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv,
+                                             int64_t L, int64_t N, int64_t Dv);
+int sparkq_quantized_sdpa(const void* q, const void* k_packed, const void* k_scales,
+                          const void* k_biases, const void* v_packed,
+                          const void* v_scales, const void* v_biases,
+                          const void* mask, int mask_kind, int mask_dtype,
+                          const int64_t* mask_strides, void* out, int64_t B,
+                          int64_t Hq, int64_t Hkv, int64_t L, int64_t N, int64_t D,
+                          int64_t Dv, int group_size, int bits, int q_dtype,
+                          int out_dtype, float scale, const int64_t* strides,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Head-wise sigmoid gate of the attention output, the step between the
  * attention and the output projection in _compiled_affine_output,

@@ -23,6 +23,7 @@ __all__ = [
     "int8_matmul", "w8a8_epilogue",
     "kv_quantize_s8", "kv_quantize_affine_u8", "kv_dequantize_s8",
     "kv_dequantize_affine_u8", "sdpa_decode", "sdpa_prefill", "sdpa_prefill_rounded",
+    "kv_quantize_affine", "kv_dequantize_affine", "sdpa_staged",
     "cpu_w4a16_gemv", "scalar_f32_to_bf16", "scalar_f32_to_f16",
     "scalar_f16_to_f32",
     "attention_gate16", "add16", "rms_norm16", "gelu16", "gelu_mul16", "rope16", "ffn_block", "qkv_rope",
@@ -382,6 +383,75 @@ def sdpa_prefill(q, kdq, vdq, scale: float, causal: bool) -> np.ndarray:
         vis = np.arange(n - length, n)[:, None] >= np.arange(n)[None, :]
         scores = np.where(vis, scores, -np.inf)
     scores -= scores.max(axis=-1, keepdims=True)
+    p = np.exp(scores)
+    p /= p.sum(axis=-1, keepdims=True)
+    return p @ v
+
+
+def kv_quantize_affine(x, group_size: int, bits: int, dtype: int = BF16):
+    """The build's affine KV quantizer at 8, 4 or 2 bits (the min/max rule of
+    sq_kv_quantize_affine_u8 with 2^bits - 1 bins): per group of G values,
+    scale = T((max-min)/nbins), bias = T(min), code = clamp(rint((x - bias) /
+    scale), 0, nbins) with the rounded scale and bias (0 when the scale is 0),
+    32/bits codes per uint32 from the lowest bits up. numpy; x [..., D]."""
+    x = np.asarray(x, np.float32)
+    nb = (1 << bits) - 1
+    d = x.shape[-1]
+    g = x.reshape(*x.shape[:-1], d // group_size, group_size)
+    lo, hi = g.min(-1), g.max(-1)
+    s16 = round16(((hi - lo) / np.float32(nb)).astype(np.float32), dtype)
+    b16 = round16(lo, dtype)
+    sf = bits_to_f32(s16, dtype)[..., None]
+    bf = bits_to_f32(b16, dtype)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(sf != 0, np.clip(np.rint((g - bf) / sf), 0, nb), 0).astype(np.uint32)
+    q = q.reshape(*x.shape[:-1], d // (32 // bits), 32 // bits)
+    words = np.zeros(q.shape[:-1], np.uint32)
+    for j in range(32 // bits):
+        words |= q[..., j] << np.uint32(bits * j)
+    return words, s16, b16
+
+
+def kv_dequantize_affine(packed, s16, b16, group_size: int, bits: int,
+                         dtype: int = BF16) -> np.ndarray:
+    """code * scale + bias, rounded once to float32, of an affine tuple of
+    `bits` bits (code j of word w is dim (32/bits)*w + j)."""
+    packed = np.asarray(packed, np.uint32)
+    cpw = 32 // bits
+    codes = ((packed[..., None] >> (np.arange(cpw, dtype=np.uint32) * np.uint32(bits)))
+             & np.uint32((1 << bits) - 1)).reshape(*packed.shape[:-1], packed.shape[-1] * cpw)
+    sf = np.repeat(bits_to_f32(s16, dtype).astype(np.float64), group_size, axis=-1)
+    bf = np.repeat(bits_to_f32(b16, dtype).astype(np.float64), group_size, axis=-1)
+    return (codes.astype(np.float64) * sf + bf).astype(np.float32)
+
+
+_LOWEST = {BF16: -3.3895313892515355e38, F16: -65504.0, F32: -3.4028234663852886e38}
+
+
+def sdpa_staged(q, kdq, vdq, scale: float, mask=None, dtype: int = BF16) -> np.ndarray:
+    """The reference's staged quantized attention
+    (X/spark_mlx_ext/int8_quantized_sdpa.py:122-153) in float64 over
+    dequantized K [B,Hkv,N,D] and V [B,Hkv,N,Dv]: scores = (q*scale) K^T;
+    mask "causal" is arange(N-L, N)[:, None] >= arange(N) (:141-142), a
+    boolean array keeps True entries and replaces the others by the lowest
+    finite value of the query dtype (mx.where with finfo.min, :147-150), a
+    floating array is added; softmax; weights V. Returns [B,Hq,L,Dv]."""
+    q = np.asarray(q, np.float64)
+    kd, vd = np.asarray(kdq, np.float64), np.asarray(vdq, np.float64)
+    bsz, hq, length, _ = q.shape
+    hkv, n = kd.shape[1], kd.shape[2]
+    k = np.repeat(kd, hq // hkv, axis=1)
+    v = np.repeat(vd, hq // hkv, axis=1)
+    scores = (q * scale) @ np.swapaxes(k, -1, -2)
+    if isinstance(mask, str):
+        mask = np.arange(n - length, n)[:, None] >= np.arange(n)[None, :]
+    if mask is not None:
+        mask = np.broadcast_to(np.asarray(mask), scores.shape)
+        if mask.dtype == np.bool_:
+            scores = np.where(mask, scores, _LOWEST[dtype])
+        else:
+            scores = scores + mask.astype(np.float64)
+    scores = scores - scores.max(axis=-1, keepdims=True)
     p = np.exp(scores)
     p /= p.sum(axis=-1, keepdims=True)
     return p @ v

@@ -85,6 +85,14 @@ int rms_norm(const void* x, const void* xres, const void* w, float eps, void* hi
 int attention_gate(const void* x, const void* attn, const void* gw, void* out, void* gate_out,
                    int64_t B, int64_t L, int64_t H, int64_t D, int64_t K, int dt,
                    hipStream_t st);
+size_t sdpa_gen_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
+                          int64_t Dv);
+int sdpa_generic(const void* q, const void* kp, const void* ks, const void* kb, const void* vp,
+                 const void* vs, const void* vb, const void* mask, int mask_kind,
+                 int mask_dtype, const int64_t* mask_strides, void* out, int64_t B, int64_t Hq,
+                 int64_t Hkv, int64_t L, int64_t N, int64_t D, int64_t Dv, int G, int bits,
+                 int qdt, int odt, float scale, const int64_t* strides, void* ws, size_t wsb,
+                 hipStream_t st);
 
 static thread_local char g_last_error[512] = "";
 
@@ -502,7 +510,8 @@ int sparkq_kv_append(const void* x, void* codes, void* scales, void* biases, int
   REQUIRE(x && codes && scales && strides, "kv_append: null tensor pointer");
   REQUIRE(B > 0 && H > 0 && L > 0 && D > 0 && offset >= 0, "kv_append: bad shape or offset");
   REQUIRE(B * H * L * D <= kI32Max * 4LL && offset + L <= kI32Max, "kv_append: shape too large");
-  REQUIRE(kv_format == SPARKQ_KV_S8_F16SCALE || kv_format == SPARKQ_KV_AFFINE_U8,
+  REQUIRE(kv_format == SPARKQ_KV_S8_F16SCALE || kv_format == SPARKQ_KV_AFFINE_U8 ||
+              kv_format == SPARKQ_KV_AFFINE_U4 || kv_format == SPARKQ_KV_AFFINE_U2,
           "kv_append: unknown kv_format %d", kv_format);
   for (int i = 0; i < 6; ++i) REQUIRE(strides[i] >= 0, "kv_append: negative stride");
   if (kv_format == SPARKQ_KV_S8_F16SCALE) {
@@ -712,6 +721,62 @@ int sparkq_attention_gate(const void* x, const void* attn, const void* gate_w, v
   DEVICE_OK();
   return attention_gate(x, attn, gate_w, out, gate_out, B, L, H, D, hidden, dtype,
                         (hipStream_t)stream);
+}
+
+size_t sparkq_quantized_sdpa_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                                             int64_t N, int64_t Dv) {
+  return sdpa_gen_workspace(B, Hq, Hkv, L, N, Dv);
+}
+
+int sparkq_quantized_sdpa(const void* q, const void* k_packed, const void* k_scales,
+                          const void* k_biases, const void* v_packed, const void* v_scales,
+                          const void* v_biases, const void* mask, int mask_kind, int mask_dtype,
+                          const int64_t* mask_strides, void* out, int64_t B, int64_t Hq,
+                          int64_t Hkv, int64_t L, int64_t N, int64_t D, int64_t Dv,
+                          int group_size, int bits, int q_dtype, int out_dtype, float scale,
+                          const int64_t* strides, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  // the validation of X/spark_mlx_ext/int8_quantized_sdpa.py:188-224
+  REQUIRE(q && k_packed && k_scales && k_biases && v_packed && v_scales && v_biases && out &&
+              strides,
+          "quantized_sdpa: null tensor pointer");
+  REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && L > 0 && N > 0 && D > 0 && Dv > 0 && Hq % Hkv == 0,
+          "Nonempty inputs and query heads divisible by KV heads required");
+  REQUIRE(bits == 2 || bits == 4 || bits == 8,
+          "Supported affine formats: bits 2/4/8, group size 32/64/128");
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "Supported affine formats: bits 2/4/8, group size 32/64/128");
+  REQUIRE(D % group_size == 0 && Dv % group_size == 0,
+          "Incompatible key packed shape, affine metadata or dtype");
+  REQUIRE_SUPPORTED(D <= 512 && Dv <= 512, "quantized_sdpa: head dims above 512 are not served");
+  REQUIRE(std::isfinite(scale), "scale must be a finite Python number");
+  REQUIRE(is_float_dtype(q_dtype), "Q and metadata must be float16, bfloat16 or float32");
+  REQUIRE(out_dtype == q_dtype || out_dtype == SPARKQ_F32,
+          "quantized_sdpa: out dtype must equal q dtype or be float32");
+  REQUIRE(mask_kind >= 0 && mask_kind <= 3, "quantized_sdpa: unknown mask kind %d", mask_kind);
+  REQUIRE(mask_kind < 2 || (mask && mask_strides), "quantized_sdpa: mask array missing");
+  REQUIRE(mask_kind != 3 || is_float_dtype(mask_dtype),
+          "quantized_sdpa: additive masks must be floating");
+  if (mask_kind >= 2)
+    for (int i = 0; i < 4; ++i)
+      REQUIRE(mask_strides[i] >= 0, "quantized_sdpa: negative mask stride");
+  for (int i : {0, 1, 2, 6, 7, 8})
+    REQUIRE(strides[i] % 4 == 0 && strides[i] >= 0,
+            "quantized_sdpa: packed strides must be non-negative multiples of 4 bytes");
+  for (int i : {3, 4, 5, 9, 10, 11})
+    REQUIRE(strides[i] >= 0, "quantized_sdpa: negative scale stride");
+  for (int i : {2, 5, 8, 11})
+    REQUIRE(strides[i] > 0, "quantized_sdpa: token strides must be positive");
+  REQUIRE(N <= kI32Max && L <= kI32Max && B * Hq * L <= kI32Max,
+          "quantized_sdpa: shape too large");
+  REQUIRE_SUPPORTED(B * Hkv * cdiv(Hq / Hkv, 8) <= 65535 && L * 64 <= kI32Max,
+                    "quantized_sdpa: too many sequences and heads for one launch");
+  REQUIRE(aligned(k_packed, 4) && aligned(v_packed, 4), "quantized_sdpa: packed codes misaligned");
+  DEVICE_OK();
+  return sdpa_generic(q, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases, mask,
+                      mask_kind, mask_dtype, mask_strides, out, B, Hq, Hkv, L, N, D, Dv,
+                      group_size, bits, q_dtype, out_dtype, scale, strides, workspace,
+                      workspace_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1390,7 +1390,9 @@ __global__ __launch_bounds__(256) void kv_quantize_s8_kernel(const void* __restr
 // format: one thread per group of G values, scale = to_dtype((max-min)/255),
 // bias = to_dtype(min), code = clamp(rint((x - bias) / scale), 0, 255) with
 // the rounded scale and bias (0 for a zero scale), four codes per uint32
-// (dim 4w+j in byte j of word w). This min/max rule is not mx.quantize's,
+// (dim 4w+j in byte j of word w). The 4- and 2-bit affine formats use the
+// same thread-per-group kernel with 15 or 3 bins and 8 or 16 codes per
+// uint32 (dim cpw*w+j at bits b*j). This min/max rule is not mx.quantize's,
 // which makes the larger-magnitude edge exact (negative scale, bias = edge).
 struct KvAppendArgs {
   const void* x;
@@ -1400,6 +1402,7 @@ struct KvAppendArgs {
   int64_t c_b, c_h, c_t;  // code strides (bytes)
   int64_t s_b, s_h, s_t;  // scale/bias strides (elements)
   int B, H, L, D, G, offset, x_dtype;
+  int bits;  // affine formats: 8, 4 or 2 bits per code
 };
 
 __global__ __launch_bounds__(256) void kv_append_s8_kernel(KvAppendArgs a) {
@@ -1442,23 +1445,24 @@ __global__ __launch_bounds__(256) void kv_append_u8_kernel(KvAppendArgs a) {
     mn = f < mn ? f : mn;
     mx = f > mx ? f : mx;
   }
-  const uint16_t s16 = T::from_f32((mx - mn) / 255.0f), b16 = T::from_f32(mn);
+  const float nbins = (float)((1 << a.bits) - 1);
+  const uint16_t s16 = T::from_f32((mx - mn) / nbins), b16 = T::from_f32(mn);
   const int64_t si = b * a.s_b + h * a.s_h + t * a.s_t + g;
   reinterpret_cast<uint16_t*>(a.scales)[si] = s16;
   reinterpret_cast<uint16_t*>(a.biases)[si] = b16;
   const float sf = T::to_f32(s16), bf = T::to_f32(b16);
+  const int cpw = 32 / a.bits;  // codes per word, the lowest bits first
   uint32_t* dst = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(a.codes) +
-                                              b * a.c_b + h * a.c_h + t * a.c_t) + g * a.G / 4;
-  for (int w = 0; w < a.G / 4; ++w) {
+                                              b * a.c_b + h * a.c_h + t * a.c_t) + g * a.G / cpw;
+  for (int w = 0; w < a.G / cpw; ++w) {
     uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < cpw; ++j) {
       float q = 0.0f;
       if (sf != 0.0f) {
-        q = __builtin_rintf((T::to_f32(v[4 * w + j]) - bf) / sf);
-        q = q < 0.0f ? 0.0f : (q > 255.0f ? 255.0f : q);
+        q = __builtin_rintf((T::to_f32(v[cpw * w + j]) - bf) / sf);
+        q = q < 0.0f ? 0.0f : (q > nbins ? nbins : q);
       }
-      word |= (uint32_t)q << (8 * j);
+      word |= (uint32_t)q << (a.bits * j);
     }
     dst[w] = word;
   }
@@ -1857,11 +1861,12 @@ int kv_append(const void* x, void* codes, void* scales, void* biases, int64_t B,
   a.G = G;
   a.offset = (int)offset;
   a.x_dtype = xdt;
+  a.bits = fmt == SPARKQ_KV_AFFINE_U4 ? 4 : fmt == SPARKQ_KV_AFFINE_U2 ? 2 : 8;
   const int64_t rows = B * H * L;
   if (fmt == SPARKQ_KV_S8_F16SCALE) {
     hipLaunchKernelGGL(kv_append_s8_kernel, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, st, a);
-  } else if ((D == 64 || D == 128 || D == 256) && G % (D / 64) == 0 && G / (D / 64) <= 64 &&
-             !env_int("SPARKQ_KV_APPEND_THREAD", 0)) {
+  } else if (a.bits == 8 && (D == 64 || D == 128 || D == 256) && G % (D / 64) == 0 &&
+             G / (D / 64) <= 64 && !env_int("SPARKQ_KV_APPEND_THREAD", 0)) {
     const dim3 grid((unsigned)cdiv(rows, 4));
     if (xdt == SPARKQ_BF16)
       launch_append_u8<BF16>((int)D, a, grid, st);

@@ -20,7 +20,7 @@ __all__ = [
 ]
 
 F32, F16, BF16 = 0, 1, 2
-KV_S8_F16SCALE, KV_AFFINE_U8 = 0, 1
+KV_S8_F16SCALE, KV_AFFINE_U8, KV_AFFINE_U4, KV_AFFINE_U2 = 0, 1, 2, 3
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_DEVICE, ERR_WORKSPACE = 0, -1, -2, -3, -4
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -66,6 +66,9 @@ SIGNATURES = {
     "sparkq_rope": (I, [P, P, I64, I64, I64, I, I, F, F, I64, I, P]),
     "sparkq_rms_norm": (I, [P, P, P, F, P, P, I64, I64, I, P]),
     "sparkq_attention_gate": (I, [P, P, P, P, P, I64, I64, I64, I64, I64, I, P]),
+    "sparkq_quantized_sdpa_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I64]),
+    "sparkq_quantized_sdpa": (I, [P, P, P, P, P, P, P, P, I, I, P, P, I64, I64, I64, I64, I64,
+                                  I64, I64, I, I, I, I, F, P, P, SZ, P]),
 }
 
 

@@ -19,7 +19,7 @@ import torch
 from torch import nn
 
 from . import _lib
-from ._lib import BF16, F16, F32, KV_AFFINE_U8, KV_S8_F16SCALE
+from ._lib import BF16, F16, F32, KV_AFFINE_U2, KV_AFFINE_U4, KV_AFFINE_U8, KV_S8_F16SCALE
 
 __all__ = [
     "W8A8Linear",
@@ -529,16 +529,20 @@ def _int8_prefill(queries, keys, values, *, scale, causal, fmt, out_dtype, out,
     return y
 
 
-def kv_append(x, cache, offset: int, *, group_size: int = 32):
+def kv_append(x, cache, offset: int, *, group_size: int = 32, bits: int = 8):
     """Quantize x [B,H,L,D] into tokens [offset, offset+L) of a preallocated
     cache, in place: cache is (codes int8 [B,H,Ncap,D], scales fp16
-    [B,H,Ncap]) for the symmetric format, or the MLX affine 8-bit tuple
-    (packed uint32 [B,H,Ncap,D/4], scales, biases [B,H,Ncap,D/G] in x.dtype).
-    The quantize-on-append step of mlx-lm's QuantizedKVCache."""
+    [B,H,Ncap]) for the symmetric format, or the MLX affine tuple of `bits`
+    (8, 4 or 2) bits (packed uint32 [B,H,Ncap,D*bits/32], scales, biases
+    [B,H,Ncap,D/G] in x.dtype). The quantize-on-append step of mlx-lm's
+    QuantizedKVCache."""
     if x.ndim != 4 or x.numel() == 0:
         raise ValueError("x must be a nonempty [B,H,L,D] tensor")
     b, h, length, d = x.shape
     fmt = KV_AFFINE_U8 if len(cache) == 3 else KV_S8_F16SCALE
+    if fmt == KV_AFFINE_U8 and bits not in (2, 4, 8):
+        raise ValueError("Supported affine formats: bits 2/4/8, group size 32/64/128")
+    wpr = d * bits // 32  # packed words per token row
     codes, scales = cache[0], cache[1]
     biases = cache[2] if fmt == KV_AFFINE_U8 else None
     ncap = codes.shape[2]
@@ -547,11 +551,12 @@ def kv_append(x, cache, offset: int, *, group_size: int = 32):
     if fmt == KV_AFFINE_U8:
         if x.dtype not in _HALF or scales.dtype != x.dtype or biases.dtype != x.dtype:
             raise ValueError("affine KV needs float16 or bfloat16 x, scales and biases")
-        if (codes.shape != (b, h, ncap, d // 4) or codes.dtype not in _PACKED
+        if (codes.shape != (b, h, ncap, wpr) or codes.dtype not in _PACKED
                 or scales.shape != (b, h, ncap, d // group_size) or biases.shape != scales.shape
                 or scales.stride() != biases.stride() or d % group_size):
             raise ValueError("Incompatible affine KV cache for this input")
         strides = _kv_strides(codes, scales, 4)
+        fmt = {8: KV_AFFINE_U8, 4: KV_AFFINE_U4, 2: KV_AFFINE_U2}[bits]
     else:
         if x.dtype not in _REAL:
             raise ValueError("x must be float16, bfloat16 or float32")
@@ -559,7 +564,7 @@ def kv_append(x, cache, offset: int, *, group_size: int = 32):
                 or scales.shape != (b, h, ncap) or scales.dtype != torch.float16):
             raise ValueError("Incompatible int8 KV cache for this input")
         strides = _kv_strides(codes, scales, 1)
-    if codes.stride(3) != 1 or (fmt == KV_AFFINE_U8 and scales.stride(-1) != 1):
+    if codes.stride(3) != 1 or (fmt != KV_S8_F16SCALE and scales.stride(-1) != 1):
         raise ValueError("the cache's innermost axes must be contiguous")
     _require_device("kv_append", x, codes, scales, biases)
     st = (ctypes.c_int64 * 6)(*strides)
@@ -574,16 +579,17 @@ class QuantizedKVCache:
     update_and_fetch(keys, values) quantizes [B,Hkv,L,D] keys and values on the
     device into storage that grows in steps of 256 tokens and returns views of
     tokens [0, offset), ready for int8_quantized_sdpa. kv_format "affine_u8"
-    keeps MLX's (packed, scales, biases) tuples with group_size; "s8" the
-    symmetric (codes, fp16 scale) pairs of the decode benchmark."""
+    keeps MLX's (packed, scales, biases) tuples with group_size and bits
+    (8, 4 or 2; mlx-lm's kv_bits); "s8" the symmetric (codes, fp16 scale)
+    pairs of the decode benchmark."""
 
     step = 256
 
     def __init__(self, group_size: int = 32, bits: int = 8, kv_format: str = "affine_u8"):
-        if bits != 8:
-            raise ValueError("only 8-bit KV quantization is supported")
         if kv_format not in ("affine_u8", "s8"):
             raise ValueError("kv_format must be 'affine_u8' or 's8'")
+        if bits not in ((2, 4, 8) if kv_format == "affine_u8" else (8,)):
+            raise ValueError("affine KV caches take bits 2, 4 or 8; the s8 format 8")
         if kv_format == "affine_u8" and group_size not in (32, 64, 128):
             raise ValueError("group_size must be 32, 64 or 128")
         self.group_size, self.bits, self.kv_format = group_size, bits, kv_format
@@ -597,7 +603,7 @@ class QuantizedKVCache:
             return (torch.zeros((b, h, capacity, d), dtype=torch.int8, device=dev),
                     torch.zeros((b, h, capacity), dtype=torch.float16, device=dev))
         g = self.group_size
-        return (torch.zeros((b, h, capacity, d // 4), dtype=torch.int32, device=dev),
+        return (torch.zeros((b, h, capacity, d * self.bits // 32), dtype=torch.int32, device=dev),
                 torch.zeros((b, h, capacity, d // g), dtype=x.dtype, device=dev),
                 torch.zeros((b, h, capacity, d // g), dtype=x.dtype, device=dev))
 
@@ -620,8 +626,8 @@ class QuantizedKVCache:
             capacity = -(-(self.offset + length) // self.step) * self.step
             self.keys = self._grow(self.keys, keys, capacity)
             self.values = self._grow(self.values, values, capacity)
-        kv_append(keys, self.keys, self.offset, group_size=self.group_size)
-        kv_append(values, self.values, self.offset, group_size=self.group_size)
+        kv_append(keys, self.keys, self.offset, group_size=self.group_size, bits=self.bits)
+        kv_append(values, self.values, self.offset, group_size=self.group_size, bits=self.bits)
         self.offset += length
         n = self.offset
         return (tuple(t[:, :, :n] for t in self.keys), tuple(t[:, :, :n] for t in self.values))
@@ -641,23 +647,31 @@ def _kv_strides(codes, scales, elem_bytes_codes):
 def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, bits: int = 8,
                         mask=None, single_pass_max_length: int = 1023, out_dtype=None,
                         out=None):
-    """Decode attention over an INT8 KV cache
+    """Attention over a quantized KV cache
     (X/spark_mlx_ext/int8_quantized_sdpa.py:156-287).
 
-    queries [B,Hq,1,D]. keys/values are either the MLX affine 8-bit tuple
-    (packed uint32 [B,Hkv,N,D/4], scales [B,Hkv,N,D/G], biases) with scales in
-    the query dtype, or the symmetric pair (codes int8 [B,Hkv,N,D], scales fp16
-    [B,Hkv,N]). Views with a sliced token capacity are read in place (strides
-    are passed through); the innermost axis must be contiguous. All N tokens
-    are visible, so mask None and "causal" are the same for one query token.
-    single_pass_max_length is validated for signature compatibility; the split
-    policy is the kernel's own.
+    queries [B,Hq,L,D]. keys/values are either the MLX affine tuple
+    (packed uint32 [B,Hkv,N,D*bits/32], scales [B,Hkv,N,D/G], biases) with
+    scales in the query dtype, or the symmetric pair (codes int8 [B,Hkv,N,D],
+    scales fp16 [B,Hkv,N]). Views with a sliced token capacity are read in
+    place (strides are passed through); the innermost axis must be
+    contiguous. As in the reference, the affine tuple takes the fused kernels
+    when bits == 8, the head dims are equal and 64/128/256 (the reference:
+    256 only), the query-to-KV head ratio is 1/2/4/8 and the mask is None or
+    "causal" (multi-token queries: 16-bit, and L <= N when causal); every
+    other supported combination (bits 2/4, any head dims that are multiples
+    of the group size, boolean or additive mask arrays, any head ratio) takes
+    the staged attention kernel, the reference's _fallback (:122-153).
+    single_pass_max_length is validated for signature compatibility; the
+    split policy is the kernels' own.
     """
     if type(single_pass_max_length) is not int or single_pass_max_length < 0:
         raise ValueError("single_pass_max_length must be a nonnegative Python int")
     if queries.ndim != 4 or len(keys) not in (2, 3) or len(values) != len(keys):
         raise ValueError("Expected Q[B,H,L,D] and affine (packed, scales, biases) KV tuples")
     batch, heads, length, dim = queries.shape
+    if any(t.ndim != 4 for t in (*keys, *values)) and len(keys) == 3:
+        raise ValueError("Every packed KV and metadata array must have four dimensions")
     if any(t.ndim != 4 for t in (keys[0], values[0])):
         raise ValueError("Every packed KV and metadata array must have four dimensions")
     kv_heads, n = keys[0].shape[1:3]
@@ -665,40 +679,52 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
         raise ValueError("Nonempty inputs and query heads divisible by KV heads required")
     if not isinstance(scale, (float, int)) or not math.isfinite(scale):
         raise ValueError("scale must be a finite Python number")
-    if mask is not None and not (isinstance(mask, str) and mask == "causal"):
-        raise ValueError("only mask=None or mask='causal' is supported")
+    simple_mask = mask is None or (isinstance(mask, str) and mask == "causal")
+    if isinstance(mask, str) and mask != "causal":
+        raise ValueError("mask string must be 'causal'")
     if queries.dtype not in _REAL:
         raise ValueError("Q and metadata must be float16, bfloat16 or float32")
-    fmt = KV_AFFINE_U8 if len(keys) == 3 else KV_S8_F16SCALE
+    if len(keys) == 2:
+        if not simple_mask:
+            raise ValueError("the symmetric int8 cache takes mask=None or mask='causal'")
+        return _s8_attention(queries, keys, values, scale=scale, causal=mask is not None,
+                             out_dtype=out_dtype, out=out)
+    # the MLX affine tuple: the reference's validation (:188-224)
+    if bits not in (2, 4, 8) or group_size not in (32, 64, 128):
+        raise ValueError("Supported affine formats: bits 2/4/8, group size 32/64/128")
+    pack = 32 // bits
+    dv = values[0].shape[-1] * pack
+    for name, (packed, s, b) in (("key", keys), ("value", values)):
+        width = dim if name == "key" else dv
+        if (width <= 0 or width % group_size
+                or packed.shape != (batch, kv_heads, n, width // pack)
+                or s.shape != (batch, kv_heads, n, width // group_size)
+                or b.shape != s.shape or packed.dtype not in _PACKED
+                or s.dtype != queries.dtype or b.dtype != queries.dtype
+                or s.stride() != b.stride()):
+            raise ValueError(f"Incompatible {name} packed shape, affine metadata or dtype")
+        if packed.stride(3) != 1 or s.stride(3) != 1:
+            raise ValueError(f"{name} innermost axis must be contiguous")
+    gqa = heads // kv_heads
+    fused = (bits == 8 and dim == dv and dim in (64, 128, 256) and gqa in (1, 2, 4, 8)
+             and simple_mask
+             and (length == 1 or (queries.dtype in _HALF and (mask is None or length <= n))))
+    if not fused:
+        return _staged_attention(queries, keys, values, scale=scale, group_size=group_size,
+                                 bits=bits, mask=mask, out_dtype=out_dtype, out=out)
     if length > 1:
-        return _int8_prefill(queries, keys, values, scale=scale, causal=mask is not None,
-                             fmt=fmt, out_dtype=out_dtype, out=out, group_size=group_size,
-                             bits=bits)
-    if fmt == KV_AFFINE_U8:
-        if bits != 8 or group_size not in (32, 64, 128):
-            raise ValueError("Supported affine formats: bits 8, group size 32/64/128")
-        for name, (packed, s, b) in (("key", keys), ("value", values)):
-            if (dim % group_size or packed.shape != (batch, kv_heads, n, dim // 4)
-                    or s.shape != (batch, kv_heads, n, dim // group_size)
-                    or b.shape != s.shape or packed.dtype not in _PACKED
-                    or s.dtype != queries.dtype or b.dtype != queries.dtype
-                    or s.stride() != b.stride()):
-                raise ValueError(f"Incompatible {name} packed shape, affine metadata or dtype")
-            if packed.stride(3) != 1 or s.stride(3) != 1:
-                raise ValueError(f"{name} innermost axis must be contiguous")
-        strides = (_kv_strides(keys[0], keys[1], 4) + _kv_strides(values[0], values[1], 4))
-        kc, ks, kb = keys
-        vc, vs, vb = values
-    else:
-        for name, (codes, s) in (("key", keys), ("value", values)):
-            if (codes.shape != (batch, kv_heads, n, dim) or codes.dtype != torch.int8
-                    or s.shape != (batch, kv_heads, n) or s.dtype != torch.float16):
-                raise ValueError(f"Incompatible {name} int8 codes or fp16 scales")
-            if codes.stride(3) != 1:
-                raise ValueError(f"{name} innermost axis must be contiguous")
-        strides = (_kv_strides(keys[0], keys[1], 1) + _kv_strides(values[0], values[1], 1))
-        (kc, ks), (vc, vs) = keys, values
-        kb = vb = None
+        return _int8_prefill_affine(queries, keys, values, scale=scale, causal=mask is not None,
+                                    group_size=group_size, bits=bits, out_dtype=out_dtype,
+                                    out=out)
+    strides = (_kv_strides(keys[0], keys[1], 4) + _kv_strides(values[0], values[1], 4))
+    (kc, ks, kb), (vc, vs, vb) = keys, values
+    return _decode(queries, kc, ks, kb, vc, vs, vb, strides, group_size, KV_AFFINE_U8, scale,
+                   out_dtype, out)
+
+
+def _decode(queries, kc, ks, kb, vc, vs, vb, strides, group_size, fmt, scale, out_dtype, out):
+    batch, heads, _, dim = queries.shape
+    kv_heads, n = kc.shape[1:3]
     _require_device("int8_quantized_sdpa", queries, kc, vc)
     out_dtype = queries.dtype if out_dtype is None else out_dtype
     q = queries.reshape(batch, heads, dim).contiguous()
@@ -712,6 +738,78 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
               _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), float(scale), st,
               ws, wsb, _lib.stream_handle(queries.device))
     return out
+
+
+def _s8_attention(queries, keys, values, *, scale, causal, out_dtype, out):
+    """The symmetric int8 + fp16-scale cache (the decode benchmark's format):
+    one query token on the decode kernels, several on the s8 prefill kernel."""
+    batch, heads, length, dim = queries.shape
+    kv_heads, n = keys[0].shape[1:3]
+    if length > 1:
+        return _int8_prefill(queries, keys, values, scale=scale, causal=causal,
+                             fmt=KV_S8_F16SCALE, out_dtype=out_dtype, out=out)
+    for name, (codes, s) in (("key", keys), ("value", values)):
+        if (codes.shape != (batch, kv_heads, n, dim) or codes.dtype != torch.int8
+                or s.shape != (batch, kv_heads, n) or s.dtype != torch.float16):
+            raise ValueError(f"Incompatible {name} int8 codes or fp16 scales")
+        if codes.stride(3) != 1:
+            raise ValueError(f"{name} innermost axis must be contiguous")
+    strides = (_kv_strides(keys[0], keys[1], 1) + _kv_strides(values[0], values[1], 1))
+    (kc, ks), (vc, vs) = keys, values
+    return _decode(queries, kc, ks, None, vc, vs, None, strides, 32, KV_S8_F16SCALE, scale,
+                   out_dtype, out)
+
+
+_MASK_NONE, _MASK_CAUSAL, _MASK_BOOL, _MASK_ADD = 0, 1, 2, 3
+
+
+def _staged_attention(queries, keys, values, *, scale, group_size, bits, mask, out_dtype, out):
+    """The reference's staged _fallback (X/spark_mlx_ext/int8_quantized_sdpa.py:
+    122-153) on the gfx950 staged-attention kernel: any bits in 2/4/8, head
+    dims that are multiples of the group size (keys and values may differ),
+    any head ratio, and masks None, "causal" (bottom-right), boolean arrays
+    (False hides a token: its score becomes the dtype's lowest value, as
+    mx.where does) or additive arrays broadcastable to [B,Hq,L,N]."""
+    batch, heads, length, dim = queries.shape
+    kv_heads, n = keys[0].shape[1:3]
+    dv = values[0].shape[-1] * (32 // bits)
+    (kc, ks, kb), (vc, vs, vb) = keys, values
+    mask_t, mstrides, kind, mdt = None, None, _MASK_NONE, F32
+    if isinstance(mask, str):
+        kind = _MASK_CAUSAL
+    elif mask is not None:
+        if not isinstance(mask, torch.Tensor) or mask.ndim > 4:
+            raise ValueError("mask must be None, 'causal' or an array of at most 4 dimensions")
+        if mask.dtype == torch.bool:
+            kind = _MASK_BOOL
+        elif mask.dtype in _REAL:
+            kind, mdt = _MASK_ADD, _lib.dtype_code(mask.dtype)
+        else:
+            raise ValueError("mask arrays must be boolean or floating")
+        try:
+            mask_t = torch.broadcast_to(mask.to(queries.device), (batch, heads, length, n))
+        except RuntimeError as err:
+            raise ValueError(f"mask of shape {tuple(mask.shape)} does not broadcast to "
+                             f"{(batch, heads, length, n)}") from err
+        if kind == _MASK_BOOL:
+            mask_t = mask_t.view(torch.uint8)
+        mstrides = (ctypes.c_int64 * 4)(*mask_t.stride())
+    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    out_dtype = queries.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (queries.dtype, torch.float32):
+        raise ValueError("out_dtype must be the query dtype or torch.float32")
+    q = queries.contiguous()
+    y = _out_buffer(out, (batch, heads, length, dv), out_dtype, queries.device)
+    st = (ctypes.c_int64 * 12)(*(_kv_strides(kc, ks, 4) + _kv_strides(vc, vs, 4)))
+    ws, wsb = _lib.workspace(queries.device,
+                             _lib.lib().sparkq_quantized_sdpa_workspace_bytes(
+                                 batch, heads, kv_heads, length, n, dv), "sdpa_staged")
+    _lib.call("sparkq_quantized_sdpa", _ptr(q), _ptr(kc), _ptr(ks), _ptr(kb), _ptr(vc),
+              _ptr(vs), _ptr(vb), _ptr(mask_t), kind, mdt, mstrides, _ptr(y), batch, heads,
+              kv_heads, length, n, dim, dv, group_size, bits, _lib.dtype_code(queries.dtype),
+              _lib.dtype_code(out_dtype), float(scale), st, ws, wsb,
+              _lib.stream_handle(queries.device))
+    return y
 
 
 # ---------------------------------------------------------------------------

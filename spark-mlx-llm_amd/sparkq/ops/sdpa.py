@@ -6,7 +6,9 @@ predicate is widened from the reference's D=256/G32 affine format to the
 formats and head sizes the gfx950 decode kernel serves (D in 64/128/256,
 affine G in 32/64/128, or symmetric s8 codes with fp16 per-token scales);
 multi-token queries (the opt-in fused_quantized_sdpa_prefill) are served on
-both formats with 16-bit queries.
+both formats with 16-bit queries. Other quantized caches (2- and 4-bit, other
+head dims, mask arrays) take the staged-attention kernel, where the
+reference's mlx-lm native path runs the same staged arithmetic.
 Unquantized caches go to torch's scaled_dot_product_attention, the analogue
 of the reference's mlx-lm native path.
 """
@@ -41,7 +43,7 @@ def dispatch_sdpa(queries, keys, values, *, cache, scale, mask, config: SDPAConf
                                                       prefill=config.fused_quantized_sdpa_prefill):
         return _int8_attention(queries, keys, values, cache=cache, scale=scale, mask=mask)
     if isinstance(keys, (tuple, list)):
-        raise ValueError("quantized KV cache outside the gfx950 decode kernel's formats")
+        return _quantized_attention(queries, keys, values, cache=cache, scale=scale, mask=mask)
     return _native_attention(queries, keys, values, scale=scale, mask=mask)
 
 
@@ -78,6 +80,19 @@ def _supports_int8(queries, keys, values, *, cache, mask, prefill=False):
         and queries.device.type == "cuda"
         and ext.is_w8a8_available()
     )
+
+
+def _quantized_attention(queries, keys, values, *, cache, scale, mask):
+    """Quantized caches the fused predicate does not take: the reference
+    hands them to mlx-lm's scaled_dot_product_attention, whose quantized
+    branch is the staged quantized_matmul / softmax / quantized_matmul form
+    (the same arithmetic as X/spark_mlx_ext/int8_quantized_sdpa.py:122-153);
+    here int8_quantized_sdpa routes them to the staged-attention kernel
+    (bits 2/4/8, any head dims, mask arrays). Like every sparkq operator it
+    runs only on the device."""
+    return ext.int8_quantized_sdpa(queries, keys, values, scale=scale,
+                                   group_size=getattr(cache, "group_size", 32),
+                                   bits=getattr(cache, "bits", 8), mask=mask)
 
 
 def _int8_attention(queries, keys, values, *, cache, scale, mask):

@@ -102,9 +102,9 @@ def test_sdpa_dispatch_validation():
 
     q = torch.zeros((1, 8, 1, 128))
     keys = (torch.zeros((1, 2, 16, 128), dtype=torch.int8), torch.ones((1, 2, 16), dtype=torch.float16))
-    # CPU tensors never take the fused route, and a quantized cache has no
-    # other route
-    with pytest.raises(ValueError, match="quantized KV cache"):
+    # CPU tensors never take the fused route; a quantized cache then goes to
+    # the staged kernel, which (like every sparkq operator) runs only on the GPU
+    with pytest.raises(ValueError, match="GPU"):
         dispatch_sdpa(q, keys, keys, cache=Cache(), scale=0.1, mask=None)
     with pytest.raises(ValueError, match="single_pass_max_length"):
         ext.int8_quantized_sdpa(q, keys, keys, scale=0.1, single_pass_max_length=-1)
@@ -123,9 +123,26 @@ def test_sdpa_dispatch_validation():
         ext.int8_quantized_sdpa(q2[:, :, :2], aff, aff, scale=0.1, group_size=16)
     with pytest.raises(ValueError, match="Incompatible key packed"):
         ext.int8_quantized_sdpa(q2[:, :, :2], aff, aff, scale=0.1, group_size=64)
-    with pytest.raises(ValueError, match="head dim"):
+    # a head dim outside 64/128/256 is a staged-kernel shape, not an error
+    aff96 = (torch.zeros((1, 2, 16, 24), dtype=torch.int32),
+             torch.ones((1, 2, 16, 3), dtype=torch.bfloat16),
+             torch.zeros((1, 2, 16, 3), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="GPU"):
         ext.int8_quantized_sdpa(torch.zeros((1, 8, 2, 96), dtype=torch.bfloat16),
-                                aff, aff, scale=0.1)
+                                aff96, aff96, scale=0.1)
+    # 4-bit tuples: the packed width is D/8; bits 3 is not an MLX KV format
+    aff4 = (torch.zeros((1, 2, 16, 16), dtype=torch.int32),
+            torch.ones((1, 2, 16, 4), dtype=torch.bfloat16),
+            torch.zeros((1, 2, 16, 4), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="GPU"):
+        ext.int8_quantized_sdpa(q2[:, :, :2], aff4, aff4, scale=0.1, bits=4)
+    with pytest.raises(ValueError, match="bits 2/4/8"):
+        ext.int8_quantized_sdpa(q2[:, :, :2], aff4, aff4, scale=0.1, bits=3)
+    with pytest.raises(ValueError, match="Incompatible key"):
+        ext.int8_quantized_sdpa(q2[:, :, :2], aff4, aff4, scale=0.1, bits=8)
+    with pytest.raises(ValueError, match="does not broadcast"):
+        ext.int8_quantized_sdpa(q2[:, :, :2], aff4, aff4, scale=0.1, bits=4,
+                                mask=torch.ones((3, 16), dtype=torch.bool))
     with pytest.raises(ValueError, match="GPU"):
         ext.int8_quantized_sdpa(q2[:, :, :2], aff, aff, scale=0.1)
     # unquantized caches take torch's attention
@@ -203,10 +220,18 @@ def test_w8a16_layer_contract():
 
 
 def test_quantized_kv_cache_contract():
-    """QuantizedKVCache mirrors mlx-lm's interface: 8 bits only, the two
-    formats, capacity in steps of 256; appends run on the device only."""
-    with pytest.raises(ValueError, match="8-bit"):
-        sparkq.QuantizedKVCache(bits=4)
+    """QuantizedKVCache mirrors mlx-lm's interface: affine caches of 8, 4 or 2
+    bits (mlx-lm's kv_bits) and the symmetric s8 format, capacity in steps of
+    256; appends run on the device only."""
+    with pytest.raises(ValueError, match="bits 2, 4 or 8"):
+        sparkq.QuantizedKVCache(bits=3)
+    with pytest.raises(ValueError, match="s8 format 8"):
+        sparkq.QuantizedKVCache(bits=4, kv_format="s8")
+    c4 = sparkq.QuantizedKVCache(bits=4, group_size=32)
+    with pytest.raises(ValueError, match="GPU"):
+        c4.update_and_fetch(torch.zeros((1, 2, 3, 96), dtype=torch.bfloat16),
+                            torch.zeros((1, 2, 3, 96), dtype=torch.bfloat16))
+    assert c4.keys[0].shape == (1, 2, 256, 12)  # 96 dims * 4 bits / 32
     with pytest.raises(ValueError, match="kv_format"):
         sparkq.QuantizedKVCache(kv_format="fp8")
     cache = sparkq.QuantizedKVCache(group_size=64)

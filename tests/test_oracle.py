@@ -710,3 +710,72 @@ def test_attention_gate16_against_torch_and_known_answers():
     g1, o1 = o.attention_gate16(ones, a16, big, o.BF16)
     assert np.all(o.bits_to_f32(g1, o.BF16) == 1.0)
     assert np.array_equal(o1, a16.transpose(0, 2, 1, 3).reshape(b, length, h * d))
+
+
+# ---------------------------------------------------------------------------
+# affine KV caches of 8, 4 and 2 bits and the staged attention over them
+# ---------------------------------------------------------------------------
+
+def test_kv_quantize_affine_matches_c_and_packing():
+    """The numpy affine KV quantizer equals the C one at 8 bits bit for bit;
+    at 4 bits its words are the W4 packing (pack4, pinned by a known answer)
+    of its codes; at 2 bits sixteen codes fill a word from the low bits; and
+    every width dequantizes within half a step of the input."""
+    x = o.randn(41, 1, 3 * 5 * 128).reshape(3, 5, 128)
+    x[0, 0, :32] = 1.5                                  # a constant group: scale 0
+    for g in (32, 64, 128):
+        p8, s8, b8 = o.kv_quantize_affine(x, g, 8, o.BF16)
+        c8, cs, cb = o.kv_quantize_affine_u8(x, g, o.BF16)
+        assert np.array_equal(p8, c8) and np.array_equal(s8, cs) and np.array_equal(b8, cb)
+        assert np.array_equal(o.kv_dequantize_affine(p8, s8, b8, g, 8, o.BF16),
+                              o.kv_dequantize_affine_u8(c8, cs, cb, g, o.BF16))
+    p4, s4, b4 = o.kv_quantize_affine(x, 32, 4, o.BF16)
+    sf = np.repeat(o.bits_to_f32(s4, o.BF16), 32, -1)
+    bf = np.repeat(o.bits_to_f32(b4, o.BF16), 32, -1)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        codes = np.where(sf != 0, np.clip(np.rint((x - bf) / sf), 0, 15), 0).astype(np.uint8)
+    assert np.array_equal(p4.reshape(-1, 16), o.pack4(codes.reshape(-1, 128)))
+    y = np.tile(np.array([0, 1, 2, 3], np.float32), 8)[None]      # one group of 32
+    p2, s2, b2 = o.kv_quantize_affine(y, 32, 2, o.F16)
+    assert o.bits_to_f32(s2, o.F16)[0, 0] == 1.0 and o.bits_to_f32(b2, o.F16)[0, 0] == 0.0
+    assert p2.tolist() == [[0xE4E4E4E4, 0xE4E4E4E4]]  # codes 0,1,2,3 from the low bits
+    for bits in (8, 4, 2):
+        p, s, b = o.kv_quantize_affine(x, 64, bits, o.F16)
+        back = o.kv_dequantize_affine(p, s, b, 64, bits, o.F16)
+        step = np.repeat(o.bits_to_f32(s, o.F16), 64, -1)
+        assert np.all(np.abs(back - x) <= step / 2 + 1e-3 * np.abs(x) + 1e-6), bits
+
+
+def test_sdpa_staged_oracle_pins():
+    """sdpa_staged against sdpa_prefill (no mask, causal), and the mask
+    semantics of the reference's fallback: an all-True boolean mask and an
+    all-zero additive one change nothing; an -inf additive entry hides a
+    token like a False; a row with nothing visible averages every value (the
+    finfo.min fill); a mask broadcast from [L,N] equals the full one; values
+    may have a head dim of their own."""
+    b, hq, hkv, length, n, d, dv = 1, 4, 2, 3, 7, 8, 16
+    q = o.randn(42, 1, b * hq * length * d).reshape(b, hq, length, d)
+    k = o.randn(42, 2, b * hkv * n * d).reshape(b, hkv, n, d)
+    v = o.randn(42, 3, b * hkv * n * d).reshape(b, hkv, n, d)
+    assert np.allclose(o.sdpa_staged(q, k, v, 0.3), o.sdpa_prefill(q, k, v, 0.3, False))
+    assert np.allclose(o.sdpa_staged(q, k, v, 0.3, "causal"), o.sdpa_prefill(q, k, v, 0.3, True))
+    ones = np.ones((length, n), bool)
+    assert np.allclose(o.sdpa_staged(q, k, v, 0.3, ones), o.sdpa_staged(q, k, v, 0.3))
+    assert np.allclose(o.sdpa_staged(q, k, v, 0.3, np.zeros((length, n))),
+                       o.sdpa_staged(q, k, v, 0.3))
+    hide = ones.copy()
+    hide[:, 2] = False
+    add = np.where(hide, 0.0, -np.inf)
+    assert np.allclose(o.sdpa_staged(q, k, v, 0.3, hide), o.sdpa_staged(q, k, v, 0.3, add))
+    none = ones.copy()
+    none[1] = False
+    out = o.sdpa_staged(q, k, v, 0.3, none)
+    vr = np.repeat(v.astype(np.float64), hq // hkv, axis=1)
+    assert np.allclose(out[:, :, 1], vr.mean(2))
+    full = np.broadcast_to(hide, (b, hq, length, n))
+    assert np.allclose(o.sdpa_staged(q, k, v, 0.3, full), o.sdpa_staged(q, k, v, 0.3, hide))
+    v2 = o.randn(42, 4, b * hkv * n * dv).reshape(b, hkv, n, dv)
+    out2 = o.sdpa_staged(q, k, v2, 0.3, "causal")
+    assert out2.shape == (b, hq, length, dv)
+    # the last causal row sees every token: the weights of the unmasked call
+    assert np.allclose(out2[:, :, -1], o.sdpa_staged(q, k, v2, 0.3)[:, :, -1])
