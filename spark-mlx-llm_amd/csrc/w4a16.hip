@@ -2521,6 +2521,11 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
     hipLaunchKernelGGL((w4_gemm_x16w_kernel<128, 4>), gw, dim3(256), 0, st, a);
 }
 
+// one row quad per wave, every quad in one round (w4q.hip); 1 = not taken
+int w4_gemvq_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
+                    int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, hipStream_t st,
+                    const void* res);
+
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
                  void* y, int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt,
                  void* ws, size_t wsb, hipStream_t st, const void* res, bool* res_done) {
@@ -2531,6 +2536,13 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
   if (need > 0 && (ws == nullptr || wsb < need))
     return set_error(SPARKQ_ERR_WORKSPACE,
                      "w4a16_linear needs a workspace of %zu bytes (got %zu)", need, wsb);
+  {
+    const int rc = w4_gemvq_linear(x, w, s, b, y, M, N, K, G, xdt, ydt, st, res);
+    if (rc != 1) {
+      if (res_done) *res_done = rc == 0 && res != nullptr;
+      return rc;
+    }
+  }
   const StreamPlan sp = plan_stream(M, N, K, G);
   if (sp.ok) {
     GemvStreamArgs a{};
