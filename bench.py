@@ -8,11 +8,16 @@ weight buffers per layer (1.70 GB per sweep, so the weights are cold in the
 graph and replayed; inputs are resident in HBM before the timed region.
 
 Also reported in the same JSON line: the M=4/8/16 sweeps, the prefill GEMM
-TFLOPS (M in 16/512/2048), W8A8 GB/s (M in 1/8/16), INT8-KV decode attention
-GB/s (B in 1/8, N in 4096/32768), the roofline of the dominant kernel and
-the oracle's multi-threaded CPU GEMV timed on this host.
+per shape (M in 16/512/2048 over the same 36 layers of distinct weights;
+GB/s at M=16, TFLOPS above) with its own roofline block (gate+up M=2048),
+W8A8 GB/s (M in 1/8/16), INT8-KV decode attention GB/s (B in 1/8, N in
+4096/32768), the roofline of the dominant kernel, and the CPU legs timed on
+this host's cores (the headline GEMV sweep, the GEMM, W8A8 and INT8-KV
+attention).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extras]
+       python bench.py --only-dominant | --only-gemm all|NAME:M   (profiler drivers)
+       python bench.py --trace-summary RUN_results.db             (per-shape rows)
 """
 
 from __future__ import annotations
@@ -130,13 +135,33 @@ def bench_w4_projection(torch, sparkq, dev, layers, name, m, iters):
     return ms / len(layers)  # per projection
 
 
-def bench_gemm(torch, sparkq, dev, layer, name, m, iters):
+def bench_gemm(torch, sparkq, dev, layers, name, m, iters):
+    """One W4A16 projection at M rows over every layer's distinct weights in
+    one graph replay (36 launches, weights cold in the MALL); returns ms per
+    launch."""
     n, k = PROJ[name]
     x = torch.randn((m, k), device=dev).to(torch.bfloat16)
-    wq, s, b = layer[name]
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    graph = capture(torch, lambda: sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y))
-    return Timer(torch).time(graph.replay, iters, 2)
+
+    def fn():
+        for layer in layers:
+            wq, s, b = layer[name]
+            sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y)
+
+    graph = capture(torch, fn)
+    ms = Timer(torch).time(graph.replay, iters, 2) / len(layers)
+    del graph
+    return ms
+
+
+def gemm_line(name, m, ms):
+    n, k = PROJ[name]
+    tf = 2 * m * n * k / (ms / 1e3) / 1e12
+    line = {"ms": round(ms, 5), "TFLOP/s": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+    if m <= 32:  # weight-streaming regime: the bound is HBM
+        gbs = w4_bytes(n, k) / (ms / 1e3) / 1e9
+        line.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+    return line
 
 
 def bench_w8a8(torch, sparkq, dev, m, iters, copies=36):
@@ -356,33 +381,205 @@ def only_dominant(torch, sparkq, dev, iters):
     log(f"dominant kernel x {iters * LAYERS} launches, then 5 copies of {256 << 20} bytes")
 
 
-def cpu_baseline(layer_host, budget_s=12.0):
-    """The oracle's OpenMP fp32 dequantize-then-dot GEMV on this host, M=1,
-    one layer's three projections per pass, repeated for ~budget_s."""
+GEMM_PMC_FILE = os.path.join(ROOT, "profiles", "w4_gemm_gate_up_m2048_pmc.md")
+
+
+def gemm_counters():
+    """MFMA and VALU busy fractions of the dominant GEMM shape (gate+up,
+    M=2048) from the committed PMC summary, or {} when there is none."""
+    out = {}
+    try:
+        for line in open(GEMM_PMC_FILE):
+            key, _, val = line.partition(":")
+            if key in ("mfma_busy_frac", "valu_busy_frac", "mfma_flop_frac"):
+                out[key] = float(val.strip())
+    except (OSError, ValueError):
+        pass
+    return out
+
+
+def only_gemm(torch, sparkq, dev, which, iters):
+    """Driver for rocprofv3 runs over the prefill GEMM: every (projection, M)
+    of the GEMM sweep (which == "all"), or one of them ("gate_up:2048"), each
+    over 36 layers of distinct weights, iters graph-free passes."""
+    shapes = [(name, m) for name in PROJ for m in (16, 512, 2048)]
+    if which != "all":
+        name, m = which.split(":")
+        shapes = [(name, int(m))]
+    gen = torch.Generator(device=dev).manual_seed(0)
+    for name, m in shapes:
+        n, k = PROJ[name]
+        ws = []
+        for _ in range(LAYERS):
+            w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+            ws.append(sparkq.affine_quantize(w, group_size=G))
+            del w
+        x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(iters):
+            for wq, s, b in ws:
+                sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y)
+        torch.cuda.synchronize()
+        log(f"{name} M={m}: {iters * LAYERS} launches")
+        del ws
+
+
+def trace_summary(path):
+    """Per-shape rows of a rocprofv3 kernel trace, from its rocpd database
+    (*_results.db, the default output) or a *_kernel_trace.csv: launches,
+    average and total duration per (kernel, grid size) in first-launch order;
+    the GEMM shapes have distinct grids."""
+    rows = {}
+
+    def add(name, grid, dur_ns):
+        e = rows.setdefault((name, grid), [0, 0.0])
+        e[0] += 1
+        e[1] += dur_ns / 1e3
+
+    if path.endswith(".db"):
+        import sqlite3
+
+        con = sqlite3.connect(path)
+        for name, gx, gy, gz, start, end in con.execute(
+                "select name, grid_x, grid_y, grid_z, start, end from kernels order by start"):
+            add(name, f"{gx}x{gy}x{gz}", end - start)
+    else:
+        import csv
+
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                grid = "x".join(r.get(f"Grid_Size_{a}", "?") for a in "XYZ")
+                add(r["Kernel_Name"], grid, int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    print("| kernel | grid (work-items) | launches | avg us | total us |")
+    print("|---|---|---|---|---|")
+    for (name, grid), (cnt, tot) in rows.items():
+        short = name if len(name) < 90 else name[:87] + "..."
+        print(f"| `{short}` | {grid} | {cnt} | {tot / cnt:.2f} | {tot:.1f} |")
+
+
+def cpu_threads():
+    """Host threads for the CPU legs: OMP_NUM_THREADS when set (the GPU host
+    allots a fixed share of its cores per GPU that way), else every core in
+    this process's affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else len(os.sched_getaffinity(0))
+
+
+def host_cpu():
+    import subprocess
+
+    import oracle as o
+
+    model = "unknown"
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next(l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name"))
+    except (OSError, StopIteration, subprocess.SubprocessError):
+        try:
+            model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
+                         if l.startswith("model name"))
+        except (OSError, StopIteration):
+            pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "isa": o.cpu_isa()}
+
+
+def _run_for(fn, budget_s, min_runs=1):
+    """Calls fn until budget_s has passed (at least min_runs times, after one
+    untimed call); returns (runs, seconds)."""
+    fn()
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and runs >= min_runs:
+            return runs, el
+
+
+def cpu_baseline(layers_host, threads, cpu, budget_s=10.0):
+    """Headline CPU leg: the oracle's OpenMP fp32 dequantize-then-dot GEMV on
+    this host at M=1 over the same 36 layers of distinct weights as the GPU
+    sweep (1.70 GB, cold in the host caches), for about budget_s."""
+    import oracle as o
+
+    x = {k: o.randn16(0, k, k).reshape(1, k) for k in (2560, 9728)}
+    per_layer = sum(w4_bytes(*PROJ[n]) for n in PROJ)
+    done = [0]
+
+    def sweep_part():
+        layer = layers_host[done[0] % len(layers_host)]
+        for name, (wq, s, b) in layer.items():
+            o.cpu_w4a16_gemv(x[PROJ[name][1]], wq, s, b, G, threads)
+        done[0] += 1
+
+    runs, el = _run_for(sweep_part, budget_s)
+    gbs = per_layer * runs / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"{runs} layers (QKV+gate_up+down, {per_layer} weight bytes each) of the 36-layer "
+                       f"W4A16 G64 GEMV sweep at M=1, cycled in order, in {el:.1f} s on {threads} threads "
+                       f"({cpu['isa']}) of {cpu['model']} ({cpu['logical_cpus']} logical CPUs); "
+                       "MLX CPU backend unavailable (mlx not installed)")}
+
+
+def cpu_legs(layers_host, threads, budget_s=2.0):
+    """The CPU legs of the other workloads, each run for about budget_s:
+    W4A16 GEMM (gate+up at M=16/512/2048), W8A8 (gate+up at M=1/8/16 over 4
+    distinct int8 weight sets) and INT8-KV decode attention (32/8 heads,
+    D=128; B=8 N=32768 is left out: 545 MB of cache per call)."""
     import numpy as np
 
     import oracle as o
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
-    x = {k: o.randn16(0, k, k).reshape(1, k) for k in (2560, 9728)}
-    per_pass = sum(w4_bytes(*PROJ[n]) for n in PROJ)
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        for name, (wq, s, b) in layer_host.items():
-            o.cpu_w4a16_gemv(x[PROJ[name][1]], wq, s, b, G, threads)
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    gbs = per_pass * passes / el / 1e9
-    try:
-        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except (OSError, StopIteration):
-        model = "unknown"
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": (f"{passes} passes of one layer's QKV+gate_up+down W4A16 G64 GEMV at M=1 "
-                       f"({per_pass} weight bytes each) in {el:.1f} s on {threads} threads, {model}; "
-                       "MLX CPU backend unavailable (mlx not installed)")}
+    res = {}
+    n, k = PROJ["gate_up"]
+    for m in (16, 512, 2048):
+        x = o.randn16(0, 100 + m, m * k).reshape(m, k)
+        i = [0]
+
+        def gemm():
+            wq, s, b = layers_host[i[0] % len(layers_host)]["gate_up"]
+            o.cpu_w4a16_gemv(x, wq, s, b, G, threads)
+            i[0] += 1
+
+        runs, el = _run_for(gemm, budget_s if m < 2048 else 0.0)
+        ms = el / runs * 1e3
+        line = {"ms": round(ms, 3), "TFLOP/s": round(2 * m * n * k / ms / 1e9, 4), "runs": runs}
+        if m <= 32:
+            line["GB/s"] = round(w4_bytes(n, k) / ms / 1e6, 2)
+        res[f"w4a16 gate_up M={m}"] = line
+    rng = np.random.default_rng(0)
+    ws = [(rng.integers(-127, 128, (n, k), dtype=np.int8), (rng.random(n) * 1e-3).astype(np.float32))
+          for _ in range(4)]
+    for m in (1, 8, 16):
+        x = o.randn16(0, 200 + m, m * k).reshape(m, k)
+        i = [0]
+
+        def w8a8():
+            wq, sw = ws[i[0] % len(ws)]
+            o.cpu_w8a8_linear(x, wq, sw, threads)
+            i[0] += 1
+
+        runs, el = _run_for(w8a8, budget_s)
+        ms = el / runs * 1e3
+        res[f"w8a8 gate_up M={m}"] = {"ms": round(ms, 3), "GB/s": round((n * k + 4 * n) / ms / 1e6, 2),
+                                      "runs": runs}
+    del ws
+    hq, hkv, d = 32, 8, 128
+    for b, nn in ((1, 4096), (1, 32768), (8, 4096)):
+        kc = rng.integers(-127, 128, (b, hkv, nn, d), dtype=np.int8)
+        vc = rng.integers(-127, 128, (b, hkv, nn, d), dtype=np.int8)
+        sc = np.full((b, hkv, nn), 0x2000, np.uint16)  # fp16 2^-7
+        q = o.randn16(0, 300 + b, b * hq * d).reshape(b, hq, d)
+        runs, el = _run_for(lambda: o.cpu_int8kv_sdpa(q, kc, sc, vc, sc, 1 / math.sqrt(d), threads),
+                            budget_s)
+        ms = el / runs * 1e3
+        kv_bytes = 2 * b * hkv * nn * d + 2 * b * hkv * nn * 2
+        res[f"int8kv_sdpa B={b} N={nn}"] = {"ms": round(ms, 3), "GB/s": round(kv_bytes / ms / 1e6, 2),
+                                            "runs": runs}
+    res["threads"] = threads
+    return res
 
 
 def main():
@@ -394,7 +591,14 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-dominant", action="store_true",
                     help="run only the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--only-gemm", default=None, metavar="all|NAME:M",
+                    help="run only prefill GEMM launches (for rocprofv3 --kernel-trace / --pmc)")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="print per-(kernel, grid) rows of a rocprofv3 kernel trace and exit")
     args = ap.parse_args()
+    if args.trace_summary is not None:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of "
                                    "it (--gpus must be 1)"}))
@@ -410,6 +614,9 @@ def main():
         raise RuntimeError("libsparkq unusable on cuda:0 (needs gfx950)")
     if args.only_dominant:
         only_dominant(torch, sparkq, dev, max(args.steps, 1))
+        return
+    if args.only_gemm:
+        only_gemm(torch, sparkq, dev, args.only_gemm, max(args.steps, 1))
         return
     log("generating 36 layers of W4A16 G64 weights")
     layers = make_w4_layers(torch, sparkq, dev, LAYERS)
@@ -446,12 +653,10 @@ def main():
         extras["w4a16_decode_sweep"] = sweeps
         log("prefill GEMM")
         gemm = {}
-        for name, (n, k) in PROJ.items():
+        for name in PROJ:
             for m in (16, 512, 2048):
-                gm = bench_gemm(torch, sparkq, dev, layers[0], name, m, 10)
-                tf = 2 * m * n * k / (gm / 1e3) / 1e12
-                gemm[f"{name} M={m}"] = {"ms": round(gm, 4), "TFLOP/s": round(tf, 1),
-                                         "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                gm = bench_gemm(torch, sparkq, dev, layers, name, m, 3 if m == 2048 else 5)
+                gemm[f"{name} M={m}"] = gemm_line(name, m, gm)
         extras["w4a16_prefill_gemm"] = gemm
         log("W8A8")
         extras["w8a8"] = {f"M={m}": bench_w8a8(torch, sparkq, dev, m, 5) for m in (1, 8, 16)}
@@ -475,14 +680,29 @@ def main():
     cpu = None
     if not args.skip_cpu:
         log("CPU baseline")
-        host = {}
-        for name, (wq, s, b) in layers[0].items():
-            host[name] = (wq.cpu().view(torch.int32).numpy().view(np.uint32),
-                          s.cpu().view(torch.int16).numpy().view(np.uint16),
-                          b.cpu().view(torch.int16).numpy().view(np.uint16))
-        cpu = cpu_baseline(host)
+        host = []
+        for layer in layers:
+            host.append({name: (wq.cpu().view(torch.int32).numpy().view(np.uint32),
+                                s.cpu().view(torch.int16).numpy().view(np.uint16),
+                                b.cpu().view(torch.int16).numpy().view(np.uint16))
+                         for name, (wq, s, b) in layer.items()})
+        threads, cpu_info = cpu_threads(), host_cpu()
+        cpu = cpu_baseline(host, threads, cpu_info)
+        cpu["host"] = cpu_info
+        if not args.skip_extras:
+            log("CPU legs of the other workloads")
+            extras["cpu_legs"] = cpu_legs(host, threads)
+        del host
 
     prefill = extras.get("w4a16_prefill_gemm", {}).get("gate_up M=2048")
+    roofline_gemm = None
+    if prefill:
+        n, k = PROJ["gate_up"]
+        roofline_gemm = {"bound": "mfma", "achieved": prefill["TFLOP/s"], "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": prefill["frac_bf16_peak"],
+                         "kernel": "gemm_prep_kernel + w4_gemm_x16w_kernel (gate+up 19456x2560, M=2048)",
+                         "flop_per_launch": 2 * 2048 * n * k, "avg_launch_ms": prefill["ms"],
+                         **gemm_counters()}
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -503,6 +723,7 @@ def main():
         "prefill_gemm_tflops": prefill["TFLOP/s"] if prefill else None,
         "prefill_gemm_frac_bf16_peak": prefill["frac_bf16_peak"] if prefill else None,
         "roofline": roofline,
+        "roofline_gemm": roofline_gemm,
         "cpu_baseline": cpu,
         "extras": extras,
     }

@@ -24,7 +24,7 @@ __all__ = [
     "kv_quantize_s8", "kv_quantize_affine_u8", "kv_dequantize_s8",
     "kv_dequantize_affine_u8", "sdpa_decode", "sdpa_prefill", "sdpa_prefill_rounded",
     "kv_quantize_affine", "kv_dequantize_affine", "sdpa_staged",
-    "cpu_w4a16_gemv", "scalar_f32_to_bf16", "scalar_f32_to_f16",
+    "cpu_w4a16_gemv", "cpu_w8a8_linear", "cpu_int8kv_sdpa", "cpu_isa", "scalar_f32_to_bf16", "scalar_f32_to_f16",
     "scalar_f16_to_f32",
     "attention_gate16", "add16", "rms_norm16", "gelu16", "gelu_mul16", "rope16", "ffn_block", "qkv_rope",
 ]
@@ -50,17 +50,38 @@ def _lib():
     return _LIB
 
 
+def _cpu_flags():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("flags"):
+                return set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return set()
+
+
+def cpu_isa() -> str:
+    """The instruction set of the CPU legs this host runs: 'avx512' when the
+    CPU has AVX-512 F/BW/VL/VNNI, else 'avx2'."""
+    return "avx512" if {"avx512f", "avx512bw", "avx512vl", "avx512_vnni"} <= _cpu_flags() else "avx2"
+
+
 def _cpu():
     global _CPU
     if _CPU is None:
-        path = os.path.join(_HERE, "libsparkq_cpubase.so")
+        name = "libsparkq_cpubase_avx512.so" if cpu_isa() == "avx512" else "libsparkq_cpubase.so"
+        path = os.path.join(_HERE, name)
         if not os.path.exists(path):
             _build()
         _CPU = ctypes.CDLL(path)
-        _CPU.sq_cpu_w4a16_gemv.restype = ctypes.c_int
-        _CPU.sq_cpu_w4a16_gemv.argtypes = [ctypes.c_void_p] * 4 + [
-            ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
-            ctypes.c_void_p, ctypes.c_int]
+        P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        for fn in ("sq_cpu_w4a16_gemv", "sq_cpu_w4a16_matmul"):
+            getattr(_CPU, fn).restype = I
+            getattr(_CPU, fn).argtypes = [P] * 4 + [I64, I64, I64, I, P, I]
+        _CPU.sq_cpu_w8a8_linear.restype = I
+        _CPU.sq_cpu_w8a8_linear.argtypes = [P, P, P, I64, I64, I64, P, I]
+        _CPU.sq_cpu_int8kv_sdpa.restype = I
+        _CPU.sq_cpu_int8kv_sdpa.argtypes = [P] * 5 + [I64] * 5 + [ctypes.c_float, P, I]
     return _CPU
 
 
@@ -612,17 +633,50 @@ def qkv_rope(x16, wq, s, b, group_size: int, n_heads: int, n_kv: int, head_dim: 
 # ---------------------------------------------------------------------------
 
 def cpu_w4a16_gemv(x16, wq, s, b, group_size: int, threads: int = 0):
-    """Multi-threaded fp32 dequantize-then-dot; returns (y fp32, threads)."""
+    """Multi-threaded fp32 dequantize-then-matmul (any M); returns (y fp32,
+    threads used)."""
     x16 = _c(x16, np.uint16)
     wq, s, b = _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
     m, k = x16.shape
     n = wq.shape[0]
     y = np.empty((m, n), np.float32)
-    used = _cpu().sq_cpu_w4a16_gemv(_p(x16), _p(wq), _p(s), _p(b), m, n, k,
-                                    group_size, _p(y), threads)
+    used = _cpu().sq_cpu_w4a16_matmul(_p(x16), _p(wq), _p(s), _p(b), m, n, k,
+                                      group_size, _p(y), threads)
     if used < 0:
         raise ValueError("unsupported CPU baseline shape")
     return y, used
+
+
+def cpu_w8a8_linear(x16, wq, sw, threads: int = 0):
+    """Multi-threaded per-token int8 quantization, int8 dots into int32 and
+    the fp32 scale epilogue; x16 bf16 bits [M,K], wq int8 [N,K], sw fp32 [N].
+    Returns (y fp32 [M,N], threads used)."""
+    x16 = _c(x16, np.uint16)
+    wq, sw = _c(wq, np.int8), _c(sw, np.float32)
+    m, k = x16.shape
+    n = wq.shape[0]
+    y = np.empty((m, n), np.float32)
+    used = _cpu().sq_cpu_w8a8_linear(_p(x16), _p(wq), _p(sw), m, n, k, _p(y), threads)
+    if used < 0:
+        raise ValueError("unsupported CPU baseline shape")
+    return y, used
+
+
+def cpu_int8kv_sdpa(q16, kc, ks16, vc, vs16, scale: float, threads: int = 0):
+    """Multi-threaded INT8-KV GQA decode attention: q16 bf16 bits [B,Hq,D],
+    kc/vc int8 [B,Hkv,N,D], ks16/vs16 fp16 bits [B,Hkv,N]. Returns (out fp32
+    [B,Hq,D], threads used)."""
+    q16 = _c(q16, np.uint16)
+    kc, vc = _c(kc, np.int8), _c(vc, np.int8)
+    ks16, vs16 = _c(ks16, np.uint16), _c(vs16, np.uint16)
+    bq, hq, d = q16.shape
+    _, hkv, n, _ = kc.shape
+    out = np.empty((bq, hq, d), np.float32)
+    used = _cpu().sq_cpu_int8kv_sdpa(_p(q16), _p(kc), _p(ks16), _p(vc), _p(vs16), bq, hq, hkv, n,
+                                     d, scale, _p(out), threads)
+    if used < 0:
+        raise ValueError("unsupported CPU baseline shape")
+    return out, used
 
 
 def attention_gate16(x16, attn16, gw16, dtype: int = BF16):

@@ -306,15 +306,43 @@ def test_sdpa_decode_against_numpy_and_invariants():
     assert np.allclose(op, out, atol=1e-12)
 
 
-def test_cpu_baseline_matches_oracle():
-    m, n, k, g = 2, 96, 256, 64
+@pytest.mark.parametrize("m,n,k", [(1, 96, 256), (2, 96, 256), (9, 37, 512), (37, 40, 1536)])
+def test_cpu_baseline_matches_oracle(m, n, k):
+    g = 64
     w = _w((n, k), seed=12)
     wq, s, b = o.w4_quantize(w, g)
     x16 = o.randn16(0, 13, m * k).reshape(m, k)
     y, used = o.cpu_w4a16_gemv(x16, wq, s, b, g)
     assert used >= 1
     ref = o.w4a16_matmul(x16, wq, s, b, g)
-    assert np.abs(y - ref).max() < 1e-4
+    assert np.abs(y - ref).max() < 1e-4 * max(1.0, np.abs(ref).max())
+
+
+def test_cpu_baseline_w8a8_is_bit_exact():
+    """The CPU W8A8 leg: per-token quantizer, int32 dots and the fp32 scale
+    product give the oracle's bits."""
+    m, n, k = 5, 70, 640
+    xf = o.bits_to_f32(o.randn16(0, 31, m * k), o.BF16).reshape(m, k)
+    xf[3] = 0.0  # an all-zero token
+    wq, sw = o.w8_quantize_channel(o.randn(0, 32, n * k, 0.02).reshape(n, k))
+    y, used = o.cpu_w8a8_linear(o.bf16_bits(xf), wq, sw)
+    qa, sa = o.a8_quantize(xf)
+    ref = o.w8a8_epilogue(o.int8_matmul(qa, wq), sa, sw)
+    assert used >= 1
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("b,n", [(1, 1), (1, 300), (2, 77)])
+def test_cpu_baseline_int8kv_sdpa_matches_oracle(b, n):
+    hq, hkv, d = 8, 2, 128
+    q16 = o.randn16(0, 40, b * hq * d).reshape(b, hq, d)
+    kc, ks = o.kv_quantize_s8(o.randn(0, 41, b * hkv * n * d).reshape(b, hkv, n, d))
+    vc, vs = o.kv_quantize_s8(o.randn(0, 42, b * hkv * n * d).reshape(b, hkv, n, d))
+    out, used = o.cpu_int8kv_sdpa(q16, kc, ks, vc, vs, 1 / math.sqrt(d))
+    ref = o.sdpa_decode(o.bits_to_f32(q16, o.BF16), o.kv_dequantize_s8(kc, ks),
+                        o.kv_dequantize_s8(vc, vs), 1 / math.sqrt(d))
+    assert used >= 1
+    assert np.abs(out - ref).max() < 1e-5
 
 
 # ---------------------------------------------------------------------------
