@@ -1520,9 +1520,13 @@ struct GemmX16Args {
   const uint16_t* b2;  // [N][K2p]
   void* y;
   int y_dtype, M, N, K, K2p;
-  // split-K (wide kernel): grid z = split, S splits of the 64-k steps; the
-  // fp32 tile partials and one counter per output tile live in the workspace
-  int S;
+  // work items (a 1-D grid): items [0, full) are whole output tiles, tile t
+  // at column block t % tiles_n and row block t / tiles_n; the tiles
+  // [full, tiles) are split along k into S pieces each, piece-major (item
+  // full + p * (tiles - full) + i is piece p of tile full + i, so the
+  // workgroups that run at the same time read the same k range), whose fp32
+  // partials and one counter per split tile live in the workspace
+  int tiles_n, tiles, full, S;
   float* part;
   unsigned* counters;
 };
@@ -1567,11 +1571,17 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
   // wave-uniform, so that the per-wave buffer descriptors live in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane >> 5, l32 = lane & 31;
-  const int n0 = blockIdx.x * (64 * NWV), m0 = blockIdx.y * kBM;
   const int K = a.K, ng = K / G;
-  // this workgroup's 64-k steps [s_begin, nsteps)
-  const int s_begin = (int)((int64_t)blockIdx.z * (K / kBK) / a.S);
-  const int nsteps = (int)((int64_t)(blockIdx.z + 1) * (K / kBK) / a.S);
+  // work item -> (tile, piece) and this workgroup's 64-k steps [s_begin, nsteps)
+  const int item = blockIdx.x;
+  const bool split = item >= a.full;
+  const int nsplit = a.tiles - a.full;
+  const int tile = split ? a.full + (item - a.full) % nsplit : item;
+  const int piece = split ? (item - a.full) / nsplit : 0;
+  const int S = split ? a.S : 1;
+  const int n0 = (tile % a.tiles_n) * (64 * NWV), m0 = (tile / a.tiles_n) * kBM;
+  const int s_begin = (int)((int64_t)piece * (K / kBK) / S);
+  const int nsteps = (int)((int64_t)(piece + 1) * (K / kBK) / S);
   const int mrows = min(kBM, a.M - m0);
   const int wn0 = n0 + 64 * wave;  // this wave's first column
   const int nrows = __builtin_amdgcn_readfirstlane(max(0, min(64, a.N - wn0)));
@@ -1664,38 +1674,50 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     if (step + 1 < nsteps) body(step + 1, std::integral_constant<int, 1>{});
   }
 
-  if (a.S > 1) {
-    // every split stores its raw tile; the last to arrive sums them in split
-    // order (deterministic), resets the counter and finishes the tile
-    constexpr int TV = 4 * 2 * 16;  // accumulators per lane
-    const int ntiles = gridDim.x * gridDim.y, tile = blockIdx.y * gridDim.x + blockIdx.x;
-    const size_t tsz = (size_t)TV * NT;
-    float* mine = a.part + ((size_t)blockIdx.z * ntiles + tile) * tsz + tid;
+  if (split) {
+    // every piece stores its raw tile (16-byte stores through to the
+    // device-coherent level, sc1, like the split-K atomics); the last to
+    // arrive adds the pieces in piece order (deterministic; its own from
+    // registers), resets the counter and finishes the tile. A lane's
+    // accumulator chunk c (16 bytes) sits at (c * NT + tid) * 16, so each
+    // store and load instruction moves 1 KB per wave.
+    const int stile = tile - a.full;
+    constexpr uint32_t PB = 4 * 2 * 16 * 4 * NT;  // bytes per piece
+    const rsrc_t rp = make_rsrc(a.part + (size_t)stile * S * (PB / 4), (uint32_t)S * PB);
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
       for (int y = 0; y < 2; ++y)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) splitk_store(mine + (size_t)((x * 2 + y) * 16 + v) * NT, acc[x][y][v]);
-    __shared__ int s_last;
-    if (!splitk_arrive(a.counters + tile, a.S, &s_last)) return;
-    const float* base = a.part + (size_t)tile * tsz + tid;
-    const size_t zstride = (size_t)ntiles * tsz;
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        f32x16_t t = f32x16_t{};
-        for (int z = 0; z < a.S; ++z) {
-          float v16[16];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) v16[v] = splitk_load(base + z * zstride + (size_t)((x * 2 + y) * 16 + v) * NT);
-#pragma unroll
-          for (int v = 0; v < 16; ++v) t[v] += v16[v];
+        for (int q = 0; q < 4; ++q) {
+          const u32x4_t v = {__float_as_uint(acc[x][y][4 * q]), __float_as_uint(acc[x][y][4 * q + 1]),
+                             __float_as_uint(acc[x][y][4 * q + 2]), __float_as_uint(acc[x][y][4 * q + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(v, rp, (uint32_t)tid * 16u,
+                                                 piece * PB + ((x * 2 + y) * 4 + q) * NT * 16, 16);
         }
-        acc[x][y] = t;
+    __shared__ int s_last;
+    if (!splitk_arrive(a.counters + stile, S, &s_last)) return;
+#pragma unroll
+    for (int xy = 0; xy < 8; ++xy) {
+      f32x16_t t = f32x16_t{};
+      for (int z = 0; z < S; ++z) {
+        if (z == piece) {
+          t += acc[xy >> 1][xy & 1];
+          continue;
+        }
+        u32x4_t v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          v[c] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rp, (uint32_t)tid * 16u, z * PB + (xy * 4 + c) * NT * 16, 16));
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t[4 * c + e] += __uint_as_float(v[c][e]);
       }
-    splitk_reset(a.counters + tile);
+      acc[xy >> 1][xy & 1] = t;
+    }
+    splitk_reset(a.counters + stile);
   }
 
   // undo the row shifts: y = 2^(ex[m] + es[n]) * acc
@@ -1732,6 +1754,34 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
   }
 
   const int gn0 = wn0 + l32;
+  if (a.y_dtype == SPARKQ_BF16 && a.N % 8 == 0 && ((uintptr_t)a.y & 15) == 0) {
+    // bf16 output through LDS (the A buffers are idle after the main loop's
+    // closing barrier): in two halves of 64 rows, each wave writes its
+    // 64 x 64 piece into its own 8 KB of LDS and stores whole 16-byte row
+    // segments, 1 KB per wave instruction, instead of one 2-byte value per
+    // lane (a wave's LDS stores and loads are performed in order)
+    unsigned char* ot = reinterpret_cast<unsigned char*>(As) + wave * 8192;
+    uint16_t* yb = reinterpret_cast<uint16_t*>(a.y);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            *reinterpret_cast<uint16_t*>(ot + (32 * x + mfma32_row(lane, v)) * 128 + (32 * y + l32) * 2) =
+                (uint16_t)bf16x2_rne(acc[2 * h + x][y][v], 0.0f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int pc = lane + 64 * i, row = pc >> 3, seg = pc & 7;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ot + row * 128 + seg * 16);
+        const int gm = m0 + 64 * h + row, gn = wn0 + 8 * seg;
+        if (gm < a.M && gn < a.N) *reinterpret_cast<u32x4_t*>(yb + (int64_t)gm * a.N + gn) = v;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int x = 0; x < 4; ++x)
 #pragma unroll
@@ -2372,27 +2422,39 @@ static GemmX16Layout gemm_x16_layout(int64_t M, int64_t N, int64_t K, int G) {
   return l;
 }
 
-// Split-K of the wide GEMM, for long rows only (K >= 4096; measured: at
-// K = 2560 the partial round trip costs more than the extra waves bring):
-// about two waves per SIMD (2048 waves of one 128x64 tile each) when the
-// output tiles alone are too few, at least twelve 64-k steps per split, and
-// only while the tile counters fit.
+// Work plan of the wide GEMM (two workgroups per CU): whole rounds of tiles
+// run unsplit, and the tiles of a last round that would leave at least three
+// quarters of the slots idle (half, for rows of 64 steps or more; all tiles,
+// when there are that few) are split along k into S pieces, S = slots /
+// tail tiles, capped at four pieces and at twelve 64-k steps per piece,
+// while the split tiles' counters fit. The
+// last piece of a tile reads the others' 128 KB partials in dependent
+// rounds of loads; measured on the MI355X, that pays only when the split
+// fills a mostly idle chip (QKV 3584 x 2560 at M = 512: 51.8 -> 36.5 us,
+// down 2560 x 9728 at M = 512: 107.5 -> 77.5 us) and costs time when a
+// quarter or more of the slots are busy anyway (QKV at M = 2048 split in
+// two: 56.7 -> 64.5 us; gate+up 19456 x 2560 at M = 2048 with its 192-tile
+// last round split in two: 239 -> 243 us); down at M = 2048 (160 tiles of
+// 152 steps) gains from three pieces.
 struct WidePlan {
-  int S;
+  int tiles_n, tiles, full, S, items;
   size_t part_bytes;
 };
 static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
-  WidePlan p{1, 0};
-  const int64_t tiles = cdiv(N, 256) * cdiv(M, kBM), nsteps = K / kBK;
-  if (tiles > kMaxCounterTiles) return p;
-  // long rows only: a split of rows under 64 steps costs more in partials
-  // than it gains in parallelism (QKV 3584x2560 at M = 2048: 57 -> 99 us at
-  // S = 2; at M = 512, 50 -> 47 us at S = 3)
-  int64_t S = nsteps >= 64 ? (2048 + 2 * tiles) / (4 * tiles) : 1;
-  S = std::min<int64_t>(S, nsteps / 12);
+  WidePlan p{};
+  const int64_t tn = cdiv(N, 256), T = tn * cdiv(M, kBM), nsteps = K / kBK;
+  const int64_t P = 2 * (int64_t)device_cus();
+  const int64_t tail = T % P;
+  int64_t S = tail && (tail <= P / 4 || (nsteps >= 64 && tail < P / 2)) ? P / tail : 1;
+  S = std::min<int64_t>(S, std::min<int64_t>(env_int("SPARKQ_W4_GEMM_MAXS", 4), nsteps / 12));
+  if (tail > kMaxCounterTiles) S = 1;
   if (env_int("SPARKQ_W4_SPLITS", 0)) S = std::min<int64_t>(env_int("SPARKQ_W4_SPLITS", 1), nsteps);
+  p.tiles_n = (int)tn;
+  p.tiles = (int)T;
   p.S = (int)std::max<int64_t>(S, 1);
-  if (p.S > 1) p.part_bytes = round_up((size_t)p.S * tiles * kBM * 256 * 4, 256);
+  p.full = (int)(p.S > 1 ? T - tail : T);
+  p.items = (int)(p.full + (T - p.full) * p.S);
+  if (p.S > 1) p.part_bytes = round_up((size_t)(T - p.full) * p.S * kBM * 256 * 4, 256);
   return p;
 }
 
@@ -2509,10 +2571,13 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   a.K = K;
   a.K2p = p.K2p;
   const WidePlan wp = plan_wide(M, N, K);
+  a.tiles_n = wp.tiles_n;
+  a.tiles = wp.tiles;
+  a.full = wp.full;
   a.S = wp.S;
   a.part = reinterpret_cast<float*>(ws + l.bytes);
   a.counters = counters;
-  dim3 gw((unsigned)cdiv(N, 256), (unsigned)cdiv(M, kBM), (unsigned)wp.S);
+  dim3 gw((unsigned)wp.items);
   if (G == 32)
     hipLaunchKernelGGL((w4_gemm_x16w_kernel<32, 4>), gw, dim3(256), 0, st, a);
   else if (G == 64)
