@@ -28,6 +28,7 @@ from .ext import (
     w8a16_per_channel,
     w8a8_linear,
 )
+from . import torch_ops  # registers torch.ops.sparkq.* (custom ops with fake kernels)
 
 __all__ = [
     "QuantizedKVCache",
