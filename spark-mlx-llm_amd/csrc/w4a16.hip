@@ -1531,8 +1531,9 @@ struct GemmX16Args {
   unsigned* counters;
 };
 
-// Wide variant: a 128 x (64*NWV) tile per workgroup of NWV waves, each wave
-// owning 128 rows x 64 columns. Activations go through LDS (shared by the
+// Wide variant: a (32*MX) x (64*NWV) tile per workgroup of NWV waves, each
+// wave owning 32*MX rows x 64 columns (MX even: the staged output goes in
+// halves of 64 rows). Activations go through LDS (shared by the
 // waves); each wave loads its own packed weights straight into registers and
 // decodes them there. The k order inside a 64-k step is permuted so that one
 // 16-byte load per lane covers the whole step: lane half j of sub-step ss
@@ -1561,11 +1562,14 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int G, int NWV>
+template <int G, int NWV, int MX>
 __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a) {
   constexpr int NT = 64 * NWV;
-  constexpr int AL = kBM * kBK / 8 / NT;  // 16-byte A pieces per thread per step
-  __shared__ __attribute__((aligned(16))) uint16_t As[2 * kBM * kBK];
+  constexpr int BM = 32 * MX;                // tile rows: MX 32-row fragments per wave
+  constexpr int AL = BM * kBK / 8 / NT;      // 16-byte A pieces per thread per step
+  // two A buffers, at least 8 KB per wave for the staged bf16 output
+  constexpr int AS = 2 * BM * kBK > NWV * 64 * 64 ? 2 * BM * kBK : NWV * 64 * 64;
+  __shared__ __attribute__((aligned(16))) uint16_t As[AS];
 
   const int tid = threadIdx.x, lane = tid & 63;
   // wave-uniform, so that the per-wave buffer descriptors live in SGPRs
@@ -1579,10 +1583,10 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
   const int tile = split ? a.full + (item - a.full) % nsplit : item;
   const int piece = split ? (item - a.full) / nsplit : 0;
   const int S = split ? a.S : 1;
-  const int n0 = (tile % a.tiles_n) * (64 * NWV), m0 = (tile / a.tiles_n) * kBM;
+  const int n0 = (tile % a.tiles_n) * (64 * NWV), m0 = (tile / a.tiles_n) * BM;
   const int s_begin = (int)((int64_t)piece * (K / kBK) / S);
   const int nsteps = (int)((int64_t)(piece + 1) * (K / kBK) / S);
-  const int mrows = min(kBM, a.M - m0);
+  const int mrows = min(BM, a.M - m0);
   const int wn0 = n0 + 64 * wave;  // this wave's first column
   const int nrows = __builtin_amdgcn_readfirstlane(max(0, min(64, a.N - wn0)));
   // rows past the tile's last one read as zero
@@ -1626,9 +1630,9 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     return reinterpret_cast<u32x4_t*>(reinterpret_cast<unsigned char*>(As) + byte_off);
   };
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[MX][2];
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int x = 0; x < MX; ++x)
 #pragma unroll
     for (int y = 0; y < 2; ++y) acc[x][y] = f32x16_t{};
 
@@ -1652,15 +1656,15 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
         bf1[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, t1), s1, c1));
       }
 #pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        const u32x4_t af = *lds_at(lds_r[ss] + (uint32_t)(st * kBM * kBK * 2 + x * 32 * 128));
+      for (int x = 0; x < MX; ++x) {
+        const u32x4_t af = *lds_at(lds_r[ss] + (uint32_t)(st * BM * kBK * 2 + x * 32 * 128));
         acc[x][0] = mfma32x32x16<F16>(af, bf0, acc[x][0]);
         acc[x][1] = mfma32x32x16<F16>(af, bf1, acc[x][1]);
       }
     }
     if (step + 1 < nsteps) {
 #pragma unroll
-      for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)((st ^ 1) * kBM * kBK * 2)) = ra[i];
+      for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)((st ^ 1) * BM * kBK * 2)) = ra[i];
     }
     __syncthreads();
   };
@@ -1682,10 +1686,10 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     // accumulator chunk c (16 bytes) sits at (c * NT + tid) * 16, so each
     // store and load instruction moves 1 KB per wave.
     const int stile = tile - a.full;
-    constexpr uint32_t PB = 4 * 2 * 16 * 4 * NT;  // bytes per piece
+    constexpr uint32_t PB = MX * 2 * 16 * 4 * NT;  // bytes per piece
     const rsrc_t rp = make_rsrc(a.part + (size_t)stile * S * (PB / 4), (uint32_t)S * PB);
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < MX; ++x)
 #pragma unroll
       for (int y = 0; y < 2; ++y)
 #pragma unroll
@@ -1698,7 +1702,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     __shared__ int s_last;
     if (!splitk_arrive(a.counters + stile, S, &s_last)) return;
 #pragma unroll
-    for (int xy = 0; xy < 8; ++xy) {
+    for (int xy = 0; xy < 2 * MX; ++xy) {
       f32x16_t t = f32x16_t{};
       for (int z = 0; z < S; ++z) {
         if (z == piece) {
@@ -1727,7 +1731,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
   for (int y = 0; y < 2; ++y) {
     const int esn = (int)__builtin_amdgcn_raw_buffer_load_b32(res, (32 * y + l32) * 4, 0, 0);
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < MX; ++x)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const u32x4_t e4 = buf_load16(rex, (uint32_t)(x * 32 + 8 * q4 + 4 * j) * 4u);
@@ -1746,7 +1750,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     for (int y = 0; y < 2; ++y)
       bf[y] = buf_load16(rb2, (uint32_t)((32 * y + l32) * K2p + ks + 8 * j) * 2u);
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
+    for (int x = 0; x < MX; ++x) {
       const u32x4_t af = buf_load16(ra2, (uint32_t)((32 * x + l32) * K2p + ks + 8 * j) * 2u);
       acc[x][0] = mfma32x32x16<BF16>(af, bf[0], acc[x][0]);
       acc[x][1] = mfma32x32x16<BF16>(af, bf[1], acc[x][1]);
@@ -1756,14 +1760,14 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
   const int gn0 = wn0 + l32;
   if (a.y_dtype == SPARKQ_BF16 && a.N % 8 == 0 && ((uintptr_t)a.y & 15) == 0) {
     // bf16 output through LDS (the A buffers are idle after the main loop's
-    // closing barrier): in two halves of 64 rows, each wave writes its
-    // 64 x 64 piece into its own 8 KB of LDS and stores whole 16-byte row
-    // segments, 1 KB per wave instruction, instead of one 2-byte value per
-    // lane (a wave's LDS stores and loads are performed in order)
+    // closing barrier): in halves of 64 rows, each wave writes its 64 x 64
+    // piece into its own 8 KB of LDS and stores whole 16-byte row segments,
+    // 1 KB per wave instruction, instead of one 2-byte value per lane (a
+    // wave's LDS stores and loads are performed in order)
     unsigned char* ot = reinterpret_cast<unsigned char*>(As) + wave * 8192;
     uint16_t* yb = reinterpret_cast<uint16_t*>(a.y);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < MX / 2; ++h) {
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -1783,7 +1787,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     return;
   }
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int x = 0; x < MX; ++x)
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
       const int gn = gn0 + 32 * y;
@@ -2422,39 +2426,58 @@ static GemmX16Layout gemm_x16_layout(int64_t M, int64_t N, int64_t K, int G) {
   return l;
 }
 
-// Work plan of the wide GEMM (two workgroups per CU): whole rounds of tiles
-// run unsplit, and the tiles of a last round that would leave at least three
-// quarters of the slots idle (half, for rows of 64 steps or more; all tiles,
-// when there are that few) are split along k into S pieces, S = slots /
-// tail tiles, capped at four pieces and at twelve 64-k steps per piece,
-// while the split tiles' counters fit. The
-// last piece of a tile reads the others' 128 KB partials in dependent
-// rounds of loads; measured on the MI355X, that pays only when the split
-// fills a mostly idle chip (QKV 3584 x 2560 at M = 512: 51.8 -> 36.5 us,
-// down 2560 x 9728 at M = 512: 107.5 -> 77.5 us) and costs time when a
-// quarter or more of the slots are busy anyway (QKV at M = 2048 split in
-// two: 56.7 -> 64.5 us; gate+up 19456 x 2560 at M = 2048 with its 192-tile
-// last round split in two: 239 -> 243 us); down at M = 2048 (160 tiles of
-// 152 steps) gains from three pieces.
+// Work plan of the wide GEMM (up to two workgroups per CU).
+//
+// Grids of 128-row tiles that would fill less than a quarter of the slots
+// (QKV 3584 x 2560 and down 2560 x 9728 at M = 512) take 64-row tiles and
+// split every tile along k into the number of pieces S that minimises
+// ceil(T*S / CUs) * ceil(steps / S) + 2*S: the longest chain of 64-k steps
+// on one CU (two workgroups sharing a CU each run at about half speed) plus
+// the cost of a piece's partial round trip. Measured on the MI355X (whole
+// call, prologue included): QKV M = 512 two pieces 35.0 us (one 45.0,
+// three 39.4, four 35.6), down M = 512 three pieces 76.2 us (two 92.0, four
+// 93.1, six 77.5).
+//
+// Larger grids keep 128-row tiles: whole rounds of tiles run unsplit, and
+// the tiles of a last round that leaves at least three quarters of the
+// slots idle (half, for rows of 64 steps or more) are split into S = slots
+// / tail tiles, capped at four pieces and at twelve 64-k steps per piece.
+// The last piece of a tile reads the others' partials in dependent rounds
+// of loads, which costs time when a quarter or more of the slots are busy
+// anyway (QKV at M = 2048 in two pieces: 59.5 -> 71.3 us; gate+up 19456 x
+// 2560 at M = 512: 89.8 -> 98.6 us); down at M = 2048 (160 tiles of 152
+// steps) gains from three pieces (190.6 -> 161.9 us).
+//
+// Split tiles need their counters in the fixed block, else nothing splits.
 struct WidePlan {
-  int tiles_n, tiles, full, S, items;
+  int MX, tiles_n, tiles, full, S, items;
   size_t part_bytes;
 };
 static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
   WidePlan p{};
-  const int64_t tn = cdiv(N, 256), T = tn * cdiv(M, kBM), nsteps = K / kBK;
-  const int64_t P = 2 * (int64_t)device_cus();
-  const int64_t tail = T % P;
-  int64_t S = tail && (tail <= P / 4 || (nsteps >= 64 && tail < P / 2)) ? P / tail : 1;
-  S = std::min<int64_t>(S, std::min<int64_t>(env_int("SPARKQ_W4_GEMM_MAXS", 4), nsteps / 12));
-  if (tail > kMaxCounterTiles) S = 1;
+  const int64_t cus = device_cus(), P = 2 * cus;
+  p.MX = cdiv(N, 256) * cdiv(M, 128) < P / 4 && M > 64 && !env_int("SPARKQ_W4_GEMM_MX4", 0) ? 2 : 4;
+  const int64_t BM = 32 * p.MX;
+  const int64_t tn = cdiv(N, 256), T = tn * cdiv(M, BM), nsteps = K / kBK;
+  int64_t tail = T % P, S = 1;
+  if (p.MX == 2) {
+    tail = T;
+    int64_t best = -1;
+    for (int64_t s = 1; s <= std::min<int64_t>(8, std::max<int64_t>(nsteps / 8, 1)); ++s) {
+      const int64_t cost = cdiv(T * s, cus) * cdiv(nsteps, s) + 2 * s;
+      if (best < 0 || cost < best) best = cost, S = s;
+    }
+  } else if (tail && (tail <= P / 4 || (nsteps >= 64 && tail < P / 2))) {
+    S = std::min<int64_t>(P / tail, std::min<int64_t>(env_int("SPARKQ_W4_GEMM_MAXS", 4), nsteps / 12));
+  }
   if (env_int("SPARKQ_W4_SPLITS", 0)) S = std::min<int64_t>(env_int("SPARKQ_W4_SPLITS", 1), nsteps);
+  if (tail > kMaxCounterTiles) S = 1;
   p.tiles_n = (int)tn;
   p.tiles = (int)T;
   p.S = (int)std::max<int64_t>(S, 1);
   p.full = (int)(p.S > 1 ? T - tail : T);
   p.items = (int)(p.full + (T - p.full) * p.S);
-  if (p.S > 1) p.part_bytes = round_up((size_t)(T - p.full) * p.S * kBM * 256 * 4, 256);
+  if (p.S > 1) p.part_bytes = round_up((size_t)(T - p.full) * p.S * BM * 256 * 4, 256);
   return p;
 }
 
@@ -2578,12 +2601,17 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   a.part = reinterpret_cast<float*>(ws + l.bytes);
   a.counters = counters;
   dim3 gw((unsigned)wp.items);
-  if (G == 32)
-    hipLaunchKernelGGL((w4_gemm_x16w_kernel<32, 4>), gw, dim3(256), 0, st, a);
-  else if (G == 64)
-    hipLaunchKernelGGL((w4_gemm_x16w_kernel<64, 4>), gw, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((w4_gemm_x16w_kernel<128, 4>), gw, dim3(256), 0, st, a);
+#define SPARKQ_X16W(GG, MM) hipLaunchKernelGGL((w4_gemm_x16w_kernel<GG, 4, MM>), gw, dim3(256), 0, st, a)
+  if (wp.MX == 2) {
+    if (G == 32) SPARKQ_X16W(32, 2);
+    else if (G == 64) SPARKQ_X16W(64, 2);
+    else SPARKQ_X16W(128, 2);
+  } else {
+    if (G == 32) SPARKQ_X16W(32, 4);
+    else if (G == 64) SPARKQ_X16W(64, 4);
+    else SPARKQ_X16W(128, 4);
+  }
+#undef SPARKQ_X16W
 }
 
 // one row quad per wave, every quad in one round (w4q.hip); 1 = not taken

@@ -120,6 +120,27 @@ def test_gemm_split_k(gpu, m, n, k, g):
     assert torch.equal(y32, _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32))
 
 
+@pytest.mark.parametrize("m,n,k,g", [(100, 520, 1024, 64), (200, 200, 4096, 32), (130, 90, 9728, 128),
+                                     (512, 2560, 9728, 64)])
+def test_gemm_tile_rows(gpu, m, n, k, g, monkeypatch):
+    """Small grids take 64-row tiles (two 32-row fragments per wave) instead
+    of 128-row ones. Without a K split both tilings add every output's
+    products in the same order, so they agree bit for bit; with the planned
+    split both match the oracle."""
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m + k)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    outs = {}
+    for mx4 in ("0", "1"):
+        monkeypatch.setenv("SPARKQ_W4_GEMM_MX4", mx4)
+        monkeypatch.delenv("SPARKQ_W4_SPLITS", raising=False)
+        y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+        check_fp32(y32.cpu().numpy(), ref)
+        check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16)), ref, o.BF16)
+        monkeypatch.setenv("SPARKQ_W4_SPLITS", "1")
+        outs[mx4] = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    assert torch.equal(outs["0"], outs["1"])
+
+
 @pytest.mark.parametrize("m,n,k,g", [(1, 37, 576, 32), (3, 41, 576, 64), (2, 4, 64, 32),
                                      (4, 130, 9728, 32), (1, 5, 10240, 128), (3, 9, 4608, 64)])
 def test_decode_ragged_shapes(gpu, m, n, k, g):
