@@ -1414,6 +1414,7 @@ struct GemmPrepArgs {
   int* es;             // [N]
   uint16_t* b2;        // [N][K2p] bf16
   int M, N, K, G, K2p;
+  int rw;  // weight rows per block
 };
 
 __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
@@ -1435,14 +1436,21 @@ __device__ __forceinline__ float block_max256(float v, float* red) {
   return v;
 }
 
-// blocks [0, M): one activation row each; blocks [M, M + N/4): four weight
-// rows each, one per wave
+// Blocks [0, nwb = ceil(N / rw)): rw weight rows each (dispatched first: they
+// run longer than a row block); blocks [nwb, nwb + M): one activation row
+// each (the conversion pass reads the row again, from L2). In a weight block
+// the (scale, bias) pairs are read coalesced into LDS, each row's
+// maximum reduced by four threads, and the outputs written coalesced: the
+// fp16 scales straight from the pair index, the bias slots through LDS as
+// whole 4-byte slot pairs.
 __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
-  __shared__ float red[4];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* red = reinterpret_cast<float*>(smem);
   const int tid = threadIdx.x, lane = tid & 63;
   const int ng = a.K / a.G;
-  if ((int)blockIdx.x < a.M) {
-    const int m = blockIdx.x;
+  const int nwb = (a.N + a.rw - 1) / a.rw;  // weight blocks come first
+  if ((int)blockIdx.x >= nwb) {
+    const int m = blockIdx.x - nwb;
     const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.K);
     const int nc = a.K / 8;
     float amax = 0.0f;
@@ -1458,6 +1466,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
     u32x4_t* dst = reinterpret_cast<u32x4_t*>(a.xh + (int64_t)m * a.K);
     uint16_t* a2 = a.a2 + (int64_t)m * a.K2p;
     const int cpg = a.G / 8;  // chunks per group: 4, 8 or 16 consecutive lanes
+    // (256 and nc are multiples of cpg: the lanes of a group are active together)
     for (int c = tid; c < nc; c += 256) {
       const u32x4_t v = xr[c];
       float f[8];
@@ -1486,28 +1495,87 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
     for (int sl = 3 * ng + tid; sl < a.K2p; sl += 256) a2[sl] = 0;
     return;
   }
-  const int n = 4 * ((int)blockIdx.x - a.M) + (tid >> 6);
-  if (n >= a.N) return;
-  const uint16_t* sr = a.sc + (int64_t)n * ng;
-  const uint16_t* br = a.bi + (int64_t)n * ng;
-  float smax = 0.0f;
-  for (int g = lane; g < ng; g += 64) smax = fmaxf(smax, fabsf(bf16_to_f32(sr[g])));
+  // weight rows [n0, n0 + nr)
+  const int rw = a.rw;
+  const int n0 = (int)blockIdx.x * rw;
+  const int nr = min(rw, a.N - n0);
+  const int nel = nr * ng;
+  uint32_t* pair = reinterpret_cast<uint32_t*>(smem + 16);          // [rw * ng] (s | b << 16)
+  int* rexp = reinterpret_cast<int*>(pair + rw * ng);               // [rw]
+  uint32_t* slots = reinterpret_cast<uint32_t*>(rexp + rw);         // [rw * K2p / 2]
+  const rsrc_t rs = make_rsrc(a.sc + (int64_t)n0 * ng, (uint32_t)nel * 2u);
+  const rsrc_t rb = make_rsrc(a.bi + (int64_t)n0 * ng, (uint32_t)nel * 2u);
+  for (int i0 = 0; i0 < nel; i0 += 4 * 256) {
+    uint32_t sv[4], bv[4];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) smax = fmaxf(smax, __shfl_xor(smax, o));
-  const int e = row_shift(smax, 10);
-  if (lane == 0) a.es[n] = e;
-  uint16_t* spr = a.sp + (int64_t)n * ng;
-  uint16_t* b2 = a.b2 + (int64_t)n * a.K2p;
-  for (int g = lane; g < ng; g += 64) {
-    const float s = bf16_to_f32(sr[g]);
-    spr[g] = f32_to_f16(ldexpf(s, -e));
-    uint16_t hi, lo;
-    split_bf16(fmaf(8.0f, s, bf16_to_f32(br[g])), hi, lo);
-    b2[3 * g] = hi;
-    b2[3 * g + 1] = lo;
-    b2[3 * g + 2] = hi;
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + 256 * u + tid;
+      sv[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, i < nel ? 2 * i : (int)kOob, 0, 0);
+      bv[u] = __builtin_amdgcn_raw_buffer_load_b16(rb, i < nel ? 2 * i : (int)kOob, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + 256 * u + tid;
+      if (i < nel) pair[i] = (sv[u] & 0xFFFFu) | (bv[u] << 16);
+    }
   }
-  for (int sl = 3 * ng + lane; sl < a.K2p; sl += 64) b2[sl] = 0;
+  __syncthreads();
+  {
+    const int r = tid >> 2, part = tid & 3;
+    float smax = 0.0f;
+    if (r < nr)
+      for (int g = part; g < ng; g += 4) smax = fmaxf(smax, fabsf(bf16_to_f32((uint16_t)pair[r * ng + g])));
+    smax = fmaxf(smax, __shfl_xor(smax, 1));
+    smax = fmaxf(smax, __shfl_xor(smax, 2));
+    if (r < nr && part == 0) {
+      const int e = row_shift(smax, 10);
+      rexp[r] = e;
+      a.es[n0 + r] = e;
+    }
+  }
+  // rw <= 64 rows: the four threads of a row are the threads above
+  __syncthreads();
+  uint16_t* spr = a.sp + (int64_t)n0 * ng;
+  uint16_t* sl16 = reinterpret_cast<uint16_t*>(slots);
+  const int K2p = a.K2p;
+  for (int i = tid; i < nel; i += 256) {
+    const int r = i / ng, g = i - r * ng;
+    const uint32_t pv = pair[i];
+    const float sf = bf16_to_f32((uint16_t)pv);
+    spr[i] = f32_to_f16(ldexpf(sf, -rexp[r]));
+    uint16_t hi, lo;
+    split_bf16(fmaf(8.0f, sf, bf16_to_f32((uint16_t)(pv >> 16))), hi, lo);
+    sl16[r * K2p + 3 * g] = hi;
+    sl16[r * K2p + 3 * g + 1] = lo;
+    sl16[r * K2p + 3 * g + 2] = hi;
+  }
+  for (int i = tid; i < nr * (K2p - 3 * ng); i += 256) {
+    const int r = i / (K2p - 3 * ng);
+    sl16[r * K2p + 3 * ng + (i - r * (K2p - 3 * ng))] = 0;
+  }
+  __syncthreads();
+  uint32_t* b2 = reinterpret_cast<uint32_t*>(a.b2 + (int64_t)n0 * K2p);
+  for (int i = tid; i < nr * K2p / 2; i += 256) b2[i] = slots[i];
+}
+
+// rows per weight block of the prologue (at most 64: four threads per row
+// reduce the row maximum; 16 by default) and its LDS bytes: the most rows
+// within 32 KB, else one row (rows of up to ~6500 groups fit in 64 KB).
+// Measured on the MI355X against one row per wave, the prologue of gate+up
+// 19456 x 2560 takes 13.5 -> 10.5 us at M = 512 and 17.7 -> 12.0 us at
+// M = 2048; QKV and down (few rows or long activation rows) are unchanged
+// within noise, as are 4 and 64 rows per block.
+struct PrepPlan {
+  int rw;
+  size_t lds;
+};
+static PrepPlan plan_prep(int K, int G) {
+  const size_t ng = (size_t)(K / G), row = ng * 4 + 4 + (size_t)bias_slots(K, G) * 2;
+  PrepPlan p{};
+  for (p.rw = (int)std::min<int64_t>(env_int("SPARKQ_PREP_RW", 16), 64); p.rw > 1; p.rw /= 2)
+    if (16 + p.rw * row <= 32768) break;
+  p.lds = 16 + p.rw * row;
+  return p;
 }
 
 struct GemmX16Args {
@@ -2578,7 +2646,9 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   p.K = K;
   p.G = G;
   p.K2p = bias_slots(K, G);
-  hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)(M + cdiv(N, 4))), dim3(256), 0, st, p);
+  const PrepPlan pp = plan_prep(K, G);
+  p.rw = pp.rw;
+  hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)(M + cdiv(N, pp.rw))), dim3(256), pp.lds, st, p);
   GemmX16Args a{};
   a.xh = p.xh;
   a.w = w;
