@@ -2,7 +2,8 @@
 // per-channel int8 weights, exact int32 accumulation on the int8 MFMA.
 //
 // Kernels
-//   i8_gemv_kernel       M <= 4 decode: whole rows per workgroup, 4 rows x
+//   i8_gemv_kernel       M <= 2 decode (M <= 4 when K % 64 != 0): whole
+//                        rows per workgroup, 4 rows x
 //                        256 bytes per load, v_dot4_i32_i8, activation
 //                        quantizer fused (one launch per projection)
 //   a8_quantize_kernel   one workgroup per token row (a8_quantize_reg_kernel
@@ -18,7 +19,7 @@
 //                        fmaf(float(acc)*sa[m], sw[n], bias[n]); splits of K
 //                        combine in the same launch (the last workgroup of a
 //                        tile sums the int32 partials).
-//   i8_rows16_kernel     5..16 token rows: 16 weight rows per workgroup, 8
+//   i8_rows_kernel       3..16 token rows: 16 weight rows per workgroup, 8
 //                        waves split K, both operands straight from global
 //                        memory into v_mfma_i32_16x16x64_i8.
 #include "common.h"
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(256, 2) void i8_skinny_kernel(I8Args args) {
 }
 
 // ---------------------------------------------------------------------------
-// decode GEMV (M <= 4), activation quantizer fused
+// decode GEMV (M <= 2; M <= 4 when K % 64 != 0), activation quantizer fused
 // ---------------------------------------------------------------------------
 // A workgroup owns R whole weight rows. Lane l = 4b + j loads the 16 bytes at
 // byte 16b of a 256-byte span of weight row 4q+j (4 rows x 256 contiguous
@@ -446,43 +447,55 @@ __global__ __launch_bounds__(256) void a8_quantize_reg_kernel(const void* __rest
 }
 
 // ---------------------------------------------------------------------------
-// 5..16 token rows: i8_rows16_kernel
+// 3..16 token rows: i8_rows_kernel
 // ---------------------------------------------------------------------------
 // One workgroup per 16 weight rows; its 8 waves split K into eighths. Both
 // int8 operands go from global memory straight into
 // v_mfma_i32_16x16x64_i8 (lane l: row l%16 of the weights / of the
 // activations, k 16*(l/16) .. +16 of each 64-k chunk); the quantized
 // activations (at most 16 x K bytes) stay in L2 for every workgroup. Each
-// wave issues the loads of eight chunks before their MFMAs; rows past M or N
-// read zeros through the bounded descriptors. The waves' int32 sums are
-// added through LDS (exact in any order) and wave 0 writes the epilogue.
-constexpr int kR16W = 8;   // waves per workgroup (K split)
-constexpr int kR16PD = 8;  // 64-k chunks in flight per wave
+// wave issues the loads of up to eight chunks (all of them in flight before
+// the first MFMA waits) and then their MFMAs; rows past M or N read zeros
+// through the bounded descriptors. The waves' int32 sums are added through
+// LDS (exact in any order) and wave 0 writes the epilogue.
+//
+// Measured on the MI355X (36 distinct weight sets per graph replay, bf16
+// activations, quantizer launch included): QKV 3584 x 2560 at M = 8 9.2 us,
+// gate+up 19456 x 2560 19.1 us, down 2560 x 9728 16.0 us. Slower, and not
+// kept: splitting K across two to four workgroups per row tile when the
+// tiles do not fill the chip (QKV 9.2 -> 13.1 us: the partials' round trip),
+// 32-row tiles sharing each activation load (gate+up 19.1 -> 22.6 us), and
+// a single launch whose workgroups quantize the activations themselves and
+// run 4x4x4 MFMAs over 256-byte row spans (QKV 9.1 -> 15.0 us at M = 8,
+// 25.7 us at M = 16: every workgroup re-reads the M x K activations).
+constexpr int kRW = 8;   // waves per workgroup (K split)
+constexpr int kRPD = 8;  // 64-k chunks in flight per wave
 
-__global__ __launch_bounds__(64 * kR16W) void i8_rows16_kernel(I8Args args) {
-  __shared__ i32x4_t red[kR16W - 1][64];
+__global__ __launch_bounds__(64 * kRW) void i8_rows_kernel(I8Args args) {
+  __shared__ i32x4_t red[kRW - 1][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, grp = lane >> 4;
   const int K = args.K, N = args.N, M = args.M;
   const int n0 = blockIdx.x * 16;
   const int nch = K / 64;
-  const int c0 = wave * nch / kR16W, c1 = (wave + 1) * nch / kR16W;
+  const int c0 = wave * nch / kRW, c1 = (wave + 1) * nch / kRW;
   const int nrows = min(16, N - n0);
   const rsrc_t rb = make_rsrc(args.b + (int64_t)n0 * K, (uint32_t)nrows * (uint32_t)K);
   const rsrc_t ra = make_rsrc(args.a, (uint32_t)M * (uint32_t)K);
   const uint32_t off = (uint32_t)(n16 * K + 16 * grp);
   i32x4_t acc = {0, 0, 0, 0};
-  for (int c = c0; c < c1; c += kR16PD) {
-    u32x4_t av[kR16PD], bv[kR16PD];
+  for (int c = c0; c < c1; c += kRPD) {
+    u32x4_t av[kRPD], bv[kRPD];
 #pragma unroll
-    for (int u = 0; u < kR16PD; ++u) {
+    for (int u = 0; u < kRPD; ++u) {
       const bool ok = c + u < c1;  // wave-uniform
       bv[u] = buf_load16(rb, ok ? off + 64u * (uint32_t)(c + u) : kOob);
       av[u] = buf_load16(ra, ok ? off + 64u * (uint32_t)(c + u) : kOob);
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < kR16PD; ++u)
+    for (int u = 0; u < kRPD; ++u)
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, av[u]),
                                                   __builtin_bit_cast(i32x4_t, bv[u]), acc, 0, 0, 0);
   }
@@ -490,8 +503,8 @@ __global__ __launch_bounds__(64 * kR16W) void i8_rows16_kernel(I8Args args) {
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int w = 0; w < kR16W - 1; ++w) acc += red[w][lane];
-  // lane (g, n16) holds token rows 4g .. 4g+3 of weight row n0 + n16
+  for (int w = 0; w < kRW - 1; ++w) acc += red[w][lane];
+  // lane (grp, n16) holds token rows 4grp .. 4grp+3 of weight row n0 + n16
   const int nn = n0 + n16;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -500,15 +513,15 @@ __global__ __launch_bounds__(64 * kR16W) void i8_rows16_kernel(I8Args args) {
   }
 }
 
-static bool use_rows16(int64_t M, int64_t N, int64_t K) {
-  return M > 4 && M <= 16 && K % 64 == 0 && N * K < (int64_t)kOob && M * K < (int64_t)kOob &&
-         !env_int("SPARKQ_I8_NO_ROWS16", 0);
+// 3..16 rows (1..16 with the decode GEMV switched off), whole 64-k chunks
+static bool use_rows(int64_t M, int64_t N, int64_t K) {
+  return M >= 1 && M <= 16 && K % 64 == 0 && N * K < (int64_t)kOob && M * K < (int64_t)kOob &&
+         !env_int("SPARKQ_I8_NO_ROWS", 0);
 }
 
-static int launch_rows16(const I8Args& args, hipStream_t st) {
-  hipLaunchKernelGGL(i8_rows16_kernel, dim3((unsigned)cdiv(args.N, 16)), dim3(64 * kR16W), 0, st,
-                     args);
-  return check_launch("i8_rows16_kernel");
+static int launch_rows(const I8Args& args, hipStream_t st) {
+  hipLaunchKernelGGL(i8_rows_kernel, dim3((unsigned)cdiv(args.N, 16)), dim3(64 * kRW), 0, st, args);
+  return check_launch("i8_rows_kernel");
 }
 
 // ---------------------------------------------------------------------------
@@ -519,6 +532,16 @@ static int launch_rows16(const I8Args& args, hipStream_t st) {
 // into SG = 1, 2 or 4 span groups; workgroups of 4 waves (8 when SG = 4)
 // cover R = 4 * waves / SG rows. The staged activations must fit the fixed
 // per-thread budget and the tensors the buffer loads' offset range.
+//
+// v_dot4 here against the 16x16x64 int8 MFMA of i8_rows_kernel (after its
+// own quantizer launch), measured on the MI355X with 36 distinct weight
+// sets per graph replay: at M = 1 and 2 the GEMV is faster (M = 1: QKV
+// 3584 x 2560 5.3 vs 12.4 us, gate+up 19456 x 2560 12.0 vs 16.2, down
+// 2560 x 9728 11.5 vs 15.0; M = 2: QKV 7.0 vs 12.5, gate+up 14.5 vs 16.7),
+// from M = 3 the MFMA path is (M = 3: QKV 8.6 vs 8.4, gate+up 18.3 vs
+// 17.1, down 15.9 vs 14.8; M = 4: QKV 9.0 vs 8.7, gate+up 18.6 vs 17.6,
+// down 16.4 vs 14.9). The GEMV re-stages M x K activations in every
+// workgroup and its dot products grow with M on the VALU.
 struct I8GemvPlan {
   bool ok;
   int SG, USr, US, NW, MQ, R;
@@ -528,7 +551,8 @@ struct I8GemvPlan {
 
 static I8GemvPlan plan_i8_gemv(int64_t M, int64_t N, int64_t K, int esize) {
   I8GemvPlan p{};
-  if (M > 4 || env_int("SPARKQ_I8_NO_GEMV", 0)) return p;
+  const int64_t maxm = K % 64 == 0 ? std::min<int64_t>(env_int("SPARKQ_I8_GEMV_MAXM", 2), 4) : 4;
+  if (M > maxm || env_int("SPARKQ_I8_NO_GEMV", 0)) return p;
   if (N * K >= (int64_t)kOob || M * K * esize >= (int64_t)kOob) return p;
   const int64_t U = cdiv(K, 256);
   if (U <= 10)
@@ -623,14 +647,13 @@ size_t w8a8_workspace(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   // the fused decode GEMV needs no workspace for any activation dtype
   if (plan_i8_gemv(M, N, K, 4).ok && plan_i8_gemv(M, N, K, 2).ok) return 0;
-  const I8Plan p = plan_i8(M, N, K);
+  const size_t part = use_rows(M, N, K) ? 0 : plan_i8(M, N, K).part_bytes;
   // counters, int8 activations, fp32 scales, int32 partials
-  return kCounterBytes + round_up((size_t)M * K, 256) + round_up((size_t)M * 4, 256) +
-         p.part_bytes;
+  return kCounterBytes + round_up((size_t)M * K, 256) + round_up((size_t)M * 4, 256) + part;
 }
 
 size_t i8_matmul_workspace(int64_t M, int64_t N, int64_t K) {
-  if (plan_i8_gemv(M, N, K, 1).ok) return 0;
+  if (plan_i8_gemv(M, N, K, 1).ok || use_rows(M, N, K)) return 0;
   const I8Plan p = plan_i8(M, N, K);
   return p.counter_bytes + p.part_bytes;
 }
@@ -676,7 +699,7 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
     g.mode = kOutRaw;
     return launch_i8_gemv(gp, g, 3, st);
   }
-  if (use_rows16(M, N, K)) {
+  if (use_rows(M, N, K)) {
     I8Args r{};
     r.a = a;
     r.b = b;
@@ -685,7 +708,7 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
     r.N = (int)N;
     r.K = (int)K;
     r.mode = kOutRaw;
-    return launch_rows16(r, st);
+    return launch_rows(r, st);
   }
   const I8Plan p = plan_i8(M, N, K);
   const size_t need = p.counter_bytes + p.part_bytes;
@@ -743,7 +766,7 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
   int32_t* part = reinterpret_cast<int32_t*>(base + kCounterBytes + round_up((size_t)M * K, 256) +
                                              round_up((size_t)M * 4, 256));
   if (int rc = a8_quantize(x, q, sa, M, K, xdt, st)) return rc;
-  if (use_rows16(M, N, K)) {
+  if (use_rows(M, N, K)) {
     I8Args r{};
     r.a = q;
     r.b = w;
@@ -757,7 +780,7 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
     r.N = (int)N;
     r.K = (int)K;
     r.mode = kOutEpilogue;
-    return launch_rows16(r, st);
+    return launch_rows(r, st);
   }
   const I8Plan p = plan_i8(M, N, K);
   I8Args args{};

@@ -51,7 +51,8 @@ def test_quantize_ties_round_to_even(gpu):
 @pytest.mark.parametrize("m,n,k", [(1, 3584, 2560), (8, 2560, 9728), (16, 19456, 2560),
                                    (33, 96, 256), (70, 130, 512), (2, 40, 32),
                                    (3, 37, 32), (4, 130, 9728), (2, 5, 10240), (1, 9, 4864),
-                                   (4, 2560, 2560), (5, 37, 64), (13, 100, 192), (16, 17, 2560)])
+                                   (4, 2560, 2560), (5, 37, 64), (13, 100, 192), (16, 17, 2560),
+                                   (7, 101, 4096), (11, 203, 2560), (9, 3, 9728)])
 def test_int8_matmul_int32_bit_exact(gpu, m, n, k):
     import sparkq
 
@@ -85,7 +86,8 @@ def _w8(n, k, seed=0):
 @pytest.mark.parametrize("dtype", [o.BF16, o.F16, o.F32])
 @pytest.mark.parametrize("m,n,k", [(1, 3584, 2560), (8, 2560, 9728), (16, 19456, 2560),
                                    (40, 100, 256), (1, 2560, 9728), (3, 37, 32), (4, 130, 4096),
-                                   (2, 21, 10240), (5, 37, 64), (12, 100, 9728)])
+                                   (2, 21, 10240), (5, 37, 64), (12, 100, 9728), (6, 101, 512),
+                                   (16, 4, 256), (9, 203, 2560), (7, 45, 9728)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_w8a8_linear_bit_exact(gpu, m, n, k, dtype, with_bias):
     import sparkq
