@@ -211,7 +211,10 @@ void w4_gemv_q_kernel(GemvQArgs a) {
 // that gives at least 8 quads per CU (two workgroups of ~nq/(2*CUs) waves
 // each), else one per CU, else one quad each; at most 16 waves. Measured
 // alternatives that ran slower on the gate+up weights: two or four quads per
-// wave (9.1-10 us against 7.8-8.1), one workgroup per CU (10.2 us).
+// wave (9.1-10 us against 7.8-8.1), one workgroup per CU (10.2 us). Rows of
+// up to 20 spans (the down projection, 2560 x 9728: 19 spans, five waves per
+// workgroup to stage its activations) ran 7.3 us here against 6.1 us in the
+// streaming kernel, so longer rows stay there.
 struct GemvQPlan {
   bool ok;
   int P, NWQ, U;

@@ -154,12 +154,14 @@ def test_decode_ragged_shapes(gpu, m, n, k, g):
 
 
 @pytest.mark.parametrize("n,k,g", [(37, 5632, 64), (36, 3712, 64), (1030, 6144, 128),
-                                   (2600, 3072, 32), (4, 9728, 64)])
+                                   (2600, 3072, 32), (4, 9728, 64), (100, 6144, 128), (2048, 8192, 64),
+                                   (1024, 10240, 32)])
 def test_decode_long_rows(gpu, n, k, g):
-    """M = 1 with rows longer than 2560 k takes the streaming kernel (one
-    workgroup per CU, row quads split evenly, items dealt round-robin): a
-    partial last row quad, a partial last span, more row quads than CUs
-    (uneven split) and fewer row quads than CUs."""
+    """M = 1 with rows longer than 2560 k: rows of up to 8 whole 512-k spans
+    and whole row quads take the one-round kernel, the rest the streaming
+    kernel (one workgroup per CU, row quads split evenly, items dealt
+    round-robin): a partial last row quad, a partial last span, more row
+    quads than CUs (uneven split) and fewer row quads than CUs."""
     for dtype in (o.BF16, o.F16):
         x, wq, s, b = w4_problem(1, n, k, g, dtype=dtype, seed=n + g)
         ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
