@@ -2549,16 +2549,18 @@ static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
   return p;
 }
 
-bool w4_mr_supported(int64_t M, int64_t N, int64_t K, int G);
+int64_t w4_mr_workspace(int64_t M, int64_t N, int64_t K, int G);
 int w4_mr_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
                  int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, hipStream_t st,
-                 const void* res);
+                 const void* res, void* ws, size_t wsb);
 
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
-  if (plan_stream(M, N, K, G).ok || w4_mr_supported(M, N, K, G) || plan_dec(M, N, K, G).ok ||
-      plan_gemv(M, N, K, G).ok)
-    return 0;
+  // in dispatch order
+  if (plan_stream(M, N, K, G).ok) return 0;
+  const int64_t mr = w4_mr_workspace(M, N, K, G);
+  if (mr >= 0) return (size_t)mr;
+  if (plan_dec(M, N, K, G).ok || plan_gemv(M, N, K, G).ok) return 0;
   // every workspace of this entry point starts with the counter block, so a
   // GEMM call never writes over the counters a later split-K call relies on
   if (M <= 32 && M < env_int("SPARKQ_W4_GEMM_FROM", 33)) {
@@ -2729,7 +2731,7 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     return check_launch("w4_gemv_stream_kernel");
   }
   {
-    const int rc = w4_mr_linear(x, w, s, b, y, M, N, K, G, xdt, ydt, st, res);
+    const int rc = w4_mr_linear(x, w, s, b, y, M, N, K, G, xdt, ydt, st, res, ws, wsb);
     if (rc != 1) {
       if (res_done) *res_done = rc == 0 && res != nullptr;
       return rc;

@@ -22,6 +22,12 @@
 //    dealt to the waves in contiguous runs. A wave sums its run of a tile in
 //    registers and leaves the sum in an LDS slot (a run touches at most two
 //    tiles); each output is the sum of its tile's slots in wave order.
+//  * Rows whose activations exceed the staging budget (the down projection,
+//    K = 9728) split K into KS ranges of whole 128-k segments
+//    and whole groups (grid.y): each workgroup stages the M rows of its range
+//    only, stores its outputs as fp32 partials, and the last workgroup of a
+//    tile range to arrive adds the KS partials in range order (coherent
+//    loads, deterministic) and writes the outputs.
 #include "common.h"
 
 namespace sparkq {
@@ -36,9 +42,12 @@ struct MrArgs {
   int y_dtype;
   int M, N, K;
   int nt;  // row tiles of 16
-  int P;   // workgroups
+  int P;   // workgroups (tile ranges)
   int TW;  // tiles of the largest workgroup
   int IW;  // items per wave
+  int KS;  // K ranges (grid.y)
+  float* part;         // [KS][M][N] partial outputs (KS > 1)
+  unsigned* counters;  // one per tile range, zero on entry and exit (KS > 1)
 };
 
 constexpr int kMrNW = 16;              // waves per workgroup
@@ -46,13 +55,14 @@ constexpr int kMrXC = 8;               // staged activation chunks (16 B) per th
 constexpr int kMrSP = 2;               // staged (scale, bias) pieces per thread, at most
 constexpr int kMrMaxLds = 160 * 1024;
 
-// LDS layout (byte offsets)
+// LDS layout (byte offsets); K is the workgroup's K range
 struct MrLds {
   int xrow;  // padded activation row (bytes)
   int xa;    // activations [M][K]
   int xs;    // group sums [K/G][16] fp32 (rows past M zero)
   int sb;    // (scale, bias) of the workgroup's rows [16*TW][K/G] dwords
   int part;  // run sums [waves][2][16][16] fp32
+  int flag;  // the split handshake's last-arrival flag
   int bytes;
 };
 __host__ __device__ __forceinline__ MrLds mr_lds(int M, int K, int TW, int G) {
@@ -62,7 +72,8 @@ __host__ __device__ __forceinline__ MrLds mr_lds(int M, int K, int TW, int G) {
   l.xs = (M * l.xrow + 15) & ~15;
   l.sb = l.xs + (K / G) * 64;
   l.part = l.sb + ((TW * 16 * (K / G) * 4 + 15) & ~15);
-  l.bytes = l.part + kMrNW * 2 * 256 * 4;
+  l.flag = l.part + kMrNW * 2 * 256 * 4;
+  l.bytes = l.flag + 16;
   return l;
 }
 
@@ -107,24 +118,26 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, r16 = lane & 15;
-  const int M = a.M, N = a.N, K = a.K;
-  const int ng = K / G, SEG = K >> 7, RB = K >> 1;
+  const int M = a.M, N = a.N, K = a.K, KS = a.KS;
+  const int Kl = K / KS, kbase = blockIdx.y * Kl;      // this workgroup's K range
+  const int ng = K / G, ngl = Kl / G, SEG = Kl >> 7, RB = K >> 1;
   const int t0 = blockIdx.x * a.nt / a.P;
   const int ntl = (blockIdx.x + 1) * a.nt / a.P - t0;  // tiles of this workgroup
   const int IW = a.IW;
   const int i0 = wave * IW;
   const int ni = max(0, min(IW, ntl * SEG - i0));      // items of this wave
-  const MrLds L = mr_lds(M, K, a.TW, G);
+  const MrLds L = mr_lds(M, Kl, a.TW, G);
 
   const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
   const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
   const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
   const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
 
-  // 1. staging loads: activation chunks and the (scale, bias) pieces of the
-  // workgroup's rows (16 * ntl contiguous rows)
-  const int nxc = (M * K) >> 3;
-  const int nsp = (ntl * 16 * ng) >> 3;
+  // 1. staging loads: activation chunks of the K range and the (scale,
+  // bias) pieces of the workgroup's rows (16 * ntl contiguous rows): 16-byte
+  // pieces of whole rows with one range, 4-byte pairs of groups with several
+  const int nxc = (M * Kl) >> 3;
+  const int nsp = KS == 1 ? (ntl * 16 * ng) >> 3 : (ntl * 16 * ngl) >> 1;
   // every thread issues the same loads (lanes with nothing to read use the
   // out-of-range offset): branches around loads here made the compiler
   // spill the staging registers
@@ -132,14 +145,29 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
 #pragma unroll
   for (int c = 0; c < kMrXC; ++c) {
     const int ci = tid + c * NT;
-    xr[c] = buf_load16(rx, ci < nxc ? 16u * ci : kOob);
+    const int m = ci / (Kl >> 3), kk = (ci - m * (Kl >> 3)) << 3;
+    xr[c] = buf_load16(rx, ci < nxc ? 2u * (uint32_t)(m * K + kbase + kk) : kOob);
   }
+  if (KS == 1) {
 #pragma unroll
-  for (int i = 0; i < kMrSP; ++i) {
-    const int pi = tid + i * NT;
-    const uint32_t off = pi < nsp ? 32u * (uint32_t)t0 * ng + 16u * pi : kOob;
-    sr[i] = buf_load16(rs, off);
-    br[i] = buf_load16(rb, off);
+    for (int i = 0; i < kMrSP; ++i) {
+      const int pi = tid + i * NT;
+      const uint32_t off = pi < nsp ? 32u * (uint32_t)t0 * ng + 16u * pi : kOob;
+      sr[i] = buf_load16(rs, off);
+      br[i] = buf_load16(rb, off);
+    }
+  } else {
+    // pair pi: row 16 t0 + pi / (ngl/2), groups kbase/G + 2 (pi % (ngl/2)) .. +1
+#pragma unroll
+    for (int i = 0; i < kMrSP; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int pi = tid + (4 * i + e) * NT;
+        const int rl = pi / (ngl >> 1), gp = pi - rl * (ngl >> 1);
+        const uint32_t off = pi < nsp ? 2u * (uint32_t)((16 * t0 + rl) * ng + kbase / G + 2 * gp) : kOob;
+        sr[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
+        br[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rb, (int)off, 0, 0);
+      }
   }
   // 2. the wave's weight items
   u32x4_t wv[NI];
@@ -148,7 +176,7 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
     const int it = i0 + k, tl = it / SEG, s = it - tl * SEG;
     const int row = 16 * (t0 + tl) + r16;
     const bool ok = k < ni && row < N;
-    wv[k] = buf_load16(rw, ok ? (uint32_t)row * RB + 64u * s + 16u * g : kOob);
+    wv[k] = buf_load16(rw, ok ? (uint32_t)row * RB + (uint32_t)(kbase >> 1) + 64u * s + 16u * g : kOob);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -159,27 +187,40 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
   for (int c = 0; c < kMrXC; ++c) {
     const int ci = tid + c * NT;
     if (ci < nxc) {
-      const int m = ci / (K >> 3), kk = (ci - m * (K >> 3)) << 3;
+      const int m = ci / (Kl >> 3), kk = (ci - m * (Kl >> 3)) << 3;
       *reinterpret_cast<u32x4_t*>(smem + L.xa + m * L.xrow + 2 * kk) = xr[c];
     }
   }
+  if (KS == 1) {
 #pragma unroll
-  for (int i = 0; i < kMrSP; ++i) {
-    const int pi = tid + i * NT;
-    if (pi < nsp) {
-      const u32x4_t s = sr[i], c = br[i];
-      u32x4_t lo, hi;
+    for (int i = 0; i < kMrSP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nsp) {
+        const u32x4_t s = sr[i], c = br[i];
+        u32x4_t lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = __builtin_amdgcn_perm(c[e], s[e], 0x05040100u);  // (s0, b0)
+          hi[e] = __builtin_amdgcn_perm(c[e], s[e], 0x07060302u);  // (s1, b1)
+        }
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kMrSP; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        lo[e] = __builtin_amdgcn_perm(c[e], s[e], 0x05040100u);  // (s0, b0)
-        hi[e] = __builtin_amdgcn_perm(c[e], s[e], 0x07060302u);  // (s1, b1)
+        const int pi = tid + (4 * i + e) * NT;
+        if (pi < nsp) {
+          sb[2 * pi] = __builtin_amdgcn_perm(br[i][e], sr[i][e], 0x05040100u);
+          sb[2 * pi + 1] = __builtin_amdgcn_perm(br[i][e], sr[i][e], 0x07060302u);
+        }
       }
-      *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
-      *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
-    }
   }
   __syncthreads();
-  for (int e = tid; e < ng * 16; e += NT) {
+  for (int e = tid; e < ngl * 16; e += NT) {
     const int grp = e >> 4, m = e & 15;
     float s = 0.0f;
     if (m < M) {
@@ -226,7 +267,7 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
         d = mfma16x16x32<T>(aop, bop, d);
         if (((c + 1) * 32) % G == 0) {
           const int grp = kb / G;
-          const uint32_t pair = sb[(tl * 16 + r16) * ng + grp];
+          const uint32_t pair = sb[(tl * 16 + r16) * ngl + grp];
           const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
           const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
           const f32x4_t xg = *reinterpret_cast<const f32x4_t*>(xs + grp * 16 + 4 * g);
@@ -242,7 +283,9 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
   if (cur >= 0) flush();
   __syncthreads();
 
-  // 5. each output: the sum of its tile's run slots in wave order
+  // 5. each output: the sum of its tile's run slots in wave order (with
+  // several K ranges, this range's partial)
+  const int64_t MN = (int64_t)M * N;
   for (int e = tid; e < ntl * 256; e += NT) {
     const int tl = e >> 8, m = (e >> 4) & 15, j = e & 15;
     const int n = 16 * (t0 + tl) + j;
@@ -254,25 +297,46 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
       v += part[(w * 2 + sl) * 256 + m * 16 + j];
     }
     const int64_t idx = (int64_t)m * N + n;
+    if (KS == 1)
+      store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
+    else
+      splitk_store(&a.part[blockIdx.y * MN + idx], v);
+  }
+  if (KS == 1) return;
+  // (the flag lives in the dynamic LDS: a static variable would take from
+  // the 160 KB the dynamic allocation is allowed)
+  if (!splitk_arrive(&a.counters[blockIdx.x], KS, reinterpret_cast<int*>(smem + L.flag))) return;
+  for (int e = tid; e < ntl * 256; e += NT) {
+    const int tl = e >> 8, m = (e >> 4) & 15, j = e & 15;
+    const int n = 16 * (t0 + tl) + j;
+    if (m >= M || n >= N) continue;
+    const int64_t idx = (int64_t)m * N + n;
+    const float v = splitk_sum(a.part + idx, MN, KS);
     store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
   }
+  splitk_reset(&a.counters[blockIdx.x]);
 }
 
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 // Plan: 9..16 rows (from 2 with SPARKQ_W4_MR_MIN), K a multiple of 128, the
-// activations, scales and run slots within 160 KB of LDS, at most 8 items
-// per wave and no wave run longer than a row (so it touches at most two
-// tiles). Measured per projection (bf16, G64): QKV 3584x2560 and gate+up
+// activations, scales and run slots within 160 KB of LDS, at most 8 items per
+// wave and no wave run longer than a row (so it touches at most two tiles).
+// The fewest K ranges (1, 2, 4 or 8) whose activation slice fits the staging
+// registers; with several, about one workgroup per CU over all ranges: down
+// 2560x9728 takes 13.5 us at 16 rows and 13.3 at 12 in four ranges, against
+// 17.1 and 15.5 on the skinny split-K kernel (at 8 rows two ranges took 14.4
+// against its 12.7, so fewer rows stay there). Measured per projection (bf16,
+// G64): QKV 3584x2560 and gate+up
 // 19456x2560 take 6.9-7.1 and 14.2-14.8 us from 5 to 16 rows, against 6.1
 // and 13.0 us at 5 rows, 6.2 and 14.4 at 8, 7.6 and 18.2 at 12 and 8.8 and
 // 21.8 at 16 on the 4x4x4 multi-row kernel; down 2560x9728 at 5 rows 12.2
 // against 9.2 us.
 struct MrPlan {
   bool ok;
-  int P, TW, IW, NI;
-  size_t lds;
+  int P, TW, IW, NI, KS;
+  size_t lds, ws;
 };
 
 static MrPlan plan_mr(int64_t M, int64_t N, int64_t K, int G) {
@@ -282,19 +346,29 @@ static MrPlan plan_mr(int64_t M, int64_t N, int64_t K, int G) {
   if (N * (K / 2) >= (int64_t)kOob || M * K * 2 >= (int64_t)kOob) return p;
   const int64_t ng = K / G;
   if ((N * ng * 2) % 16 != 0) return p;
-  const int64_t nt = cdiv(N, 16), SEG = K / 128;
-  p.P = (int)std::min<int64_t>(nt, device_cus());
-  p.TW = (int)cdiv(nt, p.P);
-  const int64_t iw = cdiv(p.TW * SEG, kMrNW);
-  if (iw > 8 || iw > SEG) return p;
-  p.IW = (int)iw;
-  p.NI = iw <= 2 ? 2 : (iw <= 4 ? 4 : 8);
-  if (M * K / 8 > (int64_t)kMrXC * 64 * kMrNW) return p;
-  if (p.TW * 16 * ng / 8 > (int64_t)kMrSP * 64 * kMrNW) return p;
-  const MrLds l = mr_lds((int)M, (int)K, p.TW, G);
-  if (l.bytes > kMrMaxLds) return p;
-  p.lds = (size_t)l.bytes;
-  p.ok = true;
+  const int64_t nt = cdiv(N, 16), cus = device_cus();
+  for (int KS = 1; KS <= 8; KS *= 2) {
+    const int64_t Kl = K / KS, ngl = Kl / G, SEG = Kl / 128;
+    if (K % KS != 0 || Kl % 128 != 0 || Kl % G != 0) continue;
+    if (KS > 1 && (ngl % 2 != 0 || ng % 2 != 0 || env_int("SPARKQ_W4_MR_NO_SPLIT", 0))) continue;
+    if (M * Kl / 8 > (int64_t)kMrXC * 64 * kMrNW) continue;
+    p.P = (int)std::min<int64_t>(nt, KS == 1 ? cus : std::max<int64_t>(1, cus / KS));
+    if (KS > 1 && p.P > kMaxCounterTiles) continue;
+    p.TW = (int)cdiv(nt, p.P);
+    const int64_t iw = cdiv(p.TW * SEG, kMrNW);
+    if (iw > 8 || iw > SEG) continue;
+    const int64_t pieces = KS == 1 ? p.TW * 16 * ng / 8 : p.TW * 16 * ngl / 2;
+    if (pieces > (int64_t)kMrSP * 64 * kMrNW * (KS == 1 ? 1 : 4)) continue;
+    const MrLds l = mr_lds((int)M, (int)Kl, p.TW, G);
+    if (l.bytes > kMrMaxLds) continue;
+    p.IW = (int)iw;
+    p.NI = iw <= 2 ? 2 : (iw <= 4 ? 4 : 8);
+    p.KS = KS;
+    p.lds = (size_t)l.bytes;
+    p.ws = KS > 1 ? kCounterBytes + round_up((size_t)KS * M * N * 4, 256) : 0;
+    p.ok = true;
+    return p;
+  }
   return p;
 }
 
@@ -305,7 +379,7 @@ static void launch_mr_n(const MrPlan& p, const MrArgs& a, hipStream_t st) {
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, kMrMaxLds);
   (void)attr;
-  hipLaunchKernelGGL(k, dim3((unsigned)p.P), dim3(64 * kMrNW), p.lds, st, a);
+  hipLaunchKernelGGL(k, dim3((unsigned)p.P, (unsigned)p.KS), dim3(64 * kMrNW), p.lds, st, a);
 }
 template <typename T, int G>
 static void launch_mr_g(const MrPlan& p, const MrArgs& a, hipStream_t st) {
@@ -326,14 +400,22 @@ static void launch_mr(const MrPlan& p, int G, const MrArgs& a, hipStream_t st) {
     launch_mr_g<T, 128>(p, a, st);
 }
 
-bool w4_mr_supported(int64_t M, int64_t N, int64_t K, int G) { return plan_mr(M, N, K, G).ok; }
+// Workspace of the plan (split counters and partials), or -1 when the shape
+// is not served.
+int64_t w4_mr_workspace(int64_t M, int64_t N, int64_t K, int G) {
+  const MrPlan p = plan_mr(M, N, K, G);
+  return p.ok ? (int64_t)p.ws : -1;
+}
 
 // Returns 1 when the shape is not served (the caller picks another kernel).
 int w4_mr_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
                  int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, hipStream_t st,
-                 const void* res) {
+                 const void* res, void* ws, size_t wsb) {
   const MrPlan p = plan_mr(M, N, K, G);
   if (!p.ok) return 1;
+  if (p.ws > 0 && (ws == nullptr || wsb < p.ws))
+    return set_error(SPARKQ_ERR_WORKSPACE, "w4a16_linear needs a workspace of %zu bytes (got %zu)",
+                     p.ws, wsb);
   MrArgs a{};
   a.x = (const uint16_t*)x;
   a.w = w;
@@ -349,6 +431,11 @@ int w4_mr_linear(const void* x, const uint32_t* w, const void* s, const void* b,
   a.P = p.P;
   a.TW = p.TW;
   a.IW = p.IW;
+  a.KS = p.KS;
+  if (p.KS > 1) {
+    a.counters = reinterpret_cast<unsigned*>(ws);
+    a.part = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
+  }
   if (xdt == SPARKQ_BF16)
     launch_mr<BF16>(p, G, a, st);
   else

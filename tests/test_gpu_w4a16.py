@@ -202,6 +202,24 @@ def test_decode_mfma_rows(gpu, m, n, k, g, monkeypatch):
         check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
 
 
+@pytest.mark.parametrize("m,n,k,g", [(16, 2560, 9728, 64), (9, 100, 9728, 32), (8, 2560, 9728, 64),
+                                     (6, 300, 8192, 128), (12, 1000, 16384, 64), (5, 48, 9728, 64)])
+def test_decode_mfma_rows_split_k(gpu, m, n, k, g, monkeypatch):
+    """Rows whose activations exceed the 16x16x32 kernel's staging split K
+    into ranges (the down projection at 9..16 rows; 5..8 rows when the
+    kernel is asked to take them); the last workgroup of a tile range adds
+    the ranges' partials. Ragged N, G32..128, both dtypes, repeated calls
+    bit-identical (the counters are left zero)."""
+    monkeypatch.setenv("SPARKQ_W4_MR_MIN", "5")
+    for dtype in (o.BF16, o.F16):
+        x, wq, s, b = w4_problem(m, n, k, g, dtype=dtype, seed=m + n + k)
+        ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
+        y32 = _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32)
+        check_fp32(y32.cpu().numpy(), ref)
+        check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
+        assert torch.equal(y32, _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32))
+
+
 @pytest.mark.parametrize("m", [2, 3, 4])
 def test_decode_mfma_rows_few(gpu, m, monkeypatch):
     """The 16x16x32 kernel below 5 rows stays correct."""
