@@ -135,6 +135,30 @@ def bench_w4_projection(torch, sparkq, dev, layers, name, m, iters):
     return ms / len(layers)  # per projection
 
 
+def bench_square_cold(torch, sparkq, dev, iters, copies=128):
+    """The single-linear workload: W4A16 G64 at M=1, K=N=2560, over `copies`
+    distinct weight sets (472 MB, cold in the 256 MB MALL) in one graph
+    replay; returns ms per launch."""
+    n = k = 2560
+    gen = torch.Generator(device=dev).manual_seed(3)
+    ws = []
+    for _ in range(copies):
+        w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        ws.append(sparkq.affine_quantize(w, group_size=G))
+        del w
+    x = torch.randn((1, k), device=dev).to(torch.bfloat16)
+    y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+
+    def fn():
+        for wq, s, b in ws:
+            sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y)
+
+    graph = capture(torch, fn)
+    ms = Timer(torch).time(graph.replay, iters, 2) / copies
+    del graph, ws
+    return ms
+
+
 def bench_gemm(torch, sparkq, dev, layers, name, m, iters):
     """One W4A16 projection at M rows over every layer's distinct weights in
     one graph replay (36 launches, weights cold in the MALL); returns ms per
@@ -525,7 +549,8 @@ def cpu_baseline(layers_host, threads, cpu, budget_s=10.0):
 
 def cpu_legs(layers_host, threads, budget_s=2.0):
     """The CPU legs of the other workloads, each run for about budget_s:
-    W4A16 GEMM (gate+up at M=16/512/2048), W8A8 (gate+up at M=1/8/16 over 4
+    the single W4A16 2560x2560 linear at M=1, W4A16 GEMM (gate+up at
+    M=16/512/2048), W8A8 (gate+up at M=1/8/16 over 4
     distinct int8 weight sets) and INT8-KV decode attention (32/8 heads,
     D=128; B=8 N=32768 is left out: 545 MB of cache per call)."""
     import numpy as np
@@ -533,6 +558,20 @@ def cpu_legs(layers_host, threads, budget_s=2.0):
     import oracle as o
 
     res = {}
+    # the single 2560 x 2560 linear at M=1: the first 2560 rows of each
+    # layer's QKV weights (36 distinct sets)
+    xq = o.randn16(0, 2560, 2560).reshape(1, 2560)
+    iq = [0]
+
+    def square():
+        wq, s, b = layers_host[iq[0] % len(layers_host)]["qkv"]
+        o.cpu_w4a16_gemv(xq, wq[:2560], s[:2560], b[:2560], G, threads)
+        iq[0] += 1
+
+    runs, el = _run_for(square, budget_s)
+    ms = el / runs * 1e3
+    res["w4a16 2560x2560 M=1"] = {"ms": round(ms, 4), "GB/s": round(w4_bytes(2560, 2560) / ms / 1e6, 2),
+                                  "runs": runs}
     n, k = PROJ["gate_up"]
     for m in (16, 512, 2048):
         x = o.randn16(0, 100 + m, m * k).reshape(m, k)
@@ -644,6 +683,11 @@ def main():
             pm = bench_w4_projection(torch, sparkq, dev, layers, name, 1, 10)
             per[name] = {"ms": round(pm, 5), "GB/s": round(w4_bytes(*PROJ[name]) / pm / 1e6, 1)}
         extras["w4a16_decode_m1_per_projection"] = per
+        sq = bench_square_cold(torch, sparkq, dev, 10)
+        sq_gbs = w4_bytes(2560, 2560) / sq / 1e6
+        extras["w4a16_m1_2560x2560_cold"] = {"ms": round(sq, 5), "GB/s": round(sq_gbs, 1),
+                                              "frac_hbm": round(sq_gbs / HBM_PEAK_GBS, 4),
+                                              "weight_bytes": w4_bytes(2560, 2560), "copies": 128}
         sweeps = {}
         for m in (4, 8, 16):
             sm, _ = bench_w4_decode(torch, sparkq, dev, layers, 10, 2, m)
