@@ -10,6 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from typing import Optional
 
 import torch
 
@@ -110,10 +111,17 @@ def stream_handle(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def call(name: str, *args) -> None:
+def call(name: str, *args, device: Optional[torch.device] = None) -> None:
     """Call an entry point and map its status to the reference's exception types
-    (validation -> ValueError, runtime -> SparkqError)."""
-    rc = getattr(lib(), name)(*args)
+    (validation -> ValueError, runtime -> SparkqError). With `device` (the
+    tensors' GPU) the call runs with that device current: the library
+    launches on the current device."""
+    if device is not None and device.type == "cuda" and device.index is not None \
+            and device.index != torch.cuda.current_device():
+        with torch.cuda.device(device):
+            rc = getattr(lib(), name)(*args)
+    else:
+        rc = getattr(lib(), name)(*args)
     if rc == OK:
         return
     msg = (lib().sparkq_last_error() or b"").decode(errors="replace")

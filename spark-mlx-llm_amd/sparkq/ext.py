@@ -144,7 +144,7 @@ def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
                              "w4a16")
     _lib.call("sparkq_w4a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
               _ptr(y), m, n, k, group_size, bits, _lib.dtype_code(x.dtype),
-              _lib.dtype_code(out_dtype), ws, wsb, _lib.stream_handle(x.device))
+              _lib.dtype_code(out_dtype), ws, wsb, _lib.stream_handle(x.device), device=x.device)
     return y.reshape(*lead, n)
 
 
@@ -185,7 +185,7 @@ def _w8_affine_matmul(op, x, weight, scales, biases, group_size, out_dtype, out)
     _lib.call("sparkq_w8_affine_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
               _ptr(y), m, n, k, group_size, _lib.dtype_code(x.dtype),
               _lib.dtype_code(scales.dtype), _lib.dtype_code(out_dtype),
-              _lib.stream_handle(x.device))
+              _lib.stream_handle(x.device), device=x.device)
     return y.reshape(*lead, n)
 
 
@@ -258,7 +258,7 @@ def affine_quantize(w, *, group_size: int = 64, bits: int = 4):
     s = torch.empty((n, k // group_size), dtype=w.dtype, device=w.device)
     b = torch.empty_like(s)
     _lib.call("sparkq_w4_quantize", _ptr(w), _ptr(wq), _ptr(s), _ptr(b), n, k, group_size,
-              _lib.dtype_code(w.dtype), _lib.stream_handle(w.device))
+              _lib.dtype_code(w.dtype), _lib.stream_handle(w.device), device=w.device)
     return wq, s, b
 
 
@@ -276,7 +276,7 @@ def affine_dequantize(weight, scales, biases, *, group_size: int = 64, bits: int
     weight, scales, biases = weight.contiguous(), scales.contiguous(), biases.contiguous()
     _lib.call("sparkq_w4a16_dequantize", _ptr(weight), _ptr(scales),
               _ptr(biases), _ptr(out), n, k, group_size,
-              _lib.dtype_code(scales.dtype), _lib.stream_handle(weight.device))
+              _lib.dtype_code(scales.dtype), _lib.stream_handle(weight.device), device=weight.device)
     return out
 
 
@@ -307,7 +307,7 @@ def quantize_per_token(x):
     q = torch.empty((m, k), dtype=torch.int8, device=x.device)
     sc = torch.empty((m,), dtype=torch.float32, device=x.device)
     _lib.call("sparkq_a8_quantize_per_token", _ptr(x2), _ptr(q), _ptr(sc), m, k,
-              _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+              _lib.dtype_code(x.dtype), _lib.stream_handle(x.device), device=x.device)
     return q, sc
 
 
@@ -324,7 +324,7 @@ def int8_matmul_int32(x, weight, *, stream=None):
                              "i8mm")
     x, weight = x.contiguous(), weight.contiguous()
     _lib.call("sparkq_int8_matmul_i32", _ptr(x), _ptr(weight),
-              _ptr(c), m, n, k, ws, wsb, _lib.stream_handle(x.device))
+              _ptr(c), m, n, k, ws, wsb, _lib.stream_handle(x.device), device=x.device)
     return c
 
 
@@ -352,7 +352,7 @@ def w8a8_linear(x, weight, scales, bias=None, *, stream=None, out_dtype=None, ou
               _ptr(scales), _ptr(bias_c),
               _lib.dtype_code(bias.dtype) if bias is not None else F32, _ptr(y), m, n, k,
               _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), ws, wsb,
-              _lib.stream_handle(x.device))
+              _lib.stream_handle(x.device), device=x.device)
     return y.reshape(*lead, n)
 
 
@@ -425,7 +425,7 @@ def w8a16_per_channel(x, weight, scales, *, stream=None, out_dtype=None, out=Non
     y = _out_buffer(out, (m, n), out_dtype, x.device)
     weight, scales = weight.contiguous(), scales.reshape(n).contiguous()
     _lib.call("sparkq_w8a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(y), m, n, k,
-              _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), _lib.stream_handle(x.device))
+              _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), _lib.stream_handle(x.device), device=x.device)
     return y.reshape(*lead, n)
 
 
@@ -445,7 +445,7 @@ def kv_quantize_s8(x):
     codes = torch.empty(x.shape, dtype=torch.int8, device=x.device)
     sc = torch.empty(x.shape[:-1], dtype=torch.float16, device=x.device)
     _lib.call("sparkq_kv_quantize_s8", _ptr(x2), _ptr(codes), _ptr(sc), r, d,
-              _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+              _lib.dtype_code(x.dtype), _lib.stream_handle(x.device), device=x.device)
     return codes, sc
 
 
@@ -489,7 +489,7 @@ def _int8_prefill_affine(queries, keys, values, *, scale, causal, group_size, bi
     _lib.call("sparkq_int8kv_sdpa_prefill_affine", _ptr(q), _ptr(kc), _ptr(ks), _ptr(kb),
               _ptr(vc), _ptr(vs), _ptr(vb), _ptr(y), batch, heads, kv_heads, length, n, dim,
               group_size, c, _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype),
-              float(scale), st, ws, wsb, _lib.stream_handle(queries.device))
+              float(scale), st, ws, wsb, _lib.stream_handle(queries.device), device=queries.device)
     return y
 
 
@@ -525,7 +525,7 @@ def _int8_prefill(queries, keys, values, *, scale, causal, fmt, out_dtype, out,
     _lib.call("sparkq_int8kv_sdpa_prefill", _ptr(q), _ptr(kc), _ptr(ks), _ptr(vc), _ptr(vs),
               _ptr(y), batch, heads, kv_heads, length, n, dim, 1 if causal else 0,
               _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), float(scale), st,
-              _lib.stream_handle(queries.device))
+              _lib.stream_handle(queries.device), device=queries.device)
     return y
 
 
@@ -570,7 +570,7 @@ def kv_append(x, cache, offset: int, *, group_size: int = 32, bits: int = 8):
     st = (ctypes.c_int64 * 6)(*strides)
     _lib.call("sparkq_kv_append", _ptr(x.contiguous()), _ptr(codes), _ptr(scales), _ptr(biases),
               b, h, length, d, offset, group_size, fmt, _lib.dtype_code(x.dtype), st,
-              _lib.stream_handle(x.device))
+              _lib.stream_handle(x.device), device=x.device)
 
 
 class QuantizedKVCache:
@@ -736,7 +736,7 @@ def _decode(queries, kc, ks, kb, vc, vs, vb, strides, group_size, fmt, scale, ou
     _lib.call("sparkq_int8kv_sdpa_decode", _ptr(q), _ptr(kc), _ptr(ks), _ptr(kb), _ptr(vc),
               _ptr(vs), _ptr(vb), _ptr(out), batch, heads, kv_heads, n, dim, group_size, fmt,
               _lib.dtype_code(queries.dtype), _lib.dtype_code(out_dtype), float(scale), st,
-              ws, wsb, _lib.stream_handle(queries.device))
+              ws, wsb, _lib.stream_handle(queries.device), device=queries.device)
     return out
 
 
@@ -808,7 +808,7 @@ def _staged_attention(queries, keys, values, *, scale, group_size, bits, mask, o
               _ptr(vs), _ptr(vb), _ptr(mask_t), kind, mdt, mstrides, _ptr(y), batch, heads,
               kv_heads, length, n, dim, dv, group_size, bits, _lib.dtype_code(queries.dtype),
               _lib.dtype_code(out_dtype), float(scale), st, ws, wsb,
-              _lib.stream_handle(queries.device))
+              _lib.stream_handle(queries.device), device=queries.device)
     return y
 
 
@@ -841,7 +841,7 @@ def rms_norm(x, weight, eps: float, *, residual=None, return_hidden: bool = Fals
     out = torch.empty_like(x2)
     hid = torch.empty_like(x2) if return_hidden else None
     _lib.call("sparkq_rms_norm", _ptr(x2), _ptr(r2), _ptr(weight.contiguous()), float(eps),
-              _ptr(hid), _ptr(out), m, k, _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+              _ptr(hid), _ptr(out), m, k, _lib.dtype_code(x.dtype), _lib.stream_handle(x.device), device=x.device)
     if return_hidden:
         return out.view(x.shape), (hid.view(x.shape) if residual is not None else x)
     return out.view(x.shape)
@@ -871,7 +871,7 @@ def rope(x, dims: int, *, traditional: bool = False, base: float = 10000.0,
         return out
     _lib.call("sparkq_rope", _ptr(xc), _ptr(out), rows, length, d, int(dims), int(bool(traditional)),
               float(base), float(scale), int(offset), _lib.dtype_code(x.dtype),
-              _lib.stream_handle(x.device))
+              _lib.stream_handle(x.device), device=x.device)
     return out
 
 
@@ -929,7 +929,7 @@ def spark_qkv_rope(x, weight, scales, biases, q_size: int, kv_size: int, num_hea
               _ptr(scales.contiguous()), _ptr(biases.contiguous()), _ptr(q), _ptr(k), _ptr(v),
               hidden, q_size, kv_size, num_heads, num_key_value_heads, head_dim, rope_dims,
               float(rope_base), int(offset), group_size, bits, _lib.dtype_code(x.dtype), ws, wsb,
-              _lib.stream_handle(dev))
+              _lib.stream_handle(dev), device=dev)
     return q, k, v
 
 
@@ -977,7 +977,7 @@ def fused_ffn(x, attention_output, norm_weight, eps: float, gate, up, down, *,
     _lib.call("sparkq_ffn", _ptr(x2), _ptr(a2), _ptr(norm_weight.contiguous()), float(eps),
               *[_ptr(t) for t in c], _ptr(out), m, k, inter, group_size,
               _lib.dtype_code(x.dtype), ctypes.c_void_p(buf.data_ptr()), buf.numel(),
-              _lib.stream_handle(dev))
+              _lib.stream_handle(dev), device=dev)
     if not return_intermediates:
         return out.view(x.shape)
     lin = _round_up(max(_lib.lib().sparkq_w4a16_workspace_bytes(m, inter, k, group_size),
@@ -1017,5 +1017,5 @@ def attention_gate(x, output, gate_weight, *, return_gate: bool = False):
     gate = torch.empty((b, length, h), dtype=x.dtype, device=x.device) if return_gate else None
     _lib.call("sparkq_attention_gate", _ptr(x), _ptr(output), _ptr(gate_weight), _ptr(out),
               _ptr(gate), b, length, h, d, hidden, _lib.dtype_code(x.dtype),
-              _lib.stream_handle(x.device))
+              _lib.stream_handle(x.device), device=x.device)
     return (out, gate) if return_gate else out
