@@ -1,4 +1,5 @@
-// w4q.hip -- W4A16 decode GEMV for one activation row, one row quad per wave.
+// w4q.hip -- W4A16 decode GEMV for up to four activation rows, one row quad
+// per wave.
 //
 // The M = 1 projection is HBM-bound, and its time is set by how the weight
 // stream is spread over the CUs: measured on the gate+up weights (19456 x
@@ -23,7 +24,8 @@
 //  * the sixteen 4-lane blocks are added by DPP and permlane swaps and
 //    lanes 0..3 write the quad's four outputs (plus an optional 16-bit
 //    residual, rounded as the reference's hidden + mlp_output).
-// K % 512 == 0 (whole spans), N % 4 == 0, rows of at most 8 spans.
+// K % 512 == 0 (whole spans), N % 4 == 0, rows of at most 8 spans, at most
+// four activation rows.
 #include <algorithm>
 
 #include "common.h"
@@ -38,7 +40,7 @@ struct GemvQArgs {
   void* y;
   const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
   int y_dtype;
-  int N, K;
+  int M, N, K;
   int nq;  // row quads
   int P;   // workgroups
 };
@@ -51,21 +53,21 @@ __device__ __forceinline__ int q_xslot(int pi, int w) {
 }
 
 struct GemvQLds {
-  int xp;  // activations [K] in pair order (2 B each)
-  int xs;  // piece sums [K/32] fp32
+  int xp;  // activations [M][K] in pair order (2 B each)
+  int xs;  // piece sums [K/32] fp32, or [K/32][4] for several rows
   int sb;  // (scale, bias) of the workgroup's rows [4*NWQ][K/G] dwords
   int bytes;
 };
-__host__ __device__ __forceinline__ GemvQLds gemvq_lds(int K, int NWQ, int G) {
+__host__ __device__ __forceinline__ GemvQLds gemvq_lds(int M, int K, int NWQ, int G) {
   GemvQLds l;
   l.xp = 0;
-  l.xs = (K * 2 + 1023) & ~1023;
-  l.sb = l.xs + (((K / 32) * 4 + 15) & ~15);
+  l.xs = (M * K * 2 + 1023) & ~1023;
+  l.sb = l.xs + (((K / 32) * 4 * (M > 1 ? 4 : 1) + 15) & ~15);
   l.bytes = l.sb + 4 * NWQ * (K / G) * 4;
   return l;
 }
 
-template <typename T, int G, int U>
+template <typename T, int G, int U, int MQ>  // MQ: 1, or 4 for 2..4 activation rows
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5)))
 void w4_gemv_q_kernel(GemvQArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -73,25 +75,25 @@ void w4_gemv_q_kernel(GemvQArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int b = lane >> 2, j = lane & 3;
-  const int N = a.N, K = a.K;
+  const int M = MQ == 1 ? 1 : a.M, N = a.N, K = a.K;
   const int RB = K >> 1;     // bytes per weight row
   const int ns = RB >> 8;    // spans per row (<= U)
   const int ng = K / G;      // groups per row
   const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
   const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
-  const GemvQLds L = gemvq_lds(K, nt >> 6, G);
+  const GemvQLds L = gemvq_lds(M, K, nt >> 6, G);
 
-  const rsrc_t rx = make_rsrc(a.x, (uint32_t)K * 2);
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)(M * K) * 2);
   const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
   const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
   const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
 
-  // 1. staging loads: activation pieces (64 B: 32 k) and 16-byte (scale,
-  // bias) pieces of the workgroup's 4*nql rows. A thread takes at most one
-  // activation piece (K <= 4096 gives at most 128; a workgroup has at least
-  // 4 waves) and at most two scale pieces (the plan checks the count); a
-  // wave with nothing to fetch skips the instruction.
-  const int nxp = K >> 5;
+  // 1. staging loads: activation pieces (64 B: 32 k; piece i of the M rows
+  // in order) and 16-byte (scale, bias) pieces of the workgroup's 4*nql
+  // rows. A thread takes at most one activation piece and at most two scale
+  // pieces (the plan gives the workgroup the waves for both); a wave with
+  // nothing to fetch skips the instruction.
+  const int nxp = M * (K >> 5);
   const int nsp = (4 * nql * ng) >> 3;
   u32x4_t xr[4], sr[2] = {}, br[2] = {};
   if (64 * wave < nxp) {
@@ -125,6 +127,8 @@ void w4_gemv_q_kernel(GemvQArgs a) {
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
     float* xs = reinterpret_cast<float*>(smem + L.xs);
     if (tid < nxp) {
+      // piece tid is piece `pc` of activation row m (rows of K/2 dwords)
+      const int m = MQ == 1 ? 0 : tid / (K >> 5), pc = tid - m * (K >> 5);
       float sum = 0.0f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -133,11 +137,11 @@ void w4_gemv_q_kernel(GemvQArgs a) {
                            __builtin_amdgcn_perm(r.z, r.x, 0x07060302u),   // (x1, x5)
                            __builtin_amdgcn_perm(r.w, r.y, 0x05040100u),   // (x2, x6)
                            __builtin_amdgcn_perm(r.w, r.y, 0x07060302u)};  // (x3, x7)
-        *reinterpret_cast<u32x4_t*>(xp + q_xslot(tid, w)) = o;
+        *reinterpret_cast<u32x4_t*>(xp + m * (K >> 1) + q_xslot(pc, w)) = o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[e], sum);
       }
-      xs[tid] = sum;
+      xs[MQ == 1 ? pc : 4 * pc + m] = sum;
     }
     uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
 #pragma unroll
@@ -164,14 +168,20 @@ void w4_gemv_q_kernel(GemvQArgs a) {
   const float* xs = reinterpret_cast<const float*>(smem + L.xs);
   const uint32_t* sb = reinterpret_cast<const uint32_t*>(smem + L.sb);
   const DecodeConsts dc = decode_consts<T>();
-  float acc = 0.0f;
+  // with several rows, lane 4b+j feeds activation row min(j, M-1) as the A
+  // operand's row j, and its result D[i] is row i's (the row quad's row j)
+  const int xrow = MQ == 1 ? 0 : min(j, M - 1);
+  float acc[MQ];
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) acc[m] = 0.0f;
 #pragma unroll
   for (int s = 0; s < U; ++s) {
     if (s < ns) {
       const int piece = 16 * s + b;
       u32x4_t xa[4];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) xa[w] = *reinterpret_cast<const u32x4_t*>(xp + 4 * q_xslot(piece, w));
+      for (int w = 0; w < 4; ++w)
+        xa[w] = *reinterpret_cast<const u32x4_t*>(xp + 4 * (xrow * (K >> 1) + q_xslot(piece, w)));
       const uint32_t pair = sb[(4 * wave + j) * ng + (512 * s + 32 * b) / G];
       // one chain of eight MFMAs per span for rows of three or more spans,
       // two chains of four below: the summation order of w4_gemv_kernel, so
@@ -194,38 +204,56 @@ void w4_gemv_q_kernel(GemvQArgs a) {
           d0 = mfma4x4<T>(xa[w][0], xa[w][1], pr[0], pr[1], d0);
           d1 = mfma4x4<T>(xa[w][2], xa[w][3], pr[2], pr[3], d1);
         }
-        d0[0] += d1[0];
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) d0[m] += d1[m];
       }
       const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
       const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
-      acc = fmaf(sf, d0[0], fmaf(bf, xs[piece], acc));
+      if constexpr (MQ == 1) {
+        acc[0] = fmaf(sf, d0[0], fmaf(bf, xs[piece], acc[0]));
+      } else {
+        const f32x4_t xm = *reinterpret_cast<const f32x4_t*>(xs + 4 * piece);
+#pragma unroll
+        for (int m = 0; m < MQ; ++m) acc[m] = fmaf(sf, d0[m], fmaf(bf, xm[m], acc[m]));
+      }
     }
   }
   // 5. sum the sixteen blocks (lanes j, j+4, ..., j+60); lanes 0..3 store
-  const float v = sum_blocks(acc);
-  if (lane < 4 && row < N) store_out(a.y, row, a.res ? add_rounded<T>(v, a.res[row]) : v, a.y_dtype);
+  // row 4q+j of each activation row
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) {
+    const float v = sum_blocks(acc[m]);
+    if (lane < 4 && row < N && m < M) {
+      const int64_t idx = (int64_t)m * N + row;
+      store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
+    }
+  }
 }
 
-// Plan: M = 1, K % 512 == 0 with at most 8 spans per row, N % 4 == 0, the
-// scale tensors ending on a 16-byte boundary. Workgroups: twice the CUs when
+// Plan: M <= 4, K % 512 == 0 with at most 8 spans per row, N % 4 == 0, the
+// scale tensors ending on a 16-byte boundary (2..4 rows: the 4x4x4 blocks'
+// four A rows carry the activation rows, and every workgroup stages all of
+// them, one 32-k piece per thread). Workgroups: twice the CUs when
 // that gives at least 8 quads per CU (two workgroups of ~nq/(2*CUs) waves
 // each), else one per CU, else one quad each; at most 16 waves. Measured
 // alternatives that ran slower on the gate+up weights: two or four quads per
-// wave (9.1-10 us against 7.8-8.1), one workgroup per CU (10.2 us). Rows of
+// wave (9.1-10 us against 7.8-8.1), one workgroup per CU (10.2 us). At 2, 3
+// and 4 rows gate+up takes 8.5 / 8.8 / 9.6 us here against 9.4 / 10.1 / 10.9
+// on the whole-row kernel (w4_gemv_kernel), QKV the same within 0.2 us. Rows of
 // up to 20 spans (the down projection, 2560 x 9728: 19 spans, five waves per
 // workgroup to stage its activations) ran 7.3 us here against 6.1 us in the
 // streaming kernel, so longer rows stay there.
 struct GemvQPlan {
   bool ok;
-  int P, NWQ, U;
+  int P, NWQ, U, MQ;
   size_t lds;
 };
 
 static GemvQPlan plan_gemvq(int64_t M, int64_t N, int64_t K, int G) {
   GemvQPlan p{};
-  if (M != 1 || env_int("SPARKQ_W4_NO_GEMVQ", 0)) return p;
+  if (M < 1 || M > env_int("SPARKQ_W4_GEMVQ_MAXM", 4) || M > 4 || env_int("SPARKQ_W4_NO_GEMVQ", 0)) return p;
   if (K % 512 != 0 || N % 4 != 0 || K / 512 > 8) return p;
-  if (N * (K / 2) >= (int64_t)kOob) return p;
+  if (N * (K / 2) >= (int64_t)kOob || M * K * 2 >= (int64_t)kOob) return p;
   const int64_t ng = K / G;
   if ((N * ng * 2) % 16 != 0 || ng % 2 != 0) return p;
   const int64_t nq = N / 4, cus = device_cus();
@@ -234,24 +262,34 @@ static GemvQPlan plan_gemvq(int64_t M, int64_t N, int64_t K, int G) {
   if (cdiv(nq, P) > 16) P = cdiv(nq, 16);
   p.P = (int)P;
   p.NWQ = (int)cdiv(nq, P);
-  if (p.NWQ < 4) p.NWQ = 4;  // threads enough to stage the activations
+  // threads enough to stage the activations, one 32-k piece each
+  p.NWQ = (int)std::max<int64_t>(std::max<int64_t>(p.NWQ, 4), cdiv(M * K / 32, 64));
+  if (p.NWQ > 16) return p;
   if (4 * p.NWQ * ng / 8 > 2 * 64 * p.NWQ) return p;  // two scale pieces per thread
   p.U = K / 512 <= 5 ? 5 : 8;
-  const GemvQLds l = gemvq_lds((int)K, p.NWQ, G);
+  p.MQ = M == 1 ? 1 : 4;
+  const GemvQLds l = gemvq_lds((int)M, (int)K, p.NWQ, G);
   if (l.bytes > 65536) return p;
   p.lds = (size_t)l.bytes;
   p.ok = true;
   return p;
 }
 
-template <typename T, int G>
-static void launch_gemvq_g(const GemvQPlan& p, const GemvQArgs& a, hipStream_t st) {
+template <typename T, int G, int MQ>
+static void launch_gemvq_m(const GemvQPlan& p, const GemvQArgs& a, hipStream_t st) {
   if (p.U == 5)
-    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, 5>), dim3((unsigned)p.P), dim3(64 * p.NWQ), p.lds,
+    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, 5, MQ>), dim3((unsigned)p.P), dim3(64 * p.NWQ), p.lds,
                        st, a);
   else
-    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, 8>), dim3((unsigned)p.P), dim3(64 * p.NWQ), p.lds,
+    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, 8, MQ>), dim3((unsigned)p.P), dim3(64 * p.NWQ), p.lds,
                        st, a);
+}
+template <typename T, int G>
+static void launch_gemvq_g(const GemvQPlan& p, const GemvQArgs& a, hipStream_t st) {
+  if (p.MQ == 1)
+    launch_gemvq_m<T, G, 1>(p, a, st);
+  else
+    launch_gemvq_m<T, G, 4>(p, a, st);
 }
 
 // Returns 1 when the shape is not this kernel's (the caller picks another).
@@ -268,6 +306,7 @@ int w4_gemvq_linear(const void* x, const uint32_t* w, const void* s, const void*
   a.y = y;
   a.res = (const uint16_t*)res;
   a.y_dtype = ydt;
+  a.M = (int)M;
   a.N = (int)N;
   a.K = (int)K;
   a.nq = (int)(N / 4);
