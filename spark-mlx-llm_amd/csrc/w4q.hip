@@ -242,7 +242,10 @@ void w4_gemv_q_kernel(GemvQArgs a) {
 // on the whole-row kernel (w4_gemv_kernel), QKV the same within 0.2 us. Rows of
 // up to 20 spans (the down projection, 2560 x 9728: 19 spans, five waves per
 // workgroup to stage its activations) ran 7.3 us here against 6.1 us in the
-// streaming kernel, so longer rows stay there.
+// streaming kernel, so longer rows stay there. Five to eight rows as two row
+// quartets per 4x4x4 block (two MFMA chains on each decoded piece) ran
+// gate+up at 5 / 6 / 8 rows in 12.8 / 13.6 / 16.9 us against 12.6 / 13.0 /
+// 14.1 on the multi-row streaming kernel, so they stay there.
 struct GemvQPlan {
   bool ok;
   int P, NWQ, U, MQ;

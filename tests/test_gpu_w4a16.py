@@ -178,6 +178,7 @@ def test_decode_multirow_stream(gpu, m, n, k, g, monkeypatch):
     count below the wave count, M not a multiple of 4 (the last row quartet
     repeats row M-1) and long rows."""
     monkeypatch.setenv("SPARKQ_W4_NO_MR", "1")
+    monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
     x, wq, s, b = w4_problem(m, n, k, g, seed=m * n)
     ref = o.w4a16_matmul(x, wq, s, b, g)
     y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
@@ -194,6 +195,7 @@ def test_decode_mfma_rows(gpu, m, n, k, g, monkeypatch):
     one-segment rows (K = 128), long rows with one tile per workgroup, both
     dtypes."""
     monkeypatch.setenv("SPARKQ_W4_MR_MIN", "5")
+    monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
     for dtype in (o.BF16, o.F16):
         x, wq, s, b = w4_problem(m, n, k, g, dtype=dtype, seed=m + n + k)
         ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
@@ -220,10 +222,32 @@ def test_decode_mfma_rows_split_k(gpu, m, n, k, g, monkeypatch):
         assert torch.equal(y32, _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32))
 
 
+@pytest.mark.parametrize("m,n,k,g", [(2, 3584, 2560, 64), (3, 100, 1024, 32), (4, 19456, 2560, 64),
+                                     (4, 1024, 4096, 128), (2, 44, 2048, 128), (3, 1028, 2560, 32),
+                                     (4, 8, 512, 64)])
+def test_decode_one_round_rows(gpu, m, n, k, g):
+    """2 <= M <= 4 on the one-round kernel (rows of whole 512-k spans, whole
+    row quads): each output row matches the oracle and equals, bit for bit,
+    the M = 1 result for that activation row alone (the summation order of a
+    row does not depend on how many rows share the launch), both dtypes;
+    rows of one and two spans (two MFMA chains), rows of eight spans, more
+    row quads than waves per workgroup, fewer row quads than CUs."""
+    for dtype in (o.BF16, o.F16):
+        x, wq, s, b = w4_problem(m, n, k, g, dtype=dtype, seed=m * n + k)
+        ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
+        y32 = _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32)
+        check_fp32(y32.cpu().numpy(), ref)
+        check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
+        for r in sorted({0, m // 2, m - 1}):
+            y1 = _run(gpu, x[r:r + 1], wq, s, b, g, dtype, out_dtype=torch.float32)
+            assert torch.equal(y32[r:r + 1], y1), r
+
+
 @pytest.mark.parametrize("m", [2, 3, 4])
 def test_decode_mfma_rows_few(gpu, m, monkeypatch):
     """The 16x16x32 kernel below 5 rows stays correct."""
     monkeypatch.setenv("SPARKQ_W4_MR_MIN", "2")
+    monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
     n, k, g = 700, 2560, 64
     x, wq, s, b = w4_problem(m, n, k, g, seed=m)
     ref = o.w4a16_matmul(x, wq, s, b, g)
