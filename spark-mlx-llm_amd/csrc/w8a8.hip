@@ -449,12 +449,12 @@ __global__ __launch_bounds__(256) void a8_quantize_reg_kernel(const void* __rest
 // ---------------------------------------------------------------------------
 // 3..16 token rows: i8_rows_kernel
 // ---------------------------------------------------------------------------
-// One workgroup per 16 weight rows; its 8 waves split K into eighths. Both
+// One workgroup per 16 weight rows; its 8 or 16 waves split K. Both
 // int8 operands go from global memory straight into
 // v_mfma_i32_16x16x64_i8 (lane l: row l%16 of the weights / of the
 // activations, k 16*(l/16) .. +16 of each 64-k chunk); the quantized
 // activations (at most 16 x K bytes) stay in L2 for every workgroup. Each
-// wave issues the loads of up to eight chunks (all of them in flight before
+// wave issues the loads of up to eight (ten) chunks (all of them in flight before
 // the first MFMA waits) and then their MFMAs; rows past M or N read zeros
 // through the bounded descriptors. The waves' int32 sums are added through
 // LDS (exact in any order) and wave 0 writes the epilogue.
@@ -468,34 +468,32 @@ __global__ __launch_bounds__(256) void a8_quantize_reg_kernel(const void* __rest
 // a single launch whose workgroups quantize the activations themselves and
 // run 4x4x4 MFMAs over 256-byte row spans (QKV 9.1 -> 15.0 us at M = 8,
 // 25.7 us at M = 16: every workgroup re-reads the M x K activations).
-constexpr int kRW = 8;   // waves per workgroup (K split)
-constexpr int kRPD = 8;  // 64-k chunks in flight per wave
-
-__global__ __launch_bounds__(64 * kRW) void i8_rows_kernel(I8Args args) {
-  __shared__ i32x4_t red[kRW - 1][64];
+template <int RW, int RPD>  // waves per workgroup (K split), 64-k chunks in flight per wave
+__global__ __launch_bounds__(64 * RW) void i8_rows_kernel(I8Args args) {
+  __shared__ i32x4_t red[RW - 1][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, grp = lane >> 4;
   const int K = args.K, N = args.N, M = args.M;
   const int n0 = blockIdx.x * 16;
   const int nch = K / 64;
-  const int c0 = wave * nch / kRW, c1 = (wave + 1) * nch / kRW;
+  const int c0 = wave * nch / RW, c1 = (wave + 1) * nch / RW;
   const int nrows = min(16, N - n0);
   const rsrc_t rb = make_rsrc(args.b + (int64_t)n0 * K, (uint32_t)nrows * (uint32_t)K);
   const rsrc_t ra = make_rsrc(args.a, (uint32_t)M * (uint32_t)K);
   const uint32_t off = (uint32_t)(n16 * K + 16 * grp);
   i32x4_t acc = {0, 0, 0, 0};
-  for (int c = c0; c < c1; c += kRPD) {
-    u32x4_t av[kRPD], bv[kRPD];
+  for (int c = c0; c < c1; c += RPD) {
+    u32x4_t av[RPD], bv[RPD];
 #pragma unroll
-    for (int u = 0; u < kRPD; ++u) {
+    for (int u = 0; u < RPD; ++u) {
       const bool ok = c + u < c1;  // wave-uniform
       bv[u] = buf_load16(rb, ok ? off + 64u * (uint32_t)(c + u) : kOob);
       av[u] = buf_load16(ra, ok ? off + 64u * (uint32_t)(c + u) : kOob);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < kRPD; ++u)
+    for (int u = 0; u < RPD; ++u)
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, av[u]),
                                                   __builtin_bit_cast(i32x4_t, bv[u]), acc, 0, 0, 0);
   }
@@ -503,7 +501,7 @@ __global__ __launch_bounds__(64 * kRW) void i8_rows_kernel(I8Args args) {
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int w = 0; w < kRW - 1; ++w) acc += red[w][lane];
+  for (int w = 0; w < RW - 1; ++w) acc += red[w][lane];
   // lane (grp, n16) holds token rows 4grp .. 4grp+3 of weight row n0 + n16
   const int nn = n0 + n16;
 #pragma unroll
@@ -519,8 +517,30 @@ static bool use_rows(int64_t M, int64_t N, int64_t K) {
          !env_int("SPARKQ_I8_NO_ROWS", 0);
 }
 
+template <int RW>
+static void launch_rows_w(int rpd, const I8Args& args, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(args.N, 16)), block(64 * RW);
+  if (rpd == 10)
+    hipLaunchKernelGGL((i8_rows_kernel<RW, 10>), grid, block, 0, st, args);
+  else
+    hipLaunchKernelGGL((i8_rows_kernel<RW, 8>), grid, block, 0, st, args);
+}
+
+// Rows of more than 64 chunks (K > 4096) take 16 waves with ten chunks in
+// flight each, so that a wave's share of K is one batch of loads (down
+// 2560 x 9728: 16.0 -> 15.0 us at M = 8, 18.2 -> 17.2 at M = 16); shorter
+// rows keep 8 waves of up to eight chunks (4 waves of ten, 16 of eight or
+// ten measured slower on QKV and gate+up).
 static int launch_rows(const I8Args& args, hipStream_t st) {
-  hipLaunchKernelGGL(i8_rows_kernel, dim3((unsigned)cdiv(args.N, 16)), dim3(64 * kRW), 0, st, args);
+  const bool long_rows = args.K / 64 > 64;
+  const int rw = env_int("SPARKQ_I8_ROWS_RW", long_rows ? 16 : 8);
+  const int rpd = env_int("SPARKQ_I8_ROWS_RPD", long_rows ? 10 : 8);
+  if (rw == 4)
+    launch_rows_w<4>(rpd, args, st);
+  else if (rw == 16)
+    launch_rows_w<16>(rpd, args, st);
+  else
+    launch_rows_w<8>(rpd, args, st);
   return check_launch("i8_rows_kernel");
 }
 
