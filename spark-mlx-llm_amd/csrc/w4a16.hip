@@ -1630,7 +1630,8 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int G, int NWV, int MX>
+// PD: 1 = the loads of step s+1 go out during step s, 2 = those of step s+2
+template <int G, int NWV, int MX, int PD>
 __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a) {
   constexpr int NT = 64 * NWV;
   constexpr int BM = 32 * MX;                // tile rows: MX 32-row fragments per wave
@@ -1681,17 +1682,29 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
 #pragma unroll
   for (int ss = 0; ss < 4; ++ss) lds_r[ss] = (uint32_t)atile_off(l32, 4 * j + ss) * 2u;
 
-  u32x4_t ra[AL], rb[2];
-  uint32_t rsv[2];
-  auto load = [&](int step) {
-    const int k0 = step * kBK;
+  // PD register sets of one step's loads. With two, the loads of step s+2
+  // go out at the start of step s into the set step s has just taken its
+  // operands from, on every path (past the last step at an out-of-range
+  // offset, which reads zeros), so the wait counts stay exact across the loop.
+  constexpr int NW = PD, NA = PD;
+  u32x4_t ra[NA][AL], rb[NW][2];
+  uint32_t rsv[NW][2];
+  auto load_a = [&](int step, int set) {
+    const bool live = PD == 1 || step < nsteps;
+    const int k0 = live ? step * kBK : 0;
 #pragma unroll
     for (int i = 0; i < AL; ++i)
-      ra[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], 2 * k0, 0));
+      ra[set][i] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(live ? xoff[i] : kOob), 2 * k0, 0));
+  };
+  auto load_w = [&](int step, int set) {
+    const bool live = PD == 1 || step < nsteps;
+    const int k0 = live ? step * kBK : 0;
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
-      rb[y] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff[y], k0 / 2, 0));
-      rsv[y] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff[y], 2 * (k0 / G), 0);
+      rb[set][y] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(live ? woff[y] : kOob), k0 / 2, 0));
+      rsv[set][y] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(live ? soff[y] : kOob), 2 * (k0 / G), 0);
     }
   };
   auto lds_at = [&](uint32_t byte_off) -> u32x4_t* {
@@ -1706,12 +1719,24 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
 
   auto body = [&](int step, auto stc) {
     constexpr int st = decltype(stc)::value;
-    const u32x4_t wb0 = rb[0], wb1 = rb[1];
-    const f16x2_t s0 = __builtin_bit_cast(f16x2_t, rsv[0] * 0x10001u);
-    const f16x2_t s1 = __builtin_bit_cast(f16x2_t, rsv[1] * 0x10001u);
+    constexpr int rs0 = NW == 1 ? 0 : st;  // weight set holding this step
+    // nothing of a step moves into the one before (it would wait there for
+    // the loads still in flight)
+    if constexpr (PD > 1) __builtin_amdgcn_sched_barrier(0);
+    const u32x4_t wb0 = rb[rs0][0], wb1 = rb[rs0][1];
+    const f16x2_t s0 = __builtin_bit_cast(f16x2_t, rsv[rs0][0] * 0x10001u);
+    const f16x2_t s1 = __builtin_bit_cast(f16x2_t, rsv[rs0][1] * 0x10001u);
     const f16x2_t c0 = s0 * f16x2_t{(_Float16)-24.0f, (_Float16)-24.0f};
     const f16x2_t c1 = s1 * f16x2_t{(_Float16)-24.0f, (_Float16)-24.0f};
-    if (step + 1 < nsteps) load(step + 1);
+    if constexpr (PD == 1) {
+      if (step + 1 < nsteps) {
+        load_a(step + 1, 0);
+        load_w(step + 1, 0);
+      }
+    } else {
+      load_a(step + 2, st);
+      load_w(step + 2, st);
+    }
 #pragma unroll
     for (int ss = 0; ss < 4; ++ss) {
       u32x4_t bf0, bf1;
@@ -1731,19 +1756,37 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
       }
     }
     if (step + 1 < nsteps) {
+      constexpr int rs1 = NA == 1 ? 0 : st ^ 1;  // activation set holding the next step
 #pragma unroll
-      for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)((st ^ 1) * BM * kBK * 2)) = ra[i];
+      for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)((st ^ 1) * BM * kBK * 2)) = ra[rs1][i];
     }
     __syncthreads();
   };
 
-  load(s_begin);
+  load_a(s_begin, 0);
+  load_w(s_begin, 0);
+  if constexpr (PD > 1) {
+    __builtin_amdgcn_sched_barrier(0);  // the sets go out in step order
+    load_a(s_begin + 1, 1);
+    load_w(s_begin + 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
-  for (int i = 0; i < AL; ++i) *lds_at(lds_w[i]) = ra[i];
+  for (int i = 0; i < AL; ++i) *lds_at(lds_w[i]) = ra[0][i];
   __syncthreads();
-  for (int step = s_begin; step < nsteps; step += 2) {
-    body(step, std::integral_constant<int, 0>{});
-    if (step + 1 < nsteps) body(step + 1, std::integral_constant<int, 1>{});
+  if constexpr (PD == 1) {
+    for (int step = s_begin; step < nsteps; step += 2) {
+      body(step, std::integral_constant<int, 0>{});
+      if (step + 1 < nsteps) body(step + 1, std::integral_constant<int, 1>{});
+    }
+  } else {
+    // pairs of steps with no branch around the loads, then an odd last step
+    int step = s_begin;
+    for (; step + 2 <= nsteps; step += 2) {
+      body(step, std::integral_constant<int, 0>{});
+      body(step + 1, std::integral_constant<int, 1>{});
+    }
+    if (step < nsteps) body(step, std::integral_constant<int, 0>{});
   }
 
   if (split) {
@@ -2525,6 +2568,7 @@ static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
   WidePlan p{};
   const int64_t cus = device_cus(), P = 2 * cus;
   p.MX = cdiv(N, 256) * cdiv(M, 128) < P / 4 && M > 64 && !env_int("SPARKQ_W4_GEMM_MX4", 0) ? 2 : 4;
+  if (env_int("SPARKQ_W4_GEMM_MX2", 0)) p.MX = 2;
   const int64_t BM = 32 * p.MX;
   const int64_t tn = cdiv(N, 256), T = tn * cdiv(M, BM), nsteps = K / kBK;
   int64_t tail = T % P, S = 1;
@@ -2673,15 +2717,26 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   a.part = reinterpret_cast<float*>(ws + l.bytes);
   a.counters = counters;
   dim3 gw((unsigned)wp.items);
-#define SPARKQ_X16W(GG, MM) hipLaunchKernelGGL((w4_gemm_x16w_kernel<GG, 4, MM>), gw, dim3(256), 0, st, a)
-  if (wp.MX == 2) {
-    if (G == 32) SPARKQ_X16W(32, 2);
-    else if (G == 64) SPARKQ_X16W(64, 2);
-    else SPARKQ_X16W(128, 2);
+#define SPARKQ_X16W(GG, MM, PP) \
+  hipLaunchKernelGGL((w4_gemm_x16w_kernel<GG, 4, MM, PP>), gw, dim3(256), 0, st, a)
+  // the 64-row tiles (grids of at most one workgroup per CU, whose steps
+  // wait on their loads) keep two steps of loads in flight: QKV 3584 x 2560
+  // at M = 512 35.0 -> 32.2 us, down 2560 x 9728 78.3 -> 70.0 us, bit-identical;
+  // the 128-row tiles have no registers for it (weights alone two steps
+  // ahead measured 0-1% slower at M = 512 and 2048)
+  const int pd = env_int("SPARKQ_W4_GEMM_PD", wp.MX == 2 ? 2 : 1);
+  if (wp.MX == 2 && pd == 2) {
+    if (G == 32) SPARKQ_X16W(32, 2, 2);
+    else if (G == 64) SPARKQ_X16W(64, 2, 2);
+    else SPARKQ_X16W(128, 2, 2);
+  } else if (wp.MX == 2) {
+    if (G == 32) SPARKQ_X16W(32, 2, 1);
+    else if (G == 64) SPARKQ_X16W(64, 2, 1);
+    else SPARKQ_X16W(128, 2, 1);
   } else {
-    if (G == 32) SPARKQ_X16W(32, 4);
-    else if (G == 64) SPARKQ_X16W(64, 4);
-    else SPARKQ_X16W(128, 4);
+    if (G == 32) SPARKQ_X16W(32, 4, 1);
+    else if (G == 64) SPARKQ_X16W(64, 4, 1);
+    else SPARKQ_X16W(128, 4, 1);
   }
 #undef SPARKQ_X16W
 }
