@@ -20,8 +20,12 @@
 //                        combine in the same launch (the last workgroup of a
 //                        tile sums the int32 partials).
 //   i8_rows_kernel       3..16 token rows: 16 weight rows per workgroup, 8
-//                        waves split K, both operands straight from global
-//                        memory into v_mfma_i32_16x16x64_i8.
+//                        (16) waves split K, both operands straight from
+//                        global memory into v_mfma_i32_16x16x64_i8.
+//   i8_rows_q_kernel     3..16 token rows over at least two row tiles per
+//                        workgroup slot (gate+up): one round of workgroups
+//                        owning up to three tiles each, the activation tile
+//                        staged once per workgroup in LDS.
 #include "common.h"
 
 namespace sparkq {
@@ -73,6 +77,7 @@ struct I8Args {
   int slab;             // 32-k chunks per LDS slab of activations
   int S;
   int mode;
+  int wgs;              // workgroups of the one-round rows kernel
 };
 
 __device__ __forceinline__ i32x16_t mfma_i8(u32x4_t a, u32x4_t b, i32x16_t c) {
@@ -511,6 +516,146 @@ __global__ __launch_bounds__(64 * RW) void i8_rows_kernel(I8Args args) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 3..16 token rows over many row tiles: i8_rows_q_kernel (one round)
+// ---------------------------------------------------------------------------
+// When the weights hold at least two 16-row tiles per workgroup slot of the
+// chip (gate+up), i8_rows_kernel re-reads the activations from L2 in every
+// wave and runs its tiles in several rounds. Here P = twice the CUs
+// workgroups each own the contiguous tiles [i*T/P, (i+1)*T/P) (at most
+// three), all resident at once:
+//  * the workgroup stages the 16 x K int8 activation tile once in LDS (rows
+//    past M read zeros through the bounded descriptor), padded rows;
+//  * wave w owns quarter w%4 of K of tile w/4 and issues all of its 16-byte
+//    weight loads (16 rows x 64 bytes per instruction) before any
+//    arithmetic, then reads the matching activations from LDS into
+//    v_mfma_i32_16x16x64_i8;
+//  * the four quarters' int32 sums are added through LDS (exact in any
+//    order) and the first wave of each tile writes the epilogue.
+// Measured on gate+up 19456 x 2560 (36 weight sets per graph replay, the
+// quantizer launch included): M = 16 22.0 -> 17.9 us, M = 8 19.0 -> 17.0,
+// M = 4 17.4 -> 16.7, M = 3 the same. The same kernel quantizing the 16-bit
+// activations itself (one launch, each workgroup repeating the per-token
+// amax and the IEEE divisions) took 24-27 us at M = 3..9 against 16-17 us
+// for the quantizer launch followed by this kernel, so it was not kept.
+constexpr int kQW = 4;    // waves per row tile (K split)
+constexpr int kQT = 3;    // row tiles per workgroup, at most
+constexpr int kQXP = 4;   // staged 16-byte activation pieces per thread
+
+__host__ __device__ __forceinline__ int rows_q_pitch(int K) { return K + 16; }
+
+template <int CPW>  // 64-k chunks per wave (K = 256 * CPW)
+__global__ __launch_bounds__(64 * kQW * kQT) void i8_rows_q_kernel(I8Args args) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NT = 64 * kQW * kQT;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, grp = lane >> 4;
+  const int K = args.K, N = args.N, M = args.M;
+  const int T = (N + 15) >> 4;
+  const int t0 = (int)((int64_t)blockIdx.x * T / args.wgs);
+  const int nt = (int)((int64_t)(blockIdx.x + 1) * T / args.wgs) - t0;
+  const int pitch = rows_q_pitch(K);
+  int8_t* xs = reinterpret_cast<int8_t*>(smem);                                  // [16][pitch]
+  i32x4_t* red = reinterpret_cast<i32x4_t*>(smem + 16 * pitch);                 // [kQT][kQW-1][64]
+
+  // 1. staging loads: piece p = row p / npr, 16 bytes at 16 * (p % npr) of
+  // the 16-row activation tile (rows past M read zeros). Issued on every
+  // path: a branch around a load would make the compiler wait for it where
+  // the paths join.
+  const int npr = K >> 4, np = 16 * npr;
+  const rsrc_t ra = make_rsrc(args.a, (uint32_t)M * (uint32_t)K);
+  u32x4_t xr[kQXP];
+#pragma unroll
+  for (int i = 0; i < kQXP; ++i) {
+    const int p = tid + i * NT;
+    const int row = p / npr, pc = p - row * npr;
+    xr[i] = buf_load16(ra, p < np && row < M ? (uint32_t)(row * K + 16 * pc) : kOob);
+  }
+  // 2. the wave's weights: tile w/4, chunks [q*CPW, (q+1)*CPW) of quarter q
+  const int tt = wave / kQW, q = wave - tt * kQW;
+  const bool has_tile = tt < nt;
+  const int n0 = (t0 + tt) * 16;
+  const int nrows = has_tile ? min(16, N - n0) : 0;
+  const rsrc_t rb = make_rsrc(args.b + (int64_t)(has_tile ? n0 : 0) * K, (uint32_t)nrows * (uint32_t)K);
+  const uint32_t off = (uint32_t)(n16 * K + 16 * grp + 64 * q * CPW);
+  u32x4_t bv[CPW];
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) bv[u] = buf_load16(rb, has_tile ? off + 64u * u : kOob);
+  __builtin_amdgcn_sched_barrier(0);  // every load above ahead of the arithmetic
+
+  // 3. activations to LDS
+#pragma unroll
+  for (int i = 0; i < kQXP; ++i) {
+    const int p = tid + i * NT;
+    if (p < np) {
+      const int row = p / npr, pc = p - row * npr;
+      *reinterpret_cast<u32x4_t*>(xs + row * pitch + 16 * pc) = xr[i];
+    }
+  }
+  __syncthreads();
+
+  // 4. the quarter's MFMAs: A = activation row n16 (k 16*grp.. of the chunk)
+  i32x4_t acc = {0, 0, 0, 0};
+  const int8_t* xa = xs + n16 * pitch + 16 * grp + 64 * q * CPW;
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xa + 64 * u);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, av),
+                                                __builtin_bit_cast(i32x4_t, bv[u]), acc, 0, 0, 0);
+  }
+  // 5. quarters 1..3 to LDS, quarter 0 adds them and writes the tile
+  if (has_tile && q > 0) red[(tt * (kQW - 1) + q - 1) * 64 + lane] = acc;
+  __syncthreads();
+  if (!has_tile || q != 0) return;
+#pragma unroll
+  for (int w = 0; w < kQW - 1; ++w) acc += red[(tt * (kQW - 1) + w) * 64 + lane];
+  // lane (grp, n16) holds token rows 4grp .. 4grp+3 of weight row n0 + n16
+  const int nn = n0 + n16;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * grp + r;
+    if (m < M && nn < N) i8_store(args, m, nn, acc[r]);
+  }
+}
+
+struct RowsQPlan {
+  bool ok;
+  int wgs, cpw;
+  size_t lds;
+};
+
+// At least two row tiles per workgroup slot (2 per CU), whole 256-k quarter
+// chunks of 4..12 64-k chunks (K = 1024 .. 3072 in steps of 512), the
+// activation tile within the staging budget.
+static RowsQPlan plan_rows_q(int64_t M, int64_t N, int64_t K) {
+  RowsQPlan p{};
+  if (env_int("SPARKQ_I8_NO_ROWSQ", 0) || M < 1 || M > 16 || K % 256 != 0) return p;
+  const int64_t cpw = K / 256;
+  if (cpw < 4 || cpw > 12 || cpw % 2 != 0) return p;
+  const int64_t T = cdiv(N, 16), P = 2 * device_cus();
+  if (T < 2 * P || K > kQXP * 64 * kQW * kQT) return p;  // one staging pass: K pieces
+  if (N * K >= (int64_t)kOob || M * K >= (int64_t)kOob) return p;
+  p.wgs = (int)std::max<int64_t>(P, cdiv(T, kQT));
+  p.cpw = (int)cpw;
+  p.lds = (size_t)16 * rows_q_pitch((int)K) + (size_t)kQT * (kQW - 1) * 64 * 16;
+  p.ok = p.lds <= 65536;
+  return p;
+}
+
+static int launch_rows_q(I8Args args, const RowsQPlan& p, hipStream_t st) {
+  args.wgs = p.wgs;
+  const dim3 grid((unsigned)p.wgs), block(64 * kQW * kQT);
+  switch (p.cpw) {
+    case 4: hipLaunchKernelGGL(i8_rows_q_kernel<4>, grid, block, p.lds, st, args); break;
+    case 6: hipLaunchKernelGGL(i8_rows_q_kernel<6>, grid, block, p.lds, st, args); break;
+    case 8: hipLaunchKernelGGL(i8_rows_q_kernel<8>, grid, block, p.lds, st, args); break;
+    case 10: hipLaunchKernelGGL(i8_rows_q_kernel<10>, grid, block, p.lds, st, args); break;
+    default: hipLaunchKernelGGL(i8_rows_q_kernel<12>, grid, block, p.lds, st, args); break;
+  }
+  return check_launch("i8_rows_q_kernel");
+}
+
 // 3..16 rows (1..16 with the decode GEMV switched off), whole 64-k chunks
 static bool use_rows(int64_t M, int64_t N, int64_t K) {
   return M >= 1 && M <= 16 && K % 64 == 0 && N * K < (int64_t)kOob && M * K < (int64_t)kOob &&
@@ -532,6 +677,8 @@ static void launch_rows_w(int rpd, const I8Args& args, hipStream_t st) {
 // rows keep 8 waves of up to eight chunks (4 waves of ten, 16 of eight or
 // ten measured slower on QKV and gate+up).
 static int launch_rows(const I8Args& args, hipStream_t st) {
+  const RowsQPlan qp = plan_rows_q(args.M, args.N, args.K);
+  if (qp.ok) return launch_rows_q(args, qp, st);
   const bool long_rows = args.K / 64 > 64;
   const int rw = env_int("SPARKQ_I8_ROWS_RW", long_rows ? 16 : 8);
   const int rpd = env_int("SPARKQ_I8_ROWS_RPD", long_rows ? 10 : 8);

@@ -67,6 +67,57 @@ def test_int8_matmul_int32_bit_exact(gpu, m, n, k):
         assert np.array_equal(c.cpu().numpy(), o.int8_matmul(a, b))
 
 
+@pytest.mark.parametrize("m,n,k", [(3, 16390, 2560), (16, 16384, 1024), (8, 19456, 3072),
+                                   (5, 17000, 1536), (12, 20000, 2048), (16, 19456, 2560)])
+def test_int8_rows_one_round(gpu, m, n, k, monkeypatch):
+    """3..16 rows over at least two 16-row tiles per workgroup slot (the
+    one-round kernel: activations staged once per workgroup, K in quarters):
+    a partial last tile, K = 1024..3072, bit-exact against the oracle on the
+    first and last tiles and sampled columns, and equal in full to the
+    per-tile kernel."""
+    import sparkq
+
+    rng = np.random.default_rng(m * 11 + n + k)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    at, bt = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    c = sparkq.int8_matmul_int32(at, bt)
+    cols = np.unique(np.concatenate([np.arange(16), np.arange(n - 16, n),
+                                     rng.choice(n, 256, replace=False)]))
+    assert np.array_equal(c.cpu().numpy()[:, cols], o.int8_matmul(a, b[cols]))
+    monkeypatch.setenv("SPARKQ_I8_NO_ROWSQ", "1")
+    assert torch.equal(c, sparkq.int8_matmul_int32(at, bt))
+
+
+@pytest.mark.parametrize("m,n,k,dtype,with_bias", [(3, 16390, 2560, o.BF16, True), (8, 19456, 2560, o.F16, False),
+                                                   (5, 17000, 1536, o.BF16, False), (9, 16384, 2560, o.BF16, True),
+                                                   (6, 20000, 3072, o.F16, True), (8, 19456, 2560, o.BF16, False)])
+def test_w8a8_linear_rows_one_round(gpu, m, n, k, dtype, with_bias, monkeypatch):
+    """W8A8 projections over the one-round rows kernel (epilogue with and
+    without bias): the fp32 output bit for bit against the oracle on the
+    first and last row tiles and sampled columns, and equal in full, in fp32
+    and in the 16-bit dtype, to the per-tile rows kernel."""
+    import sparkq
+
+    x16 = _x(m, k, dtype, seed=n)
+    xf = o.bits_to_f32(x16, dtype)
+    wq, wsc = _w8(n, k, seed=m)
+    rng = np.random.default_rng(n + k)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float32) if with_bias else None
+    xt = up16(x16, dtype, gpu)
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    bt = torch.from_numpy(bias).to(gpu) if with_bias else None
+    y32 = sparkq.w8a8_linear(xt, wt, st, bias=bt, out_dtype=torch.float32)
+    y16 = sparkq.w8a8_linear(xt, wt, st, bias=bt)
+    cols = np.unique(np.concatenate([np.arange(16), np.arange(n - 16, n), rng.choice(n, 256, replace=False)]))
+    qa, sa = o.a8_quantize(xf)
+    ref = o.w8a8_epilogue(o.int8_matmul(qa, wq[cols]), sa, wsc[cols], None if bias is None else bias[cols])
+    assert np.array_equal(y32.cpu().numpy()[:, cols].view(np.uint32), ref.view(np.uint32))
+    monkeypatch.setenv("SPARKQ_I8_NO_ROWSQ", "1")
+    assert torch.equal(y32, sparkq.w8a8_linear(xt, wt, st, bias=bt, out_dtype=torch.float32))
+    assert torch.equal(y16, sparkq.w8a8_linear(xt, wt, st, bias=bt))
+
+
 def test_int8_matmul_extreme_range(gpu):
     import sparkq
 
