@@ -702,6 +702,7 @@ struct GemvStreamArgs {
   int P;   // workgroups
   int QW;  // row quads of the largest workgroup
   const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
+  int RR;  // 1: workgroup i owns rows [i*N/P, (i+1)*N/P) (quads from its first row)
 };
 
 constexpr int kStreamXP = 1;   // staged activation pieces (64 B) per thread, at most
@@ -738,8 +739,16 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
   const int RB = K >> 1;             // bytes per weight row
   const int U = (RB + 255) >> 8;     // spans per row
   const int ng = K / G;              // groups per row
-  const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
-  const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
+  // the workgroup's rows [r0, r1), taken as row quads from r0
+  int r0, r1;
+  if (a.RR) {
+    r0 = (int)((int64_t)blockIdx.x * N / a.P);
+    r1 = (int)((int64_t)(blockIdx.x + 1) * N / a.P);
+  } else {
+    r0 = 4 * (int)((int64_t)blockIdx.x * a.nq / a.P);
+    r1 = min(N, 4 * (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P));
+  }
+  const int nql = (r1 - r0 + 3) >> 2;
   const int nitems = nql * U;
   const StreamLds L = stream_lds(K, a.QW, G);
 
@@ -767,7 +776,7 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
   for (int i = 0; i < kStreamSP; ++i) {
     const int pi = tid + i * NT;
     if (i * NT + 64 * wave < nsp) {
-      const uint32_t off = pi < nsp ? 8u * (uint32_t)qa * ng + 16u * pi : kOob;
+      const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
       sr[i] = buf_load16(rs, off);
       br[i] = buf_load16(rb, off);
     }
@@ -783,8 +792,8 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
     const int it = wave + i * NW;
     ql[i] = it / U;
     sp[i] = it - ql[i] * U;
-    const int row = 4 * (qa + ql[i]) + j, p = 256 * sp[i] + 16 * b;
-    const bool ok = i < nmy && (FULL || (row < N && p + 16 <= RB));
+    const int row = r0 + 4 * ql[i] + j, p = 256 * sp[i] + 16 * b;
+    const bool ok = i < nmy && row < r1 && (FULL || p + 16 <= RB);
     wv[i] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
   }
 
@@ -844,7 +853,7 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
     if (i < nmy) {
       const int s = sp[i];
       const int p = 256 * s + 16 * b;
-      const bool ok = FULL || (4 * (qa + ql[i]) + j < N && p + 16 <= RB);
+      const bool ok = r0 + 4 * ql[i] + j < r1 && (FULL || p + 16 <= RB);
       const int piece = FULL ? 16 * s + b : min(16 * s + b, (K >> 5) - 1);
       uint32_t xa[4][4];
 #pragma unroll
@@ -886,8 +895,8 @@ __global__ __launch_bounds__(64 * NW) void w4_gemv_stream_kernel(GemvStreamArgs 
       for (int s = 0; s < U; ++s) v += src[s * 64];
     }
     v = sum_row16(v);
-    const int row = 4 * qa + rl;
-    if (bb == 0 && rl < 4 * nql && row < N)
+    const int row = r0 + rl;
+    if (bb == 0 && row < r1)
       store_out(a.y, row, a.res ? add_rounded<T>(v, a.res[row]) : v, a.y_dtype);
   }
 }
@@ -2372,7 +2381,7 @@ int w4_qkv_rope(const void* x, const uint32_t* w, const void* s, const void* b, 
 // since they are staged in 16-byte loads.
 struct StreamPlan {
   bool ok;
-  int P, QW, NI, NW;
+  int P, QW, NI, NW, RR;
   bool full;
   size_t lds;
 };
@@ -2393,6 +2402,13 @@ static StreamPlan plan_stream(int64_t M, int64_t N, int64_t K, int G) {
   p.NW = env_int("SPARKQ_W4_STREAM_NW", 16) == 8 ? 8 : 16;
   p.P = (int)std::min<int64_t>(nq, device_cus() * (16 / p.NW));
   p.QW = (int)cdiv(nq, p.P);
+  // Row ranges instead of whole quads (every CU streams the same bytes:
+  // down 2560 x 9728 gives each CU 10 rows instead of 8 or 12) when the
+  // (scale, bias) rows of any first row start on a 16-byte boundary: down
+  // 6.2-6.4 -> 5.9 us, bit-identical. The one-round kernel of the 5-span rows
+  // (gate+up, QKV) showed no gain from the same split.
+  p.RR = env_int("SPARKQ_W4_STREAM_ROWS", 1) && ng % 8 == 0 && N >= 4 * (int64_t)p.P;
+  if (p.RR) p.QW = (int)cdiv(cdiv(N, p.P), 4);
   const int64_t ni = cdiv(p.QW * U, p.NW);
   if (ni > 8) return p;
   p.NI = ni <= 2 ? 2 : (ni <= 4 ? (int)ni : (ni <= 6 ? 6 : 8));
@@ -2777,6 +2793,7 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     a.nq = (int)cdiv(N, 4);
     a.P = sp.P;
     a.QW = sp.QW;
+    a.RR = sp.RR;
     a.res = (const uint16_t*)res;
     if (res_done) *res_done = res != nullptr;
     if (xdt == SPARKQ_BF16)
