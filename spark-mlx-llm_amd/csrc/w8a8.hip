@@ -78,6 +78,14 @@ struct I8Args {
   int S;
   int mode;
   int wgs;              // workgroups of the one-round rows kernel
+  // one launch with the quantizer (3..16 rows): producer workgroups [0, np)
+  // write the int8 rows of x into a (and their scales into sa); counters[0]
+  // counts the rows written, counters[1] the workgroups done (both zero on
+  // entry and exit)
+  const void* x;
+  int xt;               // 0 bf16, 1 fp16
+  int np;               // producer workgroups (0: a already holds the int8 rows)
+  int spin;             // polls of counters[0] before a workgroup quantizes itself
 };
 
 __device__ __forceinline__ i32x16_t mfma_i8(u32x4_t a, u32x4_t b, i32x16_t c) {
@@ -452,6 +460,131 @@ __global__ __launch_bounds__(256) void a8_quantize_reg_kernel(const void* __rest
 }
 
 // ---------------------------------------------------------------------------
+// one launch for 3..16 token rows: the quantizer runs in producer
+// workgroups while the others stream their weights
+// ---------------------------------------------------------------------------
+// The first np workgroups of the grid each quantize rows b, b + np, ... of x
+// (one whole row per pass: per-token amax, scale = amax/127 with IEEE
+// division, rint, clamp to +-127, as a8_quantize_kernel) into the int8
+// buffer with stores at the device coherence level (sc1), count the rows
+// done, and exit. Every other workgroup issues its weight loads, then polls
+// the count (at most args.spin times); past the bound it quantizes all rows
+// itself, writing the same bytes, so no workgroup waits on one that may not
+// be resident. Its activation loads and scale reads then go to the same
+// coherence level. The last workgroup to finish resets both counters.
+constexpr int kA8PP = 4;  // 16-byte activation pieces per producer thread, at most
+constexpr int kSc1 = 16;  // buffer cache policy sc1: the device coherence level (split-K partials use it too)
+
+// LEAN: one piece at a time, loaded twice (the fallback, which runs while a
+// workgroup holds its weights in registers)
+template <int XT, bool LEAN = false>
+__device__ void a8_produce_row(const I8Args& a, int row, float* red) {
+  typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+  const int K = a.K, np = K >> 3, NT = blockDim.x, tid = threadIdx.x;
+  const rsrc_t rx = make_rsrc(reinterpret_cast<const unsigned char*>(a.x) + (int64_t)row * K * 2,
+                              (uint32_t)K * 2);
+  constexpr int NV = LEAN ? 1 : kA8PP;
+  u32x4_t v[NV];
+  float mx = 0.0f;
+  if constexpr (LEAN) {
+    for (int p = tid; p < np; p += NT) {
+      const u32x4_t t = buf_load16(rx, 16u * (uint32_t)p);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(piece_elem<XT>(t, e)));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kA8PP; ++i) {
+      const int p = tid + i * NT;
+      v[i] = buf_load16(rx, p < np ? 16u * (uint32_t)p : kOob);
+    }
+#pragma unroll
+    for (int i = 0; i < kA8PP; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(piece_elem<XT>(v[i], e)));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  float am = 0.0f;
+  for (int w = 0; w < (NT >> 6); ++w) am = fmaxf(am, red[w]);
+  const float scale = am > 0.0f ? am / 127.0f : 1.0f;
+  const rsrc_t rq = make_rsrc(a.a + (int64_t)row * K, (uint32_t)K);
+#pragma unroll
+  for (int i = 0; i < (LEAN ? (np + NT - 1) / NT : kA8PP); ++i) {
+    const int p = tid + i * NT;
+    if (p < np) {
+      const u32x4_t pv = LEAN ? buf_load16(rx, 16u * (uint32_t)p) : v[LEAN ? 0 : i];
+      uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float t = __builtin_rintf(piece_elem<XT>(pv, e) / scale);
+        t = fminf(fmaxf(t, -127.0f), 127.0f);
+        packed[e >> 2] |= ((uint32_t)(int32_t)t & 0xFFu) << (8 * (e & 3));
+      }
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{packed[0], packed[1]}, rq, 8 * p, 0, kSc1);
+    }
+  }
+  if (tid == 0) splitk_store(const_cast<float*>(a.sa) + row, scale);
+  __syncthreads();  // red is reused by the next row
+}
+
+// producer workgroup b: rows b, b + np, ...; then counts them
+template <int XT>
+__device__ void a8_producer(const I8Args& a, float* red) {
+  int rows = 0;
+  for (int row = blockIdx.x; row < a.M; row += a.np, ++rows) a8_produce_row<XT>(a, row, red);
+  __builtin_amdgcn_s_waitcnt(0);  // the stores have reached the coherence level
+  __syncthreads();
+  if (threadIdx.x == 0 && rows > 0)
+    __hip_atomic_fetch_add(&a.counters[0], (unsigned)rows, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// consumer: returns once all M rows are written (by the producers or, past
+// the poll bound, by this workgroup)
+template <int XT>
+__device__ void a8_wait_rows(const I8Args& a, int* flag, float* red) {
+  if (threadIdx.x == 0) {
+    int ok = 0;
+    for (int it = 0; it < a.spin; ++it) {
+      if (splitk_load(&a.counters[0]) >= (unsigned)a.M) {
+        ok = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(8);
+    }
+    *flag = ok;
+  }
+  __syncthreads();
+  if (*flag == 0) {
+    for (int row = 0; row < a.M; ++row) a8_produce_row<XT, true>(a, row, red);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+}
+
+// every workgroup at its end; the last one resets the counters
+__device__ __forceinline__ void a8_done(const I8Args& a) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_s_waitcnt(0);
+    if (__hip_atomic_fetch_add(&a.counters[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        gridDim.x - 1) {
+      __hip_atomic_store(&a.counters[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&a.counters[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// fp32 epilogue with the scale read at the coherence level
+__device__ __forceinline__ void i8_store_sync(const I8Args& args, int gm, int nn, int32_t s) {
+  const float bias = args.bias ? load_in(args.bias, nn, args.bias_dtype) : 0.0f;
+  const float t = (float)s * splitk_load(args.sa + gm);
+  store_out(args.y, (int64_t)gm * args.N + nn, fmaf(t, args.sw[nn], bias), args.y_dtype);
+}
+
+// ---------------------------------------------------------------------------
 // 3..16 token rows: i8_rows_kernel
 // ---------------------------------------------------------------------------
 // One workgroup per 16 weight rows; its 8 or 16 waves split K. Both
@@ -473,14 +606,26 @@ __global__ __launch_bounds__(256) void a8_quantize_reg_kernel(const void* __rest
 // a single launch whose workgroups quantize the activations themselves and
 // run 4x4x4 MFMAs over 256-byte row spans (QKV 9.1 -> 15.0 us at M = 8,
 // 25.7 us at M = 16: every workgroup re-reads the M x K activations).
-template <int RW, int RPD>  // waves per workgroup (K split), 64-k chunks in flight per wave
+// XT < 0: the int8 rows are in args.a already; 0 / 1: one launch with the
+// quantizer (bf16 / fp16 x), producers first in the grid
+template <int RW, int RPD, int XT>  // waves per workgroup (K split), 64-k chunks in flight per wave
 __global__ __launch_bounds__(64 * RW) void i8_rows_kernel(I8Args args) {
   __shared__ i32x4_t red[RW - 1][64];
+  __shared__ float sred[16];
+  __shared__ int sflag;
+  if constexpr (XT >= 0) {
+    if ((int)blockIdx.x < args.np) {
+      a8_producer<XT>(args, sred);
+      a8_done(args);
+      return;
+    }
+  }
+  const int bx = XT >= 0 ? (int)blockIdx.x - args.np : (int)blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, grp = lane >> 4;
   const int K = args.K, N = args.N, M = args.M;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = bx * 16;
   const int nch = K / 64;
   const int c0 = wave * nch / RW, c1 = (wave + 1) * nch / RW;
   const int nrows = min(16, N - n0);
@@ -488,13 +633,32 @@ __global__ __launch_bounds__(64 * RW) void i8_rows_kernel(I8Args args) {
   const rsrc_t ra = make_rsrc(args.a, (uint32_t)M * (uint32_t)K);
   const uint32_t off = (uint32_t)(n16 * K + 16 * grp);
   i32x4_t acc = {0, 0, 0, 0};
+  bool waited = XT < 0;
   for (int c = c0; c < c1; c += RPD) {
     u32x4_t av[RPD], bv[RPD];
+    if (!waited) {
+      // one launch: the weights first, then the rows once they are written
 #pragma unroll
-    for (int u = 0; u < RPD; ++u) {
-      const bool ok = c + u < c1;  // wave-uniform
-      bv[u] = buf_load16(rb, ok ? off + 64u * (uint32_t)(c + u) : kOob);
-      av[u] = buf_load16(ra, ok ? off + 64u * (uint32_t)(c + u) : kOob);
+      for (int u = 0; u < RPD; ++u)
+        bv[u] = buf_load16(rb, c + u < c1 ? off + 64u * (uint32_t)(c + u) : kOob);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (XT >= 0) a8_wait_rows<XT>(args, &sflag, sred);
+      waited = true;
+#pragma unroll
+      for (int u = 0; u < RPD; ++u)
+        av[u] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                         ra, (int)(c + u < c1 ? off + 64u * (uint32_t)(c + u) : kOob), 0, kSc1));
+    } else {
+#pragma unroll
+      for (int u = 0; u < RPD; ++u) {
+        const bool ok = c + u < c1;  // wave-uniform
+        bv[u] = buf_load16(rb, ok ? off + 64u * (uint32_t)(c + u) : kOob);
+        av[u] = XT < 0 ? buf_load16(ra, ok ? off + 64u * (uint32_t)(c + u) : kOob)
+                       : __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         ra, (int)(ok ? off + 64u * (uint32_t)(c + u) : kOob),
+                                                         0, kSc1));
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -502,18 +666,29 @@ __global__ __launch_bounds__(64 * RW) void i8_rows_kernel(I8Args args) {
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, av[u]),
                                                   __builtin_bit_cast(i32x4_t, bv[u]), acc, 0, 0, 0);
   }
+  if constexpr (XT >= 0) {
+    // a wave with no chunk still takes part in the wait (it has barriers)
+    if (!waited) a8_wait_rows<XT>(args, &sflag, sred);
+  }
   if (wave > 0) red[wave - 1][lane] = acc;
   __syncthreads();
-  if (wave != 0) return;
+  if (wave == 0) {
 #pragma unroll
-  for (int w = 0; w < RW - 1; ++w) acc += red[w][lane];
-  // lane (grp, n16) holds token rows 4grp .. 4grp+3 of weight row n0 + n16
-  const int nn = n0 + n16;
+    for (int w = 0; w < RW - 1; ++w) acc += red[w][lane];
+    // lane (grp, n16) holds token rows 4grp .. 4grp+3 of weight row n0 + n16
+    const int nn = n0 + n16;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * grp + r;
-    if (m < M && nn < N) i8_store(args, m, nn, acc[r]);
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * grp + r;
+      if (m < M && nn < N) {
+        if constexpr (XT < 0)
+          i8_store(args, m, nn, acc[r]);
+        else
+          i8_store_sync(args, m, nn, acc[r]);
+      }
+    }
   }
+  if constexpr (XT >= 0) a8_done(args);
 }
 
 // ---------------------------------------------------------------------------
@@ -544,17 +719,27 @@ constexpr int kQXP = 4;   // staged 16-byte activation pieces per thread
 
 __host__ __device__ __forceinline__ int rows_q_pitch(int K) { return K + 16; }
 
-template <int CPW>  // 64-k chunks per wave (K = 256 * CPW)
+template <int CPW, int XT>  // 64-k chunks per wave (K = 256 * CPW); XT as i8_rows_kernel
 __global__ __launch_bounds__(64 * kQW * kQT) void i8_rows_q_kernel(I8Args args) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ float sred[16];
+  __shared__ int sflag;
+  if constexpr (XT >= 0) {
+    if ((int)blockIdx.x < args.np) {
+      a8_producer<XT>(args, sred);
+      a8_done(args);
+      return;
+    }
+  }
+  const int bx = XT >= 0 ? (int)blockIdx.x - args.np : (int)blockIdx.x;
   constexpr int NT = 64 * kQW * kQT;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, grp = lane >> 4;
   const int K = args.K, N = args.N, M = args.M;
   const int T = (N + 15) >> 4;
-  const int t0 = (int)((int64_t)blockIdx.x * T / args.wgs);
-  const int nt = (int)((int64_t)(blockIdx.x + 1) * T / args.wgs) - t0;
+  const int t0 = (int)((int64_t)bx * T / args.wgs);
+  const int nt = (int)((int64_t)(bx + 1) * T / args.wgs) - t0;
   const int pitch = rows_q_pitch(K);
   int8_t* xs = reinterpret_cast<int8_t*>(smem);                                  // [16][pitch]
   i32x4_t* red = reinterpret_cast<i32x4_t*>(smem + 16 * pitch);                 // [kQT][kQW-1][64]
@@ -566,11 +751,13 @@ __global__ __launch_bounds__(64 * kQW * kQT) void i8_rows_q_kernel(I8Args args) 
   const int npr = K >> 4, np = 16 * npr;
   const rsrc_t ra = make_rsrc(args.a, (uint32_t)M * (uint32_t)K);
   u32x4_t xr[kQXP];
+  if constexpr (XT < 0) {
 #pragma unroll
-  for (int i = 0; i < kQXP; ++i) {
-    const int p = tid + i * NT;
-    const int row = p / npr, pc = p - row * npr;
-    xr[i] = buf_load16(ra, p < np && row < M ? (uint32_t)(row * K + 16 * pc) : kOob);
+    for (int i = 0; i < kQXP; ++i) {
+      const int p = tid + i * NT;
+      const int row = p / npr, pc = p - row * npr;
+      xr[i] = buf_load16(ra, p < np && row < M ? (uint32_t)(row * K + 16 * pc) : kOob);
+    }
   }
   // 2. the wave's weights: tile w/4, chunks [q*CPW, (q+1)*CPW) of quarter q
   const int tt = wave / kQW, q = wave - tt * kQW;
@@ -583,6 +770,18 @@ __global__ __launch_bounds__(64 * kQW * kQT) void i8_rows_q_kernel(I8Args args) 
 #pragma unroll
   for (int u = 0; u < CPW; ++u) bv[u] = buf_load16(rb, has_tile ? off + 64u * u : kOob);
   __builtin_amdgcn_sched_barrier(0);  // every load above ahead of the arithmetic
+  if constexpr (XT >= 0) {
+    // one launch: the activation tile once the rows are written
+    a8_wait_rows<XT>(args, &sflag, sred);
+#pragma unroll
+    for (int i = 0; i < kQXP; ++i) {
+      const int p = tid + i * NT;
+      const int row = p / npr, pc = p - row * npr;
+      xr[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              ra, (int)(p < np && row < M ? (uint32_t)(row * K + 16 * pc) : kOob),
+                                              0, kSc1));
+    }
+  }
 
   // 3. activations to LDS
 #pragma unroll
@@ -607,16 +806,23 @@ __global__ __launch_bounds__(64 * kQW * kQT) void i8_rows_q_kernel(I8Args args) 
   // 5. quarters 1..3 to LDS, quarter 0 adds them and writes the tile
   if (has_tile && q > 0) red[(tt * (kQW - 1) + q - 1) * 64 + lane] = acc;
   __syncthreads();
-  if (!has_tile || q != 0) return;
+  if (has_tile && q == 0) {
 #pragma unroll
-  for (int w = 0; w < kQW - 1; ++w) acc += red[(tt * (kQW - 1) + w) * 64 + lane];
-  // lane (grp, n16) holds token rows 4grp .. 4grp+3 of weight row n0 + n16
-  const int nn = n0 + n16;
+    for (int w = 0; w < kQW - 1; ++w) acc += red[(tt * (kQW - 1) + w) * 64 + lane];
+    // lane (grp, n16) holds token rows 4grp .. 4grp+3 of weight row n0 + n16
+    const int nn = n0 + n16;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * grp + r;
-    if (m < M && nn < N) i8_store(args, m, nn, acc[r]);
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * grp + r;
+      if (m < M && nn < N) {
+        if constexpr (XT < 0)
+          i8_store(args, m, nn, acc[r]);
+        else
+          i8_store_sync(args, m, nn, acc[r]);
+      }
+    }
   }
+  if constexpr (XT >= 0) a8_done(args);
 }
 
 struct RowsQPlan {
@@ -628,7 +834,7 @@ struct RowsQPlan {
 // At least two row tiles per workgroup slot (2 per CU), whole 256-k quarter
 // chunks of 4..12 64-k chunks (K = 1024 .. 3072 in steps of 512), the
 // activation tile within the staging budget.
-static RowsQPlan plan_rows_q(int64_t M, int64_t N, int64_t K) {
+static RowsQPlan plan_rows_q(int64_t M, int64_t N, int64_t K, int np = 0) {
   RowsQPlan p{};
   if (env_int("SPARKQ_I8_NO_ROWSQ", 0) || M < 1 || M > 16 || K % 256 != 0) return p;
   const int64_t cpw = K / 256;
@@ -636,24 +842,24 @@ static RowsQPlan plan_rows_q(int64_t M, int64_t N, int64_t K) {
   const int64_t T = cdiv(N, 16), P = 2 * device_cus();
   if (T < 2 * P || K > kQXP * 64 * kQW * kQT) return p;  // one staging pass: K pieces
   if (N * K >= (int64_t)kOob || M * K >= (int64_t)kOob) return p;
-  p.wgs = (int)std::max<int64_t>(P, cdiv(T, kQT));
+  // (with producer workgroups in the grid, as many fewer tile workgroups)
+  p.wgs = (int)std::max<int64_t>(P - np, cdiv(T, kQT));
   p.cpw = (int)cpw;
   p.lds = (size_t)16 * rows_q_pitch((int)K) + (size_t)kQT * (kQW - 1) * 64 * 16;
   p.ok = p.lds <= 65536;
   return p;
 }
 
-static int launch_rows_q(I8Args args, const RowsQPlan& p, hipStream_t st) {
-  args.wgs = p.wgs;
-  const dim3 grid((unsigned)p.wgs), block(64 * kQW * kQT);
+template <int XT>
+static void launch_rows_q_x(const I8Args& args, const RowsQPlan& p, hipStream_t st) {
+  const dim3 grid((unsigned)(p.wgs + args.np)), block(64 * kQW * kQT);
   switch (p.cpw) {
-    case 4: hipLaunchKernelGGL(i8_rows_q_kernel<4>, grid, block, p.lds, st, args); break;
-    case 6: hipLaunchKernelGGL(i8_rows_q_kernel<6>, grid, block, p.lds, st, args); break;
-    case 8: hipLaunchKernelGGL(i8_rows_q_kernel<8>, grid, block, p.lds, st, args); break;
-    case 10: hipLaunchKernelGGL(i8_rows_q_kernel<10>, grid, block, p.lds, st, args); break;
-    default: hipLaunchKernelGGL(i8_rows_q_kernel<12>, grid, block, p.lds, st, args); break;
+    case 4: hipLaunchKernelGGL((i8_rows_q_kernel<4, XT>), grid, block, p.lds, st, args); break;
+    case 6: hipLaunchKernelGGL((i8_rows_q_kernel<6, XT>), grid, block, p.lds, st, args); break;
+    case 8: hipLaunchKernelGGL((i8_rows_q_kernel<8, XT>), grid, block, p.lds, st, args); break;
+    case 10: hipLaunchKernelGGL((i8_rows_q_kernel<10, XT>), grid, block, p.lds, st, args); break;
+    default: hipLaunchKernelGGL((i8_rows_q_kernel<12, XT>), grid, block, p.lds, st, args); break;
   }
-  return check_launch("i8_rows_q_kernel");
 }
 
 // 3..16 rows (1..16 with the decode GEMV switched off), whole 64-k chunks
@@ -662,33 +868,69 @@ static bool use_rows(int64_t M, int64_t N, int64_t K) {
          !env_int("SPARKQ_I8_NO_ROWS", 0);
 }
 
-template <int RW>
+template <int RW, int XT>
 static void launch_rows_w(int rpd, const I8Args& args, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(args.N, 16)), block(64 * RW);
+  const dim3 grid((unsigned)(cdiv(args.N, 16) + args.np)), block(64 * RW);
   if (rpd == 10)
-    hipLaunchKernelGGL((i8_rows_kernel<RW, 10>), grid, block, 0, st, args);
+    hipLaunchKernelGGL((i8_rows_kernel<RW, 10, XT>), grid, block, 0, st, args);
   else
-    hipLaunchKernelGGL((i8_rows_kernel<RW, 8>), grid, block, 0, st, args);
+    hipLaunchKernelGGL((i8_rows_kernel<RW, 8, XT>), grid, block, 0, st, args);
+}
+
+template <int XT>
+static void launch_rows_x(const I8Args& args, hipStream_t st) {
+  const bool long_rows = args.K / 64 > 64;
+  const int rw = env_int("SPARKQ_I8_ROWS_RW", long_rows ? 16 : 8);
+  const int rpd = env_int("SPARKQ_I8_ROWS_RPD", long_rows ? 10 : 8);
+  if (rw == 4)
+    launch_rows_w<4, XT>(rpd, args, st);
+  else if (rw == 16)
+    launch_rows_w<16, XT>(rpd, args, st);
+  else
+    launch_rows_w<8, XT>(rpd, args, st);
 }
 
 // Rows of more than 64 chunks (K > 4096) take 16 waves with ten chunks in
 // flight each, so that a wave's share of K is one batch of loads (down
 // 2560 x 9728: 16.0 -> 15.0 us at M = 8, 18.2 -> 17.2 at M = 16); shorter
 // rows keep 8 waves of up to eight chunks (4 waves of ten, 16 of eight or
-// ten measured slower on QKV and gate+up).
-static int launch_rows(const I8Args& args, hipStream_t st) {
-  const RowsQPlan qp = plan_rows_q(args.M, args.N, args.K);
-  if (qp.ok) return launch_rows_q(args, qp, st);
-  const bool long_rows = args.K / 64 > 64;
-  const int rw = env_int("SPARKQ_I8_ROWS_RW", long_rows ? 16 : 8);
-  const int rpd = env_int("SPARKQ_I8_ROWS_RPD", long_rows ? 10 : 8);
-  if (rw == 4)
-    launch_rows_w<4>(rpd, args, st);
-  else if (rw == 16)
-    launch_rows_w<16>(rpd, args, st);
+// ten measured slower on QKV and gate+up). xt: -1 = the int8 rows are in
+// args.a, 0 / 1 = one launch quantizing bf16 / fp16 args.x (args.np
+// producer workgroups, counters and int8 buffer in args).
+static int launch_rows(const I8Args& args, int xt, hipStream_t st) {
+  const RowsQPlan qp = plan_rows_q(args.M, args.N, args.K, args.np);
+  if (qp.ok) {
+    I8Args a = args;
+    a.wgs = qp.wgs;
+    if (xt == 0)
+      launch_rows_q_x<0>(a, qp, st);
+    else if (xt == 1)
+      launch_rows_q_x<1>(a, qp, st);
+    else
+      launch_rows_q_x<-1>(a, qp, st);
+    return check_launch("i8_rows_q_kernel");
+  }
+  if (xt == 0)
+    launch_rows_x<0>(args, st);
+  else if (xt == 1)
+    launch_rows_x<1>(args, st);
   else
-    launch_rows_w<8>(rpd, args, st);
+    launch_rows_x<-1>(args, st);
   return check_launch("i8_rows_kernel");
+}
+
+// One launch with the quantizer for 16-bit activations whose rows fit one
+// producer pass (K/8 16-byte pieces over the smallest rows workgroup of 512
+// threads), for rows longer than 4096 k. Measured against the quantizer
+// launch followed by the int8 kernel (36 weight sets per graph replay):
+// down 2560 x 9728 at M = 3 / 8 / 16 14.4 -> 12.2, 15.7 -> 14.2, 17.3 ->
+// 17.4 us; QKV 3584 x 2560 8.2 -> 9.2, 8.9 -> 10.4, 9.5 -> 11.7 us and
+// gate+up 17.0 -> 17.6, 17.8 -> 18.5, 18.8 -> 19.9 us, where the wait for
+// the rows (a poll after the wave's weight loads, then the activation loads)
+// costs more than the launch it saves.
+static bool use_rows_sync(int64_t M, int64_t K, int xdt) {
+  return (xdt == SPARKQ_BF16 || xdt == SPARKQ_F16) && M >= 1 && K / 8 <= (int64_t)kA8PP * 512 &&
+         (K > 4096 || env_int("SPARKQ_I8_SYNCQ_ALL", 0)) && !env_int("SPARKQ_I8_NO_SYNCQ", 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -875,7 +1117,7 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
     r.N = (int)N;
     r.K = (int)K;
     r.mode = kOutRaw;
-    return launch_rows(r, st);
+    return launch_rows(r, -1, st);
   }
   const I8Plan p = plan_i8(M, N, K);
   const size_t need = p.counter_bytes + p.part_bytes;
@@ -932,6 +1174,27 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
   float* sa = reinterpret_cast<float*>(base + kCounterBytes + round_up((size_t)M * K, 256));
   int32_t* part = reinterpret_cast<int32_t*>(base + kCounterBytes + round_up((size_t)M * K, 256) +
                                              round_up((size_t)M * 4, 256));
+  if (use_rows(M, N, K) && use_rows_sync(M, K, xdt)) {
+    I8Args r{};
+    r.a = q;
+    r.b = w;
+    r.sa = sa;
+    r.sw = wsc;
+    r.bias = bias;
+    r.bias_dtype = bias_dtype;
+    r.y = y;
+    r.y_dtype = ydt;
+    r.M = (int)M;
+    r.N = (int)N;
+    r.K = (int)K;
+    r.mode = kOutEpilogue;
+    r.counters = reinterpret_cast<unsigned*>(base);
+    r.x = x;
+    r.xt = xdt == SPARKQ_BF16 ? 0 : 1;
+    r.np = (int)M;
+    r.spin = env_int("SPARKQ_I8_SELF_QUANTIZE", 0) ? 0 : 4000;
+    return launch_rows(r, r.xt, st);
+  }
   if (int rc = a8_quantize(x, q, sa, M, K, xdt, st)) return rc;
   if (use_rows(M, N, K)) {
     I8Args r{};
@@ -947,7 +1210,7 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
     r.N = (int)N;
     r.K = (int)K;
     r.mode = kOutEpilogue;
-    return launch_rows(r, st);
+    return launch_rows(r, -1, st);
   }
   const I8Plan p = plan_i8(M, N, K);
   I8Args args{};

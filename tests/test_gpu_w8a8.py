@@ -118,6 +118,35 @@ def test_w8a8_linear_rows_one_round(gpu, m, n, k, dtype, with_bias, monkeypatch)
     assert torch.equal(y16, sparkq.w8a8_linear(xt, wt, st, bias=bt))
 
 
+@pytest.mark.parametrize("m,n,k,dtype", [(8, 3584, 2560, o.BF16), (16, 19456, 2560, o.BF16), (5, 2560, 9728, o.F16),
+                                         (3, 100, 512, o.BF16), (16, 17, 2560, o.F16), (12, 1000, 16384, o.BF16)])
+def test_w8a8_one_launch_quantizer(gpu, m, n, k, dtype, monkeypatch):
+    """3..16 rows in one launch (producer workgroups quantize the rows while
+    the others stream their weights): equal to the quantizer launch followed
+    by the int8 kernel, on consecutive calls with different activations (the
+    ready counter is left zero between calls), with the workgroups'
+    self-quantizing fallback forced, and bit for bit against the oracle on
+    sampled columns."""
+    import sparkq
+
+    monkeypatch.setenv("SPARKQ_I8_SYNCQ_ALL", "1")  # every row length, not only K > 4096
+    wq, wsc = _w8(n, k, seed=m + 1)
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    xs = [_x(m, k, dtype, seed=s) for s in (n, n + 1)]
+    xts = [up16(x, dtype, gpu) for x in xs]
+    one = [sparkq.w8a8_linear(xt, wt, st, out_dtype=torch.float32) for xt in (xts[0], xts[1], xts[0])]
+    monkeypatch.setenv("SPARKQ_I8_SELF_QUANTIZE", "1")
+    own = [sparkq.w8a8_linear(xt, wt, st, out_dtype=torch.float32) for xt in xts]
+    monkeypatch.setenv("SPARKQ_I8_NO_SYNCQ", "1")
+    two = [sparkq.w8a8_linear(xt, wt, st, out_dtype=torch.float32) for xt in xts]
+    assert torch.equal(one[0], two[0]) and torch.equal(one[1], two[1]) and torch.equal(one[2], two[0])
+    assert torch.equal(own[0], two[0]) and torch.equal(own[1], two[1])
+    cols = np.sort(np.random.default_rng(n).choice(n, min(n, 256), replace=False))
+    qa, sa = o.a8_quantize(o.bits_to_f32(xs[1], dtype))
+    ref = o.w8a8_epilogue(o.int8_matmul(qa, wq[cols]), sa, wsc[cols])
+    assert np.array_equal(one[1].cpu().numpy()[:, cols].view(np.uint32), ref.view(np.uint32))
+
+
 def test_int8_matmul_extreme_range(gpu):
     import sparkq
 
