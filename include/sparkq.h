@@ -162,9 +162,12 @@ int sparkq_int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c,
                            int64_t M, int64_t N, int64_t K, void* workspace,
                            size_t workspace_bytes, void* stream);
 
-/* Workspace for sparkq_w8a8_linear: split-K tile counters (first 16384
- * bytes, zero before the first call and left zero by every call), the int8
- * activations, their fp32 scales and any split-K int32 partials. */
+/* Workspace for sparkq_w8a8_linear: counters (first 16384 bytes, zero
+ * before the first call and left zero by every call: split-K tile counters,
+ * or the rows-ready and workgroups-done counts of the one-launch quantizer
+ * for 3..16 rows with K > 4096), the int8 activations, their fp32 scales and
+ * any split-K int32 partials. Calls that share a workspace must be ordered
+ * (one stream). */
 size_t sparkq_w8a8_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* y[m,n] = to_dtype(fmaf(float(acc[m,n]) * sa[m], sw[n], bias[n])) with acc
