@@ -286,13 +286,13 @@ __device__ __forceinline__ f32x4_t mfma16x16x32_f16(u32x4_t a, u32x4_t b, f32x4_
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-template <int D>
+template <int D, int NW = 4>  // NW waves per workgroup
 struct SdpaMfmaLds {
   static constexpr int VROW = D + 16;                 // padded token row of the V copy
   static constexpr int VT = 32 * VROW;                // one wave's V block
   static constexpr int PT = 2 * 16 * 32 * 2;          // one wave's P strips (hi, lo) [16 heads][32 tokens] fp16
-  static constexpr int LOOP = 4 * (VT + PT);
-  static constexpr int MERGE = 4 * 8 * 4 * 2 + 4 * 8 * D * 4;
+  static constexpr int LOOP = NW * (VT + PT);
+  static constexpr int MERGE = NW * 8 * 4 * 2 + NW * 8 * D * 4;
   static constexpr int BYTES = LOOP > MERGE ? LOOP : MERGE;
 };
 
@@ -301,14 +301,14 @@ struct SdpaMfmaLds {
 // maximum over the splits, the split weights and the normalizer (one wave
 // per head), then each output as the weighted sum of the partial outputs in
 // split order, eight loads in flight. sm holds GQA*S + GQA floats.
-template <int D, int GQA>
+template <int D, int GQA, int NT = 256>
 __device__ void sdpa_fold_merge(const SdpaArgs& a, int b, int kh, float* sm) {
   const int S = a.S, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float* wts = sm;             // [GQA][S]
   float* zs = sm + GQA * S;    // [GQA]
   // the maxima and sums of a head's splits are loaded together (one round
   // trip for up to 64 splits)
-  for (int h = wave; h < GQA; h += 4) {
+  for (int h = wave; h < GQA; h += NT / 64) {
     const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
     float mm = kNegInf, z = 0.0f;
     if (S <= 64) {
@@ -339,13 +339,13 @@ __device__ void sdpa_fold_merge(const SdpaArgs& a, int b, int kh, float* sm) {
   __syncthreads();
   // each thread's outputs (e = tid + 256 k) summed over the splits in split
   // order, the loads of all its outputs for eight splits in flight together
-  constexpr int E = GQA * D, EPT = (E + 255) / 256;
+  constexpr int E = GQA * D, EPT = (E + NT - 1) / NT;
   float o[EPT];
   const float* p[EPT];
   const float* w[EPT];
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
-    const int e = min(tid + 256 * k, E - 1), h = e / D, d = e - h * D;
+    const int e = min(tid + NT * k, E - 1), h = e / D, d = e - h * D;
     const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
     o[k] = 0.0f;
     p[k] = a.pacc + bh * S * D + d;
@@ -368,7 +368,7 @@ __device__ void sdpa_fold_merge(const SdpaArgs& a, int b, int kh, float* sm) {
     for (int k = 0; k < EPT; ++k) o[k] = fmaf(splitk_load(p[k] + (int64_t)s * D), w[k][s], o[k]);
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
-    const int e = tid + 256 * k;
+    const int e = tid + NT * k;
     if (e < E) {
       const int h = e / D, d = e - h * D;
       const int64_t bh = (int64_t)b * a.Hq + kh * GQA + h;
@@ -377,13 +377,14 @@ __device__ void sdpa_fold_merge(const SdpaArgs& a, int b, int kh, float* sm) {
   }
 }
 
-template <int D, int GQA>
-__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaArgs a) {
+// NW waves per workgroup: 4, or 8 for grids of at most one workgroup per CU
+template <int D, int GQA, int NW = 4>
+__global__ __launch_bounds__(64 * NW, (D == 256 || NW == 8) ? 1 : 2) void sdpa_mfma_kernel(SdpaArgs a) {
   constexpr int NC = D / 32;   // k chunks of QK
   constexpr int PL = D / 64;   // 16-byte K pieces per lane per 16-token group
   constexpr int NJ = D / 16;   // 16-dim column groups of PV
   constexpr int VL = D / 32;   // 16-byte V pieces per lane per block
-  using L = SdpaMfmaLds<D>;
+  using L = SdpaMfmaLds<D, NW>;
   __shared__ __attribute__((aligned(16))) unsigned char smem[L::BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -394,7 +395,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
   const int t_begin = split * a.tps;
   const int t_end = min(a.N, t_begin + a.tps);
   unsigned char* vtile = smem + wave * L::VT;
-  uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + 4 * L::VT + wave * L::PT);
+  uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + NW * L::VT + wave * L::PT);
 
   // query operand: lane (head n16, k quarter grp); chunk c covers dims
   // 16*(grp + 4*(c/2)) + 8*(c%2) .. +8, matching the K piece order below
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int stride = 4 * 32;
+  const int stride = NW * 32;
   // The block's registers are read in place and refilled with the block two
   // ahead once the QK product and the scales have been taken from them, so
   // no register copy waits on the loads still in flight.
@@ -589,9 +590,9 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
 
   // combine the waves through LDS (the loop's LDS is free after the barrier)
   __syncthreads();
-  float* wm = reinterpret_cast<float*>(smem);            // [4][8]
-  float* wz = wm + 32;                                   // [4][8]
-  float* wacc = wz + 32;                                 // [4][8][D]
+  float* wm = reinterpret_cast<float*>(smem);            // [NW][8]
+  float* wz = wm + NW * 8;                               // [NW][8]
+  float* wacc = wz + NW * 8;                             // [NW][8][D]
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int h = 4 * grp + r;
@@ -605,14 +606,14 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
     }
   }
   __syncthreads();
-  for (int e = tid; e < GQA * D; e += 256) {
+  for (int e = tid; e < GQA * D; e += 64 * NW) {
     const int h = e / D, d = e - h * D;
     float mm = kNegInf;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) mm = fmaxf(mm, wm[w * 8 + h]);
+    for (int w = 0; w < NW; ++w) mm = fmaxf(mm, wm[w * 8 + h]);
     float z = 0.0f, o = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float wt = exp2_guarded(wm[w * 8 + h] - mm, wm[w * 8 + h] != kNegInf);
       z = fmaf(wz[w * 8 + h], wt, z);
       o = fmaf(wacc[(w * 8 + h) * D + d], wt, o);
@@ -638,7 +639,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_mfma_kernel(SdpaAr
     __shared__ int s_last;
     if (splitk_arrive(a.counters + blockIdx.y, a.S, &s_last)) {
       __syncthreads();  // the combine above is done with the LDS it reused
-      sdpa_fold_merge<D, GQA>(a, b, kh, reinterpret_cast<float*>(smem));
+      sdpa_fold_merge<D, GQA, 64 * NW>(a, b, kh, reinterpret_cast<float*>(smem));
       splitk_reset(a.counters + blockIdx.y);
     }
   }
@@ -1574,14 +1575,28 @@ static void launch_decode_d(const SdpaArgs& a, int gqa, int fmt, dim3 grid, hipS
   }
 }
 
+template <int D, int NW>
+static void launch_mfma_w(const SdpaArgs& a, int gqa, dim3 grid, hipStream_t st) {
+  const dim3 block(64 * NW);
+  switch (gqa) {
+    case 1: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 1, NW>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 2, NW>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 4, NW>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 8, NW>), grid, block, 0, st, a); break;
+  }
+}
 template <int D>
 static void launch_mfma_d(const SdpaArgs& a, int gqa, dim3 grid, hipStream_t st) {
-  switch (gqa) {
-    case 1: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 1>), grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 2>), grid, dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 4>), grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((sdpa_mfma_kernel<D, 8>), grid, dim3(256), 0, st, a); break;
+  if constexpr (D <= 128) {
+    // eight waves when the grid fills at most half the CUs (each wave then
+    // has half the blocks): B=1 N=4096 (128 workgroups) 11.0 -> 10.2 us; at
+    // one workgroup per CU (B=1 N=32768) no gain
+    if (2 * (int64_t)grid.x * grid.y <= device_cus() && env_int("SPARKQ_SDPA_NW8", 1)) {
+      launch_mfma_w<D, 8>(a, gqa, grid, st);
+      return;
+    }
   }
+  launch_mfma_w<D, 4>(a, gqa, grid, st);
 }
 
 int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void* kb,
