@@ -2,7 +2,9 @@
 // per-channel int8 weights, exact int32 accumulation on the int8 MFMA.
 //
 // Kernels
-//   i8_gemv_kernel       M <= 2 decode (M <= 4 when K % 64 != 0): whole
+//   i8_gemv_kernel       M <= 2 decode (M <= 4 when K % 64 != 0; 16-bit
+//                        activations up to K = 4096, longer rows go to the
+//                        rows kernel's one launch): whole
 //                        rows per workgroup, 4 rows x
 //                        256 bytes per load, v_dot4_i32_i8, activation
 //                        quantizer fused (one launch per projection)
@@ -963,6 +965,13 @@ static I8GemvPlan plan_i8_gemv(int64_t M, int64_t N, int64_t K, int esize) {
   const int64_t maxm = K % 64 == 0 ? std::min<int64_t>(env_int("SPARKQ_I8_GEMV_MAXM", 2), 4) : 4;
   if (M > maxm || env_int("SPARKQ_I8_NO_GEMV", 0)) return p;
   if (N * K >= (int64_t)kOob || M * K * esize >= (int64_t)kOob) return p;
+  // 16-bit activations over rows longer than 4096 k take the rows kernel
+  // with its producer workgroups instead (down 2560 x 9728 at M = 1: 11.5
+  // -> 11.1 us; the same at M = 2), where every workgroup here would
+  // quantize the whole long row itself
+  if (esize == 2 && K > 4096 && K % 64 == 0 && K / 8 <= (int64_t)kA8PP * 512 &&
+      !env_int("SPARKQ_I8_NO_SYNCQ", 0))
+    return p;
   const int64_t U = cdiv(K, 256);
   if (U <= 10)
     p.SG = 1;
