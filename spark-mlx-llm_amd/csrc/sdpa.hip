@@ -1591,7 +1591,7 @@ static void launch_mfma_d(const SdpaArgs& a, int gqa, dim3 grid, hipStream_t st)
     // eight waves when the grid fills at most half the CUs (each wave then
     // has half the blocks): B=1 N=4096 (128 workgroups) 11.0 -> 10.2 us; at
     // one workgroup per CU (B=1 N=32768) no gain
-    if (2 * (int64_t)grid.x * grid.y <= device_cus() && env_int("SPARKQ_SDPA_NW8", 1)) {
+    if (2 * (int64_t)grid.x * grid.y <= device_cus() && !env_int("SPARKQ_SDPA_NO_NW8", 0)) {
       launch_mfma_w<D, 8>(a, gqa, grid, st);
       return;
     }

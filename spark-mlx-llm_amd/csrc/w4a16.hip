@@ -926,6 +926,7 @@ struct DecodeStreamArgs {
   int P;   // workgroups
   int QW;  // row quads of the largest workgroup
   const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
+  int RR;  // 1: workgroup i owns rows [i*N/P, (i+1)*N/P) (quads from its first row)
 };
 
 constexpr int kDecNW = 16;  // waves per workgroup
@@ -964,8 +965,16 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
   const int U = (RB + 255) >> 8;     // spans per row
   const int ng = K / G;              // groups per row
   const int np = K >> 5;             // 32-k pieces per row
-  const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
-  const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
+  // the workgroup's rows [r0, r1), taken as row quads from r0
+  int r0, r1;
+  if (a.RR) {
+    r0 = (int)((int64_t)blockIdx.x * N / a.P);
+    r1 = (int)((int64_t)(blockIdx.x + 1) * N / a.P);
+  } else {
+    r0 = 4 * (int)((int64_t)blockIdx.x * a.nq / a.P);
+    r1 = min(N, 4 * (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P));
+  }
+  const int nql = (r1 - r0 + 3) >> 2;
   const int nitems = nql * U;
   const int i0 = (int)((int64_t)wave * nitems / kDecNW);
   const int nmy = (int)((int64_t)(wave + 1) * nitems / kDecNW) - i0;
@@ -994,7 +1003,7 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
   for (int i = 0; i < kDecSP; ++i) {
     const int pi = tid + i * NT;
     if (i * NT + 64 * wave < nsp) {
-      const uint32_t off = pi < nsp ? 8u * (uint32_t)qa * ng + 16u * pi : kOob;
+      const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
       sr[i] = buf_load16(rs, off);
       br[i] = buf_load16(rb, off);
     }
@@ -1008,8 +1017,8 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
     const int it = i0 + i;
     ql[i] = it / U;
     sp[i] = it - ql[i] * U;
-    const int row = 4 * (qa + ql[i]) + j, p = 256 * sp[i] + 16 * b;
-    const bool ok = i < nmy && (FULL || (row < N && p + 16 <= RB));
+    const int row = r0 + 4 * ql[i] + j, p = 256 * sp[i] + 16 * b;
+    const bool ok = i < nmy && row < r1 && (FULL || p + 16 <= RB);
     wv[i] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
   }
 
@@ -1077,7 +1086,7 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
     if (i < nmy) {
       const int s = sp[i];
       const int p = 256 * s + 16 * b;
-      const bool ok = FULL || (4 * (qa + ql[i]) + j < N && p + 16 <= RB);
+      const bool ok = r0 + 4 * ql[i] + j < r1 && (FULL || p + 16 <= RB);
       const int piece = FULL ? 16 * s + b : min(16 * s + b, np - 1);
       // pieces past the row end carry zero codes and unrelated activations
       const uint32_t pair = ok ? sb[(4 * ql[i] + j) * ng + (2 * p) / G] : 0u;
@@ -1125,8 +1134,8 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
   // 5. each output: the sum of its quad's slots in span order
   for (int t = tid; t < 4 * nql * M; t += NT) {
     const int rl = t / M, m = t - rl * M;
-    const int row = 4 * qa + rl;
-    if (row < N) {
+    const int row = r0 + rl;
+    if (row < r1) {
       const float* src = part + (((rl >> 2) * U) * 4 + (rl & 3)) * MR + m;
       float v = 0.0f;
       for (int s = 0; s < U; ++s) v += src[s * 4 * MR];
@@ -2407,7 +2416,7 @@ static StreamPlan plan_stream(int64_t M, int64_t N, int64_t K, int G) {
   // (scale, bias) rows of any first row start on a 16-byte boundary: down
   // 6.2-6.4 -> 5.9 us, bit-identical. The one-round kernel of the 5-span rows
   // (gate+up, QKV) showed no gain from the same split.
-  p.RR = env_int("SPARKQ_W4_STREAM_ROWS", 1) && ng % 8 == 0 && N >= 4 * (int64_t)p.P;
+  p.RR = !env_int("SPARKQ_W4_STREAM_QUADS", 0) && ng % 8 == 0 && N >= 4 * (int64_t)p.P;
   if (p.RR) p.QW = (int)cdiv(cdiv(N, p.P), 4);
   const int64_t ni = cdiv(p.QW * U, p.NW);
   if (ni > 8) return p;
@@ -2463,7 +2472,7 @@ static void launch_stream(const StreamPlan& p, int G, const GemvStreamArgs& a, h
 // (whole spans and row quads); LDS up to 160 KB.
 struct DecPlan {
   bool ok;
-  int P, QW, MQ, NI;
+  int P, QW, MQ, NI, RR;
   size_t lds;
 };
 
@@ -2485,6 +2494,12 @@ static DecPlan plan_dec(int64_t M, int64_t N, int64_t K, int G) {
   const int64_t nq = N / 4, U = K / 512;
   p.P = (int)std::min<int64_t>(nq, device_cus());
   p.QW = (int)cdiv(nq, p.P);
+  // equal row ranges (not whole quads) per workgroup, as in the M = 1
+  // streaming kernel; measured within noise here (down 2560x9728 M = 2:
+  // 7.3-7.7 us with whole quads, 7.3 us with ranges; M = 4 and 8 equal), as
+  // every workgroup still issues whole quads of items
+  p.RR = !env_int("SPARKQ_W4_DEC_QUADS", 0) && ng % 8 == 0;
+  if (p.RR) p.QW = (int)cdiv(cdiv(N, p.P), 4);
   p.MQ = (int)cdiv(M, 4);
   const int64_t ni = cdiv(p.QW * U, kDecNW);
   if (ni > 8) return p;
@@ -2824,6 +2839,7 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     a.nq = (int)(N / 4);
     a.P = dp.P;
     a.QW = dp.QW;
+    a.RR = dp.RR;
     a.res = (const uint16_t*)res;
     if (res_done) *res_done = res != nullptr;
     if (xdt == SPARKQ_BF16)

@@ -170,15 +170,19 @@ def test_decode_long_rows(gpu, n, k, g):
         check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
 
 
+@pytest.mark.parametrize("quads", ["0", "1"])
 @pytest.mark.parametrize("m,n,k,g", [(3, 1100, 4096, 64), (5, 1100, 3072, 32), (12, 260, 1536, 128),
-                                     (16, 1028, 2048, 64), (2, 8, 9728, 64)])
-def test_decode_multirow_stream(gpu, m, n, k, g, monkeypatch):
+                                     (16, 1028, 2048, 64), (2, 8, 9728, 64), (4, 2600, 9728, 64)])
+def test_decode_multirow_stream(gpu, m, n, k, g, quads, monkeypatch):
     """2 <= M <= 16 on the multi-row streaming kernel (the 16x16x32 kernel
     switched off): more row quads than CUs (uneven split), fewer, a row-quad
     count below the wave count, M not a multiple of 4 (the last row quartet
-    repeats row M-1) and long rows."""
+    repeats row M-1) and long rows; each with equal row ranges per workgroup
+    (groups per row a multiple of 8; the ranges need not be whole quads) and
+    with whole row quads."""
     monkeypatch.setenv("SPARKQ_W4_NO_MR", "1")
     monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
+    monkeypatch.setenv("SPARKQ_W4_DEC_QUADS", quads)
     x, wq, s, b = w4_problem(m, n, k, g, seed=m * n)
     ref = o.w4a16_matmul(x, wq, s, b, g)
     y32 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32).cpu().numpy()
