@@ -1461,6 +1461,12 @@ __device__ __forceinline__ float block_max256(float v, float* red) {
 // maximum reduced by four threads, and the outputs written coalesced: the
 // fp16 scales straight from the pair index, the bias slots through LDS as
 // whole 4-byte slot pairs.
+// NCH > 0: the activation row's 16-byte chunks (at most 256 * NCH) are all
+// loaded at once and kept in registers for the conversion; NCH = 0 loops
+// over the row twice (the second pass from L2). Measured per call, prologue
+// and GEMM, against the two passes: QKV 3584x2560 M = 512 33.5 -> 32.6 us,
+// down 2560x9728 M = 2048 163 -> 161.5 us, the other shapes within 0.5%.
+template <int NCH>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* red = reinterpret_cast<float*>(smem);
@@ -1471,13 +1477,31 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
     const int m = blockIdx.x - nwb;
     const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(a.x + (int64_t)m * a.K);
     const int nc = a.K / 8;
+    constexpr int NR = NCH > 0 ? NCH : 1;
+    u32x4_t xv[NR];
     float amax = 0.0f;
-    for (int c = tid; c < nc; c += 256) {
-      const u32x4_t v = xr[c];
+    if constexpr (NCH > 0) {
+      // every load unconditional (past the row: the out-of-range offset reads zeros)
+      const rsrc_t rx = make_rsrc(a.x + (int64_t)m * a.K, (uint32_t)a.K * 2u);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32((uint16_t)v[e])),
-                                 fabsf(bf16_to_f32((uint16_t)(v[e] >> 16)))));
+      for (int i = 0; i < NCH; ++i) {
+        const int c = tid + 256 * i;
+        xv[i] = buf_load16(rx, c < nc ? 16u * (uint32_t)c : kOob);
+      }
+#pragma unroll
+      for (int i = 0; i < NCH; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32((uint16_t)xv[i][e])),
+                                   fabsf(bf16_to_f32((uint16_t)(xv[i][e] >> 16)))));
+    } else {
+      for (int c = tid; c < nc; c += 256) {
+        const u32x4_t v = xr[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32((uint16_t)v[e])),
+                                   fabsf(bf16_to_f32((uint16_t)(v[e] >> 16)))));
+      }
     }
     const int e = row_shift(block_max256(amax, red), 15);
     if (tid == 0) a.ex[m] = e;
@@ -1485,8 +1509,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
     uint16_t* a2 = a.a2 + (int64_t)m * a.K2p;
     const int cpg = a.G / 8;  // chunks per group: 4, 8 or 16 consecutive lanes
     // (256 and nc are multiples of cpg: the lanes of a group are active together)
-    for (int c = tid; c < nc; c += 256) {
-      const u32x4_t v = xr[c];
+    auto convert = [&](int c, const u32x4_t v) {
       float f[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1509,6 +1532,15 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
         a2[3 * g + 1] = hi;
         a2[3 * g + 2] = lo;
       }
+    };
+    if constexpr (NCH > 0) {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int c = tid + 256 * i;
+        if (c < nc) convert(c, xv[i]);
+      }
+    } else {
+      for (int c = tid; c < nc; c += 256) convert(c, xr[c]);
     }
     for (int sl = 3 * ng + tid; sl < a.K2p; sl += 256) a2[sl] = 0;
     return;
@@ -2725,7 +2757,19 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   p.K2p = bias_slots(K, G);
   const PrepPlan pp = plan_prep(K, G);
   p.rw = pp.rw;
-  hipLaunchKernelGGL(gemm_prep_kernel, dim3((unsigned)(M + cdiv(N, pp.rw))), dim3(256), pp.lds, st, p);
+  // the activation row in registers up to 2048 chunks of 16 bytes (K <= 16384)
+  const int64_t nch = env_int("SPARKQ_PREP_NO_REG", 0) ? 0 : cdiv(K / 8, 256);
+  const dim3 pg((unsigned)(M + cdiv(N, pp.rw)));
+  if (nch == 1)
+    hipLaunchKernelGGL(gemm_prep_kernel<1>, pg, dim3(256), pp.lds, st, p);
+  else if (nch == 2)
+    hipLaunchKernelGGL(gemm_prep_kernel<2>, pg, dim3(256), pp.lds, st, p);
+  else if (nch >= 3 && nch <= 4)
+    hipLaunchKernelGGL(gemm_prep_kernel<4>, pg, dim3(256), pp.lds, st, p);
+  else if (nch >= 5 && nch <= 8)
+    hipLaunchKernelGGL(gemm_prep_kernel<8>, pg, dim3(256), pp.lds, st, p);
+  else
+    hipLaunchKernelGGL(gemm_prep_kernel<0>, pg, dim3(256), pp.lds, st, p);
   GemmX16Args a{};
   a.xh = p.xh;
   a.w = w;

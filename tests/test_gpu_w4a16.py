@@ -120,6 +120,23 @@ def test_gemm_split_k(gpu, m, n, k, g):
     assert torch.equal(y32, _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32))
 
 
+@pytest.mark.parametrize("m,n,k,g", [(40, 96, 2048, 64), (33, 64, 2560, 32), (48, 40, 9728, 64),
+                                     (36, 32, 16384, 128), (34, 16, 16896, 64)])
+def test_gemm_prologue_row_paths(gpu, m, n, k, g, monkeypatch):
+    """The prologue keeps an activation row in registers up to K = 16384 (one,
+    two, four or eight 16-byte chunks per thread, the last ones past the row
+    end) and loops over longer rows; both paths give the same bits, and match
+    the oracle."""
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m + n + k)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    outs = {}
+    for no_reg in ("0", "1"):
+        monkeypatch.setenv("SPARKQ_PREP_NO_REG", no_reg)
+        outs[no_reg] = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+        check_fp32(outs[no_reg].cpu().numpy(), ref)
+    assert torch.equal(outs["0"], outs["1"])
+
+
 @pytest.mark.parametrize("m,n,k,g", [(100, 520, 1024, 64), (200, 200, 4096, 32), (130, 90, 9728, 128),
                                      (512, 2560, 9728, 64)])
 def test_gemm_tile_rows(gpu, m, n, k, g, monkeypatch):
