@@ -544,7 +544,10 @@ __device__ void a8_producer(const I8Args& a, float* red) {
 }
 
 // consumer: returns once all M rows are written (by the producers or, past
-// the poll bound, by this workgroup)
+// the poll bound, by this workgroup). A fallback may rewrite rows that a
+// producer or another fallback also writes, or that other consumers are
+// reading: every writer stores the same bytes (the quantizer is a pure
+// function of the row), so the overlap changes no value that is read.
 template <int XT>
 __device__ void a8_wait_rows(const I8Args& a, int* flag, float* red) {
   if (threadIdx.x == 0) {
