@@ -1463,9 +1463,11 @@ __device__ __forceinline__ float block_max256(float v, float* red) {
 // whole 4-byte slot pairs.
 // NCH > 0: the activation row's 16-byte chunks (at most 256 * NCH) are all
 // loaded at once and kept in registers for the conversion; NCH = 0 loops
-// over the row twice (the second pass from L2). Measured per call, prologue
-// and GEMM, against the two passes: QKV 3584x2560 M = 512 33.5 -> 32.6 us,
-// down 2560x9728 M = 2048 163 -> 161.5 us, the other shapes within 0.5%.
+// over the row twice (the second pass from L2). NCH is the exact chunk
+// count per thread (an out-of-range load still costs an issue). Measured per
+// call, prologue and GEMM, against the two passes: QKV 3584x2560 M = 512
+// 33.5 -> 32.6 us, down 2560x9728 M = 2048 163 -> 161.5 us, the other shapes
+// within 0.5%.
 template <int NCH>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -2760,16 +2762,14 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   // the activation row in registers up to 2048 chunks of 16 bytes (K <= 16384)
   const int64_t nch = env_int("SPARKQ_PREP_NO_REG", 0) ? 0 : cdiv(K / 8, 256);
   const dim3 pg((unsigned)(M + cdiv(N, pp.rw)));
-  if (nch == 1)
-    hipLaunchKernelGGL(gemm_prep_kernel<1>, pg, dim3(256), pp.lds, st, p);
-  else if (nch == 2)
-    hipLaunchKernelGGL(gemm_prep_kernel<2>, pg, dim3(256), pp.lds, st, p);
-  else if (nch >= 3 && nch <= 4)
-    hipLaunchKernelGGL(gemm_prep_kernel<4>, pg, dim3(256), pp.lds, st, p);
-  else if (nch >= 5 && nch <= 8)
-    hipLaunchKernelGGL(gemm_prep_kernel<8>, pg, dim3(256), pp.lds, st, p);
-  else
-    hipLaunchKernelGGL(gemm_prep_kernel<0>, pg, dim3(256), pp.lds, st, p);
+  switch (nch) {
+#define SPARKQ_PREP_CASE(n) \
+  case n: hipLaunchKernelGGL(gemm_prep_kernel<n>, pg, dim3(256), pp.lds, st, p); break;
+    SPARKQ_PREP_CASE(1) SPARKQ_PREP_CASE(2) SPARKQ_PREP_CASE(3) SPARKQ_PREP_CASE(4)
+    SPARKQ_PREP_CASE(5) SPARKQ_PREP_CASE(6) SPARKQ_PREP_CASE(7) SPARKQ_PREP_CASE(8)
+#undef SPARKQ_PREP_CASE
+    default: hipLaunchKernelGGL(gemm_prep_kernel<0>, pg, dim3(256), pp.lds, st, p);
+  }
   GemmX16Args a{};
   a.xh = p.xh;
   a.w = w;
