@@ -2644,6 +2644,16 @@ static WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
       const int64_t cost = cdiv(T * s, cus) * cdiv(nsteps, s) + 2 * s;
       if (best < 0 || cost < best) best = cost, S = s;
     }
+  } else if (T > cus && T < P && !env_int("SPARKQ_W4_GEMM_NO_CU1", 0)) {
+    // one round of more tiles than CUs: a workgroup pair on a CU runs at
+    // well over half the speed of one alone, so the CUs holding two whole
+    // tiles set the time; instead one whole tile per CU, and the tiles past
+    // the CUs in k pieces (at most 3: each piece adds a 128 KB partial to
+    // the last one's reads). gate+up 19456x2560: M = 512 (304 tiles) 86-88
+    // -> 78 us (three pieces; two 79.7, five 80-82, eight 90), M = 640
+    // (380 tiles, two pieces) 91-93 -> 87 us
+    tail = T - cus;
+    S = std::min<int64_t>(std::min<int64_t>(cus / tail, 3), std::max<int64_t>(nsteps / 8, 1));
   } else if (tail && (tail <= P / 4 || (nsteps >= 64 && tail < P / 2))) {
     S = std::min<int64_t>(P / tail, std::min<int64_t>(env_int("SPARKQ_W4_GEMM_MAXS", 4), nsteps / 12));
   }

@@ -120,6 +120,24 @@ def test_gemm_split_k(gpu, m, n, k, g):
     assert torch.equal(y32, _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32))
 
 
+def test_gemm_one_tile_per_cu_split(gpu, monkeypatch):
+    """A grid of more 128-row tiles than CUs but fewer than two per CU keeps
+    one whole tile per CU and splits the tiles past the CUs into k pieces
+    (270 tiles on 256 CUs: 14 tiles in three pieces); it matches the oracle
+    on the columns either side of the first split tile (the last row tile's
+    columns 19456..) and at the end, and, to fp32 rounding, the unsplit grid."""
+    m, n, k, g = 384, 23040, 1536, 64
+    x, wq, s, b = w4_problem(m, n, k, g, seed=7)
+    cols = np.r_[18944:19968, 22528:23040]
+    ref = o.w4a16_matmul(x, wq[cols], s[cols], b[cols], g)
+    y = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    check_fp32(y.cpu().numpy()[:, cols], ref)
+    check_rounded16(down16(_run(gpu, x, wq, s, b, g, o.BF16))[:, cols], ref, o.BF16)
+    monkeypatch.setenv("SPARKQ_W4_GEMM_NO_CU1", "1")
+    y1 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    assert torch.allclose(y, y1, rtol=1e-5, atol=1e-6 * float(y1.abs().max()))
+
+
 @pytest.mark.parametrize("m,n,k,g", [(40, 96, 2048, 64), (33, 64, 2560, 32), (48, 40, 9728, 64),
                                      (36, 32, 16384, 128), (34, 16, 16896, 64)])
 def test_gemm_prologue_row_paths(gpu, m, n, k, g, monkeypatch):
