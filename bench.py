@@ -159,18 +159,27 @@ def bench_square_cold(torch, sparkq, dev, iters, copies=128):
     return ms
 
 
-def bench_gemm(torch, sparkq, dev, layers, name, m, iters):
+def prepare_layers(sparkq, layers):
+    """Each layer's derived prefill buffers (sparkq.prepare_w4a16), made once
+    per weight set at load time, outside any timed region."""
+    return [{name: sparkq.prepare_w4a16(*layer[name], group_size=G) for name in layer}
+            for layer in layers]
+
+
+def bench_gemm(torch, sparkq, dev, layers, name, m, iters, prepared=None):
     """One W4A16 projection at M rows over every layer's distinct weights in
     one graph replay (36 launches, weights cold in the MALL); returns ms per
-    launch."""
+    launch. With prepared (prepare_layers), each call passes its layer's
+    derived buffer, so the GEMM prologue converts the activations only."""
     n, k = PROJ[name]
     x = torch.randn((m, k), device=dev).to(torch.bfloat16)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
 
     def fn():
-        for layer in layers:
+        for li, layer in enumerate(layers):
             wq, s, b = layer[name]
-            sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y)
+            sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y,
+                                           prepared=None if prepared is None else prepared[li][name])
 
     graph = capture(torch, fn)
     ms = Timer(torch).time(graph.replay, iters, 2) / len(layers)
@@ -425,7 +434,8 @@ def gemm_counters():
 def only_gemm(torch, sparkq, dev, which, iters):
     """Driver for rocprofv3 runs over the prefill GEMM: every (projection, M)
     of the GEMM sweep (which == "all"), or one of them ("gate_up:2048"), each
-    over 36 layers of distinct weights, iters graph-free passes."""
+    over 36 layers of distinct weights with their derived prefill buffers
+    (as the bench times them), iters graph-free passes."""
     shapes = [(name, m) for name in PROJ for m in (16, 512, 2048)]
     if which != "all":
         name, m = which.split(":")
@@ -436,14 +446,15 @@ def only_gemm(torch, sparkq, dev, which, iters):
         ws = []
         for _ in range(LAYERS):
             w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
-            ws.append(sparkq.affine_quantize(w, group_size=G))
+            wq, s, b = sparkq.affine_quantize(w, group_size=G)
+            ws.append((wq, s, b, sparkq.prepare_w4a16(wq, s, b, group_size=G)))
             del w
         x = torch.randn((m, k), device=dev).to(torch.bfloat16)
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         torch.cuda.synchronize()
         for _ in range(iters):
-            for wq, s, b in ws:
-                sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y)
+            for wq, s, b, prep in ws:
+                sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y, prepared=prep)
         torch.cuda.synchronize()
         log(f"{name} M={m}: {iters * LAYERS} launches")
         del ws
@@ -696,12 +707,19 @@ def main():
                                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         extras["w4a16_decode_sweep"] = sweeps
         log("prefill GEMM")
-        gemm = {}
+        prepared = prepare_layers(sparkq, layers)
+        gemm, unprepared = {}, {}
         for name in PROJ:
             for m in (16, 512, 2048):
-                gm = bench_gemm(torch, sparkq, dev, layers, name, m, 3 if m == 2048 else 5)
+                gm = bench_gemm(torch, sparkq, dev, layers, name, m, 3 if m == 2048 else 5,
+                                prepared)
                 gemm[f"{name} M={m}"] = gemm_line(name, m, gm)
+                if m > 32:  # the same calls computing the weight half of the prologue each time
+                    um = bench_gemm(torch, sparkq, dev, layers, name, m, 3 if m == 2048 else 5)
+                    unprepared[f"{name} M={m}"] = gemm_line(name, m, um)
         extras["w4a16_prefill_gemm"] = gemm
+        extras["w4a16_prefill_gemm_unprepared"] = unprepared
+        del prepared
         log("W8A8")
         extras["w8a8"] = {f"M={m}": bench_w8a8(torch, sparkq, dev, m, 5) for m in (1, 8, 16)}
         log("W8A16")

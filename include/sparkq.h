@@ -118,6 +118,39 @@ int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
                         int y_dtype, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* Derived weight buffer of one W4 projection, made once per weight set and
+ * kept beside it (outside the checkpoint tensors), like the reference's
+ * prepared W4 buffers that are derived lazily and rebuilt when the source
+ * arrays change (spark_mlx_llm/ops/linear.py:260-268, built by
+ * prepare_w4a16_nax4, X/spark_mlx_ext/w4a16_multirow.py:169-222). It holds
+ * the weight half of the bf16 GEMM prologue: per-row power-of-two shifted
+ * fp16 scales [N,K/G], the row shifts [N] and the bias slots [N,3K/G
+ * padded to 16] (b + 8s split into bf16 pairs). Only bfloat16 scales and
+ * biases have a prepared form. sparkq_w4a16_prepared_bytes gives its size
+ * (0 for an unsupported group size); the buffer must be 256-byte aligned.
+ * Reads scales and biases only; never allocates. */
+size_t sparkq_w4a16_prepared_bytes(int64_t N, int64_t K, int group_size);
+int sparkq_w4a16_prepare(const void* scales, const void* biases,
+                         void* prepared, size_t prepared_bytes, int64_t N,
+                         int64_t K, int group_size, int dtype, void* stream);
+
+/* sparkq_w4a16_linear with the prepared buffer of (scales, biases): the same
+ * dispatch and the same results bit for bit; when the MFMA GEMM serves the
+ * call (bf16 x, more than 32 rows) its prologue converts the activation
+ * rows only and the GEMM reads the prepared weight half. prepared may be
+ * NULL (then identical to sparkq_w4a16_linear); a non-NULL prepared needs
+ * bfloat16 x and must come from sparkq_w4a16_prepare of these very scales
+ * and biases with the same N, K and group_size (not checked). Same
+ * workspace as sparkq_w4a16_linear. Replaces the prepared-parameter call of
+ * the multirow_packed projection (spark_mlx_llm/ops/linear.py:223-244). */
+int sparkq_w4a16_linear_prepared(const void* x, const uint32_t* w,
+                                 const void* scales, const void* biases,
+                                 const void* prepared, void* y, int64_t M,
+                                 int64_t N, int64_t K, int group_size,
+                                 int bits, int x_dtype, int y_dtype,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* Dequantization to fp32: out[n,k] = fmaf(q[n,k], s[n,k/G], b[n,k/G]), the
  * exact q*s+b rounded once. (The product of a 4-bit code and a 16-bit float
  * is exact in fp32 unless it overflows, so mul-then-add agrees except there.)

@@ -21,7 +21,10 @@ size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G);
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
                  int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, void* ws,
                  size_t wsb, hipStream_t st, const void* res = nullptr,
-                 bool* res_done = nullptr);
+                 bool* res_done = nullptr, const void* prep = nullptr);
+size_t w4a16_prepared_bytes(int64_t N, int64_t K, int G);
+int w4a16_prepare(const void* s, const void* b, void* prep, int64_t N, int64_t K, int G,
+                  hipStream_t st);
 int w4a16_dequantize(const uint32_t* w, const void* s, const void* b, float* out, int64_t N,
                      int64_t K, int G, int sdt, hipStream_t st);
 int w4_quantize(const void* w, uint32_t* wq, void* s, void* b, int64_t N, int64_t K, int G,
@@ -204,10 +207,11 @@ size_t sparkq_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_s
   return w4a16_workspace(M, N, K, group_size);
 }
 
-int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
-                        const void* biases, void* y, int64_t M, int64_t N, int64_t K,
-                        int group_size, int bits, int x_dtype, int y_dtype, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+static int w4a16_linear_checked(const void* x, const uint32_t* w, const void* scales,
+                                const void* biases, const void* prepared, void* y, int64_t M,
+                                int64_t N, int64_t K, int group_size, int bits, int x_dtype,
+                                int y_dtype, void* workspace, size_t workspace_bytes,
+                                void* stream) {
   REQUIRE(x && w && scales && biases && y, "w4a16_linear: null tensor pointer");
   REQUIRE(M > 0 && N > 0 && K > 0, "w4a16_linear: M, N and K must be positive");
   REQUIRE(M <= kI32Max && N <= kI32Max && K <= kI32Max, "w4a16_linear: dimension too large");
@@ -228,9 +232,60 @@ int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
   REQUIRE(aligned(x, 16) && aligned(w, 16), "w4a16_linear: x and w must be 16-byte aligned");
   REQUIRE(aligned(scales, 4) && aligned(biases, 4) && aligned(y, 4),
           "w4a16_linear: scales, biases and y must be 4-byte aligned");
+  REQUIRE(aligned(prepared, 256), "w4a16_linear: the prepared buffer must be 256-byte aligned");
   DEVICE_OK();
   return w4a16_linear(x, w, scales, biases, y, M, N, K, group_size, x_dtype, y_dtype, workspace,
-                      workspace_bytes, (hipStream_t)stream);
+                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, prepared);
+}
+
+int sparkq_w4a16_linear(const void* x, const uint32_t* w, const void* scales,
+                        const void* biases, void* y, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits, int x_dtype, int y_dtype, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  return w4a16_linear_checked(x, w, scales, biases, nullptr, y, M, N, K, group_size, bits,
+                              x_dtype, y_dtype, workspace, workspace_bytes, stream);
+}
+
+size_t sparkq_w4a16_prepared_bytes(int64_t N, int64_t K, int group_size) {
+  if (group_size != 32 && group_size != 64 && group_size != 128) return 0;
+  return w4a16_prepared_bytes(N, K, group_size);
+}
+
+int sparkq_w4a16_prepare(const void* scales, const void* biases, void* prepared,
+                         size_t prepared_bytes, int64_t N, int64_t K, int group_size,
+                         int dtype, void* stream) {
+  REQUIRE(scales && biases && prepared, "w4a16_prepare: null tensor pointer");
+  REQUIRE(N > 0 && K > 0 && N <= kI32Max && K <= kI32Max,
+          "w4a16_prepare: N and K must be positive 32-bit sizes");
+  REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+          "w4a16_prepare: group_size must be 32, 64 or 128 (got %d)", group_size);
+  REQUIRE(K % group_size == 0 && K % 64 == 0,
+          "w4a16_prepare: K=%lld must be a multiple of 64 and of group_size=%d", (long long)K,
+          group_size);
+  REQUIRE_SUPPORTED(dtype == SPARKQ_BF16,
+                    "w4a16_prepare: only bfloat16 scales have a prepared form");
+  REQUIRE_SUPPORTED(fits_range({N, K / group_size, 2}) && fits_range({N, 3 * K / group_size + 16, 2}),
+                    "w4a16_prepare: scales or bias slots exceed the 2 GiB range of one buffer "
+                    "descriptor");
+  REQUIRE(aligned(scales, 4) && aligned(biases, 4) && aligned(prepared, 256),
+          "w4a16_prepare: scales and biases must be 4-byte and prepared 256-byte aligned");
+  const size_t need = w4a16_prepared_bytes(N, K, group_size);
+  if (prepared_bytes < need)
+    return set_error(SPARKQ_ERR_WORKSPACE, "w4a16_prepare needs %zu bytes (got %zu)", need,
+                     prepared_bytes);
+  DEVICE_OK();
+  return w4a16_prepare(scales, biases, prepared, N, K, group_size, (hipStream_t)stream);
+}
+
+int sparkq_w4a16_linear_prepared(const void* x, const uint32_t* w, const void* scales,
+                                 const void* biases, const void* prepared, void* y, int64_t M,
+                                 int64_t N, int64_t K, int group_size, int bits, int x_dtype,
+                                 int y_dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  REQUIRE(prepared == nullptr || x_dtype == SPARKQ_BF16,
+          "w4a16_linear_prepared: a prepared buffer serves bfloat16 activations only");
+  return w4a16_linear_checked(x, w, scales, biases, prepared, y, M, N, K, group_size, bits,
+                              x_dtype, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int sparkq_w4a16_dequantize(const uint32_t* w, const void* scales, const void* biases, float* out,

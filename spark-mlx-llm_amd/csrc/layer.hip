@@ -19,7 +19,8 @@ namespace sparkq {
 size_t w4a16_workspace(int64_t M, int64_t N, int64_t K, int G);
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
                  int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, void* ws,
-                 size_t wsb, hipStream_t st, const void* res, bool* res_done);
+                 size_t wsb, hipStream_t st, const void* res, bool* res_done,
+                 const void* prep = nullptr);
 int w4_ffn_gate_up(const void* x, const void* xres, const void* nw, float eps,
                    const uint32_t* wg, const void* sg, const void* bg, const uint32_t* wu,
                    const void* su, const void* bu, void* act, void* hid, void* nrm, int64_t M,

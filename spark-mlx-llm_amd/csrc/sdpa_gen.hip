@@ -26,6 +26,7 @@
 // With several context splits each workgroup stores (max, sum, outputs) and
 // sdpa_gen_merge_kernel combines them in split order.
 #include <algorithm>
+#include <cfloat>
 
 #include "common.h"
 
@@ -167,8 +168,8 @@ __global__ __launch_bounds__(256) void sdpa_gen_kernel(GenSdpaArgs a) {
                                (int64_t)n * a.m_n;
             if (a.mask_kind == kMaskBool)
               s[r] = reinterpret_cast<const unsigned char*>(a.mask)[mi] ? s[r] : a.masked;
-            else
-              s[r] += gen_load(a.mask, mi, a.mask_dtype) * 1.4426950408889634f;
+            else  // a dtype-minimum mask stays finite (its product would overflow)
+              s[r] += fmaxf(gen_load(a.mask, mi, a.mask_dtype) * 1.4426950408889634f, -FLT_MAX);
           }
         }
       }
@@ -181,8 +182,11 @@ __global__ __launch_bounds__(256) void sdpa_gen_kernel(GenSdpaArgs a) {
         const float v = n < t_end ? s[r] : -INFINITY;
         const float cm = block_reduce<true>(v, red, 0);
         const float mnew = fmaxf(mrun[r], cm);
+        // nothing visible yet (every score so far -inf from an additive
+        // mask): no weight, no rescale, so no -inf - -inf = NaN enters the
+        // sums; a -inf score weighs 0 once a finite one has been seen
         const float alpha = mrun[r] == -INFINITY ? 0.0f : exp2f(mrun[r] - mnew);
-        const float p = n < t_end ? exp2f(v - mnew) : 0.0f;
+        const float p = (n < t_end && v != -INFINITY) ? exp2f(v - mnew) : 0.0f;
         sc[r * kGenChunk + tid] = p;
         const float cz = block_reduce<false>(p, red, 1);
         zrun[r] = fmaf(zrun[r], alpha, cz);

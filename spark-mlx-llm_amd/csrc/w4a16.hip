@@ -1682,14 +1682,20 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// PD: 1 = the loads of step s+1 go out during step s, 2 = those of step s+2
-template <int G, int NWV, int MX, int PD>
+// PD: 1 = the loads of step s+1 go out during step s, 2 = those of step s+2.
+// SCH (schedule variants, PD = 1): bit 0 raises the wave priority over the
+// MFMA phase of each step; bit 1 keeps four A slots in LDS, fills slot s+2
+// during step s and synchronises the workgroup after every second step only.
+template <int G, int NWV, int MX, int PD, int SCH = 0>
 __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a) {
   constexpr int NT = 64 * NWV;
   constexpr int BM = 32 * MX;                // tile rows: MX 32-row fragments per wave
   constexpr int AL = BM * kBK / 8 / NT;      // 16-byte A pieces per thread per step
-  // two A buffers, at least 8 KB per wave for the staged bf16 output
-  constexpr int AS = 2 * BM * kBK > NWV * 64 * 64 ? 2 * BM * kBK : NWV * 64 * 64;
+  constexpr bool PRIO = (SCH & 1) != 0;
+  constexpr bool BAR2 = (SCH & 2) != 0 && PD == 1;
+  constexpr int NSLOT = BAR2 ? 4 : 2;
+  // the A slots, at least 8 KB per wave for the staged bf16 output
+  constexpr int AS = NSLOT * BM * kBK > NWV * 64 * 64 ? NSLOT * BM * kBK : NWV * 64 * 64;
   __shared__ __attribute__((aligned(16))) uint16_t As[AS];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1749,8 +1755,16 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
       ra[set][i] = __builtin_bit_cast(
           u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(live ? xoff[i] : kOob), 2 * k0, 0));
   };
+  // set 0 at step's offset, or the out-of-range offset (zeros) when not live
+  auto load_a_at = [&](int step, bool live) {
+    const int k0 = live ? step * kBK : 0;
+#pragma unroll
+    for (int i = 0; i < AL; ++i)
+      ra[0][i] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(live ? xoff[i] : kOob), 2 * k0, 0));
+  };
   auto load_w = [&](int step, int set) {
-    const bool live = PD == 1 || step < nsteps;
+    const bool live = (PD == 1 && !BAR2) || step < nsteps;
     const int k0 = live ? step * kBK : 0;
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
@@ -1771,7 +1785,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
 
   auto body = [&](int step, auto stc) {
     constexpr int st = decltype(stc)::value;
-    constexpr int rs0 = NW == 1 ? 0 : st;  // weight set holding this step
+    constexpr int rs0 = NW == 1 ? 0 : (st & 1);  // weight set holding this step
     // nothing of a step moves into the one before (it would wait there for
     // the loads still in flight)
     if constexpr (PD > 1) __builtin_amdgcn_sched_barrier(0);
@@ -1780,7 +1794,12 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
     const f16x2_t s1 = __builtin_bit_cast(f16x2_t, rsv[rs0][1] * 0x10001u);
     const f16x2_t c0 = s0 * f16x2_t{(_Float16)-24.0f, (_Float16)-24.0f};
     const f16x2_t c1 = s1 * f16x2_t{(_Float16)-24.0f, (_Float16)-24.0f};
-    if constexpr (PD == 1) {
+    if constexpr (BAR2) {
+      // A two steps ahead, the weights one; past the end the loads read the
+      // out-of-range offset (zeros), so no branch splits the wait counts
+      load_a_at(step + 2, step + 2 < nsteps);
+      load_w(step + 1, 0);
+    } else if constexpr (PD == 1) {
       if (step + 1 < nsteps) {
         load_a(step + 1, 0);
         load_w(step + 1, 0);
@@ -1789,6 +1808,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
       load_a(step + 2, st);
       load_w(step + 2, st);
     }
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ss = 0; ss < 4; ++ss) {
       u32x4_t bf0, bf1;
@@ -1807,14 +1827,48 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
         acc[x][1] = mfma32x32x16<F16>(af, bf1, acc[x][1]);
       }
     }
-    if (step + 1 < nsteps) {
-      constexpr int rs1 = NA == 1 ? 0 : st ^ 1;  // activation set holding the next step
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+    if constexpr (BAR2) {
+      if (step + 2 < nsteps) {
 #pragma unroll
-      for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)((st ^ 1) * BM * kBK * 2)) = ra[rs1][i];
+        for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)(((st + 2) & 3) * BM * kBK * 2)) = ra[0][i];
+      }
+      // slot s+2 is refilled at the end of step s, after the barrier that
+      // followed every wave's reads of step s-2; it is read in step s+2,
+      // after the barrier that ends step s or s+1
+      if constexpr ((st & 1) == 1) __syncthreads();
+    } else {
+      if (step + 1 < nsteps) {
+        constexpr int rs1 = NA == 1 ? 0 : st ^ 1;  // activation set holding the next step
+#pragma unroll
+        for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)((st ^ 1) * BM * kBK * 2)) = ra[rs1][i];
+      }
+      __syncthreads();
     }
-    __syncthreads();
   };
 
+  if constexpr (BAR2) {
+    // slots 0 and 1 hold the first two steps; the loop starts on slot 0
+    load_a_at(s_begin, true);
+    load_w(s_begin, 0);
+#pragma unroll
+    for (int i = 0; i < AL; ++i) *lds_at(lds_w[i]) = ra[0][i];
+    load_a_at(s_begin + 1, s_begin + 1 < nsteps);
+#pragma unroll
+    for (int i = 0; i < AL; ++i) *lds_at(lds_w[i] + (uint32_t)(BM * kBK * 2)) = ra[0][i];
+    __syncthreads();
+    int step = s_begin;
+    for (; step + 4 <= nsteps; step += 4) {
+      body(step, std::integral_constant<int, 0>{});
+      body(step + 1, std::integral_constant<int, 1>{});
+      body(step + 2, std::integral_constant<int, 2>{});
+      body(step + 3, std::integral_constant<int, 3>{});
+    }
+    if (step < nsteps) body(step, std::integral_constant<int, 0>{});
+    if (step + 1 < nsteps) body(step + 1, std::integral_constant<int, 1>{});
+    if (step + 2 < nsteps) body(step + 2, std::integral_constant<int, 2>{});
+    __syncthreads();  // every wave is past its last A read before the output staging
+  } else {
   load_a(s_begin, 0);
   load_w(s_begin, 0);
   if constexpr (PD > 1) {
@@ -1839,6 +1893,7 @@ __global__ __launch_bounds__(64 * NWV, 2) void w4_gemm_x16w_kernel(GemmX16Args a
       body(step + 1, std::integral_constant<int, 1>{});
     }
     if (step < nsteps) body(step, std::integral_constant<int, 0>{});
+  }
   }
 
   if (split) {
@@ -2602,6 +2657,23 @@ static GemmX16Layout gemm_x16_layout(int64_t M, int64_t N, int64_t K, int G) {
   return l;
 }
 
+// The weight half of that prologue (scaled fp16 scales, row shifts and bias
+// slots) depends on the scales and biases only, so a caller can compute it
+// once per weight set (w4a16_prepare) and hand it to every later call; the
+// per-call prologue then converts the activation rows only.
+struct PreparedLayout {
+  size_t sp, es, b2, bytes;
+};
+static PreparedLayout prepared_layout(int64_t N, int64_t K, int G) {
+  const int64_t ng = K / G, k2p = bias_slots((int)K, G);
+  PreparedLayout l;
+  l.sp = 0;
+  l.es = round_up((size_t)(N * ng * 2), 256);
+  l.b2 = l.es + round_up((size_t)(N * 4), 256);
+  l.bytes = l.b2 + round_up((size_t)(N * k2p * 2), 256);
+  return l;
+}
+
 // Work plan of the wide GEMM (up to two workgroups per CU).
 //
 // Grids of 128-row tiles that would fill less than a quarter of the slots
@@ -2748,9 +2820,31 @@ static void launch_gemm(int G, const void* x, const uint32_t* w, const void* s,
 #undef SPARKQ_GEMM
 }
 
+// One launch of the prologue over M activation rows and the weight rows of
+// p.N (p.N = 0: activation rows only; p.M = 0: weight rows only).
+static void launch_gemm_prep(const GemmPrepArgs& p, hipStream_t st) {
+  const PrepPlan pp = plan_prep(p.K, p.G);
+  GemmPrepArgs q = p;
+  q.rw = pp.rw;
+  // the activation row in registers up to 2048 chunks of 16 bytes (K <= 16384)
+  const int64_t nch = env_int("SPARKQ_PREP_NO_REG", 0) ? 0 : cdiv(p.K / 8, 256);
+  const dim3 pg((unsigned)(p.M + cdiv(p.N, pp.rw)));
+  switch (nch) {
+#define SPARKQ_PREP_CASE(n) \
+  case n: hipLaunchKernelGGL(gemm_prep_kernel<n>, pg, dim3(256), pp.lds, st, q); break;
+    SPARKQ_PREP_CASE(1) SPARKQ_PREP_CASE(2) SPARKQ_PREP_CASE(3) SPARKQ_PREP_CASE(4)
+    SPARKQ_PREP_CASE(5) SPARKQ_PREP_CASE(6) SPARKQ_PREP_CASE(7) SPARKQ_PREP_CASE(8)
+#undef SPARKQ_PREP_CASE
+    default: hipLaunchKernelGGL(gemm_prep_kernel<0>, pg, dim3(256), pp.lds, st, q);
+  }
+}
+
+// prep: the weight half made by w4a16_prepare for these scales and biases,
+// or null to compute it in this call's prologue
 static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void* s,
-                            const void* b, unsigned* counters, unsigned char* ws, void* y,
-                            int ydt, int M, int N, int K, hipStream_t st) {
+                            const void* b, const unsigned char* prep, unsigned* counters,
+                            unsigned char* ws, void* y, int ydt, int M, int N, int K,
+                            hipStream_t st) {
   const GemmX16Layout l = gemm_x16_layout(M, N, K, G);
   GemmPrepArgs p{};
   p.x = (const uint16_t*)x;
@@ -2759,27 +2853,23 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   p.xh = reinterpret_cast<uint16_t*>(ws + l.xh);
   p.ex = reinterpret_cast<int*>(ws + l.ex);
   p.a2 = reinterpret_cast<uint16_t*>(ws + l.a2);
-  p.sp = reinterpret_cast<uint16_t*>(ws + l.sp);
-  p.es = reinterpret_cast<int*>(ws + l.es);
-  p.b2 = reinterpret_cast<uint16_t*>(ws + l.b2);
   p.M = M;
   p.N = N;
   p.K = K;
   p.G = G;
   p.K2p = bias_slots(K, G);
-  const PrepPlan pp = plan_prep(K, G);
-  p.rw = pp.rw;
-  // the activation row in registers up to 2048 chunks of 16 bytes (K <= 16384)
-  const int64_t nch = env_int("SPARKQ_PREP_NO_REG", 0) ? 0 : cdiv(K / 8, 256);
-  const dim3 pg((unsigned)(M + cdiv(N, pp.rw)));
-  switch (nch) {
-#define SPARKQ_PREP_CASE(n) \
-  case n: hipLaunchKernelGGL(gemm_prep_kernel<n>, pg, dim3(256), pp.lds, st, p); break;
-    SPARKQ_PREP_CASE(1) SPARKQ_PREP_CASE(2) SPARKQ_PREP_CASE(3) SPARKQ_PREP_CASE(4)
-    SPARKQ_PREP_CASE(5) SPARKQ_PREP_CASE(6) SPARKQ_PREP_CASE(7) SPARKQ_PREP_CASE(8)
-#undef SPARKQ_PREP_CASE
-    default: hipLaunchKernelGGL(gemm_prep_kernel<0>, pg, dim3(256), pp.lds, st, p);
+  if (prep != nullptr) {
+    const PreparedLayout pl = prepared_layout(N, K, G);
+    p.sp = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(prep + pl.sp));
+    p.es = const_cast<int*>(reinterpret_cast<const int*>(prep + pl.es));
+    p.b2 = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(prep + pl.b2));
+    p.N = 0;  // the prologue converts the activation rows only
+  } else {
+    p.sp = reinterpret_cast<uint16_t*>(ws + l.sp);
+    p.es = reinterpret_cast<int*>(ws + l.es);
+    p.b2 = reinterpret_cast<uint16_t*>(ws + l.b2);
   }
+  launch_gemm_prep(p, st);
   GemmX16Args a{};
   a.xh = p.xh;
   a.w = w;
@@ -2804,6 +2894,8 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
   dim3 gw((unsigned)wp.items);
 #define SPARKQ_X16W(GG, MM, PP) \
   hipLaunchKernelGGL((w4_gemm_x16w_kernel<GG, 4, MM, PP>), gw, dim3(256), 0, st, a)
+#define SPARKQ_X16S(GG, SS) \
+  hipLaunchKernelGGL((w4_gemm_x16w_kernel<GG, 4, 4, 1, SS>), gw, dim3(256), 0, st, a)
   // the 64-row tiles (grids of at most one workgroup per CU, whose steps
   // wait on their loads) keep two steps of loads in flight: QKV 3584 x 2560
   // at M = 512 35.0 -> 32.2 us, down 2560 x 9728 78.3 -> 70.0 us, bit-identical;
@@ -2819,10 +2911,26 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
     else if (G == 64) SPARKQ_X16W(64, 2, 1);
     else SPARKQ_X16W(128, 2, 1);
   } else {
-    if (G == 32) SPARKQ_X16W(32, 4, 1);
-    else if (G == 64) SPARKQ_X16W(64, 4, 1);
-    else SPARKQ_X16W(128, 4, 1);
+    const int sch = env_int("SPARKQ_W4_GEMM_SCH", 0);
+    if (sch == 1) {
+      if (G == 32) SPARKQ_X16S(32, 1);
+      else if (G == 64) SPARKQ_X16S(64, 1);
+      else SPARKQ_X16S(128, 1);
+    } else if (sch == 2) {
+      if (G == 32) SPARKQ_X16S(32, 2);
+      else if (G == 64) SPARKQ_X16S(64, 2);
+      else SPARKQ_X16S(128, 2);
+    } else if (sch == 3) {
+      if (G == 32) SPARKQ_X16S(32, 3);
+      else if (G == 64) SPARKQ_X16S(64, 3);
+      else SPARKQ_X16S(128, 3);
+    } else {
+      if (G == 32) SPARKQ_X16W(32, 4, 1);
+      else if (G == 64) SPARKQ_X16W(64, 4, 1);
+      else SPARKQ_X16W(128, 4, 1);
+    }
   }
+#undef SPARKQ_X16S
 #undef SPARKQ_X16W
 }
 
@@ -2833,7 +2941,8 @@ int w4_gemvq_linear(const void* x, const uint32_t* w, const void* s, const void*
 
 int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
                  void* y, int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt,
-                 void* ws, size_t wsb, hipStream_t st, const void* res, bool* res_done) {
+                 void* ws, size_t wsb, hipStream_t st, const void* res, bool* res_done,
+                 const void* prep) {
   // res (16-bit [M][N], y of the same type) is added to the rounded output by
   // the decode kernels; *res_done says whether the chosen kernel did it
   if (res_done) *res_done = false;
@@ -2956,7 +3065,8 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
   }
   unsigned char* wsp = reinterpret_cast<unsigned char*>(ws) + kCounterBytes;
   if (xdt == SPARKQ_BF16 && !env_int("SPARKQ_W4_NO_X16", 0)) {
-    launch_gemm_x16(G, x, w, s, b, reinterpret_cast<unsigned*>(ws), wsp, y, ydt, (int)M, (int)N,
+    launch_gemm_x16(G, x, w, s, b, reinterpret_cast<const unsigned char*>(prep),
+                    reinterpret_cast<unsigned*>(ws), wsp, y, ydt, (int)M, (int)N,
                     (int)K, st);
     return check_launch("w4_gemm_x16w_kernel");
   }
@@ -2966,6 +3076,33 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
   else
     launch_gemm<F16>(G, x, w, s, b, xs, y, ydt, (int)M, (int)N, (int)K, st);
   return check_launch("w4_gemm_kernel");
+}
+
+size_t w4a16_prepared_bytes(int64_t N, int64_t K, int G) {
+  if (N <= 0 || K <= 0 || G <= 0) return 0;
+  return prepared_layout(N, K, G).bytes;
+}
+
+// The weight half of the bf16 GEMM prologue for one weight set, into prep
+// (w4a16_prepared_bytes); the same kernel and code path as the per-call
+// prologue, so a prepared call gives bit-identical results.
+int w4a16_prepare(const void* s, const void* b, void* prep, int64_t N, int64_t K, int G,
+                  hipStream_t st) {
+  const PreparedLayout pl = prepared_layout(N, K, G);
+  unsigned char* pb = reinterpret_cast<unsigned char*>(prep);
+  GemmPrepArgs p{};
+  p.sc = (const uint16_t*)s;
+  p.bi = (const uint16_t*)b;
+  p.sp = reinterpret_cast<uint16_t*>(pb + pl.sp);
+  p.es = reinterpret_cast<int*>(pb + pl.es);
+  p.b2 = reinterpret_cast<uint16_t*>(pb + pl.b2);
+  p.M = 0;  // weight rows only
+  p.N = (int)N;
+  p.K = (int)K;
+  p.G = G;
+  p.K2p = bias_slots((int)K, G);
+  launch_gemm_prep(p, st);
+  return check_launch("gemm_prep_kernel");
 }
 
 int w4a16_dequantize(const uint32_t* w, const void* s, const void* b, float* out,

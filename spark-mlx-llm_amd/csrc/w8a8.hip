@@ -483,6 +483,15 @@ template <int XT, bool LEAN = false>
 __device__ void a8_produce_row(const I8Args& a, int row, float* red) {
   typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
   const int K = a.K, np = K >> 3, NT = blockDim.x, tid = threadIdx.x;
+  if constexpr (!LEAN) {
+    // a workgroup narrower than the row's single pass needs (the rows
+    // kernel's width set below 512 threads) takes the looping form, which
+    // covers every piece whatever the width
+    if (np > kA8PP * NT) {
+      a8_produce_row<XT, true>(a, row, red);
+      return;
+    }
+  }
   const rsrc_t rx = make_rsrc(reinterpret_cast<const unsigned char*>(a.x) + (int64_t)row * K * 2,
                               (uint32_t)K * 2);
   constexpr int NV = LEAN ? 1 : kA8PP;

@@ -18,6 +18,7 @@ from .ext import (
     is_w8a8_available,
     kv_append,
     kv_quantize_s8,
+    prepare_w4a16,
     prepare_w4a16_nax4,
     quantize_per_token,
     rms_norm,
@@ -43,6 +44,7 @@ __all__ = [
     "is_w8a8_available",
     "kv_append",
     "kv_quantize_s8",
+    "prepare_w4a16",
     "prepare_w4a16_nax4",
     "quantize_per_token",
     "rms_norm",

@@ -38,6 +38,10 @@ SIGNATURES = {
     "sparkq_is_available": (I, []),
     "sparkq_w4a16_workspace_bytes": (SZ, [I64, I64, I64, I]),
     "sparkq_w4a16_linear": (I, [P, P, P, P, P, I64, I64, I64, I, I, I, I, P, SZ, P]),
+    "sparkq_w4a16_prepared_bytes": (SZ, [I64, I64, I]),
+    "sparkq_w4a16_prepare": (I, [P, P, P, SZ, I64, I64, I, I, P]),
+    "sparkq_w4a16_linear_prepared": (I, [P, P, P, P, P, P, I64, I64, I64, I, I, I, I, P, SZ,
+                                         P]),
     "sparkq_w4a16_dequantize": (I, [P, P, P, P, I64, I64, I, I, P]),
     "sparkq_w4_quantize": (I, [P, P, P, P, I64, I64, I, I, P]),
     "sparkq_a8_quantize_per_token": (I, [P, P, P, I64, I64, I, P]),

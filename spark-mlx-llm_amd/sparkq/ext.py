@@ -34,11 +34,13 @@ __all__ = [
     "kv_quantize_s8",
     "QuantizedKVCache",
     "kv_append",
+    "prepare_w4a16",
     "prepare_w4a16_nax4",
     "quantize_per_token",
     "rms_norm",
     "rope",
     "spark_qkv_rope",
+    "staged_quantized_sdpa",
     "w4a16_multirow",
     "w4a16_qmv",
     "w8a16_per_channel",
@@ -109,7 +111,8 @@ def _w4_check(op, x, weight, scales, biases, group_size, bits):
 
 
 def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
-                            bits: int = 4, transpose: bool = True, out_dtype=None, out=None):
+                            bits: int = 4, transpose: bool = True, out_dtype=None, out=None,
+                            prepared=None):
     """y = x @ dequantize(weight)^T for MLX affine packed weights.
 
     The equivalent of mx.quantized_matmul(x, weight, scales, biases,
@@ -120,7 +123,10 @@ def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
     the groupwise W8 affine MFMA kernel that the reference's W8 layers fall
     back to. out_dtype may be
     torch.float32 to read the unrounded fp32 epilogue; out, when given, is a
-    contiguous [..., N] tensor written in place.
+    contiguous [..., N] tensor written in place. prepared, when given, is
+    the derived buffer of prepare_w4a16 for these very scales and biases
+    (bf16 only): the prefill GEMM then skips the weight half of its
+    prologue; results are bit-identical either way.
     """
     if not transpose:
         raise ValueError("only transpose=True (x @ W^T) is supported")
@@ -142,10 +148,62 @@ def affine_quantized_matmul(x, weight, scales, biases, *, group_size: int = 64,
     weight, scales, biases = weight.contiguous(), scales.contiguous(), biases.contiguous()
     ws, wsb = _lib.workspace(x.device, _lib.lib().sparkq_w4a16_workspace_bytes(m, n, k, group_size),
                              "w4a16")
-    _lib.call("sparkq_w4a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
-              _ptr(y), m, n, k, group_size, bits, _lib.dtype_code(x.dtype),
-              _lib.dtype_code(out_dtype), ws, wsb, _lib.stream_handle(x.device), device=x.device)
+    if prepared is None:
+        _lib.call("sparkq_w4a16_linear", _ptr(x2), _ptr(weight), _ptr(scales), _ptr(biases),
+                  _ptr(y), m, n, k, group_size, bits, _lib.dtype_code(x.dtype),
+                  _lib.dtype_code(out_dtype), ws, wsb, _lib.stream_handle(x.device),
+                  device=x.device)
+    else:
+        _check_prepared(op, prepared, n, k, group_size, x)
+        _lib.call("sparkq_w4a16_linear_prepared", _ptr(x2), _ptr(weight), _ptr(scales),
+                  _ptr(biases), _ptr(prepared), _ptr(y), m, n, k, group_size, bits,
+                  _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), ws, wsb,
+                  _lib.stream_handle(x.device), device=x.device)
     return y.reshape(*lead, n)
+
+
+def _check_prepared(op, prepared, n, k, group_size, x):
+    need = _lib.lib().sparkq_w4a16_prepared_bytes(n, k, group_size)
+    if (not isinstance(prepared, torch.Tensor) or prepared.dtype != torch.uint8
+            or prepared.ndim != 1 or prepared.numel() < need or not prepared.is_contiguous()):
+        raise ValueError(f"{op}: prepared must be the uint8 buffer of prepare_w4a16 "
+                         f"({need} bytes for N={n}, K={k}, group_size={group_size})")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{op}: a prepared buffer serves bfloat16 activations only")
+    if prepared.device != x.device:
+        raise ValueError(f"{op}: prepared must live on the activations' device")
+
+
+def prepare_w4a16(weight, scales, biases, *, group_size: int | None = None):
+    """Derived buffer of one W4 projection for the prefill GEMM: the weight
+    half of its prologue (scaled fp16 scales, row shifts, bias slots),
+    computed once per weight set instead of on every call. The reference
+    derives its prepared W4 buffers the same way, once per source arrays
+    and outside the checkpoint tree (spark_mlx_llm/ops/linear.py:260-268).
+    Returns a uint8 device tensor, or None where no prepared form exists
+    (fp16 scales). Costs about (3*K/G + 16) * 2 + 2*K/G + 4 bytes per row
+    (6.6 MB for a 19456 x 2560 G64 projection, 24% of its packed bytes)."""
+    if any(not isinstance(v, torch.Tensor) for v in (weight, scales, biases)):
+        raise TypeError("weight, scales and biases must be tensors")
+    if weight.dtype not in _PACKED or weight.ndim != 2 or scales.ndim != 2:
+        raise ValueError("prepare_w4a16 requires UINT32-packed W4 weights [N,K/8] and "
+                         "scales [N,K/G]")
+    n, k = weight.shape[0], weight.shape[1] * 8
+    if scales.shape[0] != n or scales.shape[1] <= 0 or k % scales.shape[1]:
+        raise ValueError("prepare_w4a16: scales must have shape [N,K/G]")
+    g = k // scales.shape[1] if group_size is None else group_size
+    if g not in (32, 64, 128) or scales.shape != (n, k // g) or biases.shape != scales.shape:
+        raise ValueError("prepare_w4a16: group_size must be 32, 64 or 128 with scales and "
+                         "biases [N,K/G]")
+    if scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+        return None
+    _require_device("prepare_w4a16", weight, scales, biases)
+    need = _lib.lib().sparkq_w4a16_prepared_bytes(n, k, g)
+    prepared = torch.empty(need, dtype=torch.uint8, device=scales.device)
+    scales, biases = scales.contiguous(), biases.contiguous()
+    _lib.call("sparkq_w4a16_prepare", _ptr(scales), _ptr(biases), _ptr(prepared), need, n, k,
+              g, BF16, _lib.stream_handle(scales.device), device=scales.device)
+    return prepared
 
 
 def _w8_affine_matmul(op, x, weight, scales, biases, group_size, out_dtype, out):
@@ -476,7 +534,7 @@ def _int8_prefill_affine(queries, keys, values, *, scale, causal, group_size, bi
         if packed.stride(3) != 1 or s.stride(3) != 1:
             raise ValueError(f"{name} innermost axis must be contiguous")
     (kc, ks, kb), (vc, vs, vb) = keys, values
-    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    _require_device("int8_quantized_sdpa", queries, kc, ks, kb, vc, vs, vb)
     out_dtype = queries.dtype if out_dtype is None else out_dtype
     q = queries.contiguous()
     y = _out_buffer(out, (batch, heads, length, dim), out_dtype, queries.device)
@@ -517,7 +575,7 @@ def _int8_prefill(queries, keys, values, *, scale, causal, fmt, out_dtype, out,
         if codes.stride(3) != 1:
             raise ValueError(f"{name} innermost axis must be contiguous")
     (kc, ks), (vc, vs) = keys, values
-    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    _require_device("int8_quantized_sdpa", queries, kc, ks, vc, vs)
     out_dtype = queries.dtype if out_dtype is None else out_dtype
     q = queries.contiguous()
     y = _out_buffer(out, (batch, heads, length, dim), out_dtype, queries.device)
@@ -644,9 +702,25 @@ def _kv_strides(codes, scales, elem_bytes_codes):
             ss[0], ss[1], ss[2]]
 
 
+def staged_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, bits: int = 8,
+                          mask=None, out_dtype=None, out=None):
+    """Attention over an MLX affine quantized cache in the staged form
+    (dequantized keys, scores, softmax, weights times values), whatever the
+    fused predicate would choose: what mlx-lm's quantized attention computes
+    for the reference when its fused kernel is switched off
+    (spark_mlx_llm/ops/sdpa.py:39-78 with fused_quantized_sdpa=False), and
+    the reference's own _fallback (X/spark_mlx_ext/int8_quantized_sdpa.py:
+    122-153). Validates as int8_quantized_sdpa does for the affine tuple."""
+    if len(keys) != 3:
+        raise ValueError("the staged form takes the affine (packed, scales, biases) tuple")
+    return int8_quantized_sdpa(queries, keys, values, scale=scale, group_size=group_size,
+                               bits=bits, mask=mask, out_dtype=out_dtype, out=out,
+                               _allow_fused=False)
+
+
 def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, bits: int = 8,
                         mask=None, single_pass_max_length: int = 1023, out_dtype=None,
-                        out=None):
+                        out=None, _allow_fused: bool = True):
     """Attention over a quantized KV cache
     (X/spark_mlx_ext/int8_quantized_sdpa.py:156-287).
 
@@ -706,7 +780,8 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
         if packed.stride(3) != 1 or s.stride(3) != 1:
             raise ValueError(f"{name} innermost axis must be contiguous")
     gqa = heads // kv_heads
-    fused = (bits == 8 and dim == dv and dim in (64, 128, 256) and gqa in (1, 2, 4, 8)
+    fused = (_allow_fused and bits == 8 and dim == dv and dim in (64, 128, 256)
+             and gqa in (1, 2, 4, 8)
              and simple_mask
              and (length == 1 or (queries.dtype in _HALF and (mask is None or length <= n))))
     if not fused:
@@ -725,7 +800,7 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
 def _decode(queries, kc, ks, kb, vc, vs, vb, strides, group_size, fmt, scale, out_dtype, out):
     batch, heads, _, dim = queries.shape
     kv_heads, n = kc.shape[1:3]
-    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    _require_device("int8_quantized_sdpa", queries, kc, ks, kb, vc, vs, vb)
     out_dtype = queries.dtype if out_dtype is None else out_dtype
     q = queries.reshape(batch, heads, dim).contiguous()
     out = _out_buffer(out, (batch, heads, 1, dim), out_dtype, queries.device)
@@ -794,7 +869,7 @@ def _staged_attention(queries, keys, values, *, scale, group_size, bits, mask, o
         if kind == _MASK_BOOL:
             mask_t = mask_t.view(torch.uint8)
         mstrides = (ctypes.c_int64 * 4)(*mask_t.stride())
-    _require_device("int8_quantized_sdpa", queries, kc, vc)
+    _require_device("int8_quantized_sdpa", queries, kc, ks, kb, vc, vs, vb, mask_t)
     out_dtype = queries.dtype if out_dtype is None else out_dtype
     if out_dtype not in (queries.dtype, torch.float32):
         raise ValueError("out_dtype must be the query dtype or torch.float32")
@@ -963,7 +1038,8 @@ def fused_ffn(x, attention_output, norm_weight, eps: float, gate, up, down, *,
             raise ValueError(f"fused_ffn: {name} projection has the wrong packed shape or dtype")
     if group_size not in (32, 64, 128) or k % 64 or inter % 64:
         raise ValueError("fused_ffn: group_size 32/64/128 and sizes divisible by 64 required")
-    _require_device("fused_ffn", x, attention_output, norm_weight, gw, uw, dw)
+    _require_device("fused_ffn", x, attention_output, norm_weight, gw, gs, gb, uw, us, ub, dw,
+                    ds, db)
     m = prod(x.shape[:-1])
     x2 = x.reshape(m, k).contiguous()
     a2 = attention_output.reshape(m, k).contiguous()

@@ -11,6 +11,7 @@ from .linear import (
     W8A8Projection,
     W8A8QuantizedLinear,
     dispatch_linear,
+    prepare_w4_layers,
 )
 from .qkv import RoPE, dispatch_qkv
 from .sdpa import SDPAConfig, dispatch_sdpa
@@ -31,4 +32,5 @@ __all__ = [
     "dispatch_linear",
     "dispatch_qkv",
     "dispatch_sdpa",
+    "prepare_w4_layers",
 ]

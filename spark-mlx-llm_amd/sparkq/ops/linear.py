@@ -28,6 +28,7 @@ __all__ = [
     "W8A8Projection",
     "W8A8QuantizedLinear",
     "dispatch_linear",
+    "prepare_w4_layers",
 ]
 
 _GROUPS = (32, 64, 128)
@@ -77,9 +78,43 @@ class QuantizedLinear(nn.Module):
         return cls(wq, s, b, group_size=group_size, bits=bits, bias=bias)
 
     def forward(self, x):
+        prepared = None
+        if AffineParameters.supports_prepared(x.shape, x.dtype, *AffineParameters.from_module(self)):
+            prepared = _w4_prepared_parameters(self)
         y = AffineParameters.native(x, self.weight, self.scales, self.biases, self.group_size,
-                                    self.bits)
+                                    self.bits, prepared)
         return y + self.bias if self.bias is not None else y
+
+
+def _w4_prepared_parameters(layer):
+    """The layer's derived GEMM buffer for its current source tensors
+    (the identity-keyed cache of spark_mlx_llm/ops/linear.py:260-268). Kept
+    outside the module's buffers, so checkpoints never hold it; rebuilt when
+    a source tensor is replaced or modified in place (torch's version
+    counter stands in for MLX's immutable arrays)."""
+    sources = (layer.weight, layer.scales, layer.biases)
+    versions = tuple(t._version for t in sources)
+    cached = getattr(layer, "_sparkq_w4_prepared", None)
+    if (cached is not None and cached[1] == versions
+            and all(old is new for old, new in zip(cached[0], sources))):
+        return cached[2]
+    prepared = ext.prepare_w4a16(*sources, group_size=layer.group_size)
+    object.__setattr__(layer, "_sparkq_w4_prepared", (sources, versions, prepared))
+    return prepared
+
+
+def prepare_w4_layers(model):
+    """Derive the prefill buffers of every eligible W4 projection of a model
+    up front, at load time (spark_mlx_llm/ops/linear.py:636-654 evaluates its
+    prepared buffers the same way), instead of on each layer's first
+    multi-token call. Returns the number of layers prepared."""
+    count = 0
+    for layer in model.modules():
+        if (AffineParameters.accepts(layer) and layer.bits == 4
+                and layer.scales.dtype == torch.bfloat16 and _on_gfx950(layer.weight)):
+            if _w4_prepared_parameters(layer) is not None:
+                count += 1
+    return count
 
 
 def dispatch_linear(x, projection, *, config: LinearConfig | None = None):
@@ -105,6 +140,9 @@ class AffineParameters(NamedTuple):
     biases: Optional[torch.Tensor]
     group_size: int
     bits: int
+    # derived prefill buffer (ext.prepare_w4a16), passed explicitly like the
+    # reference's prepared arrays; None where the call needs none
+    prepared: Optional[torch.Tensor] = None
 
     @classmethod
     def from_module(cls, layer):
@@ -112,15 +150,20 @@ class AffineParameters(NamedTuple):
 
     @classmethod
     def resolve(cls, layer, shape, dtype, config):
-        """Choose a pure projection and the current tensors. The gfx950 kernels
-        read the native packed layout, so multirow_packed needs no derived
-        buffers (prepare_w4a16_nax4 is the identity)."""
+        """Choose a pure projection and the current tensors. The gfx950 decode
+        kernels read the native packed layout, so multirow_packed needs no
+        repacked weights (prepare_w4a16_nax4 is the identity); shapes that
+        reach the prefill GEMM get the layer's derived buffer, made once per
+        weight set (_w4_prepared_parameters)."""
         params = cls.from_module(layer)
         if config.w4_qmv_backend == "multirow_packed" and params.supports_multirow(
                 shape, dtype, *params):
             prepared = ext.prepare_w4a16_nax4(params.weight, params.scales, params.biases)
             return cls.multirow_packed, cls(*prepared, params.group_size, params.bits)
-        return params.select(shape, dtype, config), params
+        project = params.select(shape, dtype, config)
+        if project is cls.native and params.supports_prepared(shape, dtype, *params):
+            params = params._replace(prepared=_w4_prepared_parameters(layer))
+        return project, params
 
     def select(self, shape, dtype, config: LinearConfig):
         if config.w4_qmv_backend == "multirow" and self.supports_multirow(shape, dtype, *self):
@@ -140,7 +183,7 @@ class AffineParameters(NamedTuple):
         )
 
     @staticmethod
-    def _affine_ok(shape, dtype, weight, scales, biases, group_size, bits):
+    def _affine_ok(shape, dtype, weight, scales, biases, group_size, bits, prepared=None):
         return (
             bits == 4
             and group_size in _GROUPS
@@ -159,35 +202,45 @@ class AffineParameters(NamedTuple):
         )
 
     @staticmethod
-    def supports_splitk(shape, dtype, weight, scales, biases, group_size, bits):
+    def supports_splitk(shape, dtype, weight, scales, biases, group_size, bits, prepared=None):
         """One-row decode geometry (the reference's predicate, widened from its
         measured BF16/G32 shapes to every shape the gfx950 GEMV accepts)."""
         return prod(shape[:-1]) == 1 and AffineParameters._affine_ok(
             shape, dtype, weight, scales, biases, group_size, bits)
 
     @staticmethod
-    def supports_multirow(shape, dtype, weight, scales, biases, group_size, bits):
+    def supports_multirow(shape, dtype, weight, scales, biases, group_size, bits,
+                          prepared=None):
         """Verification geometries: 2..32 rows (reference: exactly 8)."""
         return (len(shape) >= 2 and 2 <= prod(shape[:-1]) <= 32
                 and AffineParameters._affine_ok(shape, dtype, weight, scales, biases,
                                                 group_size, bits))
 
     @staticmethod
-    def native(x, weight, scales, biases, group_size, bits):
-        """mx.quantized_matmul(..., transpose=True, mode="affine") on gfx950."""
-        return ext.affine_quantized_matmul(x, weight, scales, biases, group_size=group_size,
-                                           bits=bits)
+    def supports_prepared(shape, dtype, weight, scales, biases, group_size, bits,
+                          prepared=None):
+        """Shapes that the bf16 prefill GEMM serves (more than 32 rows), where
+        the derived buffer saves the weight half of its prologue."""
+        return (len(shape) >= 2 and prod(shape[:-1]) > 32 and dtype == torch.bfloat16
+                and AffineParameters._affine_ok(shape, dtype, weight, scales, biases,
+                                                group_size, bits))
 
     @staticmethod
-    def multirow(x, weight, scales, biases, group_size, bits):
+    def native(x, weight, scales, biases, group_size, bits, prepared=None):
+        """mx.quantized_matmul(..., transpose=True, mode="affine") on gfx950."""
+        return ext.affine_quantized_matmul(x, weight, scales, biases, group_size=group_size,
+                                           bits=bits, prepared=prepared)
+
+    @staticmethod
+    def multirow(x, weight, scales, biases, group_size, bits, prepared=None):
         return ext.w4a16_multirow(x, weight, scales, biases, algorithm="wide")
 
     @staticmethod
-    def multirow_packed(x, weight, scales, biases, group_size, bits):
+    def multirow_packed(x, weight, scales, biases, group_size, bits, prepared=None):
         return ext.w4a16_multirow(x, weight, scales, biases, algorithm="nax4")
 
     @staticmethod
-    def splitk(x, weight, scales, biases, group_size, bits):
+    def splitk(x, weight, scales, biases, group_size, bits, prepared=None):
         return ext.w4a16_qmv(x, weight, scales, biases)
 
 

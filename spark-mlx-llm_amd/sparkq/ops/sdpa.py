@@ -83,13 +83,19 @@ def _supports_int8(queries, keys, values, *, cache, mask, prefill=False):
 
 
 def _quantized_attention(queries, keys, values, *, cache, scale, mask):
-    """Quantized caches the fused predicate does not take: the reference
-    hands them to mlx-lm's scaled_dot_product_attention, whose quantized
-    branch is the staged quantized_matmul / softmax / quantized_matmul form
-    (the same arithmetic as X/spark_mlx_ext/int8_quantized_sdpa.py:122-153);
-    here int8_quantized_sdpa routes them to the staged-attention kernel
-    (bits 2/4/8, any head dims, mask arrays). Like every sparkq operator it
-    runs only on the device."""
+    """Quantized caches the fused route does not take (or all of them when
+    fused_quantized_sdpa is off): the reference hands them to mlx-lm's
+    scaled_dot_product_attention, whose quantized branch is the staged
+    quantized_matmul / softmax / quantized_matmul form (the same arithmetic
+    as X/spark_mlx_ext/int8_quantized_sdpa.py:122-153); here the MLX affine
+    tuple goes to the staged-attention kernel (bits 2/4/8, any head dims,
+    mask arrays), and the symmetric s8 pair, which has no staged form, to
+    int8_quantized_sdpa. Like every sparkq operator it runs only on the
+    device."""
+    if len(keys) == 3:
+        return ext.staged_quantized_sdpa(queries, keys, values, scale=scale,
+                                         group_size=getattr(cache, "group_size", 32),
+                                         bits=getattr(cache, "bits", 8), mask=mask)
     return ext.int8_quantized_sdpa(queries, keys, values, scale=scale,
                                    group_size=getattr(cache, "group_size", 32),
                                    bits=getattr(cache, "bits", 8), mask=mask)

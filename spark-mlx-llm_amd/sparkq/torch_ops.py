@@ -56,7 +56,10 @@ def affine_quantized_matmul(x: Tensor, weight: Tensor, scales: Tensor, biases: T
 
 @affine_quantized_matmul.register_fake
 def _(x, weight, scales, biases, group_size, bits, out_dtype):
-    return x.new_empty((*_lead(x), weight.shape[0]), dtype=out_dtype or x.dtype)
+    # bits=8 follows MLX's promotion of x with the scales (fp32 scales, as the
+    # converter writes for the lm_head, give an fp32 result); bits=4 keeps x's
+    result = torch.promote_types(x.dtype, scales.dtype) if bits == 8 else x.dtype
+    return x.new_empty((*_lead(x), weight.shape[0]), dtype=out_dtype or result)
 
 
 # --- W8A8 / W8A16 ------------------------------------------------------------

@@ -133,3 +133,32 @@ def test_benchmark_shapes_sampled_heads(gpu, b, n):
                             o.kv_dequantize_s8(kc[:, kh:kh + 1], ks[:, kh:kh + 1]),
                             o.kv_dequantize_s8(vc[:, kh:kh + 1], vs[:, kh:kh + 1]), scale)
         check_fp32(y[:, sl], ref)
+
+
+def test_host_cache_tensors_raise_before_launch(gpu):
+    """Every cache tensor (codes, scales, biases) and the mask must live on the
+    device: a host scales tensor raises ValueError instead of reaching a
+    kernel as a host pointer."""
+    import sparkq
+
+    b, hq, hkv, n, d, g = 1, 8, 2, 40, 128, 32
+    q16, k, v = _problem(b, hq, hkv, n, d, seed=1)
+    kc, ks = o.kv_quantize_s8(k)
+    vc, vs = o.kv_quantize_s8(v)
+    q = up16(q16[:, :, None, :], o.BF16, gpu)
+    kt, vt = torch.from_numpy(kc).to(gpu), torch.from_numpy(vc).to(gpu)
+    kst = torch.from_numpy(ks.view(np.float16))
+    vst = torch.from_numpy(vs.view(np.float16)).to(gpu)
+    with pytest.raises(ValueError, match="GPU"):
+        sparkq.int8_quantized_sdpa(q, (kt, kst), (vt, vst), scale=0.1)
+    kp, aks, akb = o.kv_quantize_affine_u8(k, g, o.BF16)
+    vp, avs, avb = o.kv_quantize_affine_u8(v, g, o.BF16)
+    keys = (up32(kp, gpu), up16(aks, o.BF16, gpu), torch.from_numpy(akb.view(np.int16)).view(
+        torch.bfloat16))
+    vals = (up32(vp, gpu), up16(avs, o.BF16, gpu), up16(avb, o.BF16, gpu))
+    with pytest.raises(ValueError, match="GPU"):    # fused decode
+        sparkq.int8_quantized_sdpa(q, keys, vals, scale=0.1, group_size=g)
+    keys = (keys[0], keys[1], up16(akb, o.BF16, gpu))
+    mask = torch.ones((1, n), dtype=torch.bool)      # staged path, host mask is moved
+    y = sparkq.int8_quantized_sdpa(q, keys, vals, scale=0.1, group_size=g, mask=mask)
+    assert y.device.type == "cuda"

@@ -128,3 +128,39 @@ def test_low_bit_cache_append_and_dispatch(gpu, bits):
                         o.kv_dequantize_affine(kp, ks, kb, g, bits, o.BF16),
                         o.kv_dequantize_affine(vp, vs, vb, g, bits, o.BF16), d ** -0.5)
     assert np.abs(y.float().cpu().numpy() - ref).max() <= 2e-2
+
+
+@pytest.mark.parametrize("qdtype", [o.BF16, o.F16])
+def test_staged_additive_mask_hides_leading_chunks(gpu, qdtype):
+    """Additive masks that hide the first 256-token chunk and the whole first
+    context split (N = 1300 runs in three splits) with -inf and with the
+    dtype's lowest finite value: those tokens weigh nothing and the row stays
+    finite, as in the reference's scores + mask softmax; a row masked
+    everywhere with the lowest finite bf16 value averages every value."""
+    import sparkq
+
+    b, hq, hkv, length, n, d, g, bits = 1, 4, 2, 3, 1300, 64, 64, 4
+    print(f"[case] staged masked lead q={qdtype} N={n}", flush=True)
+    keys, kd = _cache(gpu, b, hkv, n, d, g, bits, qdtype, 5)
+    vals, vd = _cache(gpu, b, hkv, n, d, g, bits, qdtype, 6)
+    q16 = o.round16(o.randn(7, 72, b * hq * length * d).reshape(b, hq, length, d), qdtype)
+    lowest = float(torch.finfo(TORCH16[qdtype]).min)
+    m = (np.random.default_rng(3).standard_normal((1, hq, length, n)) * 2).astype(np.float32)
+    m[:, :, 0, :600] = -np.inf
+    m[:, :, 1, :600] = lowest
+    if qdtype == o.BF16:
+        m[:, :, 2, :] = lowest
+    else:
+        m[:, :, 2, 100:700] = -np.inf
+    mask_t = torch.from_numpy(m).to(TORCH16[qdtype]).to(gpu)
+    mask_ref = o.bits_to_f32(o.round16(m, qdtype), qdtype)
+    scale = 1.0 / math.sqrt(d)
+    y = sparkq.int8_quantized_sdpa(up16(q16, qdtype, gpu), keys, vals, scale=scale,
+                                   group_size=g, bits=bits, mask=mask_t,
+                                   out_dtype=torch.float32).cpu().numpy()
+    assert np.isfinite(y).all()
+    ref = o.sdpa_staged(o.bits_to_f32(q16, qdtype), kd, vd, scale, mask_ref, qdtype)
+    check_fp32(y, ref)
+    if qdtype == o.BF16:
+        mean_v = np.repeat(vd, hq // hkv, axis=1).mean(axis=2)
+        assert np.abs(y[:, :, 2] - mean_v).max() <= 1e-4

@@ -31,6 +31,21 @@ def test_opcheck_affine_quantized_matmul(gpu, m):
                               (x, w, s, b, 64, 4, out_dtype), test_utils=UTILS)
 
 
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32])
+def test_opcheck_affine_w8(gpu, sdt):
+    """bits=8: the result dtype is x's promoted with the scales' (fp32 for the
+    converter's fp32-scaled W8 lm_head), and the fake kernel must say so."""
+    n, k, g = 256, 512, 32
+    x = torch.randn(2, k, device=gpu).to(torch.bfloat16)
+    w = torch.randint(0, 2 ** 31 - 1, (n, k // 4), device=gpu, dtype=torch.int32)
+    s = (torch.rand(n, k // g, device=gpu) * 1e-3 + 1e-4).to(sdt)
+    bb = (-128 * s.float()).to(sdt)
+    y = torch.ops.sparkq.affine_quantized_matmul(x, w, s, bb, g, 8, None)
+    assert y.dtype == torch.promote_types(x.dtype, sdt)
+    torch.library.opcheck(torch.ops.sparkq.affine_quantized_matmul.default,
+                          (x, w, s, bb, g, 8, None), test_utils=UTILS)
+
+
 def test_opcheck_w8a8_and_quantizer(gpu):
     xf = torch.randn(8, 512, device=gpu).to(torch.bfloat16)
     w = torch.randint(-127, 128, (256, 512), device=gpu, dtype=torch.int8)

@@ -176,6 +176,26 @@ def test_gemm_tile_rows(gpu, m, n, k, g, monkeypatch):
     assert torch.equal(outs["0"], outs["1"])
 
 
+@pytest.mark.parametrize("m,n,k", [(1024, 4096, 2560), (1024, 4096, 2624), (1024, 4096, 2688),
+                                   (1024, 4096, 2752), (384, 23040, 1536)])
+def test_gemm_schedule_variants_bit_identical(gpu, m, n, k, monkeypatch):
+    """The 128-row-tile GEMM's schedule variants (wave priority over the MFMA
+    phase; four A slots with a barrier every second step) change neither
+    the operands nor the summation order: every variant gives the default's
+    bits, over step counts of every remainder mod 4 and a grid whose tiles
+    past the CUs split along k; the default matches the oracle."""
+    g = 64
+    x, wq, s, b = w4_problem(m, n, k, g, seed=k + n)
+    outs = {}
+    for sch in ("0", "1", "2", "3"):
+        monkeypatch.setenv("SPARKQ_W4_GEMM_SCH", sch)
+        outs[sch] = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    for sch in ("1", "2", "3"):
+        assert torch.equal(outs[sch], outs["0"]), sch
+    cols = np.sort(np.random.default_rng(k).choice(n, size=96, replace=False))
+    check_fp32(outs["0"].cpu().numpy()[:, cols], o.w4a16_matmul(x, wq[cols], s[cols], b[cols], g))
+
+
 @pytest.mark.parametrize("m,n,k,g", [(1, 37, 576, 32), (3, 41, 576, 64), (2, 4, 64, 32),
                                      (4, 130, 9728, 32), (1, 5, 10240, 128), (3, 9, 4608, 64)])
 def test_decode_ragged_shapes(gpu, m, n, k, g):

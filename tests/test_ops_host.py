@@ -281,3 +281,22 @@ def test_layer_dispatch_contract_on_host():
         dispatch_qkv(torch.zeros(1, 2, 24, dtype=torch.bfloat16), proj, rope, q_size=8,
                      kv_size=8, n_heads=1, n_kv_heads=1, head_dim=8, offset=0)
     assert calls[-1] == (1, 2, 24)
+
+
+def test_prepared_buffer_host_rules():
+    """The derived prefill buffer: routed only for more than 32 bf16 rows on
+    the device (never on host tensors), fp16 scales have no prepared form,
+    and the operators reject a malformed buffer before any device call."""
+    layer = _layer()
+    p = AffineParameters.from_module(layer)
+    assert p.prepared is None and len(p) == 6
+    assert not AffineParameters.supports_prepared((64, 256), torch.bfloat16, *p)
+    assert ext.prepare_w4a16(layer.weight, layer.scales.half(), layer.biases.half()) is None
+    with pytest.raises(ValueError, match="GPU"):
+        ext.prepare_w4a16(layer.weight, layer.scales, layer.biases)
+    with pytest.raises(ValueError, match="group_size"):
+        ext.prepare_w4a16(layer.weight, layer.scales, layer.biases, group_size=48)
+    x = torch.zeros((64, 256), dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        ext.affine_quantized_matmul(x, layer.weight, layer.scales, layer.biases, group_size=64,
+                                    prepared=torch.zeros(8, dtype=torch.uint8))

@@ -33,6 +33,12 @@ def test_linear_fakes(lead):
     assert torch.ops.sparkq.affine_quantized_matmul(x, w4, s, s, 64, 4, None).shape == (*lead, 3584)
     y = torch.ops.sparkq.affine_quantized_matmul(x, w4, s, s, 64, 4, torch.float32)
     assert y.dtype == torch.float32
+    # bits=8 promotes x with the scales: fp32 scales (the W8 lm_head) give fp32
+    w8p, s8 = t(3584, 640, dtype=torch.uint32), t(3584, 80, dtype=torch.float32)
+    y8 = torch.ops.sparkq.affine_quantized_matmul(x, w8p, s8, s8, 32, 8, None)
+    assert y8.shape == (*lead, 3584) and y8.dtype == torch.float32
+    y8 = torch.ops.sparkq.affine_quantized_matmul(x, w8p, t(3584, 80), t(3584, 80), 32, 8, None)
+    assert y8.dtype == BF
     w8, sw = t(512, 2560, dtype=torch.int8), t(512, dtype=torch.float32)
     assert torch.ops.sparkq.w8a8_linear(x, w8, sw, None, None).shape == (*lead, 512)
     q, sa = torch.ops.sparkq.quantize_per_token(x)
