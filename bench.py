@@ -223,6 +223,34 @@ def bench_w8a8(torch, sparkq, dev, m, iters, copies=36):
     return res
 
 
+def bench_w8a8_prefill(torch, sparkq, dev, iters, copies=8):
+    """W8A8 at prefill sizes on the out_proj shape N=2560, K=4096 (the
+    reference serves out_proj at any M): the whole w8a8_linear call (per-token
+    quantizer, int8 GEMM, fp32 epilogue, bf16 out) over 8 distinct weight
+    sets per graph replay; int8 ops 2*M*N*K against the 5 POP/s dense peak."""
+    res = {}
+    n, k = 2560, 4096
+    gen = torch.Generator(device=dev).manual_seed(3)
+    ws = [(torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=gen),
+           torch.rand(n, device=dev, generator=gen) * 1e-3) for _ in range(copies)]
+    for m in (512, 2048):
+        x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+
+        def fn():
+            for q, sc in ws:
+                sparkq.w8a8_linear(x, q, sc, out=y)
+
+        graph = capture(torch, fn)
+        ms = Timer(torch).time(graph.replay, iters, 2) / copies
+        tops = 2 * m * n * k / (ms / 1e3) / 1e12
+        res[f"M={m} N={n} K={k}"] = {"ms": round(ms, 5), "TOP/s": round(tops, 1),
+                                     "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        del graph
+    del ws
+    return res
+
+
 def bench_w8a16(torch, sparkq, dev, iters):
     """W8A16 per-channel GEMV at M=1: the projections (36 distinct weight
     sets) and the W8 lm_head 131072 x 2560 (335 MB, 3 distinct copies)."""
@@ -269,6 +297,45 @@ def bench_sdpa(torch, sparkq, dev, b, n, iters):
 
     graph = capture(torch, fn)
     ms = Timer(torch).time(graph.replay, iters, 2) / copies
+    return {"ms": round(ms, 5), "GB/s": round(kv_bytes / ms / 1e6, 1),
+            "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": kv_bytes}
+
+
+def bench_low_bit_decode(torch, sparkq, dev, n, iters, bits=4, g=64, staged=False):
+    """Decode attention over a 4-bit MLX affine cache (mlx-lm's kv_bits=4,
+    group 64; the reference attends it through its staged _fallback): B=1,
+    32/8 heads, D=128, one query token, on the one-pass decode kernel over
+    the codes, or (staged=True) on the staged-attention kernel, forced with
+    an all-visible boolean mask. GB/s of the cache bytes read (codes plus
+    bf16 scales and biases)."""
+    hq, hkv, d, b = 32, 8, 128, 1
+    words = d * bits // 32
+    kv_bytes = 2 * b * hkv * n * (words * 4 + 2 * 2 * (d // g))
+    copies = max(1, min(32, (600 << 20) // kv_bytes))
+    gen = torch.Generator(device=dev).manual_seed(4)
+
+    def part():
+        packed = torch.randint(-2 ** 31, 2 ** 31 - 1, (b, hkv, n, words), dtype=torch.int32,
+                               device=dev, generator=gen)
+        sc = (torch.rand((b, hkv, n, d // g), device=dev, generator=gen) * 0.1 + 0.01)
+        bi = -sc * 7.5
+        return packed, sc.to(torch.bfloat16), bi.to(torch.bfloat16)
+
+    caches = [(part(), part()) for _ in range(copies)]
+    q = torch.randn((b, hq, 1, d), device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(d)
+
+    mask = torch.ones((1, n), dtype=torch.bool, device=dev) if staged else None
+
+    def fn():
+        for keys, vals in caches:
+            sparkq.int8_quantized_sdpa(q, keys, vals, scale=scale, group_size=g, bits=bits,
+                                       mask=mask, out=out)
+
+    graph = capture(torch, fn)
+    ms = Timer(torch).time(graph.replay, iters, 2) / copies
+    del graph, caches
     return {"ms": round(ms, 5), "GB/s": round(kv_bytes / ms / 1e6, 1),
             "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": kv_bytes}
 
@@ -722,11 +789,17 @@ def main():
         del prepared
         log("W8A8")
         extras["w8a8"] = {f"M={m}": bench_w8a8(torch, sparkq, dev, m, 5) for m in (1, 8, 16)}
+        extras["w8a8_prefill"] = bench_w8a8_prefill(torch, sparkq, dev, 5)
         log("W8A16")
         extras["w8a16_m1"] = bench_w8a16(torch, sparkq, dev, 5)
         log("INT8-KV decode attention")
         extras["int8kv_sdpa_decode"] = {f"B={b} N={n}": bench_sdpa(torch, sparkq, dev, b, n, 5)
                                         for b in (1, 8) for n in (4096, 32768)}
+        extras["sdpa_decode_4bit"] = {f"B=1 N={n}": bench_low_bit_decode(torch, sparkq, dev, n, 5)
+                                      for n in (4096, 32768)}
+        extras["staged_sdpa_decode_4bit"] = {
+            f"B=1 N={n}": bench_low_bit_decode(torch, sparkq, dev, n, 3, staged=True)
+            for n in (4096, 32768)}
         log("INT8-KV prefill attention and KV append")
         extras["int8kv_sdpa_prefill_causal"] = {
             f"L={l} N={n}": bench_prefill(torch, sparkq, dev, l, n, 5)

@@ -273,7 +273,11 @@ int sparkq_w8_affine_linear(const void* x, const uint32_t* w, const void* scales
  * Replaces int8_quantized_sdpa (X/spark_mlx_ext/int8_quantized_sdpa.py:
  * 156-287) and its kernels spark_affine_u8_sdpa_{decode,merge,short}
  * (X/spark_mlx_ext/_int8_sdpa_sources.py:8-376). D in {64,128,256};
- * Hq/Hkv in {1,2,4,8}; for the affine format group_size in {32,64,128}.
+ * Hq/Hkv in {1,2,4,8}; for the affine formats group_size in {32,64,128}.
+ * kv_format may also be SPARKQ_KV_AFFINE_U4 or SPARKQ_KV_AFFINE_U2 (the
+ * 4- and 2-bit MLX tuples of mlx-lm's QuantizedKVCache, which the reference
+ * attends through its staged _fallback, X/spark_mlx_ext/
+ * int8_quantized_sdpa.py:122-153): the same one-pass decode on their codes.
  * ---------------------------------------------------------------------- */
 size_t sparkq_int8kv_sdpa_workspace_bytes(int64_t B, int64_t Hq, int64_t N,
                                           int64_t D);

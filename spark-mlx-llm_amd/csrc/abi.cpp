@@ -396,9 +396,10 @@ static int check_sdpa_decode(const void* q, const void* k_codes, const void* k_s
   REQUIRE(is_float_dtype(q_dtype), "Q and metadata must be float16, bfloat16 or float32");
   REQUIRE(out_dtype == q_dtype || out_dtype == SPARKQ_F32,
           "int8kv_sdpa_decode: out dtype must equal q dtype or be float32");
-  REQUIRE(kv_format == SPARKQ_KV_S8_F16SCALE || kv_format == SPARKQ_KV_AFFINE_U8,
+  REQUIRE(kv_format == SPARKQ_KV_S8_F16SCALE || kv_format == SPARKQ_KV_AFFINE_U8 ||
+              kv_format == SPARKQ_KV_AFFINE_U4 || kv_format == SPARKQ_KV_AFFINE_U2,
           "int8kv_sdpa_decode: unknown kv_format %d", kv_format);
-  if (kv_format == SPARKQ_KV_AFFINE_U8) {
+  if (kv_format != SPARKQ_KV_S8_F16SCALE) {
     REQUIRE(k_biases && v_biases, "int8kv_sdpa_decode: affine format needs biases");
     REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
             "Supported affine formats: bits 2/4/8, group size 32/64/128");

@@ -354,6 +354,30 @@ __device__ __forceinline__ float load_in(const void* p, int64_t idx, int dtype) 
 // partial stores are performed (s_waitcnt 0) before bumping the tile counter,
 // so the workgroup that sees the count reach S-1 finds every partial in
 // place; it resets the counter to zero for the next launch.
+//
+// Why relaxed atomics suffice here (the ordering argument). On gfx942/gfx950
+// the LLVM AMDGPU memory model implements an agent-scope release as
+// "buffer_wbl2 sc1; s_waitcnt vmcnt(0)" before the flag access and an
+// acquire as "s_waitcnt vmcnt(0); buffer_inv sc1" after it, and a relaxed
+// agent-scope load or store as the plain access with the sc1 cache policy,
+// which is coherent at the device coherence point by itself. The L2
+// writeback and invalidate exist only for data accessed WITHOUT sc1 (dirty
+// or stale lines in one XCD's L2). Here every access to the exchanged data
+// is an sc1 access: the partial stores (splitk_store, or raw buffer stores
+// with the sc1 policy bit) and the partial loads (splitk_load, or raw
+// buffer loads with sc1). What remains of release/acquire is the ordering,
+// and the hardware gives it as follows:
+//  * writer: s_waitcnt vmcnt(0) returns only after every store of the
+//    thread has been acknowledged, and an sc1 store is acknowledged once it
+//    is performed at the coherence point; the barrier then orders all
+//    threads' completed stores before thread 0 issues the counter RMW;
+//  * reader: the partial loads are issued only after the RMW has returned
+//    its value (the branch on it, broadcast through LDS and a barrier), so
+//    they are performed after it, and being sc1 they read the coherence
+//    point, not a stale L2 line.
+// The same holds for the producer/consumer counters of the W8A8 one-launch
+// quantizer. A full acq_rel RMW would add an L2 writeback and invalidate of
+// the whole XCD L2 per arrival, which the protocol does not need.
 template <typename V>
 __device__ __forceinline__ void splitk_store(V* p, V v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -65,12 +65,48 @@ __device__ __forceinline__ float exp2_guarded(float x_minus_m, bool live) {
   return live ? __builtin_amdgcn_exp2f(x_minus_m) : 0.0f;
 }
 
+// Code width of the decode formats: FMT 0 symmetric s8, 1 affine u8, 2
+// affine u4, 3 affine u2 (the MLX packing, code j of a word at bits*j).
+template <int FMT>
+struct KvCodes {
+  static constexpr int BITS = FMT <= 1 ? 8 : (FMT == 2 ? 4 : 2);
+};
+
+// the lane's CB bytes of codes of one token (8, 4 or 2)
+template <int CB>
+__device__ __forceinline__ uint2 load_codes(const uint8_t* p) {
+  if constexpr (CB == 8) return *reinterpret_cast<const uint2*>(p);
+  if constexpr (CB == 4) return uint2{*reinterpret_cast<const uint32_t*>(p), 0u};
+  return uint2{(uint32_t)*reinterpret_cast<const uint16_t*>(p), 0u};
+}
+
+// code i of the lane's codes (little-endian bytes, BITS per code)
+template <int BITS>
+__device__ __forceinline__ uint32_t code_at(uint2 w, int i) {
+  constexpr int PW = 32 / BITS;  // codes per word
+  const uint32_t word = i < PW ? w.x : w.y;
+  return (word >> (BITS * (i % PW))) & ((1u << BITS) - 1u);
+}
+
+// DPL dims per lane: 8 for 8-bit codes; 16 for 4- and 2-bit codes (8 or 4
+// bytes a lane and token) up to four query heads per KV head, 8 above (the
+// query and accumulator registers grow with DPL * GQA). DPL divides every
+// group size, so a lane's dims share one (scale, bias).
+template <int FMT, int GQA>
+__host__ __device__ constexpr int decode_dpl() {
+  return FMT <= 1 || GQA > 4 ? 8 : 16;
+}
+
 template <int D, int GQA, int FMT>
 __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
-  constexpr int LPT = D / 8;         // lanes per token
+  constexpr int BITS = KvCodes<FMT>::BITS;
+  constexpr int DPL = decode_dpl<FMT, GQA>();  // dims per lane
+  constexpr int CB = DPL * BITS / 8;           // code bytes per lane and token
+  constexpr int LPT = D / DPL;       // lanes per token
   constexpr int TPW = 64 / LPT;      // token slots per wave
   constexpr int SLOTS = 4 * TPW;     // token slots per workgroup
   constexpr int TU = 4;              // tokens per slot per block
+  constexpr bool AFF = FMT >= 1;     // affine (scale, bias per group)
   __shared__ float wm[4][GQA], wz[4][GQA];
   __shared__ __attribute__((aligned(16))) float wacc[4][GQA][D];
 
@@ -78,34 +114,34 @@ __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
   const int split = blockIdx.x;
   const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
   const int slot = wave * TPW + lane / LPT;
-  const int dl = lane % LPT, d0 = dl * 8;
+  const int dl = lane % LPT, d0 = dl * DPL;
   const int t_begin = split * a.tps;
   const int t_end = min(a.N, t_begin + a.tps);
 
-  float qf[GQA][8], qsum[GQA];
+  float qf[GQA][DPL], qsum[GQA];
 #pragma unroll
   for (int h = 0; h < GQA; ++h) {
     const int64_t qo = ((int64_t)b * a.Hq + kh * GQA + h) * D + d0;
     qsum[h] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < DPL; ++i) {
       qf[h][i] = load_in(a.q, qo + i, a.q_dtype) * a.scale_log2;
       qsum[h] += qf[h][i];
     }
   }
 
-  const uint8_t* kcb = a.kc + b * a.kc_b + kh * a.kc_h + d0;
-  const uint8_t* vcb = a.vc + b * a.vc_b + kh * a.vc_h + d0;
-  const int64_t ksb = b * a.ks_b + kh * a.ks_h + (FMT == 1 ? d0 / a.G : 0);
-  const int64_t vsb = b * a.vs_b + kh * a.vs_h + (FMT == 1 ? d0 / a.G : 0);
+  const uint8_t* kcb = a.kc + b * a.kc_b + kh * a.kc_h + d0 * BITS / 8;
+  const uint8_t* vcb = a.vc + b * a.vc_b + kh * a.vc_h + d0 * BITS / 8;
+  const int64_t ksb = b * a.ks_b + kh * a.ks_h + (AFF ? d0 / a.G : 0);
+  const int64_t vsb = b * a.vs_b + kh * a.vs_h + (AFF ? d0 / a.G : 0);
 
-  float mrun[GQA], zrun[GQA], acc[GQA][8];
+  float mrun[GQA], zrun[GQA], acc[GQA][DPL];
 #pragma unroll
   for (int h = 0; h < GQA; ++h) {
     mrun[h] = kNegInf;
     zrun[h] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[h][i] = 0.0f;
+    for (int i = 0; i < DPL; ++i) acc[h][i] = 0.0f;
   }
 
   for (int t0 = t_begin + slot; t0 < t_end; t0 += SLOTS * TU) {
@@ -117,8 +153,8 @@ __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
       const int t = t0 + u * SLOTS;
       valid[u] = t < t_end;
       const int64_t tu = valid[u] ? t : t0;
-      kw[u] = *reinterpret_cast<const uint2*>(kcb + tu * a.kc_t);
-      vw[u] = *reinterpret_cast<const uint2*>(vcb + tu * a.vc_t);
+      kw[u] = load_codes<CB>(kcb + tu * a.kc_t);
+      vw[u] = load_codes<CB>(vcb + tu * a.vc_t);
       if constexpr (FMT == 0) {
         ksc[u] = f16_to_f32(reinterpret_cast<const uint16_t*>(a.ks)[ksb + tu * a.ks_t]);
         vsc[u] = f16_to_f32(reinterpret_cast<const uint16_t*>(a.vs)[vsb + tu * a.vs_t]);
@@ -135,19 +171,18 @@ __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
     float sc[TU][GQA];
 #pragma unroll
     for (int u = 0; u < TU; ++u) {
-      float kv[8];
+      float kv[DPL];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t word = i < 4 ? kw[u].x : kw[u].y;
-        const uint32_t byte = (word >> (8 * (i & 3))) & 0xFFu;
-        kv[i] = FMT == 0 ? (float)(int8_t)byte : (float)byte;
+      for (int i = 0; i < DPL; ++i) {
+        const uint32_t c = code_at<BITS>(kw[u], i);
+        kv[i] = FMT == 0 ? (float)(int8_t)c : (float)c;
       }
 #pragma unroll
       for (int h = 0; h < GQA; ++h) {
         float p = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) p = fmaf(qf[h][i], kv[i], p);
-        if constexpr (FMT == 1) p = fmaf(ksc[u], p, kbi[u] * qsum[h]);
+        for (int i = 0; i < DPL; ++i) p = fmaf(qf[h][i], kv[i], p);
+        if constexpr (AFF) p = fmaf(ksc[u], p, kbi[u] * qsum[h]);
 #pragma unroll
         for (int off = LPT / 2; off > 0; off >>= 1) p += __shfl_xor(p, off);
         if constexpr (FMT == 0) p *= ksc[u];
@@ -171,15 +206,14 @@ __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
       zrun[h] = fmaf(zrun[h], alpha, zs);
       mrun[h] = mb;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] *= alpha;
+      for (int i = 0; i < DPL; ++i) acc[h][i] *= alpha;
 #pragma unroll
       for (int u = 0; u < TU; ++u) {
         const float pw = FMT == 0 ? p[u] * vsc[u] : p[u];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t word = i < 4 ? vw[u].x : vw[u].y;
-          const uint32_t byte = (word >> (8 * (i & 3))) & 0xFFu;
-          const float vv = FMT == 0 ? (float)(int8_t)byte : fmaf((float)byte, vsc[u], vbi[u]);
+        for (int i = 0; i < DPL; ++i) {
+          const uint32_t c = code_at<BITS>(vw[u], i);
+          const float vv = FMT == 0 ? (float)(int8_t)c : fmaf((float)c, vsc[u], vbi[u]);
           acc[h][i] = fmaf(pw, vv, acc[h][i]);
         }
       }
@@ -198,7 +232,7 @@ __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
       const float wb = exp2_guarded(mo - mm, mo != kNegInf);
       zrun[h] = zrun[h] * wa + zo * wb;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < DPL; ++i) {
         const float ao = __shfl_xor(acc[h][i], off);
         acc[h][i] = acc[h][i] * wa + ao * wb;
       }
@@ -213,7 +247,7 @@ __global__ __launch_bounds__(256) void sdpa_decode_kernel(SdpaArgs a) {
         wz[wave][h] = zrun[h];
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) wacc[wave][h][d0 + i] = acc[h][i];
+      for (int i = 0; i < DPL; ++i) wacc[wave][h][d0 + i] = acc[h][i];
     }
   }
   __syncthreads();
@@ -1561,8 +1595,12 @@ template <int D, int GQA>
 static void launch_decode_g(const SdpaArgs& a, int fmt, dim3 grid, hipStream_t st) {
   if (fmt == SPARKQ_KV_S8_F16SCALE)
     hipLaunchKernelGGL((sdpa_decode_kernel<D, GQA, 0>), grid, dim3(256), 0, st, a);
-  else
+  else if (fmt == SPARKQ_KV_AFFINE_U8)
     hipLaunchKernelGGL((sdpa_decode_kernel<D, GQA, 1>), grid, dim3(256), 0, st, a);
+  else if (fmt == SPARKQ_KV_AFFINE_U4)
+    hipLaunchKernelGGL((sdpa_decode_kernel<D, GQA, 2>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((sdpa_decode_kernel<D, GQA, 3>), grid, dim3(256), 0, st, a);
 }
 
 template <int D>

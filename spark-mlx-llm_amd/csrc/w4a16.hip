@@ -2911,7 +2911,14 @@ static void launch_gemm_x16(int G, const void* x, const uint32_t* w, const void*
     else if (G == 64) SPARKQ_X16W(64, 2, 1);
     else SPARKQ_X16W(128, 2, 1);
   } else {
-    const int sch = env_int("SPARKQ_W4_GEMM_SCH", 0);
+    // schedule variant (SCH bits): priority over the MFMA phase with four A
+    // slots and a barrier every second step is the default, measured per
+    // call with prepared weights against the plain schedule: gate+up 19456 x
+    // 2560 M = 2048 231.2 -> 227.0 us, M = 512 75.2-76.2 -> 73.6-75.0 us,
+    // QKV and down at M = 2048 within 1%. The four slots alone ran slower
+    // (240 us), the priority alone the same (231.2 us).
+    // SPARKQ_W4_GEMM_SCH = 1..3 picks a variant, any other value the plain one
+    const int sch = env_int("SPARKQ_W4_GEMM_SCH", 3);
     if (sch == 1) {
       if (G == 32) SPARKQ_X16S(32, 1);
       else if (G == 64) SPARKQ_X16S(64, 1);

@@ -318,6 +318,189 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Segment-major variant (w4_mr16s_kernel), the default. The tile-major
+// kernel above stages the M activation rows of its K range in LDS for every
+// workgroup (80 KB at 16 x 2560), passes them once more for the group sums,
+// and reads them back per item; at one or two row tiles per workgroup (QKV
+// 3584 x 2560: 224 tiles on 256 CUs) that chain, not the weight stream, sets
+// its time. Here:
+//  * the weight loads of the wave go out first (a 16-byte piece of row r16
+//    of every tile of the workgroup at byte 16*(l/16) of each of the wave's
+//    128-k segments, contiguous segments per wave);
+//  * then the segment's activations, straight into registers in the A
+//    operand layout (row l%16, k 8*(l/16) .. +7 of each 32-k chunk; rows
+//    past M read zeros), each loaded once per workgroup and reused by all of
+//    its tiles;
+//  * the group sums X_g come from one more 16x16x32 MFMA per chunk against
+//    an all-ones operand (exact products, fp32 sums), lane (g, r) receiving
+//    the sums of activation rows 4g .. 4g+3 that its outputs need;
+//  * per group the epilogue s*D + (b - OFFSET*s)*X_g of the tile-major kernel;
+//  * every wave leaves its per-tile sums in an LDS slot, and each output is
+//    the sum of the waves' slots in wave order (deterministic).
+// Waves: NW = ceil(SEG / NS) with NS = ceil(SEG / 16) segments each, so the
+// segments divide evenly (K = 2560: 10 waves of two segments; K = 9728: 16
+// waves of five, the last of one).
+struct MrsArgs {
+  const uint16_t* x;
+  const uint32_t* w;
+  const uint16_t* sc;
+  const uint16_t* bi;
+  void* y;
+  const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
+  int y_dtype;
+  int M, N, K;
+  int nt;  // row tiles of 16
+  int P;   // workgroups (tile ranges)
+  int TW;  // tiles of the largest workgroup
+  int NS;  // segments per wave
+};
+
+struct MrsLds {
+  int sb;    // (scale, bias) of the workgroup's rows [16*TW][K/G] dwords
+  int part;  // per-wave tile sums [NW][TW][16][16] fp32
+  int bytes;
+};
+__host__ __device__ __forceinline__ MrsLds mrs_lds(int K, int TW, int NW, int G) {
+  MrsLds l;
+  l.sb = 0;
+  l.part = (TW * 16 * (K / G) * 4 + 15) & ~15;
+  l.bytes = l.part + NW * TW * 1024;
+  return l;
+}
+
+template <typename T, int G, int TWM, int NSM>
+__global__ __launch_bounds__(1024) void w4_mr16s_kernel(MrsArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int nthr = blockDim.x, NW = nthr >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r16 = lane & 15;
+  const int M = a.M, N = a.N, K = a.K;
+  const int ng = K / G, SEG = K >> 7, RB = K >> 1;
+  const int t0 = (int)((int64_t)blockIdx.x * a.nt / a.P);
+  const int ntl = (int)((int64_t)(blockIdx.x + 1) * a.nt / a.P) - t0;  // tiles of this workgroup
+  const int s0 = wave * a.NS;
+  const int ns = max(0, min(a.NS, SEG - s0));                           // segments of this wave
+  const MrsLds L = mrs_lds(K, a.TW, NW, G);
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+
+  // 1. loads, every one issued on every path (out-of-range offsets read
+  // zeros): weights, activations, then the (scale, bias) pieces of the
+  // workgroup's 16 * ntl contiguous rows
+  u32x4_t wv[NSM][TWM];
+#pragma unroll
+  for (int i = 0; i < NSM; ++i)
+#pragma unroll
+    for (int t = 0; t < TWM; ++t) {
+      const int row = 16 * (t0 + t) + r16;
+      const bool ok = i < ns && t < ntl && row < N;
+      wv[i][t] = buf_load16(rw, ok ? (uint32_t)row * RB + 64u * (uint32_t)(s0 + i) + 16u * g : kOob);
+    }
+  u32x4_t av[NSM][4];
+#pragma unroll
+  for (int i = 0; i < NSM; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bool ok = i < ns && r16 < M;
+      av[i][c] = buf_load16(rx, ok ? 2u * (uint32_t)(r16 * K + 128 * (s0 + i) + 32 * c + 8 * g) : kOob);
+    }
+  const int nsp = (ntl * 16 * ng) >> 3;
+  u32x4_t sr[2], br[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int pi = tid + h * nthr;
+    const uint32_t off = pi < nsp ? 32u * (uint32_t)t0 * ng + 16u * pi : kOob;
+    sr[h] = buf_load16(rs, off);
+    br[h] = buf_load16(rb, off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. (scale, bias) pairs to LDS
+  uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int pi = tid + h * nthr;
+    if (pi < nsp) {
+      u32x4_t lo, hi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = __builtin_amdgcn_perm(br[h][e], sr[h][e], 0x05040100u);  // (s0, b0)
+        hi[e] = __builtin_amdgcn_perm(br[h][e], sr[h][e], 0x07060302u);  // (s1, b1)
+      }
+      *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+      *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+    }
+  }
+  __syncthreads();
+
+  // 3. per segment and 32-k chunk: the group-sum MFMA, one MFMA per tile,
+  // and per group the scale epilogue of every tile
+  const DecodeConsts dc = decode_consts<T>();
+  const uint32_t one2 = T::code == SPARKQ_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const u32x4_t ones = {one2, one2, one2, one2};
+  f32x4_t acc[TWM];
+#pragma unroll
+  for (int t = 0; t < TWM; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int GPS = 128 / G;  // groups per segment
+  constexpr int CPG = G / 32;   // 32-k chunks per group
+#pragma unroll
+  for (int i = 0; i < NSM; ++i) {
+    if (i < ns) {
+      const int s = s0 + i;
+      // the segment's group sums first, then one tile at a time (a single
+      // tile's partial product stays live across the chunks of a group)
+      f32x4_t xg[GPS];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        xg[c / CPG] = mfma16x16x32<T>(av[i][c], ones,
+                                      c % CPG == 0 ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : xg[c / CPG]);
+#pragma unroll
+      for (int t = 0; t < TWM; ++t) {
+        if (t < ntl) {
+          const u32x4_t wt = transpose_rows(wv[i][t]);
+          f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            d = mfma16x16x32<T>(av[i][c], decode_w4<T>(wt[c], dc), d);
+            if ((c + 1) % CPG == 0) {
+              const uint32_t pair = sb[(t * 16 + r16) * ng + s * GPS + c / CPG];
+              const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
+              const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sf, d[r], fmaf(bf, xg[c / CPG][r], acc[t][r]));
+              d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // 4. per-wave tile sums to LDS (every wave writes its slots, zeros when it
+  // had no segment), then each output adds the waves' slots in wave order
+  float* part = reinterpret_cast<float*>(smem + L.part);
+#pragma unroll
+  for (int t = 0; t < TWM; ++t)
+    if (t < ntl)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[(wave * a.TW + t) * 256 + (4 * g + r) * 16 + r16] = acc[t][r];
+  __syncthreads();
+  for (int e = tid; e < ntl * 256; e += nthr) {
+    const int t = e >> 8, m = (e >> 4) & 15, j = e & 15;
+    const int n = 16 * (t0 + t) + j;
+    if (m >= M || n >= N) continue;
+    float v = 0.0f;
+    for (int w = 0; w < NW; ++w) v += part[(w * a.TW + t) * 256 + m * 16 + j];
+    const int64_t idx = (int64_t)m * N + n;
+    store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 // Plan: 9..16 rows (from 2 with SPARKQ_W4_MR_MIN), K a multiple of 128, the
@@ -400,9 +583,88 @@ static void launch_mr(const MrPlan& p, int G, const MrArgs& a, hipStream_t st) {
     launch_mr_g<T, 128>(p, a, st);
 }
 
+// Plan of the segment-major kernel: 9..16 rows (SPARKQ_W4_MR_MIN lowers
+// it), K a multiple of 128 with at most 8 segments per wave, one workgroup
+// per CU over contiguous tile ranges, the (scale, bias) pieces within two per
+// thread, the register arrays (tiles x segments) within 16 pieces, LDS within
+// 160 KB. SPARKQ_W4_MR_TILED keeps the tile-major kernel.
+struct MrsPlan {
+  bool ok;
+  int P, TW, NS, NW, TWM, NSM;
+  size_t lds;
+};
+
+static MrsPlan plan_mrs(int64_t M, int64_t N, int64_t K, int G) {
+  MrsPlan p{};
+  if (M < env_int("SPARKQ_W4_MR_MIN", 9) || M > 16 || env_int("SPARKQ_W4_NO_MR", 0) ||
+      env_int("SPARKQ_W4_MR_TILED", 0))
+    return p;
+  if (K % 128 != 0 || K % G != 0) return p;
+  if (N * (K / 2) >= (int64_t)kOob || M * K * 2 >= (int64_t)kOob) return p;
+  const int64_t ng = K / G, SEG = K / 128;
+  if ((N * ng * 2) % 16 != 0) return p;
+  const int64_t nt = cdiv(N, 16), cus = device_cus();
+  p.NS = (int)cdiv(SEG, 16);
+  p.NW = (int)cdiv(SEG, p.NS);
+  p.P = (int)std::min<int64_t>(nt, cus);
+  p.TW = (int)cdiv(nt, p.P);
+  // It pays where the tile-major kernel's staging outweighs its weight
+  // stream: one row tile per workgroup over rows of at most 32 segments.
+  // Measured per projection at 9 / 12 / 16 rows (bf16, G64, 36 weight
+  // sets), segment-major against tile-major: QKV 3584 x 2560 5.3 / 5.7 /
+  // 6.1 against 7.1 / 7.1 / 7.5 us; gate+up 19456 x 2560 (five tiles per
+  // workgroup) 14.4 / 14.8 / 15.3 against 14.2 / 14.4 / 15.1; down 2560 x
+  // 9728 (one tile, 76 segments, 311 KB of activations per workgroup)
+  // 13.3 / 14.9 / 16.6 against 14.8 / 13.3 / 13.6 in four K ranges.
+  // SPARKQ_W4_MR_SEG takes every shape the instantiations below fit: (1, 2),
+  // (2, 2), (5, 2) and (1, 5) tiles x segments stay within the 128 VGPRs of
+  // 16-wave workgroups.
+  const bool all = env_int("SPARKQ_W4_MR_SEG", 0) != 0;
+  if (!all && (p.TW > 1 || p.NS > 2)) return p;
+  p.TWM = p.TW <= 1 ? 1 : p.TW <= 2 ? 2 : 5;
+  p.NSM = p.NS <= 2 ? 2 : 5;
+  if (p.NS > 5 || p.TW > 5 || (p.NSM == 5 && p.TWM > 1)) return p;
+  if ((int64_t)p.TW * 16 * ng / 8 > 2LL * 64 * p.NW) return p;
+  const MrsLds l = mrs_lds((int)K, p.TW, p.NW, G);
+  if (l.bytes > kMrMaxLds) return p;
+  p.lds = (size_t)l.bytes;
+  p.ok = true;
+  return p;
+}
+
+template <typename T, int G, int TWM, int NSM>
+static void launch_mrs_k(const MrsPlan& p, const MrsArgs& a, hipStream_t st) {
+  auto* k = w4_mr16s_kernel<T, G, TWM, NSM>;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, kMrMaxLds);
+  (void)attr;
+  hipLaunchKernelGGL(k, dim3((unsigned)p.P), dim3(64 * p.NW), p.lds, st, a);
+}
+template <typename T, int G>
+static void launch_mrs_g(const MrsPlan& p, const MrsArgs& a, hipStream_t st) {
+  if (p.NSM == 5)
+    launch_mrs_k<T, G, 1, 5>(p, a, st);
+  else if (p.TWM == 1)
+    launch_mrs_k<T, G, 1, 2>(p, a, st);
+  else if (p.TWM == 2)
+    launch_mrs_k<T, G, 2, 2>(p, a, st);
+  else
+    launch_mrs_k<T, G, 5, 2>(p, a, st);
+}
+template <typename T>
+static void launch_mrs(const MrsPlan& p, int G, const MrsArgs& a, hipStream_t st) {
+  if (G == 32)
+    launch_mrs_g<T, 32>(p, a, st);
+  else if (G == 64)
+    launch_mrs_g<T, 64>(p, a, st);
+  else
+    launch_mrs_g<T, 128>(p, a, st);
+}
+
 // Workspace of the plan (split counters and partials), or -1 when the shape
 // is not served.
 int64_t w4_mr_workspace(int64_t M, int64_t N, int64_t K, int G) {
+  if (plan_mrs(M, N, K, G).ok) return 0;
   const MrPlan p = plan_mr(M, N, K, G);
   return p.ok ? (int64_t)p.ws : -1;
 }
@@ -411,6 +673,29 @@ int64_t w4_mr_workspace(int64_t M, int64_t N, int64_t K, int G) {
 int w4_mr_linear(const void* x, const uint32_t* w, const void* s, const void* b, void* y,
                  int64_t M, int64_t N, int64_t K, int G, int xdt, int ydt, hipStream_t st,
                  const void* res, void* ws, size_t wsb) {
+  const MrsPlan sp = plan_mrs(M, N, K, G);
+  if (sp.ok) {
+    MrsArgs a{};
+    a.x = (const uint16_t*)x;
+    a.w = w;
+    a.sc = (const uint16_t*)s;
+    a.bi = (const uint16_t*)b;
+    a.y = y;
+    a.res = (const uint16_t*)res;
+    a.y_dtype = ydt;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.nt = (int)cdiv(N, 16);
+    a.P = sp.P;
+    a.TW = sp.TW;
+    a.NS = sp.NS;
+    if (xdt == SPARKQ_BF16)
+      launch_mrs<BF16>(sp, G, a, st);
+    else
+      launch_mrs<F16>(sp, G, a, st);
+    return check_launch("w4_mr16s_kernel");
+  }
   const MrPlan p = plan_mr(M, N, K, G);
   if (!p.ok) return 1;
   if (p.ws > 0 && (ws == nullptr || wsb < p.ws))

@@ -80,6 +80,7 @@ struct I8Args {
   int S;
   int mode;
   int wgs;              // workgroups of the one-round rows kernel
+  int tiles_n, tiles;   // tiled GEMM: column tiles, tiles (split items are piece-major)
   // one launch with the quantizer (3..16 rows): producer workgroups [0, np)
   // write the int8 rows of x into a (and their scales into sa); counters[0]
   // counts the rows written, counters[1] the workgroups done (both zero on
@@ -948,6 +949,159 @@ static bool use_rows_sync(int64_t M, int64_t K, int xdt) {
 }
 
 // ---------------------------------------------------------------------------
+// Tiled int8 GEMM for prefill sizes (i8_gemm_kernel)
+// ---------------------------------------------------------------------------
+// The reference serves out_proj at any M with a BM128 x BN128 x BK512
+// tensor-op GEMM (X/src/spark_w8a8.cpp:120-150). Here: a 128 x 128 tile per
+// workgroup of four waves in a 2 x 2 arrangement, each wave 64 x 64 (two
+// 32-row by two 32-column fragments of v_mfma_i32_32x32x32_i8). A k step is
+// 128 bytes of every row of both operands, staged through LDS (double
+// buffered; 128-byte rows whose 16-byte chunks are swizzled by the row, so
+// the 32 rows a fragment read touches at one chunk index fall on distinct
+// banks); the loads of step s+1 go out before the MFMAs of step s. Lane
+// (l % 32, l / 32) of a fragment holds bytes 16 * (l / 32) .. +15 of row
+// l % 32 of a 32-k sub-step, for activations and weights alike. Grids with
+// fewer tiles than twice the CUs split K into S pieces: each piece stores
+// its int32 tile (16-byte stores at the device coherence level), the last
+// to arrive adds them (int32 addition is exact, so the result is the
+// unsplit one bit for bit) and writes the output, raw or through the
+// epilogue fmaf(float(acc) * sa[m], sw[n], bias[n]). Rows and columns past
+// M and N read zeros and are not stored; K % 128 == 0.
+constexpr int kI8GK = 128;  // bytes of k per step
+
+__device__ __forceinline__ uint32_t i8_tile_off(int row, int kc) {
+  const int t = row & 31;
+  return (uint32_t)(row * 128 + ((kc ^ ((t ^ (t >> 3)) & 7)) << 4));
+}
+
+__global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8Args a) {
+  constexpr int BM = 128, BN = 128, TB = (BM + BN) * kI8GK;  // bytes per stage
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * TB];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, j = lane >> 5;
+  const int M = a.M, N = a.N, K = a.K;
+  const int tile = blockIdx.x % a.tiles, piece = blockIdx.x / a.tiles;
+  const int m0 = (tile / a.tiles_n) * BM, n0 = (tile % a.tiles_n) * BN;
+  const int nst = K / kI8GK;
+  const int s_begin = (int)((int64_t)piece * nst / a.S), s_end = (int)((int64_t)(piece + 1) * nst / a.S);
+  const int mr = min(BM, M - m0), nr = min(BN, N - n0);
+  const rsrc_t ra = make_rsrc(a.a + (int64_t)m0 * K, (uint32_t)mr * (uint32_t)K);
+  const rsrc_t rb = make_rsrc(a.b + (int64_t)n0 * K, (uint32_t)nr * (uint32_t)K);
+
+  // staging: chunk p = tid + 256 i of each operand, row p / 8, chunk p % 8
+  constexpr int CH = BM * 8 / 256;  // chunks per thread and operand (4)
+  uint32_t goff[CH], loff[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int p = tid + 256 * i, row = p >> 3, kc = p & 7;
+    goff[i] = (uint32_t)(row * K + kc * 16);
+    loff[i] = i8_tile_off(row, kc);
+  }
+  u32x4_t va[CH], vb[CH];
+  auto load = [&](int step) {
+    const int k0 = step * kI8GK;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      va[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)goff[i], k0, 0));
+      vb[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)goff[i], k0, 0));
+    }
+  };
+  auto stage = [&](int buf) {
+    unsigned char* base = lds + buf * TB;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      *reinterpret_cast<u32x4_t*>(base + loff[i]) = va[i];
+      *reinterpret_cast<u32x4_t*>(base + BM * kI8GK + loff[i]) = vb[i];
+    }
+  };
+
+  i32x16_t acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = i32x16_t{};
+  // fragment rows (a multiple of 32 plus l32: the swizzle's t is l32)
+  const int ar0 = wm * 64 + l32, br0 = wn * 64 + l32;
+
+  if (s_begin < s_end) {
+    load(s_begin);
+    stage(0);
+    __syncthreads();
+  }
+  for (int step = s_begin; step < s_end; ++step) {
+    const int cur = (step - s_begin) & 1;
+    const bool more = step + 1 < s_end;
+    if (more) load(step + 1);
+    const unsigned char* base = lds + cur * TB;
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+      const int kc = 2 * ss + j;
+      u32x4_t af[2], bf[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        af[x] = *reinterpret_cast<const u32x4_t*>(base + i8_tile_off(ar0 + 32 * x, kc));
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+        bf[y] = *reinterpret_cast<const u32x4_t*>(base + BM * kI8GK + i8_tile_off(br0 + 32 * y, kc));
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) acc[x][y] = mfma_i8(af[x], bf[y], acc[x][y]);
+    }
+    if (more) stage(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (a.S > 1) {
+    // this piece's tile: chunk c (16 bytes) of every thread at (c * 256 + tid) * 16
+    constexpr uint32_t PB = 4 * 16 * 4 * 256;  // bytes per piece
+    const rsrc_t rp = make_rsrc(a.part + (size_t)tile * a.S * (PB / 4), (uint32_t)a.S * PB);
+#pragma unroll
+    for (int xy = 0; xy < 4; ++xy)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const i32x16_t& v = acc[xy >> 1][xy & 1];
+        const u32x4_t w = {(uint32_t)v[4 * q], (uint32_t)v[4 * q + 1], (uint32_t)v[4 * q + 2],
+                           (uint32_t)v[4 * q + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(w, rp, (uint32_t)tid * 16u,
+                                               piece * PB + (xy * 4 + q) * 256 * 16, kSc1);
+      }
+    if (!splitk_arrive(a.counters + tile, a.S, &s_last)) return;
+#pragma unroll
+    for (int xy = 0; xy < 4; ++xy) {
+      i32x16_t t = acc[xy >> 1][xy & 1];
+      for (int z = 0; z < a.S; ++z) {
+        if (z == piece) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4_t w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            rp, (uint32_t)tid * 16u, z * PB + (xy * 4 + q) * 256 * 16, kSc1));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t[4 * q + e] += (int32_t)w[e];
+        }
+      }
+      acc[xy >> 1][xy & 1] = t;
+    }
+    splitk_reset(a.counters + tile);
+  }
+
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int gn = n0 + wn * 64 + 32 * y + l32;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gm = m0 + wm * 64 + 32 * x + mfma32_row(lane, v);
+        if (gm < M && gn < N) i8_store(a, gm, gn, acc[x][y][v]);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 // Decode GEMV plan: a row has U = ceil(K/256) spans; a wave keeps at most 10
@@ -1073,19 +1227,59 @@ static I8Plan plan_i8(int64_t M, int64_t N, int64_t K) {
   return p;
 }
 
+// Plan of the tiled GEMM: at least 64 rows (SPARKQ_I8_GEMM_FROM; the
+// weight-streaming kernel below that), K % 128 == 0. Grids of fewer tiles
+// than twice the CUs split K into S = min(4, 2*CUs / tiles) pieces of at
+// least eight steps (tiles within the counter block).
+struct I8GemmPlan {
+  bool ok;
+  int tiles_n, tiles, S;
+  size_t part_bytes;
+};
+
+static I8GemmPlan plan_i8_gemm(int64_t M, int64_t N, int64_t K) {
+  I8GemmPlan p{};
+  if (M < env_int("SPARKQ_I8_GEMM_FROM", 64) || env_int("SPARKQ_I8_NO_GEMM", 0)) return p;
+  if (K % kI8GK != 0 || (int64_t)kI8GK * K >= (int64_t)kOob) return p;
+  const int64_t tn = cdiv(N, 128), tiles = cdiv(M, 128) * tn, cus = device_cus();
+  if (tiles * 4 > (int64_t)0x7FFFFFFF) return p;
+  int64_t S = 1;
+  if (tiles < 2 * cus && tiles <= kMaxCounterTiles)
+    S = std::min<int64_t>(std::min<int64_t>(4, 2 * cus / tiles), std::max<int64_t>(1, (K / kI8GK) / 8));
+  if (env_int("SPARKQ_I8_GEMM_SPLITS", 0) > 0 && tiles <= kMaxCounterTiles)
+    S = std::min<int64_t>(env_int("SPARKQ_I8_GEMM_SPLITS", 1), K / kI8GK);
+  p.tiles_n = (int)tn;
+  p.tiles = (int)tiles;
+  p.S = (int)std::max<int64_t>(S, 1);
+  p.part_bytes = p.S > 1 ? round_up((size_t)tiles * p.S * 65536, 256) : 0;
+  p.ok = true;
+  return p;
+}
+
 size_t w8a8_workspace(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   // the fused decode GEMV needs no workspace for any activation dtype
   if (plan_i8_gemv(M, N, K, 4).ok && plan_i8_gemv(M, N, K, 2).ok) return 0;
-  const size_t part = use_rows(M, N, K) ? 0 : plan_i8(M, N, K).part_bytes;
+  const I8GemmPlan gp = plan_i8_gemm(M, N, K);
+  const size_t part = use_rows(M, N, K) ? 0 : gp.ok ? gp.part_bytes : plan_i8(M, N, K).part_bytes;
   // counters, int8 activations, fp32 scales, int32 partials
   return kCounterBytes + round_up((size_t)M * K, 256) + round_up((size_t)M * 4, 256) + part;
 }
 
 size_t i8_matmul_workspace(int64_t M, int64_t N, int64_t K) {
   if (plan_i8_gemv(M, N, K, 1).ok || use_rows(M, N, K)) return 0;
+  const I8GemmPlan gp = plan_i8_gemm(M, N, K);
+  if (gp.ok) return gp.S > 1 ? kCounterBytes + gp.part_bytes : 0;
   const I8Plan p = plan_i8(M, N, K);
   return p.counter_bytes + p.part_bytes;
+}
+
+static int launch_i8_gemm(I8Args args, const I8GemmPlan& p, hipStream_t st) {
+  args.tiles_n = p.tiles_n;
+  args.tiles = p.tiles;
+  args.S = p.S;
+  hipLaunchKernelGGL(i8_gemm_kernel, dim3((unsigned)(p.tiles * p.S)), dim3(256), 0, st, args);
+  return check_launch("i8_gemm_kernel");
 }
 
 static int launch_i8(const I8Args& args, const I8Plan& p, hipStream_t st) {
@@ -1139,6 +1333,26 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
     r.K = (int)K;
     r.mode = kOutRaw;
     return launch_rows(r, -1, st);
+  }
+  const I8GemmPlan tp = plan_i8_gemm(M, N, K);
+  if (tp.ok) {
+    const size_t need = tp.S > 1 ? kCounterBytes + tp.part_bytes : 0;
+    if (need > 0 && (ws == nullptr || wsb < need))
+      return set_error(SPARKQ_ERR_WORKSPACE,
+                       "int8_matmul_i32 needs a workspace of %zu bytes (got %zu)", need, wsb);
+    I8Args args{};
+    args.a = a;
+    args.b = b;
+    args.c_raw = c;
+    args.M = (int)M;
+    args.N = (int)N;
+    args.K = (int)K;
+    args.mode = kOutRaw;
+    if (tp.S > 1) {
+      args.counters = reinterpret_cast<unsigned*>(ws);
+      args.part = reinterpret_cast<int32_t*>(reinterpret_cast<unsigned char*>(ws) + kCounterBytes);
+    }
+    return launch_i8_gemm(args, tp, st);
   }
   const I8Plan p = plan_i8(M, N, K);
   const size_t need = p.counter_bytes + p.part_bytes;
@@ -1232,6 +1446,27 @@ int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bi
     r.K = (int)K;
     r.mode = kOutEpilogue;
     return launch_rows(r, -1, st);
+  }
+  const I8GemmPlan tp = plan_i8_gemm(M, N, K);
+  if (tp.ok) {
+    I8Args args{};
+    args.a = q;
+    args.b = w;
+    args.sa = sa;
+    args.sw = wsc;
+    args.bias = bias;
+    args.bias_dtype = bias_dtype;
+    args.y = y;
+    args.y_dtype = ydt;
+    args.M = (int)M;
+    args.N = (int)N;
+    args.K = (int)K;
+    args.mode = kOutEpilogue;
+    if (tp.S > 1) {
+      args.counters = reinterpret_cast<unsigned*>(base);
+      args.part = part;
+    }
+    return launch_i8_gemm(args, tp, st);
   }
   const I8Plan p = plan_i8(M, N, K);
   I8Args args{};

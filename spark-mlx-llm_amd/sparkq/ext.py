@@ -706,11 +706,13 @@ def staged_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32,
                           mask=None, out_dtype=None, out=None):
     """Attention over an MLX affine quantized cache in the staged form
     (dequantized keys, scores, softmax, weights times values), whatever the
-    fused predicate would choose: what mlx-lm's quantized attention computes
-    for the reference when its fused kernel is switched off
+    fused 8-bit predicate would choose: what mlx-lm's quantized attention
+    computes for the reference when its fused kernel is switched off
     (spark_mlx_llm/ops/sdpa.py:39-78 with fused_quantized_sdpa=False), and
     the reference's own _fallback (X/spark_mlx_ext/int8_quantized_sdpa.py:
-    122-153). Validates as int8_quantized_sdpa does for the affine tuple."""
+    122-153). 4- and 2-bit caches at one query token still take the decode
+    kernel on their codes, which computes the same arithmetic in one pass.
+    Validates as int8_quantized_sdpa does for the affine tuple."""
     if len(keys) != 3:
         raise ValueError("the staged form takes the affine (packed, scales, biases) tuple")
     return int8_quantized_sdpa(queries, keys, values, scale=scale, group_size=group_size,
@@ -784,6 +786,16 @@ def int8_quantized_sdpa(queries, keys, values, *, scale, group_size: int = 32, b
              and gqa in (1, 2, 4, 8)
              and simple_mask
              and (length == 1 or (queries.dtype in _HALF and (mask is None or length <= n))))
+    # 4- and 2-bit caches at one query token: the decode kernel on their
+    # codes (the staged form's arithmetic in one pass; the reference sends
+    # them to its _fallback, whose M=1 quantized matmuls stream the cache)
+    low_bit_decode = (bits in (2, 4) and length == 1 and dim == dv and dim in (64, 128, 256)
+                      and gqa in (1, 2, 4, 8) and simple_mask)
+    if low_bit_decode:
+        strides = (_kv_strides(keys[0], keys[1], 4) + _kv_strides(values[0], values[1], 4))
+        (kc, ks, kb), (vc, vs, vb) = keys, values
+        return _decode(queries, kc, ks, kb, vc, vs, vb, strides, group_size,
+                       KV_AFFINE_U4 if bits == 4 else KV_AFFINE_U2, scale, out_dtype, out)
     if not fused:
         return _staged_attention(queries, keys, values, scale=scale, group_size=group_size,
                                  bits=bits, mask=mask, out_dtype=out_dtype, out=out)

@@ -164,3 +164,43 @@ def test_staged_additive_mask_hides_leading_chunks(gpu, qdtype):
     if qdtype == o.BF16:
         mean_v = np.repeat(vd, hq // hkv, axis=1).mean(axis=2)
         assert np.abs(y[:, :, 2] - mean_v).max() <= 1e-4
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("b,hq,hkv,n,d,g,qdtype", [
+    (1, 32, 8, 4096, 128, 64, o.BF16),    # the 4-bit decode bench geometry (split context)
+    (2, 16, 4, 777, 64, 32, o.F16),
+    (1, 8, 1, 300, 256, 128, o.BF16),     # eight query heads per KV head
+    (3, 4, 4, 1, 128, 32, o.BF16),        # one token: the value row itself
+    (1, 16, 8, 5000, 128, 64, o.F32)])
+def test_low_bit_decode_matches_oracle(gpu, bits, b, hq, hkv, n, d, g, qdtype):
+    """One query token over a 4- or 2-bit MLX affine cache takes the decode
+    kernel on the codes (16 dims a lane, 8 at eight query heads per KV
+    head): the fp32 output within the north-star tolerance of the fp64
+    attention over the dequantized cache, the 16-bit output equal to its
+    rounding, for head dims 64/128/256, groups 32/64/128, head ratios 1..8,
+    split contexts and a single token."""
+    import sparkq
+
+    print(f"[case] low-bit decode bits={bits} b={b} hq={hq} hkv={hkv} N={n} D={d} G={g}",
+          flush=True)
+    mdt = o.BF16 if qdtype == o.F32 else qdtype
+    tdt = torch.float32 if qdtype == o.F32 else None
+    keys, kd = _cache(gpu, b, hkv, n, d, g, bits, mdt, n + bits, tdt)
+    vals, vd = _cache(gpu, b, hkv, n, d, g, bits, mdt, n + bits + 1, tdt)
+    qf = o.randn(n, 73, b * hq * d).reshape(b, hq, 1, d)
+    if qdtype == o.F32:
+        qt, qref = torch.from_numpy(qf).to(gpu), qf
+    else:
+        q16 = o.round16(qf, qdtype)
+        qt, qref = up16(q16, qdtype, gpu), o.bits_to_f32(q16, qdtype)
+    scale = 1.0 / math.sqrt(d)
+    y = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=scale, group_size=g, bits=bits,
+                                   out_dtype=torch.float32).cpu().numpy()
+    ref = o.sdpa_decode(qref[:, :, 0], kd, vd, scale)
+    check_fp32(y.reshape(b, hq, d), ref)
+    if n == 1:
+        vrow = np.repeat(vd[:, :, 0], hq // hkv, axis=1)
+        assert np.allclose(y.reshape(b, hq, d), vrow, rtol=1e-6, atol=1e-6)
+    y16 = sparkq.int8_quantized_sdpa(qt, keys, vals, scale=scale, group_size=g, bits=bits)
+    assert np.array_equal(y16.float().cpu().numpy(), torch.from_numpy(y).to(qt.dtype).float().numpy())

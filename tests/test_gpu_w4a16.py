@@ -187,13 +187,13 @@ def test_gemm_schedule_variants_bit_identical(gpu, m, n, k, monkeypatch):
     g = 64
     x, wq, s, b = w4_problem(m, n, k, g, seed=k + n)
     outs = {}
-    for sch in ("0", "1", "2", "3"):
+    for sch in ("8", "1", "2", "3"):   # 8: the plain schedule; 3: the default
         monkeypatch.setenv("SPARKQ_W4_GEMM_SCH", sch)
         outs[sch] = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
     for sch in ("1", "2", "3"):
-        assert torch.equal(outs[sch], outs["0"]), sch
+        assert torch.equal(outs[sch], outs["8"]), sch
     cols = np.sort(np.random.default_rng(k).choice(n, size=96, replace=False))
-    check_fp32(outs["0"].cpu().numpy()[:, cols], o.w4a16_matmul(x, wq[cols], s[cols], b[cols], g))
+    check_fp32(outs["3"].cpu().numpy()[:, cols], o.w4a16_matmul(x, wq[cols], s[cols], b[cols], g))
 
 
 @pytest.mark.parametrize("m,n,k,g", [(1, 37, 576, 32), (3, 41, 576, 64), (2, 4, 64, 32),
@@ -247,14 +247,19 @@ def test_decode_multirow_stream(gpu, m, n, k, g, quads, monkeypatch):
 
 @pytest.mark.parametrize("m,n,k,g", [(5, 1100, 3072, 32), (8, 3584, 2560, 64), (16, 19456, 2560, 64),
                                      (16, 1000, 1152, 128), (5, 40, 9728, 64), (16, 16, 128, 32),
-                                     (11, 2560, 4096, 64)])
-def test_decode_mfma_rows(gpu, m, n, k, g, monkeypatch):
-    """5 <= M <= 16 on the 16x16x32 kernel (taken from 9 rows by default): a
-    partial last row tile, the benchmark's QKV and gate+up shapes,
-    one-segment rows (K = 128), long rows with one tile per workgroup, both
-    dtypes."""
+                                     (11, 2560, 4096, 64), (16, 2560, 9728, 64), (9, 3584, 2560, 32)])
+@pytest.mark.parametrize("tiled", ["0", "1"])
+def test_decode_mfma_rows(gpu, m, n, k, g, tiled, monkeypatch):
+    """5 <= M <= 16 on the 16x16x32 kernels (taken from 9 rows by default),
+    the segment-major one (activations loaded once per workgroup into
+    registers, group sums from an all-ones MFMA) and the tile-major one
+    (activations staged in LDS): a partial last row tile, the benchmark's
+    QKV, gate+up and down shapes, one-segment rows (K = 128), long rows with
+    one tile per workgroup, both dtypes."""
     monkeypatch.setenv("SPARKQ_W4_MR_MIN", "5")
     monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
+    monkeypatch.setenv("SPARKQ_W4_MR_TILED", tiled)
+    monkeypatch.setenv("SPARKQ_W4_MR_SEG", "1" if tiled == "0" else "0")
     for dtype in (o.BF16, o.F16):
         x, wq, s, b = w4_problem(m, n, k, g, dtype=dtype, seed=m + n + k)
         ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
@@ -266,12 +271,13 @@ def test_decode_mfma_rows(gpu, m, n, k, g, monkeypatch):
 @pytest.mark.parametrize("m,n,k,g", [(16, 2560, 9728, 64), (9, 100, 9728, 32), (8, 2560, 9728, 64),
                                      (6, 300, 8192, 128), (12, 1000, 16384, 64), (5, 48, 9728, 64)])
 def test_decode_mfma_rows_split_k(gpu, m, n, k, g, monkeypatch):
-    """Rows whose activations exceed the 16x16x32 kernel's staging split K
-    into ranges (the down projection at 9..16 rows; 5..8 rows when the
-    kernel is asked to take them); the last workgroup of a tile range adds
-    the ranges' partials. Ragged N, G32..128, both dtypes, repeated calls
-    bit-identical (the counters are left zero)."""
+    """Rows whose activations exceed the tile-major 16x16x32 kernel's staging
+    split K into ranges (the down projection at 9..16 rows; 5..8 rows when
+    the kernel is asked to take them); the last workgroup of a tile range
+    adds the ranges' partials. Ragged N, G32..128, both dtypes, repeated
+    calls bit-identical (the counters are left zero)."""
     monkeypatch.setenv("SPARKQ_W4_MR_MIN", "5")
+    monkeypatch.setenv("SPARKQ_W4_MR_TILED", "1")
     for dtype in (o.BF16, o.F16):
         x, wq, s, b = w4_problem(m, n, k, g, dtype=dtype, seed=m + n + k)
         ref = o.w4a16_matmul(x, wq, s, b, g, dtype)

@@ -255,3 +255,62 @@ def test_readme_known_answer(gpu):
                             torch.ones(4, dtype=torch.float32, device=gpu))
     y = lin(torch.ones((1, 32), dtype=torch.bfloat16, device=gpu))
     assert y.float().cpu().tolist() == [[32.0] * 4]
+
+
+@pytest.mark.parametrize("m", [512, 2048])
+def test_w8a8_prefill_out_proj_bit_exact(gpu, m):
+    """W8A8 at prefill sizes, the reference's out_proj at any M
+    (X/src/spark_w8a8.cpp:71-151): N=2560, K=4096. int32 accumulators
+    (raw entry point) and the fp32 epilogue bit for bit on sampled rows and
+    columns, the bf16 output its correctly rounded value."""
+    import sparkq
+
+    n, k = 2560, 4096
+    print(f"[case] w8a8 prefill m={m}", flush=True)
+    wq, wsc = _w8(n, k, seed=m)
+    x16 = _x(m, k, o.BF16, seed=m + 1)
+    xt = up16(x16, o.BF16, gpu)
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    y32 = sparkq.w8a8_linear(xt, wt, st, out_dtype=torch.float32).cpu().numpy()
+    y16 = down16(sparkq.w8a8_linear(xt, wt, st))
+    qa, sa = o.a8_quantize(o.bits_to_f32(x16, o.BF16))
+    qt, _ = sparkq.quantize_per_token(xt)
+    acc_t = sparkq.int8_matmul_int32(qt, wt).cpu().numpy()
+    rng = np.random.default_rng(m)
+    rows = np.sort(rng.choice(m, 96, replace=False))
+    cols = np.sort(rng.choice(n, 160, replace=False))
+    acc = o.int8_matmul(qa[rows], wq[cols])
+    assert np.array_equal(acc_t[np.ix_(rows, cols)], acc)
+    ref = o.w8a8_epilogue(acc, sa[rows], wsc[cols])
+    assert np.array_equal(y32[np.ix_(rows, cols)].view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(y16[np.ix_(rows, cols)], o.round16(ref, o.BF16))
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 96, 256), (130, 300, 512), (200, 2560, 1024),
+                                   (1000, 130, 384), (257, 64, 8192), (96, 4100, 128)])
+@pytest.mark.parametrize("splits", ["0", "1", "3"])
+def test_int8_gemm_tiled_bit_exact(gpu, m, n, k, splits, monkeypatch):
+    """The tiled int8 GEMM (64 rows and more, K % 128 == 0): rows and columns
+    that leave partial 128 x 128 tiles, one k step, long rows, and K split
+    into pieces (the planned count, forced to 1, forced to 3): the raw int32
+    accumulators equal the int64 oracle in every element, and so do the
+    fp32 epilogue values of w8a8_linear."""
+    import sparkq
+
+    monkeypatch.setenv("SPARKQ_I8_GEMM_SPLITS", splits)
+    print(f"[case] int8 gemm m={m} n={n} k={k} splits={splits}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    a[3] = 127
+    b[5] = -127
+    c = sparkq.int8_matmul_int32(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    assert np.array_equal(c.cpu().numpy(), o.int8_matmul(a, b))
+    wq, wsc = _w8(n, k, seed=n)
+    x16 = _x(m, k, o.BF16, seed=k)
+    xt = up16(x16, o.BF16, gpu)
+    y32 = sparkq.w8a8_linear(xt, torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu),
+                             out_dtype=torch.float32).cpu().numpy()
+    qa, sa = o.a8_quantize(o.bits_to_f32(x16, o.BF16))
+    ref = o.w8a8_epilogue(o.int8_matmul(qa, wq), sa, wsc)
+    assert np.array_equal(y32.view(np.uint32), ref.view(np.uint32))
