@@ -484,6 +484,49 @@ def only_dominant(torch, sparkq, dev, iters):
 GEMM_PMC_FILE = os.path.join(ROOT, "profiles", "w4_gemm_gate_up_m2048_pmc.md")
 
 
+GEMM_TRACE_FILE = os.path.join(ROOT, "profiles", "w4a16_gemm_per_shape_trace.md")
+
+
+def gemm_trace():
+    """Kernel-only and prologue average durations (us) of the dominant GEMM
+    shape (gate+up, M=2048, prepared weights) from the committed per-shape
+    kernel trace, or {} when there is none."""
+    out = {}
+    try:
+        for line in open(GEMM_TRACE_FILE):
+            key, _, val = line.partition(":")
+            if key in ("gate_up_m2048_kernel_us", "gate_up_m2048_prologue_us"):
+                out[key] = float(val.strip())
+    except (OSError, ValueError):
+        pass
+    return out
+
+
+def only_sdpa(torch, sparkq, dev, which, iters):
+    """Driver for rocprofv3 runs over the INT8-KV decode (the symmetric s8
+    cache, 32/8 heads, D=128): each "B:N" of which, iters graph-free launches
+    over rotated caches."""
+    hq, hkv, d = 32, 8, 128
+    for spec in which.split(","):
+        b, n = (int(v) for v in spec.split(":"))
+        kv_bytes = 2 * b * hkv * n * d + 2 * b * hkv * n * 2
+        copies = max(1, min(32, (600 << 20) // kv_bytes))
+        caches = []
+        for _ in range(copies):
+            kc, ks = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
+            vc, vs = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
+            caches.append(((kc, ks), (vc, vs)))
+        q = torch.randn((b, hq, 1, d), device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        torch.cuda.synchronize()
+        for _ in range(iters):
+            for keys, vals in caches:
+                sparkq.int8_quantized_sdpa(q, keys, vals, scale=1.0 / math.sqrt(d), out=out)
+        torch.cuda.synchronize()
+        log(f"INT8-KV decode B={b} N={n}: {iters * copies} launches ({kv_bytes} KV bytes each)")
+        del caches
+
+
 def gemm_counters():
     """MFMA and VALU busy fractions of the dominant GEMM shape (gate+up,
     M=2048) from the committed PMC summary, or {} when there is none."""
@@ -710,6 +753,8 @@ def main():
                     help="run only the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--only-gemm", default=None, metavar="all|NAME:M",
                     help="run only prefill GEMM launches (for rocprofv3 --kernel-trace / --pmc)")
+    ap.add_argument("--only-sdpa", default=None, metavar="B:N[,B:N]",
+                    help="run only INT8-KV decode launches (for rocprofv3 --kernel-trace / --pmc)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="print per-(kernel, grid) rows of a rocprofv3 kernel trace and exit")
     args = ap.parse_args()
@@ -734,6 +779,9 @@ def main():
         return
     if args.only_gemm:
         only_gemm(torch, sparkq, dev, args.only_gemm, max(args.steps, 1))
+        return
+    if args.only_sdpa:
+        only_sdpa(torch, sparkq, dev, args.only_sdpa, max(args.steps, 1))
         return
     log("generating 36 layers of W4A16 G64 weights")
     layers = make_w4_layers(torch, sparkq, dev, LAYERS)
@@ -833,11 +881,25 @@ def main():
     roofline_gemm = None
     if prefill:
         n, k = PROJ["gate_up"]
+        flop = 2 * 2048 * n * k
         roofline_gemm = {"bound": "mfma", "achieved": prefill["TFLOP/s"], "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": prefill["frac_bf16_peak"],
-                         "kernel": "gemm_prep_kernel + w4_gemm_x16w_kernel (gate+up 19456x2560, M=2048)",
-                         "flop_per_launch": 2 * 2048 * n * k, "avg_launch_ms": prefill["ms"],
-                         **gemm_counters()}
+                         "kernel": "gemm_prep_kernel (activation rows) + w4_gemm_x16w_kernel "
+                                   "(gate+up 19456x2560, M=2048, weights prepared once per set)",
+                         "flop_per_launch": flop, "avg_launch_ms": prefill["ms"],
+                         "prologue_included": True}
+        unprep = extras.get("w4a16_prefill_gemm_unprepared", {}).get("gate_up M=2048")
+        if unprep:
+            roofline_gemm["unprepared_TFLOP/s"] = unprep["TFLOP/s"]
+        tr = gemm_trace()
+        if "gate_up_m2048_kernel_us" in tr:
+            ku = tr["gate_up_m2048_kernel_us"]
+            roofline_gemm["kernel_only_avg_us_rocprof"] = ku
+            roofline_gemm["kernel_only_TFLOP/s_rocprof"] = round(flop / ku / 1e6, 1)
+            roofline_gemm["kernel_only_frac_rocprof"] = round(flop / ku / 1e6 / BF16_PEAK_TFLOPS, 4)
+        if "gate_up_m2048_prologue_us" in tr:
+            roofline_gemm["prologue_avg_us_rocprof"] = tr["gate_up_m2048_prologue_us"]
+        roofline_gemm.update(gemm_counters())
     line = {
         "metric": METRIC,
         "value": round(value, 1),
