@@ -17,7 +17,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "sparkq", "libsparkq.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["w4a16.hip", "w4q.hip", "w4mr.hip", "w8a8.hip", "w8a16.hip", "w8aff.hip", "sdpa.hip", "sdpa_gen.hip",
+SOURCES = ["w4a16.hip", "w4q.hip", "w4mr.hip", "w8a8.hip", "w8a16.hip", "w8aff.hip", "sdpa.hip", "sdpa_affine.hip", "sdpa_gen.hip",
            "layer.hip",
            "abi.cpp"]
 ARCH = "gfx950"
