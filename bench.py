@@ -301,14 +301,15 @@ def bench_sdpa(torch, sparkq, dev, b, n, iters):
             "frac_hbm": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4), "kv_bytes": kv_bytes}
 
 
-def bench_low_bit_decode(torch, sparkq, dev, n, iters, bits=4, g=64, staged=False):
-    """Decode attention over a 4-bit MLX affine cache (mlx-lm's kv_bits=4,
-    group 64; the reference attends it through its staged _fallback): B=1,
-    32/8 heads, D=128, one query token, on the one-pass decode kernel over
-    the codes, or (staged=True) on the staged-attention kernel, forced with
-    an all-visible boolean mask. GB/s of the cache bytes read (codes plus
-    bf16 scales and biases)."""
-    hq, hkv, d, b = 32, 8, 128, 1
+def bench_low_bit_decode(torch, sparkq, dev, n, iters, bits=4, g=64, staged=False, b=1):
+    """Decode attention over an MLX affine cache: by default 4-bit (mlx-lm's
+    kv_bits=4, group 64; the reference attends it through its staged
+    _fallback), with bits=8, g=32 the reference's fused-kernel format. 32/8
+    heads, D=128, one query token, on the one-pass decode kernel over the
+    codes, or (staged=True) on the staged-attention kernel, forced with an
+    all-visible boolean mask. GB/s of the cache bytes read (codes plus bf16
+    scales and biases)."""
+    hq, hkv, d = 32, 8, 128
     words = d * bits // 32
     kv_bytes = 2 * b * hkv * n * (words * 4 + 2 * 2 * (d // g))
     copies = max(1, min(32, (600 << 20) // kv_bytes))
@@ -845,6 +846,9 @@ def main():
                                         for b in (1, 8) for n in (4096, 32768)}
         extras["sdpa_decode_4bit"] = {f"B=1 N={n}": bench_low_bit_decode(torch, sparkq, dev, n, 5)
                                       for n in (4096, 32768)}
+        extras["sdpa_decode_affine_u8"] = {
+            f"B={b} N={n}": bench_low_bit_decode(torch, sparkq, dev, n, 5, bits=8, g=32, b=b)
+            for b in (1, 8) for n in (4096, 32768)}
         extras["staged_sdpa_decode_4bit"] = {
             f"B=1 N={n}": bench_low_bit_decode(torch, sparkq, dev, n, 3, staged=True)
             for n in (4096, 32768)}

@@ -1514,6 +1514,7 @@ static void launch_mfma_d(const SdpaArgs& a, int gqa, dim3 grid, hipStream_t st)
 
 // the matrix-core decode over the affine caches (sdpa_affine.hip)
 bool sdpa_affine_mfma_ok(const SdpaArgs& a, int64_t D, int fmt);
+int sdpa_affine_mfma_occupancy(int64_t D, int G);
 void launch_sdpa_affine_mfma(const SdpaArgs& a, int64_t D, int fmt, dim3 grid, hipStream_t st);
 
 int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void* kb,
@@ -1562,12 +1563,26 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
   const bool mfma = fmt == SPARKQ_KV_S8_F16SCALE && (qdt == SPARKQ_BF16 || qdt == SPARKQ_F16) &&
                     !env_int("SPARKQ_SDPA_NO_MFMA", 0);
   const bool amfma = !env_int("SPARKQ_SDPA_NO_MFMA", 0) && sdpa_affine_mfma_ok(a, D, fmt);
-  if (S > 1) {
-    const size_t rows = (size_t)B * Hq * S;
+  if (amfma && S > 1 && !env_int("SPARKQ_SDPA_SPLITS", 0)) {
+    // a kernel built for one workgroup per CU takes no more splits than fill
+    // the CUs once: a second round of workgroups costs more than the longer
+    // splits (B=8 N=4096, u8 G32: 8 splits in two rounds vs 4 in one)
+    const int64_t fit = device_cus() * (int64_t)sdpa_affine_mfma_occupancy(D, G) / (B * Hkv);
+    if (fit < S) {
+      int64_t s2 = std::max<int64_t>(fit, 1);
+      tps = cdiv(N, s2);
+      s2 = cdiv(N, tps);
+      a.S = (int)s2;
+      a.tps = (int)tps;
+    }
+  }
+  const int S2 = a.S;
+  if (S2 > 1) {
+    const size_t rows = (size_t)B * Hq * S2;
     unsigned char* base = reinterpret_cast<unsigned char*>(ws);
     // the MFMA kernels merge the splits themselves when their LDS holds the
     // split weights and the counters cover every (batch, KV head)
-    if ((mfma || amfma) && (int64_t)gqa * S <= 2048 && B * Hkv <= kMaxCounterTiles &&
+    if ((mfma || amfma) && (int64_t)gqa * S2 <= 2048 && B * Hkv <= kMaxCounterTiles &&
         !env_int("SPARKQ_SDPA_MERGE_KERNEL", 0))
       a.counters = reinterpret_cast<unsigned*>(base);
     base += kCounterBytes;
@@ -1575,7 +1590,7 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
     a.pz = reinterpret_cast<float*>(base + round_up(rows * 4, 256));
     a.pacc = reinterpret_cast<float*>(base + 2 * round_up(rows * 4, 256));
   }
-  dim3 grid((unsigned)S, (unsigned)(B * Hkv));
+  dim3 grid((unsigned)S2, (unsigned)(B * Hkv));
   if (amfma) {
     launch_sdpa_affine_mfma(a, D, fmt, grid, st);
   } else if (mfma) {
@@ -1592,9 +1607,9 @@ int int8kv_sdpa_decode(const void* q, const void* kc, const void* ks, const void
   else
     launch_decode_d<256>(a, gqa, fmt, grid, st);
   if (int rc = check_launch("sdpa_decode_kernel")) return rc;
-  if (S > 1 && !a.counters) {
+  if (S2 > 1 && !a.counters) {
     hipLaunchKernelGGL(sdpa_merge_kernel, dim3((unsigned)(B * Hq)), dim3(256), 0, st, a.pm,
-                       a.pz, a.pacc, out, odt, S, (int)D);
+                       a.pz, a.pacc, out, odt, S2, (int)D);
     if (int rc = check_launch("sdpa_merge_kernel")) return rc;
   }
   return SPARKQ_OK;

@@ -124,8 +124,11 @@ __host__ __device__ constexpr int aff_pipe() { return D == 256 ? 1 : 2; }
 template <int D, int FMT, int G>
 __host__ __device__ constexpr int aff_occ() { return D == 256 || G == 32 ? 1 : 2; }
 
-// T: the query (and scale) dtype tag; FMT 1/2/3: u8/u4/u2 codes.
-template <int D, int FMT, int G, typename T>
+// T: the query (and scale) dtype tag; FMT 1/2/3: u8/u4/u2 codes. PACK: the
+// 16 MFMA rows are (query head, group of dims) pairs, head-major, which
+// needs (heads per KV head) * D/G <= 16; otherwise the rows are the query
+// heads and the PV product runs once per group (see below).
+template <int D, int FMT, int G, typename T, bool PACK>
 __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_kernel(SdpaArgs a) {
   constexpr int BITS = FMT == 1 ? 8 : (FMT == 2 ? 4 : 2);
   constexpr int NW = 4;
@@ -144,6 +147,7 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
   constexpr int SWD = NGR >= 2 ? NGR / 2 : 1;   // words of one packed scale vector
   constexpr int SB = 2 * NGR;                   // bytes of one scale vector
   constexpr int PIPE = aff_pipe<D, FMT, G>();
+  constexpr int NPE = PACK ? 1 : NGR;           // bias sums per row
   static_assert(VL >= 1 && 64 * VL == 32 * PPR, "V pieces");
   __shared__ __attribute__((aligned(16))) unsigned char smem[L::BYTES];
 
@@ -158,13 +162,14 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
   unsigned char* vtile = smem + wave * L::VT;
   uint32_t* pstrip = reinterpret_cast<uint32_t*>(smem + NW * L::VT + wave * L::PT);
 
-  // query operand: lane (head n16, k quarter grp) holds dims 32 w + 8 grp ..
-  // +8 of window w in k-slot order; per window the sum of the fp16 values
+  // query operand: lane (row n16, k quarter grp) holds dims 32 w + 8 grp ..
+  // +8 of window w of the row's head in k-slot order; per window the sum of
+  // the fp16 values
   u32x4_t qa[NWIN];
   float qsw[NWIN];
   float qmul_h;
   {
-    const int h = n16;
+    const int h = PACK ? n16 / NGR : n16;
     const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) +
                            ((int64_t)b * a.Hq + kh * gqa + min(h, gqa - 1)) * D;
     float qv[NWIN][8];
@@ -198,8 +203,8 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
     }
     qmul_h = ldexpf(a.scale_log2, e);
   }
-  // score lanes: head 4 grp + r, token n16 (+16 for the second token group);
-  // per head and group the query sum
+  // score lanes: row 4 grp + r, token n16 (+16 for the second token group);
+  // per row and group of dims the sum of the row's query
   float qg[4][NGR], qmul[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -285,15 +290,26 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
     }
   };
 
-  float mrun[4], zl[4], pe[4][NGR];
+  float mrun[4], zl[4], pe[4][NPE];
   f32x4_t acc[NJ];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     mrun[r] = kNegInf;
     zl[r] = 0.0f;
 #pragma unroll
-    for (int g = 0; g < NGR; ++g) pe[r][g] = 0.0f;
+    for (int g = 0; g < NPE; ++g) pe[r][g] = 0.0f;
   }
+  // PACK: the group of dims of score row 4 grp + r, and that group's element
+  // of a packed scale vector
+  auto row_group = [&](int r) -> int { return NGR <= 4 ? r % NGR : (4 * grp + r) % NGR; };
+  auto row_elem = [&](const uint32_t* v, int r) -> float {
+    if constexpr (NGR <= 4) {
+      return aff_elem<T>(v, r % NGR);
+    } else {
+      const uint32_t w = (grp & 1) ? v[2 + (r >> 1)] : v[r >> 1];
+      return (r & 1) ? hi16<T>(w) : lo16<T>(w);
+    }
+  };
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -354,62 +370,89 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
       mb = fmaxf(mb, mrun[r]);
       alpha[r] = exp2_guarded(mrun[r] - mb, mrun[r] != kNegInf);
       mrun[r] = mb;
-      // rows past gqa (padding) get zero weights, so their strip rows stay zero
-      const bool live = 4 * grp + r < gqa;
+      // rows past the heads (padding) get zero weights, so their strip rows
+      // are zero
+      const bool live = (PACK ? (4 * grp + r) / NGR : 4 * grp + r) < gqa;
       p0[r] = exp2_guarded(s0 - mb, ok0 && live);
       p1[r] = exp2_guarded(s1 - mb, ok1 && live);
       zl[r] = fmaf(zl[r], alpha[r], p0[r] + p1[r]);
+      if constexpr (PACK) {
+        pe[r][0] = fmaf(pe[r][0], alpha[r], fmaf(p0[r], row_elem(bvl[0], r), p1[r] * row_elem(bvl[1], r)));
+      } else {
 #pragma unroll
-      for (int g = 0; g < NGR; ++g)
-        pe[r][g] = fmaf(pe[r][g], alpha[r],
-                        fmaf(p0[r], aff_elem<T>(bvl[0], g), p1[r] * aff_elem<T>(bvl[1], g)));
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      acc[j][0] *= alpha[0];
-      acc[j][1] *= alpha[1];
-      acc[j][2] *= alpha[2];
-      acc[j][3] *= alpha[3];
-    }
-    // PV one group at a time through the wave's strip: position 2 n16 + g2
-    // holds token 16 g2 + n16 (one 32-bit write per lane, head and half)
-    const unsigned char* vaddr = vtile + (8 * grp + (n16 >> 1)) * L::VROW + 8 * (n16 & 1);
-#pragma unroll
-    for (int g = 0; g < NGR; ++g) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int h = 4 * grp + r;
-        const float f0 = p0[r] * aff_elem<T>(svl[0], g), f1 = p1[r] * aff_elem<T>(svl[1], g);
-        const uint32_t hi = pack_round<BF16>(f0, f1);
-        const float r0 = f0 - lo16<BF16>(hi), r1 = f1 - hi16<BF16>(hi);
-        const uint32_t mid = pack_round<BF16>(r0, r1);
-        const uint32_t lo = pack_round<BF16>(r0 - lo16<BF16>(mid), r1 - hi16<BF16>(mid));
-        pstrip[h * 16 + n16] = hi;
-        pstrip[256 + h * 16 + n16] = mid;
-        pstrip[512 + h * 16 + n16] = lo;
+        for (int g = 0; g < NGR; ++g)
+          pe[r][g] = fmaf(pe[r][g], alpha[r],
+                          fmaf(p0[r], aff_elem<T>(bvl[0], g), p1[r] * aff_elem<T>(bvl[1], g)));
       }
+    }
+    // the accumulators are rescaled only when some row's maximum moved in
+    // this block (alpha is exactly 1 otherwise), a wave-uniform branch
+    const bool moved = alpha[0] != 1.0f || alpha[1] != 1.0f || alpha[2] != 1.0f || alpha[3] != 1.0f;
+    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        acc[j][0] *= alpha[0];
+        acc[j][1] *= alpha[1];
+        acc[j][2] *= alpha[2];
+        acc[j][3] *= alpha[3];
+      }
+    }
+    // PV through the wave's strips (three bf16 terms of the weights, rows as
+    // above): position 2 n16 + g2 holds token 16 g2 + n16 (one 32-bit write
+    // per lane, row and term)
+    const unsigned char* vaddr = vtile + (8 * grp + (n16 >> 1)) * L::VROW + 8 * (n16 & 1);
+    auto strip_row = [&](int r, float sv0, float sv1) {
+      const int row = 4 * grp + r;
+      const float f0 = p0[r] * sv0, f1 = p1[r] * sv1;
+      const uint32_t hi = pack_round<BF16>(f0, f1);
+      const float r0 = f0 - lo16<BF16>(hi), r1 = f1 - hi16<BF16>(hi);
+      const uint32_t mid = pack_round<BF16>(r0, r1);
+      const uint32_t lo = pack_round<BF16>(r0 - lo16<BF16>(mid), r1 - hi16<BF16>(mid));
+      pstrip[row * 16 + n16] = hi;
+      pstrip[256 + row * 16 + n16] = mid;
+      pstrip[512 + row * 16 + n16] = lo;
+    };
+    // the B operands of column block cb (its DPB sub-dims) into the
+    // accumulators, with the columns outside group g zeroed when a block
+    // spans two groups (g < 0: all columns)
+    auto pv_block = [&](int cb, int g, const u32x4_t& pa, const u32x4_t& pm, const u32x4_t& pl) {
+      typedef int v2i_t __attribute__((ext_vector_type(2)));
+      const v2i_t t8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (__attribute__((address_space(3))) v2i_t*)(vaddr + 16 * cb));
+      const bool mine = g < 0 || CSPAN <= G || ((CSPAN * cb + DPB * n16) / G == g);
+#pragma unroll
+      for (int m = 0; m < DPB; ++m) {
+        u32x4_t vb = aff_vdecode<BITS>((uint32_t)t8.x, (uint32_t)t8.y, m);
+        if (!mine) vb = u32x4_t{0u, 0u, 0u, 0u};
+        acc[cb * DPB + m] = mfma16x16x32_bf16(pa, vb, acc[cb * DPB + m]);
+        acc[cb * DPB + m] = mfma16x16x32_bf16(pm, vb, acc[cb * DPB + m]);
+        acc[cb * DPB + m] = mfma16x16x32_bf16(pl, vb, acc[cb * DPB + m]);
+      }
+    };
+    if constexpr (PACK) {
+      // one strip: row (head, group) weighs its group's value scale; every
+      // output row is computed for every column, the epilogue keeps the
+      // rows of each column's group
+#pragma unroll
+      for (int r = 0; r < 4; ++r) strip_row(r, row_elem(svl[0], r), row_elem(svl[1], r));
       const u32x4_t pa = *reinterpret_cast<const u32x4_t*>(pstrip + n16 * 16 + 4 * grp);
       const u32x4_t pm = *reinterpret_cast<const u32x4_t*>(pstrip + 256 + n16 * 16 + 4 * grp);
       const u32x4_t pl = *reinterpret_cast<const u32x4_t*>(pstrip + 512 + n16 * 16 + 4 * grp);
-      // the 16-byte column blocks holding this group's dims
-      const int CB0 = g * G / CSPAN;
-      constexpr int NCB = CSPAN <= G ? G / CSPAN : 1;
 #pragma unroll
-      for (int cb = CB0; cb < CB0 + NCB; ++cb) {
-        typedef int v2i_t __attribute__((ext_vector_type(2)));
-        const v2i_t t8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (__attribute__((address_space(3))) v2i_t*)(vaddr + 16 * cb));
-        // a column block wider than the group (2-bit codes, G = 32): the
-        // lanes of the other group's columns take zeros
-        const bool mine = CSPAN <= G || ((CSPAN * cb + DPB * n16) / G == g);
+      for (int cb = 0; cb < NJ / DPB; ++cb) pv_block(cb, -1, pa, pm, pl);
+    } else {
+      // rows are heads: one strip per group, each through the column blocks
+      // holding the group's dims
 #pragma unroll
-        for (int m = 0; m < DPB; ++m) {
-          u32x4_t vb = aff_vdecode<BITS>((uint32_t)t8.x, (uint32_t)t8.y, m);
-          if (!mine) vb = u32x4_t{0u, 0u, 0u, 0u};
-          acc[cb * DPB + m] = mfma16x16x32_bf16(pa, vb, acc[cb * DPB + m]);
-          acc[cb * DPB + m] = mfma16x16x32_bf16(pm, vb, acc[cb * DPB + m]);
-          acc[cb * DPB + m] = mfma16x16x32_bf16(pl, vb, acc[cb * DPB + m]);
-        }
+      for (int g = 0; g < NGR; ++g) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) strip_row(r, aff_elem<T>(svl[0], g), aff_elem<T>(svl[1], g));
+        const u32x4_t pa = *reinterpret_cast<const u32x4_t*>(pstrip + n16 * 16 + 4 * grp);
+        const u32x4_t pm = *reinterpret_cast<const u32x4_t*>(pstrip + 256 + n16 * 16 + 4 * grp);
+        const u32x4_t pl = *reinterpret_cast<const u32x4_t*>(pstrip + 512 + n16 * 16 + 4 * grp);
+        constexpr int NCB = CSPAN <= G ? G / CSPAN : 1;
+#pragma unroll
+        for (int cb = g * G / CSPAN; cb < g * G / CSPAN + NCB; ++cb) pv_block(cb, g, pa, pm, pl);
       }
     }
   };
@@ -436,7 +479,7 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
   for (int r = 0; r < 4; ++r) {
     zl[r] = sum_row16(zl[r]);
 #pragma unroll
-    for (int g = 0; g < NGR; ++g) pe[r][g] = sum_row16(pe[r][g]);
+    for (int g = 0; g < NPE; ++g) pe[r][g] = sum_row16(pe[r][g]);
   }
 
   // combine the waves through LDS (the loop's LDS is free after the barrier)
@@ -446,9 +489,11 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
   float* wacc = wz + NW * 8;                             // [NW][8][D]
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int h = 4 * grp + r;
+    const int row = 4 * grp + r;
+    const int h = PACK ? row / NGR : row;
+    const int rg = PACK ? row_group(r) : 0;  // the row's group (PACK)
     if (h < gqa) {
-      if (n16 == 0) {
+      if (n16 == 0 && rg == 0) {
         wm[wave * 8 + h] = mrun[r];
         wz[wave * 8 + h] = zl[r];
       }
@@ -457,13 +502,19 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
 #pragma unroll
         for (int m = 0; m < DPB; ++m) {
           const int d = CSPAN * cb + DPB * n16 + m;
-          float bias;
-          if constexpr (CSPAN <= G) {
-            bias = pe[r][CSPAN * cb / G];
+          if constexpr (PACK) {
+            // the column's group: fixed per block unless a block spans two
+            const int gd = CSPAN <= G ? CSPAN * cb / G : (CSPAN * cb + DPB * n16) / G;
+            if (gd == rg) wacc[(wave * 8 + h) * D + d] = acc[cb * DPB + m][r] + pe[r][0];
           } else {
-            bias = n16 >= 8 ? pe[r][(CSPAN * cb + CSPAN / 2) / G] : pe[r][CSPAN * cb / G];
+            float bias;
+            if constexpr (CSPAN <= G) {
+              bias = pe[r][CSPAN * cb / G];
+            } else {
+              bias = n16 >= 8 ? pe[r][(CSPAN * cb + CSPAN / 2) / G] : pe[r][CSPAN * cb / G];
+            }
+            wacc[(wave * 8 + h) * D + d] = acc[cb * DPB + m][r] + bias;
           }
-          wacc[(wave * 8 + h) * D + d] = acc[cb * DPB + m][r] + bias;
         }
     }
   }
@@ -507,14 +558,25 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
   }
 }
 
+// rows as (head, group) pairs when they fit in 16; the per-group passes
+// otherwise (instantiated only where some head count needs them)
+template <int D, int FMT, int G, typename T>
+static void launch_affine_p(const SdpaArgs& a, dim3 grid, hipStream_t st) {
+  constexpr bool NEED_HEADS = 8 * (D / G) > 16;
+  if (NEED_HEADS && (a.Hq / a.Hkv) * (D / G) > 16)
+    hipLaunchKernelGGL((sdpa_affine_mfma_kernel<D, FMT, G, T, !NEED_HEADS>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((sdpa_affine_mfma_kernel<D, FMT, G, T, true>), grid, dim3(256), 0, st, a);
+}
+
 template <int D, int FMT, typename T>
 static void launch_affine_g(const SdpaArgs& a, dim3 grid, hipStream_t st) {
   if (a.G == 32) {
-    hipLaunchKernelGGL((sdpa_affine_mfma_kernel<D, FMT, 32, T>), grid, dim3(256), 0, st, a);
+    launch_affine_p<D, FMT, 32, T>(a, grid, st);
   } else if (a.G == 64) {
-    hipLaunchKernelGGL((sdpa_affine_mfma_kernel<D, FMT, 64, T>), grid, dim3(256), 0, st, a);
+    launch_affine_p<D, FMT, 64, T>(a, grid, st);
   } else if constexpr (D >= 128) {
-    hipLaunchKernelGGL((sdpa_affine_mfma_kernel<D, FMT, 128, T>), grid, dim3(256), 0, st, a);
+    launch_affine_p<D, FMT, 128, T>(a, grid, st);
   }
 }
 
@@ -547,6 +609,12 @@ bool sdpa_affine_mfma_ok(const SdpaArgs& a, int64_t D, int fmt) {
   for (const void* p : {(const void*)a.kc, (const void*)a.vc, a.q})
     if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
   return true;
+}
+
+// workgroups per CU the kernel for (D, G) is built for
+int sdpa_affine_mfma_occupancy(int64_t D, int G) {
+  if (D == 256) return aff_occ<256, 1, 32>();
+  return G == 32 ? aff_occ<128, 1, 32>() : aff_occ<128, 1, 64>();
 }
 
 void launch_sdpa_affine_mfma(const SdpaArgs& a, int64_t D, int fmt, dim3 grid, hipStream_t st) {
