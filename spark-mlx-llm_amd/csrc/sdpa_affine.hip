@@ -17,15 +17,23 @@
 //    The windows of a group accumulate together and the group's fp32 result
 //    takes sk * acc + (bk - 1024 sk) * sum(q'), which is the reference's
 //    factorization with the code offset folded into the bias term.
-//  * PV on v_mfma_f32_16x16x32_bf16 per group: A = p * sv (one value per
-//    head, token and group) as the sum of three bf16 terms (24 significant
-//    bits and the fp32 exponent range, so any bf16 or fp16 scale), transposed
-//    to head-major through per-wave LDS strips; B = the codes themselves, exact in bf16, read from a per-wave
-//    LDS copy of the block with ds_read_b64_tr_b8 (the 8 bytes of a lane are
-//    one code byte of 8 tokens) and converted with v_cvt_f32_ubyte. The
-//    bias term p * bv is an fp32 sum per (head, group).
+//  * PV on v_mfma_f32_16x16x32_bf16: A = p * sv (one value per head, token
+//    and group) as the sum of three bf16 terms (24 significant bits and the
+//    fp32 exponent range, so any bf16 or fp16 scale), transposed to
+//    row-major through per-wave LDS strips; B = the codes themselves, exact
+//    in bf16, read from a per-wave LDS copy of the block with
+//    ds_read_b64_tr_b8 (the 8 bytes of a lane are one code byte of 8 tokens)
+//    and converted with v_cvt_f32_ubyte. The bias term p * bv is an fp32 sum
+//    per (head, group).
+//  * Rows: when (heads per KV head) * (groups per row) <= 16 the 16 MFMA rows
+//    are (head, group) pairs: the QK rows of one head repeat, each row's
+//    strip weighs its own group's value scale, and one strip per block feeds
+//    the PV product of every column; the epilogue keeps, for each column,
+//    the rows of its group. Otherwise the rows are the heads and the PV
+//    product runs once per group with that group's strip.
 // Each workgroup (4 waves) owns one (sequence, KV head) and one context
-// split; a wave walks 32-token blocks with the next two in flight. Waves
+// split; a wave walks 32-token blocks with the next blocks in flight. The
+// accumulators are rescaled only in blocks where a row maximum moved. Waves
 // combine through LDS; a split's partial is merged by the last workgroup of
 // its (sequence, KV head) as in the s8 kernel.
 #include <type_traits>
@@ -162,63 +170,6 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
   unsigned char* vtile = smem + wave * L::VT;
   uint32_t* pstrip = reinterpret_cast<uint32_t*>(smem + NW * L::VT + wave * L::PT);
 
-  // query operand: lane (row n16, k quarter grp) holds dims 32 w + 8 grp ..
-  // +8 of window w of the row's head in k-slot order; per window the sum of
-  // the fp16 values
-  u32x4_t qa[NWIN];
-  float qsw[NWIN];
-  float qmul_h;
-  {
-    const int h = PACK ? n16 / NGR : n16;
-    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) +
-                           ((int64_t)b * a.Hq + kh * gqa + min(h, gqa - 1)) * D;
-    float qv[NWIN][8];
-    float qmax = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NWIN; ++w) {
-      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(qrow + 32 * w + 8 * grp);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = (i & 1) ? hi16<T>(x[i >> 1]) : lo16<T>(x[i >> 1]);
-        qv[w][i] = h < gqa ? v : 0.0f;
-        qmax = fmaxf(qmax, fabsf(qv[w][i]));
-      }
-    }
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
-    const int e = (qmax > 0.0f && qmax <= 3.4028235e38f) ? ilogbf(qmax) - 14 : 0;
-#pragma unroll
-    for (int w = 0; w < NWIN; ++w) {
-      float s = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const _Float16 lo = (_Float16)ldexpf(qv[w][aff_kslot_dim<BITS>(2 * i)], -e);
-        const _Float16 hi = (_Float16)ldexpf(qv[w][aff_kslot_dim<BITS>(2 * i + 1)], -e);
-        s += (float)lo + (float)hi;
-        qa[w][i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-      }
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
-      qsw[w] = s;
-    }
-    qmul_h = ldexpf(a.scale_log2, e);
-  }
-  // score lanes: row 4 grp + r, token n16 (+16 for the second token group);
-  // per row and group of dims the sum of the row's query
-  float qg[4][NGR], qmul[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int src = (4 * grp + r) & 15;
-    qmul[r] = __shfl(qmul_h, src);
-#pragma unroll
-    for (int g = 0; g < NGR; ++g) {
-      float s = 0.0f;
-#pragma unroll
-      for (int w = 0; w < WPG; ++w) s += qsw[g * WPG + w];
-      qg[r][g] = __shfl(s, src);
-    }
-  }
-
   const rsrc_t rk = make_rsrc(a.kc + b * a.kc_b + kh * a.kc_h, (uint32_t)(t_end * a.kc_t));
   const rsrc_t rv = make_rsrc(a.vc + b * a.vc_b + kh * a.vc_h, (uint32_t)(t_end * a.vc_t));
   const uint16_t* ksb = reinterpret_cast<const uint16_t*>(a.ks) + b * a.ks_b + kh * a.ks_h;
@@ -289,6 +240,70 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
       load_vec(rvb, tok * (uint32_t)a.vs_t * 2u, bvr[set][g2]);
     }
   };
+  // the first blocks are in flight while the query operand is built (their
+  // loads do not depend on it)
+  const int stride = NW * 32;
+  int t0 = t_begin + 32 * wave;
+  load(0, t0);
+  if constexpr (PIPE == 2) load(1, t0 + stride);
+
+  // query operand: lane (row n16, k quarter grp) holds dims 32 w + 8 grp ..
+  // +8 of window w of the row's head in k-slot order; per window the sum of
+  // the fp16 values
+  u32x4_t qa[NWIN];
+  float qsw[NWIN];
+  float qmul_h;
+  {
+    const int h = PACK ? n16 / NGR : n16;
+    const uint16_t* qrow = reinterpret_cast<const uint16_t*>(a.q) +
+                           ((int64_t)b * a.Hq + kh * gqa + min(h, gqa - 1)) * D;
+    float qv[NWIN][8];
+    float qmax = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWIN; ++w) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(qrow + 32 * w + 8 * grp);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = (i & 1) ? hi16<T>(x[i >> 1]) : lo16<T>(x[i >> 1]);
+        qv[w][i] = h < gqa ? v : 0.0f;
+        qmax = fmaxf(qmax, fabsf(qv[w][i]));
+      }
+    }
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    const int e = (qmax > 0.0f && qmax <= 3.4028235e38f) ? ilogbf(qmax) - 14 : 0;
+#pragma unroll
+    for (int w = 0; w < NWIN; ++w) {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const _Float16 lo = (_Float16)ldexpf(qv[w][aff_kslot_dim<BITS>(2 * i)], -e);
+        const _Float16 hi = (_Float16)ldexpf(qv[w][aff_kslot_dim<BITS>(2 * i + 1)], -e);
+        s += (float)lo + (float)hi;
+        qa[w][i] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      qsw[w] = s;
+    }
+    qmul_h = ldexpf(a.scale_log2, e);
+  }
+  // score lanes: row 4 grp + r, token n16 (+16 for the second token group);
+  // per row and group of dims the sum of the row's query
+  float qg[4][NGR], qmul[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int src = (4 * grp + r) & 15;
+    qmul[r] = __shfl(qmul_h, src);
+#pragma unroll
+    for (int g = 0; g < NGR; ++g) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WPG; ++w) s += qsw[g * WPG + w];
+      qg[r][g] = __shfl(s, src);
+    }
+  }
+
 
   float mrun[4], zl[4], pe[4][NPE];
   f32x4_t acc[NJ];
@@ -313,7 +328,6 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int stride = NW * 32;
   auto block = [&](int t0, auto setc) {
     constexpr int set = decltype(setc)::value;
     __builtin_amdgcn_sched_barrier(0);
@@ -456,13 +470,10 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
       }
     }
   };
-  int t0 = t_begin + 32 * wave;
   const int nb = t0 < t_end ? (t_end - t0 + stride - 1) / stride : 0;
   if constexpr (PIPE == 2) {
     // blocks in pairs with no branch in the loop body (so the wait counts
     // carried around it stay exact), then an odd last block
-    load(0, t0);
-    load(1, t0 + stride);
     int ib = 0;
     for (; ib + 2 <= nb; ib += 2, t0 += 2 * stride) {
       block(t0, std::integral_constant<int, 0>{});
@@ -470,7 +481,6 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
     }
     if (ib < nb) block(t0, std::integral_constant<int, 0>{});
   } else {
-    load(0, t0);
     for (int ib = 0; ib < nb; ++ib, t0 += stride) block(t0, std::integral_constant<int, 0>{});
   }
 
@@ -552,7 +562,15 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
     __shared__ int s_last;
     if (splitk_arrive(a.counters + blockIdx.y, a.S, &s_last)) {
       __syncthreads();  // the combine above is done with the LDS it reused
-      sdpa_fold_merge<D, 8, 64 * NW>(a, b, kh, reinterpret_cast<float*>(smem), gqa);
+      // register arrays sized for the actual head count (more splits in
+      // flight per output with fewer heads)
+      float* sm = reinterpret_cast<float*>(smem);
+      if (gqa <= 2)
+        sdpa_fold_merge<D, 2, 64 * NW>(a, b, kh, sm, gqa);
+      else if (gqa <= 4)
+        sdpa_fold_merge<D, 4, 64 * NW>(a, b, kh, sm, gqa);
+      else
+        sdpa_fold_merge<D, 8, 64 * NW>(a, b, kh, sm, gqa);
       splitk_reset(a.counters + blockIdx.y);
     }
   }
