@@ -306,42 +306,6 @@ __global__ __launch_bounds__(64 * NW, (D == 256 || NW == 8) ? 1 : 2) void sdpa_m
   unsigned char* vtile = smem + wave * L::VT;
   uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + NW * L::VT + wave * L::PT);
 
-  const rsrc_t rk = make_rsrc(a.kc + b * a.kc_b + kh * a.kc_h, (uint32_t)(t_end * a.kc_t));
-  const rsrc_t rv = make_rsrc(a.vc + b * a.vc_b + kh * a.vc_h, (uint32_t)(t_end * a.vc_t));
-  const rsrc_t rks = make_rsrc(reinterpret_cast<const uint16_t*>(a.ks) + b * a.ks_b + kh * a.ks_h,
-                               (uint32_t)(t_end * a.ks_t * 2));
-  const rsrc_t rvs = make_rsrc(reinterpret_cast<const uint16_t*>(a.vs) + b * a.vs_b + kh * a.vs_h,
-                               (uint32_t)(t_end * a.vs_t * 2));
-
-  // block registers, two sets (the next two blocks are in flight while one
-  // is computed): K pieces [token group][piece], V pieces, the K and V
-  // scales of the block's 32 tokens (lane t % 32). Every load is issued
-  // unconditionally (past t_end it reads zeros through the bounded
-  // descriptors), so the loop's wait counts stay exact instead of draining
-  // all loads each block.
-  u32x4_t kr[2][2][PL], vr[2][VL];
-  uint16_t skr[2], svr[2];
-  auto load = [&](int set, int t0) {
-#pragma unroll
-    for (int g2 = 0; g2 < 2; ++g2)
-#pragma unroll
-      for (int i = 0; i < PL; ++i)
-        kr[set][g2][i] = buf_load16(rk, (uint32_t)((t0 + 16 * g2 + n16) * a.kc_t + 16 * (grp + 4 * i)));
-#pragma unroll
-    for (int v = 0; v < VL; ++v) {
-      const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
-      vr[set][v] = buf_load16(rv, (uint32_t)((t0 + tok) * a.vc_t + 16 * pc));
-    }
-    skr[set] = buf_load2(rks, (uint32_t)((t0 + (lane & 31)) * a.ks_t * 2));
-    svr[set] = buf_load2(rvs, (uint32_t)((t0 + (lane & 31)) * a.vs_t * 2));
-  };
-  // the first two blocks are in flight while the query operand is built
-  // (their loads do not depend on it)
-  const int stride = NW * 32;
-  int t0 = t_begin + 32 * wave;
-  load(0, t0);
-  load(1, t0 + stride);
-
   // query operand: lane (head n16, k quarter grp); chunk c covers dims
   // 16*(grp + 4*(c/2)) + 8*(c%2) .. +8, matching the K piece order below
   u32x4_t qa[NC];
@@ -392,6 +356,35 @@ __global__ __launch_bounds__(64 * NW, (D == 256 || NW == 8) ? 1 : 2) void sdpa_m
   for (int i = lane; i < 2 * 16 * 32; i += 64)
     if ((i & 511) / 32 >= GQA) pstrip[i] = 0;
 
+  const rsrc_t rk = make_rsrc(a.kc + b * a.kc_b + kh * a.kc_h, (uint32_t)(t_end * a.kc_t));
+  const rsrc_t rv = make_rsrc(a.vc + b * a.vc_b + kh * a.vc_h, (uint32_t)(t_end * a.vc_t));
+  const rsrc_t rks = make_rsrc(reinterpret_cast<const uint16_t*>(a.ks) + b * a.ks_b + kh * a.ks_h,
+                               (uint32_t)(t_end * a.ks_t * 2));
+  const rsrc_t rvs = make_rsrc(reinterpret_cast<const uint16_t*>(a.vs) + b * a.vs_b + kh * a.vs_h,
+                               (uint32_t)(t_end * a.vs_t * 2));
+
+  // block registers, two sets (the next two blocks are in flight while one
+  // is computed): K pieces [token group][piece], V pieces, the K and V
+  // scales of the block's 32 tokens (lane t % 32). Every load is issued
+  // unconditionally (past t_end it reads zeros through the bounded
+  // descriptors), so the loop's wait counts stay exact instead of draining
+  // all loads each block.
+  u32x4_t kr[2][2][PL], vr[2][VL];
+  uint16_t skr[2], svr[2];
+  auto load = [&](int set, int t0) {
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2)
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        kr[set][g2][i] = buf_load16(rk, (uint32_t)((t0 + 16 * g2 + n16) * a.kc_t + 16 * (grp + 4 * i)));
+#pragma unroll
+    for (int v = 0; v < VL; ++v) {
+      const int f = lane + 64 * v, tok = f / (D / 16), pc = f % (D / 16);
+      vr[set][v] = buf_load16(rv, (uint32_t)((t0 + tok) * a.vc_t + 16 * pc));
+    }
+    skr[set] = buf_load2(rks, (uint32_t)((t0 + (lane & 31)) * a.ks_t * 2));
+    svr[set] = buf_load2(rvs, (uint32_t)((t0 + (lane & 31)) * a.vs_t * 2));
+  };
 
   float mrun[4], zl[4], psl[4];
   f32x4_t acc[NJ];
@@ -404,6 +397,7 @@ __global__ __launch_bounds__(64 * NW, (D == 256 || NW == 8) ? 1 : 2) void sdpa_m
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+  const int stride = NW * 32;
   // The block's registers are read in place and refilled with the block two
   // ahead once the QK product and the scales have been taken from them, so
   // no register copy waits on the loads still in flight.
@@ -483,9 +477,12 @@ __global__ __launch_bounds__(64 * NW, (D == 256 || NW == 8) ? 1 : 2) void sdpa_m
       acc[j] = mfma16x16x32_f16(pl, vf, acc[j]);
     }
   };
+  int t0 = t_begin + 32 * wave;
   // blocks in pairs with no branch in the loop body (so the wait counts
   // carried around it stay exact), then an odd last block
   const int nb = t0 < t_end ? (t_end - t0 + stride - 1) / stride : 0;
+  load(0, t0);
+  load(1, t0 + stride);
   int ib = 0;
   for (; ib + 2 <= nb; ib += 2, t0 += 2 * stride) {
     block(t0, std::integral_constant<int, 0>{});
