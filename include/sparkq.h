@@ -46,7 +46,7 @@ enum sparkq_kv_format {
   /* MLX affine 4-bit and 2-bit tuples: packed uint32 [B,Hkv,Ncap,D*bits/32],
    * code of dim cpw*w+j at bits (bits*j) of word w (cpw = 32/bits), scales
    * and biases [B,Hkv,Ncap,D/G]. Appended by sparkq_kv_append and read by
-   * sparkq_quantized_sdpa. */
+   * sparkq_quantized_sdpa and, at one query token, sparkq_int8kv_sdpa_decode. */
   SPARKQ_KV_AFFINE_U4 = 2,
   SPARKQ_KV_AFFINE_U2 = 3,
 };
@@ -267,7 +267,9 @@ int sparkq_w8_affine_linear(const void* x, const uint32_t* w, const void* scales
  *   All N tokens are visible (bottom-right causal decode with L=1).
  * out = softmax(scale * q . K^T) . V in fp32 with an online softmax, split
  * over the context and merged by log-sum-exp (in the same launch, by the
- * last split to finish, for the symmetric format with a 16-bit query). A
+ * last split to finish, for 16-bit queries; for the affine formats when
+ * every scale and bias vector of a token is aligned to its byte width and
+ * the code rows and q are 16-byte aligned, as in a contiguous cache). A
  * split decode needs the workspace: per-(batch, KV head) counters in its
  * first 16384 bytes (zero before the first call, left zero), then partials.
  * Replaces int8_quantized_sdpa (X/spark_mlx_ext/int8_quantized_sdpa.py:

@@ -175,11 +175,11 @@ def test_staged_additive_mask_hides_leading_chunks(gpu, qdtype):
     (1, 16, 8, 5000, 128, 64, o.F32)])
 def test_low_bit_decode_matches_oracle(gpu, bits, b, hq, hkv, n, d, g, qdtype):
     """One query token over a 4- or 2-bit MLX affine cache takes the decode
-    kernel on the codes (16 dims a lane, 8 at eight query heads per KV
-    head): the fp32 output within the north-star tolerance of the fp64
-    attention over the dequantized cache, the 16-bit output equal to its
-    rounding, for head dims 64/128/256, groups 32/64/128, head ratios 1..8,
-    split contexts and a single token."""
+    entry on the codes (the matrix-core kernel for 16-bit queries, the
+    vector kernel for fp32 ones): the fp32 output within the north-star
+    tolerance of the fp64 attention over the dequantized cache, the 16-bit
+    output equal to its rounding, for head dims 64/128/256, groups
+    32/64/128, head ratios 1..8, split contexts and a single token."""
     import sparkq
 
     print(f"[case] low-bit decode bits={bits} b={b} hq={hq} hkv={hkv} N={n} D={d} G={g}",
