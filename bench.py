@@ -504,27 +504,47 @@ def gemm_trace():
 
 
 def only_sdpa(torch, sparkq, dev, which, iters):
-    """Driver for rocprofv3 runs over the INT8-KV decode (the symmetric s8
-    cache, 32/8 heads, D=128): each "B:N" of which, iters graph-free launches
-    over rotated caches."""
+    """Driver for rocprofv3 runs over the INT8-KV decode (32/8 heads, D=128):
+    each "B:N" of which over the symmetric s8 cache, or "FMT:B:N" with FMT
+    s8, u8 (the MLX affine u8 G32 tuple, the reference's fused format) or u4
+    (4-bit G64), iters graph-free launches over rotated caches."""
     hq, hkv, d = 32, 8, 128
     for spec in which.split(","):
-        b, n = (int(v) for v in spec.split(":"))
-        kv_bytes = 2 * b * hkv * n * d + 2 * b * hkv * n * 2
+        parts = spec.split(":")
+        fmt = parts[0] if len(parts) == 3 else "s8"
+        b, n = (int(v) for v in parts[-2:])
+        bits, g = {"s8": (8, 0), "u8": (8, 32), "u4": (4, 64)}[fmt]
+        if fmt == "s8":
+            kv_bytes = 2 * b * hkv * n * d + 2 * b * hkv * n * 2
+        else:
+            kv_bytes = 2 * b * hkv * n * (d * bits // 8 + 2 * 2 * (d // g))
         copies = max(1, min(32, (600 << 20) // kv_bytes))
+        gen = torch.Generator(device=dev).manual_seed(4)
+
+        def part():
+            words = d * bits // 32
+            packed = torch.randint(-2 ** 31, 2 ** 31 - 1, (b, hkv, n, words), dtype=torch.int32,
+                                   device=dev, generator=gen)
+            sc = torch.rand((b, hkv, n, d // g), device=dev, generator=gen) * 0.01 + 0.001
+            return packed, sc.to(torch.bfloat16), (-sc * (1 << (bits - 1))).to(torch.bfloat16)
+
         caches = []
         for _ in range(copies):
-            kc, ks = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
-            vc, vs = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
-            caches.append(((kc, ks), (vc, vs)))
+            if fmt == "s8":
+                kc, ks = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
+                vc, vs = sparkq.kv_quantize_s8(torch.randn((b, hkv, n, d), device=dev, dtype=torch.bfloat16))
+                caches.append(((kc, ks), (vc, vs)))
+            else:
+                caches.append((part(), part()))
         q = torch.randn((b, hq, 1, d), device=dev).to(torch.bfloat16)
         out = torch.empty_like(q)
+        kw = {} if fmt == "s8" else {"group_size": g, "bits": bits}
         torch.cuda.synchronize()
         for _ in range(iters):
             for keys, vals in caches:
-                sparkq.int8_quantized_sdpa(q, keys, vals, scale=1.0 / math.sqrt(d), out=out)
+                sparkq.int8_quantized_sdpa(q, keys, vals, scale=1.0 / math.sqrt(d), out=out, **kw)
         torch.cuda.synchronize()
-        log(f"INT8-KV decode B={b} N={n}: {iters * copies} launches ({kv_bytes} KV bytes each)")
+        log(f"INT8-KV decode {fmt} B={b} N={n}: {iters * copies} launches ({kv_bytes} KV bytes each)")
         del caches
 
 
@@ -754,8 +774,9 @@ def main():
                     help="run only the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--only-gemm", default=None, metavar="all|NAME:M",
                     help="run only prefill GEMM launches (for rocprofv3 --kernel-trace / --pmc)")
-    ap.add_argument("--only-sdpa", default=None, metavar="B:N[,B:N]",
-                    help="run only INT8-KV decode launches (for rocprofv3 --kernel-trace / --pmc)")
+    ap.add_argument("--only-sdpa", default=None, metavar="[FMT:]B:N[,...]",
+                    help="run only INT8-KV decode launches (for rocprofv3 --kernel-trace / --pmc); "
+                         "FMT s8 (default), u8 (affine G32) or u4 (affine G64)")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="print per-(kernel, grid) rows of a rocprofv3 kernel trace and exit")
     args = ap.parse_args()
