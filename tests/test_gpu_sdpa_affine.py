@@ -41,6 +41,14 @@ CASES = [
     (2, 1, 32, 8, 5000, 128, 32, o.BF16),   # 2-bit G32: column blocks span two groups
     (2, 2, 16, 4, 129, 64, 32, o.F16),      # 8-byte value pieces
     (2, 1, 8, 1, 70, 256, 64, o.BF16),
+    # rows as heads with one PV pass per group (heads x groups > 16)
+    (8, 1, 64, 8, 500, 128, 32, o.BF16),    # 8 heads x 4 groups
+    (4, 1, 32, 4, 300, 256, 32, o.F16),     # 8 x 8
+    (2, 1, 32, 4, 200, 256, 32, o.BF16),    # 8 x 8, 2-bit column blocks spanning two groups
+    (8, 2, 16, 2, 650, 256, 64, o.BF16),    # 8 x 4
+    # (head, group) rows at the widest group count and at 16 rows
+    (8, 1, 8, 4, 300, 256, 32, o.F16),      # 2 x 8: the row's group depends on the lane group
+    (2, 1, 16, 4, 333, 256, 64, o.BF16),    # 4 x 4
 ]
 
 
