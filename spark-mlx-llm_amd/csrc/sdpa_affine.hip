@@ -32,8 +32,7 @@
 //    the rows of its group. Otherwise the rows are the heads and the PV
 //    product runs once per group with that group's strip.
 // Each workgroup (4 waves) owns one (sequence, KV head) and one context
-// split; a wave walks 32-token blocks with the next blocks in flight. The
-// accumulators are rescaled only in blocks where a row maximum moved. Waves
+// split; a wave walks 32-token blocks with the next blocks in flight. Waves
 // combine through LDS; a split's partial is merged by the last workgroup of
 // its (sequence, KV head) as in the s8 kernel.
 #include <type_traits>
@@ -399,17 +398,14 @@ __global__ __launch_bounds__(256, (aff_occ<D, FMT, G>())) void sdpa_affine_mfma_
                           fmaf(p0[r], aff_elem<T>(bvl[0], g), p1[r] * aff_elem<T>(bvl[1], g)));
       }
     }
-    // the accumulators are rescaled only when some row's maximum moved in
-    // this block (alpha is exactly 1 otherwise), a wave-uniform branch
-    const bool moved = alpha[0] != 1.0f || alpha[1] != 1.0f || alpha[2] != 1.0f || alpha[3] != 1.0f;
-    if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+    // rescaled every block: a wave-uniform branch that skipped this when no
+    // row maximum moved measured slower (it splits the block's wait counts)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        acc[j][0] *= alpha[0];
-        acc[j][1] *= alpha[1];
-        acc[j][2] *= alpha[2];
-        acc[j][3] *= alpha[3];
-      }
+    for (int j = 0; j < NJ; ++j) {
+      acc[j][0] *= alpha[0];
+      acc[j][1] *= alpha[1];
+      acc[j][2] *= alpha[2];
+      acc[j][3] *= alpha[3];
     }
     // PV through the wave's strips (three bf16 terms of the weights, rows as
     // above): position 2 n16 + g2 holds token 16 g2 + n16 (one 32-bit write
