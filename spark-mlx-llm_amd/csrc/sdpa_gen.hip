@@ -56,19 +56,26 @@ struct GenSdpaArgs {
   int q_dtype, out_dtype;
   int RC, nch;                    // query heads per workgroup, chunks per KV head
   int S, tps;                     // context splits, tokens per split
+  int vt;                         // value tokens per LDS stage
   float scale_log2;               // softmax scale times log2(e)
   float masked;                   // score of a masked entry, in log2 units
 };
 
-constexpr int kMaskNone = 0, kMaskCausal = 1, kMaskBool = 2, kMaskAdd = 3;
+[[maybe_unused]] constexpr int kMaskNone = 0, kMaskCausal = 1, kMaskBool = 2, kMaskAdd = 3;
 constexpr int kGenMaxRC = 8;
 constexpr int kGenMaxDim = 512;
 constexpr int kGenChunk = 256;
-constexpr int kGenVT = 32;  // value tokens per LDS stage
 constexpr int kGenMaxOut = (kGenMaxRC * kGenMaxDim) / 256;
+constexpr int kGenLdsFloats = 16384;  // 64 KB of LDS per workgroup
 
+// value tokens per LDS stage: what fits beside the queries and weights, a
+// multiple of 8 from 8 to 64
+__host__ __device__ __forceinline__ int gen_value_tokens(int RC, int D, int Dv) {
+  const int room = (kGenLdsFloats - RC * D - RC * kGenChunk - 8 * RC) / Dv;
+  return room >= 64 ? 64 : (room / 8 * 8 < 8 ? 8 : room / 8 * 8);
+}
 __host__ __device__ __forceinline__ size_t gen_lds_bytes(int RC, int D, int Dv) {
-  return (size_t)(RC * D + RC * kGenChunk + kGenVT * Dv + 8 * RC) * 4;
+  return (size_t)(RC * D + RC * kGenChunk + gen_value_tokens(RC, D, Dv) * Dv + 8 * RC) * 4;
 }
 
 __device__ __forceinline__ float gen_load(const void* p, int64_t i, int dt) {
@@ -90,7 +97,26 @@ __device__ __forceinline__ float block_reduce(float v, float* red, int slot) {
   return MAX ? fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3])) : (r[0] + r[1]) + (r[2] + r[3]);
 }
 
+// Metadata (scales, biases) loads: MF32 for fp32 metadata, else 16-bit
+// (bf16 or fp16 by q_dtype). A load's data is only used after every load of
+// its batch has been issued, so one wait covers the batch.
+template <bool MF32>
+__device__ __forceinline__ float gen_meta(rsrc_t r, int64_t idx, int dt) {
+  if constexpr (MF32) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)(idx * 4), 0, 0));
+  } else {
+    const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(r, (int)(idx * 2), 0, 0);
+    const float fb = __uint_as_float(h << 16), fh = f16_to_f32((uint16_t)h);
+    return dt == SPARKQ_BF16 ? fb : fh;
+  }
+}
+
+template <int BITS, bool MF32>
 __global__ __launch_bounds__(256) void sdpa_gen_kernel(GenSdpaArgs a) {
+  constexpr int CPW = 32 / BITS;                 // codes per word
+  constexpr uint32_t CMASK = (1u << BITS) - 1u;
+  constexpr int WPP = 128 / CPW;                 // words per pass of 128 dims of a key row
+  constexpr int VB = 8;                          // value elements per thread per load batch
   extern __shared__ float lds[];
   const int tid = threadIdx.x;
   const int l = blockIdx.x / a.S, split = blockIdx.x - (blockIdx.x / a.S) * a.S;
@@ -100,13 +126,13 @@ __global__ __launch_bounds__(256) void sdpa_gen_kernel(GenSdpaArgs a) {
   const int R = a.Hq / a.Hkv;
   const int h0 = kvh * R + chunk * a.RC;
   const int rc = min(a.RC, R - chunk * a.RC);
-  const int D = a.D, Dv = a.Dv, G = a.G, bits = a.bits;
-  const int cpw = 32 / bits;                 // codes per word
-  const uint32_t cmask = (1u << bits) - 1u;
+  const int D = a.D, Dv = a.Dv, G = a.G;
+  const int gsh = G == 32 ? 5 : (G == 64 ? 6 : 7);  // log2 of the group size
+  const int VT = a.vt;                       // value tokens per LDS stage
   float* qs = lds;                           // [RC][D]
   float* sc = qs + a.RC * D;                 // [RC][256]
-  float* vt = sc + a.RC * kGenChunk;         // [32][Dv]
-  float* red = vt + kGenVT * Dv;             // reductions
+  float* vt = sc + a.RC * kGenChunk;         // [VT][Dv]
+  float* red = vt + VT * Dv;                 // reductions
 
   for (int i = tid; i < rc * D; i += 256) {
     const int r = i / D, d = i - (i / D) * D;
@@ -127,34 +153,66 @@ __global__ __launch_bounds__(256) void sdpa_gen_kernel(GenSdpaArgs a) {
   const int t_begin = split * a.tps;
   const int t_end = min(a.N, t_begin + a.tps);
   const int limit = a.N - a.L + l;  // causal: last visible token of this row
-  const uint32_t* kbase = a.kp + b * a.kp_b + kvh * a.kp_h;
-  const uint32_t* vbase = a.vp + b * a.vp_b + kvh * a.vp_h;
+  // bounded descriptors over this (sequence, KV head)'s first t_end tokens;
+  // every index below is clamped into them
+  const int wpr = D * BITS / 32, vwpr = Dv * BITS / 32;  // words per key / value row
+  const int ng = D / G, nvg = Dv / G;
+  const rsrc_t rk = make_rsrc(a.kp + b * a.kp_b + kvh * a.kp_h,
+                              (uint32_t)(((int64_t)(t_end - 1) * a.kp_t + wpr) * 4));
+  const rsrc_t rv = make_rsrc(a.vp + b * a.vp_b + kvh * a.vp_h,
+                              (uint32_t)(((int64_t)(t_end - 1) * a.vp_t + vwpr) * 4));
+  const int esz = MF32 ? 4 : 2;
   const int64_t ksb = b * a.ks_b + kvh * a.ks_h, vsb = b * a.vs_b + kvh * a.vs_h;
+  const rsrc_t rks = make_rsrc(reinterpret_cast<const unsigned char*>(a.ks) + ksb * esz,
+                               (uint32_t)(((int64_t)(t_end - 1) * a.ks_t + ng) * esz));
+  const rsrc_t rkb = make_rsrc(reinterpret_cast<const unsigned char*>(a.kb) + ksb * esz,
+                               (uint32_t)(((int64_t)(t_end - 1) * a.ks_t + ng) * esz));
+  const rsrc_t rvs = make_rsrc(reinterpret_cast<const unsigned char*>(a.vs) + vsb * esz,
+                               (uint32_t)(((int64_t)(t_end - 1) * a.vs_t + nvg) * esz));
+  const rsrc_t rvb = make_rsrc(reinterpret_cast<const unsigned char*>(a.vb) + vsb * esz,
+                               (uint32_t)(((int64_t)(t_end - 1) * a.vs_t + nvg) * esz));
+  const float inv_dv = 1.0f / (float)Dv;
   __syncthreads();
 
   for (int n0 = t_begin; n0 < t_end; n0 += kGenChunk) {
-    // 1. scores of token n0+tid for every head of the chunk
+    // 1. scores of token n0+tid for every head of the chunk: the key row in
+    // passes of 128 dims, each pass's words and its groups' scales and
+    // biases loaded together before any is used
     const int n = n0 + tid;
+    const int nl = min(n, t_end - 1);
     float s[kGenMaxRC];
 #pragma unroll
     for (int r = 0; r < kGenMaxRC; ++r) s[r] = 0.0f;
-    if (n < t_end) {
-      const uint32_t* kr = kbase + (int64_t)n * a.kp_t;
-      const int64_t si = ksb + (int64_t)n * a.ks_t;
-      for (int g = 0; g < D / G; ++g) {
-        const float gs = gen_load(a.ks, si + g, a.q_dtype);
-        const float gb = gen_load(a.kb, si + g, a.q_dtype);
-        for (int w = g * G / cpw; w < (g + 1) * G / cpw; ++w) {
-          const uint32_t word = kr[w];
-          for (int j = 0; j < cpw; ++j) {
-            const float kv = fmaf((float)((word >> (bits * j)) & cmask), gs, gb);
-            const int d = w * cpw + j;
+    for (int w0 = 0; w0 < wpr; w0 += WPP) {
+      // each word with its group's scale and bias (a group spans at least
+      // one word; repeated loads of a group hit the cache)
+      uint32_t kw[WPP];
+      float gs[WPP], gb[WPP];
+#pragma unroll
+      for (int i = 0; i < WPP; ++i) {  // words past the row read zeros (out of range)
+        const bool in = w0 + i < wpr;
+        kw[i] = __builtin_amdgcn_raw_buffer_load_b32(
+            rk, in ? (int)(((int64_t)nl * a.kp_t + w0 + i) * 4) : (int)kOob, 0, 0);
+        const int64_t gi = (int64_t)nl * a.ks_t + (min(w0 + i, wpr - 1) * CPW >> gsh);
+        gs[i] = gen_meta<MF32>(rks, gi, a.q_dtype);
+        gb[i] = gen_meta<MF32>(rkb, gi, a.q_dtype);
+      }
+      const int nw = min(WPP, wpr - w0);  // words of this pass (uniform)
+#pragma unroll
+      for (int i = 0; i < WPP; ++i) {
+        if (i < nw) {
+#pragma unroll
+          for (int j = 0; j < CPW; ++j) {
+            const float kv = fmaf((float)((kw[i] >> (BITS * j)) & CMASK), gs[i], gb[i]);
+            const int d = (w0 + i) * CPW + j;
 #pragma unroll
             for (int r = 0; r < kGenMaxRC; ++r)
               if (r < rc) s[r] = fmaf(qs[r * D + d], kv, s[r]);
           }
         }
       }
+    }
+    if (n < t_end) {
       if (a.mask_kind == kMaskCausal) {
         if (n > limit) {
 #pragma unroll
@@ -199,17 +257,35 @@ __global__ __launch_bounds__(256) void sdpa_gen_kernel(GenSdpaArgs a) {
         __syncthreads();
       }
     }
-    // 3. values, 32 tokens at a time through LDS
+    // 3. values, VT tokens at a time through LDS, dequantized in batches of
+    // VB elements per thread whose loads go out together
     const int cend = min(kGenChunk, t_end - n0);
-    for (int t0 = 0; t0 < cend; t0 += kGenVT) {
-      const int nt = min(kGenVT, cend - t0);
-      for (int i = tid; i < nt * Dv; i += 256) {
-        const int t = i / Dv, d = i - (i / Dv) * Dv;
-        const int64_t tok = n0 + t0 + t;
-        const uint32_t word = vbase[tok * a.vp_t + d / cpw];
-        const int64_t si = vsb + tok * a.vs_t + d / G;
-        vt[i] = fmaf((float)((word >> (bits * (d % cpw))) & cmask),
-                     gen_load(a.vs, si, a.q_dtype), gen_load(a.vb, si, a.q_dtype));
+    for (int t0 = 0; t0 < cend; t0 += VT) {
+      const int nt = min(VT, cend - t0);
+      for (int i0 = 0; i0 < nt * Dv; i0 += 256 * VB) {
+        uint32_t vw[VB];
+        float vsf[VB], vbf[VB];
+        int vi[VB];
+#pragma unroll
+        for (int u = 0; u < VB; ++u) {
+          const int i = min(i0 + tid + 256 * u, nt * Dv - 1);
+          // (token, dim) of element i: a float quotient, corrected by one
+          int t = (int)((float)i * inv_dv);
+          int d = i - t * Dv;
+          t = d < 0 ? t - 1 : (d >= Dv ? t + 1 : t);
+          d = i - t * Dv;
+          const int64_t tok = min(n0 + t0 + t, t_end - 1);
+          vi[u] = i;
+          vw[u] = __builtin_amdgcn_raw_buffer_load_b32(
+              rv, (int)((tok * a.vp_t + d / CPW) * 4), 0, 0);
+          const int64_t si = tok * a.vs_t + (d >> gsh);
+          vsf[u] = gen_meta<MF32>(rvs, si, a.q_dtype);
+          vbf[u] = gen_meta<MF32>(rvb, si, a.q_dtype);
+          vw[u] = (vw[u] >> (BITS * (d % CPW))) & CMASK;
+        }
+#pragma unroll
+        for (int u = 0; u < VB; ++u)
+          if (i0 + tid + 256 * u < nt * Dv) vt[vi[u]] = fmaf((float)vw[u], vsf[u], vbf[u]);
       }
       __syncthreads();
 #pragma unroll
@@ -253,36 +329,53 @@ __global__ __launch_bounds__(256) void sdpa_gen_kernel(GenSdpaArgs a) {
   }
 }
 
-// one workgroup per output row: out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) z_s,
-// in split order
+// one workgroup per output row: out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) z_s.
+// The split maxima and sums are reduced across the threads (a fixed tree, so
+// the result is deterministic), the weights go to LDS, and each output sums
+// its partials in split order with eight loads in flight.
 __global__ __launch_bounds__(256) void sdpa_gen_merge_kernel(const float* __restrict__ pm,
                                                              const float* __restrict__ pz,
                                                              const float* __restrict__ pacc,
                                                              void* __restrict__ out,
                                                              int out_dtype, int S, int Dv) {
+  __shared__ float wts[1024];
+  __shared__ float red[8];
+  const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
-  float mm = -INFINITY;
-  for (int s = 0; s < S; ++s) mm = fmaxf(mm, pm[row * S + s]);
+  float m = -INFINITY;
+  for (int s = tid; s < S; s += 256) m = fmaxf(m, pm[row * S + s]);
+  const float mm = block_reduce<true>(m, red, 0);
   float z = 0.0f;
-  for (int s = 0; s < S; ++s) {
-    const float m = pm[row * S + s];
-    z = fmaf(pz[row * S + s], m == -INFINITY ? 0.0f : exp2f(m - mm), z);
+  for (int s = tid; s < S; s += 256) {
+    const float ms = pm[row * S + s];
+    const float w = ms == -INFINITY ? 0.0f : exp2f(ms - mm);
+    wts[s] = w;
+    z = fmaf(pz[row * S + s], w, z);
   }
-  for (int d = threadIdx.x; d < Dv; d += 256) {
+  z = block_reduce<false>(z, red, 1);
+  __syncthreads();
+  for (int d = tid; d < Dv; d += 256) {
+    const float* p = pacc + row * S * Dv + d;
     float o = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float m = pm[row * S + s];
-      o = fmaf(pacc[(row * S + s) * Dv + d], m == -INFINITY ? 0.0f : exp2f(m - mm), o);
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(s + u) * Dv];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o = fmaf(v[u], wts[s + u], o);
     }
+    for (; s < S; ++s) o = fmaf(p[(int64_t)s * Dv], wts[s], o);
     store_out(out, row * Dv + d, o / z, out_dtype);
   }
 }
 
-// context splits: enough workgroups to cover the chip twice, at least 512
-// tokens per split, at most 64 splits
+
+// context splits: enough workgroups to cover the chip four times, at least
+// 128 tokens per split, at most 128 splits
 static int gen_splits(int64_t rows_grid, int64_t N, int64_t* tps) {
-  int64_t S = std::max<int64_t>(1, cdiv(512, std::max<int64_t>(rows_grid, 1)));
-  S = std::min<int64_t>(S, std::min<int64_t>(64, cdiv(N, 512)));
+  int64_t S = std::max<int64_t>(1, cdiv(1024, std::max<int64_t>(rows_grid, 1)));
+  S = std::min<int64_t>(S, std::min<int64_t>(128, cdiv(N, 128)));
   S = std::max<int64_t>(S, 1);
   *tps = cdiv(N, S);
   return (int)cdiv(N, *tps);
@@ -294,6 +387,24 @@ static void gen_plan(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N, i
   *RC = (int)std::min<int64_t>(R, kGenMaxRC);
   *nch = (int)cdiv(R, *RC);
   *S = gen_splits(L * B * Hkv * *nch, N, tps);
+}
+
+template <int BITS>
+static void launch_gen_m(const GenSdpaArgs& a, bool mf32, dim3 grid, size_t lds, hipStream_t st) {
+  // (the workgroup's dynamic LDS stays within 64 KB, the default limit)
+  if (mf32)
+    hipLaunchKernelGGL((sdpa_gen_kernel<BITS, true>), grid, dim3(256), lds, st, a);
+  else
+    hipLaunchKernelGGL((sdpa_gen_kernel<BITS, false>), grid, dim3(256), lds, st, a);
+}
+static void launch_gen_b(const GenSdpaArgs& a, int bits, bool mf32, dim3 grid, size_t lds,
+                         hipStream_t st) {
+  if (bits == 2)
+    launch_gen_m<2>(a, mf32, grid, lds, st);
+  else if (bits == 4)
+    launch_gen_m<4>(a, mf32, grid, lds, st);
+  else
+    launch_gen_m<8>(a, mf32, grid, lds, st);
 }
 
 size_t sdpa_gen_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t N,
@@ -376,13 +487,10 @@ int sdpa_generic(const void* q, const void* kp, const void* ks, const void* kb, 
     a.pz = reinterpret_cast<float*>(p + round_up(rows * a.S * 4, 256));
     a.pacc = reinterpret_cast<float*>(p + 2 * round_up(rows * a.S * 4, 256));
   }
+  a.vt = gen_value_tokens(a.RC, (int)D, (int)Dv);
   const size_t lds = gen_lds_bytes(a.RC, (int)D, (int)Dv);
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(sdpa_gen_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-      (int)gen_lds_bytes(kGenMaxRC, kGenMaxDim, kGenMaxDim));
-  (void)attr;
   const dim3 grid((unsigned)(L * a.S), (unsigned)(B * Hkv * a.nch));
-  hipLaunchKernelGGL(sdpa_gen_kernel, grid, dim3(256), lds, st, a);
+  launch_gen_b(a, bits, qdt == SPARKQ_F32, grid, lds, st);
   if (int rc = check_launch("sdpa_gen_kernel")) return rc;
   if (a.S > 1) {
     hipLaunchKernelGGL(sdpa_gen_merge_kernel, dim3((unsigned)(B * Hq * L)), dim3(256), 0, st,
