@@ -42,6 +42,8 @@ CASES = [
     (1, 4, 2, 6, 4, 64, 64, 32, 8, o.BF16, "causal"),       # L > N: early rows see nothing
     (1, 8, 2, 1, 5000, 64, 64, 32, 4, o.F32, None),         # fp32 queries and metadata
     (1, 8, 8, 3, 20, 512, 512, 128, 2, o.BF16, "bool"),     # the widest head dims
+    (1, 32, 8, 1, 20000, 128, 128, 64, 4, o.BF16, "bool"),  # 128 context splits merged
+    (2, 12, 4, 3, 9000, 96, 96, 32, 8, o.F16, "causal"),    # many splits, three rows, ratio 3
 ]
 
 
@@ -68,7 +70,8 @@ def test_staged_attention_matches_oracle(gpu, b, hq, hkv, length, n, d, dv, g, b
     rng = np.random.default_rng(seed)
     if mask == "bool":
         m = rng.random((length, n)) > 0.4
-        m[0] = False                     # a row that sees nothing: the mean of V
+        if length > 1:
+            m[0] = False                 # a row that sees nothing: the mean of V
         mask_t, mask_ref = torch.from_numpy(m).to(gpu), m
     elif mask == "add":
         m = (rng.standard_normal((1, hq, length, n)) * 2).astype(np.float32)
