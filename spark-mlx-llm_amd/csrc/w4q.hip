@@ -16,11 +16,14 @@
 //  * the activations (in the pair order of the strided decode) with their
 //    32-k piece sums, and the (scale, bias) pairs of the workgroup's rows,
 //    are staged once per workgroup in LDS;
-//  * a wave issues the loads of its whole row quad up front (one 16-byte
-//    load per lane and 256-byte span: lane 4b+j reads bytes 16b.. of row
-//    4q+j), then per span reads its activation piece from LDS, decodes the
-//    codes to OFFSET + q 16-bit pairs and runs eight 4x4x4 MFMAs, and adds
-//    s*D + (b - OFFSET*s)*X for its group;
+//  * a wave loads its row quad one 16-byte load per lane and 256-byte span
+//    (lane 4b+j reads bytes 16b.. of row 4q+j): all spans up front on small
+//    grids, two spans ahead of the arithmetic when the CU holds 12 or more
+//    row-quad waves (gate+up 7.8-8.2 -> 7.5 us: the CU's memory queue then
+//    interleaves its waves' spans, so the arithmetic runs under the stream
+//    instead of after it); per span it reads its activation piece from LDS,
+//    decodes the codes to OFFSET + q 16-bit pairs and runs eight 4x4x4
+//    MFMAs, and adds s*D + (b - OFFSET*s)*X for its group;
 //  * the sixteen 4-lane blocks are added by DPP and permlane swaps and
 //    lanes 0..3 write the quad's four outputs (plus an optional 16-bit
 //    residual, rounded as the reference's hidden + mlp_output).
@@ -67,103 +70,46 @@ __host__ __device__ __forceinline__ GemvQLds gemvq_lds(int M, int K, int NWQ, in
   return l;
 }
 
-template <typename T, int G, int U, int MQ>  // MQ: 1, or 4 for 2..4 activation rows
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5)))
-void w4_gemv_q_kernel(GemvQArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int nt = blockDim.x;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int b = lane >> 2, j = lane & 3;
-  const int M = MQ == 1 ? 1 : a.M, N = a.N, K = a.K;
-  const int RB = K >> 1;     // bytes per weight row
-  const int ns = RB >> 8;    // spans per row (<= U)
-  const int ng = K / G;      // groups per row
-  const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
-  const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
-  const GemvQLds L = gemvq_lds(M, K, nt >> 6, G);
-
-  const rsrc_t rx = make_rsrc(a.x, (uint32_t)(M * K) * 2);
-  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
-  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
-  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
-
-  // 1. staging loads: activation pieces (64 B: 32 k; piece i of the M rows
-  // in order) and 16-byte (scale, bias) pieces of the workgroup's 4*nql
-  // rows. A thread takes at most one activation piece and at most two scale
-  // pieces (the plan gives the workgroup the waves for both); a wave with
-  // nothing to fetch skips the instruction.
-  const int nxp = M * (K >> 5);
-  const int nsp = (4 * nql * ng) >> 3;
-  u32x4_t xr[4], sr[2] = {}, br[2] = {};
-  if (64 * wave < nxp) {
-    const uint32_t off = tid < nxp ? 64u * tid : kOob;
+// Staging of the one-round kernels: activation piece pc (64 B, 32 k, in
+// r[0..3]) to LDS row xrow in the pair order of the strided decode, returning
+// the piece's sum; and 16-byte (scale, bias) pieces t to (s, b) pairs.
+template <typename T>
+__device__ __forceinline__ float stage_x_piece(uint32_t* xrow, int pc, const u32x4_t (&r)[4]) {
+  float sum = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) xr[w] = buf_load16(rx, off + 16 * w);
+  for (int w = 0; w < 4; ++w) {
+    const u32x4_t o = {__builtin_amdgcn_perm(r[w].z, r[w].x, 0x05040100u),   // (x0, x4)
+                       __builtin_amdgcn_perm(r[w].z, r[w].x, 0x07060302u),   // (x1, x5)
+                       __builtin_amdgcn_perm(r[w].w, r[w].y, 0x05040100u),   // (x2, x6)
+                       __builtin_amdgcn_perm(r[w].w, r[w].y, 0x07060302u)};  // (x3, x7)
+    *reinterpret_cast<u32x4_t*>(xrow + q_xslot(pc, w)) = o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[w][e], sum);
   }
+  return sum;
+}
+__device__ __forceinline__ void stage_sb_piece(uint32_t* sb, int t, u32x4_t s, u32x4_t b) {
+  u32x4_t lo, hi;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int t = tid + h * nt;
-    if (64 * wave + h * nt < nsp) {
-      const uint32_t off = t < nsp ? 8u * (uint32_t)qa * ng + 16u * t : kOob;
-      sr[h] = buf_load16(rs, off);
-      br[h] = buf_load16(rb, off);
-    }
+  for (int e = 0; e < 4; ++e) {
+    lo[e] = __builtin_amdgcn_perm(b[e], s[e], 0x05040100u);  // (s0, b0)
+    hi[e] = __builtin_amdgcn_perm(b[e], s[e], 0x07060302u);  // (s1, b1)
   }
+  *reinterpret_cast<u32x4_t*>(sb + 8 * t) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+  *reinterpret_cast<u32x4_t*>(sb + 8 * t + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+}
 
-  // 2. the wave's row quad: one load per span, all in flight
-  const bool has_quad = wave < nql;
-  const int row = 4 * (qa + wave) + j;
-  u32x4_t wv[U];
-#pragma unroll
-  for (int s = 0; s < U; ++s)
-    wv[s] = buf_load16(rw, has_quad && s < ns ? (uint32_t)row * RB + 256u * s + 16u * b : kOob);
-
-  // keep every load above ahead of the arithmetic below
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 3. staged data to LDS
-  {
-    uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
-    float* xs = reinterpret_cast<float*>(smem + L.xs);
-    if (tid < nxp) {
-      // piece tid is piece `pc` of activation row m (rows of K/2 dwords)
-      const int m = MQ == 1 ? 0 : tid / (K >> 5), pc = tid - m * (K >> 5);
-      float sum = 0.0f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const u32x4_t r = xr[w];
-        const u32x4_t o = {__builtin_amdgcn_perm(r.z, r.x, 0x05040100u),   // (x0, x4)
-                           __builtin_amdgcn_perm(r.z, r.x, 0x07060302u),   // (x1, x5)
-                           __builtin_amdgcn_perm(r.w, r.y, 0x05040100u),   // (x2, x6)
-                           __builtin_amdgcn_perm(r.w, r.y, 0x07060302u)};  // (x3, x7)
-        *reinterpret_cast<u32x4_t*>(xp + m * (K >> 1) + q_xslot(pc, w)) = o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[e], sum);
-      }
-      xs[MQ == 1 ? pc : 4 * pc + m] = sum;
-    }
-    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int t = tid + h * nt;
-      if (t < nsp) {
-        u32x4_t lo, hi;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lo[e] = __builtin_amdgcn_perm(br[h][e], sr[h][e], 0x05040100u);  // (s0, b0)
-          hi[e] = __builtin_amdgcn_perm(br[h][e], sr[h][e], 0x07060302u);  // (s1, b1)
-        }
-        *reinterpret_cast<u32x4_t*>(sb + 8 * t) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
-        *reinterpret_cast<u32x4_t*>(sb + 8 * t + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
-      }
-    }
-  }
-  __syncthreads();
-  if (!has_quad) return;
-
-  // 4. per span: activations from LDS, decode, eight 4x4x4 MFMAs, group
-  // epilogue
+// Steps 4 and 5 of the one-round kernels: per span, the activation piece
+// from LDS, the decode, eight 4x4x4 MFMAs and the group epilogue; then the
+// sixteen lane blocks (lanes j, j+4, ..., j+60) summed and lanes 0..3
+// storing row 4q+j of each activation row. wave indexes the row quad's
+// (scale, bias) rows in LDS.
+template <typename T, int G, int U, int MQ, int D>
+__device__ __forceinline__ void gemvq_spans(const GemvQArgs& a, u32x4_t (&wv)[U], rsrc_t rw,
+                                            uint32_t wbase, const unsigned char* smem,
+                                            const GemvQLds& L, int ns, int wave, int M, int row) {
+  const int lane = threadIdx.x & 63, b = lane >> 2, j = lane & 3;
+  const int K = a.K, N = a.N, ng = K / G;
   const unsigned char* xp = smem + L.xp;
   const float* xs = reinterpret_cast<const float*>(smem + L.xs);
   const uint32_t* sb = reinterpret_cast<const uint32_t*>(smem + L.sb);
@@ -176,6 +122,8 @@ void w4_gemv_q_kernel(GemvQArgs a) {
   for (int m = 0; m < MQ; ++m) acc[m] = 0.0f;
 #pragma unroll
   for (int s = 0; s < U; ++s) {
+    // span s + D's load goes out as span s is taken up
+    if (s + D < U) wv[s + D] = buf_load16(rw, s + D < ns ? wbase + 256u * (s + D) : kOob);
     if (s < ns) {
       const int piece = 16 * s + b;
       u32x4_t xa[4];
@@ -218,8 +166,6 @@ void w4_gemv_q_kernel(GemvQArgs a) {
       }
     }
   }
-  // 5. sum the sixteen blocks (lanes j, j+4, ..., j+60); lanes 0..3 store
-  // row 4q+j of each activation row
 #pragma unroll
   for (int m = 0; m < MQ; ++m) {
     const float v = sum_blocks(acc[m]);
@@ -228,6 +174,103 @@ void w4_gemv_q_kernel(GemvQArgs a) {
       store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
     }
   }
+}
+
+// MQ: 1, or 4 for 2..4 activation rows; D: weight loads of a wave in flight
+// (the first D spans' go out before the staging loads)
+template <typename T, int G, int U, int MQ, int D>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5)))
+void w4_gemv_q_kernel(GemvQArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int nt = blockDim.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, j = lane & 3;
+  const int M = MQ == 1 ? 1 : a.M, N = a.N, K = a.K;
+  const int RB = K >> 1;     // bytes per weight row
+  const int ns = RB >> 8;    // spans per row (<= U)
+  const int ng = K / G;      // groups per row
+  const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
+  const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
+  const GemvQLds L = gemvq_lds(M, K, nt >> 6, G);
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)(M * K) * 2);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+
+  // 1. the wave's row quad, lane 4b+j reading bytes 256s + 16b of row 4q+j
+  // for span s. With D < U spans in flight, the loads of the first D go out
+  // here, ahead of the staging loads, and each later one goes out as the
+  // span D before it is taken up, so that the CU's memory queue serves all
+  // its waves' early spans before their late ones and every wave computes
+  // while the stream lasts (with all spans in flight at once, the waves
+  // issued last got their whole row last and computed it after the stream
+  // ended). With D = U, all of them go out after the staging loads.
+  const bool has_quad = wave < nql;
+  const int row = 4 * (qa + wave) + j;
+  const uint32_t wbase = has_quad ? (uint32_t)row * RB + 16u * b : kOob;
+  u32x4_t wv[U];
+  if constexpr (D < U) {
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+      wv[s] = buf_load16(rw, has_quad && s < ns ? wbase + 256u * s : kOob);
+  }
+
+  // 2. staging loads: activation pieces (64 B: 32 k; piece i of the M rows
+  // in order) and 16-byte (scale, bias) pieces of the workgroup's 4*nql
+  // rows. A thread takes at most one activation piece and at most two scale
+  // pieces (the plan gives the workgroup the waves for both); a wave with
+  // nothing to fetch skips the instruction.
+  const int nxp = M * (K >> 5);
+  const int nsp = (4 * nql * ng) >> 3;
+  u32x4_t xr[4], sr[2] = {}, br[2] = {};
+  if (64 * wave < nxp) {
+    const uint32_t off = tid < nxp ? 64u * tid : kOob;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) xr[w] = buf_load16(rx, off + 16 * w);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = tid + h * nt;
+    if (64 * wave + h * nt < nsp) {
+      const uint32_t off = t < nsp ? 8u * (uint32_t)qa * ng + 16u * t : kOob;
+      sr[h] = buf_load16(rs, off);
+      br[h] = buf_load16(rb, off);
+    }
+  }
+
+  if constexpr (D == U) {
+#pragma unroll
+    for (int s = 0; s < U; ++s)
+      wv[s] = buf_load16(rw, has_quad && s < ns ? wbase + 256u * s : kOob);
+  }
+
+  // keep every load above ahead of the arithmetic below
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. staged data to LDS
+  {
+    uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
+    float* xs = reinterpret_cast<float*>(smem + L.xs);
+    if (tid < nxp) {
+      // piece tid is piece `pc` of activation row m (rows of K/2 dwords)
+      const int m = MQ == 1 ? 0 : tid / (K >> 5), pc = tid - m * (K >> 5);
+      xs[MQ == 1 ? pc : 4 * pc + m] = stage_x_piece<T>(xp + m * (K >> 1), pc, xr);
+    }
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = tid + h * nt;
+      if (t < nsp) stage_sb_piece(sb, t, sr[h], br[h]);
+    }
+  }
+  __syncthreads();
+  if (!has_quad) return;
+
+  // 4. per span: activations from LDS, decode, eight 4x4x4 MFMAs, group
+  // epilogue; 5. the row quad's outputs
+  gemvq_spans<T, G, U, MQ, D>(a, wv, rw, wbase, smem, L, ns, wave, M, row);
 }
 
 // Plan: M <= 4, K % 512 == 0 with at most 8 spans per row, N % 4 == 0, the
@@ -248,7 +291,7 @@ void w4_gemv_q_kernel(GemvQArgs a) {
 // 14.1 on the multi-row streaming kernel, so they stay there.
 struct GemvQPlan {
   bool ok;
-  int P, NWQ, U, MQ;
+  int P, NWQ, U, MQ, D;
   size_t lds;
 };
 
@@ -265,11 +308,18 @@ static GemvQPlan plan_gemvq(int64_t M, int64_t N, int64_t K, int G) {
   if (cdiv(nq, P) > 16) P = cdiv(nq, 16);
   p.P = (int)P;
   p.NWQ = (int)cdiv(nq, P);
+  p.U = K / 512 <= 5 ? 5 : 8;
+  // weight loads in flight per wave: two when the CU holds at least 12 row-quad
+  // waves (gate+up: 19), all spans for smaller grids, whose few waves need
+  // every load in flight to keep the CU's stream going (QKV 3584 x 2560: 3.5
+  // waves per CU ran 3.68 -> 3.83 us at two)
+  const int64_t wpc = cdiv(P * p.NWQ, cus);
+  p.D = (int)env_int("SPARKQ_W4_GEMVQ_DEPTH", wpc >= 12 ? 2 : 8);
+  if (p.D != 1 && p.D != 2) p.D = 8;
   // threads enough to stage the activations, one 32-k piece each
   p.NWQ = (int)std::max<int64_t>(std::max<int64_t>(p.NWQ, 4), cdiv(M * K / 32, 64));
   if (p.NWQ > 16) return p;
   if (4 * p.NWQ * ng / 8 > 2 * 64 * p.NWQ) return p;  // two scale pieces per thread
-  p.U = K / 512 <= 5 ? 5 : 8;
   p.MQ = M == 1 ? 1 : 4;
   const GemvQLds l = gemvq_lds((int)M, (int)K, p.NWQ, G);
   if (l.bytes > 65536) return p;
@@ -278,14 +328,22 @@ static GemvQPlan plan_gemvq(int64_t M, int64_t N, int64_t K, int G) {
   return p;
 }
 
+template <typename T, int G, int MQ, int U>
+static void launch_gemvq_u(const GemvQPlan& p, const GemvQArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)p.P), block(64 * p.NWQ);
+  if (p.D == 1)
+    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, U, MQ, 1>), grid, block, p.lds, st, a);
+  else if (p.D == 2)
+    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, U, MQ, 2>), grid, block, p.lds, st, a);
+  else
+    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, U, MQ, U>), grid, block, p.lds, st, a);
+}
 template <typename T, int G, int MQ>
 static void launch_gemvq_m(const GemvQPlan& p, const GemvQArgs& a, hipStream_t st) {
   if (p.U == 5)
-    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, 5, MQ>), dim3((unsigned)p.P), dim3(64 * p.NWQ), p.lds,
-                       st, a);
+    launch_gemvq_u<T, G, MQ, 5>(p, a, st);
   else
-    hipLaunchKernelGGL((w4_gemv_q_kernel<T, G, 8, MQ>), dim3((unsigned)p.P), dim3(64 * p.NWQ), p.lds,
-                       st, a);
+    launch_gemvq_u<T, G, MQ, 8>(p, a, st);
 }
 template <typename T, int G>
 static void launch_gemvq_g(const GemvQPlan& p, const GemvQArgs& a, hipStream_t st) {

@@ -308,6 +308,24 @@ def test_decode_one_round_rows(gpu, m, n, k, g):
             assert torch.equal(y32[r:r + 1], y1), r
 
 
+@pytest.mark.parametrize("depth", ["1", "2"])
+@pytest.mark.parametrize("m,n,k,g", [(1, 19456, 2560, 64), (1, 1100, 3072, 32), (3, 1028, 4096, 128),
+                                     (4, 3584, 2560, 64), (1, 8, 512, 64)])
+def test_decode_one_round_load_depth(gpu, m, n, k, g, depth, monkeypatch):
+    """The one-round kernel with one or two weight loads per wave in flight
+    (each next span's load issued as a span is taken up; rows of 1..8 spans,
+    spans past the row's end, fewer row quads than waves): the output is bit
+    for bit that of all spans in flight, and within the oracle's tolerance."""
+    x, wq, s, b = w4_problem(m, n, k, g, seed=n + k + m)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    monkeypatch.setenv("SPARKQ_W4_GEMVQ_DEPTH", "8")
+    y_all = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    monkeypatch.setenv("SPARKQ_W4_GEMVQ_DEPTH", depth)
+    y = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    check_fp32(y.cpu().numpy(), ref)
+    assert torch.equal(y, y_all)
+
+
 @pytest.mark.parametrize("m", [2, 3, 4])
 def test_decode_mfma_rows_few(gpu, m, monkeypatch):
     """The 16x16x32 kernel below 5 rows stays correct."""
