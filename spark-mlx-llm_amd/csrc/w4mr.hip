@@ -111,7 +111,9 @@ __device__ __forceinline__ u32x4_t transpose_rows(u32x4_t v) {
   return u32x4_t{w0, w1, w2, w3};
 }
 
-template <typename T, int G, int NI>
+// D: weight items of a wave in flight (D < NI: the first D go out with the
+// staging loads, each later one as the item D before it is taken up)
+template <typename T, int G, int NI, int D>
 __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int NT = 64 * kMrNW;
@@ -169,15 +171,23 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
         br[i][e] = __builtin_amdgcn_raw_buffer_load_b32(rb, (int)off, 0, 0);
       }
   }
-  // 2. the wave's weight items
+  // 2. the wave's weight items: the first D now. With every item's load in
+  // flight at once, the CU's memory queue (activations, scales and weights:
+  // ~200 KB a CU for gate+up at 16 rows) kept each wave waiting at issue for
+  // up to ~7 us, the staging barrier waited for the last of them, and the
+  // items' arithmetic (3-5 us) ran after the stream; with one or two in
+  // flight the staging completes early (barrier ~6.6 -> ~4.4 us) and the
+  // items are computed as the weights arrive (gate+up at 16 rows 15.0 ->
+  // 13.3 us, down 13.6 -> 12.8-13.2).
   u32x4_t wv[NI];
-#pragma unroll
-  for (int k = 0; k < NI; ++k) {
+  auto wload = [&](int k) {
     const int it = i0 + k, tl = it / SEG, s = it - tl * SEG;
     const int row = 16 * (t0 + tl) + r16;
     const bool ok = k < ni && row < N;
     wv[k] = buf_load16(rw, ok ? (uint32_t)row * RB + (uint32_t)(kbase >> 1) + 64u * s + 16u * g : kOob);
-  }
+  };
+#pragma unroll
+  for (int k = 0; k < D; ++k) wload(k);
   __builtin_amdgcn_sched_barrier(0);
 
   // 3. activations and (scale, bias) pairs to LDS, then the group sums
@@ -247,6 +257,7 @@ __global__ __launch_bounds__(64 * kMrNW) void w4_mr16_kernel(MrArgs a) {
   };
 #pragma unroll
   for (int k = 0; k < NI; ++k) {
+    if (k + D < NI) wload(k + D);
     if (k < ni) {
       const int it = i0 + k, tl = it / SEG, s = it - tl * SEG;
       if (tl != cur) {
@@ -518,7 +529,7 @@ __global__ __launch_bounds__(1024) void w4_mr16s_kernel(MrsArgs a) {
 // against 9.2 us.
 struct MrPlan {
   bool ok;
-  int P, TW, IW, NI, KS;
+  int P, TW, IW, NI, KS, D;
   size_t lds, ws;
 };
 
@@ -547,6 +558,12 @@ static MrPlan plan_mr(int64_t M, int64_t N, int64_t K, int G) {
     p.IW = (int)iw;
     p.NI = iw <= 2 ? 2 : (iw <= 4 ? 4 : 8);
     p.KS = KS;
+    // weight items in flight per wave (SPARKQ_W4_MR_DEPTH: 1, 2, or 0 for
+    // all); one measured best (M = 9 / 12 / 16 sweeps 1365 / 1397 / 1340 ->
+    // 1492 / 1505 / 1458 GB/s; two 1475 / 1485 / 1430)
+    const char* de = getenv("SPARKQ_W4_MR_DEPTH");
+    const int dv = de ? atoi(de) : 1;
+    p.D = dv == 0 || p.NI <= 2 ? p.NI : (dv == 1 ? 1 : 2);
     p.lds = (size_t)l.bytes;
     p.ws = KS > 1 ? kCounterBytes + round_up((size_t)KS * M * N * 4, 256) : 0;
     p.ok = true;
@@ -555,14 +572,23 @@ static MrPlan plan_mr(int64_t M, int64_t N, int64_t K, int G) {
   return p;
 }
 
-template <typename T, int G, int NI>
-static void launch_mr_n(const MrPlan& p, const MrArgs& a, hipStream_t st) {
-  auto* k = w4_mr16_kernel<T, G, NI>;
+template <typename T, int G, int NI, int D>
+static void launch_mr_d(const MrPlan& p, const MrArgs& a, hipStream_t st) {
+  auto* k = w4_mr16_kernel<T, G, NI, D>;
   // dynamic LDS above 64 KB must be enabled per kernel
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, kMrMaxLds);
   (void)attr;
   hipLaunchKernelGGL(k, dim3((unsigned)p.P, (unsigned)p.KS), dim3(64 * kMrNW), p.lds, st, a);
+}
+template <typename T, int G, int NI>
+static void launch_mr_n(const MrPlan& p, const MrArgs& a, hipStream_t st) {
+  if (p.D == NI)
+    launch_mr_d<T, G, NI, NI>(p, a, st);
+  else if (p.D == 1)
+    launch_mr_d<T, G, NI, 1>(p, a, st);
+  else
+    launch_mr_d<T, G, NI, 2>(p, a, st);
 }
 template <typename T, int G>
 static void launch_mr_g(const MrPlan& p, const MrArgs& a, hipStream_t st) {

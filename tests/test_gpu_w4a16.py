@@ -326,6 +326,23 @@ def test_decode_one_round_load_depth(gpu, m, n, k, g, depth, monkeypatch):
     assert torch.equal(y, y_all)
 
 
+@pytest.mark.parametrize("m,n,k,g", [(16, 19456, 2560, 64), (12, 2560, 9728, 64), (9, 1000, 1152, 128)])
+def test_decode_mfma_rows_load_depth(gpu, m, n, k, g, monkeypatch):
+    """The tile-major 16x16x32 kernel with one, two or all weight items of a
+    wave in flight (each next item's load issued as an item is taken up;
+    whole K and K ranges): bit-identical outputs, within the oracle's
+    tolerance."""
+    monkeypatch.setenv("SPARKQ_W4_MR_TILED", "1")
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m + n)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    outs = []
+    for depth in ("0", "1", "2"):
+        monkeypatch.setenv("SPARKQ_W4_MR_DEPTH", depth)
+        outs.append(_run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32))
+    check_fp32(outs[1].cpu().numpy(), ref)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 @pytest.mark.parametrize("m", [2, 3, 4])
 def test_decode_mfma_rows_few(gpu, m, monkeypatch):
     """The 16x16x32 kernel below 5 rows stays correct."""
