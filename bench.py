@@ -820,7 +820,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(),
-                "kernel": "w4_gemv_q_kernel<BF16,64,5> (gate+up 19456x2560, M=1)",
+                "kernel": "w4_gemv_q_kernel<BF16,64,5,1,2> (gate+up 19456x2560, M=1)",
                 "bytes_per_launch": gu_bytes, "avg_launch_ms": round(gu_ms, 5)}
 
     extras = {}
