@@ -952,7 +952,9 @@ __host__ __device__ __forceinline__ DecLds dec_lds(int M, int K, int QW, int G, 
   return l;
 }
 
-template <typename T, int G, int MQ, int NI, bool FULL>
+// D: weight items of a wave in flight (D < NI: the first D go out ahead of the
+// staging loads, each later one as the item D before it is taken up)
+template <typename T, int G, int MQ, int NI, bool FULL, int D>
 __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStreamArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int NT = 64 * kDecNW;
@@ -985,6 +987,25 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
   const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
   const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
 
+  // the wave's items (slots past its last item read nothing)
+  int ql[NI], sp[NI];
+  u32x4_t wv[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int it = i0 + i;
+    ql[i] = it / U;
+    sp[i] = it - ql[i] * U;
+  }
+  auto wload = [&](int i) {
+    const int row = r0 + 4 * ql[i] + j, p = 256 * sp[i] + 16 * b;
+    const bool ok = i < nmy && row < r1 && (FULL || p + 16 <= RB);
+    wv[i] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
+  };
+  if constexpr (D < NI) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) wload(i);
+  }
+
   // 1. staging loads (a wave with no piece to fetch skips the instruction)
   const int nxp = M * np;
   const int nsp = (4 * nql * ng) >> 3;
@@ -1009,17 +1030,10 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
     }
   }
 
-  // 2. every weight load of the wave (slots past its last item read nothing)
-  int ql[NI], sp[NI];
-  u32x4_t wv[NI];
+  // 2. with every item in flight at once (D = NI), the weight loads
+  if constexpr (D == NI) {
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int it = i0 + i;
-    ql[i] = it / U;
-    sp[i] = it - ql[i] * U;
-    const int row = r0 + 4 * ql[i] + j, p = 256 * sp[i] + 16 * b;
-    const bool ok = i < nmy && row < r1 && (FULL || p + 16 <= RB);
-    wv[i] = buf_load16(rw, ok ? (uint32_t)row * RB + p : kOob);
+    for (int i = 0; i < NI; ++i) wload(i);
   }
 
   // keep every load above ahead of the arithmetic below
@@ -1083,6 +1097,7 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
   int first = nmy > 0 ? sp[0] : 0;   // first span of the current run
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
+    if (i + D < NI) wload(i + D);
     if (i < nmy) {
       const int s = sp[i];
       const int p = 256 * s + 16 * b;
@@ -2561,7 +2576,7 @@ static void launch_stream(const StreamPlan& p, int G, const GemvStreamArgs& a, h
 // (whole spans and row quads); LDS up to 160 KB.
 struct DecPlan {
   bool ok;
-  int P, QW, MQ, NI, RR;
+  int P, QW, MQ, NI, RR, D;
   size_t lds;
 };
 
@@ -2598,18 +2613,35 @@ static DecPlan plan_dec(int64_t M, int64_t N, int64_t K, int G) {
   const DecLds l = dec_lds((int)M, (int)K, p.QW, G, p.MQ);
   if (l.bytes > kDecMaxLds) return p;
   p.lds = (size_t)l.bytes;
+  // one weight item per wave in flight, the next issued as an item is taken
+  // up, for waves of four or more items: every item in flight at once kept
+  // the waves at issue while the CU's memory queue drained and put the items'
+  // arithmetic after the stream (M = 2 / 4 / 6 / 8 sweeps 2073 / 2054 / 1530 /
+  // 1419 -> 2119 / 2104 / 1604 / 1467 GB/s, gate+up at 8 rows 14.3-14.6 ->
+  // 13.2-14.2 us, down at 4 rows 8.5 -> 8.1 us); two items a wave (QKV at 8
+  // rows) stay all in flight (6.1 -> 6.2 us at one). SPARKQ_W4_DEC_DEPTH: 1 or
+  // 8 (all).
+  const int64_t dd = env_int("SPARKQ_W4_DEC_DEPTH", p.NI >= 4 ? 1 : 8);
+  p.D = dd == 1 ? 1 : p.NI;
   p.ok = true;
   return p;
 }
 
-template <typename T, int G, int MQ, int NI>
-static void launch_dec_n(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {
-  auto* k = w4_decode_stream_kernel<T, G, MQ, NI, true>;
+template <typename T, int G, int MQ, int NI, int D>
+static void launch_dec_k(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {
+  auto* k = w4_decode_stream_kernel<T, G, MQ, NI, true, D>;
   // dynamic LDS above 64 KB must be enabled per kernel
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, kDecMaxLds);
   (void)attr;
   hipLaunchKernelGGL(k, dim3((unsigned)p.P), dim3(64 * kDecNW), p.lds, st, a);
+}
+template <typename T, int G, int MQ, int NI>
+static void launch_dec_n(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {
+  if (p.D == 1)
+    launch_dec_k<T, G, MQ, NI, 1>(p, a, st);
+  else
+    launch_dec_k<T, G, MQ, NI, NI>(p, a, st);
 }
 template <typename T, int G, int MQ>
 static void launch_dec_m(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {

@@ -326,6 +326,24 @@ def test_decode_one_round_load_depth(gpu, m, n, k, g, depth, monkeypatch):
     assert torch.equal(y, y_all)
 
 
+@pytest.mark.parametrize("m,n,k,g", [(8, 19456, 2560, 64), (4, 2560, 9728, 64), (6, 1100, 3072, 32),
+                                     (5, 40, 9728, 64)])
+def test_decode_multirow_stream_load_depth(gpu, m, n, k, g, monkeypatch):
+    """The multi-row streaming kernel with one weight item of a wave in flight
+    (each next item's load issued as an item is taken up) and with every item
+    in flight: bit-identical outputs, within the oracle's tolerance."""
+    monkeypatch.setenv("SPARKQ_W4_NO_MR", "1")
+    monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m * 7 + n)
+    ref = o.w4a16_matmul(x, wq, s, b, g)
+    outs = []
+    for depth in ("8", "1"):
+        monkeypatch.setenv("SPARKQ_W4_DEC_DEPTH", depth)
+        outs.append(_run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32))
+    check_fp32(outs[1].cpu().numpy(), ref)
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("m,n,k,g", [(16, 19456, 2560, 64), (12, 2560, 9728, 64), (9, 1000, 1152, 128)])
 def test_decode_mfma_rows_load_depth(gpu, m, n, k, g, monkeypatch):
     """The tile-major 16x16x32 kernel with one, two or all weight items of a
