@@ -81,6 +81,7 @@ struct I8Args {
   int mode;
   int wgs;              // workgroups of the one-round rows kernel
   int tiles_n, tiles;   // tiled GEMM: column tiles, tiles (split items are piece-major)
+  int full;             // tiled GEMM: items [0, full) are whole tiles, the tiles past them split in S
   // one launch with the quantizer (3..16 rows): producer workgroups [0, np)
   // write the int8 rows of x into a (and their scales into sa); counters[0]
   // counts the rows written, counters[1] the workgroups done (both zero on
@@ -965,8 +966,10 @@ static bool use_rows_sync(int64_t M, int64_t K, int xdt) {
 // its int32 tile (16-byte stores at the device coherence level), the last
 // to arrive adds them (int32 addition is exact, so the result is the
 // unsplit one bit for bit) and writes the output, raw or through the
-// epilogue fmaf(float(acc) * sa[m], sw[n], bias[n]). Rows and columns past
-// M and N read zeros and are not stored; K % 128 == 0.
+// epilogue fmaf(float(acc) * sa[m], sw[n], bias[n]); grids of one to two
+// tiles per CU keep one whole tile per CU and split only the tiles past
+// them. Rows and columns past M and N read zeros and are not stored;
+// K % 128 == 0.
 constexpr int kI8GK = 128;  // bytes of k per step
 
 __device__ __forceinline__ uint32_t i8_tile_off(int row, int kc) {
@@ -983,10 +986,18 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8Args a) {
   const int wm = wave & 1, wn = wave >> 1;
   const int l32 = lane & 31, j = lane >> 5;
   const int M = a.M, N = a.N, K = a.K;
-  const int tile = blockIdx.x % a.tiles, piece = blockIdx.x / a.tiles;
+  // work item -> (tile, piece): items [0, full) are whole tiles; tile full + i
+  // of the rest is split in S pieces, piece p at item full + p * nsplit + i
+  // (piece-major, so that the workgroups running together read one k range)
+  const int item = blockIdx.x, nsplit = a.tiles - a.full;
+  const bool split = item >= a.full;
+  const int si = split ? (item - a.full) % nsplit : 0;  // split tile index
+  const int tile = split ? a.full + si : item;
+  const int piece = split ? (item - a.full) / nsplit : 0;
+  const int S = split ? a.S : 1;
   const int m0 = (tile / a.tiles_n) * BM, n0 = (tile % a.tiles_n) * BN;
   const int nst = K / kI8GK;
-  const int s_begin = (int)((int64_t)piece * nst / a.S), s_end = (int)((int64_t)(piece + 1) * nst / a.S);
+  const int s_begin = (int)((int64_t)piece * nst / S), s_end = (int)((int64_t)(piece + 1) * nst / S);
   const int mr = min(BM, M - m0), nr = min(BN, N - n0);
   const rsrc_t ra = make_rsrc(a.a + (int64_t)m0 * K, (uint32_t)mr * (uint32_t)K);
   const rsrc_t rb = make_rsrc(a.b + (int64_t)n0 * K, (uint32_t)nr * (uint32_t)K);
@@ -1055,10 +1066,10 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8Args a) {
     __syncthreads();
   }
 
-  if (a.S > 1) {
+  if (S > 1) {
     // this piece's tile: chunk c (16 bytes) of every thread at (c * 256 + tid) * 16
     constexpr uint32_t PB = 4 * 16 * 4 * 256;  // bytes per piece
-    const rsrc_t rp = make_rsrc(a.part + (size_t)tile * a.S * (PB / 4), (uint32_t)a.S * PB);
+    const rsrc_t rp = make_rsrc(a.part + (size_t)si * S * (PB / 4), (uint32_t)S * PB);
 #pragma unroll
     for (int xy = 0; xy < 4; ++xy)
 #pragma unroll
@@ -1069,11 +1080,11 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8Args a) {
         __builtin_amdgcn_raw_buffer_store_b128(w, rp, (uint32_t)tid * 16u,
                                                piece * PB + (xy * 4 + q) * 256 * 16, kSc1);
       }
-    if (!splitk_arrive(a.counters + tile, a.S, &s_last)) return;
+    if (!splitk_arrive(a.counters + si, S, &s_last)) return;
 #pragma unroll
     for (int xy = 0; xy < 4; ++xy) {
       i32x16_t t = acc[xy >> 1][xy & 1];
-      for (int z = 0; z < a.S; ++z) {
+      for (int z = 0; z < S; ++z) {
         if (z == piece) continue;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1085,7 +1096,7 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8Args a) {
       }
       acc[xy >> 1][xy & 1] = t;
     }
-    splitk_reset(a.counters + tile);
+    splitk_reset(a.counters + si);
   }
 
 #pragma unroll
@@ -1233,7 +1244,7 @@ static I8Plan plan_i8(int64_t M, int64_t N, int64_t K) {
 // least eight steps (tiles within the counter block).
 struct I8GemmPlan {
   bool ok;
-  int tiles_n, tiles, S;
+  int tiles_n, tiles, S, full;
   size_t part_bytes;
 };
 
@@ -1243,15 +1254,32 @@ static I8GemmPlan plan_i8_gemm(int64_t M, int64_t N, int64_t K) {
   if (K % kI8GK != 0 || (int64_t)kI8GK * K >= (int64_t)kOob) return p;
   const int64_t tn = cdiv(N, 128), tiles = cdiv(M, 128) * tn, cus = device_cus();
   if (tiles * 4 > (int64_t)0x7FFFFFFF) return p;
-  int64_t S = 1;
-  if (tiles < 2 * cus && tiles <= kMaxCounterTiles)
+  // Fewer tiles than CUs: every tile split in S pieces. Between one and two
+  // tiles per CU (M=2048 out_proj: 320 tiles on 256 CUs), one whole tile per
+  // CU and the tiles past them split in S pieces, so that every CU runs one
+  // whole tile and at most one piece instead of a quarter of the CUs running
+  // two whole tiles (the whole call at M=2048, N=2560, K=4096: 64.0-64.1 ->
+  // 57.7-59.3 us; SPARKQ_I8_GEMM_NO_CU1 keeps the unsplit grid).
+  int64_t S = 1, full = 0;
+  if (tiles < cus && tiles <= kMaxCounterTiles) {
     S = std::min<int64_t>(std::min<int64_t>(4, 2 * cus / tiles), std::max<int64_t>(1, (K / kI8GK) / 8));
-  if (env_int("SPARKQ_I8_GEMM_SPLITS", 0) > 0 && tiles <= kMaxCounterTiles)
+  } else if (tiles < 2 * cus && !env_int("SPARKQ_I8_GEMM_NO_CU1", 0)) {
+    const int64_t rest = tiles - cus;
+    const int64_t s = std::min<int64_t>(std::min<int64_t>(4, cus / rest), std::max<int64_t>(1, (K / kI8GK) / 8));
+    if (s > 1 && rest <= kMaxCounterTiles) {
+      S = s;
+      full = cus;
+    }
+  }
+  if (env_int("SPARKQ_I8_GEMM_SPLITS", 0) > 0 && tiles <= kMaxCounterTiles) {
     S = std::min<int64_t>(env_int("SPARKQ_I8_GEMM_SPLITS", 1), K / kI8GK);
+    full = 0;
+  }
   p.tiles_n = (int)tn;
   p.tiles = (int)tiles;
   p.S = (int)std::max<int64_t>(S, 1);
-  p.part_bytes = p.S > 1 ? round_up((size_t)tiles * p.S * 65536, 256) : 0;
+  p.full = p.S > 1 ? (int)full : (int)tiles;
+  p.part_bytes = p.S > 1 ? round_up((size_t)(tiles - p.full) * p.S * 65536, 256) : 0;
   p.ok = true;
   return p;
 }
@@ -1278,7 +1306,9 @@ static int launch_i8_gemm(I8Args args, const I8GemmPlan& p, hipStream_t st) {
   args.tiles_n = p.tiles_n;
   args.tiles = p.tiles;
   args.S = p.S;
-  hipLaunchKernelGGL(i8_gemm_kernel, dim3((unsigned)(p.tiles * p.S)), dim3(256), 0, st, args);
+  args.full = p.full;
+  hipLaunchKernelGGL(i8_gemm_kernel, dim3((unsigned)(p.full + (p.tiles - p.full) * p.S)), dim3(256), 0, st,
+                     args);
   return check_launch("i8_gemm_kernel");
 }
 

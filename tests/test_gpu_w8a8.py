@@ -286,6 +286,28 @@ def test_w8a8_prefill_out_proj_bit_exact(gpu, m):
     assert np.array_equal(y16[np.ix_(rows, cols)], o.round16(ref, o.BF16))
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 2176, 2048), (2048, 2560, 4096)])
+def test_int8_gemm_whole_and_split_tiles(gpu, m, n, k, monkeypatch):
+    """Between one and two 128 x 128 tiles per CU, the tiled int8 GEMM runs one
+    whole tile per CU and splits only the tiles past them (the last row tile's
+    columns here): the int32 accumulators of rows in both regions equal the
+    int64 oracle, and equal the unsplit grid's bit for bit."""
+    import sparkq
+
+    print(f"[case] int8 gemm whole+split m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    at, bt = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    c = sparkq.int8_matmul_int32(at, bt).cpu().numpy()
+    rows = np.sort(np.concatenate([rng.choice(m - 128, 48, replace=False),
+                                   m - 128 + rng.choice(128, 48, replace=False)]))
+    cols = np.sort(rng.choice(n, 128, replace=False))
+    assert np.array_equal(c[np.ix_(rows, cols)], o.int8_matmul(a[rows], b[cols]))
+    monkeypatch.setenv("SPARKQ_I8_GEMM_NO_CU1", "1")
+    assert np.array_equal(sparkq.int8_matmul_int32(at, bt).cpu().numpy(), c)
+
+
 @pytest.mark.parametrize("m,n,k", [(64, 96, 256), (130, 300, 512), (200, 2560, 1024),
                                    (1000, 130, 384), (257, 64, 8192), (96, 4100, 128)])
 @pytest.mark.parametrize("splits", ["0", "1", "3"])
