@@ -962,7 +962,7 @@ static bool use_rows_sync(int64_t M, int64_t K, int xdt) {
 // banks); the loads of step s+1 go out before the MFMAs of step s. Lane
 // (l % 32, l / 32) of a fragment holds bytes 16 * (l / 32) .. +15 of row
 // l % 32 of a 32-k sub-step, for activations and weights alike. Grids with
-// fewer tiles than twice the CUs split K into S pieces: each piece stores
+// fewer tiles than CUs split K into S pieces: each piece stores
 // its int32 tile (16-byte stores at the device coherence level), the last
 // to arrive adds them (int32 addition is exact, so the result is the
 // unsplit one bit for bit) and writes the output, raw or through the
