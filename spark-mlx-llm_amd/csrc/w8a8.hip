@@ -8,6 +8,10 @@
 //                        rows per workgroup, 4 rows x
 //                        256 bytes per load, v_dot4_i32_i8, activation
 //                        quantizer fused (one launch per projection)
+//   i8_gemv_stream_kernel  M = 1 over rows longer than 4096 k, M = 2 over
+//                        runs of at most 48 KB a CU: one 16-wave workgroup
+//                        per CU streams a contiguous run of weight rows in
+//                        1 KB items, all loads in flight; quantizer fused
 //   a8_quantize_kernel   one workgroup per token row (a8_quantize_reg_kernel
 //                        for rows of up to 32 KB: one load round trip): amax, scale = amax/127
 //                        (1 when 0), q = clamp(rint(x/scale), -127, 127);
@@ -247,6 +251,61 @@ __device__ __forceinline__ float piece_elem(const u32x4_t& v, int e) {
   return XT == 0 ? bf16_to_f32(h) : f16_to_f32(h);
 }
 
+// Sum over the 64 lanes of a wave (int32, exact): quads by DPP, the sixteen
+// quads by row rotations and the row and half swaps; lane 0's value.
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);
+  const auto r16 = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  v = (int)r16[0] + (int)r16[1];
+  const auto r32 = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return __builtin_amdgcn_readfirstlane((int)r32[0] + (int)r32[1]);
+}
+
+// Maximum over the 64 lanes of a wave (fmaxf: a NaN lane is ignored, as in a
+// chain of fmaxf), lane 0's value.
+__device__ __forceinline__ float wave_max(float v) {
+  v = max_row16(v);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
+}
+
+// Per-token amax of the staged activation pieces (piece pi of token row
+// pi*EP/K): each thread's maxima per row, reduced over the wave, then one
+// LDS atomic max per wave and row (exact in any order). All lanes active.
+template <int MQ, int NP, int XT>
+__device__ __forceinline__ void staged_amax(const u32x4_t (&xr)[NP], int nxp, int K, unsigned* amax) {
+  constexpr int EP = XT == 2 ? 4 : 8;
+  const int tid = threadIdx.x, NT = blockDim.x;
+  float mx[MQ];
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) mx[m] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int pi = tid + i * NT;
+    if (pi < nxp) {
+      float v = 0.0f;
+#pragma unroll
+      for (int e = 0; e < EP; ++e) v = fmaxf(v, fabsf(piece_elem<XT>(xr[i], e)));
+      const int r = (pi * EP) / K;
+#pragma unroll
+      for (int m = 0; m < MQ; ++m)
+        if (r == m) mx[m] = fmaxf(mx[m], v);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) {
+    const float w = wave_max(mx[m]);
+    if ((tid & 63) == 0)
+      __hip_atomic_fetch_max(&amax[m], __float_as_uint(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
 template <int MQ, int US, int NW, int XT>  // XT 3: int8 activations (raw int32 mode)
 __global__ __launch_bounds__(64 * NW) void i8_gemv_kernel(I8GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -296,17 +355,7 @@ __global__ __launch_bounds__(64 * NW) void i8_gemv_kernel(I8GemvArgs a) {
   if (tid < 4) amax[tid] = 0u;
   __syncthreads();
   if constexpr (XT != 3) {
-#pragma unroll
-    for (int i = 0; i < kI8XP; ++i) {
-      const int pi = tid + i * NT;
-      if (pi < nxp) {
-        float mx = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EP; ++e) mx = fmaxf(mx, fabsf(piece_elem<XT>(xr[i], e)));
-        __hip_atomic_fetch_max(&amax[(pi * EP) / K], __float_as_uint(mx), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-    }
+    staged_amax<MQ, kI8XP, XT>(xr, nxp, K, amax);
     __syncthreads();
   }
 #pragma unroll
@@ -403,6 +452,137 @@ __global__ __launch_bounds__(64 * NW) void i8_gemv_kernel(I8GemvArgs a) {
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// streaming int8 GEMV (M <= 2, rows of at least 1024 k), quantizer fused
+// ---------------------------------------------------------------------------
+// One workgroup of 16 waves per CU owns the rows [i*N/P, (i+1)*N/P), whose
+// weights are one contiguous run of bytes. The run is dealt to the waves in
+// 1 KB items (lane l: bytes 16l..16l+15 of the item; item t to wave t % 16),
+// and every weight load of a wave is issued at the start, right after the
+// activation staging loads, so each CU streams the same bytes with all of
+// them in flight. The workgroup quantizes the activations itself (per-token
+// amax over the whole row, scale = amax/127 with IEEE division, rint, clamp
+// to +-127, as a8_quantize_kernel) into LDS. Each lane meets its 16 weights
+// with the 16 activations of their columns in four v_dot4_i32_i8 per token
+// row; an item covers at most two weight rows (K >= 1024), whose lane sums
+// are added over the wave and into the rows' LDS sums (int32 addition is
+// exact in any order, so the output equals i8_gemv_kernel's bit for bit).
+constexpr int kI8SXP = 4;  // staged 16-byte activation pieces per thread, at most
+
+template <int MQ, int NI, int XT>
+__global__ __launch_bounds__(1024) void i8_gemv_stream_kernel(I8GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NW = 16, NT = 64 * NW;
+  constexpr int ES = XT == 2 ? 4 : 2;  // activation element bytes
+  constexpr int EP = 16 / ES;          // elements per piece
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = a.N, K = a.K;
+  const int r0 = (int)((int64_t)blockIdx.x * N / gridDim.x);
+  const int r1 = (int)((int64_t)(blockIdx.x + 1) * N / gridDim.x);
+  const int nr = r1 - r0;
+  const uint32_t base = (uint32_t)r0 * K;    // first byte of the run
+  const uint32_t B = (uint32_t)nr * K;       // bytes of the run
+  const int nit = (int)((B + 1023u) >> 10);  // items
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);                    // [MQ][K]
+  unsigned* amax = reinterpret_cast<unsigned*>(smem + ((MQ * K + 15) & ~15));
+  int* rsum = reinterpret_cast<int*>(amax + 4);                     // [nr][MQ]
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)MQ * K * ES);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * K);
+
+  // 1. staging loads of the activations (a wave with no piece skips them)
+  const int nxp = (MQ * K * ES) >> 4;
+  u32x4_t xr[kI8SXP];
+#pragma unroll
+  for (int i = 0; i < kI8SXP; ++i) {
+    const int pi = tid + i * NT;
+    if (i * NT + 64 * wave < nxp) xr[i] = buf_load16(rx, pi < nxp ? 16u * pi : kOob);
+  }
+  // 2. every weight load of the wave; bytes past the run read nothing
+  u32x4_t wv[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const uint32_t o = 1024u * (uint32_t)(wave + NW * i) + 16u * lane;
+    wv[i] = buf_load16(rw, o < B ? base + o : kOob);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. per-token amax (exact in any order), then the quantized rows in LDS
+  if (tid < 4) amax[tid] = 0u;
+  for (int t = tid; t < nr * MQ; t += NT) rsum[t] = 0;
+  __syncthreads();
+  staged_amax<MQ, kI8SXP, XT>(xr, nxp, K, amax);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kI8SXP; ++i) {
+    const int pi = tid + i * NT;
+    if (pi < nxp) {
+      const float am = __uint_as_float(amax[(pi * EP) / K]);
+      const float scale = am > 0.0f ? am / 127.0f : 1.0f;
+      uint32_t packed[EP / 4];
+#pragma unroll
+      for (int e = 0; e < EP / 4; ++e) packed[e] = 0u;
+#pragma unroll
+      for (int e = 0; e < EP; ++e) {
+        float v = __builtin_rintf(piece_elem<XT>(xr[i], e) / scale);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        packed[e >> 2] |= ((uint32_t)(int32_t)v & 0xFFu) << (8 * (e & 3));
+      }
+      if constexpr (EP == 8) {
+        *reinterpret_cast<uint2*>(xq + 8 * pi) = uint2{packed[0], packed[1]};
+      } else {
+        *reinterpret_cast<uint32_t*>(xq + 4 * pi) = packed[0];
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. the wave's items in issue order: lane row and column by a float
+  // quotient corrected once (o < 2^24), the item's first row from lane 0
+  const float invk = 1.0f / (float)K;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int it = wave + NW * i;
+    if (it < nit) {
+      const int o = 1024 * it + 16 * lane;
+      int rl = (int)((float)o * invk);
+      int col = o - rl * K;
+      if (col >= K) { col -= K; ++rl; }
+      if (col < 0) { col += K; --rl; }
+      const int ra = __builtin_amdgcn_readfirstlane(rl);
+      const bool two = __builtin_amdgcn_readlane(rl, 63) != ra && ra + 1 < nr;
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) {
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xq + m * K + col);
+        int t = 0;
+        t = __builtin_amdgcn_sdot4((int)wv[i].x, (int)xv.x, t, false);
+        t = __builtin_amdgcn_sdot4((int)wv[i].y, (int)xv.y, t, false);
+        t = __builtin_amdgcn_sdot4((int)wv[i].z, (int)xv.z, t, false);
+        t = __builtin_amdgcn_sdot4((int)wv[i].w, (int)xv.w, t, false);
+        const int ta = rl == ra ? t : 0;
+        const int sa = wave_sum_i32(ta);
+        if (lane == 0) atomicAdd(&rsum[ra * MQ + m], sa);
+        if (two) {
+          const int sb = wave_sum_i32(t - ta);
+          if (lane == 0) atomicAdd(&rsum[(ra + 1) * MQ + m], sb);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 5. epilogue: one thread per (row, token row)
+  for (int t = tid; t < nr * MQ; t += NT) {
+    const int rl = t / MQ, m = t - rl * MQ, row = r0 + rl;
+    const float sw = a.sw[row];
+    const float bias = a.bias ? load_in(a.bias, row, a.bias_dtype) : 0.0f;
+    const float am = __uint_as_float(amax[m]);
+    const float sa = am > 0.0f ? am / 127.0f : 1.0f;
+    store_out(a.y, (int64_t)m * N + row, fmaf((float)rsum[t] * sa, sw, bias), a.y_dtype);
   }
 }
 
@@ -1204,6 +1384,69 @@ static int launch_i8_gemv(const I8GemvPlan& p, const I8GemvArgs& a, int xt, hipS
   return check_launch("i8_gemv_kernel");
 }
 
+// Streaming int8 GEMV plan (M <= 2, 16-bit or fp32 activations): one
+// workgroup per CU, equal row ranges, at most 12 items of 1 KB per wave; the
+// activation rows must fit the staging registers and the run's byte offsets
+// the float quotient. Taken where it measured faster (MI355X, 36 distinct
+// weight sets per graph replay, bf16): one row over more than 4096 k (down
+// 2560 x 9728: 10.7 us against 11.1 on the rows kernel with its producer
+// workgroups and 10.85 on i8_gemv_kernel) and two rows over runs of at most
+// 48 KB a CU (QKV 3584 x 2560: 6.7 against 7.3 us). One row over short rows
+// (QKV 5.7 against 5.1 us) and runs of 97-194 KB at two rows (down 14.1
+// against 11.6, gate+up 20.5 against 15.3) stay on the other kernels, whose
+// several workgroups per CU overlap their staging chains.
+struct I8StreamPlan {
+  bool ok;
+  int P, NI;
+  size_t lds;
+};
+
+static I8StreamPlan plan_i8_stream(int64_t M, int64_t N, int64_t K, int esize) {
+  I8StreamPlan p{};
+  if (M < 1 || M > 2 || env_int("SPARKQ_I8_NO_STREAM", 0)) return p;
+  if (K < 1024 || K % 16 != 0 || N * K >= (int64_t)kOob) return p;
+  if (M * K * esize > (int64_t)kI8SXP * 16 * 1024) return p;
+  p.P = (int)std::min<int64_t>(N, device_cus());
+  const int64_t rows = cdiv(N, p.P), bytes = rows * K;
+  if (bytes >= (int64_t)1 << 24) return p;
+  const bool measured = M == 1 ? K > 4096 : bytes <= 48 * 1024;
+  if (!measured && !env_int("SPARKQ_I8_STREAM", 0)) return p;
+  const int64_t ni = cdiv(cdiv(bytes, 1024), 16);
+  if (ni > 12) return p;
+  p.NI = ni <= 4 ? 4 : (ni <= 6 ? 6 : (ni <= 8 ? 8 : 12));
+  p.lds = round_up((size_t)M * K, 16) + 16 + (size_t)rows * M * 4;
+  p.ok = p.lds <= 65536;
+  return p;
+}
+
+template <int MQ, int NI>
+static void launch_i8_stream_x(const I8StreamPlan& p, const I8GemvArgs& a, int xt,
+                               hipStream_t st) {
+  const dim3 grid((unsigned)p.P), block(1024);
+  switch (xt) {
+    case 0: hipLaunchKernelGGL((i8_gemv_stream_kernel<MQ, NI, 0>), grid, block, p.lds, st, a); break;
+    case 1: hipLaunchKernelGGL((i8_gemv_stream_kernel<MQ, NI, 1>), grid, block, p.lds, st, a); break;
+    default: hipLaunchKernelGGL((i8_gemv_stream_kernel<MQ, NI, 2>), grid, block, p.lds, st, a); break;
+  }
+}
+template <int MQ>
+static void launch_i8_stream_n(const I8StreamPlan& p, const I8GemvArgs& a, int xt,
+                               hipStream_t st) {
+  switch (p.NI) {
+    case 4: launch_i8_stream_x<MQ, 4>(p, a, xt, st); break;
+    case 6: launch_i8_stream_x<MQ, 6>(p, a, xt, st); break;
+    case 8: launch_i8_stream_x<MQ, 8>(p, a, xt, st); break;
+    default: launch_i8_stream_x<MQ, 12>(p, a, xt, st); break;
+  }
+}
+static int launch_i8_stream(const I8StreamPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  if (a.M == 1)
+    launch_i8_stream_n<1>(p, a, xt, st);
+  else
+    launch_i8_stream_n<2>(p, a, xt, st);
+  return check_launch("i8_gemv_stream_kernel");
+}
+
 // activation type code of the GEMV kernel (3 = int8) and its element size
 static int i8_xt(int xdt) { return xdt == SPARKQ_BF16 ? 0 : (xdt == SPARKQ_F16 ? 1 : 2); }
 static int esize_of(int xdt) { return xdt == SPARKQ_F32 ? 4 : 2; }
@@ -1410,6 +1653,23 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
 int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bias,
                 int bias_dtype, void* y, int64_t M, int64_t N, int64_t K, int xdt, int ydt,
                 void* ws, size_t wsb, hipStream_t st) {
+  const I8StreamPlan sp = plan_i8_stream(M, N, K, esize_of(xdt));
+  if (sp.ok) {
+    I8GemvArgs g{};
+    g.x = x;
+    g.w = w;
+    g.sw = wsc;
+    g.bias = bias;
+    g.bias_dtype = bias_dtype;
+    g.y = y;
+    g.y_dtype = ydt;
+    g.x_dtype = xdt;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.mode = kOutEpilogue;
+    return launch_i8_stream(sp, g, i8_xt(xdt), st);
+  }
   const I8GemvPlan gp = plan_i8_gemv(M, N, K, esize_of(xdt));
   if (gp.ok) {
     I8GemvArgs g{};

@@ -196,6 +196,46 @@ def test_w8a8_linear_bit_exact(gpu, m, n, k, dtype, with_bias):
         assert np.array_equal(down16(y)[:, cols], o.round16(ref, dtype))
 
 
+@pytest.mark.parametrize("dtype", [o.BF16, o.F16, o.F32])
+@pytest.mark.parametrize("m,n,k", [(1, 2560, 9728), (2, 2560, 9728), (1, 3584, 2560), (2, 19456, 2560),
+                                   (1, 37, 1056), (2, 300, 4096), (1, 257, 1024), (2, 100, 8192),
+                                   (1, 9, 2048)])
+def test_w8a8_linear_stream(gpu, m, n, k, dtype, monkeypatch):
+    """1..2 rows on the streaming int8 GEMV (one workgroup per CU over a
+    contiguous run of weight rows, 1 KB items that may cross a row end, the
+    quantizer fused): the fp32 epilogue bit for bit against the oracle on
+    sampled columns and the first and last rows of every run, and equal in
+    full to the kernels that serve these shapes without it."""
+    import sparkq
+
+    print(f"[case] w8a8 stream m={m} n={n} k={k} dtype={dtype}", flush=True)
+    wq, wsc = _w8(n, k, seed=4)
+    if dtype == o.F32:
+        xf = o.randn(5, m, m * k).reshape(m, k)
+        xt = torch.from_numpy(xf).to(gpu)
+    else:
+        x16 = _x(m, k, dtype, seed=5)
+        xf = o.bits_to_f32(x16, dtype)
+        xt = up16(x16, dtype, gpu)
+    bias = o.randn(6, n, n)
+    bias_t = torch.from_numpy(bias).to(gpu)
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    monkeypatch.setenv("SPARKQ_I8_STREAM", "1")
+    y32 = sparkq.w8a8_linear(xt, wt, st, bias_t, out_dtype=torch.float32)
+    y16 = sparkq.w8a8_linear(xt, wt, st, bias_t)
+    monkeypatch.setenv("SPARKQ_I8_NO_STREAM", "1")
+    assert torch.equal(y32, sparkq.w8a8_linear(xt, wt, st, bias_t, out_dtype=torch.float32))
+    assert torch.equal(y16, sparkq.w8a8_linear(xt, wt, st, bias_t))
+    p = min(n, 256)
+    edges = {r for i in range(p) for r in (i * n // p, (i + 1) * n // p - 1)}
+    rng = np.random.default_rng(n + k)
+    cols = np.array(sorted(edges | set(rng.choice(n, min(n, 256), replace=False).tolist())))
+    cols = cols[:768]
+    qa, sa = o.a8_quantize(xf)
+    ref = o.w8a8_epilogue(o.int8_matmul(qa, wq[cols]), sa, wsc[cols], bias[cols])
+    assert np.array_equal(y32.cpu().numpy()[:, cols].view(np.uint32), ref.view(np.uint32))
+
+
 BENCH_PROJ = {"qkv": (3584, 2560), "gate_up": (19456, 2560), "down": (2560, 9728)}
 
 
