@@ -45,6 +45,29 @@ def test_w8a16_matches_oracle(gpu, m, n, k, dtype):
     check_rounded16(down16(_run(gpu, x, w8, sc, dtype)), ref, dtype)
 
 
+@pytest.mark.parametrize("n,k", [(3584, 2560), (19456, 2560), (37, 512), (1030, 2560), (5, 256),
+                                 (300, 1024), (600, 2304)])
+def test_w8a16_one_round(gpu, n, k, monkeypatch):
+    """M = 1 over whole 256-k spans up to K = 2560 on the one-round kernel (one
+    row quad per wave, spans in order with one, two or every load in flight):
+    the three issue depths give identical bits, each within the oracle's
+    tolerance, as is the streaming kernel on the same problem; a partial row
+    quad, fewer quads than CUs and more than eight per CU."""
+    for dtype in (o.BF16, o.F16):
+        x, w8, sc = _problem(1, n, k, dtype, seed=n + 3 * k)
+        ref = o.w8a16_matmul(x, w8, sc, dtype)
+        outs = []
+        for depth in ("8", "1", "2"):
+            monkeypatch.setenv("SPARKQ_W8A16_Q_DEPTH", depth)
+            outs.append(_run(gpu, x, w8, sc, dtype, out_dtype=torch.float32))
+        check_fp32(outs[0].cpu().numpy(), ref)
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+        check_rounded16(down16(_run(gpu, x, w8, sc, dtype)), ref, dtype)
+        monkeypatch.setenv("SPARKQ_W8A16_NO_Q", "1")
+        check_fp32(_run(gpu, x, w8, sc, dtype, out_dtype=torch.float32).cpu().numpy(), ref)
+        monkeypatch.delenv("SPARKQ_W8A16_NO_Q")
+
+
 def test_one_hot_picks_scaled_column(gpu):
     n, k = 300, 1024
     _, w8, sc = _problem(1, n, k, o.BF16, seed=3)
