@@ -8,6 +8,8 @@
 //                        rows per workgroup, 4 rows x
 //                        256 bytes per load, v_dot4_i32_i8, activation
 //                        quantizer fused (one launch per projection)
+//   i8_gemvq_kernel      M = 2 over whole 256-k spans up to K = 2560: one
+//                        row quad per wave over its whole row, quantizer fused
 //   i8_gemv_stream_kernel  M = 1 over rows longer than 4096 k, M = 2 over
 //                        runs of at most 48 KB a CU: one 16-wave workgroup
 //                        per CU streams a contiguous run of weight rows in
@@ -238,6 +240,7 @@ struct I8GemvArgs {
   int M, N, K;
   int SG, USr, R;
   int mode;
+  int nq, P;  // one-round kernel: row quads, workgroups
 };
 
 constexpr int kI8XP = 4;  // staged 16-byte activation pieces per thread, at most
@@ -583,6 +586,137 @@ __global__ __launch_bounds__(1024) void i8_gemv_stream_kernel(I8GemvArgs a) {
     const float am = __uint_as_float(amax[m]);
     const float sa = am > 0.0f ? am / 127.0f : 1.0f;
     store_out(a.y, (int64_t)m * N + row, fmaf((float)rsum[t] * sa, sw, bias), a.y_dtype);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// one-round int8 GEMV (M <= 2, rows of up to 2560 k), quantizer fused
+// ---------------------------------------------------------------------------
+// The layout of the W4 and W8A16 one-round GEMVs: every workgroup owns a
+// contiguous range of row quads, one quad per wave, and the grid holds every
+// quad at once. The workgroup stages and quantizes the activations as
+// i8_gemv_kernel does (per-token amax, IEEE division, rint, clamp); a wave
+// walks its quad's 256-byte spans in order (lane 4b+j: bytes 256s + 16b of
+// row 4q+j) with D spans' loads in flight (the first D ahead of the staging
+// loads, each later one issued as the span D before it is taken up; all of
+// them right after the staging loads when D = U), four v_dot4_i32_i8 per
+// span and token row, and adds the quad's lanes by shuffles (int32: exact,
+// so the output equals i8_gemv_kernel's bit for bit).
+constexpr int kI8QXP = 4;  // staged 16-byte activation pieces per thread, at most
+
+template <int MQ, int U, int D, int XT>
+__global__ __launch_bounds__(1024) void i8_gemvq_kernel(I8GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int ES = XT == 2 ? 4 : 2;  // activation element bytes
+  constexpr int EP = 16 / ES;          // elements per piece
+  const int NT = blockDim.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, j = lane & 3;
+  const int N = a.N, K = a.K;
+  const int ns = K >> 8;  // spans per row (<= U)
+  const int qa = (int)((int64_t)blockIdx.x * a.nq / a.P);
+  const int nql = (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P) - qa;
+  int8_t* xq = reinterpret_cast<int8_t*>(smem);                    // [MQ][K]
+  unsigned* amax = reinterpret_cast<unsigned*>(smem + ((MQ * K + 15) & ~15));
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)MQ * K * ES);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * K);
+
+  const bool has_quad = wave < nql;
+  const int row = 4 * (qa + wave) + j;
+  const uint32_t wbase = has_quad && row < N ? (uint32_t)row * K + 16u * b : kOob;
+  u32x4_t wv[U];
+  if constexpr (D < U) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) wv[s] = buf_load16(rw, s < ns ? wbase + 256u * s : kOob);
+  }
+  // staging loads: the MQ rows' 16-byte pieces; a wave with none skips them
+  const int nxp = (MQ * K * ES) >> 4;
+  u32x4_t xr[kI8QXP];
+#pragma unroll
+  for (int i = 0; i < kI8QXP; ++i) {
+    const int pi = tid + i * NT;
+    if (i * NT + 64 * wave < nxp) xr[i] = buf_load16(rx, pi < nxp ? 16u * pi : kOob);
+  }
+  if constexpr (D == U) {
+#pragma unroll
+    for (int s = 0; s < U; ++s) wv[s] = buf_load16(rw, s < ns ? wbase + 256u * s : kOob);
+  }
+  // keep every load above ahead of the arithmetic below
+  __builtin_amdgcn_sched_barrier(0);
+
+  // per-token amax, then the quantized rows in LDS
+  if (tid < 4) amax[tid] = 0u;
+  __syncthreads();
+  staged_amax<MQ, kI8QXP, XT>(xr, nxp, K, amax);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kI8QXP; ++i) {
+    const int pi = tid + i * NT;
+    if (pi < nxp) {
+      const float am = __uint_as_float(amax[(pi * EP) / K]);
+      const float scale = am > 0.0f ? am / 127.0f : 1.0f;
+      uint32_t packed[EP / 4];
+#pragma unroll
+      for (int e = 0; e < EP / 4; ++e) packed[e] = 0u;
+#pragma unroll
+      for (int e = 0; e < EP; ++e) {
+        float v = __builtin_rintf(piece_elem<XT>(xr[i], e) / scale);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        packed[e >> 2] |= ((uint32_t)(int32_t)v & 0xFFu) << (8 * (e & 3));
+      }
+      if constexpr (EP == 8) {
+        *reinterpret_cast<uint2*>(xq + 8 * pi) = uint2{packed[0], packed[1]};
+      } else {
+        *reinterpret_cast<uint32_t*>(xq + 4 * pi) = packed[0];
+      }
+    }
+  }
+  __syncthreads();
+  if (!has_quad) return;
+
+  int32_t acc[MQ];
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) acc[m] = 0;
+#pragma unroll
+  for (int s = 0; s < U; ++s) {
+    // span s + D's load goes out as span s is taken up
+    if (s + D < U) wv[s + D] = buf_load16(rw, s + D < ns ? wbase + 256u * (s + D) : kOob);
+    if (s < ns) {
+      const int p = 256 * s + 16 * b;
+#pragma unroll
+      for (int m = 0; m < MQ; ++m) {
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xq + m * K + p);
+        int32_t t = acc[m];
+        t = __builtin_amdgcn_sdot4((int)wv[s].x, (int)xv.x, t, false);
+        t = __builtin_amdgcn_sdot4((int)wv[s].y, (int)xv.y, t, false);
+        t = __builtin_amdgcn_sdot4((int)wv[s].z, (int)xv.z, t, false);
+        t = __builtin_amdgcn_sdot4((int)wv[s].w, (int)xv.w, t, false);
+        acc[m] = t;
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MQ; ++m) {
+    int32_t v = acc[m];
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 8);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    acc[m] = v;
+  }
+  // lanes 0..3 hold rows 4q..4q+3
+  const int orow = 4 * (qa + wave) + lane;
+  if (lane < 4 && orow < N) {
+    const float sw = a.sw[orow];
+    const float bias = a.bias ? load_in(a.bias, orow, a.bias_dtype) : 0.0f;
+#pragma unroll
+    for (int m = 0; m < MQ; ++m) {
+      const float am = __uint_as_float(amax[m]);
+      const float sa = am > 0.0f ? am / 127.0f : 1.0f;
+      store_out(a.y, (int64_t)m * N + orow, fmaf((float)acc[m] * sa, sw, bias), a.y_dtype);
+    }
   }
 }
 
@@ -1447,6 +1581,76 @@ static int launch_i8_stream(const I8StreamPlan& p, const I8GemvArgs& a, int xt, 
   return check_launch("i8_gemv_stream_kernel");
 }
 
+// One-round int8 GEMV plan (M <= 2, K % 256 == 0, K <= 2560): the W4
+// one-round grid (twice the CUs workgroups when that gives at least 8 quads
+// per CU, else one per CU, at most 16 row-quad waves each), with at least the
+// waves that stage the activations; two spans in flight per wave where a CU
+// holds 12 or more row-quad waves, every span on smaller grids. Taken at two
+// rows, where it measured faster (MI355X, 36 distinct weight sets per graph
+// replay, bf16): QKV 3584 x 2560 6.8 -> 6.0 us against the streaming int8
+// GEMV, gate+up 19456 x 2560 15.4 -> 13.6 us (13.9 at one span in flight,
+// 16.8 at all) against i8_gemv_kernel. At one row i8_gemv_kernel's 1216
+// four-wave workgroups stay faster on gate+up (12.0 against 12.9-14.4 us)
+// and QKV is even (5.1 / 5.0 us).
+struct I8QPlan {
+  bool ok;
+  int P, NWQ, U, D;
+  size_t lds;
+};
+
+static I8QPlan plan_i8q(int64_t M, int64_t N, int64_t K, int esize) {
+  I8QPlan p{};
+  if (M < 1 || M > 2 || K % 256 != 0 || K > 2560 || env_int("SPARKQ_I8_NO_Q", 0)) return p;
+  if (M != 2 && !env_int("SPARKQ_I8_Q", 0)) return p;
+  if (N * K >= (int64_t)kOob) return p;
+  const int64_t nq = cdiv(N, 4), cus = device_cus();
+  int64_t P = std::min<int64_t>(nq, cus * (nq >= 8 * cus ? 2 : 1));
+  if (cdiv(nq, P) > 16) P = cdiv(nq, 16);
+  p.P = (int)P;
+  const int64_t wpc = cdiv(nq, cus);
+  p.NWQ = (int)std::max<int64_t>(cdiv(nq, P), cdiv(M * K * esize / 16, 64 * kI8QXP));
+  if (p.NWQ > 16) return p;
+  p.U = K <= 1024 ? 4 : 10;
+  const int64_t d = env_int("SPARKQ_I8_Q_DEPTH", wpc >= 12 ? 2 : 8);
+  p.D = d == 1 || d == 2 ? (int)d : p.U;
+  p.lds = round_up((size_t)M * K, 16) + 16;
+  p.ok = true;
+  return p;
+}
+
+template <int MQ, int U, int D>
+static void launch_i8q_x(const I8QPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  const dim3 grid((unsigned)p.P), block(64 * p.NWQ);
+  switch (xt) {
+    case 0: hipLaunchKernelGGL((i8_gemvq_kernel<MQ, U, D, 0>), grid, block, p.lds, st, a); break;
+    case 1: hipLaunchKernelGGL((i8_gemvq_kernel<MQ, U, D, 1>), grid, block, p.lds, st, a); break;
+    default: hipLaunchKernelGGL((i8_gemvq_kernel<MQ, U, D, 2>), grid, block, p.lds, st, a); break;
+  }
+}
+template <int MQ, int U>
+static void launch_i8q_u(const I8QPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  if (p.D == 1)
+    launch_i8q_x<MQ, U, 1>(p, a, xt, st);
+  else if (p.D == 2)
+    launch_i8q_x<MQ, U, 2>(p, a, xt, st);
+  else
+    launch_i8q_x<MQ, U, U>(p, a, xt, st);
+}
+template <int MQ>
+static void launch_i8q_m(const I8QPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  if (p.U == 4)
+    launch_i8q_u<MQ, 4>(p, a, xt, st);
+  else
+    launch_i8q_u<MQ, 10>(p, a, xt, st);
+}
+static int launch_i8q(const I8QPlan& p, const I8GemvArgs& a, int xt, hipStream_t st) {
+  if (a.M == 1)
+    launch_i8q_m<1>(p, a, xt, st);
+  else
+    launch_i8q_m<2>(p, a, xt, st);
+  return check_launch("i8_gemvq_kernel");
+}
+
 // activation type code of the GEMV kernel (3 = int8) and its element size
 static int i8_xt(int xdt) { return xdt == SPARKQ_BF16 ? 0 : (xdt == SPARKQ_F16 ? 1 : 2); }
 static int esize_of(int xdt) { return xdt == SPARKQ_F32 ? 4 : 2; }
@@ -1653,6 +1857,25 @@ int int8_matmul_i32(const int8_t* a, const int8_t* b, int32_t* c, int64_t M, int
 int w8a8_linear(const void* x, const int8_t* w, const float* wsc, const void* bias,
                 int bias_dtype, void* y, int64_t M, int64_t N, int64_t K, int xdt, int ydt,
                 void* ws, size_t wsb, hipStream_t st) {
+  const I8QPlan qp = plan_i8q(M, N, K, esize_of(xdt));
+  if (qp.ok) {
+    I8GemvArgs g{};
+    g.x = x;
+    g.w = w;
+    g.sw = wsc;
+    g.bias = bias;
+    g.bias_dtype = bias_dtype;
+    g.y = y;
+    g.y_dtype = ydt;
+    g.x_dtype = xdt;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.mode = kOutEpilogue;
+    g.nq = (int)cdiv(N, 4);
+    g.P = qp.P;
+    return launch_i8q(qp, g, i8_xt(xdt), st);
+  }
   const I8StreamPlan sp = plan_i8_stream(M, N, K, esize_of(xdt));
   if (sp.ok) {
     I8GemvArgs g{};

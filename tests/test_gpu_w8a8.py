@@ -236,6 +236,49 @@ def test_w8a8_linear_stream(gpu, m, n, k, dtype, monkeypatch):
     assert np.array_equal(y32.cpu().numpy()[:, cols].view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("dtype", [o.BF16, o.F16, o.F32])
+@pytest.mark.parametrize("m,n,k", [(1, 3584, 2560), (2, 3584, 2560), (1, 19456, 2560), (2, 19456, 2560),
+                                   (1, 37, 512), (2, 1030, 2560), (1, 5, 256), (2, 300, 1024)])
+def test_w8a8_linear_one_round(gpu, m, n, k, dtype, monkeypatch):
+    """1..2 rows over whole 256-k spans up to K = 2560 on the one-round int8
+    GEMV (one row quad per wave over its whole row, the quantizer fused, one,
+    two or every span in flight): the fp32 epilogue bit for bit against the
+    oracle on the first and last rows and sampled columns, and equal in full
+    to the kernels that serve these shapes without it; a partial row quad,
+    fewer quads than CUs and more than eight per CU."""
+    import sparkq
+
+    print(f"[case] w8a8 one-round m={m} n={n} k={k} dtype={dtype}", flush=True)
+    wq, wsc = _w8(n, k, seed=8)
+    if dtype == o.F32:
+        xf = o.randn(9, m, m * k).reshape(m, k)
+        xt = torch.from_numpy(xf).to(gpu)
+    else:
+        x16 = _x(m, k, dtype, seed=9)
+        xf = o.bits_to_f32(x16, dtype)
+        xt = up16(x16, dtype, gpu)
+    bias = o.randn(10, n, n)
+    bias_t = torch.from_numpy(bias).to(gpu)
+    wt, st = torch.from_numpy(wq).to(gpu), torch.from_numpy(wsc).to(gpu)
+    monkeypatch.setenv("SPARKQ_I8_Q", "1")
+    outs = []
+    for depth in ("8", "1", "2"):
+        monkeypatch.setenv("SPARKQ_I8_Q_DEPTH", depth)
+        outs.append(sparkq.w8a8_linear(xt, wt, st, bias_t, out_dtype=torch.float32))
+    y16 = sparkq.w8a8_linear(xt, wt, st, bias_t)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    monkeypatch.setenv("SPARKQ_I8_NO_Q", "1")
+    monkeypatch.delenv("SPARKQ_I8_Q")
+    assert torch.equal(outs[0], sparkq.w8a8_linear(xt, wt, st, bias_t, out_dtype=torch.float32))
+    assert torch.equal(y16, sparkq.w8a8_linear(xt, wt, st, bias_t))
+    rng = np.random.default_rng(n + k + m)
+    cols = np.unique(np.concatenate([np.arange(min(n, 8)), np.arange(max(0, n - 8), n),
+                                     rng.choice(n, min(n, 256), replace=False)]))
+    qa, sa = o.a8_quantize(xf)
+    ref = o.w8a8_epilogue(o.int8_matmul(qa, wq[cols]), sa, wsc[cols], bias[cols])
+    assert np.array_equal(outs[0].cpu().numpy()[:, cols].view(np.uint32), ref.view(np.uint32))
+
+
 BENCH_PROJ = {"qkv": (3584, 2560), "gate_up": (19456, 2560), "down": (2560, 9728)}
 
 
