@@ -177,7 +177,7 @@ __device__ __forceinline__ void gemvq_spans(const GemvQArgs& a, u32x4_t (&wv)[U]
 }
 
 // MQ: 1, or 4 for 2..4 activation rows; D: weight loads of a wave in flight
-// (the first D spans' go out before the staging loads)
+// (the first D spans' go out right after the staging loads)
 template <typename T, int G, int U, int MQ, int D>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(5)))
 void w4_gemv_q_kernel(GemvQArgs a) {
@@ -201,21 +201,18 @@ void w4_gemv_q_kernel(GemvQArgs a) {
 
   // 1. the wave's row quad, lane 4b+j reading bytes 256s + 16b of row 4q+j
   // for span s. With D < U spans in flight, the loads of the first D go out
-  // here, ahead of the staging loads, and each later one goes out as the
-  // span D before it is taken up, so that the CU's memory queue serves all
-  // its waves' early spans before their late ones and every wave computes
-  // while the stream lasts (with all spans in flight at once, the waves
-  // issued last got their whole row last and computed it after the stream
-  // ended). With D = U, all of them go out after the staging loads.
+  // right after the staging loads and each later one as the span D before
+  // it is taken up, so that the CU's memory queue serves all its waves'
+  // early spans before their late ones and every wave computes while the
+  // stream lasts (with all spans in flight at once, the waves issued last
+  // got their whole row last and computed it after the stream ended). The
+  // staging loads go first: the workgroup's barrier waits for them, not for
+  // the weights (gate+up 7.67 -> 7.53 us, 4 rows 9.22 -> 9.03 us against the
+  // first D weight loads ahead of them). With D = U all spans go out there.
   const bool has_quad = wave < nql;
   const int row = 4 * (qa + wave) + j;
   const uint32_t wbase = has_quad ? (uint32_t)row * RB + 16u * b : kOob;
   u32x4_t wv[U];
-  if constexpr (D < U) {
-#pragma unroll
-    for (int s = 0; s < D; ++s)
-      wv[s] = buf_load16(rw, has_quad && s < ns ? wbase + 256u * s : kOob);
-  }
 
   // 2. staging loads: activation pieces (64 B: 32 k; piece i of the M rows
   // in order) and 16-byte (scale, bias) pieces of the workgroup's 4*nql
@@ -240,11 +237,10 @@ void w4_gemv_q_kernel(GemvQArgs a) {
     }
   }
 
-  if constexpr (D == U) {
+  // the first D spans' weights (all of them when D = U)
 #pragma unroll
-    for (int s = 0; s < U; ++s)
-      wv[s] = buf_load16(rw, has_quad && s < ns ? wbase + 256u * s : kOob);
-  }
+  for (int s = 0; s < D; ++s)
+    wv[s] = buf_load16(rw, has_quad && s < ns ? wbase + 256u * s : kOob);
 
   // keep every load above ahead of the arithmetic below
   __builtin_amdgcn_sched_barrier(0);
