@@ -87,6 +87,7 @@ struct I8Args {
   int mode;
   int wgs;              // workgroups of the one-round rows kernel
   int tiles_n, tiles;   // tiled GEMM: column tiles, tiles (split items are piece-major)
+  int gm;               // tiled GEMM: tile rows per group of the tile order (0: row-major)
   int full;             // tiled GEMM: items [0, full) are whole tiles, the tiles past them split in S
   // one launch with the quantizer (3..16 rows): producer workgroups [0, np)
   // write the int8 rows of x into a (and their scales into sa); counters[0]
@@ -1282,8 +1283,11 @@ static bool use_rows_sync(int64_t M, int64_t K, int xdt) {
 // unsplit one bit for bit) and writes the output, raw or through the
 // epilogue fmaf(float(acc) * sa[m], sw[n], bias[n]); grids of one to two
 // tiles per CU keep one whole tile per CU and split only the tiles past
-// them. Rows and columns past M and N read zeros and are not stored;
-// K % 128 == 0.
+// them. Work item i runs on XCD i % 8 (round-robin dispatch): the tile
+// order gives each XCD a contiguous chunk of tiles walked in groups of four
+// tile rows, so the tiles an XCD runs together share their A rows and B
+// columns in its L2. Rows and columns past M and N read zeros and are not
+// stored; K % 128 == 0.
 constexpr int kI8GK = 128;  // bytes of k per step
 
 __device__ __forceinline__ uint32_t i8_tile_off(int row, int kc) {
@@ -1309,7 +1313,19 @@ __global__ __launch_bounds__(256, 2) void i8_gemm_kernel(I8Args a) {
   const int tile = split ? a.full + si : item;
   const int piece = split ? (item - a.full) / nsplit : 0;
   const int S = split ? a.S : 1;
-  const int m0 = (tile / a.tiles_n) * BM, n0 = (tile % a.tiles_n) * BN;
+  int tm = tile / a.tiles_n, tn = tile - tm * a.tiles_n;
+  if (a.gm > 0) {
+    // XCD-contiguous chunks of the tile order (workgroups go to the XCDs
+    // round-robin, so item i runs on XCD i % 8), each chunk walking groups of
+    // gm tile rows column by column
+    const int T = a.tiles;
+    const int v = (T & 7) == 0 ? (tile & 7) * (T >> 3) + (tile >> 3) : tile;
+    const int tiles_m = T / a.tiles_n, width = a.gm * a.tiles_n;
+    const int g = v / width, fm = g * a.gm, gs = min(tiles_m - fm, a.gm), r = v - g * width;
+    tm = fm + r % gs;
+    tn = r / gs;
+  }
+  const int m0 = tm * BM, n0 = tn * BN;
   const int nst = K / kI8GK;
   const int s_begin = (int)((int64_t)piece * nst / S), s_end = (int)((int64_t)(piece + 1) * nst / S);
   const int mr = min(BM, M - m0), nr = min(BN, N - n0);
@@ -1751,6 +1767,10 @@ size_t i8_matmul_workspace(int64_t M, int64_t N, int64_t K) {
 
 static int launch_i8_gemm(I8Args args, const I8GemmPlan& p, hipStream_t st) {
   args.tiles_n = p.tiles_n;
+  // XCD-grouped tile order, groups of four tile rows (M = 2048 / 4096 out_proj
+  // 780 -> 800 / 844 -> 868 TOP/s; M = 512 unchanged); SPARKQ_I8_GEMM_ROWMAJOR
+  // keeps the row-major order
+  args.gm = env_int("SPARKQ_I8_GEMM_ROWMAJOR", 0) ? 0 : (int)env_int("SPARKQ_I8_GEMM_GM", 4);
   args.tiles = p.tiles;
   args.S = p.S;
   args.full = p.full;

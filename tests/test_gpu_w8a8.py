@@ -391,6 +391,30 @@ def test_int8_gemm_whole_and_split_tiles(gpu, m, n, k, monkeypatch):
     assert np.array_equal(sparkq.int8_matmul_int32(at, bt).cpu().numpy(), c)
 
 
+@pytest.mark.parametrize("m,n,k,gm", [(2048, 2560, 1024, "4"), (4096, 2560, 512, "2"), (640, 1000, 256, "4"),
+                                      (300, 300, 384, "8"), (2048, 2176, 2048, "4")])
+def test_int8_gemm_tile_order(gpu, m, n, k, gm, monkeypatch):
+    """The XCD-grouped tile order (each XCD's work items take a contiguous
+    chunk of the order, walked in groups of gm tile rows) against row-major
+    order: identical int32 accumulators over whole grids, tile counts that
+    are and are not multiples of eight, with and without k pieces; sampled
+    elements equal the int64 oracle."""
+    import sparkq
+
+    print(f"[case] int8 gemm tile order m={m} n={n} k={k} gm={gm}", flush=True)
+    rng = np.random.default_rng(m * 3 + n + k)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    at, bt = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    monkeypatch.setenv("SPARKQ_I8_GEMM_GM", gm)
+    c = sparkq.int8_matmul_int32(at, bt)
+    monkeypatch.setenv("SPARKQ_I8_GEMM_ROWMAJOR", "1")
+    assert torch.equal(c, sparkq.int8_matmul_int32(at, bt))
+    rows = np.sort(rng.choice(m, 64, replace=False))
+    cols = np.sort(rng.choice(n, 96, replace=False))
+    assert np.array_equal(c.cpu().numpy()[np.ix_(rows, cols)], o.int8_matmul(a[rows], b[cols]))
+
+
 @pytest.mark.parametrize("m,n,k", [(64, 96, 256), (130, 300, 512), (200, 2560, 1024),
                                    (1000, 130, 384), (257, 64, 8192), (96, 4100, 128)])
 @pytest.mark.parametrize("splits", ["0", "1", "3"])
