@@ -138,6 +138,33 @@ def test_gemm_one_tile_per_cu_split(gpu, monkeypatch):
     assert torch.allclose(y, y1, rtol=1e-5, atol=1e-6 * float(y1.abs().max()))
 
 
+@pytest.mark.parametrize("m,n,k,gm,same_split", [(2048, 2560, 9728, "4", True), (1024, 3584, 2560, "8", True),
+                                                 (300, 1000, 1024, "4", True), (640, 4096, 2048, "2", True),
+                                                 (512, 19456, 2560, "4", False)])
+def test_gemm_tile_order(gpu, m, n, k, gm, same_split, monkeypatch):
+    """The XCD-grouped tile order of the prefill GEMM (each XCD's work items
+    take a contiguous chunk of the order, walked in groups of gm tile rows)
+    against row-major order. Where every tile or none is split along k, each
+    output's products are summed in the same order either way: identical
+    bits (whole grids in k pieces, tile counts that are and are not
+    multiples of eight, 64- and 128-row tiles). Where only the tiles past one
+    per CU are split (304 tiles on 256 CUs), the order picks which tiles
+    those are, and a split tile adds its fp32 partials in a different order:
+    within the oracle's tolerance and fp32 rounding of each other."""
+    g = 64
+    x, wq, s, b = w4_problem(m, n, k, g, seed=m + 5 * n)
+    monkeypatch.setenv("SPARKQ_W4_GEMM_GM", gm)
+    y = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    monkeypatch.setenv("SPARKQ_W4_GEMM_ROWMAJOR", "1")
+    y0 = _run(gpu, x, wq, s, b, g, o.BF16, out_dtype=torch.float32)
+    if same_split:
+        assert torch.equal(y, y0)
+    else:
+        assert torch.allclose(y, y0, rtol=1e-5, atol=1e-6 * float(y0.abs().max()))
+    cols = np.sort(np.random.default_rng(n).choice(n, 64, replace=False))
+    check_fp32(y.cpu().numpy()[:, cols], o.w4a16_matmul(x, wq[cols], s[cols], b[cols], g))
+
+
 @pytest.mark.parametrize("m,n,k,g", [(40, 96, 2048, 64), (33, 64, 2560, 32), (48, 40, 9728, 64),
                                      (36, 32, 16384, 128), (34, 16, 16896, 64)])
 def test_gemm_prologue_row_paths(gpu, m, n, k, g, monkeypatch):
