@@ -577,11 +577,13 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void sdpa_prefill_kernel(Sdp
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, grp = lane >> 4;
-  const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
+  int bx, by;
+  xcd_grid_item(a.xcd != 0, bx, by);
+  const int b = by / a.Hkv, kh = by - b * a.Hkv;
   const int R = a.L * GQA;                     // query rows (position, head) of this KV head
   // the wave's first row; under the causal mask the later (longer) row
   // tiles start first
-  const int row0 = (a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x) * 64 + wave * 16;
+  const int row0 = (a.causal ? (int)gridDim.x - 1 - bx : bx) * 64 + wave * 16;
   // last visible token of row rr (bottom-right causal), -1 for rows past R
   auto last_tok = [&](int rr) -> int {
     return rr >= R ? -1 : (a.causal ? a.N - a.L + rr / GQA : a.N - 1);
@@ -907,7 +909,9 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void sdpa_prefill_affine_ker
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, grp = lane >> 4;
-  const int b = blockIdx.y / a.Hkv, kh = blockIdx.y - b * a.Hkv;
+  int bx, by;
+  xcd_grid_item(a.xcd != 0, bx, by);
+  const int b = by / a.Hkv, kh = by - b * a.Hkv;
   const int gqa = a.Hq / a.Hkv;
   const int R = a.L * gqa;  // (position, head) rows of this KV head
   // Row tiles of 128. Under the causal mask tile t walks ~t+1 times the
@@ -919,7 +923,7 @@ __global__ __launch_bounds__(256, D <= 128 ? 2 : 1) void sdpa_prefill_affine_ker
   // of the blocks of tile x / S and the last chunk to finish merges.
   const int ntiles = (R + 127) / 128;
   const int S = SPLIT ? a.S : 1;
-  const int xt = S > 1 ? (int)blockIdx.x / S : (int)blockIdx.x, chunk = (int)blockIdx.x - xt * S;
+  const int xt = S > 1 ? bx / S : bx, chunk = bx - xt * S;
   const int npass = D <= 128 && a.pair && ntiles - 1 - xt != xt ? 2 : 1;
   for (int pass = 0; pass < npass; ++pass) {
   const int tile = D <= 128 && a.pair ? (pass == 0 ? ntiles - 1 - xt : xt)
@@ -1659,6 +1663,10 @@ int int8kv_sdpa_prefill(const void* q, const void* kc, const void* ks, const voi
   a.S = 1;
   a.tps = (int)N;
   a.scale_log2 = scale * 1.4426950408889634f;
+  // the row tiles of one (sequence, KV head) on one XCD, sharing its L2 for
+  // the K/V blocks every wave re-reads (B=1 causal, 32/8 heads, D=128: L=N=2048
+  // 185 -> 246 TFLOP/s; L=512 N=4096 unchanged)
+  a.xcd = !env_int("SPARKQ_PREFILL_NO_XCD", 0);
   const int gqa = (int)(Hq / Hkv);
   dim3 grid((unsigned)cdiv(L * gqa, 64), (unsigned)(B * Hkv));
   if (D == 64)
@@ -1761,6 +1769,9 @@ int int8kv_sdpa_prefill_affine(const void* q, const void* kc, const void* ks, co
   a.pair = plan.pair;
   a.tps = (int)N;
   a.scale_log2 = scale * 1.4426950408889634f;
+  // XCD-grouped work order (L=512 N=4096: D=128 275 -> 286, D=256 332 -> 344
+  // TFLOP/s; L=N=2048 unchanged)
+  a.xcd = !env_int("SPARKQ_PREFILL_NO_XCD", 0);
   if (plan.S > 1) {
     unsigned char* base = reinterpret_cast<unsigned char*>(ws);
     const size_t rows = round_up((size_t)plan.ntiles_all * plan.S * 128 * 4, 256);

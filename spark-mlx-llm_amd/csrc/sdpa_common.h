@@ -30,7 +30,25 @@ struct SdpaArgs {
   int L, causal;     // prefill: query length, bottom-right causal mask
   int pair;          // affine prefill: each workgroup takes row tiles T-1-x and x
   float scale_log2;  // softmax scale * log2(e)
+  int xcd;           // prefill: XCD-grouped work order (xcd_grid_item)
 };
+
+// Workgroup (x, y) of a 2-D grid is dispatched as item y * gx + x and runs
+// on XCD item % 8. With xcd set, the item order is regrouped so that each XCD
+// takes a contiguous chunk of the (y, x) order: the row tiles of one
+// (sequence, KV head) share an XCD's L2 for their K/V blocks, and within a
+// chunk the items keep their relative order (the longest causal tiles still
+// start first). A bijection on the grid; a grid of a size not divisible by
+// 8 keeps its order.
+__device__ __forceinline__ void xcd_grid_item(bool xcd, int& x, int& y) {
+  x = (int)blockIdx.x;
+  y = (int)blockIdx.y;
+  const int gx = (int)gridDim.x, T = gx * (int)gridDim.y;
+  if (!xcd || (T & 7) != 0) return;
+  const int id = y * gx + x, v = (id & 7) * (T >> 3) + (id >> 3);
+  y = v / gx;
+  x = v - y * gx;
+}
 
 constexpr float kNegInf = -__builtin_huge_valf();
 

@@ -263,6 +263,36 @@ def test_prefill_affine_split_repeats(gpu, b, hq, hkv, length, n, d):
     assert rel_l2(out, ref) <= _AFF_TOL[o.BF16][0] and _row_rel(out, ref) <= _AFF_TOL[o.BF16][1]
 
 
+@pytest.mark.parametrize("fmt,b,hq,hkv,length,n,d", [
+    ("s8", 2, 32, 8, 257, 257, 128), ("s8", 1, 32, 8, 100, 300, 128), ("s8", 1, 16, 2, 40, 129, 256),
+    ("affine_u8", 4, 32, 8, 512, 512, 64), ("affine_u8", 1, 32, 8, 70, 2000, 128),
+    ("affine_u8", 2, 8, 2, 37, 100, 128)])
+def test_prefill_xcd_order_identical(gpu, fmt, b, hq, hkv, length, n, d, monkeypatch):
+    """The XCD-grouped work order of both prefill kernels (the row tiles of
+    one (sequence, KV head) dispatched to one XCD) changes no row's
+    arithmetic: identical outputs with and without it, for grids whose size
+    is and is not a multiple of eight, paired causal tiles and context
+    splits."""
+    import sparkq
+
+    print(f"[prefill xcd] {fmt} b={b} hq={hq} hkv={hkv} L={length} N={n} D={d}", flush=True)
+    q = up16(_x16(n + d, 70, (b, hq, length, d)), o.BF16, gpu)
+    if fmt == "s8":
+        kc, ks = o.kv_quantize_s8(o.randn(n, 71, b * hkv * n * d).reshape(b, hkv, n, d))
+        vc, vs = o.kv_quantize_s8(o.randn(n, 72, b * hkv * n * d).reshape(b, hkv, n, d))
+        keys = (torch.from_numpy(kc).to(gpu), torch.from_numpy(ks.view(np.float16)).to(gpu))
+        vals = (torch.from_numpy(vc).to(gpu), torch.from_numpy(vs.view(np.float16)).to(gpu))
+        group = {}
+    else:
+        keys, vals, _, _ = _affine_cache(gpu, b, hkv, n, d, 32, n + d, o.BF16)
+        group = {"group_size": 32}
+    run = lambda: sparkq.int8_quantized_sdpa(q, keys, vals, scale=0.09, mask="causal",  # noqa: E731
+                                             out_dtype=torch.float32, **group)
+    y = run()
+    monkeypatch.setenv("SPARKQ_PREFILL_NO_XCD", "1")
+    assert torch.equal(y, run())
+
+
 def test_prefill_affine_dispatch(gpu):
     """dispatch_sdpa routes multi-token queries over the affine tuple to the
     fused kernel when fused_quantized_sdpa_prefill is set."""
