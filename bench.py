@@ -784,7 +784,7 @@ def main():
         trace_summary(args.trace_summary)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of "
+        print(json.dumps({"error": "bench.py measures one GPU; multi-GPU runs are not part of "
                                    "it (--gpus must be 1)"}))
         sys.exit(2)
 

@@ -54,7 +54,7 @@ enum sparkq_kv_format {
 /* Status codes. */
 #define SPARKQ_OK 0
 #define SPARKQ_ERR_INVALID (-1)     /* bad shape, dtype, pointer or size */
-#define SPARKQ_ERR_UNSUPPORTED (-2) /* valid request this build does not run */
+#define SPARKQ_ERR_UNSUPPORTED (-2) /* valid request the library does not run */
 #define SPARKQ_ERR_DEVICE (-3)      /* HIP runtime or launch failure */
 #define SPARKQ_ERR_WORKSPACE (-4)   /* workspace missing or too small */
 
@@ -224,7 +224,7 @@ int sparkq_w8a8_linear(const void* x, const int8_t* w, const float* w_scales,
  * K % 16 == 0 and M*K <= 32768. Replaces w8a16_per_channel
  * (X/src/spark_w8a16.cpp:80-110, bindings X/src/bindings.cpp:17; kernel
  * X/src/kernels/w8a16_matvec.metal:12-31), which takes one activation row;
- * rows 2..4 are this build's extension for short verify batches.
+ * rows 2..4 extend it for short verify batches.
  * ---------------------------------------------------------------------- */
 int sparkq_w8a16_linear(const void* x, const int8_t* w, const float* scales,
                         void* y, int64_t M, int64_t N, int64_t K, int x_dtype,

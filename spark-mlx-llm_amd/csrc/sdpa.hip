@@ -1714,7 +1714,7 @@ static AffPrefillPlan plan_prefill_affine(int64_t B, int64_t Hq, int64_t Hkv, in
     const char* e = std::getenv("SPARKQ_PREFILL_SPLIT_TARGET");
     return e ? std::max(1, std::atoi(e)) : 256;
   }();
-  if (!p.pair && p.ntiles_all < target && p.ntiles_all <= kCounterBytes / 4)
+  if (!p.pair && p.ntiles_all < target && p.ntiles_all <= (int64_t)(kCounterBytes / 4))
     p.S = (int)std::min<int64_t>(8, cdiv(target, p.ntiles_all));
   p.bytes = p.S > 1 ? kCounterBytes + round_up((size_t)p.ntiles_all * p.S * 128 * 4, 256) * 2 +
                           (size_t)p.ntiles_all * p.S * 128 * D * 4

@@ -1487,7 +1487,7 @@ template <int NCH>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(GemmPrepArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* red = reinterpret_cast<float*>(smem);
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x;
   const int ng = a.K / a.G;
   const int nwb = (a.N + a.rw - 1) / a.rw;  // weight blocks come first
   if ((int)blockIdx.x >= nwb) {
