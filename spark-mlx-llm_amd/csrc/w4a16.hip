@@ -20,6 +20,9 @@
 //   w4_decode_stream_kernel  2 <= M <= 16: the same layout with each decoded
 //                       piece feeding eight MFMAs per row quartet and lane
 //                       sums kept in registers over a run of spans
+//   w4_decode_phased_kernel  5 <= M <= 8 with rows whose activations exceed
+//                       the staging registers or LDS: the same, activations
+//                       staged a K phase at a time
 //   w4_skinny_kernel    M <= 32: weight streaming, 32 rows x 64 k per wave
 //                       step, MFMA 32x32x16, in-workgroup split-K over waves,
 //                       cross-workgroup split-K combined in the same launch by
@@ -927,6 +930,8 @@ struct DecodeStreamArgs {
   int QW;  // row quads of the largest workgroup
   const uint16_t* res;  // 16-bit residual added to the rounded output (or null)
   int RR;  // 1: workgroup i owns rows [i*N/P, (i+1)*N/P) (quads from its first row)
+  int PH;   // K phases (phased kernel): the activations are staged SPH spans at a time
+  int SPH;  // spans per phase (the last phase may hold fewer)
 };
 
 constexpr int kDecNW = 16;  // waves per workgroup
@@ -947,6 +952,19 @@ __host__ __device__ __forceinline__ DecLds dec_lds(int M, int K, int QW, int G, 
   l.xp = 0;
   l.xs = (M * K * 2 + 1023) & ~1023;
   l.sb = l.xs + (K / 32) * 16 * MQ;
+  l.part = l.sb + ((4 * QW * (K / G) * 4 + 15) & ~15);
+  l.bytes = l.part + QW * U * 4 * 4 * MQ * 4;
+  return l;
+}
+// the same layout with npw 32-k pieces of each activation row staged at once
+// (K phases: xp [M][npw], xs [npw][4*MQ])
+__host__ __device__ __forceinline__ DecLds dec_lds_phased(int M, int K, int QW, int G, int MQ,
+                                                          int npw) {
+  const int U = ((K >> 1) + 255) >> 8;
+  DecLds l;
+  l.xp = 0;
+  l.xs = (M * npw * 64 + 1023) & ~1023;
+  l.sb = l.xs + npw * 16 * MQ;
   l.part = l.sb + ((4 * QW * (K / G) * 4 + 15) & ~15);
   l.bytes = l.part + QW * U * 4 * 4 * MQ * 4;
   return l;
@@ -1142,6 +1160,255 @@ __global__ __launch_bounds__(64 * kDecNW) void w4_decode_stream_kernel(DecodeStr
         }
         if (i + 1 < NI) first = sp[i + 1];
       }
+    }
+  }
+  __syncthreads();
+
+  // 5. each output: the sum of its quad's slots in span order
+  for (int t = tid; t < 4 * nql * M; t += NT) {
+    const int rl = t / M, m = t - rl * M;
+    const int row = r0 + rl;
+    if (row < r1) {
+      const float* src = part + (((rl >> 2) * U) * 4 + (rl & 3)) * MR + m;
+      float v = 0.0f;
+      for (int s = 0; s < U; ++s) v += src[s * 4 * MR];
+      const int64_t idx = (int64_t)m * N + row;
+      store_out(a.y, idx, a.res ? add_rounded<T>(v, a.res[idx]) : v, a.y_dtype);
+    }
+  }
+}
+
+// K-phased variant (5..8 rows, two row quartets, at most two items a wave
+// per phase): for rows whose activation slab exceeds the staging registers or
+// LDS (the down projection at 7 and 8 rows), the activations are staged SPH
+// spans (16*SPH pieces) at a time. Each phase deals its own (row quad, span)
+// items to the waves, in quad-major order over the phase's spans, with every
+// item of a wave in flight. Once a phase's activations are in LDS, each wave
+// issues the next phase's staging and weight loads and then takes up its
+// items of the current phase; a barrier ends the current phase's reads before
+// the next one's activations overwrite them. Runs of items end at phase
+// boundaries, so each output is still the sum of its quad's span slots in
+// span order. (A separate kernel: folding the phases into the one above
+// changed its code and cost its 5..8-row shapes 2-3%.)
+template <typename T, int G>
+__global__ __launch_bounds__(64 * kDecNW) void w4_decode_phased_kernel(DecodeStreamArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int NT = 64 * kDecNW;
+  constexpr int MQ = 2, MR = 8;      // two row quartets (rows past M repeat row M-1)
+  constexpr int NI = 2;              // items of a wave per phase, at most
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, j = lane & 3;
+  const int M = a.M, N = a.N, K = a.K;
+  const int RB = K >> 1;             // bytes per weight row (a multiple of 256)
+  const int U = RB >> 8;             // spans per row
+  const int ng = K / G;              // groups per row
+  const int np = K >> 5;             // 32-k pieces per row
+  const int PH = a.PH, SPH = a.SPH;  // phases, spans per phase
+  const int npw = 16 * SPH;          // pieces of a row staged at once
+  // the workgroup's rows [r0, r1), taken as row quads from r0
+  int r0, r1;
+  if (a.RR) {
+    r0 = (int)((int64_t)blockIdx.x * N / a.P);
+    r1 = (int)((int64_t)(blockIdx.x + 1) * N / a.P);
+  } else {
+    r0 = 4 * (int)((int64_t)blockIdx.x * a.nq / a.P);
+    r1 = min(N, 4 * (int)((int64_t)(blockIdx.x + 1) * a.nq / a.P));
+  }
+  const int nql = (r1 - r0 + 3) >> 2;
+  const DecLds L = dec_lds_phased(M, K, a.QW, G, MQ, npw);
+
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)M * K * 2);
+  const rsrc_t rw = make_rsrc(a.w, (uint32_t)N * RB);
+  const rsrc_t rs = make_rsrc(a.sc, (uint32_t)N * ng * 2);
+  const rsrc_t rb = make_rsrc(a.bi, (uint32_t)N * ng * 2);
+
+  // the wave's items of phase ph, (row quad, span) pairs; returns their count
+  // (slots past the last item read nothing)
+  auto take_items = [&](int ph, int (&qv)[NI], int (&sv)[NI]) {
+    const int s0 = ph * SPH, us = min(U - s0, SPH);
+    const int nitems = nql * us;
+    const int i0 = (int)((int64_t)wave * nitems / kDecNW);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      qv[i] = (i0 + i) / us;
+      sv[i] = s0 + i0 + i - qv[i] * us;
+    }
+    return (int)((int64_t)(wave + 1) * nitems / kDecNW) - i0;
+  };
+  auto wload = [&](int q, int s, bool live) {
+    const int row = r0 + 4 * q + j;
+    return buf_load16(rw, live && row < r1 ? (uint32_t)row * RB + 256 * s + 16 * b : kOob);
+  };
+  // staged activation pieces of phase ph: pi = m * npw + (piece - 16 * s0)
+  const int nxp = M * npw;
+  u32x4_t xr[kDecXP][4];
+  auto xload = [&](int ph) {
+    const int s0 = ph * SPH, us = min(U - s0, SPH);
+#pragma unroll
+    for (int i = 0; i < kDecXP; ++i) {
+      const int pi = tid + i * NT;
+      if (i * NT + 64 * wave < nxp) {
+        const int m = pi / npw, lp = pi - m * npw;
+        const uint32_t off =
+            pi < nxp && lp < 16 * us ? 64u * (uint32_t)(m * np + 16 * s0 + lp) : kOob;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) xr[i][w] = buf_load16(rx, off + 16 * w);
+      }
+    }
+  };
+
+  // 1. the first phase's staging loads, the scales and biases, its weights
+  int ql[NI], sp[NI];
+  int nmy = take_items(0, ql, sp);
+  xload(0);
+  const int nsp = (4 * nql * ng) >> 3;
+  u32x4_t sr[kDecSP], br[kDecSP];
+#pragma unroll
+  for (int i = 0; i < kDecSP; ++i) {
+    const int pi = tid + i * NT;
+    if (i * NT + 64 * wave < nsp) {
+      const uint32_t off = pi < nsp ? 2u * (uint32_t)r0 * ng + 16u * pi : kOob;
+      sr[i] = buf_load16(rs, off);
+      br[i] = buf_load16(rb, off);
+    }
+  }
+  u32x4_t wv[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) wv[i] = wload(ql[i], sp[i], i < nmy);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. clear the quad slots; the scales and biases to LDS (once, so that their
+  // registers are free before the phase loop)
+  {
+    float* part = reinterpret_cast<float*>(smem + L.part);
+    const int nslot = nql * U * 16 * MQ;
+    for (int e = tid; e < nslot; e += NT) part[e] = 0.0f;
+    uint32_t* sb = reinterpret_cast<uint32_t*>(smem + L.sb);
+#pragma unroll
+    for (int i = 0; i < kDecSP; ++i) {
+      const int pi = tid + i * NT;
+      if (pi < nsp) {
+        const u32x4_t s = sr[i], c = br[i];
+        u32x4_t lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = __builtin_amdgcn_perm(c[e], s[e], 0x05040100u);  // (s0, b0)
+          hi[e] = __builtin_amdgcn_perm(c[e], s[e], 0x07060302u);  // (s1, b1)
+        }
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi) = u32x4_t{lo[0], hi[0], lo[1], hi[1]};
+        *reinterpret_cast<u32x4_t*>(sb + 8 * pi + 4) = u32x4_t{lo[2], hi[2], lo[3], hi[3]};
+      }
+    }
+  }
+
+  const DecodeConsts dc = decode_consts<T>();
+  const unsigned char* xpc = smem + L.xp;
+  const float* xsc = reinterpret_cast<const float*>(smem + L.xs);
+  const uint32_t* sb = reinterpret_cast<const uint32_t*>(smem + L.sb);
+  float* part = reinterpret_cast<float*>(smem + L.part);
+  for (int ph = 0; ph < PH; ++ph) {
+    const int s0 = ph * SPH;  // the phase's first span
+    // 3. the phase's activations to LDS, with the sums of their pieces
+    {
+      uint32_t* xp = reinterpret_cast<uint32_t*>(smem + L.xp);
+      float* xs = reinterpret_cast<float*>(smem + L.xs);
+#pragma unroll
+      for (int i = 0; i < kDecXP; ++i) {
+        const int pi = tid + i * NT;
+        if (pi < nxp) {
+          float sum = 0.0f;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const u32x4_t r = xr[i][w];
+            const u32x4_t o = {__builtin_amdgcn_perm(r.z, r.x, 0x05040100u),   // (x0, x4)
+                               __builtin_amdgcn_perm(r.z, r.x, 0x07060302u),   // (x1, x5)
+                               __builtin_amdgcn_perm(r.w, r.y, 0x05040100u),   // (x2, x6)
+                               __builtin_amdgcn_perm(r.w, r.y, 0x07060302u)};  // (x3, x7)
+            *reinterpret_cast<u32x4_t*>(xp + gemv_xslot(pi, w)) = o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum = pair_sum<T>(r[e], sum);
+          }
+          const int m = pi / npw, piece = pi - m * npw;
+          xs[piece * MR + m] = sum;
+        }
+      }
+    }
+    __syncthreads();
+
+    // the next phase's staging and weight loads go out behind this phase's
+    int qn[NI], sn[NI], nn = 0;
+    u32x4_t wn[NI];
+    const bool more = ph + 1 < PH;
+    if (more) {
+      nn = take_items(ph + 1, qn, sn);
+      xload(ph + 1);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) wn[i] = wload(qn[i], sn[i], i < nn);
+    }
+
+    // 4. the wave's items in order; per-lane sums while the row quad stays
+    f32x4_t acc[MQ];
+#pragma unroll
+    for (int q = 0; q < MQ; ++q) acc[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    int first = nmy > 0 ? sp[0] : 0;   // first span of the current run
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      if (i < nmy) {
+        const int s = sp[i];
+        const int p = 256 * s + 16 * b;
+        const bool ok = r0 + 4 * ql[i] + j < r1;
+        const int lpc = 16 * (s - s0) + b;   // the piece's place in the staged slab
+        const uint32_t pair = ok ? sb[(4 * ql[i] + j) * ng + (2 * p) / G] : 0u;
+        const float sf = T::to_f32((uint16_t)(pair & 0xFFFFu));
+        const float bf = fmaf(-T::OFFSET, sf, T::to_f32((uint16_t)(pair >> 16)));
+        uint32_t pr[4][4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) decode_w4_strided<T>(wv[i][w], dc, pr[w]);
+#pragma unroll
+        for (int q = 0; q < MQ; ++q) {
+          const int pi = min(4 * q + j, M - 1) * npw + lpc;
+          f32x4_t d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = d0;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xpc + 4 * gemv_xslot(pi, w));
+            d0 = mfma4x4<T>(v.x, v.y, pr[w][0], pr[w][1], d0);
+            d1 = mfma4x4<T>(v.z, v.w, pr[w][2], pr[w][3], d1);
+          }
+          const f32x4_t xm = *reinterpret_cast<const f32x4_t*>(xsc + lpc * MR + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float t = fmaf(sf, d0[e] + d1[e], bf * xm[e]);
+            acc[q][e] += ok ? t : 0.0f;
+          }
+        }
+        // end of a run: next item in another row quad, or the wave's last
+        const bool last = i + 1 >= nmy || (i + 1 < NI && ql[i + 1] != ql[i]);
+        if (last) {
+          float* dst = part + ((ql[i] * U + first) * 4) * MR;
+#pragma unroll
+          for (int q = 0; q < MQ; ++q) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = sum_blocks(acc[q][e]);
+              if (lane < 4) dst[lane * MR + 4 * q + e] = v;
+            }
+            acc[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+          if (i + 1 < NI) first = sp[i + 1];
+        }
+      }
+    }
+
+    if (more) {
+      nmy = nn;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        ql[i] = qn[i];
+        sp[i] = sn[i];
+        wv[i] = wn[i];
+      }
+      __syncthreads();
     }
   }
   __syncthreads();
@@ -2589,6 +2856,7 @@ static void launch_stream(const StreamPlan& p, int G, const GemvStreamArgs& a, h
 struct DecPlan {
   bool ok;
   int P, QW, MQ, NI, RR, D;
+  int PH, SPH;  // K phases and spans per phase (PH = 1: the whole row staged)
   size_t lds;
 };
 
@@ -2617,14 +2885,30 @@ static DecPlan plan_dec(int64_t M, int64_t N, int64_t K, int G) {
   p.RR = !env_int("SPARKQ_W4_DEC_QUADS", 0) && ng % 8 == 0;
   if (p.RR) p.QW = (int)cdiv(cdiv(N, p.P), 4);
   p.MQ = (int)cdiv(M, 4);
-  const int64_t ni = cdiv(p.QW * U, kDecNW);
+  const int64_t nt = 64 * kDecNW;
+  if (4 * p.QW * ng / 8 > kDecSP * nt) return p;
+  // K phases: the fewest whose staged activation slab fits the staging
+  // registers and LDS. More than one for 5..8 rows and at most two items per
+  // wave and phase only: the phased kernel holds the next phase's staging and
+  // weight registers beside the current ones (126 VGPRs there; three row
+  // quartets or four items spill). SPARKQ_W4_DEC_PHASES: at least that many;
+  // SPARKQ_W4_DEC_NO_PHASES: one.
+  const int64_t phmax = env_int("SPARKQ_W4_DEC_NO_PHASES", 0) || p.MQ != 2 ? 1 : 4;
+  for (int64_t want = std::max<int64_t>(1, env_int("SPARKQ_W4_DEC_PHASES", 1)); want <= phmax; ++want) {
+    const int64_t sph = cdiv(U, want), npw = 16 * sph;
+    if (M * npw > kDecXP * nt) continue;
+    if (cdiv(U, sph) > 1 && cdiv(p.QW * sph, kDecNW) > 2) continue;
+    const DecLds l = dec_lds_phased((int)M, (int)K, p.QW, G, p.MQ, (int)npw);
+    if (l.bytes > kDecMaxLds) continue;
+    p.SPH = (int)sph;
+    p.PH = (int)cdiv(U, sph);
+    p.lds = (size_t)l.bytes;
+    break;
+  }
+  if (p.PH == 0) return p;
+  const int64_t ni = cdiv(p.QW * p.SPH, kDecNW);
   if (ni > 8) return p;
   p.NI = ni <= 2 ? 2 : (ni <= 4 ? 4 : 8);
-  const int64_t nt = 64 * kDecNW;
-  if (M * (K / 32) > kDecXP * nt || 4 * p.QW * ng / 8 > kDecSP * nt) return p;
-  const DecLds l = dec_lds((int)M, (int)K, p.QW, G, p.MQ);
-  if (l.bytes > kDecMaxLds) return p;
-  p.lds = (size_t)l.bytes;
   // one weight item per wave in flight, the next issued as an item is taken
   // up, for waves of four or more items: every item in flight at once kept
   // the waves at issue while the CU's memory queue drained and put the items'
@@ -2634,7 +2918,7 @@ static DecPlan plan_dec(int64_t M, int64_t N, int64_t K, int G) {
   // rows) stay all in flight (6.1 -> 6.2 us at one). SPARKQ_W4_DEC_DEPTH: 1 or
   // 8 (all).
   const int64_t dd = env_int("SPARKQ_W4_DEC_DEPTH", p.NI >= 4 ? 1 : 8);
-  p.D = dd == 1 ? 1 : p.NI;
+  p.D = dd == 1 && p.PH == 1 ? 1 : p.NI;
   p.ok = true;
   return p;
 }
@@ -2666,6 +2950,14 @@ static void launch_dec_m(const DecPlan& p, const DecodeStreamArgs& a, hipStream_
 }
 template <typename T, int G>
 static void launch_dec_g(const DecPlan& p, const DecodeStreamArgs& a, hipStream_t st) {
+  if (p.PH > 1) {
+    auto* k = w4_decode_phased_kernel<T, G>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, kDecMaxLds);
+    (void)attr;
+    hipLaunchKernelGGL(k, dim3((unsigned)p.P), dim3(64 * kDecNW), p.lds, st, a);
+    return;
+  }
   switch (p.MQ) {
     case 1: launch_dec_m<T, G, 1>(p, a, st); break;
     case 2: launch_dec_m<T, G, 2>(p, a, st); break;
@@ -3059,6 +3351,8 @@ int w4a16_linear(const void* x, const uint32_t* w, const void* s, const void* b,
     a.P = dp.P;
     a.QW = dp.QW;
     a.RR = dp.RR;
+    a.PH = dp.PH;
+    a.SPH = dp.SPH;
     a.res = (const uint16_t*)res;
     if (res_done) *res_done = res != nullptr;
     if (xdt == SPARKQ_BF16)

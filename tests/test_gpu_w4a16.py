@@ -371,6 +371,31 @@ def test_decode_multirow_stream_load_depth(gpu, m, n, k, g, monkeypatch):
     assert torch.equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("m,n,k,g,phases", [(7, 2560, 9728, 64, "1"), (8, 2560, 9728, 32, "1"),
+                                            (8, 8, 9728, 64, "1"), (6, 1000, 12288, 128, "1"),
+                                            (7, 1028, 9728, 32, "1"), (5, 300, 16384, 64, "1"),
+                                            (5, 1100, 3072, 32, "2"), (5, 1100, 3072, 32, "4"),
+                                            (8, 3584, 2560, 64, "3"), (6, 44, 4096, 32, "2")])
+def test_decode_multirow_stream_phased(gpu, m, n, k, g, phases, monkeypatch):
+    """The multi-row streaming kernel with its activations staged in K phases
+    (5..8 rows): the down projection at 7 and 8 rows (two phases of 10 and 9
+    spans), slabs past LDS at 6 rows (K = 12288) and past the staging
+    registers at 5 rows (K = 16384), a partial last row quad, fewer row quads
+    than CUs, and phases asked for on short rows (spans per phase 3 / 2 / 2 /
+    4, a shorter last phase); both dtypes within the oracle's tolerance,
+    repeated calls bit-identical."""
+    monkeypatch.setenv("SPARKQ_W4_NO_MR", "1")
+    monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
+    monkeypatch.setenv("SPARKQ_W4_DEC_PHASES", phases)
+    for dtype in (o.BF16, o.F16):
+        x, wq, s, b = w4_problem(m, n, k, g, dtype=dtype, seed=m * 13 + n + k)
+        ref = o.w4a16_matmul(x, wq, s, b, g, dtype)
+        y32 = _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32)
+        check_fp32(y32.cpu().numpy(), ref)
+        check_rounded16(down16(_run(gpu, x, wq, s, b, g, dtype)), ref, dtype)
+        assert torch.equal(y32, _run(gpu, x, wq, s, b, g, dtype, out_dtype=torch.float32))
+
+
 @pytest.mark.parametrize("m,n,k,g", [(16, 19456, 2560, 64), (12, 2560, 9728, 64), (9, 1000, 1152, 128)])
 def test_decode_mfma_rows_load_depth(gpu, m, n, k, g, monkeypatch):
     """The tile-major 16x16x32 kernel with one, two or all weight items of a
