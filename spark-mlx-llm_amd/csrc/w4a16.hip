@@ -22,7 +22,7 @@
 //                       sums kept in registers over a run of spans
 //   w4_decode_phased_kernel  5 <= M <= 8 with rows whose activations exceed
 //                       the staging registers or LDS: the same, activations
-//                       staged a K phase at a time
+//                       staged a K phase at a time (opt-in)
 //   w4_skinny_kernel    M <= 32: weight streaming, 32 rows x 64 k per wave
 //                       step, MFMA 32x32x16, in-workgroup split-K over waves,
 //                       cross-workgroup split-K combined in the same launch by
@@ -2891,10 +2891,14 @@ static DecPlan plan_dec(int64_t M, int64_t N, int64_t K, int G) {
   // registers and LDS. More than one for 5..8 rows and at most two items per
   // wave and phase only: the phased kernel holds the next phase's staging and
   // weight registers beside the current ones (126 VGPRs there; three row
-  // quartets or four items spill). SPARKQ_W4_DEC_PHASES: at least that many;
-  // SPARKQ_W4_DEC_NO_PHASES: one.
-  const int64_t phmax = env_int("SPARKQ_W4_DEC_NO_PHASES", 0) || p.MQ != 2 ? 1 : 4;
-  for (int64_t want = std::max<int64_t>(1, env_int("SPARKQ_W4_DEC_PHASES", 1)); want <= phmax; ++want) {
+  // quartets or four items spill). Phases are opt-in (SPARKQ_W4_DEC_PHASES=n:
+  // at least n): the phased down projection at 7 and 8 rows was faster than
+  // the skinny kernel back to back (12.57 -> 12.2 us at 7 rows) but not inside
+  // the decode sweep (QKV, gate+up, down per layer: 8 rows 1146 -> 1161 us, 7
+  // rows equal), so those rows keep the skinny kernel by default.
+  const int64_t want0 = env_int("SPARKQ_W4_DEC_PHASES", 0);
+  const int64_t phmax = want0 < 1 || p.MQ != 2 ? 1 : 4;
+  for (int64_t want = std::max<int64_t>(1, want0); want <= phmax; ++want) {
     const int64_t sph = cdiv(U, want), npw = 16 * sph;
     if (M * npw > kDecXP * nt) continue;
     if (cdiv(U, sph) > 1 && cdiv(p.QW * sph, kDecNW) > 2) continue;

@@ -44,9 +44,8 @@ def test_abi_version_and_workspace_queries():
     # the M <= 4 decode GEMV keeps whole rows in one workgroup: no workspace
     assert lib.sparkq_w4a16_workspace_bytes(1, 2560, 9728, 64) == 0
     assert lib.sparkq_w4a16_workspace_bytes(4, 19456, 2560, 64) == 0
-    # down at 8 rows stages its activations in K phases inside one workgroup
-    # per row range; at 16 rows its K ranges go to separate workgroups
-    assert lib.sparkq_w4a16_workspace_bytes(8, 2560, 9728, 64) == 0
+    # wider decode batches split K across workgroups
+    assert lib.sparkq_w4a16_workspace_bytes(8, 2560, 9728, 64) > 0
     assert lib.sparkq_w4a16_workspace_bytes(16, 2560, 9728, 64) > 0
     # prefill: the group-sum prologue buffer [K/G][M] fp32
     assert lib.sparkq_w4a16_workspace_bytes(2048, 19456, 2560, 64) >= 2048 * 40 * 4

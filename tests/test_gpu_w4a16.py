@@ -378,11 +378,11 @@ def test_decode_multirow_stream_load_depth(gpu, m, n, k, g, monkeypatch):
                                             (8, 3584, 2560, 64, "3"), (6, 44, 4096, 32, "2")])
 def test_decode_multirow_stream_phased(gpu, m, n, k, g, phases, monkeypatch):
     """The multi-row streaming kernel with its activations staged in K phases
-    (5..8 rows): the down projection at 7 and 8 rows (two phases of 10 and 9
-    spans), slabs past LDS at 6 rows (K = 12288) and past the staging
+    (5..8 rows, opt-in): the down projection at 7 and 8 rows (two phases of 10
+    and 9 spans), slabs past LDS at 6 rows (K = 12288) and past the staging
     registers at 5 rows (K = 16384), a partial last row quad, fewer row quads
-    than CUs, and phases asked for on short rows (spans per phase 3 / 2 / 2 /
-    4, a shorter last phase); both dtypes within the oracle's tolerance,
+    than CUs, and more phases asked for on short rows (spans per phase 3 / 2 /
+    2 / 4, a shorter last phase); both dtypes within the oracle's tolerance,
     repeated calls bit-identical."""
     monkeypatch.setenv("SPARKQ_W4_NO_MR", "1")
     monkeypatch.setenv("SPARKQ_W4_NO_GEMVQ", "1")
