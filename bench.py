@@ -763,6 +763,31 @@ def cpu_legs(layers_host, threads, budget_s=2.0):
     return res
 
 
+def launch_floor(torch, sparkq, dev, iters):
+    """Launch-to-launch floor of graph replay: back-to-back W4A16 G64 launches
+    at M=1 and K=512 (one 1 KB span per row quad, next to no work) for N = 4,
+    1024 and 8192 (1, 256 and 512 workgroups), 256 launches captured in one
+    graph; prints a markdown row per case with the time per launch (HIP
+    events over the replays). Under rocprofv3 --kernel-trace the kernel's own
+    duration is the rest: the launch-to-launch gap is the difference."""
+    k, launches = 512, 256
+    print("| N x K | launches per replay | us per launch (graph replay) |")
+    print("|---|---|---|")
+    for n in (4, 1024, 8192):
+        w = (torch.randn((n, k), device=dev) * 0.02).to(torch.bfloat16)
+        wq, s, b = sparkq.affine_quantize(w, group_size=G)
+        x = torch.randn((1, k), device=dev).to(torch.bfloat16)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+
+        def fn():
+            for _ in range(launches):
+                sparkq.affine_quantized_matmul(x, wq, s, b, group_size=G, out=y)
+
+        graph = capture(torch, fn)
+        ms = Timer(torch).time(graph.replay, iters, 2)
+        print(f"| {n} x {k} | {launches} | {ms * 1e3 / launches:.3f} |", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -777,6 +802,8 @@ def main():
     ap.add_argument("--only-sdpa", default=None, metavar="[FMT:]B:N[,...]",
                     help="run only INT8-KV decode launches (for rocprofv3 --kernel-trace / --pmc); "
                          "FMT s8 (default), u8 (affine G32) or u4 (affine G64)")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="time back-to-back near-empty GEMV launches in graph replay and exit")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="print per-(kernel, grid) rows of a rocprofv3 kernel trace and exit")
     args = ap.parse_args()
@@ -804,6 +831,9 @@ def main():
         return
     if args.only_sdpa:
         only_sdpa(torch, sparkq, dev, args.only_sdpa, max(args.steps, 1))
+        return
+    if args.launch_floor:
+        launch_floor(torch, sparkq, dev, max(args.steps, 1))
         return
     log("generating 36 layers of W4A16 G64 weights")
     layers = make_w4_layers(torch, sparkq, dev, LAYERS)
