@@ -609,11 +609,16 @@ static void launch_mr(const MrPlan& p, int G, const MrArgs& a, hipStream_t st) {
     launch_mr_g<T, 128>(p, a, st);
 }
 
-// Plan of the segment-major kernel: 9..16 rows (SPARKQ_W4_MR_MIN lowers
-// it), K a multiple of 128 with at most 8 segments per wave, one workgroup
+// Plan of the segment-major kernel: 5..16 rows (SPARKQ_W4_MR_MIN sets the
+// least), K a multiple of 128 with at most 8 segments per wave, one workgroup
 // per CU over contiguous tile ranges, the (scale, bias) pieces within two per
 // thread, the register arrays (tiles x segments) within 16 pieces, LDS within
-// 160 KB. SPARKQ_W4_MR_TILED keeps the tile-major kernel.
+// 160 KB. SPARKQ_W4_MR_TILED keeps the tile-major kernel. From 5 rows, not 9
+// as the tile-major kernel: per projection at 5 / 6 / 7 / 8 rows (bf16, G64,
+// 36 weight sets) QKV 3584 x 2560 took 4.98 / 5.12 / 5.23 / 5.31 us against
+// 6.04 / 6.07 / 6.15 / 6.24 on the 4x4x4 multi-row streaming kernel, and the
+// 2560 x 2560 linear 4.87 / 5.00 / 5.12 / 5.21 against 5.33 / 5.37 / 5.45 /
+// 5.53 (2..4 rows keep the one-round kernel, equal within 0.05 us).
 struct MrsPlan {
   bool ok;
   int P, TW, NS, NW, TWM, NSM;
@@ -622,7 +627,7 @@ struct MrsPlan {
 
 static MrsPlan plan_mrs(int64_t M, int64_t N, int64_t K, int G) {
   MrsPlan p{};
-  if (M < env_int("SPARKQ_W4_MR_MIN", 9) || M > 16 || env_int("SPARKQ_W4_NO_MR", 0) ||
+  if (M < env_int("SPARKQ_W4_MR_MIN", 5) || M > 16 || env_int("SPARKQ_W4_NO_MR", 0) ||
       env_int("SPARKQ_W4_MR_TILED", 0))
     return p;
   if (K % 128 != 0 || K % G != 0) return p;
