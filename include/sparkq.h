@@ -81,13 +81,17 @@ int sparkq_is_available(void);
  * group_size in {32, 64, 128}; bits must be 4; K % 64 == 0; K % G == 0.
  * Dispatches internally (sparkq_w4a16_workspace_bytes gives the size each
  * shape needs; the decode GEMVs need none):
- *   - M = 1 with rows of whole 512-k spans (at most 8) and N % 4 == 0: the
- *     one-round GEMV (one row quad per wave, every quad resident at once);
+ *   - 1 <= M <= 4 with rows of whole 512-k spans (at most 8) and N % 4 == 0:
+ *     the one-round GEMV (one row quad per wave, every quad resident at once);
  *   - M = 1, rows longer than that: the streaming GEMV (one workgroup per
  *     CU, 4x4x4 MFMA blocks, activations staged once per CU);
- *   - 9 <= M <= 16 with K % 128 == 0: the 16x16x32 MFMA decode (16 weight
- *     rows x 16 activation rows per MFMA); rows whose activations exceed its
- *     staging split K into ranges combined in the same launch (workspace);
+ *   - 5 <= M <= 16 with K % 128 == 0, at most one 16-row tile per CU and
+ *     rows of at most 32 128-k segments: the segment-major 16x16x32 MFMA
+ *     decode (16 weight rows x 16 activation rows per MFMA, activations
+ *     loaded straight into registers);
+ *   - 9 <= M <= 16 with K % 128 == 0 otherwise: the tile-major 16x16x32 MFMA
+ *     decode; rows whose activations exceed its staging split K into ranges
+ *     combined in the same launch (workspace);
  *   - 2 <= M <= 16 with K % 512 == 0 and N % 4 == 0 (except M <= 4 with
  *     K <= 2560), when the M activation rows fit LDS: the multi-row
  *     streaming GEMV (one decode shared by all row quartets);
